@@ -1,0 +1,209 @@
+"""Benchmark of the MI355X batched-FFT path (one JSON line on stdout).
+
+Default workload (BASELINE metric "batched f32 C2C effective HBM GB/s"):
+C1 = 1-D C2C forward, f32, N=1024, batch 8192, inputs resident in HBM.
+A step is one execute of the plan over one batch. Buffers rotate over 8
+input/output pairs (1 GiB) so the 256 MB Infinity Cache cannot hold the
+working set between steps.
+
+  value      = algorithmic bytes (2 * N * batch * 8) / average step time, GB/s
+  roofline   = the dominant kernel's algorithmic bytes / its average launch
+               duration (HIP events on the launch stream) against 8 TB/s
+  cpu_baseline = the oracle (a port of vkfft-rs src/reference.rs) timed on
+               this host's cores over a bounded sample of the same workload
+
+--config selects another BASELINE config (c2, c3, c4, c5a, c5b) for
+measurement runs; --all prints one line per config.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "vkfft-rs_amd"))
+
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    "c1": dict(workload="1d_c2c_fwd_f32_n1024_b8192", dims=[1024], batch=8192, kind="c2c", prec="f32"),
+    "c2": dict(workload="1d_r2c_fwd_c2r_inv_f32_n1048576_b256", dims=[1 << 20], batch=256, kind="r2c_c2r",
+               prec="f32"),
+    "c3": dict(workload="2d_c2c_fwd_f32_4096x4096_b16", dims=[4096, 4096], batch=16, kind="c2c", prec="f32"),
+    "c4": dict(workload="3d_c2c_fwd_f64_512x512x512_b1", dims=[512, 512, 512], batch=1, kind="c2c", prec="f64"),
+    "c5a": dict(workload="1d_c2c_fwd_f32_n4099_b4096_bluestein", dims=[4099], batch=4096, kind="c2c",
+                prec="f32"),
+    "c5b": dict(workload="1d_c2c_fwd_f32_n65537_b4096_bluestein", dims=[65537], batch=4096, kind="c2c",
+                prec="f32"),
+}
+
+
+def algorithmic(cfg):
+    """(bytes, flops) of one step: one read + one write of the logical data
+    (BASELINE.md section 2); flops 5 N log2 N per transform (logical N)."""
+    n = 1
+    for d in cfg["dims"]:
+        n *= d
+    b = cfg["batch"]
+    if cfg["kind"] == "r2c_c2r":
+        per_dir = n * 4 + (n // 2 + 1) * 8
+        return 2 * per_dir * b, 2 * 5 * n * math.log2(n) * b
+    es = 8 if cfg["prec"] == "f32" else 16
+    return 2 * n * b * es, 5 * n * math.log2(n) * b
+
+
+def build_plans(vk, ctx, cfg):
+    prec = vk.Precision.F32 if cfg["prec"] == "f32" else vk.Precision.F64
+    if cfg["kind"] == "r2c_c2r":
+        f = vk.TransformIr.build(vk.FftConfig.new(cfg["dims"]).with_batch_count(cfg["batch"]).with_precision(prec)
+                                 .with_transform(vk.TransformKind.RealToComplex), vk.Direction.Forward)
+        i = vk.TransformIr.build(vk.FftConfig.new(cfg["dims"]).with_batch_count(cfg["batch"]).with_precision(prec)
+                                 .with_transform(vk.TransformKind.ComplexToReal).with_inverse_normalization(True),
+                                 vk.Direction.Inverse)
+        return [ctx.plan(f), ctx.plan(i)]
+    ir = vk.TransformIr.build(vk.FftConfig.new(cfg["dims"]).with_batch_count(cfg["batch"]).with_precision(prec),
+                              vk.Direction.Forward)
+    return [ctx.plan(ir)]
+
+
+def run_gpu(cfg, steps, warmup, rotate):
+    import torch
+
+    torch.cuda.init()  # torch's HIP runtime first: the library then binds to the same one
+    import vkfft_amd as vk
+
+    ctx = vk.HipExecutionContext(0)
+    plans = build_plans(vk, ctx, cfg)
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    # buffers: rotate pairs unless the working set is already >= 1 GiB
+    in_bytes, out_bytes = plans[0].in_bytes, plans[0].out_bytes
+    pairs = max(1, min(rotate, (1 << 30) // max(in_bytes + out_bytes, 1) + 1)) if in_bytes + out_bytes < (1 << 30) else 1
+    bufs = []
+    for _ in range(pairs):
+        x = torch.rand(in_bytes // 4, device="cuda", generator=gen, dtype=torch.float32) * 2 - 1
+        y = torch.empty(out_bytes // 4, device="cuda", dtype=torch.float32)
+        z = torch.empty(in_bytes // 4, device="cuda", dtype=torch.float32) if len(plans) == 2 else None
+        bufs.append((x, y, z))
+    s = stream.cuda_stream
+
+    def step(i):
+        x, y, z = bufs[i % pairs]
+        plans[0].execute(x.data_ptr(), y.data_ptr(), 0, s)
+        if len(plans) == 2:
+            plans[1].execute(y.data_ptr(), z.data_ptr(), 0, s)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    # per-launch durations of the dominant (first) kernel, events around single launches
+    launches = [p.describe() for p in plans]
+    per_launch = []
+    if len(plans[0].describe()["passes"]) == 1 and len(plans) == 1:
+        per_launch = [total_ms / steps]
+    else:
+        evs = []
+        for i in range(min(steps, 20)):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            x, y, _ = bufs[i % pairs]
+            a.record(stream)
+            plans[0].execute(x.data_ptr(), y.data_ptr(), 0, s)
+            b.record(stream)
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        per_launch = [a.elapsed_time(b) for a, b in evs]
+    info = {"device": ctx.device_name(), "profile": ctx.device_profile(), "plans": launches, "pairs": pairs}
+    ctx.close()
+    return total_ms / steps, sum(per_launch) / len(per_launch), info
+
+
+def cpu_baseline(cfg, budget_s=15.0):
+    """The oracle (C port of reference.rs, f64) on a bounded batch sample."""
+    import numpy as np
+
+    from oracle import oracle as o
+
+    threads = min(16, os.cpu_count() or 1)
+    n = 1
+    for d in cfg["dims"]:
+        n *= d
+    if len(cfg["dims"]) > 1 or cfg["kind"] != "c2c":
+        return None
+    # time one transform to size the sample to about budget_s of CPU work
+    x1 = o.complex_uniform(n, 1, np.complex128)
+    t0 = time.perf_counter()
+    o.fft(x1)
+    per = max(time.perf_counter() - t0, 1e-6)
+    sample = int(max(threads, min(cfg["batch"], budget_s / per)))
+    sample -= sample % threads or 0
+    sample = max(sample, threads)
+    x = o.complex_uniform(n * sample, 2, np.complex128)
+    t0 = time.perf_counter()
+    o.fft_batch(x, n, threads=threads)
+    wall = time.perf_counter() - t0
+    bytes_sample = 2 * n * sample * (8 if cfg["prec"] == "f32" else 16)
+    return {"value": round(bytes_sample / wall / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{sample} of {cfg['batch']} transforms of N={n}, oracle (reference.rs port, f64), "
+                      f"{wall:.2f} s wall on {threads} threads ({per * sample:.1f} s CPU work est.)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c1", choices=sorted(CONFIGS))
+    ap.add_argument("--all", action="store_true", help="one line per BASELINE config")
+    ap.add_argument("--rotate", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+    names = list(CONFIGS) if args.all else [args.config]
+    for name in names:
+        cfg = CONFIGS[name]
+        steps = args.steps if name == "c1" else max(5, min(args.steps, 30))
+        ms, launch_ms, info = run_gpu(cfg, steps, args.warmup, args.rotate)
+        nbytes, flops = algorithmic(cfg)
+        value = nbytes / (ms * 1e-3) / 1e9
+        first = info["plans"][0]["passes"]
+        dom_bytes = nbytes if (len(first) == 1 and len(info["plans"]) == 1) else None
+        roof = None
+        if dom_bytes:
+            ach = dom_bytes / (launch_ms * 1e-3) / 1e9
+            roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                    "kernel": first[0]["kernel"], "launch_ms": round(launch_ms, 5)}
+        out = {
+            "metric": "batched f32 C2C effective HBM GB/s (2*N*batch*bytes/time)",
+            "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32" if cfg["prec"] == "f32" else "f64", "data": "synthetic uniform[-1,1) (torch, seeded)",
+            "config": {"workload": cfg["workload"], "dims": cfg["dims"], "batch": cfg["batch"],
+                       "buffer_pairs": info["pairs"]},
+            "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+            "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
+            "roofline": roof,
+            "cpu_baseline": None if (args.no_cpu or name != "c1") else cpu_baseline(cfg),
+            "device": info["device"],
+        }
+        print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,168 @@
+/*
+ * vkfx.h -- C ABI of the MI355X (gfx950) batched-FFT execution library.
+ *
+ * This is the drop-in boundary below vkfft-rs's `NativeRuntime` HIP backend.
+ * A Rust `HipNativeRuntime` binds these symbols and forwards
+ * `execute_transform_f32/f64` and `submit_transform_*` to them instead of
+ * lowering `TransformIr` to HIP source and JIT-compiling it with HIPRTC.
+ * Citations are vkfft-rs paths (file:line) of the interface each entry
+ * replaces. No HIP or torch types appear in the signatures: device buffers
+ * and streams are passed as plain pointers.
+ *
+ * Layout conventions (vkfft-rs `Complex<T>` is #[repr(C)] {re, im},
+ * src/complex.rs:4-9):
+ *   - complex data is interleaved {re, im} of the plan precision;
+ *   - dims are in vkfft-rs order, slowest to fastest (src/config.rs:662-666),
+ *     the last dim contiguous, batches back to back;
+ *   - R2C input is real (n reals per batch), output n/2+1 complex per batch;
+ *     C2R is the reverse (src/program_ir.rs:6679-6711);
+ *   - forward uses exp(-2 pi i jk/n); inverse exp(+2 pi i jk/n), scaled by
+ *     1/n only when `normalize` is set (src/config.rs:10-15, 691).
+ */
+#ifndef VKFX_H
+#define VKFX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. 0 = success. Negative values map onto vkfft-rs `VkFftError`
+ * variants (src/error.rs:6-57); vkfx_last_error() holds the message. */
+enum vkfx_status {
+    VKFX_OK = 0,
+    VKFX_ERR_NATIVE_UNAVAILABLE = -1,      /* NativeUnavailable{backend:"HIP"} */
+    VKFX_ERR_NATIVE_RUNTIME = -2,          /* NativeRuntime{message}: a hipError_t */
+    VKFX_ERR_UNSUPPORTED_KERNEL_PATH = -3, /* UnsupportedKernelPath */
+    VKFX_ERR_UNSUPPORTED_PRECISION = -4,   /* UnsupportedPrecision */
+    VKFX_ERR_INPUT_LENGTH_MISMATCH = -5,   /* InputLengthMismatch{expected, actual} */
+    VKFX_ERR_RESOURCE_LIMIT = -6,          /* ResourceLimitExceeded */
+    VKFX_ERR_INVALID_ARGUMENT = -7,        /* InvalidKernelIr / ZeroLength / invalid config */
+    VKFX_ERR_ARITHMETIC_OVERFLOW = -8      /* ArithmeticOverflow */
+};
+
+enum vkfx_transform { VKFX_C2C = 0, VKFX_R2C = 1, VKFX_C2R = 2 }; /* TransformKind, config.rs */
+enum vkfx_precision { VKFX_F32 = 0, VKFX_F64 = 1 };              /* Precision::{F32,F64} */
+enum vkfx_direction { VKFX_FORWARD = -1, VKFX_INVERSE = 1 };     /* Direction::exponent_sign */
+enum vkfx_algorithm {                                            /* AxisAlgorithm, planner.rs:46-59 */
+    VKFX_ALG_STOCKHAM = 0,
+    VKFX_ALG_RADER = 1,
+    VKFX_ALG_BLUESTEIN = 2
+};
+
+#define VKFX_MAX_RANK 4
+
+typedef struct vkfx_context vkfx_context;
+typedef struct vkfx_plan vkfx_plan;
+
+/* DeviceProfile fields the planner and the kernels depend on
+ * (src/config.rs:250-265; HIP query at src/backend/hip/runtime.rs:369-406). */
+typedef struct {
+    uint64_t shared_memory_bytes;      /* hipDeviceAttributeMaxSharedMemoryPerBlock */
+    uint64_t shared_memory_pow2_bytes; /* largest power of two <= shared_memory_bytes */
+    uint64_t max_threads_per_block;
+    uint64_t warp_size;
+    uint64_t compute_units;
+    uint64_t global_memory_bytes;
+    char name[256];
+    char arch[64];
+} vkfx_device_profile;
+
+/* Plan descriptor: the part of `TransformIr` (src/application.rs:48-167) the
+ * kernels need, plus the planner's per-axis decision so the library executes
+ * exactly what vkfft-rs planned (src/planner.rs:168-241). With
+ * use_library_planner = 1 the library fills axis_algorithm/convolution_len
+ * itself from its restatement of the planner (vkfx_planner_axis). */
+typedef struct {
+    uint32_t rank;                          /* 1..VKFX_MAX_RANK */
+    uint64_t dims[VKFX_MAX_RANK];           /* FftConfig::dimensions, slowest..fastest */
+    uint64_t batch;                         /* FftConfig::batch_count (>= 1) */
+    int32_t transform;                      /* vkfx_transform */
+    int32_t precision;                      /* vkfx_precision */
+    int32_t direction;                      /* vkfx_direction; R2C forward, C2R inverse */
+    int32_t normalize;                      /* FftConfig::normalize_inverse */
+    int32_t use_library_planner;            /* 1 = plan axes here */
+    int32_t axis_algorithm[VKFX_MAX_RANK];  /* vkfx_algorithm per axis */
+    uint64_t convolution_len[VKFX_MAX_RANK];/* Bluestein M per axis (0 = not Bluestein) */
+} vkfx_plan_desc;
+
+/* ---------------------------------------------------------------- context */
+
+/* HipExecutionContext::new(device_index) (src/backend/hip/runtime.rs:1643-1656,
+ * 2349-2431): selects the device, reads its profile, creates one stream of
+ * default priority. Fails with VKFX_ERR_NATIVE_UNAVAILABLE without a GPU. */
+int vkfx_context_create(int device_index, vkfx_context **out);
+int vkfx_context_destroy(vkfx_context *ctx);
+
+/* NativeRuntime::device_profile / device_name (src/backend/native_runtime.rs:162-166). */
+int vkfx_context_profile(const vkfx_context *ctx, vkfx_device_profile *out);
+
+/* ------------------------------------------------------------------- plan */
+
+/* Replaces NativeSourceBackend::lower_transform + the HIPRTC compile/module
+ * caches (src/backend/native.rs:696-746, src/backend/hip/runtime.rs:742-800,
+ * 2109-2195): builds the kernel-launch list, uploads twiddle/chirp/spectrum
+ * tables and allocates the plan's workspace once. */
+int vkfx_plan_create(vkfx_context *ctx, const vkfx_plan_desc *desc, vkfx_plan **out);
+int vkfx_plan_destroy(vkfx_plan *plan);
+
+/* Byte sizes of one execute's input and output buffers, and of the scratch
+ * a caller may pass to vkfx_execute (0 when the plan needs none). */
+int vkfx_plan_io_bytes(const vkfx_plan *plan, uint64_t *in_bytes, uint64_t *out_bytes);
+int vkfx_plan_workspace_bytes(const vkfx_plan *plan, uint64_t *out);
+
+/* Writes a JSON description of the plan (axes, algorithms, Bluestein M,
+ * four-step splits, kernel passes with grid/block/LDS) into buf. Returns the
+ * number of bytes needed (excluding the NUL), or a negative status. */
+int vkfx_plan_describe(const vkfx_plan *plan, char *buf, size_t cap);
+
+/* ---------------------------------------------------------------- execute */
+
+/* Device-resident asynchronous execute on `stream` (a hipStream_t; NULL = the
+ * context's stream). Replaces HipExecutionContext::submit_prepared's kernel
+ * launches (src/backend/hip/runtime.rs:1998-2107) without host copies.
+ * d_in and d_out may alias for C2C (in place). d_work may be NULL, in which
+ * case the plan's own workspace is used. */
+int vkfx_execute(vkfx_plan *plan, const void *d_in, void *d_out, void *d_work, void *stream);
+
+/* Host round trip, the contract of NativeRuntime::execute_transform_f32/f64
+ * (src/backend/native_runtime.rs:339-359): copies h_in to the device,
+ * executes, copies the result to h_out and synchronises. Sizes are checked
+ * against the plan (VKFX_ERR_INPUT_LENGTH_MISMATCH, native_runtime.rs:1262-1270). */
+int vkfx_execute_host(vkfx_plan *plan, const void *h_in, uint64_t in_bytes, void *h_out, uint64_t out_bytes);
+
+/* Waits for all work on the context's stream (ticket wait,
+ * src/backend/hip/runtime.rs:1530-1608). */
+int vkfx_context_synchronize(vkfx_context *ctx);
+
+/* Thread-local message of the last failing call on this thread. */
+const char *vkfx_last_error(void);
+
+/* Library version string. */
+const char *vkfx_version(void);
+
+/* ---------------------------------------------------- planner restatement */
+
+/* plan_c2c_axis_algorithm_for_device for the HIP/AMD profile
+ * (src/planner.rs:349-440) with PlannerTuning::for_device (src/config.rs:395-420).
+ * axis_is_strided: 0 for the contiguous (last) dimension. allow_recursive_rader
+ * mirrors PlannerTuning::with_recursive_fft_rader. Outputs the algorithm and,
+ * for Bluestein, the convolution length M (upstream_bluestein_auto_padding,
+ * src/scheduler.rs:361-373). */
+int vkfx_planner_axis(uint64_t len, uint64_t batch, int32_t precision, int32_t axis_is_strided,
+                      int32_t allow_recursive_rader, uint64_t shared_memory_bytes,
+                      int32_t *algorithm, uint64_t *convolution_len);
+
+/* upstream_bluestein_auto_padding for HIP/AMD (src/scheduler.rs:225-373). */
+int vkfx_planner_bluestein_padding(uint64_t len, uint64_t batch, int32_t precision,
+                                   uint64_t shared_memory_bytes, uint64_t *padded);
+
+/* planner::next_smooth_at_least over {2,3,5,7} (src/planner.rs:684-733). */
+uint64_t vkfx_planner_next_smooth(uint64_t target);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VKFX_H */

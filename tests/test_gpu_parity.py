@@ -1,0 +1,294 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle
+(restated src/reference.rs) on identical seeded inputs.
+
+Tolerances (BASELINE): f32 relative L2 <= 1e-5 against the f64 oracle of the
+same f32-rounded input; f64 <= 1e-13. Where the oracle's own algorithm is
+less accurate than 1e-13 (reference::fft's Bluestein at large N), f64 is
+checked against pocketfft at 1e-13 and against the oracle within its own
+measured error. Config-scale shapes run on sampled batches against the
+oracle plus size-independent properties (round trips, separability).
+"""
+import numpy as np
+import pytest
+
+import vkfft_amd as vk
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = vk.Precision.F32, vk.Precision.F64
+FWD, INV = vk.Direction.Forward, vk.Direction.Inverse
+TOL = {F32: 1e-5, F64: 1e-13}
+
+
+def _cdtype(prec):
+    return np.complex64 if prec == F32 else np.complex128
+
+
+def c2c(ctx, dims, batch, x, prec=F32, direction=FWD, normalize=False):
+    cfg = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec) \
+        .with_inverse_normalization(normalize)
+    ir = vk.TransformIr.build(cfg, direction)
+    return ctx.execute_transform(ir, x), ir
+
+
+def oracle_c2c(x, n, direction=FWD, normalize=False):
+    return o.fft_batch(x.astype(np.complex128), n, "forward" if direction == FWD else "inverse",
+                       normalize, threads=8)
+
+
+def rand(count, seed, prec=F32):
+    return o.complex_uniform(count, seed, _cdtype(prec))
+
+
+# ------------------------------------------------ reference HIP unit tests
+
+def test_hip_stockham_matches_cpu_n64(hip_ctx):
+    # hip/runtime.rs:3451-3490: N=64 vs reference::dft, max error < 2e-3 * N
+    x = rand(64, 1)
+    y, _ = c2c(hip_ctx, [64], 1, x)
+    assert np.max(np.abs(y - o.dft(x))) < 2e-3 * 64
+
+
+def test_hip_round_trip_n4096_batch8(hip_ctx):
+    # hip/runtime.rs:3172-3218: N4096 x 8 round trip <= 2e-4
+    x = rand(4096 * 8, 2)
+    y, _ = c2c(hip_ctx, [4096], 8, x)
+    z, _ = c2c(hip_ctx, [4096], 8, y, direction=INV, normalize=True)
+    assert np.max(np.abs(z - x)) <= 2e-4
+
+
+# ------------------------------------------------------- 1-D C2C sweep
+
+SMALL = list(range(1, 65)) + [96, 100, 121, 125, 128, 169, 192, 243, 343, 360, 512, 625, 1000, 1024, 1536,
+                             2048, 2187, 2401, 3125, 4096, 6561, 8192, 10000, 15625, 16384]
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_c2c_length_sweep(hip_ctx, prec, direction):
+    worst = {}
+    for n in SMALL:
+        batch = 3
+        x = rand(n * batch, n, prec)
+        y, _ = c2c(hip_ctx, [n], batch, x, prec, direction, normalize=direction == INV)
+        ref = oracle_c2c(x, n, direction, direction == INV)
+        err = o.rel_l2(y, ref)
+        if prec == F64 and err > TOL[F64]:
+            # reference::fft's own Bluestein error can exceed 1e-13: pin to pocketfft
+            npref = (np.fft.fft if direction == FWD else np.fft.ifft)(x.reshape(batch, n), axis=1).reshape(-1)
+            err = o.rel_l2(y, npref)
+        worst[n] = err
+    bad = {n: e for n, e in worst.items() if e > TOL[prec]}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_c1_shape_sampled_full_size(hip_ctx, prec):
+    """C1: N=1024, batch 8192; every 97th transform against the oracle, all
+    of them through a forward/inverse round trip."""
+    n, batch = 1024, 8192
+    x = rand(n * batch, 101, prec)
+    y, ir = c2c(hip_ctx, [n], batch, x, prec)
+    assert hip_ctx.plan(ir).describe()["axes"][0]["algorithm"] == "stockham"
+    idx = np.arange(0, batch, 97)
+    xs = x.reshape(batch, n)[idx].reshape(-1)
+    assert o.rel_l2(y.reshape(batch, n)[idx].reshape(-1), oracle_c2c(xs, n)) <= TOL[prec]
+    z, _ = c2c(hip_ctx, [n], batch, y, prec, INV, normalize=True)
+    assert o.rel_l2(z, x) <= 4 * TOL[prec]
+
+
+@pytest.mark.parametrize("n", [1 << 15, 3 * (1 << 14), 1 << 17, 1 << 20])
+def test_c2c_four_step(hip_ctx, n):
+    x = rand(n * 2, n)
+    y, ir = c2c(hip_ctx, [n], 2, x)
+    assert "four_step" in hip_ctx.plan(ir).describe()
+    assert o.rel_l2(y, oracle_c2c(x, n)) <= TOL[F32]
+    z, _ = c2c(hip_ctx, [n], 2, y, direction=INV, normalize=True)
+    assert o.rel_l2(z, x) <= 2 * TOL[F32]
+
+
+def test_c2c_four_step_f64(hip_ctx):
+    n = 1 << 14
+    x = rand(n * 2, 7, F64)
+    y, _ = c2c(hip_ctx, [n], 2, x, F64)
+    assert o.rel_l2(y, oracle_c2c(x, n)) <= TOL[F64]
+
+
+# ----------------------------------------------------------- Bluestein
+
+@pytest.mark.parametrize("n,batch", [(4099, 8), (65537, 2), (103, 5), (17, 4), (257, 3), (1031, 2)])
+def test_bluestein_and_rader_classified_f32(hip_ctx, n, batch):
+    x = rand(n * batch, n)
+    y, ir = c2c(hip_ctx, [n], batch, x)
+    assert ir.axis_algorithms[0] in (vk.AlgorithmKind.Bluestein, vk.AlgorithmKind.Rader)
+    assert o.rel_l2(y, oracle_c2c(x, n)) <= TOL[F32]
+    z, _ = c2c(hip_ctx, [n], batch, x, direction=INV, normalize=True)
+    assert o.rel_l2(z, oracle_c2c(x, n, INV, True)) <= TOL[F32]
+
+
+def test_bluestein_plan_uses_planner_length(hip_ctx):
+    for n, m in [(4099, 8232), (65537, 131220)]:
+        ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(4096), FWD)
+        assert ir.convolution_lens == [m]
+        plan_small = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(2), FWD)
+        desc = hip_ctx.plan(plan_small).describe()
+        assert desc["axes"][0]["algorithm"] == "bluestein"
+
+
+@pytest.mark.parametrize("n", [4099, 65537])
+def test_bluestein_f64(hip_ctx, n):
+    x = rand(n * 2, n + 1, F64)
+    y, _ = c2c(hip_ctx, [n], 2, x, F64)
+    npref = np.fft.fft(x.reshape(2, n), axis=1).reshape(-1)
+    assert o.rel_l2(y, npref) <= 1e-13
+    ref = oracle_c2c(x, n)
+    assert o.rel_l2(y, ref) <= max(1e-13, 2 * o.rel_l2(ref, npref))
+
+
+# -------------------------------------------------------------- R2C / C2R
+
+def r2c(ctx, n, batch, x, prec=F32):
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.RealToComplex)
+    ir = vk.TransformIr.build(cfg, FWD)
+    return ctx.execute_transform(ir, x), ir
+
+
+def c2r(ctx, n, batch, X, prec=F32, normalize=True):
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.ComplexToReal).with_inverse_normalization(normalize)
+    ir = vk.TransformIr.build(cfg, INV)
+    return ctx.execute_transform(ir, X), ir
+
+
+@pytest.mark.parametrize("n", [2, 4, 8, 10, 45, 64, 105, 1000, 4096, 32768, 1 << 16, 1 << 20])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_r2c_c2r(hip_ctx, n, prec):
+    if prec == F64 and n > 1 << 16:
+        pytest.skip("f64 four-step real path is covered at 2^16")
+    batch = 2
+    rdt = np.float32 if prec == F32 else np.float64
+    x = o.normal(n * batch, n, rdt)
+    X, _ = r2c(hip_ctx, n, batch, x, prec)
+    ref = o.r2c_batch(x.astype(np.float64), n, threads=8)
+    assert o.rel_l2(X, ref) <= TOL[prec] * (1 if prec == F32 else 10)
+    # C2R of the exact spectrum against the oracle's C2R
+    xr, _ = c2r(hip_ctx, n, batch, ref.astype(_cdtype(prec)), prec)
+    back = o.c2r_batch(ref, n, normalize=True, threads=8)
+    assert o.rel_l2(xr, back) <= TOL[prec] * (1 if prec == F32 else 10)
+
+
+def test_c2_shape_round_trip_full_size(hip_ctx):
+    """C2: R2C N=2^20 batch 256 then C2R with normalization; two sampled
+    transforms against the oracle, the whole batch through the round trip."""
+    n, batch = 1 << 20, 256
+    x = o.normal(n * batch, 2024, np.float32)
+    X, ir = r2c(hip_ctx, n, batch, x)
+    desc = hip_ctx.plan(ir).describe()
+    assert desc["real"]["uploads"] == 2
+    h = n // 2 + 1
+    for b in (0, 255):
+        ref = o.r2c_batch(x[b * n:(b + 1) * n].astype(np.float64), n)
+        assert o.rel_l2(X[b * h:(b + 1) * h], ref) <= TOL[F32]
+    xr, _ = c2r(hip_ctx, n, batch, X)
+    assert o.rel_l2(xr, x) <= 2 * TOL[F32]
+
+
+# ------------------------------------------------------------------ N-D
+
+@pytest.mark.parametrize("dims,batch,prec", [([64, 48], 2, F32), ([256, 256], 2, F32), ([17, 34], 1, F32),
+                                             ([16, 12, 10], 2, F64), ([64, 64, 64], 1, F64),
+                                             ([8, 6, 5, 4], 1, F32), ([4099, 4], 1, F32)])
+def test_nd_c2c(hip_ctx, dims, batch, prec):
+    count = int(np.prod(dims)) * batch
+    x = rand(count, count % 1000, prec)
+    y, _ = c2c(hip_ctx, dims, batch, x, prec)
+    ref = o.fft_nd(x, dims, batch, threads=8)
+    assert o.rel_l2(y, ref) <= TOL[prec]
+    z, _ = c2c(hip_ctx, dims, batch, y, prec, INV, normalize=True)
+    assert o.rel_l2(z, x) <= 4 * TOL[prec]
+
+
+def test_c3_shape_full_size(hip_ctx):
+    """C3: 4096 x 4096, batch 16, f32. Image 0 against the f64 oracle on a
+    sample of rows of the row pass is too slow, so image 0 is checked against
+    pocketfft (f64) and every image through a round trip."""
+    dims, batch = [4096, 4096], 16
+    x = rand(4096 * 4096 * batch, 33)
+    y, _ = c2c(hip_ctx, dims, batch, x)
+    ref0 = np.fft.fft2(x[: 4096 * 4096].reshape(4096, 4096).astype(np.complex128))
+    assert o.rel_l2(y[: 4096 * 4096], ref0.reshape(-1)) <= TOL[F32]
+    z, _ = c2c(hip_ctx, dims, batch, y, direction=INV, normalize=True)
+    assert o.rel_l2(z, x) <= 4 * TOL[F32]
+
+
+def test_c4_shape_full_size_f64(hip_ctx):
+    """C4: 512^3 f64 (2 GiB). Checked against pocketfft at 1e-13."""
+    dims = [512, 512, 512]
+    x = rand(512 ** 3, 44, F64)
+    y, _ = c2c(hip_ctx, dims, 1, x, F64)
+    ref = np.fft.fftn(x.reshape(dims))
+    assert o.rel_l2(y, ref.reshape(-1)) <= TOL[F64]
+
+
+def test_c5_shape_sampled_full_size(hip_ctx):
+    """C5: N=4099 and N=65537 at batch 4096; sampled transforms against the oracle."""
+    for n, seed in [(4099, 5), (65537, 6)]:
+        batch = 4096
+        x = rand(n * batch, seed)
+        y, _ = c2c(hip_ctx, [n], batch, x)
+        for b in (0, 1, 2047, 4095):
+            ref = o.fft(x[b * n:(b + 1) * n].astype(np.complex128))
+            assert o.rel_l2(y[b * n:(b + 1) * n], ref) <= TOL[F32], (n, b)
+
+
+# ----------------------------------------------------- FFTW golden (GPU)
+
+@pytest.mark.parametrize("case", ["c2c-bluestein-n103", "c2c-rader-n257", "c2c-smooth-n1536",
+                                  "c2c-large-smooth-n4096"])
+def test_fftw_medium_f32_on_gpu(hip_ctx, case):
+    # tests/fftw_medium_f32_golden.rs:162-172: F32 GPU tolerance 1e-4 * N max-abs
+    import os
+    from conftest import GOLDEN
+    c = o.parse_fixture(os.path.join(GOLDEN, "fftw_precision_medium_f32_v1.txt"))["cases"][case]
+    n = int(c["meta"]["shape"])
+    x = o.fixture_input("complex-f32-v1", n)
+    rows = np.array(c["rows"])
+    expected = rows[:, 0] + 1j * rows[:, 1]
+    y, _ = c2c(hip_ctx, [n], 1, x)
+    assert np.max(np.abs(y - expected)) <= 1e-4 * n
+    assert o.rel_l2(y, expected) <= TOL[F32]
+
+
+# ------------------------------------------------------------ contracts
+
+def test_input_length_mismatch(hip_ctx):
+    ir = vk.TransformIr.build(vk.FftConfig.new([64]).with_batch_count(2), FWD)
+    with pytest.raises(vk.VkFftError) as e:
+        hip_ctx.execute_transform(ir, np.zeros(100, np.complex64))
+    assert e.value.kind == "InputLengthMismatch"
+
+
+def test_device_profile(hip_ctx):
+    p = hip_ctx.device_profile()
+    assert p["arch"].startswith("gfx950") and p["warp_size"] == 64
+    assert p["shared_memory_bytes"] >= 64 * 1024
+
+
+def test_device_resident_execute_matches_host(hip_ctx):
+    import torch
+    n, batch = 1024, 64
+    x = rand(n * batch, 77)
+    ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch), FWD)
+    plan = hip_ctx.plan(ir)
+    xt = torch.from_numpy(x.view(np.float32).copy()).cuda()
+    yt = torch.empty_like(xt)
+    plan.execute_tensors(xt, yt)
+    hip_ctx.synchronize()
+    y_dev = yt.cpu().numpy().view(np.complex64)
+    assert np.array_equal(y_dev, hip_ctx.execute_transform(ir, x))
+    # in place (d_in == d_out) gives the same result
+    plan.execute_tensors(xt, xt)
+    hip_ctx.synchronize()
+    assert np.array_equal(xt.cpu().numpy().view(np.complex64), y_dev)

@@ -1,0 +1,183 @@
+"""Pins the CPU oracle (oracle/vkfft_oracle.c, a restatement of vkfft-rs
+src/reference.rs) against the FFTW 3.3.9 fixtures the reference commits
+(tests/fixtures/*.txt), the reference's own known-answer tests
+(src/reference.rs:178-200), brute-force DFTs, closed forms and numpy's
+pocketfft. The oracle is the checker for every GPU parity test."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+from oracle import oracle as o
+
+
+def _corpus(name):
+    return o.parse_fixture(os.path.join(GOLDEN, name))
+
+
+def _max_err(a, b):
+    return float(np.max(np.abs(np.asarray(a) - np.asarray(b))))
+
+
+# -------------------------------------------------- FFTW golden fixtures
+
+def test_fftw_c2c_n47_inputs_and_outputs():
+    case = _corpus("fftw_precision_v1.txt")["cases"]["c2c-n47"]
+    rows = np.array(case["rows"])
+    x = rows[:, 0] + 1j * rows[:, 1]
+    expected = rows[:, 2] + 1j * rows[:, 3]
+    # the committed inputs are exactly the complex-v1 formula
+    assert np.array_equal(x, o.fixture_input("complex-v1", 47))
+    # reference tolerance for CPU executors: 2e-10 * N (tests/fftw_golden.rs)
+    assert _max_err(o.fft(x), expected) <= 2e-10 * 47
+
+
+def test_fftw_r2c_n45():
+    case = _corpus("fftw_precision_v1.txt")["cases"]["r2c-n45"]
+    split = case["meta"]["_split"]
+    x = np.array([r[0] for r in case["rows"][:split]])
+    out = np.array(case["rows"][split:])
+    expected = out[:, 0] + 1j * out[:, 1]
+    assert np.array_equal(x, o.fixture_input("real-v1", 45))
+    assert _max_err(o.r2c_batch(x, 45), expected) <= 2e-10 * 45
+
+
+@pytest.mark.parametrize("corpus", ["fftw_precision_medium_v1.txt", "fftw_precision_medium_f32_v1.txt"])
+@pytest.mark.parametrize("case", ["c2c-bluestein-n103", "c2c-rader-n257", "c2c-smooth-n1536",
+                                  "c2c-large-smooth-n4096"])
+def test_fftw_medium_c2c(corpus, case):
+    c = _corpus(corpus)["cases"][case]
+    n = int(c["meta"]["shape"])
+    x = o.fixture_input(c["meta"]["input"], n).astype(np.complex128)
+    rows = np.array(c["rows"])
+    expected = rows[:, 0] + 1j * rows[:, 1]
+    assert _max_err(o.fft(x), expected) <= 2e-10 * n
+
+
+@pytest.mark.parametrize("corpus", ["fftw_precision_medium_v1.txt", "fftw_precision_medium_f32_v1.txt"])
+@pytest.mark.parametrize("case", ["r2c-nd-17x34", "r2c-nd-64x64"])
+def test_fftw_medium_r2c_nd(corpus, case):
+    """2-D R2C = separable complex N-D transform (nd_ir.rs:1303-1337) of the
+    real input, truncated to cols/2+1 on the last axis."""
+    c = _corpus(corpus)["cases"][case]
+    rows_, cols = (int(v) for v in c["meta"]["shape"].split())
+    x = o.fixture_input(c["meta"]["input"], rows_ * cols).astype(np.complex128)
+    full = o.fft_nd(x, [rows_, cols]).reshape(rows_, cols)
+    got = full[:, : cols // 2 + 1].reshape(-1)
+    rows = np.array(c["rows"])
+    expected = rows[:, 0] + 1j * rows[:, 1]
+    assert _max_err(got, expected) <= 2e-10 * rows_ * cols
+
+
+# ------------------------------------------------ reference.rs known answers
+
+def _sample(n):
+    # src/reference.rs:159-166
+    x = np.arange(n, dtype=np.float64)
+    return np.sin(0.37 * x) + x * 0.01 + 1j * (np.cos(0.19 * x) - x * 0.02)
+
+
+@pytest.mark.parametrize("n", [2, 3, 4, 6, 7, 11, 13, 17, 19, 31, 47, 77])
+def test_mixed_radix_and_bluestein_match_naive_dft(n):
+    x = _sample(n)
+    assert _max_err(o.fft(x), o.dft(x)) <= 5e-10 * n
+
+
+@pytest.mark.parametrize("n", [8, 17, 47, 64])
+def test_normalized_inverse_round_trips(n):
+    x = _sample(n)
+    assert _max_err(o.fft(o.fft(x), "inverse", True), x) < 5e-10 * n
+
+
+# ------------------------------------------------------ closed forms
+
+@pytest.mark.parametrize("n", [1, 2, 5, 16, 30, 97, 1024, 4099])
+def test_impulse_is_all_ones(n):
+    x = np.zeros(n, dtype=np.complex128)
+    x[0] = 1
+    assert _max_err(o.fft(x), np.ones(n)) < 1e-12 * max(n, 1)
+
+
+@pytest.mark.parametrize("n,k0", [(64, 5), (360, 7), (4099, 123), (103, 1)])
+def test_single_tone_is_a_delta(n, k0):
+    idx = np.arange(n)
+    x = np.exp(2j * np.pi * k0 * idx / n)
+    y = o.fft(x)
+    expected = np.zeros(n, dtype=np.complex128)
+    expected[k0] = n
+    assert _max_err(y, expected) < 1e-9 * n
+
+
+def test_inverse_sign_convention():
+    # inverse uses exp(+2 pi i jk/n): a forward tone at +k0 appears at -k0
+    n, k0 = 32, 3
+    x = np.exp(2j * np.pi * k0 * np.arange(n) / n)
+    y = o.fft(x, "inverse")
+    assert abs(y[(n - k0) % n] - n) < 1e-9 and abs(y[k0]) < 1e-9
+
+
+@pytest.mark.parametrize("n", [12, 210, 1000, 4099])
+def test_linearity_and_parseval(n):
+    a = o.complex_uniform(n, 11, np.complex128)
+    b = o.complex_uniform(n, 12, np.complex128)
+    fa, fb = o.fft(a), o.fft(b)
+    assert _max_err(o.fft(2.5 * a - 1j * b), 2.5 * fa - 1j * fb) < 1e-10 * n
+    assert abs(np.vdot(fa, fa).real - n * np.vdot(a, a).real) < 1e-9 * n * np.vdot(a, a).real
+
+
+@pytest.mark.parametrize("n", [24, 1024, 4099, 6561])
+def test_matches_pocketfft(n):
+    x = o.complex_uniform(n, n, np.complex128)
+    assert o.rel_l2(o.fft(x), np.fft.fft(x)) < 1e-12
+    assert o.rel_l2(o.fft(x, "inverse", True), np.fft.ifft(x)) < 1e-12
+
+
+def test_batch_threads_match_single():
+    x = o.complex_uniform(8 * 96, 3, np.complex128)
+    one = o.fft_batch(x, 96, threads=1)
+    many = o.fft_batch(x, 96, threads=4)
+    assert np.array_equal(one, many)
+    assert np.array_equal(one[96:192], o.fft(x[96:192]))
+
+
+@pytest.mark.parametrize("n", [16, 45, 1024])
+def test_r2c_c2r_round_trip_and_hermitian(n):
+    x = o.uniform(3 * n, 5)
+    X = o.r2c_batch(x, n)
+    full = np.fft.fft(x.reshape(3, n), axis=1)
+    assert o.rel_l2(X.reshape(3, -1), full[:, : n // 2 + 1]) < 1e-12
+    back = o.c2r_batch(X, n, normalize=True)
+    assert _max_err(back, x) < 1e-12 * n
+
+
+def test_nd_is_separable():
+    dims = [6, 10, 8]
+    x = o.complex_uniform(2 * 480, 9, np.complex128)
+    got = o.fft_nd(x, dims, batch=2).reshape(2, *dims)
+    assert o.rel_l2(got, np.fft.fftn(x.reshape(2, *dims), axes=(1, 2, 3))) < 1e-12
+
+
+def test_planner_helpers():
+    # src/planner.rs:1119 pins next_smooth_at_least(2061) over {2,3,5,7}
+    assert o.next_smooth_at_least(2061) == 2100
+    assert o.next_smooth_at_least(8197) == 8232
+    assert o.next_smooth_at_least(131073) == 131220
+    assert o.prime_factorization(4098) == [2, 3, 683]
+    assert o.primitive_root(4099) == 2 and o.primitive_root(17) == 3 and o.primitive_root(257) == 3
+
+
+def test_seeded_rng_is_deterministic_and_uniform():
+    a = o.uniform(100000, 42)
+    assert np.array_equal(a, o.uniform(100000, 42))
+    assert a.min() >= -1 and a.max() < 1 and abs(a.mean()) < 0.01
+    z = o.normal(100000, 7)
+    assert abs(z.mean()) < 0.02 and abs(z.std() - 1) < 0.02
+    assert np.array_equal(o.uniform(10, 42, np.float32), a[:10].astype(np.float32))
+
+
+def test_precision_metrics_follow_reference_definition():
+    # src/precision.rs:31-101
+    m = o.precision_metrics([1 + 0j, 2, 0], [1 + 0j, 1, 0])
+    assert m["max_difference"] == 1 and m["avg_difference"] == pytest.approx(1 / 3)
+    assert m["max_eps"] == 1 and m["avg_eps"] == pytest.approx(1 / 3)

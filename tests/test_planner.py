@@ -1,0 +1,69 @@
+"""Planner restatement (vkfft-rs_amd/csrc/planner.cpp) pinned against values
+the reference asserts or that follow from its tables, called through the C ABI."""
+import pytest
+
+import vkfft_amd as vk
+from oracle import oracle as o
+
+A = vk.AlgorithmKind
+
+
+def test_readme_axis_classes():
+    # README.md:39-43 / planner.rs:1095-1101: [1024, 17, 65537] -> Stockham / Rader / Bluestein
+    assert vk.planner_axis(1024)[0] == A.Stockham
+    assert vk.planner_axis(17)[0] == A.Rader
+    assert vk.planner_axis(65537)[0] == A.Bluestein
+
+
+def test_config_c5_bluestein_lengths():
+    # 4098 = 2*3*683 fails the safe-prime gate (planner.rs:498-503): Bluestein,
+    # first "good" 2357-smooth M >= 8197 (scheduler.rs:283-357)
+    assert vk.planner_axis(4099, 4096) == (A.Bluestein, 8232)
+    # 65537 pads past 2^17 = 131072 < 2N-1: first good smooth length is 131220
+    assert vk.planner_axis(65537, 4096) == (A.Bluestein, 131220)
+    assert vk.planner_axis(4099, 4096, vk.Precision.F64) == (A.Bluestein, 8232)
+
+
+def test_recursive_rader_opt_in_changes_4099():
+    # PlannerTuning::with_recursive_fft_rader (config.rs:376-379, planner.rs:414-422)
+    assert vk.planner_axis(4099, 4096, recursive_rader=True)[0] == A.Rader
+
+
+def test_bluestein_table_rows():
+    # tests/f32_bluestein_higher_axis_grouped_padding.rs:114-118: AMD p263 -> 625
+    assert vk.bluestein_padding(263, 1, vk.Precision.F32, 32 * 1024) == 625
+    # table edges (scheduler.rs:178-208): 103 in [89,129) -> 256; 3281 in [2593,3282) -> 6561
+    assert vk.bluestein_padding(103) == 256
+    assert vk.bluestein_padding(3281) == 6561
+    assert vk.bluestein_padding(3300) == 8192
+    # wide table (scheduler.rs:121-176) for F64
+    assert vk.bluestein_padding(103, 1, vk.Precision.F64) == 243
+    assert vk.bluestein_padding(1000, 1, vk.Precision.F64) == 2016
+    assert vk.bluestein_padding(1009, 1, vk.Precision.F64) == 2048
+
+
+@pytest.mark.parametrize("n", [4099, 5003, 65537, 100003, 12289])
+def test_generic_padding_is_smooth_and_long_enough(n):
+    m = vk.bluestein_padding(n, 64)
+    assert m >= 2 * n - 1
+    assert all(p in (2, 3, 5, 7) for p in o.prime_factorization(m))
+    # it is never below the plain smooth search of reference::fft
+    assert m >= o.next_smooth_at_least(2 * n - 1)
+
+
+@pytest.mark.parametrize("n,alg", [(2, A.Stockham), (13, A.Stockham), (26, A.Stockham), (34, A.Rader),
+                                   (89, A.Bluestein), (257, A.Rader), (263, A.Bluestein), (97, A.Rader)])
+def test_small_axis_classes(n, alg):
+    # direct Rader for 17 <= p < 89; FFT-Rader for safe primes (257-1 = 2^8,
+    # 97-1 = 2^5*3); Bluestein otherwise (89: 88 = 2^3*11 < 17 passes the gate?
+    # no: 89 is >= the direct cap and 88 = 8*11 has factors < 17, so FFT-Rader)
+    got = vk.planner_axis(n)[0]
+    if n == 89:
+        assert got == A.Rader
+    else:
+        assert got == alg
+
+
+def test_next_smooth_matches_oracle():
+    for t in [1, 2, 7, 11, 2061, 8197, 131073, 99991]:
+        assert vk.next_smooth_at_least(t) == o.next_smooth_at_least(t)

@@ -1,0 +1,302 @@
+// fft_device.hpp -- complex arithmetic, DFT butterflies and the LDS-resident
+// Stockham stage used by every gfx950 kernel in this library.
+//
+// Stage semantics follow vkfft-rs's Stockham definition
+// (src/kernel_ir.rs:4565-4608, docs/KERNEL_IR.md:20-37): for a stage of radix
+// R whose previous radices multiply to P, butterfly b (0 <= b < N/R) reads
+// in(i) = b + i*N/R, multiplies input i by exp(s*2*pi*i*j*i/(P*R)) with
+// j = b mod P, runs a length-R DFT and writes out(q) = j + (b-j)*R + q*P.
+// After the last stage the sequence is in natural order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "radix_constants.hpp"
+
+namespace vkfx {
+
+template <typename T>
+struct alignas(2 * sizeof(T)) cpx {
+    T re, im;
+};
+
+template <typename T>
+__device__ __forceinline__ cpx<T> mk(T r, T i) {
+    cpx<T> v;
+    v.re = r;
+    v.im = i;
+    return v;
+}
+template <typename T>
+__device__ __forceinline__ cpx<T> operator+(cpx<T> a, cpx<T> b) {
+    return mk(a.re + b.re, a.im + b.im);
+}
+template <typename T>
+__device__ __forceinline__ cpx<T> operator-(cpx<T> a, cpx<T> b) {
+    return mk(a.re - b.re, a.im - b.im);
+}
+template <typename T>
+__device__ __forceinline__ cpx<T> cmul(cpx<T> a, cpx<T> b) {
+    return mk(a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re);
+}
+// a * conj(b)
+template <typename T>
+__device__ __forceinline__ cpx<T> cmulc(cpx<T> a, cpx<T> b) {
+    return mk(a.re * b.re + a.im * b.im, a.im * b.re - a.re * b.im);
+}
+template <typename T>
+__device__ __forceinline__ cpx<T> conj(cpx<T> a) {
+    return mk(a.re, -a.im);
+}
+template <typename T>
+__device__ __forceinline__ cpx<T> scale(cpx<T> a, T s) {
+    return mk(a.re * s, a.im * s);
+}
+// (S * i) * a, S = +-1
+template <int S, typename T>
+__device__ __forceinline__ cpx<T> muli(cpx<T> a) {
+    return S > 0 ? mk(-a.im, a.re) : mk(a.im, -a.re);
+}
+// Twiddle tables hold forward roots exp(-2*pi*i*k/N); the inverse direction
+// (S = +1) uses their conjugates.
+template <int S, typename T>
+__device__ __forceinline__ cpx<T> twmul(cpx<T> a, cpx<T> w) {
+    return S < 0 ? cmul(a, w) : cmulc(a, w);
+}
+
+// ------------------------------------------------------------- butterflies
+// All butterflies compute X[q] = sum_i x[i] * exp(S*2*pi*i*i*q/R) in place.
+
+template <int S, typename T>
+__device__ __forceinline__ void dft2(cpx<T>* x) {
+    cpx<T> a = x[0];
+    x[0] = a + x[1];
+    x[1] = a - x[1];
+}
+
+template <int S, typename T>
+__device__ __forceinline__ void dft4(cpx<T>& x0, cpx<T>& x1, cpx<T>& x2, cpx<T>& x3) {
+    cpx<T> t0 = x0 + x2, t1 = x0 - x2, t2 = x1 + x3, t3 = muli<S>(x1 - x3);
+    x0 = t0 + t2;
+    x2 = t0 - t2;
+    x1 = t1 + t3;
+    x3 = t1 - t3;
+}
+
+template <int S, typename T>
+__device__ __forceinline__ void dft8(cpx<T>* x) {
+    cpx<T> e0 = x[0], e1 = x[2], e2 = x[4], e3 = x[6];
+    cpx<T> o0 = x[1], o1 = x[3], o2 = x[5], o3 = x[7];
+    dft4<S>(e0, e1, e2, e3);
+    dft4<S>(o0, o1, o2, o3);
+    const T c = (T)0.707106781186547524400844362104849039;
+    // o1 *= exp(S*i*pi/4), o2 *= S*i, o3 *= exp(S*3*i*pi/4)
+    o1 = S < 0 ? mk(c * (o1.re + o1.im), c * (o1.im - o1.re)) : mk(c * (o1.re - o1.im), c * (o1.im + o1.re));
+    o2 = muli<S>(o2);
+    o3 = S < 0 ? mk(c * (o3.im - o3.re), -c * (o3.re + o3.im)) : mk(-c * (o3.re + o3.im), c * (o3.re - o3.im));
+    x[0] = e0 + o0;
+    x[4] = e0 - o0;
+    x[1] = e1 + o1;
+    x[5] = e1 - o1;
+    x[2] = e2 + o2;
+    x[6] = e2 - o2;
+    x[3] = e3 + o3;
+    x[7] = e3 - o3;
+}
+
+template <int S, typename T>
+__device__ __forceinline__ void dft16(cpx<T>* x) {
+    cpx<T> e[8], o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        e[i] = x[2 * i];
+        o[i] = x[2 * i + 1];
+    }
+    dft8<S>(e);
+    dft8<S>(o);
+    // cos/sin(pi*q/8), q = 0..7
+    const T C[8] = {(T)1.0,
+                    (T)0.923879532511286756128183189396788933,
+                    (T)0.707106781186547524400844362104849039,
+                    (T)0.382683432365089771728459984030398866,
+                    (T)0.0,
+                    (T)-0.382683432365089771728459984030398866,
+                    (T)-0.707106781186547524400844362104849039,
+                    (T)-0.923879532511286756128183189396788933};
+    const T Sn[8] = {(T)0.0,
+                     (T)0.382683432365089771728459984030398866,
+                     (T)0.707106781186547524400844362104849039,
+                     (T)0.923879532511286756128183189396788933,
+                     (T)1.0,
+                     (T)0.923879532511286756128183189396788933,
+                     (T)0.707106781186547524400844362104849039,
+                     (T)0.382683432365089771728459984030398866};
+#pragma unroll
+    for (int q = 1; q < 8; ++q) {
+        if (q == 4) {
+            o[q] = muli<S>(o[q]);
+        } else {
+            cpx<T> w = mk(C[q], (T)S * Sn[q]);
+            o[q] = cmul(o[q], w);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        x[q] = e[q] + o[q];
+        x[q + 8] = e[q] - o[q];
+    }
+}
+
+template <int R>
+struct OddTables;
+template <>
+struct OddTables<3> {
+    static __device__ __forceinline__ double c(int j) { return kCos3[j]; }
+    static __device__ __forceinline__ double s(int j) { return kSin3[j]; }
+};
+template <>
+struct OddTables<5> {
+    static __device__ __forceinline__ double c(int j) { return kCos5[j]; }
+    static __device__ __forceinline__ double s(int j) { return kSin5[j]; }
+};
+template <>
+struct OddTables<7> {
+    static __device__ __forceinline__ double c(int j) { return kCos7[j]; }
+    static __device__ __forceinline__ double s(int j) { return kSin7[j]; }
+};
+template <>
+struct OddTables<11> {
+    static __device__ __forceinline__ double c(int j) { return kCos11[j]; }
+    static __device__ __forceinline__ double s(int j) { return kSin11[j]; }
+};
+template <>
+struct OddTables<13> {
+    static __device__ __forceinline__ double c(int j) { return kCos13[j]; }
+    static __device__ __forceinline__ double s(int j) { return kSin13[j]; }
+};
+
+// Odd prime R: pair x[m] with x[R-m]; X[q] and X[R-q] share the cosine sum
+// and differ in the sign of the (S*i)-rotated sine sum.
+template <int R, int S, typename T>
+__device__ __forceinline__ void dft_odd(cpx<T>* x) {
+    constexpr int H = (R - 1) / 2;
+    cpx<T> a[H], b[H];
+#pragma unroll
+    for (int m = 1; m <= H; ++m) {
+        a[m - 1] = x[m] + x[R - m];
+        b[m - 1] = x[m] - x[R - m];
+    }
+    cpx<T> x0 = x[0];
+    cpx<T> y0 = x0;
+#pragma unroll
+    for (int m = 0; m < H; ++m) y0 = y0 + a[m];
+    cpx<T> out[R];
+    out[0] = y0;
+#pragma unroll
+    for (int q = 1; q <= H; ++q) {
+        cpx<T> A = x0;
+        cpx<T> B = mk((T)0, (T)0);
+#pragma unroll
+        for (int m = 1; m <= H; ++m) {
+            const int j = (m * q) % R;
+            const T cj = (T)OddTables<R>::c(j);
+            const T sj = (T)OddTables<R>::s(j);
+            A = mk(A.re + a[m - 1].re * cj, A.im + a[m - 1].im * cj);
+            B = mk(B.re + b[m - 1].re * sj, B.im + b[m - 1].im * sj);
+        }
+        cpx<T> iB = muli<S>(B);
+        out[q] = A + iB;
+        out[R - q] = A - iB;
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q) x[q] = out[q];
+}
+
+template <int R, int S, typename T>
+__device__ __forceinline__ void dft(cpx<T>* x) {
+    if constexpr (R == 2) {
+        dft2<S>(x);
+    } else if constexpr (R == 4) {
+        dft4<S>(x[0], x[1], x[2], x[3]);
+    } else if constexpr (R == 8) {
+        dft8<S>(x);
+    } else if constexpr (R == 16) {
+        dft16<S>(x);
+    } else {
+        dft_odd<R, S>(x);
+    }
+}
+
+// Butterflies per thread per stage held in registers. The host picks the
+// threads per line so that ceil((N/R)/threads) never exceeds this bound.
+template <int R>
+__host__ __device__ constexpr int max_butterflies_per_thread() {
+    return R <= 2 ? 16 : R <= 3 ? 10 : R <= 4 ? 8 : R <= 5 ? 6 : R <= 8 ? 4 : R <= 13 ? 2 : 2;
+}
+
+// LDS element index of element e in a line (one pad slot every 2^ps).
+__device__ __forceinline__ int lpad(int e, int ps) { return e + (e >> ps); }
+
+// One Stockham stage over a line held in LDS, in place: every thread first
+// loads all of its butterfly inputs, the block synchronises, then writes.
+template <typename T, int S, int R>
+__device__ __forceinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
+                                          const int TT, const int t, const int ps,
+                                          const cpx<T>* __restrict__ tw) {
+    constexpr int MJ = max_butterflies_per_thread<R>();
+    const int NB = N / R;
+    cpx<T> v[MJ][R];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int b = t + j * TT;
+        if (b < NB) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) v[j][i] = line[lpad(b + i * NB, ps)];
+        }
+    }
+    __syncthreads();
+    const int step = N / (P * R);
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int b = t + j * TT;
+        if (b < NB) {
+            const int k = b % P;
+            if (P > 1) {
+#pragma unroll
+                for (int i = 1; i < R; ++i) v[j][i] = twmul<S>(v[j][i], tw[k * i * step]);
+            }
+            dft<R, S>(v[j]);
+            const int base = (b - k) * R + k;
+#pragma unroll
+            for (int q = 0; q < R; ++q) line[lpad(base + q * P, ps)] = v[j][q];
+        }
+    }
+    __syncthreads();
+}
+
+// Runs every stage of a runtime radix list over the line at `line`.
+template <typename T, int S>
+__device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int N, const int TT,
+                                           const int t, const int ps, const int nst,
+                                           const int* __restrict__ radix,
+                                           const cpx<T>* __restrict__ tw) {
+    int P = 1;
+    for (int s = 0; s < nst; ++s) {
+        const int R = radix[s];
+        switch (R) {
+            case 2: stage_lds<T, S, 2>(line, N, P, TT, t, ps, tw); break;
+            case 3: stage_lds<T, S, 3>(line, N, P, TT, t, ps, tw); break;
+            case 4: stage_lds<T, S, 4>(line, N, P, TT, t, ps, tw); break;
+            case 5: stage_lds<T, S, 5>(line, N, P, TT, t, ps, tw); break;
+            case 7: stage_lds<T, S, 7>(line, N, P, TT, t, ps, tw); break;
+            case 8: stage_lds<T, S, 8>(line, N, P, TT, t, ps, tw); break;
+            case 11: stage_lds<T, S, 11>(line, N, P, TT, t, ps, tw); break;
+            case 13: stage_lds<T, S, 13>(line, N, P, TT, t, ps, tw); break;
+            case 16: stage_lds<T, S, 16>(line, N, P, TT, t, ps, tw); break;
+            default: break;
+        }
+        P *= R;
+    }
+}
+
+}  // namespace vkfx

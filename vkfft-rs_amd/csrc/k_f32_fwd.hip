@@ -1,0 +1,7 @@
+// Kernel instantiations for one precision and first-FFT direction; split so
+// the four variants compile in parallel.
+#include "fft_kernels_impl.hpp"
+
+namespace vkfx {
+KernelFn pick_f32_fwd(KernelKind kind) { return pick<float, -1>(kind); }
+}  // namespace vkfx

@@ -1,0 +1,76 @@
+// kernels.hpp -- host-visible launch interface of the gfx950 kernel library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vkfx {
+
+constexpr int kMaxStages = 24;
+constexpr int kMaxLinesPerBlock = 64;
+
+// Kernel families. Each is one HBM pass over its lines; see the comments on
+// the IO policies in fft_kernels.hip for what each one loads and stores.
+enum KernelKind : int {
+    KK_PLAIN = 0,      // C2C lines along any axis, scale on store
+    KK_R2C_FULL,       // odd-length R2C: real -> complex FFT, keep n/2+1
+    KK_C2R_FULL,       // odd-length C2R: Hermitian expand, FFT, keep real
+    KK_R2C_HALF,       // even R2C in one kernel: packed half-size FFT + post
+    KK_C2R_HALF,       // even C2R in one kernel: pre + packed half-size FFT
+    KK_FS_A,           // four-step column pass + W_M twiddle on store
+    KK_FS_A_BLUE,      // same, input = chirp * x with zero padding
+    KK_FS_A_C2R,       // same, input = even-half C2R preprocess of X
+    KK_FS_B,           // four-step row pass, transposed store
+    KK_FS_B_R2C,       // four-step row pass + R2C postprocess (mirror rows)
+    KK_BLUE_B,         // Bluestein row pass: FFT, spectrum multiply, IFFT, W_M^-1
+    KK_FS_C_BLUE,      // Bluestein column pass: IFFT, chirp, truncate
+    KK_BLUE_1,         // Bluestein in one kernel (convolution fits LDS)
+    KK_COUNT
+};
+
+enum KFlags : int {
+    KF_IN_ROWMAJOR = 1,   // a line's elements are contiguous in the input
+    KF_OUT_ROWMAJOR = 2,  // a line's elements are contiguous in the output
+};
+
+struct KArgs {
+    const void* in;
+    void* out;
+    long long in_es, in_cs, in_os;     // input element / column / outer strides
+    long long out_es, out_cs, out_os;  // output strides
+    long long C;                       // columns per outer index (line = o*C + c)
+    long long nlines;                  // total lines
+    int N;                             // FFT length run in LDS
+    int TT;                            // threads per line
+    int G;                             // lines per block
+    int LS;                            // LDS stride between lines (elements)
+    int PS;                            // LDS pad shift
+    int nstages;
+    int radix[kMaxStages];
+    int flags;
+    const void* tw;                    // exp(-2 pi i k/N), k < N
+    double scale;
+    const void* chirp;                 // Bluestein chirp, logical length
+    const void* spec;                  // Bluestein kernel spectrum (1/M folded in)
+    const void* tlo;                   // two-level table for exp(-2 pi i k/M)
+    const void* thi;
+    int tshift;
+    const void* rlo;                   // two-level table for exp(-2 pi i k/Nreal)
+    const void* rhi;
+    int rshift;
+    long long M;                       // four-step / half-spectrum / convolution length
+    long long nvalid;                  // logical input length (zero pad beyond)
+    long long nout;                    // logical output length per line (truncate)
+    long long N1, N2;                  // four-step factors (M = N1*N2)
+};
+
+// Launches one kernel. prec: 0 = f32, 1 = f64. dir: -1 forward, +1 inverse
+// (direction of the first FFT the kernel runs). Returns a hipError_t value.
+int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block,
+           size_t lds_bytes, hipStream_t stream);
+
+// Largest dynamic LDS a block may request on this device (bytes).
+size_t max_lds_bytes();
+
+}  // namespace vkfx

@@ -1,0 +1,1119 @@
+// runtime.cpp -- context, plans and the C ABI of the MI355X FFT path.
+//
+// A plan is a list of kernel launches (fft_kernels.hip) with their tables
+// (twiddles, chirps, kernel spectra) uploaded once at plan time, mirroring
+// what vkfft-rs's HIP runtime keeps in its module/LUT caches
+// (src/backend/hip/runtime.rs:1422-1468, 2019-2039) but without any source
+// generation or JIT step.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "planner.hpp"
+#include "vkfx.h"
+
+using namespace vkfx;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(VKFX_ERR_NATIVE_RUNTIME, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+typedef long double ld;
+const ld kPi = 3.141592653589793238462643383279502884L;
+
+// exp(-2 pi i k / n) with exact integer reduction of k.
+void root(ld k, ld n, ld& c, ld& s) {
+    ld a = -2.0L * kPi * k / n;
+    c = cosl(a);
+    s = sinl(a);
+}
+
+}  // namespace
+
+struct vkfx_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    vkfx_device_profile profile{};
+};
+
+namespace {
+
+enum BufSel : int { SEL_IN = 0, SEL_OUT = 1, SEL_WORK = 2 };
+
+struct Launch {
+    KernelKind kind;
+    int dir;
+    KArgs a;
+    unsigned grid, block;
+    size_t lds;
+    int in_sel, out_sel;
+    size_t in_off, out_off;  // byte offsets into the selected buffers
+    std::string label;
+};
+
+// Line geometry of one FFT length inside a kernel.
+struct Geometry {
+    int N = 1, TT = 1, G = 1, LS = 1, PS = 4;
+    std::vector<int> radix;
+    size_t lds = 0;
+    bool ok = false;
+};
+
+int max_bpt(int r) {
+    return r <= 2 ? 16 : r <= 3 ? 10 : r <= 4 ? 8 : r <= 5 ? 6 : r <= 8 ? 4 : 2;
+}
+
+// Stage radices: power-of-two part split into ceil(p/4) stages as evenly as
+// possible (radix 16/8/4/2), then one stage per odd prime factor.
+bool radix_schedule(size_t n, std::vector<int>& out) {
+    out.clear();
+    size_t m = n;
+    int p = 0;
+    while (m % 2 == 0) {
+        m /= 2;
+        ++p;
+    }
+    if (p > 0) {
+        int s = (p + 3) / 4;
+        int base = p / s, extra = p % s;
+        for (int i = 0; i < s; ++i) out.push_back(1 << (base + (i < extra ? 1 : 0)));
+    }
+    for (int q : {3, 5, 7, 11, 13})
+        while (m % q == 0) {
+            m /= q;
+            out.push_back(q);
+        }
+    return m == 1;
+}
+
+Geometry geometry(size_t n, int prec, int want_g, size_t lds_max, size_t lds_budget) {
+    Geometry g;
+    if (n == 0 || n > (1u << 20)) return g;
+    if (!radix_schedule(n, g.radix)) return g;
+    if ((int)g.radix.size() > kMaxStages) return g;
+    g.N = (int)n;
+    int tt = 1;
+    for (int r : g.radix) {
+        int nb = (int)n / r;
+        tt = std::max(tt, (nb + max_bpt(r) - 1) / max_bpt(r));
+    }
+    if (tt > 512) return g;
+    g.TT = tt;
+    const size_t sz = prec ? 16 : 8;
+    g.PS = prec ? 3 : 4;
+    int ls = (int)n + ((int)n >> g.PS);
+    if (ls % 2 == 0) ls += 1;
+    g.LS = ls;
+    const size_t line_bytes = (size_t)ls * sz;
+    if (line_bytes > lds_max) return g;
+    size_t budget = std::max(lds_budget, line_bytes);
+    budget = std::min(budget, lds_max);
+    int G = std::max(1, want_g);
+    G = std::min(G, 512 / tt);
+    G = std::min<int>(G, (int)(budget / line_bytes));
+    G = std::min(G, kMaxLinesPerBlock);
+    if (G < 1) return g;
+    g.G = G;
+    g.lds = (size_t)G * line_bytes;
+    g.ok = true;
+    return g;
+}
+
+}  // namespace
+
+struct vkfx_plan {
+    vkfx_context* ctx = nullptr;
+    vkfx_plan_desc desc{};
+    std::vector<Launch> launches;
+    std::vector<std::unique_ptr<DevBuf>> tables;
+    std::map<std::string, const void*> table_cache;
+    DevBuf work;
+    size_t work_bytes = 0;
+    size_t in_bytes = 0, out_bytes = 0;
+    std::string json;
+    DevBuf host_in, host_out;  // staging for vkfx_execute_host
+};
+
+namespace {
+
+// Dynamic LDS a plan may give one block: the device limit minus the kernels'
+// static per-line bookkeeping (kMaxLinesPerBlock LineInfo records).
+size_t lds_max_for(const vkfx_context* ctx) {
+    size_t v = ctx->profile.shared_memory_bytes;
+    if (!v) v = 65536;
+    return v - 4096;
+}
+
+int upload(vkfx_plan* p, const std::string& key, const void* host, size_t bytes, const void** dev) {
+    auto it = p->table_cache.find(key);
+    if (it != p->table_cache.end()) {
+        *dev = it->second;
+        return VKFX_OK;
+    }
+    auto b = std::make_unique<DevBuf>();
+    hipError_t e = hipMalloc(&b->p, bytes ? bytes : 16);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(table)");
+    b->bytes = bytes;
+    if (bytes) {
+        e = hipMemcpy(b->p, host, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpy(table)");
+    }
+    *dev = b->p;
+    p->table_cache[key] = b->p;
+    p->tables.push_back(std::move(b));
+    return VKFX_OK;
+}
+
+// Complex table of precision prec from long-double pairs.
+std::vector<unsigned char> pack(const std::vector<ld>& re, const std::vector<ld>& im, int prec) {
+    const size_t n = re.size();
+    std::vector<unsigned char> bytes(n * (prec ? 16 : 8));
+    if (prec) {
+        double* d = (double*)bytes.data();
+        for (size_t i = 0; i < n; ++i) {
+            d[2 * i] = (double)re[i];
+            d[2 * i + 1] = (double)im[i];
+        }
+    } else {
+        float* f = (float*)bytes.data();
+        for (size_t i = 0; i < n; ++i) {
+            f[2 * i] = (float)re[i];
+            f[2 * i + 1] = (float)im[i];
+        }
+    }
+    return bytes;
+}
+
+// Stage twiddles exp(-2 pi i k/n), k < n.
+int stage_table(vkfx_plan* p, size_t n, int prec, const void** dev) {
+    std::string key = "tw:" + std::to_string(n) + ":" + std::to_string(prec);
+    if (p->table_cache.count(key)) {
+        *dev = p->table_cache[key];
+        return VKFX_OK;
+    }
+    std::vector<ld> re(n), im(n);
+    for (size_t k = 0; k < n; ++k) root((ld)k, (ld)n, re[k], im[k]);
+    auto b = pack(re, im, prec);
+    return upload(p, key, b.data(), b.size(), dev);
+}
+
+// Two-level table for exp(-2 pi i k/L), k <= L: lo[j] = root(j), j < 2^s;
+// hi[h] = root(h*2^s). The kernels form hi[k>>s]*lo[k&(2^s-1)].
+int two_level(vkfx_plan* p, size_t L, int prec, const void** lo, const void** hi, int* shift) {
+    int s = 0;
+    while (((size_t)1 << (2 * s)) < L + 1) ++s;
+    s = std::max(s, 1);
+    const size_t nlo = (size_t)1 << s, nhi = (L >> s) + 2;
+    std::string key = "tl:" + std::to_string(L) + ":" + std::to_string(prec);
+    std::vector<ld> re(nlo), im(nlo);
+    for (size_t j = 0; j < nlo; ++j) root((ld)j, (ld)L, re[j], im[j]);
+    auto b = pack(re, im, prec);
+    int rc = upload(p, key + ":lo", b.data(), b.size(), lo);
+    if (rc) return rc;
+    re.assign(nhi, 0);
+    im.assign(nhi, 0);
+    for (size_t h = 0; h < nhi; ++h) root((ld)(h << s), (ld)L, re[h], im[h]);
+    b = pack(re, im, prec);
+    rc = upload(p, key + ":hi", b.data(), b.size(), hi);
+    *shift = s;
+    return rc;
+}
+
+// Bluestein chirp c[n] = exp(sign * pi i n^2 / N) with n^2 reduced mod 2N
+// (bluestein_ir.rs / lut.rs:295-304 define c[n] = exp(s*pi*i*n^2/N)).
+std::vector<ld> chirp_angles(size_t N) {
+    std::vector<ld> a(N);
+    const unsigned __int128 twoN = 2 * (unsigned __int128)N;
+    for (size_t n = 0; n < N; ++n) {
+        unsigned __int128 sq = ((unsigned __int128)n * n) % twoN;
+        a[n] = kPi * (ld)(unsigned long long)sq / (ld)N;
+    }
+    return a;
+}
+
+// In-place long-double FFT of smooth length (exp(-2 pi i jk/n)), recursive
+// decimation in time; used once per plan for the Bluestein kernel spectrum.
+void host_fft(std::vector<ld>& re, std::vector<ld>& im) {
+    const size_t n = re.size();
+    if (n <= 1) return;
+    size_t r = 0;
+    for (size_t q : {2, 3, 5, 7, 11, 13})
+        if (n % q == 0) {
+            r = q;
+            break;
+        }
+    if (r == 0) {  // naive DFT for a prime remainder
+        std::vector<ld> orr(n), oi(n);
+        for (size_t k = 0; k < n; ++k) {
+            ld sr = 0, si = 0;
+            for (size_t j = 0; j < n; ++j) {
+                ld c, s;
+                root((ld)((j * k) % n), (ld)n, c, s);
+                sr += re[j] * c - im[j] * s;
+                si += re[j] * s + im[j] * c;
+            }
+            orr[k] = sr;
+            oi[k] = si;
+        }
+        re.swap(orr);
+        im.swap(oi);
+        return;
+    }
+    const size_t m = n / r;
+    std::vector<std::vector<ld>> sr(r, std::vector<ld>(m)), si(r, std::vector<ld>(m));
+    for (size_t lane = 0; lane < r; ++lane) {
+        for (size_t i = 0; i < m; ++i) {
+            sr[lane][i] = re[lane + r * i];
+            si[lane][i] = im[lane + r * i];
+        }
+        host_fft(sr[lane], si[lane]);
+    }
+    for (size_t k = 0; k < n; ++k) {
+        ld ar = 0, ai = 0;
+        for (size_t lane = 0; lane < r; ++lane) {
+            ld c, s;
+            root((ld)((lane * k) % n), (ld)n, c, s);
+            const ld xr = sr[lane][k % m], xi = si[lane][k % m];
+            ar += xr * c - xi * s;
+            ai += xr * s + xi * c;
+        }
+        re[k] = ar;
+        im[k] = ai;
+    }
+}
+
+struct BlueTables {
+    const void* chirp = nullptr;
+    const void* spec = nullptr;
+};
+
+// chirp (length N, sign = transform direction) and the kernel spectrum
+// FFT_M(b) / M with b[n] = conj(c[n]) mirrored (reference.rs:121-131). With
+// n1 > 0 the spectrum is stored transposed for the four-step row pass.
+int bluestein_tables(vkfx_plan* p, size_t N, size_t M, int sign, int prec, size_t n1, size_t n2, BlueTables* t) {
+    std::vector<ld> ang = chirp_angles(N);
+    std::vector<ld> cr(N), ci(N);
+    for (size_t n = 0; n < N; ++n) {
+        cr[n] = cosl(ang[n]);
+        ci[n] = sign * sinl(ang[n]);
+    }
+    auto b = pack(cr, ci, prec);
+    std::string key = "chirp:" + std::to_string(N) + ":" + std::to_string(sign) + ":" + std::to_string(prec);
+    int rc = upload(p, key, b.data(), b.size(), &t->chirp);
+    if (rc) return rc;
+    std::vector<ld> br(M, 0), bi(M, 0);
+    for (size_t n = 0; n < N; ++n) {
+        br[n] = cr[n];
+        bi[n] = -ci[n];
+        if (n) {
+            br[M - n] = cr[n];
+            bi[M - n] = -ci[n];
+        }
+    }
+    host_fft(br, bi);
+    const ld inv = 1.0L / (ld)M;
+    std::vector<ld> sr(M), si(M);
+    for (size_t k = 0; k < M; ++k) {
+        size_t dst = k;
+        if (n1) {
+            const size_t k1 = k % n1, k2 = k / n1;
+            dst = k1 * n2 + k2;
+        }
+        sr[dst] = br[k] * inv;
+        si[dst] = bi[k] * inv;
+    }
+    b = pack(sr, si, prec);
+    key = "spec:" + std::to_string(N) + ":" + std::to_string(M) + ":" + std::to_string(sign) + ":" +
+          std::to_string(prec) + ":" + std::to_string(n1);
+    return upload(p, key, b.data(), b.size(), &t->spec);
+}
+
+size_t csize(int prec) { return prec ? 16 : 8; }
+size_t rsize(int prec) { return prec ? 8 : 4; }
+
+// Chooses M = N1 * N2 with both factors feasible single-upload lengths,
+// minimising max(N1, N2) (N1 >= N2 on ties). need_even_rows: N1 % (2*h) == 0
+// for the mirror-row R2C pass.
+bool four_step_split(size_t M, int prec, size_t lds_max, size_t* n1, size_t* n2) {
+    size_t best1 = 0, best2 = 0, bestmax = SIZE_MAX;
+    for (size_t a = 2; a * a <= M; ++a) {
+        if (M % a) continue;
+        const size_t b = M / a;
+        const size_t hi = std::max(a, b), lo = std::min(a, b);
+        if (!geometry(hi, prec, 1, lds_max, lds_max).ok || !geometry(lo, prec, 1, lds_max, lds_max).ok) continue;
+        if (hi < bestmax) {
+            bestmax = hi;
+            best1 = hi;
+            best2 = lo;
+        }
+    }
+    if (!best1) return false;
+    *n1 = best1;
+    *n2 = best2;
+    return true;
+}
+
+struct Ctx {
+    vkfx_plan* p;
+    int prec;
+    size_t lds_max;
+    size_t lds_budget = 80 * 1024;
+    std::ostringstream js;
+    bool first_pass = true;
+};
+
+void note_pass(Ctx& c, const Launch& L) {
+    if (!c.first_pass) c.js << ",";
+    c.first_pass = false;
+    c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.a.N << ",\"lines\":" << L.a.nlines
+         << ",\"grid\":" << L.grid << ",\"block\":" << L.block << ",\"lines_per_block\":" << L.a.G
+         << ",\"lds_bytes\":" << L.lds << ",\"radices\":[";
+    for (int i = 0; i < L.a.nstages; ++i) c.js << (i ? "," : "") << L.a.radix[i];
+    c.js << "]}";
+}
+
+int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, long long nlines, unsigned grid,
+               int in_sel, size_t in_off, int out_sel, size_t out_off, const char* label) {
+    a.N = g.N;
+    a.TT = g.TT;
+    a.G = g.G;
+    a.LS = g.LS;
+    a.PS = g.PS;
+    a.nstages = (int)g.radix.size();
+    for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
+    a.nlines = nlines;
+    int rc = stage_table(c.p, g.N, c.prec, &a.tw);
+    if (rc) return rc;
+    Launch L{kind, dir, a, grid, (unsigned)(g.G * g.TT), g.lds, in_sel, out_sel, in_off, out_off, label};
+    c.p->launches.push_back(L);
+    return VKFX_OK;
+}
+
+unsigned blocks_for(long long lines, int G) { return (unsigned)((lines + G - 1) / G); }
+
+KArgs blank() {
+    KArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.scale = 1.0;
+    a.C = 1;
+    return a;
+}
+
+size_t chunk_for(size_t batch, size_t per_batch_bytes) {
+    size_t budget = 96ull << 20;
+    if (const char* e = getenv("VKFX_WORK_BUDGET_MB")) budget = (size_t)atoll(e) << 20;
+    size_t c = std::max<size_t>(1, budget / std::max<size_t>(per_batch_bytes, 1));
+    return std::min(c, batch);
+}
+
+// ---- 1-D complex -----------------------------------------------------------
+
+int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorithm alg, size_t conv_len) {
+    vkfx_plan* p = c.p;
+    const int prec = c.prec;
+    const size_t cs = csize(prec);
+    const double sc = (dir > 0 && normalize) ? 1.0 / (double)n : 1.0;
+    if (alg == Algorithm::Stockham) {
+        Geometry g = geometry(n, prec, 256, c.lds_max, c.lds_budget);
+        if (g.ok) {
+            g = geometry(n, prec, std::max(1, 256 / g.TT), c.lds_max, c.lds_budget);
+            KArgs a = blank();
+            a.in_es = a.out_es = 1;
+            a.in_os = a.out_os = (long long)n;
+            a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+            a.scale = sc;
+            return add_launch(c, KK_PLAIN, dir, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                              "stockham");
+        }
+        size_t n1, n2;
+        if (!four_step_split(n, prec, c.lds_max, &n1, &n2))
+            return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no two-upload four-step split for length " + std::to_string(n));
+        Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+        Geometry gb = geometry(n2, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+        if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "four-step geometry");
+        const size_t chunk = chunk_for(batch, n * cs);
+        p->work_bytes = std::max(p->work_bytes, chunk * n * cs);
+        const void *tlo, *thi;
+        int tsh;
+        int rc = two_level(p, n, prec, &tlo, &thi, &tsh);
+        if (rc) return rc;
+        c.js << "\"four_step\":{\"len\":" << n << ",\"n1\":" << n1 << ",\"n2\":" << n2 << ",\"chunk\":" << chunk
+             << "},";
+        for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+            const size_t cb = std::min(chunk, batch - b0);
+            KArgs a = blank();
+            a.C = (long long)n2;
+            a.in_es = (long long)n2, a.in_cs = 1, a.in_os = (long long)n;
+            a.out_es = (long long)n2, a.out_cs = 1, a.out_os = (long long)n;
+            a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+            a.M = (long long)n, a.N1 = (long long)n1, a.N2 = (long long)n2;
+            long long lines = (long long)(cb * n2);
+            rc = add_launch(c, KK_FS_A, dir, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * n * cs, SEL_WORK, 0,
+                            "four_step_columns");
+            if (rc) return rc;
+            KArgs b = blank();
+            b.C = (long long)n1;
+            b.in_es = 1, b.in_cs = (long long)n2, b.in_os = (long long)n;
+            b.out_es = (long long)n1, b.out_cs = 1, b.out_os = (long long)n;
+            b.flags = KF_IN_ROWMAJOR;
+            b.scale = sc;
+            b.M = (long long)n, b.N1 = (long long)n1, b.N2 = (long long)n2;
+            lines = (long long)(cb * n1);
+            rc = add_launch(c, KK_FS_B, dir, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_OUT, b0 * n * cs,
+                            "four_step_rows");
+            if (rc) return rc;
+        }
+        return VKFX_OK;
+    }
+    // Bluestein (and, until a Rader kernel exists, Rader-classified axes).
+    const size_t M = conv_len ? conv_len : next_smooth_at_least(2 * n - 1, {2, 3, 5, 7});
+    if (M < 2 * n - 1) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein convolution length below 2N-1");
+    Geometry g = geometry(M, prec, 1, c.lds_max, c.lds_max);
+    if (g.ok) {
+        BlueTables t;
+        int rc = bluestein_tables(p, n, M, dir, prec, 0, 0, &t);
+        if (rc) return rc;
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = a.out_os = (long long)n;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        a.scale = sc;
+        a.chirp = t.chirp, a.spec = t.spec;
+        a.nvalid = (long long)n, a.nout = (long long)n, a.M = (long long)M;
+        c.js << "\"bluestein\":{\"len\":" << n << ",\"m\":" << M << ",\"uploads\":1},";
+        return add_launch(c, KK_BLUE_1, -1, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                          "bluestein_single");
+    }
+    size_t n1, n2;
+    if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for Bluestein M " + std::to_string(M));
+    Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gb = geometry(n2, prec, std::max(1, 256 / std::max(1, geometry(n2, prec, 1, c.lds_max, c.lds_max).TT)),
+                           c.lds_max, c.lds_budget);
+    if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "Bluestein four-step geometry");
+    BlueTables t;
+    int rc = bluestein_tables(p, n, M, dir, prec, n1, n2, &t);
+    if (rc) return rc;
+    const void *tlo, *thi;
+    int tsh;
+    rc = two_level(p, M, prec, &tlo, &thi, &tsh);
+    if (rc) return rc;
+    const size_t chunk = chunk_for(batch, M * cs);
+    p->work_bytes = std::max(p->work_bytes, chunk * M * cs);
+    c.js << "\"bluestein\":{\"len\":" << n << ",\"m\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
+         << ",\"chunk\":" << chunk << "},";
+    for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+        const size_t cb = std::min(chunk, batch - b0);
+        KArgs a = blank();
+        a.C = (long long)n2;
+        a.in_es = (long long)n2, a.in_cs = 1, a.in_os = (long long)n;
+        a.out_es = (long long)n2, a.out_cs = 1, a.out_os = (long long)M;
+        a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+        a.chirp = t.chirp;
+        a.nvalid = (long long)n, a.M = (long long)M, a.N1 = (long long)n1, a.N2 = (long long)n2;
+        long long lines = (long long)(cb * n2);
+        rc = add_launch(c, KK_FS_A_BLUE, -1, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * n * cs, SEL_WORK, 0,
+                        "bluestein_columns");
+        if (rc) return rc;
+        KArgs b = blank();
+        b.C = (long long)n1;
+        b.in_es = 1, b.in_cs = (long long)n2, b.in_os = (long long)M;
+        b.out_es = 1, b.out_cs = (long long)n2, b.out_os = (long long)M;
+        b.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        b.spec = t.spec;
+        b.tlo = tlo, b.thi = thi, b.tshift = tsh;
+        b.M = (long long)M, b.N1 = (long long)n1, b.N2 = (long long)n2;
+        lines = (long long)(cb * n1);
+        rc = add_launch(c, KK_BLUE_B, -1, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_WORK, 0,
+                        "bluestein_rows");
+        if (rc) return rc;
+        KArgs d = blank();
+        d.C = (long long)n2;
+        d.in_es = (long long)n2, d.in_cs = 1, d.in_os = (long long)M;
+        d.out_es = (long long)n2, d.out_cs = 1, d.out_os = (long long)n;
+        d.chirp = t.chirp;
+        d.scale = sc;
+        d.nout = (long long)n, d.M = (long long)M, d.N1 = (long long)n1, d.N2 = (long long)n2;
+        lines = (long long)(cb * n2);
+        rc = add_launch(c, KK_FS_C_BLUE, 1, ga, d, lines, blocks_for(lines, ga.G), SEL_WORK, 0, SEL_OUT, b0 * n * cs,
+                        "bluestein_columns_out");
+        if (rc) return rc;
+    }
+    return VKFX_OK;
+}
+
+// ---- N-D complex -----------------------------------------------------------
+
+int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
+    const int prec = c.prec;
+    const int dir = d.direction;
+    size_t total = d.batch;
+    for (uint32_t i = 0; i < d.rank; ++i) total *= d.dims[i];
+    bool first = true;
+    for (int ax = (int)d.rank - 1; ax >= 0; --ax) {
+        const size_t len = d.dims[ax];
+        if (len == 1) continue;
+        size_t inner = 1;
+        for (uint32_t j = ax + 1; j < d.rank; ++j) inner *= d.dims[j];
+        const size_t outer = total / (len * inner);
+        const double sc = (dir > 0 && d.normalize) ? 1.0 / (double)len : 1.0;
+        const bool contiguous = inner == 1;
+        const int alg = d.axis_algorithm[ax];
+        KArgs a = blank();
+        a.C = (long long)inner;
+        a.in_es = a.out_es = (long long)inner;
+        a.in_cs = a.out_cs = 1;
+        a.in_os = a.out_os = (long long)(len * inner);
+        a.flags = contiguous ? (KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR) : 0;
+        a.scale = sc;
+        const long long lines = (long long)(outer * inner);
+        const int in_sel = first ? SEL_IN : SEL_OUT;
+        int rc;
+        if (alg == VKFX_ALG_STOCKHAM) {
+            Geometry g0 = geometry(len, prec, 1, c.lds_max, c.lds_max);
+            if (!g0.ok)
+                return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                            "N-D axis length " + std::to_string(len) + " exceeds one upload");
+            const int want = contiguous ? std::max(1, 256 / g0.TT) : (prec ? 8 : 16);
+            Geometry g = geometry(len, prec, want, c.lds_max, c.lds_budget);
+            rc = add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, 0, SEL_OUT, 0,
+                            contiguous ? "stockham_rows" : "stockham_columns");
+        } else {
+            const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
+                                                   : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
+            Geometry g = geometry(M, prec, contiguous ? 1 : 4, c.lds_max, c.lds_max);
+            if (!g.ok)
+                return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                            "N-D Bluestein axis needs more than one upload (M=" + std::to_string(M) + ")");
+            BlueTables t;
+            rc = bluestein_tables(c.p, len, M, dir, prec, 0, 0, &t);
+            if (rc) return rc;
+            a.chirp = t.chirp, a.spec = t.spec;
+            a.nvalid = (long long)len, a.nout = (long long)len, a.M = (long long)M;
+            rc = add_launch(c, KK_BLUE_1, -1, g, a, lines, blocks_for(lines, g.G), in_sel, 0, SEL_OUT, 0,
+                            "bluestein_axis");
+        }
+        if (rc) return rc;
+        first = false;
+    }
+    if (first) {  // every axis has length 1: the transform is a copy (times scale 1)
+        Geometry g = geometry(1, prec, 64, c.lds_max, c.lds_budget);
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = a.out_os = 1;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        return add_launch(c, KK_PLAIN, dir, g, a, (long long)total, blocks_for(total, g.G), SEL_IN, 0, SEL_OUT, 0,
+                          "copy");
+    }
+    return VKFX_OK;
+}
+
+// ---- real ------------------------------------------------------------------
+
+int plan_r2c(Ctx& c, size_t n, size_t batch) {
+    vkfx_plan* p = c.p;
+    const int prec = c.prec;
+    const size_t cs = csize(prec), rs = rsize(prec);
+    const size_t h = n / 2 + 1;
+    if (n % 2) {
+        Geometry g0 = geometry(n, prec, 1, c.lds_max, c.lds_max);
+        if (!g0.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "odd R2C length needs a single-upload smooth length");
+        Geometry g = geometry(n, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = (long long)n, a.out_os = (long long)h;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        a.nout = (long long)h;
+        return add_launch(c, KK_R2C_FULL, -1, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                          "r2c_full");
+    }
+    const size_t M = n / 2;
+    const void *rlo, *rhi;
+    int rsh;
+    int rc = two_level(p, n, prec, &rlo, &rhi, &rsh);
+    if (rc) return rc;
+    Geometry g0 = geometry(M, prec, 1, c.lds_max, c.lds_max);
+    if (g0.ok) {
+        Geometry g = geometry(M, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = (long long)M, a.out_os = (long long)h;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        a.rlo = rlo, a.rhi = rhi, a.rshift = rsh;
+        c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":1},";
+        return add_launch(c, KK_R2C_HALF, -1, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                          "r2c_even_half");
+    }
+    size_t n1, n2;
+    if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for R2C half length");
+    // the mirror-row pass needs N1 divisible by 2H; H lines + H mirrors per block
+    Geometry gb1 = geometry(n2, prec, 1, c.lds_max, c.lds_max);
+    int H = prec ? 4 : 8;
+    while (H > 1 && (n1 % (2 * H) != 0)) H /= 2;
+    if (n1 % (2 * H) != 0) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "R2C four-step rows must be even");
+    Geometry gb = geometry(n2, prec, 2 * H, c.lds_max, c.lds_max);
+    if (!gb1.ok || gb.G != 2 * H) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "R2C four-step row geometry");
+    Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    const void *tlo, *thi;
+    int tsh;
+    rc = two_level(p, M, prec, &tlo, &thi, &tsh);
+    if (rc) return rc;
+    const size_t chunk = chunk_for(batch, M * cs);
+    p->work_bytes = std::max(p->work_bytes, chunk * M * cs);
+    c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
+         << ",\"chunk\":" << chunk << "},";
+    for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+        const size_t cb = std::min(chunk, batch - b0);
+        KArgs a = blank();
+        a.C = (long long)n2;
+        a.in_es = (long long)n2, a.in_cs = 1, a.in_os = (long long)M;
+        a.out_es = (long long)n2, a.out_cs = 1, a.out_os = (long long)M;
+        a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+        a.M = (long long)M, a.N1 = (long long)n1, a.N2 = (long long)n2;
+        long long lines = (long long)(cb * n2);
+        rc = add_launch(c, KK_FS_A, -1, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * n * rs, SEL_WORK, 0,
+                        "r2c_columns");
+        if (rc) return rc;
+        KArgs b = blank();
+        b.C = (long long)n1;
+        b.in_es = 1, b.in_cs = (long long)n2, b.in_os = (long long)M;
+        b.out_os = (long long)h;
+        b.flags = KF_IN_ROWMAJOR;
+        b.rlo = rlo, b.rhi = rhi, b.rshift = rsh;
+        b.M = (long long)M, b.N1 = (long long)n1, b.N2 = (long long)n2;
+        lines = (long long)(cb * n1);
+        const unsigned grid = (unsigned)(cb * (n1 / (2 * H)));
+        rc = add_launch(c, KK_FS_B_R2C, -1, gb, b, lines, grid, SEL_WORK, 0, SEL_OUT, b0 * h * cs, "r2c_rows_post");
+        if (rc) return rc;
+    }
+    return VKFX_OK;
+}
+
+int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
+    vkfx_plan* p = c.p;
+    const int prec = c.prec;
+    const size_t cs = csize(prec), rs = rsize(prec);
+    const size_t h = n / 2 + 1;
+    const double sc = normalize ? 1.0 / (double)n : 1.0;
+    if (n % 2) {
+        Geometry g0 = geometry(n, prec, 1, c.lds_max, c.lds_max);
+        if (!g0.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "odd C2R length needs a single-upload smooth length");
+        Geometry g = geometry(n, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = (long long)h, a.out_os = (long long)n;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        a.scale = sc;
+        return add_launch(c, KK_C2R_FULL, 1, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                          "c2r_full");
+    }
+    const size_t M = n / 2;
+    const void *rlo, *rhi;
+    int rsh;
+    int rc = two_level(p, n, prec, &rlo, &rhi, &rsh);
+    if (rc) return rc;
+    Geometry g0 = geometry(M, prec, 1, c.lds_max, c.lds_max);
+    if (g0.ok) {
+        Geometry g = geometry(M, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = (long long)h, a.out_os = (long long)M;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        a.rlo = rlo, a.rhi = rhi, a.rshift = rsh;
+        a.scale = sc;
+        c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":1},";
+        return add_launch(c, KK_C2R_HALF, 1, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                          "c2r_even_half");
+    }
+    size_t n1, n2;
+    if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for C2R half length");
+    Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gb = geometry(n2, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    const void *tlo, *thi;
+    int tsh;
+    rc = two_level(p, M, prec, &tlo, &thi, &tsh);
+    if (rc) return rc;
+    const size_t chunk = chunk_for(batch, M * cs);
+    p->work_bytes = std::max(p->work_bytes, chunk * M * cs);
+    c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
+         << ",\"chunk\":" << chunk << "},";
+    for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+        const size_t cb = std::min(chunk, batch - b0);
+        KArgs a = blank();
+        a.C = (long long)n2;
+        a.in_es = (long long)n2, a.in_cs = 1, a.in_os = (long long)h;
+        a.out_es = (long long)n2, a.out_cs = 1, a.out_os = (long long)M;
+        a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+        a.rlo = rlo, a.rhi = rhi, a.rshift = rsh;
+        a.M = (long long)M, a.N1 = (long long)n1, a.N2 = (long long)n2;
+        long long lines = (long long)(cb * n2);
+        rc = add_launch(c, KK_FS_A_C2R, 1, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * h * cs, SEL_WORK, 0,
+                        "c2r_columns_pre");
+        if (rc) return rc;
+        KArgs b = blank();
+        b.C = (long long)n1;
+        b.in_es = 1, b.in_cs = (long long)n2, b.in_os = (long long)M;
+        b.out_es = (long long)n1, b.out_cs = 1, b.out_os = (long long)M;
+        b.flags = KF_IN_ROWMAJOR;
+        b.scale = sc;
+        b.M = (long long)M, b.N1 = (long long)n1, b.N2 = (long long)n2;
+        lines = (long long)(cb * n1);
+        rc = add_launch(c, KK_FS_B, 1, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_OUT, b0 * n * rs,
+                        "c2r_rows");
+        if (rc) return rc;
+    }
+    return VKFX_OK;
+}
+
+PlannerDevice planner_device(uint64_t shared) {
+    PlannerDevice d;
+    if (shared) {
+        d.shared_memory_bytes = shared;
+        size_t p2 = 1;
+        while (p2 * 2 <= shared) p2 *= 2;
+        d.shared_memory_pow2_bytes = p2;
+    }
+    return d;
+}
+
+}  // namespace
+
+// ============================================================== C ABI
+
+extern "C" {
+
+const char* vkfx_last_error(void) { return g_err.c_str(); }
+
+const char* vkfx_version(void) { return "vkfx-mi355x 0.1.0 (gfx950)"; }
+
+int vkfx_context_create(int device_index, vkfx_context** out) {
+    if (!out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail(VKFX_ERR_NATIVE_UNAVAILABLE, "HIP runtime has no usable device");
+    if (device_index < 0 || device_index >= count)
+        return fail(VKFX_ERR_NATIVE_UNAVAILABLE, "HIP device index out of range");
+    e = hipSetDevice(device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    auto* ctx = new vkfx_context();
+    ctx->device = device_index;
+    e = hipStreamCreate(&ctx->stream);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "hipStreamCreate");
+    }
+    vkfx_device_profile& pr = ctx->profile;
+    pr.shared_memory_bytes = prop.sharedMemPerBlock;
+    size_t p2 = 1;
+    while (p2 * 2 <= pr.shared_memory_bytes) p2 *= 2;
+    pr.shared_memory_pow2_bytes = p2;
+    pr.max_threads_per_block = prop.maxThreadsPerBlock;
+    pr.warp_size = prop.warpSize;
+    pr.compute_units = prop.multiProcessorCount;
+    pr.global_memory_bytes = prop.totalGlobalMem;
+    std::snprintf(pr.name, sizeof(pr.name), "%s", prop.name[0] ? prop.name : prop.gcnArchName);
+    std::snprintf(pr.arch, sizeof(pr.arch), "%s", prop.gcnArchName);
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return fail(VKFX_ERR_NATIVE_UNAVAILABLE, std::string("library built for gfx950, device is ") + prop.gcnArchName);
+    }
+    *out = ctx;
+    return VKFX_OK;
+}
+
+int vkfx_context_destroy(vkfx_context* ctx) {
+    if (!ctx) return VKFX_OK;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return VKFX_OK;
+}
+
+int vkfx_context_profile(const vkfx_context* ctx, vkfx_device_profile* out) {
+    if (!ctx || !out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    *out = ctx->profile;
+    return VKFX_OK;
+}
+
+int vkfx_context_synchronize(vkfx_context* ctx) {
+    if (!ctx) return fail(VKFX_ERR_INVALID_ARGUMENT, "null context");
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? VKFX_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan** out) {
+    if (!ctx || !desc_in || !out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    vkfx_plan_desc d = *desc_in;
+    if (d.rank < 1 || d.rank > VKFX_MAX_RANK) return fail(VKFX_ERR_INVALID_ARGUMENT, "rank must be 1..4");
+    if (d.batch == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "batch count must be >= 1");
+    for (uint32_t i = 0; i < d.rank; ++i)
+        if (d.dims[i] == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "ZeroLength: axis " + std::to_string(i));
+    if (d.precision != VKFX_F32 && d.precision != VKFX_F64)
+        return fail(VKFX_ERR_UNSUPPORTED_PRECISION, "only F32 and F64 are supported by this path");
+    if (d.direction != VKFX_FORWARD && d.direction != VKFX_INVERSE)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "direction must be -1 or +1");
+    if (d.transform == VKFX_R2C && d.direction != VKFX_FORWARD)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "R2C requires Direction::Forward");
+    if (d.transform == VKFX_C2R && d.direction != VKFX_INVERSE)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "C2R requires Direction::Inverse");
+    if (d.transform < VKFX_C2C || d.transform > VKFX_C2R) return fail(VKFX_ERR_INVALID_ARGUMENT, "unknown transform");
+    if (d.transform != VKFX_C2C && d.rank != 1)
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "multi-dimensional R2C/C2R is outside this path");
+    const bool f64 = d.precision == VKFX_F64;
+    size_t total = d.batch;
+    for (uint32_t i = 0; i < d.rank; ++i) {
+        if (d.dims[i] > (size_t)1 << 40 || total > ((size_t)1 << 46) / d.dims[i])
+            return fail(VKFX_ERR_ARITHMETIC_OVERFLOW, "tensor element count overflow");
+        total *= d.dims[i];
+    }
+    PlannerDevice pdev = planner_device(ctx->profile.shared_memory_bytes);
+    PlannerTuning tuning = tuning_for_amd(f64);
+    try {
+        if (d.use_library_planner) {
+            for (uint32_t i = 0; i < d.rank; ++i) {
+                AxisDecision ad;
+                if (d.transform == VKFX_C2C)
+                    ad = plan_c2c_axis(d.dims[i], d.batch, f64, i + 1 != d.rank, tuning, pdev);
+                else
+                    ad = plan_axis_portable(d.dims[i], tuning);
+                d.axis_algorithm[i] = (int32_t)ad.algorithm;
+                d.convolution_len[i] = ad.convolution_len;
+            }
+        }
+    } catch (const std::exception& ex) {
+        return fail(VKFX_ERR_INVALID_ARGUMENT, std::string("planner: ") + ex.what());
+    }
+    (void)hipSetDevice(ctx->device);
+    auto* p = new vkfx_plan();
+    p->ctx = ctx;
+    p->desc = d;
+    Ctx c{p, f64 ? 1 : 0, lds_max_for(ctx)};
+    if (const char* e = getenv("VKFX_LDS_BUDGET_KB")) c.lds_budget = (size_t)atoll(e) << 10;
+    const size_t cs = csize(c.prec), rs = rsize(c.prec);
+    c.js << "{\"rank\":" << d.rank << ",\"dims\":[";
+    for (uint32_t i = 0; i < d.rank; ++i) c.js << (i ? "," : "") << d.dims[i];
+    c.js << "],\"batch\":" << d.batch << ",\"precision\":\"" << (f64 ? "f64" : "f32") << "\",\"transform\":\""
+         << (d.transform == VKFX_C2C ? "c2c" : d.transform == VKFX_R2C ? "r2c" : "c2r") << "\",\"axes\":[";
+    for (uint32_t i = 0; i < d.rank; ++i) {
+        const int alg = d.axis_algorithm[i];
+        c.js << (i ? "," : "") << "{\"len\":" << d.dims[i] << ",\"algorithm\":\""
+             << (alg == VKFX_ALG_STOCKHAM ? "stockham" : alg == VKFX_ALG_RADER ? "rader" : "bluestein") << "\"";
+        if (alg == VKFX_ALG_RADER) c.js << ",\"executed_as\":\"bluestein\"";
+        if (d.convolution_len[i]) c.js << ",\"convolution_len\":" << d.convolution_len[i];
+        c.js << "}";
+    }
+    c.js << "],";
+    int rc = VKFX_OK;
+    try {
+        if (d.transform == VKFX_C2C) {
+            p->in_bytes = p->out_bytes = total * cs;
+            if (d.rank == 1) {
+                const int alg = d.axis_algorithm[0];
+                Algorithm a = alg == VKFX_ALG_STOCKHAM ? Algorithm::Stockham : Algorithm::Bluestein;
+                size_t conv = d.convolution_len[0];
+                if (alg == VKFX_ALG_RADER) conv = 0;  // executed through Bluestein, M = next smooth >= 2N-1
+                rc = plan_c2c_1d(c, d.dims[0], d.batch, d.direction, d.normalize != 0, a, conv);
+            } else {
+                rc = plan_c2c_nd(c, d);
+            }
+        } else if (d.transform == VKFX_R2C) {
+            const size_t n = d.dims[0];
+            p->in_bytes = d.batch * n * rs;
+            p->out_bytes = d.batch * (n / 2 + 1) * cs;
+            rc = plan_r2c(c, n, d.batch);
+        } else {
+            const size_t n = d.dims[0];
+            p->in_bytes = d.batch * (n / 2 + 1) * cs;
+            p->out_bytes = d.batch * n * rs;
+            rc = plan_c2r(c, n, d.batch, d.normalize != 0);
+        }
+    } catch (const std::exception& ex) {
+        rc = fail(VKFX_ERR_INVALID_ARGUMENT, std::string("plan: ") + ex.what());
+    }
+    if (rc) {
+        delete p;
+        return rc;
+    }
+    c.js << "\"workspace_bytes\":" << p->work_bytes << ",\"passes\":[";
+    for (const Launch& L : p->launches) note_pass(c, L);
+    c.js << "]}";
+    p->json = c.js.str();
+    if (p->work_bytes) {
+        hipError_t e = hipMalloc(&p->work.p, p->work_bytes);
+        if (e != hipSuccess) {
+            delete p;
+            return hip_fail(e, "hipMalloc(workspace)");
+        }
+        p->work.bytes = p->work_bytes;
+    }
+    *out = p;
+    return VKFX_OK;
+}
+
+int vkfx_plan_destroy(vkfx_plan* plan) {
+    if (!plan) return VKFX_OK;
+    (void)hipSetDevice(plan->ctx->device);
+    (void)hipStreamSynchronize(plan->ctx->stream);
+    delete plan;
+    return VKFX_OK;
+}
+
+int vkfx_plan_io_bytes(const vkfx_plan* plan, uint64_t* in_bytes, uint64_t* out_bytes) {
+    if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
+    if (in_bytes) *in_bytes = plan->in_bytes;
+    if (out_bytes) *out_bytes = plan->out_bytes;
+    return VKFX_OK;
+}
+
+int vkfx_plan_workspace_bytes(const vkfx_plan* plan, uint64_t* out) {
+    if (!plan || !out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    *out = plan->work_bytes;
+    return VKFX_OK;
+}
+
+int vkfx_plan_describe(const vkfx_plan* plan, char* buf, size_t cap) {
+    if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
+    if (buf && cap) {
+        const size_t n = std::min(cap - 1, plan->json.size());
+        std::memcpy(buf, plan->json.data(), n);
+        buf[n] = 0;
+    }
+    return (int)plan->json.size();
+}
+
+int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, void* stream) {
+    if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
+    if (!d_in || !d_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null device buffer");
+    if (plan->desc.transform != VKFX_C2C && d_in == d_out)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "R2C/C2R cannot run in place");
+    void* work = d_work ? d_work : plan->work.p;
+    if (plan->work_bytes && !work) return fail(VKFX_ERR_INVALID_ARGUMENT, "plan needs a workspace");
+    hipStream_t s = stream ? (hipStream_t)stream : plan->ctx->stream;
+    (void)hipSetDevice(plan->ctx->device);
+    const int prec = plan->desc.precision == VKFX_F64 ? 1 : 0;
+    for (const Launch& L : plan->launches) {
+        KArgs a = L.a;
+        auto sel = [&](int which, size_t off) -> char* {
+            char* base = which == SEL_IN ? (char*)d_in : which == SEL_OUT ? (char*)d_out : (char*)work;
+            return base + off;
+        };
+        a.in = sel(L.in_sel, L.in_off);
+        a.out = sel(L.out_sel, L.out_off);
+        int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, s);
+        if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
+    }
+    return VKFX_OK;
+}
+
+int vkfx_execute_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, void* h_out, uint64_t out_bytes) {
+    if (!plan || !h_in || !h_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    if (in_bytes != plan->in_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "InputLengthMismatch: expected " + std::to_string(plan->in_bytes) +
+                                                        " bytes, got " + std::to_string(in_bytes));
+    if (out_bytes != plan->out_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "output buffer: expected " + std::to_string(plan->out_bytes) +
+                                                        " bytes, got " + std::to_string(out_bytes));
+    (void)hipSetDevice(plan->ctx->device);
+    hipStream_t s = plan->ctx->stream;
+    auto ensure = [&](DevBuf& b, size_t bytes) -> int {
+        if (b.bytes >= bytes && b.p) return VKFX_OK;
+        if (b.p) (void)hipFree(b.p);
+        b.p = nullptr;
+        b.bytes = 0;
+        hipError_t e = hipMalloc(&b.p, bytes ? bytes : 16);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(staging)");
+        b.bytes = bytes;
+        return VKFX_OK;
+    };
+    int rc = ensure(plan->host_in, plan->in_bytes);
+    if (!rc) rc = ensure(plan->host_out, plan->out_bytes);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(plan->host_in.p, h_in, in_bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D)");
+    rc = vkfx_execute(plan, plan->host_in.p, plan->host_out.p, nullptr, s);
+    if (rc) return rc;
+    e = hipMemcpyAsync(h_out, plan->host_out.p, out_bytes, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H)");
+    e = hipStreamSynchronize(s);
+    return e == hipSuccess ? VKFX_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int vkfx_planner_axis(uint64_t len, uint64_t batch, int32_t precision, int32_t axis_is_strided,
+                      int32_t allow_recursive_rader, uint64_t shared_memory_bytes, int32_t* algorithm,
+                      uint64_t* convolution_len) {
+    if (!algorithm || !convolution_len) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output");
+    if (len == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "ZeroLength");
+    try {
+        const bool f64 = precision == VKFX_F64;
+        AxisDecision d = plan_c2c_axis(len, batch ? batch : 1, f64, axis_is_strided != 0,
+                                       tuning_for_amd(f64, allow_recursive_rader != 0),
+                                       planner_device(shared_memory_bytes));
+        *algorithm = (int32_t)d.algorithm;
+        *convolution_len = d.convolution_len;
+    } catch (const std::exception& ex) {
+        return fail(VKFX_ERR_INVALID_ARGUMENT, ex.what());
+    }
+    return VKFX_OK;
+}
+
+int vkfx_planner_bluestein_padding(uint64_t len, uint64_t batch, int32_t precision, uint64_t shared_memory_bytes,
+                                   uint64_t* padded) {
+    if (!padded) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output");
+    if (len < 2) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein length must be >= 2");
+    try {
+        *padded = bluestein_auto_padding(len, batch ? batch : 1, precision == VKFX_F64,
+                                         planner_device(shared_memory_bytes));
+    } catch (const std::exception& ex) {
+        return fail(VKFX_ERR_INVALID_ARGUMENT, ex.what());
+    }
+    return VKFX_OK;
+}
+
+uint64_t vkfx_planner_next_smooth(uint64_t target) {
+    try {
+        return next_smooth_at_least(target, {2, 3, 5, 7});
+    } catch (...) {
+        return 0;
+    }
+}
+
+}  // extern "C"

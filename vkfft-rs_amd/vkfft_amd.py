@@ -1,0 +1,390 @@
+"""Host-side mirror of vkfft-rs's transform API over the MI355X C ABI.
+
+The names follow the Rust crate so callers and tests read like its own code:
+`FftConfig` (src/config.rs:609-1034), `Direction`/`TransformKind`/`Precision`,
+`TransformIr.build` (src/application.rs:48-167) and a `HipExecutionContext`
+with `execute_transform_f32/f64` (src/backend/native_runtime.rs:339-359,
+src/backend/hip/runtime.rs:1982-1988). Everything below calls
+libvkfft_mi355x.so through ctypes; there is no CPU fallback: if the library
+or the GPU is missing, the calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import json
+import os
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvkfft_mi355x.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "vkfx.h")
+MAX_RANK = 4
+
+_lib = None
+
+
+class VkFftError(RuntimeError):
+    """Mirrors vkfft-rs `VkFftError` (src/error.rs:6-57)."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = STATUS_NAMES.get(status, "Unknown")
+        super().__init__(f"{self.kind}: {message}")
+
+
+STATUS_NAMES = {
+    -1: "NativeUnavailable",
+    -2: "NativeRuntime",
+    -3: "UnsupportedKernelPath",
+    -4: "UnsupportedPrecision",
+    -5: "InputLengthMismatch",
+    -6: "ResourceLimitExceeded",
+    -7: "InvalidArgument",
+    -8: "ArithmeticOverflow",
+}
+
+
+class Direction(enum.IntEnum):
+    Forward = -1
+    Inverse = 1
+
+
+class TransformKind(enum.IntEnum):
+    ComplexToComplex = 0
+    RealToComplex = 1
+    ComplexToReal = 2
+
+
+class Precision(enum.IntEnum):
+    F32 = 0
+    F64 = 1
+
+
+class AlgorithmKind(enum.IntEnum):
+    Stockham = 0
+    Rader = 1
+    Bluestein = 2
+
+
+class _PlanDesc(ctypes.Structure):
+    _fields_ = [
+        ("rank", ctypes.c_uint32),
+        ("dims", ctypes.c_uint64 * MAX_RANK),
+        ("batch", ctypes.c_uint64),
+        ("transform", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+        ("direction", ctypes.c_int32),
+        ("normalize", ctypes.c_int32),
+        ("use_library_planner", ctypes.c_int32),
+        ("axis_algorithm", ctypes.c_int32 * MAX_RANK),
+        ("convolution_len", ctypes.c_uint64 * MAX_RANK),
+    ]
+
+
+class _Profile(ctypes.Structure):
+    _fields_ = [
+        ("shared_memory_bytes", ctypes.c_uint64),
+        ("shared_memory_pow2_bytes", ctypes.c_uint64),
+        ("max_threads_per_block", ctypes.c_uint64),
+        ("warp_size", ctypes.c_uint64),
+        ("compute_units", ctypes.c_uint64),
+        ("global_memory_bytes", ctypes.c_uint64),
+        ("name", ctypes.c_char * 256),
+        ("arch", ctypes.c_char * 64),
+    ]
+
+
+def lib():
+    """Loads libvkfft_mi355x.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise VkFftError(-1, f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u64, i32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32
+        L.vkfx_last_error.restype = ctypes.c_char_p
+        L.vkfx_version.restype = ctypes.c_char_p
+        L.vkfx_context_create.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+        L.vkfx_context_destroy.argtypes = [vp]
+        L.vkfx_context_profile.argtypes = [vp, ctypes.POINTER(_Profile)]
+        L.vkfx_context_synchronize.argtypes = [vp]
+        L.vkfx_plan_create.argtypes = [vp, ctypes.POINTER(_PlanDesc), ctypes.POINTER(vp)]
+        L.vkfx_plan_destroy.argtypes = [vp]
+        L.vkfx_plan_io_bytes.argtypes = [vp, ctypes.POINTER(u64), ctypes.POINTER(u64)]
+        L.vkfx_plan_workspace_bytes.argtypes = [vp, ctypes.POINTER(u64)]
+        L.vkfx_plan_describe.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
+        L.vkfx_execute.argtypes = [vp, vp, vp, vp, vp]
+        L.vkfx_execute_host.argtypes = [vp, vp, u64, vp, u64]
+        L.vkfx_planner_axis.argtypes = [u64, u64, i32, i32, i32, u64, ctypes.POINTER(i32), ctypes.POINTER(u64)]
+        L.vkfx_planner_bluestein_padding.argtypes = [u64, u64, i32, u64, ctypes.POINTER(u64)]
+        L.vkfx_planner_next_smooth.argtypes = [u64]
+        L.vkfx_planner_next_smooth.restype = u64
+        _lib = L
+    return _lib
+
+
+def _check(rc: int):
+    if rc != 0:
+        raise VkFftError(rc, lib().vkfx_last_error().decode(errors="replace"))
+
+
+def header_symbols() -> List[str]:
+    """Function names declared in include/vkfx.h."""
+    import re
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"\b(vkfx_[a-z_0-9]+)\s*\(", text)))
+
+
+# ------------------------------------------------------------------ planner
+
+def planner_axis(length: int, batch: int = 1, precision: Precision = Precision.F32, strided: bool = False,
+                 recursive_rader: bool = False, shared_memory_bytes: int = 160 * 1024):
+    """plan_c2c_axis_algorithm_for_device on the HIP/AMD profile (planner.rs:349-440)."""
+    alg, m = ctypes.c_int32(), ctypes.c_uint64()
+    _check(lib().vkfx_planner_axis(length, batch, int(precision), int(strided), int(recursive_rader),
+                                   shared_memory_bytes, ctypes.byref(alg), ctypes.byref(m)))
+    return AlgorithmKind(alg.value), int(m.value)
+
+
+def bluestein_padding(length: int, batch: int = 1, precision: Precision = Precision.F32,
+                      shared_memory_bytes: int = 160 * 1024) -> int:
+    """upstream_bluestein_auto_padding for HIP/AMD (scheduler.rs:361-373)."""
+    out = ctypes.c_uint64()
+    _check(lib().vkfx_planner_bluestein_padding(length, batch, int(precision), shared_memory_bytes,
+                                                ctypes.byref(out)))
+    return int(out.value)
+
+
+def next_smooth_at_least(target: int) -> int:
+    return int(lib().vkfx_planner_next_smooth(target))
+
+
+# ------------------------------------------------------------------- config
+
+@dataclass
+class FftConfig:
+    """Builder mirroring vkfft-rs `FftConfig` (dims slowest -> fastest)."""
+    dimensions: List[int]
+    batch_count: int = 1
+    precision: Precision = Precision.F32
+    transform: TransformKind = TransformKind.ComplexToComplex
+    normalize_inverse: bool = False
+    allow_recursive_fft_rader: bool = False
+
+    @staticmethod
+    def new(dimensions: Sequence[int]) -> "FftConfig":
+        return FftConfig(list(int(d) for d in dimensions))
+
+    def with_batch_count(self, batch: int) -> "FftConfig":
+        self.batch_count = int(batch)
+        return self
+
+    def with_precision(self, precision: Precision) -> "FftConfig":
+        self.precision = Precision(precision)
+        return self
+
+    def with_transform(self, transform: TransformKind) -> "FftConfig":
+        self.transform = TransformKind(transform)
+        return self
+
+    def with_inverse_normalization(self, normalize: bool = True) -> "FftConfig":
+        self.normalize_inverse = bool(normalize)
+        return self
+
+    def validate(self):
+        # FftConfig::validate (src/config.rs:1036): non-empty, non-zero dims
+        if not self.dimensions or len(self.dimensions) > MAX_RANK:
+            raise VkFftError(-7, "dimensions must hold 1..4 axes")
+        for axis, d in enumerate(self.dimensions):
+            if d <= 0:
+                raise VkFftError(-7, f"ZeroLength {{ axis: {axis} }}")
+        if self.batch_count <= 0:
+            raise VkFftError(-7, "batch_count must be >= 1")
+
+
+@dataclass
+class TransformIr:
+    """The plan-time object of application.rs:48-167 for this path."""
+    config: FftConfig
+    direction: Direction
+    axis_algorithms: List[AlgorithmKind] = field(default_factory=list)
+    convolution_lens: List[int] = field(default_factory=list)
+
+    @staticmethod
+    def build(config: FftConfig, direction: Direction) -> "TransformIr":
+        config.validate()
+        direction = Direction(direction)
+        if config.transform == TransformKind.RealToComplex and direction != Direction.Forward:
+            raise VkFftError(-7, "RealToComplex requires Direction::Forward")
+        if config.transform == TransformKind.ComplexToReal and direction != Direction.Inverse:
+            raise VkFftError(-7, "ComplexToReal requires Direction::Inverse")
+        ir = TransformIr(config, direction)
+        rank = len(config.dimensions)
+        for axis, n in enumerate(config.dimensions):
+            if config.transform == TransformKind.ComplexToComplex:
+                alg, m = planner_axis(n, config.batch_count, config.precision, strided=axis + 1 != rank,
+                                      recursive_rader=config.allow_recursive_fft_rader)
+            else:
+                alg, m = AlgorithmKind.Stockham, 0
+            ir.axis_algorithms.append(alg)
+            ir.convolution_lens.append(m)
+        return ir
+
+    def desc(self) -> _PlanDesc:
+        c = self.config
+        d = _PlanDesc()
+        d.rank = len(c.dimensions)
+        for i, n in enumerate(c.dimensions):
+            d.dims[i] = n
+        d.batch = c.batch_count
+        d.transform = int(c.transform)
+        d.precision = int(c.precision)
+        d.direction = int(self.direction)
+        d.normalize = int(c.normalize_inverse)
+        d.use_library_planner = 0 if self.config.transform == TransformKind.ComplexToComplex else 1
+        for i, (a, m) in enumerate(zip(self.axis_algorithms, self.convolution_lens)):
+            d.axis_algorithm[i] = int(a)
+            d.convolution_len[i] = m
+        return d
+
+    @property
+    def real_dtype(self):
+        return np.float32 if self.config.precision == Precision.F32 else np.float64
+
+    @property
+    def complex_dtype(self):
+        return np.complex64 if self.config.precision == Precision.F32 else np.complex128
+
+    def input_count(self) -> int:
+        c = self.config
+        n = int(np.prod(c.dimensions)) * c.batch_count
+        if c.transform == TransformKind.ComplexToReal:
+            return c.batch_count * (c.dimensions[-1] // 2 + 1)
+        return n
+
+    def output_count(self) -> int:
+        c = self.config
+        n = int(np.prod(c.dimensions)) * c.batch_count
+        if c.transform == TransformKind.RealToComplex:
+            return c.batch_count * (c.dimensions[-1] // 2 + 1)
+        return n
+
+
+class Plan:
+    """A built plan: launch list, tables and workspace on one device."""
+
+    def __init__(self, ctx: "HipExecutionContext", ir: TransformIr):
+        self.ctx = ctx
+        self.ir = ir
+        self.handle = ctypes.c_void_p()
+        d = ir.desc()
+        _check(lib().vkfx_plan_create(ctx.handle, ctypes.byref(d), ctypes.byref(self.handle)))
+        i, o, w = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().vkfx_plan_io_bytes(self.handle, ctypes.byref(i), ctypes.byref(o)))
+        _check(lib().vkfx_plan_workspace_bytes(self.handle, ctypes.byref(w)))
+        self.in_bytes, self.out_bytes, self.workspace_bytes = int(i.value), int(o.value), int(w.value)
+
+    def describe(self) -> dict:
+        n = lib().vkfx_plan_describe(self.handle, None, 0)
+        buf = ctypes.create_string_buffer(n + 1)
+        lib().vkfx_plan_describe(self.handle, buf, n + 1)
+        return json.loads(buf.value.decode())
+
+    def execute(self, d_in: int, d_out: int, d_work: int = 0, stream: int = 0):
+        """Device-resident asynchronous execute (raw device pointers)."""
+        _check(lib().vkfx_execute(self.handle, ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
+                                  ctypes.c_void_p(d_work or None), ctypes.c_void_p(stream or None)))
+
+    def execute_tensors(self, x, y, stream=None):
+        """Execute on torch tensors already resident on the GPU."""
+        if x.numel() * x.element_size() != self.in_bytes or y.numel() * y.element_size() != self.out_bytes:
+            raise VkFftError(-5, f"InputLengthMismatch: expected {self.in_bytes}/{self.out_bytes} bytes")
+        if not (x.is_cuda and y.is_cuda and x.is_contiguous() and y.is_contiguous()):
+            raise VkFftError(-7, "tensors must be contiguous device tensors")
+        s = stream.cuda_stream if stream is not None else 0
+        self.execute(x.data_ptr(), y.data_ptr(), 0, s)
+
+    def close(self):
+        if self.handle:
+            lib().vkfx_plan_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipExecutionContext:
+    """`HipExecutionContext::new(device_index)` over the C ABI."""
+
+    def __init__(self, device_index: int = 0):
+        self.handle = ctypes.c_void_p()
+        _check(lib().vkfx_context_create(device_index, ctypes.byref(self.handle)))
+        self._plans = {}
+
+    def device_profile(self) -> dict:
+        p = _Profile()
+        _check(lib().vkfx_context_profile(self.handle, ctypes.byref(p)))
+        return {k: (getattr(p, k).decode() if isinstance(getattr(p, k), bytes) else int(getattr(p, k)))
+                for k, _ in _Profile._fields_}
+
+    def device_name(self) -> str:
+        return self.device_profile()["name"]
+
+    def plan(self, ir: TransformIr) -> Plan:
+        key = (tuple(ir.config.dimensions), ir.config.batch_count, int(ir.config.precision),
+               int(ir.config.transform), ir.config.normalize_inverse, int(ir.direction),
+               tuple(int(a) for a in ir.axis_algorithms), tuple(ir.convolution_lens))
+        if key not in self._plans:
+            self._plans[key] = Plan(self, ir)
+        return self._plans[key]
+
+    def _execute_host(self, ir: TransformIr, x: np.ndarray, in_dtype, out_dtype, out_count):
+        x = np.ascontiguousarray(x, dtype=in_dtype).reshape(-1)
+        if x.size != ir.input_count():
+            raise VkFftError(-5, f"InputLengthMismatch {{ expected: {ir.input_count()}, actual: {x.size} }}")
+        plan = self.plan(ir)
+        out = np.empty(out_count, dtype=out_dtype)
+        _check(lib().vkfx_execute_host(plan.handle, x.ctypes.data, x.nbytes, out.ctypes.data, out.nbytes))
+        return out
+
+    def execute_transform(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
+        kind = ir.config.transform
+        if kind == TransformKind.RealToComplex:
+            return self._execute_host(ir, x, ir.real_dtype, ir.complex_dtype, ir.output_count())
+        if kind == TransformKind.ComplexToReal:
+            return self._execute_host(ir, x, ir.complex_dtype, ir.real_dtype, ir.output_count())
+        return self._execute_host(ir, x, ir.complex_dtype, ir.complex_dtype, ir.output_count())
+
+    def execute_transform_f32(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
+        if ir.config.precision != Precision.F32:
+            raise VkFftError(-4, "execute_transform_f32 needs an F32 TransformIr")
+        return self.execute_transform(ir, x)
+
+    def execute_transform_f64(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
+        if ir.config.precision != Precision.F64:
+            raise VkFftError(-4, "execute_transform_f64 needs an F64 TransformIr")
+        return self.execute_transform(ir, x)
+
+    def synchronize(self):
+        _check(lib().vkfx_context_synchronize(self.handle))
+
+    def close(self):
+        for p in self._plans.values():
+            p.close()
+        self._plans.clear()
+        if self.handle:
+            lib().vkfx_context_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
