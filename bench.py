@@ -130,8 +130,26 @@ def run_gpu(cfg, steps, warmup, rotate):
     return total_ms / steps, sum(per_launch) / len(per_launch), info
 
 
+def copy_bandwidth(nbytes=1 << 30, reps=20):
+    """Measured device-to-device copy rate (read + write bytes / time), the
+    practical HBM ceiling on this box next to the nominal 8 TB/s."""
+    import torch
+    x = torch.empty(nbytes // 4, device="cuda", dtype=torch.float32).fill_(1.0)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        y.copy_(x)
+    b.record()
+    torch.cuda.synchronize()
+    return 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+
+
 def cpu_baseline(cfg, budget_s=15.0):
-    """The oracle (C port of reference.rs, f64) on a bounded batch sample."""
+    """The oracle (C port of reference.rs, f64) on a bounded sample: the
+    config's own batch, repeated until about budget_s of CPU work is done."""
     import numpy as np
 
     from oracle import oracle as o
@@ -142,22 +160,23 @@ def cpu_baseline(cfg, budget_s=15.0):
         n *= d
     if len(cfg["dims"]) > 1 or cfg["kind"] != "c2c":
         return None
-    # time one transform to size the sample to about budget_s of CPU work
     x1 = o.complex_uniform(n, 1, np.complex128)
     t0 = time.perf_counter()
     o.fft(x1)
-    per = max(time.perf_counter() - t0, 1e-6)
-    sample = int(max(threads, min(cfg["batch"], budget_s / per)))
-    sample -= sample % threads or 0
-    sample = max(sample, threads)
-    x = o.complex_uniform(n * sample, 2, np.complex128)
+    per = max(time.perf_counter() - t0, 1e-6)          # CPU seconds per transform
+    batch = min(cfg["batch"], max(threads, int(budget_s / per)))
+    reps = max(1, int(round(budget_s / (per * batch))))
+    x = o.complex_uniform(n * batch, 2, np.complex128)
     t0 = time.perf_counter()
-    o.fft_batch(x, n, threads=threads)
+    for _ in range(reps):
+        o.fft_batch(x, n, threads=threads)
     wall = time.perf_counter() - t0
-    bytes_sample = 2 * n * sample * (8 if cfg["prec"] == "f32" else 16)
-    return {"value": round(bytes_sample / wall / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{sample} of {cfg['batch']} transforms of N={n}, oracle (reference.rs port, f64), "
-                      f"{wall:.2f} s wall on {threads} threads ({per * sample:.1f} s CPU work est.)"}
+    done = batch * reps
+    bytes_done = 2 * n * done * (8 if cfg["prec"] == "f32" else 16)
+    return {"value": round(bytes_done / wall / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} x {batch} transforms of N={n} (of batch {cfg['batch']}) through the oracle "
+                      f"(C port of reference.rs, f64), {wall:.2f} s wall on {threads} threads, "
+                      f"~{per * done:.1f} s CPU work"}
 
 
 def main():
@@ -169,16 +188,23 @@ def main():
     ap.add_argument("--all", action="store_true", help="one line per BASELINE config")
     ap.add_argument("--rotate", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--batch", type=int, default=0, help="override the config's batch (tuning runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md).",
               file=sys.stderr)
         sys.exit(2)
     names = list(CONFIGS) if args.all else [args.config]
+    copy_gbs = None
     for name in names:
-        cfg = CONFIGS[name]
+        cfg = dict(CONFIGS[name])
+        if args.batch:
+            cfg["batch"] = args.batch
+            cfg["workload"] += f"_batch_override_{args.batch}"
         steps = args.steps if name == "c1" else max(5, min(args.steps, 30))
         ms, launch_ms, info = run_gpu(cfg, steps, args.warmup, args.rotate)
+        if copy_gbs is None:
+            copy_gbs = copy_bandwidth()
         nbytes, flops = algorithmic(cfg)
         value = nbytes / (ms * 1e-3) / 1e9
         first = info["plans"][0]["passes"]
@@ -197,6 +223,8 @@ def main():
             "config": {"workload": cfg["workload"], "dims": cfg["dims"], "batch": cfg["batch"],
                        "buffer_pairs": info["pairs"]},
             "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+            "hbm_copy_gbs": round(copy_gbs, 1),
+            "pct_of_copy": round(100 * value / copy_gbs, 2),
             "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
             "roofline": roof,
             "cpu_baseline": None if (args.no_cpu or name != "c1") else cpu_baseline(cfg),

@@ -199,7 +199,10 @@ def test_c2_shape_round_trip_full_size(hip_ctx):
 
 @pytest.mark.parametrize("dims,batch,prec", [([64, 48], 2, F32), ([256, 256], 2, F32), ([17, 34], 1, F32),
                                              ([16, 12, 10], 2, F64), ([64, 64, 64], 1, F64),
-                                             ([8, 6, 5, 4], 1, F32), ([4099, 4], 1, F32)])
+                                             ([8, 6, 5, 4], 1, F32), ([4099, 4], 1, F32),
+                                             # strided axes long enough to run as two split passes
+                                             ([1024, 8], 2, F32), ([2048, 3], 1, F32), ([1000, 6], 1, F64),
+                                             ([3, 768, 5], 2, F32)])
 def test_nd_c2c(hip_ctx, dims, batch, prec):
     count = int(np.prod(dims)) * batch
     x = rand(count, count % 1000, prec)

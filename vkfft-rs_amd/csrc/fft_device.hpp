@@ -237,12 +237,46 @@ __host__ __device__ constexpr int max_butterflies_per_thread() {
 // LDS element index of element e in a line (one pad slot every 2^ps).
 __device__ __forceinline__ int lpad(int e, int ps) { return e + (e >> ps); }
 
+// Stage twiddle exp(-2 pi i m/N). Early stages (small P) touch few distinct
+// table entries per wave, so they read the full table; late stages would
+// scatter a wave over the whole table, so they combine two sqrt(N)-size
+// tables (one extra complex multiply, both tables stay in L1).
+struct StageTw {
+    const void* full;
+    const void* lo;
+    const void* hi;
+    int shift;
+};
+template <typename T>
+__device__ __forceinline__ cpx<T> stage_root(const StageTw& w, int m, bool scattered) {
+    if (!scattered) return ((const cpx<T>*)w.full)[m];
+    const cpx<T>* L = (const cpx<T>*)w.lo;
+    const cpx<T>* H = (const cpx<T>*)w.hi;
+    return cmul(H[m >> w.shift], L[m & ((1 << w.shift) - 1)]);
+}
+constexpr int kScatterP = 32;  // stages with P >= this use the two-level tables
+
+// p[i] = w^i for i < R from w = p[1] by a product tree of depth <= log2(R):
+// w^i = w^(i - 2^m) * w^(2^m), 2^m the highest power of two in i. One table
+// lookup per butterfly instead of R-1; the rounding error stays within a few
+// ulp (depth <= 4 for R = 16).
+template <int R, typename T>
+__device__ __forceinline__ void root_powers(cpx<T> w, cpx<T>* p) {
+    p[0] = mk((T)1, (T)0);
+    if constexpr (R > 1) p[1] = w;
+#pragma unroll
+    for (int i = 2; i < R; ++i) {
+        int hb = 1;
+        while (hb * 2 <= i) hb *= 2;
+        p[i] = hb == i ? cmul(p[i / 2], p[i / 2]) : cmul(p[i - hb], p[hb]);
+    }
+}
+
 // One Stockham stage over a line held in LDS, in place: every thread first
 // loads all of its butterfly inputs, the block synchronises, then writes.
 template <typename T, int S, int R>
 __device__ __forceinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
-                                          const int TT, const int t, const int ps,
-                                          const cpx<T>* __restrict__ tw) {
+                                          const int TT, const int t, const int ps, const StageTw& tw) {
     constexpr int MJ = max_butterflies_per_thread<R>();
     const int NB = N / R;
     cpx<T> v[MJ][R];
@@ -262,8 +296,10 @@ __device__ __forceinline__ void stage_lds(cpx<T>* __restrict__ line, const int N
         if (b < NB) {
             const int k = b % P;
             if (P > 1) {
+                cpx<T> wp[R];
+                root_powers<R>(stage_root<T>(tw, k * step, P >= kScatterP), wp);
 #pragma unroll
-                for (int i = 1; i < R; ++i) v[j][i] = twmul<S>(v[j][i], tw[k * i * step]);
+                for (int i = 1; i < R; ++i) v[j][i] = twmul<S>(v[j][i], wp[i]);
             }
             dft<R, S>(v[j]);
             const int base = (b - k) * R + k;
@@ -278,8 +314,7 @@ __device__ __forceinline__ void stage_lds(cpx<T>* __restrict__ line, const int N
 template <typename T, int S>
 __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int N, const int TT,
                                            const int t, const int ps, const int nst,
-                                           const int* __restrict__ radix,
-                                           const cpx<T>* __restrict__ tw) {
+                                           const int* __restrict__ radix, const StageTw& tw) {
     int P = 1;
     for (int s = 0; s < nst; ++s) {
         const int R = radix[s];

@@ -1,10 +1,10 @@
 // fft_kernels_impl.hpp -- gfx950 kernels of the batched FFT path.
 //
 // Every kernel is one HBM pass over a set of "lines" (1-D sequences along one
-// axis). A block owns G lines; each line is staged in LDS, transformed there
-// by the Stockham stages of fft_device.hpp, and written back. IO policies
+// axis). A block owns G lines; each line is transformed by the Stockham
+// stages of fft_device.hpp with LDS exchanges between stages. IO policies
 // decide where a line lives in HBM and which pointwise work is fused into the
-// load (prologue) and the store (epilogue):
+// load and the store:
 //
 //   IoPlain       C2C along any axis (contiguous rows or strided columns)
 //   IoR2CFull     odd-length R2C through a full complex FFT (real_ir.rs:935-946)
@@ -23,6 +23,14 @@
 //                 the inverse four-step twiddle in one kernel
 //   IoFsCBlue     Bluestein column pass: IFFT, chirp multiply, truncate to N
 //   IoBlue1       whole Bluestein transform when the convolution fits LDS
+//
+// Two kernel templates run these policies:
+//   k_dyn  -- runtime length and radix list; lines are staged through LDS on
+//             both ends (any length the planner accepts).
+//   k_fix  -- compile-time shape (length, radices, threads per line, lines per
+//             block, lane mapping). When the lane mapping matches the memory
+//             layout the first stage reads HBM straight into registers and the
+//             last stage writes registers straight to HBM.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -33,18 +41,44 @@ namespace vkfx {
 
 struct LineInfo {
     long long ib, ob, o, c;
+    long long tr;  // four-step twiddle row (c / twdiv)
     int valid;
 };
 
-__device__ __forceinline__ LineInfo line_default(const KArgs& a, unsigned blk, int g) {
+enum Layout : int { LAY_ANY = 0, LAY_ROW = 1, LAY_COL = 2, LAY_STAGED = 3 };
+
+// Runtime dimensions (k_dyn) and compile-time dimensions (k_fix) seen by the
+// IO policies through the same interface.
+struct DynDims {
+    static __device__ __forceinline__ int N(const KArgs& a) { return a.N; }
+    static __device__ __forceinline__ int G(const KArgs& a) { return a.G; }
+    static __device__ __forceinline__ int LS(const KArgs& a) { return a.LS; }
+    static __device__ __forceinline__ int PS(const KArgs& a) { return a.PS; }
+};
+template <int N_, int G_, int LS_, int PS_>
+struct FixDims {
+    static __device__ __forceinline__ constexpr int N(const KArgs&) { return N_; }
+    static __device__ __forceinline__ constexpr int G(const KArgs&) { return G_; }
+    static __device__ __forceinline__ constexpr int LS(const KArgs&) { return LS_; }
+    static __device__ __forceinline__ constexpr int PS(const KArgs&) { return PS_; }
+};
+
+__device__ __forceinline__ LineInfo line_default(const KArgs& a, long long blk, int g) {
     LineInfo L;
-    long long line = (long long)blk * a.G + g;
+    long long line = blk * a.G + g;
     L.valid = line < a.nlines;
     if (!L.valid) line = 0;
-    L.o = line / a.C;
-    L.c = line - L.o * a.C;
-    L.ib = L.o * a.in_os + L.c * a.in_cs;
-    L.ob = L.o * a.out_os + L.c * a.out_cs;
+    const long long r = line / a.C;
+    L.c = line - r * a.C;
+    long long o1 = 0;
+    L.o = r;
+    if (a.C1 > 1) {
+        L.o = r / a.C1;
+        o1 = r - L.o * a.C1;
+    }
+    L.ib = L.o * a.in_os + o1 * a.in_os1 + L.c * a.in_cs;
+    L.ob = L.o * a.out_os + o1 * a.out_os1 + L.c * a.out_cs;
+    L.tr = a.twdiv > 1 ? L.c / a.twdiv : L.c;
     return L;
 }
 
@@ -78,81 +112,112 @@ __device__ __forceinline__ cpx<T> zero() {
     return mk((T)0, (T)0);
 }
 
+// Generic staged prologue/epilogue built from the element functions.
+template <class IO, class D, typename T>
+__device__ __forceinline__ void staged_load(const KArgs& a, cpx<T>* lds, const LineInfo* li, bool rowmajor) {
+    coop_for(D::G(a), D::N(a), rowmajor, [&](int g, int e) {
+        lds[g * D::LS(a) + lpad(e, D::PS(a))] = li[g].valid ? IO::template load_elem<T>(a, li[g], e) : zero<T>();
+    });
+}
+template <class IO, class D, typename T, int S>
+__device__ __forceinline__ void staged_store(const KArgs& a, const cpx<T>* lds, const LineInfo* li, bool rowmajor) {
+    coop_for(D::G(a), IO::template out_count<D>(a), rowmajor, [&](int g, int e) {
+        if (li[g].valid) IO::template store_elem<T, S>(a, li[g], e, lds[g * D::LS(a) + lpad(e, D::PS(a))]);
+    });
+}
+
 // ---------------------------------------------------------------- IO kinds
 
 struct IoPlain {
     static constexpr bool kTwoPass = false;
-    static __device__ LineInfo line(const KArgs& a, unsigned blk, int g) { return line_default(a, blk, g); }
+    static constexpr bool kStoreTw = false;  // store multiplies by a per-element pass twiddle
+    static constexpr int kLoad = LAY_ANY;
+    static constexpr int kStore = LAY_ANY;
+    static __device__ LineInfo line(const KArgs& a, long long blk, int g) { return line_default(a, blk, g); }
+    template <class D>
+    static __device__ __forceinline__ int out_count(const KArgs& a) { return D::N(a); }
     template <typename T>
-    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
-        const cpx<T>* in = (const cpx<T>*)a.in;
-        coop_for(a.G, a.N, a.flags & KF_IN_ROWMAJOR, [&](int g, int e) {
-            lds[g * a.LS + lpad(e, a.PS)] = li[g].valid ? in[li[g].ib + e * a.in_es] : zero<T>();
-        });
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        return ((const cpx<T>*)a.in)[L.ib + e * a.in_es];
     }
     template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(v, (T)a.scale);
+    }
+    // staged variants used when an end cannot be direct
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, a.flags & KF_IN_ROWMAJOR);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        const T s = (T)a.scale;
-        coop_for(a.G, a.N, a.flags & KF_OUT_ROWMAJOR, [&](int g, int e) {
-            if (li[g].valid) out[li[g].ob + e * a.out_es] = scale(lds[g * a.LS + lpad(e, a.PS)], s);
-        });
+        staged_store<IoPlain, D, T, S>(a, lds, li, a.flags & KF_OUT_ROWMAJOR);
     }
 };
 
 struct IoR2CFull : IoPlain {
+    template <class D>
+    static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
     template <typename T>
-    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
-        const T* in = (const T*)a.in;
-        coop_for(a.G, a.N, a.flags & KF_IN_ROWMAJOR, [&](int g, int e) {
-            lds[g * a.LS + lpad(e, a.PS)] = li[g].valid ? mk(in[li[g].ib + e * a.in_es], (T)0) : zero<T>();
-        });
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        return mk(((const T*)a.in)[L.ib + e * a.in_es], (T)0);
     }
     template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        if (e < a.nout) ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(v, (T)a.scale);
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoR2CFull, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        const T s = (T)a.scale;
-        coop_for(a.G, (int)a.nout, a.flags & KF_OUT_ROWMAJOR, [&](int g, int e) {
-            if (li[g].valid) out[li[g].ob + e * a.out_es] = scale(lds[g * a.LS + lpad(e, a.PS)], s);
-        });
+        staged_store<IoR2CFull, D, T, S>(a, lds, li, true);
     }
 };
 
 struct IoC2RFull : IoPlain {
     template <typename T>
-    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
         const int n = a.N, h = n / 2 + 1;
-        coop_for(a.G, n, a.flags & KF_IN_ROWMAJOR, [&](int g, int e) {
-            cpx<T> v = zero<T>();
-            if (li[g].valid) v = e < h ? in[li[g].ib + e * a.in_es] : conj(in[li[g].ib + (n - e) * a.in_es]);
-            lds[g * a.LS + lpad(e, a.PS)] = v;
-        });
+        return e < h ? in[L.ib + e * a.in_es] : conj(in[L.ib + (n - e) * a.in_es]);
     }
     template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        ((T*)a.out)[L.ob + e * a.out_es] = v.re * (T)a.scale;
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoC2RFull, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        T* out = (T*)a.out;
-        const T s = (T)a.scale;
-        coop_for(a.G, a.N, a.flags & KF_OUT_ROWMAJOR, [&](int g, int e) {
-            if (li[g].valid) out[li[g].ob + e * a.out_es] = lds[g * a.LS + lpad(e, a.PS)].re * s;
-        });
+        staged_store<IoC2RFull, D, T, S>(a, lds, li, true);
     }
 };
 
-// Even-length R2C with the half-size FFT (length M = a.N) in LDS. Input is
-// the real line viewed as M complex pairs z[n] = x[2n] + i x[2n+1].
+// Even-length R2C with the half-size FFT (length M = N) in LDS. Input is the
+// real line viewed as M complex pairs z[n] = x[2n] + i x[2n+1]; the store
+// needs Z[k] and Z[M-k] together, so it is always staged.
 struct IoR2CHalf : IoPlain {
-    template <typename T, int S>
+    static constexpr int kLoad = LAY_ROW;
+    static constexpr int kStore = LAY_STAGED;
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
         cpx<T>* out = (cpx<T>*)a.out;
-        const int M = a.N;
-        coop_for(a.G, M + 1, a.flags & KF_OUT_ROWMAJOR, [&](int g, int k) {
+        const int M = D::N(a);
+        coop_for(D::G(a), M + 1, true, [&](int g, int k) {
             if (!li[g].valid) return;
-            const cpx<T>* Z = lds + g * a.LS;
+            const cpx<T>* Z = lds + g * D::LS(a);
             const int k0 = k == M ? 0 : k;
             const int km = k == 0 ? 0 : M - k;
-            cpx<T> A = Z[lpad(k0, a.PS)];
-            cpx<T> B = conj(Z[lpad(km, a.PS)]);
+            cpx<T> A = Z[lpad(k0, D::PS(a))];
+            cpx<T> B = conj(Z[lpad(km, D::PS(a))]);
             cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
             cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
             out[li[g].ob + k * a.out_es] = scale(X, (T)0.5);
@@ -163,79 +228,96 @@ struct IoR2CHalf : IoPlain {
 // Even-length C2R: Z[k] = (X[k] + conj X[M-k]) + i W_N^-k (X[k] - conj X[M-k]),
 // then the inverse half-size FFT; the complex result is the real output pairs.
 struct IoC2RHalf : IoPlain {
+    static constexpr int kLoad = LAY_ROW;
+    static constexpr int kStore = LAY_ROW;
     template <typename T>
-    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int k) {
         const cpx<T>* in = (const cpx<T>*)a.in;
-        const int M = a.N;
-        coop_for(a.G, M, a.flags & KF_IN_ROWMAJOR, [&](int g, int k) {
-            cpx<T> Z = zero<T>();
-            if (li[g].valid) {
-                cpx<T> X = in[li[g].ib + k * a.in_es];
-                cpx<T> Xm = conj(in[li[g].ib + (M - k) * a.in_es]);
-                cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
-                Z = (X + Xm) + muli<1>(cmulc(X - Xm, w));
-            }
-            lds[g * a.LS + lpad(k, a.PS)] = Z;
-        });
+        cpx<T> X = in[L.ib + k * a.in_es];
+        cpx<T> Xm = conj(in[L.ib + (a.N - k) * a.in_es]);
+        cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
+        return (X + Xm) + muli<1>(cmulc(X - Xm, w));
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoC2RHalf, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoPlain, D, T, S>(a, lds, li, true);
     }
 };
 
 // Four-step column pass. Line = column n2 of the [N1][N2] view (C = N2);
-// FFT over n1 (length N1 = a.N); store Y[k1][n2] * W_M^(dir * n2 * k1).
+// FFT over n1 (length N1); store Y[k1][n2] * W_M^(dir * n2 * k1).
 struct IoFsA : IoPlain {
+    static constexpr int kLoad = LAY_COL;
+    static constexpr int kStore = LAY_COL;
+    static constexpr bool kStoreTw = true;
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> tw_root(const KArgs& a, long long m) {
+        return tw2<T>(a.tlo, a.thi, a.tshift, m);
+    }
     template <typename T, int S>
+    static __device__ __forceinline__ void store_twiddled(const KArgs& a, const LineInfo& L, int e, cpx<T> v,
+                                                          cpx<T> w) {
+        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = twmul<S>(v, w);
+    }
+    template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        store_twiddled<T, S>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.tr * e));
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, false);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        coop_for(a.G, a.N, false, [&](int g, int e) {
-            if (!li[g].valid) return;
-            cpx<T> w = tw2<T>(a.tlo, a.thi, a.tshift, li[g].c * e);
-            out[li[g].ob + e * a.out_es] = twmul<S>(lds[g * a.LS + lpad(e, a.PS)], w);
-        });
+        staged_store<IoFsA, D, T, S>(a, lds, li, false);
     }
 };
 
 struct IoFsABlue : IoFsA {
     template <typename T>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        const long long n = L.c + (long long)e * a.N2;
+        if (n >= a.nvalid) return zero<T>();
+        return cmul(((const cpx<T>*)a.in)[L.ib + e * a.in_es], ((const cpx<T>*)a.chirp)[n]);
+    }
+    template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
-        const cpx<T>* in = (const cpx<T>*)a.in;
-        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
-        coop_for(a.G, a.N, false, [&](int g, int e) {
-            const long long n = li[g].c + (long long)e * a.N2;
-            cpx<T> v = zero<T>();
-            if (li[g].valid && n < a.nvalid) v = cmul(in[li[g].ib + e * a.in_es], chirp[n]);
-            lds[g * a.LS + lpad(e, a.PS)] = v;
-        });
+        staged_load<IoFsABlue, D>(a, lds, li, false);
     }
 };
 
 struct IoFsAC2R : IoFsA {
     template <typename T>
-    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
-        coop_for(a.G, a.N, false, [&](int g, int e) {
-            cpx<T> Z = zero<T>();
-            if (li[g].valid) {
-                const long long k = li[g].c + (long long)e * a.N2;
-                cpx<T> X = in[li[g].ib + e * a.in_es];
-                cpx<T> Xm = conj(in[li[g].o * a.in_os + (a.M - k)]);
-                cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
-                Z = (X + Xm) + muli<1>(cmulc(X - Xm, w));
-            }
-            lds[g * a.LS + lpad(e, a.PS)] = Z;
-        });
+        const long long k = L.c + (long long)e * a.N2;
+        cpx<T> X = in[L.ib + e * a.in_es];
+        cpx<T> Xm = conj(in[L.o * a.in_os + (a.M - k)]);
+        cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
+        return (X + Xm) + muli<1>(cmulc(X - Xm, w));
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoFsAC2R, D>(a, lds, li, false);
     }
 };
 
 // Four-step row pass. Line = row k1 (C = N1), contiguous in the scratch;
-// FFT over n2 (length N2 = a.N); store X[k1 + N1*k2] (column-coalesced).
+// FFT over n2 (length N2); store X[k1 + N1*k2] (column-coalesced).
 struct IoFsB : IoPlain {
-    template <typename T, int S>
+    static constexpr int kLoad = LAY_ROW;
+    static constexpr int kStore = LAY_COL;
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        const T s = (T)a.scale;
-        coop_for(a.G, a.N, false, [&](int g, int e) {
-            if (li[g].valid) out[li[g].ob + e * a.out_es] = scale(lds[g * a.LS + lpad(e, a.PS)], s);
-        });
+        staged_store<IoPlain, D, T, S>(a, lds, li, false);
     }
 };
 
@@ -244,7 +326,9 @@ struct IoFsB : IoPlain {
 // row 0), so Z[k] and Z[M-k] are both in its LDS when the postprocess
 // X[k] = 1/2 [(Z[k] + conj Z[M-k]) - i W_N^k (Z[k] - conj Z[M-k])] runs.
 struct IoFsBR2C : IoPlain {
-    static __device__ LineInfo line(const KArgs& a, unsigned blk, int g) {
+    static constexpr int kLoad = LAY_ROW;
+    static constexpr int kStore = LAY_STAGED;
+    static __device__ LineInfo line(const KArgs& a, long long blk, int g) {
         const int H = a.G / 2;
         const long long nbk = a.N1 / (2 * H);
         LineInfo L;
@@ -260,16 +344,21 @@ struct IoFsBR2C : IoPlain {
         L.valid = L.o * a.N1 < a.nlines;
         if (!L.valid) L.o = 0;
         L.c = k1;
+        L.tr = k1;
         L.ib = L.o * a.in_os + k1 * a.in_cs;
         L.ob = L.o * a.out_os;
         return L;
     }
-    template <typename T, int S>
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
         cpx<T>* out = (cpx<T>*)a.out;
-        const int H = a.G / 2;
-        const int N2 = a.N;
-        coop_for(a.G, N2, false, [&](int g, int k2) {
+        const int G = D::G(a), H = G / 2;
+        const int N2 = D::N(a);
+        coop_for(G, N2, false, [&](int g, int k2) {
             if (!li[g].valid) return;
             const long long k1 = li[g].c;
             int gp, k2m;
@@ -284,8 +373,8 @@ struct IoFsBR2C : IoPlain {
                 k2m = N2 - 1 - k2;
             }
             const long long k = k1 + a.N1 * k2;
-            cpx<T> A = lds[g * a.LS + lpad(k2, a.PS)];
-            cpx<T> B = conj(lds[gp * a.LS + lpad(k2m, a.PS)]);
+            cpx<T> A = lds[g * D::LS(a) + lpad(k2, D::PS(a))];
+            cpx<T> B = conj(lds[gp * D::LS(a) + lpad(k2m, D::PS(a))]);
             cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
             cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
             out[li[g].ob + k] = scale(X, (T)0.5);
@@ -299,121 +388,298 @@ struct IoFsBR2C : IoPlain {
 // the inverse four-step twiddle W_M^(-k1*m2); rows stay in place.
 struct IoBlueB : IoPlain {
     static constexpr bool kTwoPass = true;
-    template <typename T>
+    static constexpr int kLoad = LAY_ROW;
+    static constexpr int kStore = LAY_ROW;
+    template <typename T, class D>
     static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
         const cpx<T>* spec = (const cpx<T>*)a.spec;
-        coop_for(a.G, a.N, true, [&](int g, int e) {
-            cpx<T>& v = lds[g * a.LS + lpad(e, a.PS)];
-            v = cmul(v, spec[li[g].c * a.N + e]);
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
+            v = cmul(v, spec[li[g].c * D::N(a) + e]);
         });
     }
+    static constexpr bool kStoreTw = true;
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> tw_root(const KArgs& a, long long m) {
+        return tw2<T>(a.tlo, a.thi, a.tshift, m);
+    }
+    // the inverse pass twiddle root(-k1*m2) regardless of the kernel direction
     template <typename T, int S>
+    static __device__ __forceinline__ void store_twiddled(const KArgs& a, const LineInfo& L, int e, cpx<T> v,
+                                                          cpx<T> w) {
+        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = cmulc(v, w);
+    }
+    template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        store_twiddled<T, S>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.c * e));
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        coop_for(a.G, a.N, true, [&](int g, int e) {
-            if (!li[g].valid) return;
-            cpx<T> w = tw2<T>(a.tlo, a.thi, a.tshift, li[g].c * e);
-            out[li[g].ob + e * a.out_es] = cmulc(lds[g * a.LS + lpad(e, a.PS)], w);
-        });
+        staged_store<IoBlueB, D, T, S>(a, lds, li, true);
     }
 };
 
 // Bluestein column pass: inverse FFT over k1 gives conv[m2 + N2*m1]; keep
 // m < N and multiply by the chirp (and the caller's scale).
 struct IoFsCBlue : IoPlain {
+    static constexpr int kLoad = LAY_COL;
+    static constexpr int kStore = LAY_COL;
     template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        const long long m = L.c + (long long)e * a.N2;
+        if (m >= a.nout) return;
+        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(cmul(v, ((const cpx<T>*)a.chirp)[m]), (T)a.scale);
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoPlain, D>(a, lds, li, false);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
-        const T s = (T)a.scale;
-        coop_for(a.G, a.N, false, [&](int g, int e) {
-            const long long m = li[g].c + (long long)e * a.N2;
-            if (!li[g].valid || m >= a.nout) return;
-            out[li[g].ob + e * a.out_es] = scale(cmul(lds[g * a.LS + lpad(e, a.PS)], chirp[m]), s);
-        });
+        staged_store<IoFsCBlue, D, T, S>(a, lds, li, false);
     }
 };
 
-// Whole Bluestein transform in LDS: a = chirp * x zero-padded to M = a.N,
+// Whole Bluestein transform in LDS: a = chirp * x zero-padded to M = N,
 // FFT, multiply by the kernel spectrum, IFFT, chirp multiply, truncate.
 struct IoBlue1 : IoPlain {
     static constexpr bool kTwoPass = true;
+    template <class D>
+    static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
     template <typename T>
-    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
-        const cpx<T>* in = (const cpx<T>*)a.in;
-        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
-        coop_for(a.G, a.N, a.flags & KF_IN_ROWMAJOR, [&](int g, int e) {
-            cpx<T> v = zero<T>();
-            if (li[g].valid && e < a.nvalid) v = cmul(in[li[g].ib + e * a.in_es], chirp[e]);
-            lds[g * a.LS + lpad(e, a.PS)] = v;
-        });
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        if (e >= a.nvalid) return zero<T>();
+        return cmul(((const cpx<T>*)a.in)[L.ib + e * a.in_es], ((const cpx<T>*)a.chirp)[e]);
     }
-    template <typename T>
+    template <typename T, int S>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        if (e >= a.nout) return;
+        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(cmul(v, ((const cpx<T>*)a.chirp)[e]), (T)a.scale);
+    }
+    template <typename T, class D>
     static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
         const cpx<T>* spec = (const cpx<T>*)a.spec;
-        coop_for(a.G, a.N, true, [&](int g, int e) {
-            cpx<T>& v = lds[g * a.LS + lpad(e, a.PS)];
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
             v = cmul(v, spec[e]);
         });
     }
-    template <typename T, int S>
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoBlue1, D>(a, lds, li, a.flags & KF_IN_ROWMAJOR);
+    }
+    template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
-        cpx<T>* out = (cpx<T>*)a.out;
-        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
-        const T s = (T)a.scale;
-        coop_for(a.G, (int)a.nout, a.flags & KF_OUT_ROWMAJOR, [&](int g, int e) {
-            if (li[g].valid)
-                out[li[g].ob + e * a.out_es] = scale(cmul(lds[g * a.LS + lpad(e, a.PS)], chirp[e]), s);
-        });
+        staged_store<IoBlue1, D, T, S>(a, lds, li, a.flags & KF_OUT_ROWMAJOR);
     }
 };
 
-// ------------------------------------------------------------------ kernel
+// ------------------------------------------------------- dynamic kernel
 
 template <typename T, int S, class IO>
-__global__ __launch_bounds__(512) void k_fft(const KArgs a) {
+__global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
     __shared__ LineInfo li[kMaxLinesPerBlock];
     const int tid = threadIdx.x;
     if (tid < a.G) li[tid] = IO::line(a, blockIdx.x, tid);
     __syncthreads();
-    IO::template prologue<T>(a, lds, li);
+    IO::template prologue<T, DynDims>(a, lds, li);
     __syncthreads();
     const int g = tid / a.TT, t = tid - g * a.TT;
     cpx<T>* line = lds + g * a.LS;
-    const cpx<T>* tw = (const cpx<T>*)a.tw;
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
     run_stages<T, S>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
     if constexpr (IO::kTwoPass) {
-        IO::template mid<T>(a, lds, li);
+        IO::template mid<T, DynDims>(a, lds, li);
         __syncthreads();
         run_stages<T, -S>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
     }
-    IO::template epilogue<T, S>(a, lds, li);
+    IO::template epilogue<T, S, DynDims>(a, lds, li);
+}
+
+// -------------------------------------------------- fixed-shape kernel
+
+template <int... R>
+struct RList {};
+
+// N: length, TT: threads per line, G: lines per block, PS: LDS pad shift,
+// COL: lane mapping (false: threads of a line are adjacent lanes, for lines
+// contiguous in HBM; true: lines are adjacent lanes, for strided lines).
+// LS: LDS stride between lines in elements (chosen per shape to keep the
+// stage reads and writes free of bank conflicts).
+template <int N_, int TT_, int G_, int PS_, int LS_, bool COL_, int... R>
+struct Shape {
+    static constexpr int N = N_, TT = TT_, G = G_, PS = PS_, LS = LS_;
+    static constexpr bool COL = COL_;
+    static_assert(LS_ >= N_ + ((N_ - 1) >> PS_), "LDS line stride too small");
+    using Radices = RList<R...>;
+    using Dims = FixDims<N_, G_, LS_, PS_>;
+};
+
+// One stage with compile-time geometry. SRC/DST: 0 = the line in LDS,
+// 1 = HBM through the IO policy's element functions.
+template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST>
+__device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line, const LineInfo& L, int t,
+                                       const StageTw& tw) {
+    constexpr int NB = N / R;
+    constexpr int MJ = (NB + TT - 1) / TT;
+    constexpr bool EXACT = (NB % TT) == 0;
+    cpx<T> v[MJ][R];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int b = t + j * TT;
+        if (EXACT || b < NB) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int e = b + i * NB;
+                if constexpr (SRC) {
+                    v[j][i] = L.valid ? IO::template load_elem<T>(a, L, e) : zero<T>();
+                } else {
+                    v[j][i] = line[lpad(e, PS)];
+                }
+            }
+        }
+    }
+    if constexpr (!SRC) __syncthreads();
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int b = t + j * TT;
+        if (EXACT || b < NB) {
+            const int k = b % P;
+            if constexpr (P > 1) {
+                constexpr int step = N / (P * R);
+                cpx<T> wp[R];
+                root_powers<R>(stage_root<T>(tw, k * step, P >= kScatterP), wp);
+#pragma unroll
+                for (int i = 1; i < R; ++i) v[j][i] = twmul<S>(v[j][i], wp[i]);
+            }
+            dft<R, S>(v[j]);
+            const int base = (b - k) * R + k;
+            if constexpr (DST && IO::kStoreTw) {
+                // last stage: outputs o = b + q*N/R carry the pass twiddle
+                // root(tr*o) = root(tr*b) * root(tr*N/R)^q
+                if (L.valid) {
+                    const cpx<T> wb = IO::template tw_root<T>(a, L.tr * b);
+                    cpx<T> sp[R];
+                    root_powers<R>(IO::template tw_root<T>(a, L.tr * NB), sp);
+#pragma unroll
+                    for (int q = 0; q < R; ++q)
+                        IO::template store_twiddled<T, S>(a, L, base + q * P, v[j][q], cmul(wb, sp[q]));
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < R; ++q) {
+                    const int o = base + q * P;
+                    if constexpr (DST) {
+                        if (L.valid) IO::template store_elem<T, S>(a, L, o, v[j][q]);
+                    } else {
+                        line[lpad(o, PS)] = v[j][q];
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (!DST) __syncthreads();
+}
+
+template <typename T, int S, class IO, class Sh, int SRC0, int DSTL, int P, int R, int... Rest>
+__device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, const LineInfo& L, int t,
+                                        const StageTw& tw, RList<R, Rest...>) {
+    constexpr bool last = sizeof...(Rest) == 0;
+    fstage<T, S, IO, Sh::N, P, R, Sh::TT, Sh::PS, (P == 1 ? SRC0 : 0), (last ? DSTL : 0)>(a, line, L, t, tw);
+    if constexpr (!last) fstages<T, S, IO, Sh, SRC0, DSTL, P * R>(a, line, L, t, tw, RList<Rest...>{});
+}
+
+template <class IO, bool COL>
+struct Direct {
+    static constexpr int mine = COL ? LAY_COL : LAY_ROW;
+    static constexpr bool load = IO::kLoad == LAY_ANY || IO::kLoad == mine;
+    static constexpr bool store = IO::kStore == LAY_ANY || IO::kStore == mine;
+};
+
+template <typename T, int S, class IO, class Sh>
+__device__ __forceinline__ void fix_body(const KArgs& a, cpx<T>* lds, LineInfo* li, long long blk) {
+    using D = typename Sh::Dims;
+    constexpr bool LD = Direct<IO, Sh::COL>::load;
+    constexpr bool SD = Direct<IO, Sh::COL>::store;
+    const int tid = threadIdx.x;
+    if (tid < Sh::G) li[tid] = IO::line(a, blk, tid);
+    __syncthreads();
+    const int g = Sh::COL ? tid % Sh::G : tid / Sh::TT;
+    const int t = Sh::COL ? tid / Sh::G : tid % Sh::TT;
+    cpx<T>* line = lds + g * Sh::LS;
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
+    const LineInfo L = li[g];
+    if constexpr (!LD) {
+        IO::template prologue<T, D>(a, lds, li);
+        __syncthreads();
+    }
+    if constexpr (IO::kTwoPass) {
+        fstages<T, S, IO, Sh, LD ? 1 : 0, 0, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        IO::template mid<T, D>(a, lds, li);
+        __syncthreads();
+        fstages<T, -S, IO, Sh, 0, SD ? 1 : 0, 1>(a, line, L, t, tw, typename Sh::Radices{});
+    } else {
+        fstages<T, S, IO, Sh, LD ? 1 : 0, SD ? 1 : 0, 1>(a, line, L, t, tw, typename Sh::Radices{});
+    }
+    if constexpr (!SD) IO::template epilogue<T, S, D>(a, lds, li);
+}
+
+// One block per group of G lines (grid = number of groups).
+template <typename T, int S, class IO, class Sh>
+__global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ LineInfo li[Sh::G];
+    fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blockIdx.x);
+}
+
+// Persistent variant: a grid sized to the resident capacity walks the groups
+// with a grid stride, so the groups in flight stay within a compact window of
+// HBM and no workgroup is dispatched per group.
+template <typename T, int S, class IO, class Sh>
+__global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix_persist(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ LineInfo li[Sh::G];
+    for (long long blk = blockIdx.x; blk < a.nblk; blk += gridDim.x) {
+        fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blk);
+        __syncthreads();
+    }
 }
 
 // ------------------------------------------------------------- selection
 
-using KernelFn = void (*)(const KArgs);
-
 template <typename T, int S>
 KernelFn pick(KernelKind kind) {
     switch (kind) {
-        case KK_PLAIN: return k_fft<T, S, IoPlain>;
-        case KK_R2C_FULL: return k_fft<T, S, IoR2CFull>;
-        case KK_C2R_FULL: return k_fft<T, S, IoC2RFull>;
-        case KK_R2C_HALF: return k_fft<T, S, IoR2CHalf>;
-        case KK_C2R_HALF: return k_fft<T, S, IoC2RHalf>;
-        case KK_FS_A: return k_fft<T, S, IoFsA>;
-        case KK_FS_A_BLUE: return k_fft<T, S, IoFsABlue>;
-        case KK_FS_A_C2R: return k_fft<T, S, IoFsAC2R>;
-        case KK_FS_B: return k_fft<T, S, IoFsB>;
-        case KK_FS_B_R2C: return k_fft<T, S, IoFsBR2C>;
-        case KK_BLUE_B: return k_fft<T, S, IoBlueB>;
-        case KK_FS_C_BLUE: return k_fft<T, S, IoFsCBlue>;
-        case KK_BLUE_1: return k_fft<T, S, IoBlue1>;
+        case KK_PLAIN: return k_dyn<T, S, IoPlain>;
+        case KK_R2C_FULL: return k_dyn<T, S, IoR2CFull>;
+        case KK_C2R_FULL: return k_dyn<T, S, IoC2RFull>;
+        case KK_R2C_HALF: return k_dyn<T, S, IoR2CHalf>;
+        case KK_C2R_HALF: return k_dyn<T, S, IoC2RHalf>;
+        case KK_FS_A: return k_dyn<T, S, IoFsA>;
+        case KK_FS_A_BLUE: return k_dyn<T, S, IoFsABlue>;
+        case KK_FS_A_C2R: return k_dyn<T, S, IoFsAC2R>;
+        case KK_FS_B: return k_dyn<T, S, IoFsB>;
+        case KK_FS_B_R2C: return k_dyn<T, S, IoFsBR2C>;
+        case KK_BLUE_B: return k_dyn<T, S, IoBlueB>;
+        case KK_FS_C_BLUE: return k_dyn<T, S, IoFsCBlue>;
+        case KK_BLUE_1: return k_dyn<T, S, IoBlue1>;
         default: return nullptr;
     }
 }
 
 }  // namespace vkfx
+
+// Registry entry of one fixed-shape instantiation. Radix lists are
+// zero-terminated; nst is filled in by the registry lookup.
+#define VKFX_FIXED(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, ...)                                   \
+    FixedKernel {                                                                                     \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, 0, {__VA_ARGS__},                                        \
+            (KernelFn)(k_fix<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>),                    \
+            (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)             \
+    }

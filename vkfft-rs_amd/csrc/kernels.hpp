@@ -39,7 +39,10 @@ struct KArgs {
     void* out;
     long long in_es, in_cs, in_os;     // input element / column / outer strides
     long long out_es, out_cs, out_os;  // output strides
-    long long C;                       // columns per outer index (line = o*C + c)
+    long long C;                       // columns per outer index (line = (o2*C1 + o1)*C + c)
+    long long C1;                      // second outer level (1 = single level)
+    long long in_os1, out_os1;         // strides of the second outer level
+    long long twdiv;                   // four-step twiddle row = c / twdiv
     long long nlines;                  // total lines
     int N;                             // FFT length run in LDS
     int TT;                            // threads per line
@@ -50,6 +53,9 @@ struct KArgs {
     int radix[kMaxStages];
     int flags;
     const void* tw;                    // exp(-2 pi i k/N), k < N
+    const void* swlo;                  // same roots as two sqrt(N)-size tables:
+    const void* swhi;                  //   root(m) = swhi[m >> swshift] * swlo[m & mask]
+    int swshift;
     double scale;
     const void* chirp;                 // Bluestein chirp, logical length
     const void* spec;                  // Bluestein kernel spectrum (1/M folded in)
@@ -63,12 +69,35 @@ struct KArgs {
     long long nvalid;                  // logical input length (zero pad beyond)
     long long nout;                    // logical output length per line (truncate)
     long long N1, N2;                  // four-step factors (M = N1*N2)
+    long long nblk;                    // line groups (persistent kernels walk them)
 };
 
+using KernelFn = void (*)(const KArgs);
+
+// A kernel instantiated for one compile-time shape (fft_kernels_impl.hpp
+// k_fix): the host must launch it with exactly this geometry.
+struct FixedKernel {
+    KernelKind kind;
+    int prec, dir;
+    int N, TT, G, PS, LS;
+    bool col;  // lanes run across lines (strided layouts)
+    int nst;
+    int radix[8];
+    KernelFn fn;          // one block per group of G lines
+    KernelFn fn_persist;  // grid-stride over groups, grid sized to residency
+};
+
+// Finds a fixed-shape kernel for (kind, precision, first-FFT direction,
+// length, lane mapping); nullptr when only the runtime-shape kernel applies.
+// Setting VKFX_DISABLE_FIXED=1 in the environment forces the runtime-shape kernels.
+const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool col);
+
 // Launches one kernel. prec: 0 = f32, 1 = f64. dir: -1 forward, +1 inverse
-// (direction of the first FFT the kernel runs). Returns a hipError_t value.
+// (direction of the first FFT the kernel runs). fixed: the fixed-shape
+// instantiation to run, or nullptr for the runtime-shape kernel. Returns a
+// hipError_t value.
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block,
-           size_t lds_bytes, hipStream_t stream);
+           size_t lds_bytes, hipStream_t stream, const FixedKernel* fixed = nullptr);
 
 // Largest dynamic LDS a block may request on this device (bytes).
 size_t max_lds_bytes();

@@ -1,0 +1,19 @@
+// Fixed-shape Bluestein kernels (C5): N = 4099 with M = 8232 in one kernel,
+// N = 65537 with M = 131220 = 405 x 324 in three passes.
+#include "fft_kernels_impl.hpp"
+
+namespace vkfx {
+
+static const FixedKernel kTable[] = {
+    VKFX_FIXED(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 448, 1, 5, 8489, false, 8, 3, 7, 7, 7),
+    VKFX_FIXED(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 406, true, 3, 3, 3, 3, 5),
+    VKFX_FIXED(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, 4, 3, 3, 3, 3),
+    VKFX_FIXED(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 406, true, 3, 3, 3, 3, 5),
+};
+
+const FixedKernel* fixed_table_blue(int* count) {
+    *count = (int)(sizeof(kTable) / sizeof(kTable[0]));
+    return kTable;
+}
+
+}  // namespace vkfx

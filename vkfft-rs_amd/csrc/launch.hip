@@ -1,15 +1,66 @@
 // launch.hip -- dispatches a KernelKind to its instantiation and launches it.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include "kernels.hpp"
 
 namespace vkfx {
 
-using KernelFn = void (*)(const KArgs);
 KernelFn pick_f32_fwd(KernelKind kind);
 KernelFn pick_f32_inv(KernelKind kind);
 KernelFn pick_f64_fwd(KernelKind kind);
 KernelFn pick_f64_inv(KernelKind kind);
+const FixedKernel* fixed_table_plain(int* count);
+const FixedKernel* fixed_table_real(int* count);
+const FixedKernel* fixed_table_blue(int* count);
+
+const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool col) {
+    static const bool disabled = [] {
+        const char* e = getenv("VKFX_DISABLE_FIXED");
+        return e && e[0] == '1';
+    }();
+    if (disabled) return nullptr;
+    static FixedKernel* all = nullptr;
+    static int total = 0;
+    if (!all) {
+        const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_real, fixed_table_blue};
+        int counts[3], sum = 0;
+        const FixedKernel* ptrs[3];
+        for (int i = 0; i < 3; ++i) {
+            ptrs[i] = tables[i](&counts[i]);
+            sum += counts[i];
+        }
+        FixedKernel* merged = new FixedKernel[sum];
+        int k = 0;
+        for (int i = 0; i < 3; ++i)
+            for (int j = 0; j < counts[i]; ++j) {
+                merged[k] = ptrs[i][j];
+                int n = 0;
+                while (n < 8 && merged[k].radix[n]) ++n;
+                merged[k].nst = n;
+                ++k;
+            }
+        total = sum;
+        all = merged;
+    }
+    // VKFX_FIXED_PICK=k selects the k-th registered variant of a shape key
+    // (tuning runs); the default is the first.
+    static const int pick = [] {
+        const char* e = getenv("VKFX_FIXED_PICK");
+        return e ? atoi(e) : 0;
+    }();
+    const FixedKernel* first = nullptr;
+    int seen = 0;
+    for (int i = 0; i < total; ++i) {
+        const FixedKernel& f = all[i];
+        if (f.kind == kind && f.prec == prec && f.dir == dir && f.N == N && f.col == col) {
+            if (!first) first = &f;
+            if (seen++ == pick) return &f;
+        }
+    }
+    return first;
+}
 
 static int lds_limit_bytes() {
     static int cached = -1;
@@ -26,8 +77,18 @@ static int lds_limit_bytes() {
 
 size_t max_lds_bytes() { return (size_t)lds_limit_bytes(); }
 
+// Blocks per CU of a persistent launch (0 = one block per group). Tuning knob:
+// VKFX_PERSIST_BLOCKS_PER_CU.
+static int persist_blocks_per_cu() {
+    static const int v = [] {
+        const char* e = getenv("VKFX_PERSIST_BLOCKS_PER_CU");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block, size_t lds_bytes,
-           hipStream_t stream) {
+           hipStream_t stream, const FixedKernel* fixed) {
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1))
         return (int)hipErrorInvalidValue;
     if (grid == 0) return (int)hipSuccess;
@@ -38,13 +99,38 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         return (int)hipErrorInvalidConfiguration;
     KernelFn fn = prec == 0 ? (dir < 0 ? pick_f32_fwd(kind) : pick_f32_inv(kind))
                             : (dir < 0 ? pick_f64_fwd(kind) : pick_f64_inv(kind));
+    if (fixed) {
+        // the fixed shape must be launched with exactly its own geometry
+        if (fixed->kind != kind || fixed->prec != prec || fixed->dir != dir || fixed->N != a.N ||
+            fixed->TT != a.TT || fixed->G != a.G || fixed->PS != a.PS || fixed->LS != a.LS ||
+            fixed->nst != a.nstages)
+            return (int)hipErrorInvalidConfiguration;
+        for (int i = 0; i < fixed->nst; ++i)
+            if (fixed->radix[i] != a.radix[i]) return (int)hipErrorInvalidConfiguration;
+        fn = fixed->fn;
+    }
     if (!fn) return (int)hipErrorInvalidValue;
+    KArgs args = a;
+    args.nblk = grid;
+    if (fixed && persist_blocks_per_cu() > 0) {
+        // persistent launch: at most the resident capacity, groups by grid stride
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+                cus = 256;
+        }
+        fn = fixed->fn_persist;
+        const unsigned cap = (unsigned)(cus * persist_blocks_per_cu());
+        if (grid > cap) grid = cap;
+    }
     if (lds_bytes > 65536) {
         hipError_t e =
             hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
         if (e != hipSuccess) return (int)e;
     }
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(block), lds_bytes, stream, a);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(block), lds_bytes, stream, args);
     return (int)hipGetLastError();
 }
 

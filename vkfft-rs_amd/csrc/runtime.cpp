@@ -62,6 +62,7 @@ void root(ld k, ld n, ld& c, ld& s) {
 struct vkfx_context {
     int device = 0;
     hipStream_t stream = nullptr;
+    hipStream_t aux = nullptr;  // second lane for chunked plans (default priority)
     vkfx_device_profile profile{};
 };
 
@@ -78,6 +79,8 @@ struct Launch {
     int in_sel, out_sel;
     size_t in_off, out_off;  // byte offsets into the selected buffers
     std::string label;
+    const FixedKernel* fixed;
+    int chunk;  // batch chunk; chunks alternate between two stream lanes
 };
 
 // Line geometry of one FFT length inside a kernel.
@@ -86,6 +89,7 @@ struct Geometry {
     std::vector<int> radix;
     size_t lds = 0;
     bool ok = false;
+    const FixedKernel* fixed = nullptr;
 };
 
 int max_bpt(int r) {
@@ -148,6 +152,29 @@ Geometry geometry(size_t n, int prec, int want_g, size_t lds_max, size_t lds_bud
     return g;
 }
 
+// Geometry of a kernel launch: the fixed-shape instantiation for
+// (kind, precision, direction, length, lane mapping) when one is registered
+// and fits, else the runtime-shape geometry.
+Geometry kernel_geometry(KernelKind kind, int prec, int dir, size_t n, bool col, int want_g, size_t lds_max,
+                         size_t lds_budget) {
+    if (n <= (1u << 20)) {
+        if (const FixedKernel* f = find_fixed(kind, prec, dir, (int)n, col)) {
+            Geometry g;
+            g.N = f->N;
+            g.TT = f->TT;
+            g.G = f->G;
+            g.PS = f->PS;
+            g.LS = f->LS;
+            g.radix.assign(f->radix, f->radix + f->nst);
+            g.lds = (size_t)g.G * g.LS * (prec ? 16 : 8);
+            g.fixed = f;
+            g.ok = g.lds <= lds_max;
+            if (g.ok) return g;
+        }
+    }
+    return geometry(n, prec, want_g, lds_max, lds_budget);
+}
+
 }  // namespace
 
 struct vkfx_plan {
@@ -157,7 +184,10 @@ struct vkfx_plan {
     std::vector<std::unique_ptr<DevBuf>> tables;
     std::map<std::string, const void*> table_cache;
     DevBuf work;
-    size_t work_bytes = 0;
+    size_t work_bytes = 0;  // per lane while planning; total after plan_create
+    size_t work_lane = 0;   // workspace bytes of one stream lane
+    int lanes = 1;          // 2: chunks alternate between the caller's stream and the aux stream
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
     std::string json;
     DevBuf host_in, host_out;  // staging for vkfx_execute_host
@@ -389,6 +419,7 @@ struct Ctx {
     size_t lds_budget = 80 * 1024;
     std::ostringstream js;
     bool first_pass = true;
+    int cur_chunk = 0;
 };
 
 void note_pass(Ctx& c, const Launch& L) {
@@ -396,7 +427,8 @@ void note_pass(Ctx& c, const Launch& L) {
     c.first_pass = false;
     c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.a.N << ",\"lines\":" << L.a.nlines
          << ",\"grid\":" << L.grid << ",\"block\":" << L.block << ",\"lines_per_block\":" << L.a.G
-         << ",\"lds_bytes\":" << L.lds << ",\"radices\":[";
+         << ",\"lds_bytes\":" << L.lds << ",\"fixed_shape\":" << (L.fixed ? "true" : "false")
+         << ",\"radices\":[";
     for (int i = 0; i < L.a.nstages; ++i) c.js << (i ? "," : "") << L.a.radix[i];
     c.js << "]}";
 }
@@ -413,7 +445,10 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     a.nlines = nlines;
     int rc = stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
-    Launch L{kind, dir, a, grid, (unsigned)(g.G * g.TT), g.lds, in_sel, out_sel, in_off, out_off, label};
+    rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
+    if (rc) return rc;
+    Launch L{kind, dir, a, grid, (unsigned)(g.G * g.TT), g.lds, in_sel, out_sel, in_off, out_off, label, g.fixed,
+             c.cur_chunk};
     c.p->launches.push_back(L);
     return VKFX_OK;
 }
@@ -425,6 +460,8 @@ KArgs blank() {
     std::memset(&a, 0, sizeof(a));
     a.scale = 1.0;
     a.C = 1;
+    a.C1 = 1;
+    a.twdiv = 1;
     return a;
 }
 
@@ -445,20 +482,30 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     if (alg == Algorithm::Stockham) {
         Geometry g = geometry(n, prec, 256, c.lds_max, c.lds_budget);
         if (g.ok) {
-            g = geometry(n, prec, std::max(1, 256 / g.TT), c.lds_max, c.lds_budget);
-            KArgs a = blank();
-            a.in_es = a.out_es = 1;
-            a.in_os = a.out_os = (long long)n;
-            a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
-            a.scale = sc;
-            return add_launch(c, KK_PLAIN, dir, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
-                              "stockham");
+            g = kernel_geometry(KK_PLAIN, prec, dir, n, false, std::max(1, 256 / g.TT), c.lds_max, c.lds_budget);
+            // one launch by default (VKFX_SPLIT=k splits the batch for tuning runs)
+            size_t parts = 1;
+            if (const char* e = getenv("VKFX_SPLIT")) parts = std::max(1, std::min(atoi(e), 64));
+            const size_t per = (batch + parts - 1) / parts;
+            for (size_t b0 = 0; b0 < batch; b0 += per) {
+                c.cur_chunk = (int)(b0 / per);
+                const size_t cb = std::min(per, batch - b0);
+                KArgs a = blank();
+                a.in_es = a.out_es = 1;
+                a.in_os = a.out_os = (long long)n;
+                a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+                a.scale = sc;
+                int rc = add_launch(c, KK_PLAIN, dir, g, a, (long long)cb, blocks_for(cb, g.G), SEL_IN, b0 * n * cs,
+                                    SEL_OUT, b0 * n * cs, "stockham");
+                if (rc) return rc;
+            }
+            return VKFX_OK;
         }
         size_t n1, n2;
         if (!four_step_split(n, prec, c.lds_max, &n1, &n2))
             return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no two-upload four-step split for length " + std::to_string(n));
-        Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
-        Geometry gb = geometry(n2, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+        Geometry ga = kernel_geometry(KK_FS_A, prec, dir, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+        Geometry gb = kernel_geometry(KK_FS_B, prec, dir, n2, false, prec ? 8 : 16, c.lds_max, c.lds_budget);
         if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "four-step geometry");
         const size_t chunk = chunk_for(batch, n * cs);
         p->work_bytes = std::max(p->work_bytes, chunk * n * cs);
@@ -469,6 +516,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
         c.js << "\"four_step\":{\"len\":" << n << ",\"n1\":" << n1 << ",\"n2\":" << n2 << ",\"chunk\":" << chunk
              << "},";
         for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+            c.cur_chunk = (int)(b0 / chunk);
             const size_t cb = std::min(chunk, batch - b0);
             KArgs a = blank();
             a.C = (long long)n2;
@@ -497,7 +545,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     // Bluestein (and, until a Rader kernel exists, Rader-classified axes).
     const size_t M = conv_len ? conv_len : next_smooth_at_least(2 * n - 1, {2, 3, 5, 7});
     if (M < 2 * n - 1) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein convolution length below 2N-1");
-    Geometry g = geometry(M, prec, 1, c.lds_max, c.lds_max);
+    Geometry g = kernel_geometry(KK_BLUE_1, prec, -1, M, false, 1, c.lds_max, c.lds_max);
     if (g.ok) {
         BlueTables t;
         int rc = bluestein_tables(p, n, M, dir, prec, 0, 0, &t);
@@ -516,10 +564,12 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     size_t n1, n2;
     if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
         return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for Bluestein M " + std::to_string(M));
-    Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
-    Geometry gb = geometry(n2, prec, std::max(1, 256 / std::max(1, geometry(n2, prec, 1, c.lds_max, c.lds_max).TT)),
-                           c.lds_max, c.lds_budget);
-    if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "Bluestein four-step geometry");
+    Geometry ga = kernel_geometry(KK_FS_A_BLUE, prec, -1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gc = kernel_geometry(KK_FS_C_BLUE, prec, 1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gb = kernel_geometry(KK_BLUE_B, prec, -1, n2, false,
+                                  std::max(1, 256 / std::max(1, geometry(n2, prec, 1, c.lds_max, c.lds_max).TT)),
+                                  c.lds_max, c.lds_budget);
+    if (!ga.ok || !gb.ok || !gc.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "Bluestein four-step geometry");
     BlueTables t;
     int rc = bluestein_tables(p, n, M, dir, prec, n1, n2, &t);
     if (rc) return rc;
@@ -532,6 +582,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     c.js << "\"bluestein\":{\"len\":" << n << ",\"m\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
          << ",\"chunk\":" << chunk << "},";
     for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+            c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, batch - b0);
         KArgs a = blank();
         a.C = (long long)n2;
@@ -564,7 +615,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
         d.scale = sc;
         d.nout = (long long)n, d.M = (long long)M, d.N1 = (long long)n1, d.N2 = (long long)n2;
         lines = (long long)(cb * n2);
-        rc = add_launch(c, KK_FS_C_BLUE, 1, ga, d, lines, blocks_for(lines, ga.G), SEL_WORK, 0, SEL_OUT, b0 * n * cs,
+        rc = add_launch(c, KK_FS_C_BLUE, 1, gc, d, lines, blocks_for(lines, gc.G), SEL_WORK, 0, SEL_OUT, b0 * n * cs,
                         "bluestein_columns_out");
         if (rc) return rc;
     }
@@ -573,66 +624,151 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
 
 // ---- N-D complex -----------------------------------------------------------
 
+// A strided axis whose single-upload kernel could hold only a few adjacent
+// columns per block (narrow HBM segments, one block per CU) is split into two
+// passes of length L1 x L2 = len over 32-column tiles: FFT over n1 with the
+// W_len^(n2*k1) twiddle, then FFT over n2 with a natural-order store.
+bool split_strided_axis(size_t len, int prec, size_t lds_budget, size_t* l1, size_t* l2) {
+    const size_t cs = csize(prec);
+    const size_t want_cols = prec ? 8 : 16;
+    if (len * want_cols * cs <= lds_budget) return false;
+    size_t best1 = 0, best2 = 0, bestmax = SIZE_MAX;
+    for (size_t a = 2; a * a <= len; ++a) {
+        if (len % a) continue;
+        const size_t b = len / a, hi = std::max(a, b), lo = std::min(a, b);
+        std::vector<int> rs;
+        if (!radix_schedule(hi, rs) || !radix_schedule(lo, rs)) continue;
+        if (hi < bestmax) {
+            bestmax = hi;
+            best1 = hi;
+            best2 = lo;
+        }
+    }
+    if (!best1 || best1 * want_cols * cs > lds_budget) return false;
+    *l1 = best1;
+    *l2 = best2;
+    return true;
+}
+
 int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
     const int prec = c.prec;
     const int dir = d.direction;
-    size_t total = d.batch;
-    for (uint32_t i = 0; i < d.rank; ++i) total *= d.dims[i];
-    bool first = true;
-    for (int ax = (int)d.rank - 1; ax >= 0; --ax) {
-        const size_t len = d.dims[ax];
-        if (len == 1) continue;
-        size_t inner = 1;
-        for (uint32_t j = ax + 1; j < d.rank; ++j) inner *= d.dims[j];
-        const size_t outer = total / (len * inner);
-        const double sc = (dir > 0 && d.normalize) ? 1.0 / (double)len : 1.0;
-        const bool contiguous = inner == 1;
-        const int alg = d.axis_algorithm[ax];
-        KArgs a = blank();
-        a.C = (long long)inner;
-        a.in_es = a.out_es = (long long)inner;
-        a.in_cs = a.out_cs = 1;
-        a.in_os = a.out_os = (long long)(len * inner);
-        a.flags = contiguous ? (KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR) : 0;
-        a.scale = sc;
-        const long long lines = (long long)(outer * inner);
-        const int in_sel = first ? SEL_IN : SEL_OUT;
-        int rc;
-        if (alg == VKFX_ALG_STOCKHAM) {
-            Geometry g0 = geometry(len, prec, 1, c.lds_max, c.lds_max);
-            if (!g0.ok)
-                return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
-                            "N-D axis length " + std::to_string(len) + " exceeds one upload");
-            const int want = contiguous ? std::max(1, 256 / g0.TT) : (prec ? 8 : 16);
-            Geometry g = geometry(len, prec, want, c.lds_max, c.lds_budget);
-            rc = add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, 0, SEL_OUT, 0,
-                            contiguous ? "stockham_rows" : "stockham_columns");
-        } else {
-            const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
-                                                   : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
-            Geometry g = geometry(M, prec, contiguous ? 1 : 4, c.lds_max, c.lds_max);
-            if (!g.ok)
-                return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
-                            "N-D Bluestein axis needs more than one upload (M=" + std::to_string(M) + ")");
-            BlueTables t;
-            rc = bluestein_tables(c.p, len, M, dir, prec, 0, 0, &t);
-            if (rc) return rc;
-            a.chirp = t.chirp, a.spec = t.spec;
-            a.nvalid = (long long)len, a.nout = (long long)len, a.M = (long long)M;
-            rc = add_launch(c, KK_BLUE_1, -1, g, a, lines, blocks_for(lines, g.G), in_sel, 0, SEL_OUT, 0,
-                            "bluestein_axis");
-        }
-        if (rc) return rc;
-        first = false;
+    const size_t cs = csize(prec);
+    size_t per_batch = 1;
+    for (uint32_t i = 0; i < d.rank; ++i) per_batch *= d.dims[i];
+    // Batch chunks small enough for the Infinity Cache to keep a chunk's
+    // intermediate between its axis passes.
+    size_t chunk = d.batch;
+    bool any_split = false;
+    for (uint32_t ax = 0; ax + 1 < d.rank; ++ax) {
+        size_t l1, l2;
+        if (d.axis_algorithm[ax] == VKFX_ALG_STOCKHAM && d.dims[ax] > 1 &&
+            split_strided_axis(d.dims[ax], prec, c.lds_budget, &l1, &l2))
+            any_split = true;
     }
-    if (first) {  // every axis has length 1: the transform is a copy (times scale 1)
-        Geometry g = geometry(1, prec, 64, c.lds_max, c.lds_budget);
-        KArgs a = blank();
-        a.in_es = a.out_es = 1;
-        a.in_os = a.out_os = 1;
-        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
-        return add_launch(c, KK_PLAIN, dir, g, a, (long long)total, blocks_for(total, g.G), SEL_IN, 0, SEL_OUT, 0,
-                          "copy");
+    size_t chunk_budget = 128ull << 20;
+    if (const char* e = getenv("VKFX_ND_CHUNK_MB")) chunk_budget = (size_t)atoll(e) << 20;
+    chunk = std::max<size_t>(1, std::min(d.batch, chunk_budget / std::max<size_t>(per_batch * cs, 1)));
+    if (any_split) c.p->work_bytes = std::max(c.p->work_bytes, chunk * per_batch * cs);
+    c.js << "\"nd\":{\"chunk\":" << chunk << "},";
+    for (size_t b0 = 0; b0 < d.batch; b0 += chunk) {
+        c.cur_chunk = (int)(b0 / chunk);
+        const size_t cb = std::min(chunk, d.batch - b0);
+        const size_t off = b0 * per_batch * cs;
+        const size_t total = cb * per_batch;
+        bool first = true;
+        for (int ax = (int)d.rank - 1; ax >= 0; --ax) {
+            const size_t len = d.dims[ax];
+            if (len == 1) continue;
+            size_t inner = 1;
+            for (uint32_t j = ax + 1; j < d.rank; ++j) inner *= d.dims[j];
+            const size_t outer = total / (len * inner);
+            const double sc = (dir > 0 && d.normalize) ? 1.0 / (double)len : 1.0;
+            const bool contiguous = inner == 1;
+            const int alg = d.axis_algorithm[ax];
+            const int in_sel = first ? SEL_IN : SEL_OUT;
+            int rc;
+            size_t l1 = 0, l2 = 0;
+            if (alg == VKFX_ALG_STOCKHAM && !contiguous && split_strided_axis(len, prec, c.lds_budget, &l1, &l2)) {
+                // pass A: lines (o, n2, c), FFT over n1 at stride L2*inner, twiddle, store in place pattern
+                Geometry ga = kernel_geometry(KK_FS_A, prec, dir, l1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+                Geometry gb = kernel_geometry(KK_PLAIN, prec, dir, l2, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+                if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "split axis geometry");
+                const void *tlo, *thi;
+                int tsh;
+                rc = two_level(c.p, len, prec, &tlo, &thi, &tsh);
+                if (rc) return rc;
+                KArgs a = blank();
+                a.C = (long long)(l2 * inner);
+                a.in_cs = a.out_cs = 1;
+                a.in_es = a.out_es = (long long)(l2 * inner);
+                a.in_os = a.out_os = (long long)(len * inner);
+                a.twdiv = (long long)inner;
+                a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+                long long lines = (long long)(outer * l2 * inner);
+                rc = add_launch(c, KK_FS_A, dir, ga, a, lines, blocks_for(lines, ga.G), in_sel, off, SEL_WORK, 0,
+                                "split_axis_pass1");
+                if (rc) return rc;
+                // pass B: lines (o, k1, c), FFT over n2 at stride inner, store k1 + L1*k2
+                KArgs b = blank();
+                b.C = (long long)inner;
+                b.C1 = (long long)l1;
+                b.in_cs = b.out_cs = 1;
+                b.in_es = (long long)inner, b.in_os1 = (long long)(l2 * inner), b.in_os = (long long)(len * inner);
+                b.out_es = (long long)(l1 * inner), b.out_os1 = (long long)inner, b.out_os = (long long)(len * inner);
+                b.scale = sc;
+                lines = (long long)(outer * l1 * inner);
+                rc = add_launch(c, KK_PLAIN, dir, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_OUT, off,
+                                "split_axis_pass2");
+                if (rc) return rc;
+                first = false;
+                continue;
+            }
+            KArgs a = blank();
+            a.C = (long long)inner;
+            a.in_es = a.out_es = (long long)inner;
+            a.in_cs = a.out_cs = 1;
+            a.in_os = a.out_os = (long long)(len * inner);
+            a.flags = contiguous ? (KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR) : 0;
+            a.scale = sc;
+            const long long lines = (long long)(outer * inner);
+            if (alg == VKFX_ALG_STOCKHAM) {
+                Geometry g0 = geometry(len, prec, 1, c.lds_max, c.lds_max);
+                if (!g0.ok)
+                    return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                                "N-D axis length " + std::to_string(len) + " exceeds one upload");
+                const int want = contiguous ? std::max(1, 256 / g0.TT) : (prec ? 8 : 16);
+                Geometry g = kernel_geometry(KK_PLAIN, prec, dir, len, !contiguous, want, c.lds_max, c.lds_budget);
+                rc = add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
+                                contiguous ? "stockham_rows" : "stockham_columns");
+            } else {
+                const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
+                                                       : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
+                Geometry g = geometry(M, prec, contiguous ? 1 : 4, c.lds_max, c.lds_max);
+                if (!g.ok)
+                    return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                                "N-D Bluestein axis needs more than one upload (M=" + std::to_string(M) + ")");
+                BlueTables t;
+                rc = bluestein_tables(c.p, len, M, dir, prec, 0, 0, &t);
+                if (rc) return rc;
+                a.chirp = t.chirp, a.spec = t.spec;
+                a.nvalid = (long long)len, a.nout = (long long)len, a.M = (long long)M;
+                rc = add_launch(c, KK_BLUE_1, -1, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
+                                "bluestein_axis");
+            }
+            if (rc) return rc;
+            first = false;
+        }
+        if (first) {  // every axis has length 1: the transform is a copy
+            Geometry g = geometry(1, prec, 64, c.lds_max, c.lds_budget);
+            KArgs a = blank();
+            a.in_es = a.out_es = 1;
+            a.in_os = a.out_os = 1;
+            a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+            int rc = add_launch(c, KK_PLAIN, dir, g, a, (long long)total, blocks_for(total, g.G), SEL_IN, off, SEL_OUT,
+                                off, "copy");
+            if (rc) return rc;
+        }
     }
     return VKFX_OK;
 }
@@ -663,7 +799,7 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     if (rc) return rc;
     Geometry g0 = geometry(M, prec, 1, c.lds_max, c.lds_max);
     if (g0.ok) {
-        Geometry g = geometry(M, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        Geometry g = kernel_geometry(KK_R2C_HALF, prec, -1, M, false, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
         KArgs a = blank();
         a.in_es = a.out_es = 1;
         a.in_os = (long long)M, a.out_os = (long long)h;
@@ -681,9 +817,10 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     int H = prec ? 4 : 8;
     while (H > 1 && (n1 % (2 * H) != 0)) H /= 2;
     if (n1 % (2 * H) != 0) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "R2C four-step rows must be even");
-    Geometry gb = geometry(n2, prec, 2 * H, c.lds_max, c.lds_max);
+    Geometry gb = kernel_geometry(KK_FS_B_R2C, prec, -1, n2, false, 2 * H, c.lds_max, c.lds_max);
+    if (gb.fixed && n1 % gb.G == 0) H = gb.G / 2;
     if (!gb1.ok || gb.G != 2 * H) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "R2C four-step row geometry");
-    Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry ga = kernel_geometry(KK_FS_A, prec, -1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
     const void *tlo, *thi;
     int tsh;
     rc = two_level(p, M, prec, &tlo, &thi, &tsh);
@@ -693,6 +830,7 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
          << ",\"chunk\":" << chunk << "},";
     for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+            c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, batch - b0);
         KArgs a = blank();
         a.C = (long long)n2;
@@ -744,7 +882,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     if (rc) return rc;
     Geometry g0 = geometry(M, prec, 1, c.lds_max, c.lds_max);
     if (g0.ok) {
-        Geometry g = geometry(M, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        Geometry g = kernel_geometry(KK_C2R_HALF, prec, 1, M, false, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
         KArgs a = blank();
         a.in_es = a.out_es = 1;
         a.in_os = (long long)h, a.out_os = (long long)M;
@@ -758,8 +896,9 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     size_t n1, n2;
     if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
         return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for C2R half length");
-    Geometry ga = geometry(n1, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
-    Geometry gb = geometry(n2, prec, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry ga = kernel_geometry(KK_FS_A_C2R, prec, 1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gb = kernel_geometry(KK_FS_B, prec, 1, n2, false, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "C2R four-step geometry");
     const void *tlo, *thi;
     int tsh;
     rc = two_level(p, M, prec, &tlo, &thi, &tsh);
@@ -769,6 +908,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
          << ",\"chunk\":" << chunk << "},";
     for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+            c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, batch - b0);
         KArgs a = blank();
         a.C = (long long)n2;
@@ -834,7 +974,9 @@ int vkfx_context_create(int device_index, vkfx_context** out) {
     auto* ctx = new vkfx_context();
     ctx->device = device_index;
     e = hipStreamCreate(&ctx->stream);
+    if (e == hipSuccess) e = hipStreamCreate(&ctx->aux);
     if (e != hipSuccess) {
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return hip_fail(e, "hipStreamCreate");
     }
@@ -851,6 +993,7 @@ int vkfx_context_create(int device_index, vkfx_context** out) {
     std::snprintf(pr.arch, sizeof(pr.arch), "%s", prop.gcnArchName);
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         (void)hipStreamDestroy(ctx->stream);
+        (void)hipStreamDestroy(ctx->aux);
         delete ctx;
         return fail(VKFX_ERR_NATIVE_UNAVAILABLE, std::string("library built for gfx950, device is ") + prop.gcnArchName);
     }
@@ -862,7 +1005,9 @@ int vkfx_context_destroy(vkfx_context* ctx) {
     if (!ctx) return VKFX_OK;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamSynchronize(ctx->aux);
     (void)hipStreamDestroy(ctx->stream);
+    (void)hipStreamDestroy(ctx->aux);
     delete ctx;
     return VKFX_OK;
 }
@@ -876,6 +1021,7 @@ int vkfx_context_profile(const vkfx_context* ctx, vkfx_device_profile* out) {
 int vkfx_context_synchronize(vkfx_context* ctx) {
     if (!ctx) return fail(VKFX_ERR_INVALID_ARGUMENT, "null context");
     hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->aux);
     return e == hipSuccess ? VKFX_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
@@ -973,7 +1119,23 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         delete p;
         return rc;
     }
-    c.js << "\"workspace_bytes\":" << p->work_bytes << ",\"passes\":[";
+    int nchunks = 1;
+    for (const Launch& L : p->launches) nchunks = std::max(nchunks, L.chunk + 1);
+    // two lanes pay a fork/join (two events, ~10 us) per execute, so only
+    // plans with several chunks use them
+    p->lanes = nchunks >= 4 ? 2 : 1;
+    if (const char* e = getenv("VKFX_LANES")) p->lanes = (atoi(e) == 1) ? 1 : p->lanes;
+    p->work_lane = p->work_bytes;
+    p->work_bytes = p->work_lane * p->lanes;
+    if (p->lanes == 2) {
+        hipError_t e = hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&p->ev_join, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            delete p;
+            return hip_fail(e, "hipEventCreate");
+        }
+    }
+    c.js << "\"lanes\":" << p->lanes << ",\"workspace_bytes\":" << p->work_bytes << ",\"passes\":[";
     for (const Launch& L : p->launches) note_pass(c, L);
     c.js << "]}";
     p->json = c.js.str();
@@ -993,6 +1155,9 @@ int vkfx_plan_destroy(vkfx_plan* plan) {
     if (!plan) return VKFX_OK;
     (void)hipSetDevice(plan->ctx->device);
     (void)hipStreamSynchronize(plan->ctx->stream);
+    (void)hipStreamSynchronize(plan->ctx->aux);
+    if (plan->ev_fork) (void)hipEventDestroy(plan->ev_fork);
+    if (plan->ev_join) (void)hipEventDestroy(plan->ev_join);
     delete plan;
     return VKFX_OK;
 }
@@ -1030,16 +1195,32 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
     hipStream_t s = stream ? (hipStream_t)stream : plan->ctx->stream;
     (void)hipSetDevice(plan->ctx->device);
     const int prec = plan->desc.precision == VKFX_F64 ? 1 : 0;
+    hipStream_t lane_stream[2] = {s, plan->ctx->aux};
+    if (plan->lanes == 2) {
+        // fork: the aux lane starts after everything already queued on s
+        hipError_t e = hipEventRecord(plan->ev_fork, s);
+        if (e == hipSuccess) e = hipStreamWaitEvent(plan->ctx->aux, plan->ev_fork, 0);
+        if (e != hipSuccess) return hip_fail(e, "stream fork");
+    }
     for (const Launch& L : plan->launches) {
+        const int lane = plan->lanes == 2 ? (L.chunk & 1) : 0;
         KArgs a = L.a;
         auto sel = [&](int which, size_t off) -> char* {
-            char* base = which == SEL_IN ? (char*)d_in : which == SEL_OUT ? (char*)d_out : (char*)work;
+            char* base = which == SEL_IN ? (char*)d_in
+                         : which == SEL_OUT ? (char*)d_out
+                                            : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };
         a.in = sel(L.in_sel, L.in_off);
         a.out = sel(L.out_sel, L.out_off);
-        int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, s);
+        int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, lane_stream[lane], L.fixed);
         if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
+    }
+    if (plan->lanes == 2) {
+        // join: s continues only after the aux lane's work
+        hipError_t e = hipEventRecord(plan->ev_join, plan->ctx->aux);
+        if (e == hipSuccess) e = hipStreamWaitEvent(s, plan->ev_join, 0);
+        if (e != hipSuccess) return hip_fail(e, "stream join");
     }
     return VKFX_OK;
 }
