@@ -179,6 +179,68 @@ def cpu_baseline(cfg, budget_s=15.0):
                       f"~{per * done:.1f} s CPU work"}
 
 
+COPY_BYTES = 1 << 30  # copy_bandwidth(): 1 GiB read + 1 GiB written per launch
+
+
+def rocprof_summary(dirs, workload_kernel="vkfx"):
+    """Markdown summary of rocprofv3 CSV output directories: kernel stats
+    (--kernel-trace --stats) and FETCH_SIZE / WRITE_SIZE (--pmc), the latter
+    per launch and scaled by what the same counter reads for the 1 GiB
+    device copy that copy_bandwidth() runs in the same process."""
+    import csv
+    import glob
+    lines = []
+    traffic = {}
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
+            lines.append(f"### kernel stats ({os.path.basename(f)})\n")
+            lines.append("| kernel | calls | avg us | min us | max us | % |")
+            lines.append("|---|---|---|---|---|---|")
+            for r in list(csv.DictReader(open(f)))[:8]:
+                lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                             f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {r['Percentage']} |")
+            lines.append("")
+        for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+            per = {}
+            for r in csv.DictReader(open(f)):
+                key = (r["Kernel_Name"], r["Counter_Name"])
+                per.setdefault(key, []).append(float(r["Counter_Value"]))
+            for (k, c), v in per.items():
+                tag = "fft" if workload_kernel in k else ("copy" if "copyBuffer" in k else None)
+                if tag:
+                    traffic.setdefault(c, {}).setdefault(tag, []).append((k, sum(v) / len(v)))
+    if traffic:
+        lines.append("### HBM traffic per launch (rocprofv3 --pmc, KiB per dispatch)\n")
+        lines.append("| counter | kernel | raw KiB/launch | copy-kernel raw KiB (1 GiB moved) | scaled bytes/launch |")
+        lines.append("|---|---|---|---|---|")
+        result = {}
+        for c, tags in sorted(traffic.items()):
+            copy = [v for _, v in tags.get("copy", [])]
+            ref = max(copy) if copy else None
+            for k, v in tags.get("fft", []):
+                scaled = v / ref * COPY_BYTES if ref else None
+                lines.append(f"| {c} | `{k[:90]}` | {v:.1f} | {ref if ref else 'n/a'} | "
+                             f"{'%.4g' % scaled if scaled else 'n/a'} |")
+                result.setdefault(k, {})[c] = scaled
+        lines.append("")
+        for k, cs in result.items():
+            if "FETCH_SIZE" in cs and "WRITE_SIZE" in cs and cs["FETCH_SIZE"] and cs["WRITE_SIZE"]:
+                lines.append(f"traffic_bytes_per_launch `{k[:90]}`: {cs['FETCH_SIZE'] + cs['WRITE_SIZE']:.6g}")
+    return "\n".join(lines)
+
+
+def profiled_traffic(workload):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprof
+    summary profiles/<workload>.md (None when absent)."""
+    path = os.path.join(ROOT, "profiles", f"{workload}.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.rsplit(":", 1)[1])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,7 +251,12 @@ def main():
     ap.add_argument("--rotate", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch (tuning runs)")
+    ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
+                    help="print a markdown summary of rocprofv3 CSV output directories and exit")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md).",
               file=sys.stderr)
@@ -213,7 +280,7 @@ def main():
         if dom_bytes:
             ach = dom_bytes / (launch_ms * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                    "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(cfg["workload"]),
                     "kernel": first[0]["kernel"], "launch_ms": round(launch_ms, 5)}
         out = {
             "metric": "batched f32 C2C effective HBM GB/s (2*N*batch*bytes/time)",
