@@ -50,13 +50,15 @@ enum Layout : int { LAY_ANY = 0, LAY_ROW = 1, LAY_COL = 2, LAY_STAGED = 3 };
 // Runtime dimensions (k_dyn) and compile-time dimensions (k_fix) seen by the
 // IO policies through the same interface.
 struct DynDims {
+    static constexpr bool NTI = false, NTO = false;
     static __device__ __forceinline__ int N(const KArgs& a) { return a.N; }
     static __device__ __forceinline__ int G(const KArgs& a) { return a.G; }
     static __device__ __forceinline__ int LS(const KArgs& a) { return a.LS; }
     static __device__ __forceinline__ int PS(const KArgs& a) { return a.PS; }
 };
-template <int N_, int G_, int LS_, int PS_>
+template <int N_, int G_, int LS_, int PS_, bool NTI_ = false, bool NTO_ = false>
 struct FixDims {
+    static constexpr bool NTI = NTI_, NTO = NTO_;
     static __device__ __forceinline__ constexpr int N(const KArgs&) { return N_; }
     static __device__ __forceinline__ constexpr int G(const KArgs&) { return G_; }
     static __device__ __forceinline__ constexpr int LS(const KArgs&) { return LS_; }
@@ -112,17 +114,65 @@ __device__ __forceinline__ cpx<T> zero() {
     return mk((T)0, (T)0);
 }
 
+// HBM element access; NT = nontemporal (streamed data that is not re-read
+// by this kernel, so it should not displace cached tables).
+template <bool NT, typename T>
+__device__ __forceinline__ cpx<T> ldg(const cpx<T>* p) {
+    if constexpr (NT) {
+        return mk(__builtin_nontemporal_load(&p->re), __builtin_nontemporal_load(&p->im));
+    } else {
+        return *p;
+    }
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void stg(cpx<T>* p, cpx<T> v) {
+    if constexpr (NT) {
+        __builtin_nontemporal_store(v.re, &p->re);
+        __builtin_nontemporal_store(v.im, &p->im);
+    } else {
+        *p = v;
+    }
+}
+// Input/output accessors honouring the per-launch streaming flags.
+// (The hint must be a compile-time choice: a runtime branch between the two
+// forms is merged into one plain access by the compiler.)
+template <bool NT, typename T>
+__device__ __forceinline__ cpx<T> ldg_in(const KArgs&, const cpx<T>* p) {
+    return ldg<NT>(p);
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void stg_out(const KArgs&, cpx<T>* p, cpx<T> v) {
+    stg<NT>(p, v);
+}
+template <bool NT, typename T>
+__device__ __forceinline__ T ldg_s(const T* p) {
+    if constexpr (NT) {
+        return __builtin_nontemporal_load(p);
+    } else {
+        return *p;
+    }
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void stg_s(T* p, T v) {
+    if constexpr (NT) {
+        __builtin_nontemporal_store(v, p);
+    } else {
+        *p = v;
+    }
+}
+
 // Generic staged prologue/epilogue built from the element functions.
 template <class IO, class D, typename T>
 __device__ __forceinline__ void staged_load(const KArgs& a, cpx<T>* lds, const LineInfo* li, bool rowmajor) {
     coop_for(D::G(a), D::N(a), rowmajor, [&](int g, int e) {
-        lds[g * D::LS(a) + lpad(e, D::PS(a))] = li[g].valid ? IO::template load_elem<T>(a, li[g], e) : zero<T>();
+        lds[g * D::LS(a) + lpad(e, D::PS(a))] =
+            li[g].valid ? IO::template load_elem<T, D::NTI>(a, li[g], e) : zero<T>();
     });
 }
 template <class IO, class D, typename T, int S>
 __device__ __forceinline__ void staged_store(const KArgs& a, const cpx<T>* lds, const LineInfo* li, bool rowmajor) {
     coop_for(D::G(a), IO::template out_count<D>(a), rowmajor, [&](int g, int e) {
-        if (li[g].valid) IO::template store_elem<T, S>(a, li[g], e, lds[g * D::LS(a) + lpad(e, D::PS(a))]);
+        if (li[g].valid) IO::template store_elem<T, S, D::NTO>(a, li[g], e, lds[g * D::LS(a) + lpad(e, D::PS(a))]);
     });
 }
 
@@ -136,13 +186,13 @@ struct IoPlain {
     static __device__ LineInfo line(const KArgs& a, long long blk, int g) { return line_default(a, blk, g); }
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return D::N(a); }
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
-        return ((const cpx<T>*)a.in)[L.ib + e * a.in_es];
+        return ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es);
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
-        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(v, (T)a.scale);
+        stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, scale(v, (T)a.scale));
     }
     // staged variants used when an end cannot be direct
     template <typename T, class D>
@@ -158,13 +208,13 @@ struct IoPlain {
 struct IoR2CFull : IoPlain {
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
-        return mk(((const T*)a.in)[L.ib + e * a.in_es], (T)0);
+        return mk(ldg_s<NTIO>((const T*)a.in + L.ib + e * a.in_es), (T)0);
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
-        if (e < a.nout) ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(v, (T)a.scale);
+        if (e < a.nout) stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, scale(v, (T)a.scale));
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -177,15 +227,15 @@ struct IoR2CFull : IoPlain {
 };
 
 struct IoC2RFull : IoPlain {
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
         const int n = a.N, h = n / 2 + 1;
-        return e < h ? in[L.ib + e * a.in_es] : conj(in[L.ib + (n - e) * a.in_es]);
+        return e < h ? ldg_in<NTIO>(a, in + L.ib + e * a.in_es) : conj(ldg_in<NTIO>(a, in + L.ib + (n - e) * a.in_es));
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
-        ((T*)a.out)[L.ob + e * a.out_es] = v.re * (T)a.scale;
+        stg_s<NTIO>((T*)a.out + L.ob + e * a.out_es, v.re * (T)a.scale);
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -220,7 +270,7 @@ struct IoR2CHalf : IoPlain {
             cpx<T> B = conj(Z[lpad(km, D::PS(a))]);
             cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
             cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
-            out[li[g].ob + k * a.out_es] = scale(X, (T)0.5);
+            stg_out<D::NTO>(a, out + li[g].ob + k * a.out_es, scale(X, (T)0.5));
         });
     }
 };
@@ -230,11 +280,11 @@ struct IoR2CHalf : IoPlain {
 struct IoC2RHalf : IoPlain {
     static constexpr int kLoad = LAY_ROW;
     static constexpr int kStore = LAY_ROW;
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int k) {
         const cpx<T>* in = (const cpx<T>*)a.in;
-        cpx<T> X = in[L.ib + k * a.in_es];
-        cpx<T> Xm = conj(in[L.ib + (a.N - k) * a.in_es]);
+        cpx<T> X = ldg_in<NTIO>(a, in + L.ib + k * a.in_es);
+        cpx<T> Xm = conj(ldg_in<NTIO>(a, in + L.ib + (a.N - k) * a.in_es));
         cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
         return (X + Xm) + muli<1>(cmulc(X - Xm, w));
     }
@@ -258,14 +308,14 @@ struct IoFsA : IoPlain {
     static __device__ __forceinline__ cpx<T> tw_root(const KArgs& a, long long m) {
         return tw2<T>(a.tlo, a.thi, a.tshift, m);
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_twiddled(const KArgs& a, const LineInfo& L, int e, cpx<T> v,
                                                           cpx<T> w) {
-        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = twmul<S>(v, w);
+        stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, twmul<S>(v, w));
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
-        store_twiddled<T, S>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.tr * e));
+        store_twiddled<T, S, NTIO>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.tr * e));
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -278,11 +328,11 @@ struct IoFsA : IoPlain {
 };
 
 struct IoFsABlue : IoFsA {
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const long long n = L.c + (long long)e * a.N2;
         if (n >= a.nvalid) return zero<T>();
-        return cmul(((const cpx<T>*)a.in)[L.ib + e * a.in_es], ((const cpx<T>*)a.chirp)[n]);
+        return cmul(ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es), ((const cpx<T>*)a.chirp)[n]);
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -291,11 +341,11 @@ struct IoFsABlue : IoFsA {
 };
 
 struct IoFsAC2R : IoFsA {
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
         const long long k = L.c + (long long)e * a.N2;
-        cpx<T> X = in[L.ib + e * a.in_es];
+        cpx<T> X = ldg_in<NTIO>(a, in + L.ib + e * a.in_es);
         cpx<T> Xm = conj(in[L.o * a.in_os + (a.M - k)]);
         cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
         return (X + Xm) + muli<1>(cmulc(X - Xm, w));
@@ -377,7 +427,7 @@ struct IoFsBR2C : IoPlain {
             cpx<T> B = conj(lds[gp * D::LS(a) + lpad(k2m, D::PS(a))]);
             cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
             cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
-            out[li[g].ob + k] = scale(X, (T)0.5);
+            stg_out<D::NTO>(a, out + li[g].ob + k, scale(X, (T)0.5));
             if (k == 0) out[li[g].ob + a.M] = mk(A.re - A.im, (T)0);
         });
     }
@@ -404,14 +454,14 @@ struct IoBlueB : IoPlain {
         return tw2<T>(a.tlo, a.thi, a.tshift, m);
     }
     // the inverse pass twiddle root(-k1*m2) regardless of the kernel direction
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_twiddled(const KArgs& a, const LineInfo& L, int e, cpx<T> v,
                                                           cpx<T> w) {
-        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = cmulc(v, w);
+        stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, cmulc(v, w));
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
-        store_twiddled<T, S>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.c * e));
+        store_twiddled<T, S, NTIO>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.c * e));
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -428,11 +478,11 @@ struct IoBlueB : IoPlain {
 struct IoFsCBlue : IoPlain {
     static constexpr int kLoad = LAY_COL;
     static constexpr int kStore = LAY_COL;
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
         const long long m = L.c + (long long)e * a.N2;
         if (m >= a.nout) return;
-        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(cmul(v, ((const cpx<T>*)a.chirp)[m]), (T)a.scale);
+        stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, scale(cmul(v, ((const cpx<T>*)a.chirp)[m]), (T)a.scale));
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -450,15 +500,15 @@ struct IoBlue1 : IoPlain {
     static constexpr bool kTwoPass = true;
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
-    template <typename T>
+    template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         if (e >= a.nvalid) return zero<T>();
-        return cmul(((const cpx<T>*)a.in)[L.ib + e * a.in_es], ((const cpx<T>*)a.chirp)[e]);
+        return cmul(ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es), ((const cpx<T>*)a.chirp)[e]);
     }
-    template <typename T, int S>
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
         if (e >= a.nout) return;
-        ((cpx<T>*)a.out)[L.ob + e * a.out_es] = scale(cmul(v, ((const cpx<T>*)a.chirp)[e]), (T)a.scale);
+        stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, scale(cmul(v, ((const cpx<T>*)a.chirp)[e]), (T)a.scale));
     }
     template <typename T, class D>
     static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -514,6 +564,8 @@ struct RList {};
 // stage reads and writes free of bank conflicts).
 template <int N_, int TT_, int G_, int PS_, int LS_, bool COL_, int... R>
 struct Shape {
+    static constexpr int WPE = 0;  // waves-per-EU hint (0 = compiler default)
+    static constexpr bool NTI = false, NTO = false;  // nontemporal HBM loads / stores
     static constexpr int N = N_, TT = TT_, G = G_, PS = PS_, LS = LS_;
     static constexpr bool COL = COL_;
     static_assert(LS_ >= N_ + ((N_ - 1) >> PS_), "LDS line stride too small");
@@ -523,7 +575,7 @@ struct Shape {
 
 // One stage with compile-time geometry. SRC/DST: 0 = the line in LDS,
 // 1 = HBM through the IO policy's element functions.
-template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST>
+template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST, bool NTI, bool NTO>
 __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line, const LineInfo& L, int t,
                                        const StageTw& tw) {
     constexpr int NB = N / R;
@@ -538,7 +590,7 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
             for (int i = 0; i < R; ++i) {
                 const int e = b + i * NB;
                 if constexpr (SRC) {
-                    v[j][i] = L.valid ? IO::template load_elem<T>(a, L, e) : zero<T>();
+                    v[j][i] = L.valid ? IO::template load_elem<T, NTI>(a, L, e) : zero<T>();
                 } else {
                     v[j][i] = line[lpad(e, PS)];
                 }
@@ -569,14 +621,14 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                     root_powers<R>(IO::template tw_root<T>(a, L.tr * NB), sp);
 #pragma unroll
                     for (int q = 0; q < R; ++q)
-                        IO::template store_twiddled<T, S>(a, L, base + q * P, v[j][q], cmul(wb, sp[q]));
+                        IO::template store_twiddled<T, S, NTO>(a, L, base + q * P, v[j][q], cmul(wb, sp[q]));
                 }
             } else {
 #pragma unroll
                 for (int q = 0; q < R; ++q) {
                     const int o = base + q * P;
                     if constexpr (DST) {
-                        if (L.valid) IO::template store_elem<T, S>(a, L, o, v[j][q]);
+                        if (L.valid) IO::template store_elem<T, S, NTO>(a, L, o, v[j][q]);
                     } else {
                         line[lpad(o, PS)] = v[j][q];
                     }
@@ -591,7 +643,8 @@ template <typename T, int S, class IO, class Sh, int SRC0, int DSTL, int P, int 
 __device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, const LineInfo& L, int t,
                                         const StageTw& tw, RList<R, Rest...>) {
     constexpr bool last = sizeof...(Rest) == 0;
-    fstage<T, S, IO, Sh::N, P, R, Sh::TT, Sh::PS, (P == 1 ? SRC0 : 0), (last ? DSTL : 0)>(a, line, L, t, tw);
+    fstage<T, S, IO, Sh::N, P, R, Sh::TT, Sh::PS, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO>(
+        a, line, L, t, tw);
     if constexpr (!last) fstages<T, S, IO, Sh, SRC0, DSTL, P * R>(a, line, L, t, tw, RList<Rest...>{});
 }
 
@@ -638,6 +691,21 @@ __global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix(const KArgs a) {
     fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blockIdx.x);
 }
 
+// Variant shapes for tuning: a waves-per-EU occupancy hint and nontemporal IO.
+template <class Base, int W, bool NTIN, bool NTOUT>
+struct Tuned : Base {
+    static constexpr int WPE = W;
+    static constexpr bool NTI = NTIN, NTO = NTOUT;
+    using Dims = FixDims<Base::N, Base::G, Base::LS, Base::PS, NTIN, NTOUT>;
+};
+template <typename T, int S, class IO, class Sh>
+__global__ __launch_bounds__(Sh::G* Sh::TT) __attribute__((amdgpu_waves_per_eu(Sh::WPE > 0 ? Sh::WPE : 1, 8))) void k_fix_occ(
+    const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ LineInfo li[Sh::G];
+    fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blockIdx.x);
+}
+
 // Persistent variant: a grid sized to the resident capacity walks the groups
 // with a grid stride, so the groups in flight stay within a compact window of
 // HBM and no workgroup is dispatched per group.
@@ -677,6 +745,17 @@ KernelFn pick(KernelKind kind) {
 
 // Registry entry of one fixed-shape instantiation. Radix lists are
 // zero-terminated; nst is filled in by the registry lookup.
+#define VKFX_FIXED_OCC(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, W, NTI, NTO, ...)                  \
+    FixedKernel {                                                                                      \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, 0, {__VA_ARGS__},                                         \
+            (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>), \
+            (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)              \
+    }
+// The same shape with nontemporal HBM streaming (inputs read once, outputs
+// written once).
+// NTI / NTO: nontemporal loads of the pass input / stores of its output.
+#define VKFX_FIXED_NT(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...) \
+    VKFX_FIXED_OCC(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, 0, NTI, NTO, __VA_ARGS__)
 #define VKFX_FIXED(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, ...)                                   \
     FixedKernel {                                                                                     \
         KIND, PREC, S, N, TT, G, PS, LS, COL, 0, {__VA_ARGS__},                                        \

@@ -5,10 +5,10 @@
 namespace vkfx {
 
 static const FixedKernel kTable[] = {
-    VKFX_FIXED(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 448, 1, 5, 8489, false, 8, 3, 7, 7, 7),
-    VKFX_FIXED(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 406, true, 3, 3, 3, 3, 5),
-    VKFX_FIXED(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, 4, 3, 3, 3, 3),
-    VKFX_FIXED(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 406, true, 3, 3, 3, 3, 5),
+    VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 448, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
+    VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 406, true, true, false, 3, 3, 3, 3, 5),
+    VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, false, false, 4, 3, 3, 3, 3),
+    VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 406, true, false, true, 3, 3, 3, 3, 5),
 };
 
 const FixedKernel* fixed_table_blue(int* count) {

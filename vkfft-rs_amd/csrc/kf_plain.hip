@@ -6,30 +6,25 @@ namespace vkfx {
 
 static const FixedKernel kTable[] = {
     // 1-D rows of 1024 (C1): one wave per line, 16 elements per thread
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 2, 5, 1056, false, 16, 16, 4),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, 1, 1024, 64, 2, 5, 1056, false, 16, 16, 4),
-    // tuning variants of the forward 1024 row kernel (VKFX_FIXED_PICK=1..4; 4 = previous padding)
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 1, 5, 1056, false, 16, 16, 4),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 4, 5, 1056, false, 16, 16, 4),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 5, 1056, false, 8, 8, 4, 4),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 2, 4, 1089, false, 16, 16, 4),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
     // rows of 4096 (C3 axis 1)
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 5, 4224, false, 16, 16, 16),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 5, 4224, false, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 5, 4224, false, true, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 5, 4224, false, true, true, 16, 16, 16),
     // columns of 4096 (C3 axis 0): 4 adjacent columns per block
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 4096, 128, 4, 4, 4360, true, 16, 16, 16),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, 1, 4096, 128, 4, 4, 4360, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 128, 4, 4, 4360, true, true, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 128, 4, 4, 4360, true, true, true, 16, 16, 16),
     // f64 512 rows and columns (C4)
-    VKFX_FIXED(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 4, 544, false, 8, 8, 8),
-    VKFX_FIXED(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 4, 544, false, 8, 8, 8),
-    VKFX_FIXED(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 3, 578, true, 8, 8, 8),
-    VKFX_FIXED(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 3, 578, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 4, 544, false, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 4, 544, false, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 3, 578, true, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 3, 578, true, true, true, 8, 8, 8),
     // 64-point column passes of a split strided axis (4096 = 64 x 64): 32
     // adjacent columns per block, 256-byte row segments
-    VKFX_FIXED(KK_FS_A, IoFsA, float, 0, -1, 64, 8, 32, 30, 65, true, 8, 8),
-    VKFX_FIXED(KK_FS_A, IoFsA, float, 0, 1, 64, 8, 32, 30, 65, true, 8, 8),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, -1, 64, 8, 32, 30, 65, true, 8, 8),
-    VKFX_FIXED(KK_PLAIN, IoPlain, float, 0, 1, 64, 8, 32, 30, 65, true, 8, 8),
+    VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 64, 8, 32, 30, 65, true, true, true, 8, 8),
+    VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, 1, 64, 8, 32, 30, 65, true, true, true, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 64, 8, 32, 30, 65, true, true, true, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 64, 8, 32, 30, 65, true, true, true, 8, 8),
 };
 
 const FixedKernel* fixed_table_plain(int* count) {

@@ -1074,6 +1074,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     p->desc = d;
     Ctx c{p, f64 ? 1 : 0, lds_max_for(ctx)};
     if (const char* e = getenv("VKFX_LDS_BUDGET_KB")) c.lds_budget = (size_t)atoll(e) << 10;
+
     const size_t cs = csize(c.prec), rs = rsize(c.prec);
     c.js << "{\"rank\":" << d.rank << ",\"dims\":[";
     for (uint32_t i = 0; i < d.rank; ++i) c.js << (i ? "," : "") << d.dims[i];
