@@ -127,6 +127,38 @@ def test_bluestein_and_rader_classified_f32(hip_ctx, n, batch):
     assert o.rel_l2(z, oracle_c2c(x, n, INV, True)) <= TOL[F32]
 
 
+@pytest.mark.parametrize("n,mode", [(17, "fft"), (97, "fft"), (257, "fft"), (89, "fft"), (12289, "fft"),
+                                    (47, "direct"), (59, "direct"), (83, "direct")])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_rader(hip_ctx, n, mode, prec):
+    """Rader-classified primes execute as Rader (FFT convolution when p-1 is
+    Stockham-smooth, direct multiplication below 89), rader_ir.rs:1957-2101."""
+    if prec == F64 and n == 12289:
+        pytest.skip("F64 LDS capacity (10240 elements) makes the planner pick Bluestein for 12289")
+    batch = 3
+    x = rand(n * batch, n + 7, prec)
+    ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec), FWD)
+    assert ir.axis_algorithms == [vk.AlgorithmKind.Rader]
+    desc = hip_ctx.plan(ir).describe()
+    assert desc["rader"]["mode"] == mode and desc["rader"]["prime"] == n
+    y = hip_ctx.execute_transform(ir, x)
+    ref = oracle_c2c(x, n)
+    tol = TOL[prec] if prec == F32 else max(TOL[F64], 2 * o.rel_l2(ref, np.fft.fft(x.reshape(batch, n), axis=1).reshape(-1)))
+    assert o.rel_l2(y, ref) <= tol
+    z, _ = c2c(hip_ctx, [n], batch, x, prec, INV, normalize=True)
+    assert o.rel_l2(z, oracle_c2c(x, n, INV, True)) <= tol
+
+
+def test_rader_recursive_opt_in_falls_back_to_bluestein(hip_ctx):
+    cfg = vk.FftConfig.new([4099]).with_batch_count(2)
+    cfg.allow_recursive_fft_rader = True
+    ir = vk.TransformIr.build(cfg, FWD)
+    assert ir.axis_algorithms == [vk.AlgorithmKind.Rader]
+    assert hip_ctx.plan(ir).describe().get("rader_fallback") == "bluestein"
+    x = rand(4099 * 2, 3)
+    assert o.rel_l2(hip_ctx.execute_transform(ir, x), oracle_c2c(x, 4099)) <= TOL[F32]
+
+
 def test_bluestein_plan_uses_planner_length(hip_ctx):
     for n, m in [(4099, 8232), (65537, 131220)]:
         ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(4096), FWD)
@@ -202,7 +234,9 @@ def test_c2_shape_round_trip_full_size(hip_ctx):
                                              ([8, 6, 5, 4], 1, F32), ([4099, 4], 1, F32),
                                              # strided axes long enough to run as two split passes
                                              ([1024, 8], 2, F32), ([2048, 3], 1, F32), ([1000, 6], 1, F64),
-                                             ([3, 768, 5], 2, F32)])
+                                             ([3, 768, 5], 2, F32),
+                                             # Rader axes inside N-D transforms (contiguous and strided)
+                                             ([8, 17], 2, F32), ([47, 8], 1, F32), ([97, 6], 1, F64)])
 def test_nd_c2c(hip_ctx, dims, batch, prec):
     count = int(np.prod(dims)) * batch
     x = rand(count, count % 1000, prec)

@@ -64,6 +64,13 @@ def test_small_axis_classes(n, alg):
         assert got == alg
 
 
+def test_f64_rader_limit_follows_lds_capacity():
+    # planner.rs:442-463: the FFT-Rader scan stops at LDS/complex_bytes; 160 KiB
+    # holds 10240 f64 complex values, so 12289 is Rader in F32, Bluestein in F64
+    assert vk.planner_axis(12289, 1, vk.Precision.F32)[0] == A.Rader
+    assert vk.planner_axis(12289, 1, vk.Precision.F64)[0] == A.Bluestein
+
+
 def test_next_smooth_matches_oracle():
     for t in [1, 2, 7, 11, 2061, 8197, 131073, 99991]:
         assert vk.next_smooth_at_least(t) == o.next_smooth_at_least(t)

@@ -528,6 +528,85 @@ struct IoBlue1 : IoPlain {
     }
 };
 
+// Rader, FFT convolution (rader_ir.rs:1957-2101): a[s] = x[g^-s] gathered
+// into LDS, FFT of length p-1 (= N here), multiply by FFT(b)/(p-1) with
+// b[n] = exp(dir 2 pi i g^n / p), inverse FFT, X[g^m] = x0 + conv[m] and
+// X[0] = x0 + A[0] (the DC of the gathered sequence is sum x - x0). x0 sits
+// in the last LDS slot of the line so in-place execution is safe.
+struct IoRader : IoPlain {
+    static constexpr bool kTwoPass = true;
+    static constexpr int kLoad = LAY_STAGED;
+    static constexpr int kStore = LAY_STAGED;
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        const cpx<T>* in = (const cpx<T>*)a.in;
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            cpx<T>* line = lds + g * D::LS(a);
+            line[lpad(e, D::PS(a))] = li[g].valid ? in[li[g].ib + (long long)a.pin[e] * a.in_es] : zero<T>();
+            if (e == 0) line[D::LS(a) - 1] = li[g].valid ? in[li[g].ib] : zero<T>();
+        });
+    }
+    template <typename T, class D>
+    static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        const cpx<T>* spec = (const cpx<T>*)a.spec;
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            cpx<T>* line = lds + g * D::LS(a);
+            cpx<T>& v = line[lpad(e, D::PS(a))];
+            if (e == 0 && li[g].valid)
+                ((cpx<T>*)a.out)[li[g].ob] = scale(line[D::LS(a) - 1] + v, (T)a.scale);
+            v = cmul(v, spec[e]);
+        });
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        cpx<T>* out = (cpx<T>*)a.out;
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            if (!li[g].valid) return;
+            const cpx<T>* line = lds + g * D::LS(a);
+            out[li[g].ob + (long long)a.pout[e] * a.out_es] =
+                scale(line[D::LS(a) - 1] + line[lpad(e, D::PS(a))], (T)a.scale);
+        });
+    }
+};
+
+// Rader by direct multiplication for small primes whose p-1 is not
+// Stockham-smooth (rader_ir.rs:381): one thread per convolution output m,
+// conv[m] = sum_s a[s] b[(m - s) mod (p-1)], b[n] = exp(dir 2 pi i g^n / p).
+// N = p-1 <= 87, G lines per block, block = G * N threads.
+template <typename T>
+__global__ __launch_bounds__(512) void k_rader_direct(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
+    __shared__ LineInfo li[kMaxLinesPerBlock];
+    const int tid = threadIdx.x, N = a.N;
+    if (tid < a.G) li[tid] = line_default(a, blockIdx.x, tid);
+    __syncthreads();
+    const cpx<T>* in = (const cpx<T>*)a.in;
+    for (int idx = tid; idx < a.G * (N + 1); idx += blockDim.x) {
+        const int g = idx / (N + 1), s = idx - g * (N + 1);
+        cpx<T> v = zero<T>();
+        if (li[g].valid) v = s < N ? in[li[g].ib + (long long)a.pin[s] * a.in_es] : in[li[g].ib];
+        lds[g * (N + 1) + s] = v;
+    }
+    __syncthreads();
+    const int g = tid / N, m = tid - g * N;
+    if (g >= a.G || !li[g].valid) return;
+    const cpx<T>* av = lds + g * (N + 1);
+    const cpx<T>* b = (const cpx<T>*)a.spec;
+    const cpx<T> x0 = av[N];
+    cpx<T> acc = zero<T>(), dc = zero<T>();
+    int bi = m;
+    for (int s = 0; s < N; ++s) {
+        acc = acc + cmul(av[s], b[bi]);
+        dc = dc + av[s];
+        bi = bi == 0 ? N - 1 : bi - 1;
+    }
+    cpx<T>* out = (cpx<T>*)a.out;
+    const T sc = (T)a.scale;
+    out[li[g].ob + (long long)a.pout[m] * a.out_es] = scale(x0 + acc, sc);
+    if (m == 0) out[li[g].ob] = scale(x0 + dc, sc);
+}
+
 // ------------------------------------------------------- dynamic kernel
 
 template <typename T, int S, class IO>
@@ -737,6 +816,8 @@ KernelFn pick(KernelKind kind) {
         case KK_BLUE_B: return k_dyn<T, S, IoBlueB>;
         case KK_FS_C_BLUE: return k_dyn<T, S, IoFsCBlue>;
         case KK_BLUE_1: return k_dyn<T, S, IoBlue1>;
+        case KK_RADER_FFT: return k_dyn<T, S, IoRader>;
+        case KK_RADER_DIRECT: return k_rader_direct<T>;
         default: return nullptr;
     }
 }

@@ -26,6 +26,8 @@ enum KernelKind : int {
     KK_BLUE_B,         // Bluestein row pass: FFT, spectrum multiply, IFFT, W_M^-1
     KK_FS_C_BLUE,      // Bluestein column pass: IFFT, chirp, truncate
     KK_BLUE_1,         // Bluestein in one kernel (convolution fits LDS)
+    KK_RADER_FFT,      // prime length p: gather, FFT(p-1), kernel multiply, IFFT, scatter
+    KK_RADER_DIRECT,   // prime length p: gather, O(p^2) cyclic convolution, scatter
     KK_COUNT
 };
 
@@ -70,6 +72,8 @@ struct KArgs {
     long long nout;                    // logical output length per line (truncate)
     long long N1, N2;                  // four-step factors (M = N1*N2)
     long long nblk;                    // line groups (persistent kernels walk them)
+    const int* pin;                    // Rader gather: a[s] = x[pin[s]]
+    const int* pout;                   // Rader scatter: X[pout[m]] = x0 + conv[m]
 };
 
 using KernelFn = void (*)(const KArgs);

@@ -472,6 +472,108 @@ size_t chunk_for(size_t batch, size_t per_batch_bytes) {
     return std::min(c, batch);
 }
 
+// ---- Rader ---------------------------------------------------------------
+
+struct RaderTables {
+    const void* pin = nullptr;
+    const void* pout = nullptr;
+    const void* spec = nullptr;
+    bool fft = false;
+};
+
+// Rader tables for a prime p with generator g (lut.rs:374-435): pin[s] =
+// g^(-s) mod p (gather), pout[m] = g^m mod p (scatter) and the kernel
+// b[n] = exp(dir 2 pi i g^n / p); in FFT mode the kernel is stored as
+// FFT_{p-1}(b) / (p-1).
+int rader_tables(vkfx_plan* p, size_t prime, int dir, int prec, bool fft, RaderTables* t) {
+    const size_t L = prime - 1, g = primitive_root(prime);
+    if (!g) return fail(VKFX_ERR_INVALID_ARGUMENT, "Rader length is not prime");
+    std::vector<int> pw(L), pin(L), pout(L);
+    size_t r = 1;
+    for (size_t e = 0; e < L; ++e) {
+        pw[e] = (int)r;
+        r = (r * g) % prime;
+    }
+    for (size_t s = 0; s < L; ++s) {
+        pin[s] = pw[(L - s) % L];
+        pout[s] = pw[s];
+    }
+    std::string key = "rader:" + std::to_string(prime);
+    int rc = upload(p, key + ":pin", pin.data(), L * sizeof(int), &t->pin);
+    if (rc) return rc;
+    rc = upload(p, key + ":pout", pout.data(), L * sizeof(int), &t->pout);
+    if (rc) return rc;
+    std::vector<ld> br(L), bi(L);
+    for (size_t e = 0; e < L; ++e) {
+        ld c, s;
+        root((ld)pw[e], (ld)prime, c, s);  // exp(-2 pi i g^e / p)
+        br[e] = c;
+        bi[e] = dir < 0 ? s : -s;
+    }
+    if (fft) {
+        host_fft(br, bi);
+        const ld inv = 1.0L / (ld)L;
+        for (size_t e = 0; e < L; ++e) {
+            br[e] *= inv;
+            bi[e] *= inv;
+        }
+    }
+    auto b = pack(br, bi, prec);
+    rc = upload(p, key + ":spec:" + std::to_string(dir) + ":" + std::to_string(prec) + (fft ? ":f" : ":d"), b.data(),
+                b.size(), &t->spec);
+    t->fft = fft;
+    return rc;
+}
+
+bool is_prime(size_t n) { return n >= 2 && prime_factorization(n).size() == 1; }
+
+// Adds one Rader launch over `lines` lines of a prime-length axis; false when
+// this prime needs the recursive extension (executed through Bluestein).
+int add_rader(Ctx& c, size_t prime, int dir, KArgs a, long long lines, int in_sel, size_t in_off, int out_sel,
+              size_t out_off, bool* done) {
+    *done = false;
+    const size_t L = prime - 1;
+    std::vector<int> rs;
+    const bool smooth = radix_schedule(L, rs);
+    bool fft = false;
+    Geometry g;
+    if (smooth) {
+        g = geometry(L, c.prec, 1, c.lds_max, c.lds_max);
+        fft = g.ok;
+    }
+    if (!fft && prime >= 89) return VKFX_OK;  // beyond direct multiplication: caller falls back
+    RaderTables t;
+    int rc = rader_tables(c.p, prime, dir, c.prec, fft, &t);
+    if (rc) return rc;
+    a.pin = (const int*)t.pin, a.pout = (const int*)t.pout, a.spec = t.spec;
+    if (fft) {
+        g = geometry(L, c.prec, std::max(1, 128 / g.TT), c.lds_max, c.lds_budget);
+        const int need = (int)L + (int)((L - 1) >> g.PS) + 2;  // x0 slot after the line
+        if (g.LS < need) {
+            g.LS = need | 1;
+            g.lds = (size_t)g.G * g.LS * csize(c.prec);
+        }
+        c.js << "\"rader\":{\"prime\":" << prime << ",\"mode\":\"fft\",\"convolution_len\":" << L << "},";
+        rc = add_launch(c, KK_RADER_FFT, -1, g, a, lines, blocks_for(lines, g.G), in_sel, in_off, out_sel, out_off,
+                        "rader_fft");
+    } else {
+        Geometry d;
+        d.N = (int)L;
+        d.TT = (int)L;
+        d.G = std::max(1, std::min(kMaxLinesPerBlock, 256 / (int)L));
+        d.LS = (int)L + 1;
+        d.PS = 30;
+        d.lds = (size_t)d.G * d.LS * csize(c.prec);
+        d.ok = true;
+        c.js << "\"rader\":{\"prime\":" << prime << ",\"mode\":\"direct\",\"convolution_len\":" << L << "},";
+        rc = add_launch(c, KK_RADER_DIRECT, -1, d, a, lines, blocks_for(lines, d.G), in_sel, in_off, out_sel,
+                        out_off, "rader_direct");
+    }
+    if (rc) return rc;
+    *done = true;
+    return VKFX_OK;
+}
+
 // ---- 1-D complex -----------------------------------------------------------
 
 int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorithm alg, size_t conv_len) {
@@ -542,7 +644,18 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
         }
         return VKFX_OK;
     }
-    // Bluestein (and, until a Rader kernel exists, Rader-classified axes).
+    if (alg == Algorithm::Rader && is_prime(n) && n > 2) {
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = a.out_os = (long long)n;
+        a.scale = sc;
+        bool done = false;
+        int rc = add_rader(c, n, dir, a, (long long)batch, SEL_IN, 0, SEL_OUT, 0, &done);
+        if (rc || done) return rc;
+    }
+    if (alg == Algorithm::Rader) c.js << "\"rader_fallback\":\"bluestein\",";
+    // Bluestein (also Rader axes that need the recursive extension or have
+    // composite length).
     const size_t M = conv_len ? conv_len : next_smooth_at_least(2 * n - 1, {2, 3, 5, 7});
     if (M < 2 * n - 1) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein convolution length below 2N-1");
     Geometry g = kernel_geometry(KK_BLUE_1, prec, -1, M, false, 1, c.lds_max, c.lds_max);
@@ -742,6 +855,15 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
                 rc = add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
                                 contiguous ? "stockham_rows" : "stockham_columns");
             } else {
+                if (alg == VKFX_ALG_RADER && is_prime(len) && len > 2) {
+                    bool done = false;
+                    rc = add_rader(c, len, dir, a, lines, in_sel, off, SEL_OUT, off, &done);
+                    if (rc) return rc;
+                    if (done) {
+                        first = false;
+                        continue;
+                    }
+                }
                 const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
                                                        : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
                 Geometry g = geometry(M, prec, contiguous ? 1 : 4, c.lds_max, c.lds_max);
@@ -1084,7 +1206,6 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         const int alg = d.axis_algorithm[i];
         c.js << (i ? "," : "") << "{\"len\":" << d.dims[i] << ",\"algorithm\":\""
              << (alg == VKFX_ALG_STOCKHAM ? "stockham" : alg == VKFX_ALG_RADER ? "rader" : "bluestein") << "\"";
-        if (alg == VKFX_ALG_RADER) c.js << ",\"executed_as\":\"bluestein\"";
         if (d.convolution_len[i]) c.js << ",\"convolution_len\":" << d.convolution_len[i];
         c.js << "}";
     }
@@ -1095,9 +1216,11 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             p->in_bytes = p->out_bytes = total * cs;
             if (d.rank == 1) {
                 const int alg = d.axis_algorithm[0];
-                Algorithm a = alg == VKFX_ALG_STOCKHAM ? Algorithm::Stockham : Algorithm::Bluestein;
+                Algorithm a = alg == VKFX_ALG_STOCKHAM ? Algorithm::Stockham
+                              : alg == VKFX_ALG_RADER  ? Algorithm::Rader
+                                                       : Algorithm::Bluestein;
                 size_t conv = d.convolution_len[0];
-                if (alg == VKFX_ALG_RADER) conv = 0;  // executed through Bluestein, M = next smooth >= 2N-1
+                if (alg == VKFX_ALG_RADER) conv = 0;  // Bluestein fallback uses M = next smooth >= 2N-1
                 rc = plan_c2c_1d(c, d.dims[0], d.batch, d.direction, d.normalize != 0, a, conv);
             } else {
                 rc = plan_c2c_nd(c, d);
