@@ -213,6 +213,49 @@ __device__ __forceinline__ void dft_odd(cpx<T>* x) {
 }
 
 template <int R, int S, typename T>
+__device__ __forceinline__ void dft(cpx<T>* x);
+
+// exp(S 2 pi i m / R) for the internal twiddles of composite butterflies,
+// folded to compile-time constants after unrolling (m, R constant).
+template <int R, int S, typename T>
+__device__ __forceinline__ cpx<T> unit_root(int m) {
+    constexpr double kTwoPi = 6.283185307179586476925286766559005768;
+    m %= R;
+    if (m == 0) return mk((T)1, (T)0);
+    // exact values at the quarter points keep the error of the multiply at zero
+    if (4 * m == R) return mk((T)0, (T)S);
+    if (2 * m == R) return mk((T)-1, (T)0);
+    if (4 * m == 3 * R) return mk((T)0, (T)-S);
+    return mk((T)__builtin_cos(kTwoPi * m / R), (T)(S * __builtin_sin(kTwoPi * m / R)));
+}
+
+// Composite DFT of length R = R1 * R2 (n = R2*n1 + n2, k = k1 + R1*k2): R2
+// DFTs of length R1, the internal twiddles W_R^(n2*k1), R1 DFTs of length R2.
+template <int R1, int R2, int S, typename T>
+__device__ __forceinline__ void dft_composite(cpx<T>* x) {
+    constexpr int R = R1 * R2;
+    cpx<T> y[R];
+#pragma unroll
+    for (int n2 = 0; n2 < R2; ++n2) {
+        cpx<T> col[R1];
+#pragma unroll
+        for (int n1 = 0; n1 < R1; ++n1) col[n1] = x[R2 * n1 + n2];
+        dft<R1, S>(col);
+#pragma unroll
+        for (int k1 = 0; k1 < R1; ++k1) y[k1 * R2 + n2] = (n2 * k1 % R) == 0 ? col[k1] : cmul(col[k1], unit_root<R, S, T>(n2 * k1));
+    }
+#pragma unroll
+    for (int k1 = 0; k1 < R1; ++k1) {
+        cpx<T> row[R2];
+#pragma unroll
+        for (int n2 = 0; n2 < R2; ++n2) row[n2] = y[k1 * R2 + n2];
+        dft<R2, S>(row);
+#pragma unroll
+        for (int k2 = 0; k2 < R2; ++k2) x[k1 + R1 * k2] = row[k2];
+    }
+}
+
+template <int R, int S, typename T>
 __device__ __forceinline__ void dft(cpx<T>* x) {
     if constexpr (R == 2) {
         dft2<S>(x);
@@ -222,6 +265,14 @@ __device__ __forceinline__ void dft(cpx<T>* x) {
         dft8<S>(x);
     } else if constexpr (R == 16) {
         dft16<S>(x);
+    } else if constexpr (R == 6) {
+        dft_composite<3, 2, S>(x);
+    } else if constexpr (R == 9) {
+        dft_composite<3, 3, S>(x);
+    } else if constexpr (R == 10) {
+        dft_composite<5, 2, S>(x);
+    } else if constexpr (R == 12) {
+        dft_composite<3, 4, S>(x);
     } else {
         dft_odd<R, S>(x);
     }
@@ -324,7 +375,11 @@ __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int 
             case 4: stage_lds<T, S, 4>(line, N, P, TT, t, ps, tw); break;
             case 5: stage_lds<T, S, 5>(line, N, P, TT, t, ps, tw); break;
             case 7: stage_lds<T, S, 7>(line, N, P, TT, t, ps, tw); break;
+            case 6: stage_lds<T, S, 6>(line, N, P, TT, t, ps, tw); break;
             case 8: stage_lds<T, S, 8>(line, N, P, TT, t, ps, tw); break;
+            case 9: stage_lds<T, S, 9>(line, N, P, TT, t, ps, tw); break;
+            case 10: stage_lds<T, S, 10>(line, N, P, TT, t, ps, tw); break;
+            case 12: stage_lds<T, S, 12>(line, N, P, TT, t, ps, tw); break;
             case 11: stage_lds<T, S, 11>(line, N, P, TT, t, ps, tw); break;
             case 13: stage_lds<T, S, 13>(line, N, P, TT, t, ps, tw); break;
             case 16: stage_lds<T, S, 16>(line, N, P, TT, t, ps, tw); break;

@@ -92,7 +92,10 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1))
         return (int)hipErrorInvalidValue;
     if (grid == 0) return (int)hipSuccess;
-    if (block == 0 || block > 512 || a.G < 1 || a.G > kMaxLinesPerBlock || (unsigned)(a.G * a.TT) != block)
+    // runtime-shape kernels are built for at most 512 threads, fixed shapes
+    // for exactly their own G * TT (at most 1024)
+    if (block == 0 || block > (fixed ? 1024u : 512u) || a.G < 1 || a.G > kMaxLinesPerBlock ||
+        (unsigned)(a.G * a.TT) != block)
         return (int)hipErrorInvalidConfiguration;
     if (a.nstages < 0 || a.nstages > kMaxStages) return (int)hipErrorInvalidValue;
     if (lds_bytes < (size_t)a.G * (size_t)a.LS * (prec ? 16 : 8) || lds_bytes > (size_t)lds_limit_bytes())

@@ -97,7 +97,8 @@ int max_bpt(int r) {
 }
 
 // Stage radices: power-of-two part split into ceil(p/4) stages as evenly as
-// possible (radix 16/8/4/2), then one stage per odd prime factor.
+// possible (radix 16/8/4/2), pairs of 3 as radix 9, then one stage per
+// remaining odd prime factor.
 bool radix_schedule(size_t n, std::vector<int>& out) {
     out.clear();
     size_t m = n;
@@ -111,7 +112,14 @@ bool radix_schedule(size_t n, std::vector<int>& out) {
         int base = p / s, extra = p % s;
         for (int i = 0; i < s; ++i) out.push_back(1 << (base + (i < extra ? 1 : 0)));
     }
-    for (int q : {3, 5, 7, 11, 13})
+    int threes = 0;
+    while (m % 3 == 0) {
+        m /= 3;
+        ++threes;
+    }
+    for (; threes >= 2; threes -= 2) out.push_back(9);
+    if (threes) out.push_back(3);
+    for (int q : {5, 7, 11, 13})
         while (m % q == 0) {
             m /= q;
             out.push_back(q);
