@@ -247,6 +247,27 @@ def test_nd_c2c(hip_ctx, dims, batch, prec):
     assert o.rel_l2(z, x) <= 4 * TOL[prec]
 
 
+@pytest.mark.parametrize("dims,batch,prec", [([64, 64, 64], 1, F64), ([8, 4096, 8], 1, F32),
+                                             ([32, 64, 48], 2, F64), ([6, 20, 64, 40], 2, F32)])
+def test_nd_slab_chunks(hip_ctx, monkeypatch, dims, batch, prec):
+    """Volumes above the chunk budget run axes 1.. slab chunk by slab chunk
+    (ragged last chunk, split strided middle axis, several batches), then
+    axis 0 over the whole volume."""
+    monkeypatch.setenv("VKFX_ND_CHUNK_MB", "1")
+    ctx = vk.HipExecutionContext(0)  # own plan cache: plans read the budget when built
+    try:
+        count = int(np.prod(dims)) * batch
+        x = rand(count, count % 997, prec)
+        y, ir = c2c(ctx, dims, batch, x, prec)
+        desc = ctx.plan(ir).describe()
+        assert desc["nd"]["slabs_per_chunk"] > 0
+        assert desc["lanes"] == 1
+        ref = o.fft_nd(x, dims, batch, threads=8)
+        assert o.rel_l2(y, ref) <= TOL[prec]
+    finally:
+        ctx.close()
+
+
 def test_c3_shape_full_size(hip_ctx):
     """C3: 4096 x 4096, batch 16, f32. Image 0 against the f64 oracle on a
     sample of rows of the row pass is too slow, so image 0 is checked against

@@ -70,12 +70,22 @@ __device__ __forceinline__ LineInfo line_default(const KArgs& a, long long blk, 
     long long line = blk * a.G + g;
     L.valid = line < a.nlines;
     if (!L.valid) line = 0;
-    const long long r = line / a.C;
-    L.c = line - r * a.C;
+    // line = (o * C1 + o1) * C + c; 32-bit division whenever the operands fit
+    long long r;
+    if (a.C == 1) {
+        r = line;
+        L.c = 0;
+    } else if (line < (1ll << 31) && a.C < (1ll << 31)) {
+        r = (long long)((unsigned)line / (unsigned)a.C);
+        L.c = line - r * a.C;
+    } else {
+        r = line / a.C;
+        L.c = line - r * a.C;
+    }
     long long o1 = 0;
     L.o = r;
     if (a.C1 > 1) {
-        L.o = r / a.C1;
+        L.o = (r < (1ll << 31) && a.C1 < (1ll << 31)) ? (long long)((unsigned)r / (unsigned)a.C1) : r / a.C1;
         o1 = r - L.o * a.C1;
     }
     L.ib = L.o * a.in_os + o1 * a.in_os1 + L.c * a.in_cs;
@@ -194,6 +204,25 @@ struct IoPlain {
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
         stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, scale(v, (T)a.scale));
     }
+    // Pointer form of the element functions for the direct stages: element
+    // e0 + i*step of a line is at in_ptr(e0) + i*step*in_es, so a thread
+    // computes one address and steps it by a uniform stride. A policy whose
+    // load_elem / store_elem (or store_twiddled) does more than this plain
+    // access sets kPtrLoad / kPtrStore false.
+    static constexpr bool kPtrLoad = true;
+    static constexpr bool kPtrStore = true;
+    template <typename T>
+    static __device__ __forceinline__ const cpx<T>* in_ptr(const KArgs& a, const LineInfo& L, int e) {
+        return (const cpx<T>*)a.in + L.ib + (long long)e * a.in_es;
+    }
+    template <typename T>
+    static __device__ __forceinline__ cpx<T>* out_ptr(const KArgs& a, const LineInfo& L, int e) {
+        return (cpx<T>*)a.out + L.ob + (long long)e * a.out_es;
+    }
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_at(const KArgs& a, cpx<T>* p, cpx<T> v) {
+        stg_out<NTIO>(a, p, scale(v, (T)a.scale));
+    }
     // staged variants used when an end cannot be direct
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -206,6 +235,7 @@ struct IoPlain {
 };
 
 struct IoR2CFull : IoPlain {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
     template <typename T, bool NTIO = false>
@@ -227,6 +257,7 @@ struct IoR2CFull : IoPlain {
 };
 
 struct IoC2RFull : IoPlain {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
@@ -278,6 +309,7 @@ struct IoR2CHalf : IoPlain {
 // Even-length C2R: Z[k] = (X[k] + conj X[M-k]) + i W_N^-k (X[k] - conj X[M-k]),
 // then the inverse half-size FFT; the complex result is the real output pairs.
 struct IoC2RHalf : IoPlain {
+    static constexpr bool kPtrLoad = false;
     static constexpr int kLoad = LAY_ROW;
     static constexpr int kStore = LAY_ROW;
     template <typename T, bool NTIO = false>
@@ -314,6 +346,10 @@ struct IoFsA : IoPlain {
         stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, twmul<S>(v, w));
     }
     template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_tw_at(const KArgs& a, cpx<T>* p, cpx<T> v, cpx<T> w) {
+        stg_out<NTIO>(a, p, twmul<S>(v, w));
+    }
+    template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
         store_twiddled<T, S, NTIO>(a, L, e, v, tw2<T>(a.tlo, a.thi, a.tshift, L.tr * e));
     }
@@ -328,6 +364,7 @@ struct IoFsA : IoPlain {
 };
 
 struct IoFsABlue : IoFsA {
+    static constexpr bool kPtrLoad = false;
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const long long n = L.c + (long long)e * a.N2;
@@ -341,6 +378,33 @@ struct IoFsABlue : IoFsA {
 };
 
 struct IoFsAC2R : IoFsA {
+    static constexpr bool kPtrLoad = false;
+    // With KF_MIRROR_PAIRS a block owns H = G/2 columns n2 = j*H + g and
+    // their mirrors N2 - n2 (column N2/2 stands in for the mirror of column
+    // 0), so the mirror loads X[M - k] of each column fall on the cache lines
+    // its partner column loads in the same block. Needs N2 % G == 0, G even.
+    static __device__ LineInfo line(const KArgs& a, long long blk, int g) {
+        if (!(a.flags & KF_MIRROR_PAIRS)) return line_default(a, blk, g);
+        const int H = a.G / 2;
+        const long long nbk = a.N2 / (2 * H);
+        LineInfo L;
+        L.o = blk / nbk;
+        const long long j = blk - L.o * nbk;
+        long long c;
+        if (g < H) {
+            c = j * H + g;
+        } else {
+            c = a.N2 - (j * H + (g - H));
+            if (c == a.N2) c = a.N2 / 2;
+        }
+        L.valid = L.o * a.N2 < a.nlines;
+        if (!L.valid) L.o = 0;
+        L.c = c;
+        L.tr = c;
+        L.ib = L.o * a.in_os + c * a.in_cs;
+        L.ob = L.o * a.out_os + c * a.out_cs;
+        return L;
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
@@ -437,6 +501,7 @@ struct IoFsBR2C : IoPlain {
 // transposed as spec[k1*N2 + k2] with 1/M folded in), inverse FFT over k2 and
 // the inverse four-step twiddle W_M^(-k1*m2); rows stay in place.
 struct IoBlueB : IoPlain {
+    static constexpr bool kPtrStore = false;
     static constexpr bool kTwoPass = true;
     static constexpr int kLoad = LAY_ROW;
     static constexpr int kStore = LAY_ROW;
@@ -476,6 +541,7 @@ struct IoBlueB : IoPlain {
 // Bluestein column pass: inverse FFT over k1 gives conv[m2 + N2*m1]; keep
 // m < N and multiply by the chirp (and the caller's scale).
 struct IoFsCBlue : IoPlain {
+    static constexpr bool kPtrStore = false;
     static constexpr int kLoad = LAY_COL;
     static constexpr int kStore = LAY_COL;
     template <typename T, int S, bool NTIO = false>
@@ -497,6 +563,7 @@ struct IoFsCBlue : IoPlain {
 // Whole Bluestein transform in LDS: a = chirp * x zero-padded to M = N,
 // FFT, multiply by the kernel spectrum, IFFT, chirp multiply, truncate.
 struct IoBlue1 : IoPlain {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
     static constexpr bool kTwoPass = true;
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
@@ -534,6 +601,7 @@ struct IoBlue1 : IoPlain {
 // X[0] = x0 + A[0] (the DC of the gathered sequence is sum x - x0). x0 sits
 // in the last LDS slot of the line so in-place execution is safe.
 struct IoRader : IoPlain {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
     static constexpr bool kTwoPass = true;
     static constexpr int kLoad = LAY_STAGED;
     static constexpr int kStore = LAY_STAGED;
@@ -652,6 +720,35 @@ struct Shape {
     using Dims = FixDims<N_, G_, LS_, PS_>;
 };
 
+// LDS slot of element e0 + i*STEP. When STEP is a multiple of the pad period
+// 2^PS the pad of every element is the pad of e0 plus a constant, so the
+// slots are one base plus compile-time offsets.
+template <int PS, int STEP>
+__device__ __forceinline__ int lds_step(int e0, int i) {
+    if constexpr (PS >= 30) {
+        return e0 + i * STEP;
+    } else if constexpr (STEP % (1 << PS) == 0) {
+        return lpad(e0, PS) + i * (STEP + (STEP >> PS));
+    } else {
+        return lpad(e0 + i * STEP, PS);
+    }
+}
+// LDS slot of Stockham output base + q*P of a radix-R butterfly, base =
+// (b - k)*R + k with k = b mod P. If P*R divides 2^PS the R outputs stay in
+// one pad period of base, so they share its pad.
+template <int PS, int P, int R>
+__device__ __forceinline__ int lds_out(int base, int q) {
+    if constexpr (PS >= 30) {
+        return base + q * P;
+    } else if constexpr (P % (1 << PS) == 0) {
+        return lpad(base, PS) + q * (P + (P >> PS));
+    } else if constexpr ((1 << PS) % (P * R) == 0) {
+        return lpad(base, PS) + q * P;
+    } else {
+        return lpad(base + q * P, PS);
+    }
+}
+
 // One stage with compile-time geometry. SRC/DST: 0 = the line in LDS,
 // 1 = HBM through the IO policy's element functions.
 template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST, bool NTI, bool NTO>
@@ -665,13 +762,21 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
     for (int j = 0; j < MJ; ++j) {
         const int b = t + j * TT;
         if (EXACT || b < NB) {
+            if constexpr (SRC && IO::kPtrLoad) {
+                // line() maps a line past the end onto line 0, so these loads
+                // stay inside the buffer; such a line's stores are skipped
+                const cpx<T>* p = IO::template in_ptr<T>(a, L, b);
+                const long long st = (long long)NB * a.in_es;
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int e = b + i * NB;
-                if constexpr (SRC) {
-                    v[j][i] = L.valid ? IO::template load_elem<T, NTI>(a, L, e) : zero<T>();
-                } else {
-                    v[j][i] = line[lpad(e, PS)];
+                for (int i = 0; i < R; ++i) v[j][i] = ldg_in<NTI>(a, p + i * st);
+            } else {
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    if constexpr (SRC) {
+                        v[j][i] = L.valid ? IO::template load_elem<T, NTI>(a, L, b + i * NB) : zero<T>();
+                    } else {
+                        v[j][i] = line[lds_step<PS, NB>(b, i)];
+                    }
                 }
             }
         }
@@ -698,18 +803,32 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                     const cpx<T> wb = IO::template tw_root<T>(a, L.tr * b);
                     cpx<T> sp[R];
                     root_powers<R>(IO::template tw_root<T>(a, L.tr * NB), sp);
+                    if constexpr (IO::kPtrStore) {
+                        cpx<T>* p = IO::template out_ptr<T>(a, L, base);
+                        const long long st = (long long)P * a.out_es;
 #pragma unroll
-                    for (int q = 0; q < R; ++q)
-                        IO::template store_twiddled<T, S, NTO>(a, L, base + q * P, v[j][q], cmul(wb, sp[q]));
+                        for (int q = 0; q < R; ++q)
+                            IO::template store_tw_at<T, S, NTO>(a, p + q * st, v[j][q], cmul(wb, sp[q]));
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < R; ++q)
+                            IO::template store_twiddled<T, S, NTO>(a, L, base + q * P, v[j][q], cmul(wb, sp[q]));
+                    }
+                }
+            } else if constexpr (DST && IO::kPtrStore) {
+                if (L.valid) {
+                    cpx<T>* p = IO::template out_ptr<T>(a, L, base);
+                    const long long st = (long long)P * a.out_es;
+#pragma unroll
+                    for (int q = 0; q < R; ++q) IO::template store_at<T, S, NTO>(a, p + q * st, v[j][q]);
                 }
             } else {
 #pragma unroll
                 for (int q = 0; q < R; ++q) {
-                    const int o = base + q * P;
                     if constexpr (DST) {
-                        if (L.valid) IO::template store_elem<T, S, NTO>(a, L, o, v[j][q]);
+                        if (L.valid) IO::template store_elem<T, S, NTO>(a, L, base + q * P, v[j][q]);
                     } else {
-                        line[lpad(o, PS)] = v[j][q];
+                        line[lds_out<PS, P, R>(base, q)] = v[j][q];
                     }
                 }
             }
@@ -828,7 +947,7 @@ KernelFn pick(KernelKind kind) {
 // zero-terminated; nst is filled in by the registry lookup.
 #define VKFX_FIXED_OCC(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, W, NTI, NTO, ...)                  \
     FixedKernel {                                                                                      \
-        KIND, PREC, S, N, TT, G, PS, LS, COL, 0, {__VA_ARGS__},                                         \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                               \
             (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>), \
             (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)              \
     }
@@ -839,7 +958,7 @@ KernelFn pick(KernelKind kind) {
     VKFX_FIXED_OCC(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, 0, NTI, NTO, __VA_ARGS__)
 #define VKFX_FIXED(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, ...)                                   \
     FixedKernel {                                                                                     \
-        KIND, PREC, S, N, TT, G, PS, LS, COL, 0, {__VA_ARGS__},                                        \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, false, false, 0, {__VA_ARGS__},                          \
             (KernelFn)(k_fix<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>),                    \
             (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)             \
     }

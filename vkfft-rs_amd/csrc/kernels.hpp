@@ -34,6 +34,7 @@ enum KernelKind : int {
 enum KFlags : int {
     KF_IN_ROWMAJOR = 1,   // a line's elements are contiguous in the input
     KF_OUT_ROWMAJOR = 2,  // a line's elements are contiguous in the output
+    KF_MIRROR_PAIRS = 4,  // C2R column pass: a block owns columns and their mirrors
 };
 
 struct KArgs {
@@ -85,6 +86,7 @@ struct FixedKernel {
     int prec, dir;
     int N, TT, G, PS, LS;
     bool col;  // lanes run across lines (strided layouts)
+    bool nti, nto;  // nontemporal loads of the pass input / stores of its output
     int nst;
     int radix[8];
     KernelFn fn;          // one block per group of G lines
@@ -95,6 +97,10 @@ struct FixedKernel {
 // length, lane mapping); nullptr when only the runtime-shape kernel applies.
 // Setting VKFX_DISABLE_FIXED=1 in the environment forces the runtime-shape kernels.
 const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool col);
+
+// The registered instantiation with the same shape as f and the given
+// nontemporal load/store choice; f itself when none is registered.
+const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto);
 
 // Launches one kernel. prec: 0 = f32, 1 = f64. dir: -1 forward, +1 inverse
 // (direction of the first FFT the kernel runs). fixed: the fixed-shape

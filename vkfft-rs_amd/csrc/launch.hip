@@ -14,26 +14,28 @@ KernelFn pick_f64_inv(KernelKind kind);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
 const FixedKernel* fixed_table_blue(int* count);
+const FixedKernel* fixed_table_nd(int* count);
 
-const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool col) {
-    static const bool disabled = [] {
-        const char* e = getenv("VKFX_DISABLE_FIXED");
-        return e && e[0] == '1';
-    }();
-    if (disabled) return nullptr;
-    static FixedKernel* all = nullptr;
-    static int total = 0;
-    if (!all) {
-        const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_real, fixed_table_blue};
-        int counts[3], sum = 0;
-        const FixedKernel* ptrs[3];
-        for (int i = 0; i < 3; ++i) {
+// All registered fixed-shape instantiations, merged once (thread-safe
+// static initialisation).
+static const FixedKernel* registry(int* count) {
+    struct Merged {
+        const FixedKernel* all;
+        int total;
+    };
+    static const Merged m = [] {
+        const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_real, fixed_table_blue,
+                                                fixed_table_nd};
+        constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
+        int counts[kTables], sum = 0;
+        const FixedKernel* ptrs[kTables];
+        for (int i = 0; i < kTables; ++i) {
             ptrs[i] = tables[i](&counts[i]);
             sum += counts[i];
         }
         FixedKernel* merged = new FixedKernel[sum];
         int k = 0;
-        for (int i = 0; i < 3; ++i)
+        for (int i = 0; i < kTables; ++i)
             for (int j = 0; j < counts[i]; ++j) {
                 merged[k] = ptrs[i][j];
                 int n = 0;
@@ -41,9 +43,20 @@ const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool co
                 merged[k].nst = n;
                 ++k;
             }
-        total = sum;
-        all = merged;
-    }
+        return Merged{merged, sum};
+    }();
+    *count = m.total;
+    return m.all;
+}
+
+const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool col) {
+    static const bool disabled = [] {
+        const char* e = getenv("VKFX_DISABLE_FIXED");
+        return e && e[0] == '1';
+    }();
+    if (disabled) return nullptr;
+    int total = 0;
+    const FixedKernel* all = registry(&total);
     // VKFX_FIXED_PICK=k selects the k-th registered variant of a shape key
     // (tuning runs); the default is the first.
     static const int pick = [] {
@@ -60,6 +73,23 @@ const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool co
         }
     }
     return first;
+}
+
+const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto) {
+    if (!f || (f->nti == nti && f->nto == nto)) return f;
+    int total = 0;
+    const FixedKernel* all = registry(&total);
+    for (int i = 0; i < total; ++i) {
+        const FixedKernel& v = all[i];
+        if (v.kind != f->kind || v.prec != f->prec || v.dir != f->dir || v.N != f->N || v.col != f->col ||
+            v.TT != f->TT || v.G != f->G || v.PS != f->PS || v.LS != f->LS || v.nst != f->nst || v.nti != nti ||
+            v.nto != nto)
+            continue;
+        bool same = true;
+        for (int s = 0; s < v.nst; ++s) same = same && v.radix[s] == f->radix[s];
+        if (same) return &v;
+    }
+    return f;
 }
 
 static int lds_limit_bytes() {

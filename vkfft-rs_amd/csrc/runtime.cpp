@@ -195,6 +195,7 @@ struct vkfx_plan {
     size_t work_bytes = 0;  // per lane while planning; total after plan_create
     size_t work_lane = 0;   // workspace bytes of one stream lane
     int lanes = 1;          // 2: chunks alternate between the caller's stream and the aux stream
+    bool serial = false;    // chunks depend on each other: one lane
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
     std::string json;
@@ -436,6 +437,8 @@ void note_pass(Ctx& c, const Launch& L) {
     c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.a.N << ",\"lines\":" << L.a.nlines
          << ",\"grid\":" << L.grid << ",\"block\":" << L.block << ",\"lines_per_block\":" << L.a.G
          << ",\"lds_bytes\":" << L.lds << ",\"fixed_shape\":" << (L.fixed ? "true" : "false")
+         << ",\"nontemporal\":[" << (L.fixed && L.fixed->nti ? "true" : "false") << ","
+         << (L.fixed && L.fixed->nto ? "true" : "false") << "]"
          << ",\"radices\":[";
     for (int i = 0; i < L.a.nstages; ++i) c.js << (i ? "," : "") << L.a.radix[i];
     c.js << "]}";
@@ -626,7 +629,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
         c.js << "\"four_step\":{\"len\":" << n << ",\"n1\":" << n1 << ",\"n2\":" << n2 << ",\"chunk\":" << chunk
              << "},";
         for (size_t b0 = 0; b0 < batch; b0 += chunk) {
-            c.cur_chunk = (int)(b0 / chunk);
+        c.cur_chunk = (int)(b0 / chunk);
             const size_t cb = std::min(chunk, batch - b0);
             KArgs a = blank();
             a.C = (long long)n2;
@@ -703,7 +706,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     c.js << "\"bluestein\":{\"len\":" << n << ",\"m\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
          << ",\"chunk\":" << chunk << "},";
     for (size_t b0 = 0; b0 < batch; b0 += chunk) {
-            c.cur_chunk = (int)(b0 / chunk);
+        c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, batch - b0);
         KArgs a = blank();
         a.C = (long long)n2;
@@ -791,115 +794,150 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
     if (const char* e = getenv("VKFX_ND_CHUNK_MB")) chunk_budget = (size_t)atoll(e) << 20;
     chunk = std::max<size_t>(1, std::min(d.batch, chunk_budget / std::max<size_t>(per_batch * cs, 1)));
     if (any_split) c.p->work_bytes = std::max(c.p->work_bytes, chunk * per_batch * cs);
-    c.js << "\"nd\":{\"chunk\":" << chunk << "},";
+    // A volume larger than the chunk budget runs its axes 1.. (which stay
+    // inside one slab of fixed index along axis 0) slab chunk by slab chunk,
+    // then axis 0 over the whole volume.
+    const size_t slab = per_batch / d.dims[0];
+    int slab_axes = 0;
+    for (uint32_t ax = 1; ax < d.rank; ++ax) slab_axes += d.dims[ax] > 1;
+    size_t slabs = 0;
+    if (chunk == 1 && per_batch * cs > chunk_budget && d.dims[0] > 1 && slab_axes >= 2)
+        slabs = std::max<size_t>(1, chunk_budget / (slab * cs));
+    c.js << "\"nd\":{\"chunk\":" << chunk << ",\"slabs_per_chunk\":" << slabs << "},";
+
+    // Launches of one axis over `total` elements at byte offset `off`.
+    auto axis_pass = [&](int ax, size_t total, size_t off, int in_sel) -> int {
+        const size_t len = d.dims[ax];
+        size_t inner = 1;
+        for (uint32_t j = ax + 1; j < d.rank; ++j) inner *= d.dims[j];
+        const size_t outer = total / (len * inner);
+        const double sc = (dir > 0 && d.normalize) ? 1.0 / (double)len : 1.0;
+        const bool contiguous = inner == 1;
+        const int alg = d.axis_algorithm[ax];
+        int rc;
+        size_t l1 = 0, l2 = 0;
+        if (alg == VKFX_ALG_STOCKHAM && !contiguous && split_strided_axis(len, prec, c.lds_budget, &l1, &l2)) {
+            // pass A: lines (o, n2, c), FFT over n1 at stride L2*inner, twiddle, store in place pattern
+            Geometry ga = kernel_geometry(KK_FS_A, prec, dir, l1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+            Geometry gb = kernel_geometry(KK_PLAIN, prec, dir, l2, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+            if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "split axis geometry");
+            const void *tlo, *thi;
+            int tsh;
+            rc = two_level(c.p, len, prec, &tlo, &thi, &tsh);
+            if (rc) return rc;
+            KArgs a = blank();
+            a.C = (long long)(l2 * inner);
+            a.in_cs = a.out_cs = 1;
+            a.in_es = a.out_es = (long long)(l2 * inner);
+            a.in_os = a.out_os = (long long)(len * inner);
+            a.twdiv = (long long)inner;
+            a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+            long long lines = (long long)(outer * l2 * inner);
+            rc = add_launch(c, KK_FS_A, dir, ga, a, lines, blocks_for(lines, ga.G), in_sel, off, SEL_WORK, 0,
+                            "split_axis_pass1");
+            if (rc) return rc;
+            // pass B: lines (o, k1, c), FFT over n2 at stride inner, store k1 + L1*k2
+            KArgs b = blank();
+            b.C = (long long)inner;
+            b.C1 = (long long)l1;
+            b.in_cs = b.out_cs = 1;
+            b.in_es = (long long)inner, b.in_os1 = (long long)(l2 * inner), b.in_os = (long long)(len * inner);
+            b.out_es = (long long)(l1 * inner), b.out_os1 = (long long)inner, b.out_os = (long long)(len * inner);
+            b.scale = sc;
+            lines = (long long)(outer * l1 * inner);
+            rc = add_launch(c, KK_PLAIN, dir, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_OUT, off,
+                            "split_axis_pass2");
+            return rc;
+        }
+        KArgs a = blank();
+        a.C = (long long)inner;
+        a.in_es = a.out_es = (long long)inner;
+        a.in_cs = a.out_cs = 1;
+        a.in_os = a.out_os = (long long)(len * inner);
+        a.flags = contiguous ? (KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR) : 0;
+        a.scale = sc;
+        const long long lines = (long long)(outer * inner);
+        if (alg == VKFX_ALG_STOCKHAM) {
+            Geometry g0 = geometry(len, prec, 1, c.lds_max, c.lds_max);
+            if (!g0.ok)
+                return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                            "N-D axis length " + std::to_string(len) + " exceeds one upload");
+            const int want = contiguous ? std::max(1, 256 / g0.TT) : (prec ? 8 : 16);
+            Geometry g = kernel_geometry(KK_PLAIN, prec, dir, len, !contiguous, want, c.lds_max, c.lds_budget);
+            rc = add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
+                            contiguous ? "stockham_rows" : "stockham_columns");
+        } else {
+            if (alg == VKFX_ALG_RADER && is_prime(len) && len > 2) {
+                bool done = false;
+                rc = add_rader(c, len, dir, a, lines, in_sel, off, SEL_OUT, off, &done);
+                if (rc) return rc;
+                if (done) return VKFX_OK;
+            }
+            const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
+                                                   : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
+            Geometry g = geometry(M, prec, contiguous ? 1 : 4, c.lds_max, c.lds_max);
+            if (!g.ok)
+                return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                            "N-D Bluestein axis needs more than one upload (M=" + std::to_string(M) + ")");
+            BlueTables t;
+            rc = bluestein_tables(c.p, len, M, dir, prec, 0, 0, &t);
+            if (rc) return rc;
+            a.chirp = t.chirp, a.spec = t.spec;
+            a.nvalid = (long long)len, a.nout = (long long)len, a.M = (long long)M;
+            rc = add_launch(c, KK_BLUE_1, -1, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
+                            "bluestein_axis");
+        }
+        return rc;
+    };
+    auto copy_pass = [&](size_t total, size_t off) -> int {
+        // every axis has length 1: the transform is a copy
+        Geometry g = geometry(1, prec, 64, c.lds_max, c.lds_budget);
+        KArgs a = blank();
+        a.in_es = a.out_es = 1;
+        a.in_os = a.out_os = 1;
+        a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+        return add_launch(c, KK_PLAIN, dir, g, a, (long long)total, blocks_for(total, g.G), SEL_IN, off, SEL_OUT, off,
+                          "copy");
+    };
+
+    int next_chunk = 0;
     for (size_t b0 = 0; b0 < d.batch; b0 += chunk) {
-        c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, d.batch - b0);
         const size_t off = b0 * per_batch * cs;
         const size_t total = cb * per_batch;
+        if (slabs) {
+            for (size_t s0 = 0; s0 < d.dims[0]; s0 += slabs) {
+                c.cur_chunk = next_chunk++;
+                const size_t ns = std::min(slabs, d.dims[0] - s0);
+                bool sfirst = true;
+                for (int ax = (int)d.rank - 1; ax >= 1; --ax) {
+                    if (d.dims[ax] == 1) continue;
+                    int rc = axis_pass(ax, ns * slab, off + s0 * slab * cs, sfirst ? SEL_IN : SEL_OUT);
+                    if (rc) return rc;
+                    sfirst = false;
+                }
+            }
+            c.cur_chunk = next_chunk++;
+            int rc = axis_pass(0, total, off, SEL_OUT);
+            if (rc) return rc;
+            continue;
+        }
+        c.cur_chunk = next_chunk++;
         bool first = true;
         for (int ax = (int)d.rank - 1; ax >= 0; --ax) {
-            const size_t len = d.dims[ax];
-            if (len == 1) continue;
-            size_t inner = 1;
-            for (uint32_t j = ax + 1; j < d.rank; ++j) inner *= d.dims[j];
-            const size_t outer = total / (len * inner);
-            const double sc = (dir > 0 && d.normalize) ? 1.0 / (double)len : 1.0;
-            const bool contiguous = inner == 1;
-            const int alg = d.axis_algorithm[ax];
-            const int in_sel = first ? SEL_IN : SEL_OUT;
-            int rc;
-            size_t l1 = 0, l2 = 0;
-            if (alg == VKFX_ALG_STOCKHAM && !contiguous && split_strided_axis(len, prec, c.lds_budget, &l1, &l2)) {
-                // pass A: lines (o, n2, c), FFT over n1 at stride L2*inner, twiddle, store in place pattern
-                Geometry ga = kernel_geometry(KK_FS_A, prec, dir, l1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
-                Geometry gb = kernel_geometry(KK_PLAIN, prec, dir, l2, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
-                if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "split axis geometry");
-                const void *tlo, *thi;
-                int tsh;
-                rc = two_level(c.p, len, prec, &tlo, &thi, &tsh);
-                if (rc) return rc;
-                KArgs a = blank();
-                a.C = (long long)(l2 * inner);
-                a.in_cs = a.out_cs = 1;
-                a.in_es = a.out_es = (long long)(l2 * inner);
-                a.in_os = a.out_os = (long long)(len * inner);
-                a.twdiv = (long long)inner;
-                a.tlo = tlo, a.thi = thi, a.tshift = tsh;
-                long long lines = (long long)(outer * l2 * inner);
-                rc = add_launch(c, KK_FS_A, dir, ga, a, lines, blocks_for(lines, ga.G), in_sel, off, SEL_WORK, 0,
-                                "split_axis_pass1");
-                if (rc) return rc;
-                // pass B: lines (o, k1, c), FFT over n2 at stride inner, store k1 + L1*k2
-                KArgs b = blank();
-                b.C = (long long)inner;
-                b.C1 = (long long)l1;
-                b.in_cs = b.out_cs = 1;
-                b.in_es = (long long)inner, b.in_os1 = (long long)(l2 * inner), b.in_os = (long long)(len * inner);
-                b.out_es = (long long)(l1 * inner), b.out_os1 = (long long)inner, b.out_os = (long long)(len * inner);
-                b.scale = sc;
-                lines = (long long)(outer * l1 * inner);
-                rc = add_launch(c, KK_PLAIN, dir, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_OUT, off,
-                                "split_axis_pass2");
-                if (rc) return rc;
-                first = false;
-                continue;
-            }
-            KArgs a = blank();
-            a.C = (long long)inner;
-            a.in_es = a.out_es = (long long)inner;
-            a.in_cs = a.out_cs = 1;
-            a.in_os = a.out_os = (long long)(len * inner);
-            a.flags = contiguous ? (KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR) : 0;
-            a.scale = sc;
-            const long long lines = (long long)(outer * inner);
-            if (alg == VKFX_ALG_STOCKHAM) {
-                Geometry g0 = geometry(len, prec, 1, c.lds_max, c.lds_max);
-                if (!g0.ok)
-                    return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
-                                "N-D axis length " + std::to_string(len) + " exceeds one upload");
-                const int want = contiguous ? std::max(1, 256 / g0.TT) : (prec ? 8 : 16);
-                Geometry g = kernel_geometry(KK_PLAIN, prec, dir, len, !contiguous, want, c.lds_max, c.lds_budget);
-                rc = add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
-                                contiguous ? "stockham_rows" : "stockham_columns");
-            } else {
-                if (alg == VKFX_ALG_RADER && is_prime(len) && len > 2) {
-                    bool done = false;
-                    rc = add_rader(c, len, dir, a, lines, in_sel, off, SEL_OUT, off, &done);
-                    if (rc) return rc;
-                    if (done) {
-                        first = false;
-                        continue;
-                    }
-                }
-                const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
-                                                       : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
-                Geometry g = geometry(M, prec, contiguous ? 1 : 4, c.lds_max, c.lds_max);
-                if (!g.ok)
-                    return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
-                                "N-D Bluestein axis needs more than one upload (M=" + std::to_string(M) + ")");
-                BlueTables t;
-                rc = bluestein_tables(c.p, len, M, dir, prec, 0, 0, &t);
-                if (rc) return rc;
-                a.chirp = t.chirp, a.spec = t.spec;
-                a.nvalid = (long long)len, a.nout = (long long)len, a.M = (long long)M;
-                rc = add_launch(c, KK_BLUE_1, -1, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT, off,
-                                "bluestein_axis");
-            }
+            if (d.dims[ax] == 1) continue;
+            int rc = axis_pass(ax, total, off, first ? SEL_IN : SEL_OUT);
             if (rc) return rc;
             first = false;
         }
-        if (first) {  // every axis has length 1: the transform is a copy
-            Geometry g = geometry(1, prec, 64, c.lds_max, c.lds_budget);
-            KArgs a = blank();
-            a.in_es = a.out_es = 1;
-            a.in_os = a.out_os = 1;
-            a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
-            int rc = add_launch(c, KK_PLAIN, dir, g, a, (long long)total, blocks_for(total, g.G), SEL_IN, off, SEL_OUT,
-                                off, "copy");
+        if (first) {
+            int rc = copy_pass(total, off);
             if (rc) return rc;
         }
     }
+    // One stream lane: slab chunks feed the axis-0 pass of their volume, and
+    // a single chunk in flight keeps its intermediate in the Infinity Cache.
+    c.p->serial = true;
     return VKFX_OK;
 }
 
@@ -960,7 +998,7 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
          << ",\"chunk\":" << chunk << "},";
     for (size_t b0 = 0; b0 < batch; b0 += chunk) {
-            c.cur_chunk = (int)(b0 / chunk);
+        c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, batch - b0);
         KArgs a = blank();
         a.C = (long long)n2;
@@ -1026,9 +1064,15 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     size_t n1, n2;
     if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
         return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for C2R half length");
+    // take the orientation whose two passes have fixed shapes registered
+    if (!find_fixed(KK_FS_A_C2R, prec, 1, (int)n1, true) && find_fixed(KK_FS_A_C2R, prec, 1, (int)n2, true) &&
+        find_fixed(KK_FS_B, prec, 1, (int)n1, false))
+        std::swap(n1, n2);
     Geometry ga = kernel_geometry(KK_FS_A_C2R, prec, 1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
     Geometry gb = kernel_geometry(KK_FS_B, prec, 1, n2, false, prec ? 8 : 16, c.lds_max, c.lds_budget);
     if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "C2R four-step geometry");
+    // columns beside their mirrors in one block when the groups tile N2 evenly
+    const bool pairs = ga.G % 2 == 0 && n2 % 2 == 0 && n2 % (size_t)ga.G == 0;
     const void *tlo, *thi;
     int tsh;
     rc = two_level(p, M, prec, &tlo, &thi, &tsh);
@@ -1036,9 +1080,9 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     const size_t chunk = chunk_for(batch, M * cs);
     p->work_bytes = std::max(p->work_bytes, chunk * M * cs);
     c.js << "\"real\":{\"len\":" << n << ",\"half\":" << M << ",\"uploads\":2,\"n1\":" << n1 << ",\"n2\":" << n2
-         << ",\"chunk\":" << chunk << "},";
+         << ",\"chunk\":" << chunk << ",\"mirror_pairs\":" << (pairs ? "true" : "false") << "},";
     for (size_t b0 = 0; b0 < batch; b0 += chunk) {
-            c.cur_chunk = (int)(b0 / chunk);
+        c.cur_chunk = (int)(b0 / chunk);
         const size_t cb = std::min(chunk, batch - b0);
         KArgs a = blank();
         a.C = (long long)n2;
@@ -1047,6 +1091,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
         a.tlo = tlo, a.thi = thi, a.tshift = tsh;
         a.rlo = rlo, a.rhi = rhi, a.rshift = rsh;
         a.M = (long long)M, a.N1 = (long long)n1, a.N2 = (long long)n2;
+        if (pairs) a.flags |= KF_MIRROR_PAIRS;
         long long lines = (long long)(cb * n2);
         rc = add_launch(c, KK_FS_A_C2R, 1, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * h * cs, SEL_WORK, 0,
                         "c2r_columns_pre");
@@ -1253,10 +1298,27 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     }
     int nchunks = 1;
     for (const Launch& L : p->launches) nchunks = std::max(nchunks, L.chunk + 1);
+    // Nontemporal roles of the fixed-shape passes: a pass reading the
+    // caller's input streams it (nontemporal loads), the last pass of a chunk
+    // streams the caller's output (nontemporal stores), and every other access
+    // stays cached so that a chunk's intermediate is served from the Infinity
+    // Cache by the next pass. VKFX_NT_ROLES=0 keeps each shape's first
+    // registered variant.
+    static const bool nt_roles = [] {
+        const char* e = getenv("VKFX_NT_ROLES");
+        return !(e && e[0] == '0');
+    }();
+    for (size_t i = 0; nt_roles && i < p->launches.size(); ++i) {
+        Launch& L = p->launches[i];
+        if (!L.fixed) continue;
+        bool last = true;
+        for (size_t j = i + 1; j < p->launches.size() && last; ++j) last = p->launches[j].chunk != L.chunk;
+        L.fixed = fixed_variant(L.fixed, L.in_sel == SEL_IN, L.out_sel == SEL_OUT && last);
+    }
     // two lanes pay a fork/join (two events, ~10 us) per execute, so only
     // plans with several chunks use them
-    p->lanes = nchunks >= 4 ? 2 : 1;
-    if (const char* e = getenv("VKFX_LANES")) p->lanes = (atoi(e) == 1) ? 1 : p->lanes;
+    p->lanes = nchunks >= 4 && !p->serial ? 2 : 1;
+    if (const char* e = getenv("VKFX_LANES")) p->lanes = (atoi(e) == 1 || p->serial) ? 1 : p->lanes;
     p->work_lane = p->work_bytes;
     p->work_bytes = p->work_lane * p->lanes;
     if (p->lanes == 2) {
