@@ -5,9 +5,12 @@
 namespace vkfx {
 
 static const FixedKernel kTable[] = {
-    // 1-D rows of 1024 (C1): one wave per line, 16 elements per thread
+    // 1-D rows of 1024 (C1): two waves per line, 8 elements per thread in the
+    // radix-8 stages (16 in the radix-16 load stage)
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 5, 1056, false, true, true, 16, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 1024, 128, 1, 5, 1056, false, true, true, 16, 8, 8),
+    // one wave per line (VKFX_FIXED_PICK=1)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
     // rows of 4096 (C3 axis 1)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 5, 4224, false, true, true, 16, 16, 16),
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 5, 4224, false, true, true, 16, 16, 16),
