@@ -43,6 +43,18 @@ CONFIGS = {
 }
 
 
+# BASELINE's metric for the default workload; the other configs report the
+# same quantities for their own transform.
+METRICS = {
+    "c1": "batched f32 C2C effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+    "c2": "batched f32 R2C + C2R effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+    "c3": "batched f32 2-D C2C effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+    "c4": "f64 3-D C2C effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+    "c5a": "batched f32 C2C (Bluestein axis) effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+    "c5b": "batched f32 C2C (Bluestein axis) effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+}
+
+
 def algorithmic(cfg):
     """(bytes, flops) of one step: one read + one write of the logical data
     (BASELINE.md section 2); flops 5 N log2 N per transform (logical N)."""
@@ -130,6 +142,35 @@ def run_gpu(cfg, steps, warmup, rotate):
     return total_ms / steps, sum(per_launch) / len(per_launch), info
 
 
+def plain_copy_bandwidth(nbytes=1 << 30, reps=10):
+    """The library's own copy (a transform whose only axis has length 1:
+    dims [1], f64, 1 GiB) on device buffers. Its kernel
+    (k_dyn<double, -1, IoPlain>) moves 8-16 bytes per lane like the FFT
+    kernels, so its FETCH_SIZE / WRITE_SIZE counters calibrate theirs."""
+    import torch
+
+    torch.cuda.init()
+    import vkfft_amd as vk
+
+    ctx = vk.HipExecutionContext(0)
+    ir = vk.TransformIr.build(vk.FftConfig.new([1]).with_batch_count(nbytes // 16).with_precision(vk.Precision.F64),
+                              vk.Direction.Forward)
+    plan = ctx.plan(ir)
+    x = torch.zeros(nbytes // 4, device="cuda", dtype=torch.float32)
+    y = torch.empty_like(x)
+    s = torch.cuda.current_stream()
+    plan.execute(x.data_ptr(), y.data_ptr(), 0, s.cuda_stream)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    for _ in range(reps):
+        plan.execute(x.data_ptr(), y.data_ptr(), 0, s.cuda_stream)
+    b.record(s)
+    torch.cuda.synchronize()
+    ctx.close()
+    return 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+
+
 def copy_bandwidth(nbytes=1 << 30, reps=20):
     """Measured device-to-device copy rate (read + write bytes / time), the
     practical HBM ceiling on this box next to the nominal 8 TB/s."""
@@ -179,14 +220,15 @@ def cpu_baseline(cfg, budget_s=15.0):
                       f"~{per * done:.1f} s CPU work"}
 
 
-COPY_BYTES = 1 << 30  # copy_bandwidth(): 1 GiB read + 1 GiB written per launch
+COPY_BYTES = 1 << 30  # plain_copy_bandwidth(): 1 GiB read + 1 GiB written per launch
+CALIBRATION_KERNEL = "k_dyn<double, -1, vkfx::IoPlain>"
 
 
 def rocprof_summary(dirs, workload_kernel="vkfx"):
     """Markdown summary of rocprofv3 CSV output directories: kernel stats
     (--kernel-trace --stats) and FETCH_SIZE / WRITE_SIZE (--pmc), the latter
-    per launch and scaled by what the same counter reads for the 1 GiB
-    device copy that copy_bandwidth() runs in the same process."""
+    per launch and scaled by what the same counter reads for the 1 GiB plain
+    copy that plain_copy_bandwidth() runs in the same process."""
     import csv
     import glob
     lines = []
@@ -206,12 +248,13 @@ def rocprof_summary(dirs, workload_kernel="vkfx"):
                 key = (r["Kernel_Name"], r["Counter_Name"])
                 per.setdefault(key, []).append(float(r["Counter_Value"]))
             for (k, c), v in per.items():
-                tag = "fft" if workload_kernel in k else ("copy" if "copyBuffer" in k else None)
-                if tag:
-                    traffic.setdefault(c, {}).setdefault(tag, []).append((k, sum(v) / len(v)))
+                if CALIBRATION_KERNEL in k:
+                    traffic.setdefault(c, {}).setdefault("copy", []).append((k, max(v)))
+                elif workload_kernel in k:
+                    traffic.setdefault(c, {}).setdefault("fft", []).append((k, sum(v) / len(v)))
     if traffic:
         lines.append("### HBM traffic per launch (rocprofv3 --pmc, KiB per dispatch)\n")
-        lines.append("| counter | kernel | raw KiB/launch | copy-kernel raw KiB (1 GiB moved) | scaled bytes/launch |")
+        lines.append("| counter | kernel | raw KiB/launch | plain-copy raw KiB (1 GiB moved) | scaled bytes/launch |")
         lines.append("|---|---|---|---|---|")
         result = {}
         for c, tags in sorted(traffic.items()):
@@ -262,7 +305,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     names = list(CONFIGS) if args.all else [args.config]
-    copy_gbs = None
+    copy_gbs = plain_gbs = None
     for name in names:
         cfg = dict(CONFIGS[name])
         if args.batch:
@@ -272,6 +315,7 @@ def main():
         ms, launch_ms, info = run_gpu(cfg, steps, args.warmup, args.rotate)
         if copy_gbs is None:
             copy_gbs = copy_bandwidth()
+            plain_gbs = plain_copy_bandwidth()
         nbytes, flops = algorithmic(cfg)
         value = nbytes / (ms * 1e-3) / 1e9
         first = info["plans"][0]["passes"]
@@ -283,7 +327,7 @@ def main():
                     "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(cfg["workload"]),
                     "kernel": first[0]["kernel"], "launch_ms": round(launch_ms, 5)}
         out = {
-            "metric": "batched f32 C2C effective HBM GB/s (2*N*batch*bytes/time)",
+            "metric": METRICS[name],
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "f32" if cfg["prec"] == "f32" else "f64", "data": "synthetic uniform[-1,1) (torch, seeded)",
@@ -291,6 +335,7 @@ def main():
                        "buffer_pairs": info["pairs"]},
             "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
             "hbm_copy_gbs": round(copy_gbs, 1),
+            "hbm_plain_copy_gbs": round(plain_gbs, 1),
             "pct_of_copy": round(100 * value / copy_gbs, 2),
             "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
             "roofline": roof,
