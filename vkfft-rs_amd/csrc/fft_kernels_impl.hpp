@@ -379,10 +379,11 @@ struct IoFsABlue : IoFsA {
 
 struct IoFsAC2R : IoFsA {
     static constexpr bool kPtrLoad = false;
+    static constexpr int kLoad = LAY_STAGED;
     // With KF_MIRROR_PAIRS a block owns H = G/2 columns n2 = j*H + g and
     // their mirrors N2 - n2 (column N2/2 stands in for the mirror of column
-    // 0), so the mirror loads X[M - k] of each column fall on the cache lines
-    // its partner column loads in the same block. Needs N2 % G == 0, G even.
+    // 0): X is read once into LDS and each pair (X[k], X[M-k]) is turned into
+    // (Z[k], Z[M-k]) there. Needs N2 % G == 0, G even.
     static __device__ LineInfo line(const KArgs& a, long long blk, int g) {
         if (!(a.flags & KF_MIRROR_PAIRS)) return line_default(a, blk, g);
         const int H = a.G / 2;
@@ -405,6 +406,7 @@ struct IoFsAC2R : IoFsA {
         L.ob = L.o * a.out_os + c * a.out_cs;
         return L;
     }
+    // Z[k] = (X[k] + conj X[M-k]) + i (X[k] - conj X[M-k]) conj(w_k), w_k = exp(-2 pi i k / 2M)
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T>* in = (const cpx<T>*)a.in;
@@ -414,9 +416,52 @@ struct IoFsAC2R : IoFsA {
         cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
         return (X + Xm) + muli<1>(cmulc(X - Xm, w));
     }
+    // Both members of a pair from A = X[k], B = X[M-k]; w_(M-k) = -conj(w_k).
+    template <typename T>
+    static __device__ __forceinline__ void pair(const KArgs& a, long long k, cpx<T>& A, cpx<T>& B) {
+        const cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
+        const cpx<T> zk = (A + conj(B)) + muli<1>(cmulc(A - conj(B), w));
+        const cpx<T> zm = (B + conj(A)) - muli<1>(cmul(B - conj(A), w));
+        A = zk;
+        B = zm;
+    }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
-        staged_load<IoFsAC2R, D>(a, lds, li, false);
+        if (!(a.flags & KF_MIRROR_PAIRS)) {
+            staged_load<IoFsAC2R, D>(a, lds, li, false);
+            return;
+        }
+        staged_load<IoPlain, D>(a, lds, li, false);  // X of the 2H columns, each element once
+        __syncthreads();
+        const int N1 = D::N(a), H = D::G(a) / 2, LS = D::LS(a), PS = D::PS(a);
+        const long long N2 = a.N2;
+        const bool first = li[0].c == 0;  // the block holding columns 0 and N2/2
+        // regular pairs: column c (line g) row e with column N2 - c (line g + H) row N1-1-e
+        for (int idx = threadIdx.x; idx < H * N1; idx += blockDim.x) {
+            const int e = idx / H, g = idx - e * H;
+            if (first && g == 0) continue;
+            cpx<T>& A = lds[g * LS + lpad(e, PS)];
+            cpx<T>& B = lds[(g + H) * LS + lpad(N1 - 1 - e, PS)];
+            pair<T>(a, li[g].c + (long long)e * N2, A, B);
+        }
+        if (first) {
+            // column 0: rows e and N1 - e; row 0 pairs with the Nyquist bin X[M]
+            for (int e = threadIdx.x; e <= N1 / 2; e += blockDim.x) {
+                cpx<T>& A = lds[lpad(e, PS)];
+                if (e == 0) {
+                    cpx<T> B = ((const cpx<T>*)a.in)[li[0].o * a.in_os + a.M];
+                    pair<T>(a, 0, A, B);
+                } else if (2 * e == N1) {
+                    cpx<T> B = A;
+                    pair<T>(a, (long long)e * N2, A, B);
+                } else {
+                    pair<T>(a, (long long)e * N2, A, lds[lpad(N1 - e, PS)]);
+                }
+            }
+            // column N2/2 (line H): rows e and N1-1-e
+            for (int e = threadIdx.x; e < N1 / 2; e += blockDim.x)
+                pair<T>(a, (long long)e * N2 + N2 / 2, lds[H * LS + lpad(e, PS)], lds[H * LS + lpad(N1 - 1 - e, PS)]);
+        }
     }
 };
 
