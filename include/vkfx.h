@@ -137,6 +137,48 @@ int vkfx_execute_host(vkfx_plan *plan, const void *h_in, uint64_t in_bytes, void
  * src/backend/hip/runtime.rs:1530-1608). */
 int vkfx_context_synchronize(vkfx_context *ctx);
 
+/* ------------------------------------------------- async tickets, chains */
+
+typedef struct vkfx_ticket vkfx_ticket;
+
+/* NativeAsyncRuntime::submit_transform_f32/f64_async
+ * (src/backend/native_runtime.rs:406-451): copies h_in into pinned staging,
+ * then queues the upload, the plan and the download on a stream of the
+ * context's pool and returns at once. Each ticket owns its device buffers,
+ * workspace and stream until vkfx_ticket_destroy, so several tickets (of one
+ * plan or of several) may be in flight together (the reference's
+ * multi-submission test, src/backend/hip/runtime.rs:3038-3095). The plan must
+ * outlive its tickets; submit from one thread at a time (the context is
+ * single-owner like HipExecutionContext). */
+int vkfx_submit_host(vkfx_plan *plan, const void *h_in, uint64_t in_bytes, vkfx_ticket **out);
+
+/* *ready = 1 when the ticket's work has finished, 0 otherwise; never blocks. */
+int vkfx_ticket_ready(const vkfx_ticket *ticket, int32_t *ready);
+
+/* Ticket::wait: blocks until the work is done and copies the result into
+ * h_out (out_bytes must equal the plan's output bytes). The ticket stays
+ * valid (wait may be repeated) until destroyed. */
+int vkfx_ticket_wait(vkfx_ticket *ticket, void *h_out, uint64_t out_bytes);
+
+/* Drop of a ticket (src/backend/hip/runtime.rs:1610-1619): synchronises if
+ * the work is still running, then returns its buffers and stream to the
+ * context's pools. */
+int vkfx_ticket_destroy(vkfx_ticket *ticket);
+
+/* Device-resident chain, the HIP counterpart of
+ * CudaExecutionContext::execute_program_chain_complex32
+ * (src/backend/cuda/runtime.rs:1744-1809): plans[i]'s output is plans[i+1]'s
+ * input and stays on the device (pooled ping-pong buffers, reused in stream
+ * order). Each plan's output bytes must equal the next plan's input bytes
+ * (VKFX_ERR_INPUT_LENGTH_MISMATCH otherwise). Asynchronous on `stream`
+ * (NULL = the context's stream); all plans belong to one context. */
+int vkfx_execute_chain(vkfx_plan *const *plans, uint32_t count, const void *d_in, void *d_out, void *stream);
+
+/* execute_program_chain_complex32_into: host input, device-resident chain,
+ * result written straight into h_out; synchronises. */
+int vkfx_execute_chain_host(vkfx_plan *const *plans, uint32_t count, const void *h_in, uint64_t in_bytes,
+                            void *h_out, uint64_t out_bytes);
+
 /* Thread-local message of the last failing call on this thread. */
 const char *vkfx_last_error(void);
 

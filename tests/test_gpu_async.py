@@ -1,0 +1,138 @@
+"""Async tickets and device-resident chains through the C ABI (the HIP side
+of NativeAsyncRuntime, src/backend/native_runtime.rs:406-451, and of the
+resident program chains, src/backend/cuda/runtime.rs:1744-1809).
+
+Results of a ticket or a chain must equal the synchronous execute of the same
+plans bit for bit (same kernels, own buffers), and the oracle within the
+BASELINE tolerances."""
+import numpy as np
+import pytest
+
+import vkfft_amd as vk
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = vk.Precision.F32, vk.Precision.F64
+FWD, INV = vk.Direction.Forward, vk.Direction.Inverse
+
+
+def c2c_ir(dims, batch, prec=F32, direction=FWD, normalize=False):
+    cfg = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec) \
+        .with_inverse_normalization(normalize)
+    return vk.TransformIr.build(cfg, direction)
+
+
+def real_irs(n, batch):
+    r2c = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch)
+                               .with_transform(vk.TransformKind.RealToComplex), FWD)
+    c2r = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch)
+                               .with_transform(vk.TransformKind.ComplexToReal)
+                               .with_inverse_normalization(True), INV)
+    return r2c, c2r
+
+
+def test_tickets_in_flight(hip_ctx):
+    # hip/runtime.rs:3038-3095: several submissions in flight from one thread
+    cases = [(c2c_ir([1024], 64), o.complex_uniform(1024 * 64, 1, np.complex64)),
+             (c2c_ir([1024], 64), o.complex_uniform(1024 * 64, 2, np.complex64)),
+             (c2c_ir([4099], 8), o.complex_uniform(4099 * 8, 3, np.complex64)),
+             (c2c_ir([96, 80], 3, F64), o.complex_uniform(96 * 80 * 3, 4, np.complex128))]
+    tickets = [hip_ctx.submit_transform_async(ir, x) for ir, x in cases]
+    outs = [t.wait() for t in tickets]
+    for (ir, x), y in zip(cases, outs):
+        sync = hip_ctx.execute_transform(ir, x)
+        assert np.array_equal(y, sync)
+        dims = ir.config.dimensions
+        ref = o.fft_nd(x, dims, ir.config.batch_count, threads=8) if len(dims) > 1 else \
+            o.fft_batch(x.astype(np.complex128), dims[0], "forward", False, threads=8)
+        tol = 1e-5 if ir.config.precision == F32 else 1e-13
+        assert o.rel_l2(y, ref) <= tol
+
+
+def test_ticket_ready_and_drop(hip_ctx):
+    ir = c2c_ir([2048], 32)
+    x = o.complex_uniform(2048 * 32, 5, np.complex64)
+    t = hip_ctx.submit_transform_async(ir, x)
+    y = t.wait()
+    assert np.array_equal(y, hip_ctx.execute_transform(ir, x))
+    # a ticket dropped without wait synchronises and returns its buffers
+    t2 = hip_ctx.submit_transform_async(ir, x)
+    t2.close()
+    t3 = hip_ctx.submit_transform_async(ir, x)
+    while not t3.ready():
+        pass
+    assert np.array_equal(t3.wait(), y)
+
+
+def test_tickets_two_lane_plan_isolated(hip_ctx):
+    """A chunked plan (four-step, two stream lanes) in two concurrent tickets:
+    each ticket has its own workspace."""
+    ir = c2c_ir([1 << 20], 64)
+    plan = hip_ctx.plan(ir)
+    assert plan.describe()["lanes"] == 2
+    xa = o.complex_uniform((1 << 20) * 64, 6, np.complex64)
+    xb = o.complex_uniform((1 << 20) * 64, 7, np.complex64)
+    ta = hip_ctx.submit_transform_async(ir, xa)
+    tb = hip_ctx.submit_transform_async(ir, xb)
+    ya, yb = ta.wait(), tb.wait()
+    assert np.array_equal(ya, hip_ctx.execute_transform(ir, xa))
+    assert np.array_equal(yb, hip_ctx.execute_transform(ir, xb))
+    n = 1 << 20
+    for b in (0, 63):
+        ref = o.fft(xb[b * n:(b + 1) * n].astype(np.complex128))
+        assert o.rel_l2(yb[b * n:(b + 1) * n], ref) <= 1e-5
+
+
+def test_real_ticket(hip_ctx):
+    r2c, c2r = real_irs(1 << 14, 6)
+    x = o.normal((1 << 14) * 6, 8, np.float32)
+    t = hip_ctx.submit_transform_async(r2c, x)
+    X = t.wait()
+    assert np.array_equal(X, hip_ctx.execute_transform(r2c, x))
+    h = (1 << 14) // 2 + 1
+    ref = o.r2c_batch(x[: 1 << 14].astype(np.float64), 1 << 14)
+    assert o.rel_l2(X[:h], ref) <= 1e-5
+
+
+def test_chain_host_round_trips(hip_ctx):
+    fwd = c2c_ir([1024], 16)
+    inv = c2c_ir([1024], 16, direction=INV, normalize=True)
+    x = o.complex_uniform(1024 * 16, 9, np.complex64)
+    z = hip_ctx.execute_chain([fwd, inv], x)
+    seq = hip_ctx.execute_transform(inv, hip_ctx.execute_transform(fwd, x))
+    assert np.array_equal(z, seq)
+    assert o.rel_l2(z, x) <= 2e-5
+    r2c, c2r = real_irs(1 << 20, 2)
+    xr = o.normal((1 << 20) * 2, 10, np.float32)
+    zr = hip_ctx.execute_chain([r2c, c2r], xr)
+    assert zr.dtype == np.float32
+    assert o.rel_l2(zr, xr) <= 2e-5
+    # three transforms: fwd, inv, fwd == fwd
+    y3 = hip_ctx.execute_chain([fwd, inv, fwd], x)
+    assert o.rel_l2(y3, hip_ctx.execute_transform(fwd, x)) <= 2e-5
+
+
+def test_chain_device_resident(hip_ctx):
+    import torch
+    fwd = c2c_ir([64, 64], 4, F64)
+    inv = c2c_ir([64, 64], 4, F64, INV, True)
+    x = o.complex_uniform(64 * 64 * 4, 11, np.complex128)
+    dx = torch.from_numpy(x.view(np.float64).copy()).cuda()
+    dy = torch.empty_like(dx)
+    s = torch.cuda.current_stream()
+    vk.execute_chain([hip_ctx.plan(fwd), hip_ctx.plan(inv)], dx.data_ptr(), dy.data_ptr(), s.cuda_stream)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().view(np.complex128)
+    assert o.rel_l2(y, x) <= 1e-13
+
+
+def test_chain_transition_mismatch(hip_ctx):
+    a = c2c_ir([1024], 2)
+    b = c2c_ir([2048], 2)
+    with pytest.raises(vk.VkFftError) as ei:
+        hip_ctx.execute_chain([a, b], o.complex_uniform(2048, 1, np.complex64))
+    assert ei.value.status == -5
+    with pytest.raises(vk.VkFftError) as ei:
+        hip_ctx.execute_chain([a], o.complex_uniform(100, 1, np.complex64))
+    assert ei.value.status == -5

@@ -59,11 +59,22 @@ void root(ld k, ld n, ld& c, ld& s) {
 
 }  // namespace
 
+// Pooled device / pinned host buffer. `ready` (optional) is recorded on the
+// stream of its last user; the next user's stream waits on it, so reuse is
+// stream-ordered.
+struct PoolBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    hipEvent_t ready = nullptr;
+};
+
 struct vkfx_context {
     int device = 0;
     hipStream_t stream = nullptr;
     hipStream_t aux = nullptr;  // second lane for chunked plans (default priority)
     vkfx_device_profile profile{};
+    std::vector<PoolBuf> dev_pool, host_pool;  // free buffers
+    std::vector<hipStream_t> stream_pool;      // free streams for tickets
 };
 
 namespace {
@@ -1181,6 +1192,18 @@ int vkfx_context_destroy(vkfx_context* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamSynchronize(ctx->aux);
+    for (hipStream_t s : ctx->stream_pool) {
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamDestroy(s);
+    }
+    for (PoolBuf& b : ctx->dev_pool) {
+        if (b.ready) (void)hipEventDestroy(b.ready);
+        (void)hipFree(b.p);
+    }
+    for (PoolBuf& b : ctx->host_pool) {
+        if (b.ready) (void)hipEventDestroy(b.ready);
+        (void)hipHostFree(b.p);
+    }
     (void)hipStreamDestroy(ctx->stream);
     (void)hipStreamDestroy(ctx->aux);
     delete ctx;
@@ -1492,3 +1515,236 @@ uint64_t vkfx_planner_next_smooth(uint64_t target) {
 }
 
 }  // extern "C"
+
+// ---- async tickets and device-resident chains -------------------------------
+
+namespace {
+
+// Takes a pooled buffer of exactly `bytes` (device or pinned host), or
+// allocates one. When `s` is given and the buffer carries a release event,
+// s waits on it before the buffer is touched.
+int pool_take(vkfx_context* ctx, bool host, size_t bytes, hipStream_t s, PoolBuf* out) {
+    std::vector<PoolBuf>& pool = host ? ctx->host_pool : ctx->dev_pool;
+    for (size_t i = 0; i < pool.size(); ++i) {
+        if (pool[i].bytes != bytes) continue;
+        *out = pool[i];
+        pool.erase(pool.begin() + (long)i);
+        if (out->ready) {
+            hipError_t e = s ? hipStreamWaitEvent(s, out->ready, 0) : hipEventSynchronize(out->ready);
+            if (e != hipSuccess) return hip_fail(e, "pool buffer wait");
+        }
+        return VKFX_OK;
+    }
+    PoolBuf b;
+    b.bytes = bytes;
+    hipError_t e = host ? hipHostMalloc(&b.p, bytes ? bytes : 16, hipHostMallocDefault)
+                        : hipMalloc(&b.p, bytes ? bytes : 16);
+    if (e != hipSuccess) return hip_fail(e, host ? "hipHostMalloc" : "hipMalloc");
+    *out = b;
+    return VKFX_OK;
+}
+
+// Returns a buffer to its pool; with a stream, its release event is recorded
+// there so the next user waits for the work already queued on it.
+void pool_give(vkfx_context* ctx, bool host, PoolBuf b, hipStream_t s) {
+    if (!b.p) return;
+    if (s) {
+        if (!b.ready && hipEventCreateWithFlags(&b.ready, hipEventDisableTiming) != hipSuccess) b.ready = nullptr;
+        if (b.ready && hipEventRecord(b.ready, s) != hipSuccess) {
+            (void)hipStreamSynchronize(s);
+        }
+        if (!b.ready) (void)hipStreamSynchronize(s);
+    }
+    (host ? ctx->host_pool : ctx->dev_pool).push_back(b);
+}
+
+int chain_check(vkfx_plan* const* plans, uint32_t count) {
+    if (!plans || count == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "resident chain requires at least one plan");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!plans[i]) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan in chain");
+        if (plans[i]->ctx != plans[0]->ctx) return fail(VKFX_ERR_INVALID_ARGUMENT, "chain plans span contexts");
+        if (i + 1 < count && plans[i]->out_bytes != plans[i + 1]->in_bytes)
+            return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH,
+                        "resident chain transition " + std::to_string(i) + ": output " +
+                            std::to_string(plans[i]->out_bytes) + " bytes, next input " +
+                            std::to_string(plans[i + 1]->in_bytes) + " bytes");
+    }
+    return VKFX_OK;
+}
+
+// Runs the chain on s; intermediates come from the device pool and go back
+// with release events recorded on s.
+int chain_run(vkfx_plan* const* plans, uint32_t count, const void* d_in, void* d_out, hipStream_t s) {
+    vkfx_context* ctx = plans[0]->ctx;
+    PoolBuf tmp[2];
+    const void* cur = d_in;
+    int rc = VKFX_OK;
+    for (uint32_t i = 0; i < count && !rc; ++i) {
+        void* dst = d_out;
+        if (i + 1 < count) {
+            PoolBuf& t = tmp[i & 1];
+            if (t.p && t.bytes != plans[i]->out_bytes) {
+                pool_give(ctx, false, t, s);
+                t = PoolBuf();
+            }
+            if (!t.p) rc = pool_take(ctx, false, plans[i]->out_bytes, s, &t);
+            if (rc) break;
+            dst = t.p;
+        }
+        rc = vkfx_execute(plans[i], cur, dst, nullptr, s);
+        cur = dst;
+    }
+    for (PoolBuf& t : tmp) pool_give(ctx, false, t, s);
+    return rc;
+}
+
+}  // namespace
+
+struct vkfx_ticket {
+    vkfx_plan* plan = nullptr;
+    hipStream_t stream = nullptr;
+    hipEvent_t done = nullptr;
+    PoolBuf d_in, d_out, d_work, h_in, h_out;
+};
+
+int vkfx_submit_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, vkfx_ticket** out) {
+    if (!plan || !h_in || !out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (in_bytes != plan->in_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "InputLengthMismatch: expected " + std::to_string(plan->in_bytes) +
+                                                        " bytes, got " + std::to_string(in_bytes));
+    vkfx_context* ctx = plan->ctx;
+    (void)hipSetDevice(ctx->device);
+    auto* t = new vkfx_ticket();
+    t->plan = plan;
+    auto cleanup = [&](int rc) {
+        if (t->stream) (void)hipStreamSynchronize(t->stream);
+        pool_give(ctx, false, t->d_in, nullptr);
+        pool_give(ctx, false, t->d_out, nullptr);
+        pool_give(ctx, false, t->d_work, nullptr);
+        pool_give(ctx, true, t->h_in, nullptr);
+        pool_give(ctx, true, t->h_out, nullptr);
+        if (t->stream) ctx->stream_pool.push_back(t->stream);
+        if (t->done) (void)hipEventDestroy(t->done);
+        delete t;
+        return rc;
+    };
+    hipError_t e = hipSuccess;
+    if (!ctx->stream_pool.empty()) {
+        t->stream = ctx->stream_pool.back();
+        ctx->stream_pool.pop_back();
+    } else {
+        e = hipStreamCreate(&t->stream);  // default priority
+        if (e != hipSuccess) {
+            t->stream = nullptr;
+            return cleanup(hip_fail(e, "hipStreamCreate"));
+        }
+    }
+    e = hipEventCreateWithFlags(&t->done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        t->done = nullptr;
+        return cleanup(hip_fail(e, "hipEventCreate"));
+    }
+    int rc = pool_take(ctx, false, plan->in_bytes, t->stream, &t->d_in);
+    if (!rc) rc = pool_take(ctx, false, plan->out_bytes, t->stream, &t->d_out);
+    if (!rc && plan->work_bytes) rc = pool_take(ctx, false, plan->work_bytes, t->stream, &t->d_work);
+    if (!rc) rc = pool_take(ctx, true, plan->in_bytes, nullptr, &t->h_in);
+    if (!rc) rc = pool_take(ctx, true, plan->out_bytes, nullptr, &t->h_out);
+    if (rc) return cleanup(rc);
+    std::memcpy(t->h_in.p, h_in, in_bytes);
+    e = hipMemcpyAsync(t->d_in.p, t->h_in.p, in_bytes, hipMemcpyHostToDevice, t->stream);
+    if (e != hipSuccess) return cleanup(hip_fail(e, "hipMemcpyAsync(H2D)"));
+    rc = vkfx_execute(plan, t->d_in.p, t->d_out.p, t->d_work.p, t->stream);
+    if (rc) return cleanup(rc);
+    e = hipMemcpyAsync(t->h_out.p, t->d_out.p, plan->out_bytes, hipMemcpyDeviceToHost, t->stream);
+    if (e == hipSuccess) e = hipEventRecord(t->done, t->stream);
+    if (e != hipSuccess) return cleanup(hip_fail(e, "ticket enqueue"));
+    *out = t;
+    return VKFX_OK;
+}
+
+int vkfx_ticket_ready(const vkfx_ticket* t, int32_t* ready) {
+    if (!t || !ready) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    hipError_t e = hipEventQuery(t->done);
+    if (e == hipSuccess) {
+        *ready = 1;
+        return VKFX_OK;
+    }
+    if (e == hipErrorNotReady) {
+        *ready = 0;
+        return VKFX_OK;
+    }
+    return hip_fail(e, "hipEventQuery");
+}
+
+int vkfx_ticket_wait(vkfx_ticket* t, void* h_out, uint64_t out_bytes) {
+    if (!t || !h_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    if (out_bytes != t->plan->out_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "output buffer: expected " + std::to_string(t->plan->out_bytes) +
+                                                        " bytes, got " + std::to_string(out_bytes));
+    hipError_t e = hipEventSynchronize(t->done);
+    if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    std::memcpy(h_out, t->h_out.p, out_bytes);
+    return VKFX_OK;
+}
+
+int vkfx_ticket_destroy(vkfx_ticket* t) {
+    if (!t) return VKFX_OK;
+    vkfx_context* ctx = t->plan->ctx;
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(t->stream);
+    pool_give(ctx, false, t->d_in, nullptr);
+    pool_give(ctx, false, t->d_out, nullptr);
+    pool_give(ctx, false, t->d_work, nullptr);
+    pool_give(ctx, true, t->h_in, nullptr);
+    pool_give(ctx, true, t->h_out, nullptr);
+    ctx->stream_pool.push_back(t->stream);
+    (void)hipEventDestroy(t->done);
+    delete t;
+    return e == hipSuccess ? VKFX_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int vkfx_execute_chain(vkfx_plan* const* plans, uint32_t count, const void* d_in, void* d_out, void* stream) {
+    int rc = chain_check(plans, count);
+    if (rc) return rc;
+    if (!d_in || !d_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null device buffer");
+    vkfx_context* ctx = plans[0]->ctx;
+    (void)hipSetDevice(ctx->device);
+    return chain_run(plans, count, d_in, d_out, stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int vkfx_execute_chain_host(vkfx_plan* const* plans, uint32_t count, const void* h_in, uint64_t in_bytes,
+                            void* h_out, uint64_t out_bytes) {
+    int rc = chain_check(plans, count);
+    if (rc) return rc;
+    if (!h_in || !h_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    if (in_bytes != plans[0]->in_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "InputLengthMismatch: expected " +
+                                                        std::to_string(plans[0]->in_bytes) + " bytes, got " +
+                                                        std::to_string(in_bytes));
+    if (out_bytes != plans[count - 1]->out_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "output buffer: expected " +
+                                                        std::to_string(plans[count - 1]->out_bytes) +
+                                                        " bytes, got " + std::to_string(out_bytes));
+    vkfx_context* ctx = plans[0]->ctx;
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->stream;
+    PoolBuf din, dout;
+    rc = pool_take(ctx, false, in_bytes, s, &din);
+    if (!rc) rc = pool_take(ctx, false, out_bytes, s, &dout);
+    hipError_t e = hipSuccess;
+    if (!rc) {
+        e = hipMemcpyAsync(din.p, h_in, in_bytes, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(H2D)");
+    }
+    if (!rc) rc = chain_run(plans, count, din.p, dout.p, s);
+    if (!rc) {
+        e = hipMemcpyAsync(h_out, dout.p, out_bytes, hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(D2H)");
+    }
+    e = hipStreamSynchronize(s);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    pool_give(ctx, false, din, nullptr);
+    pool_give(ctx, false, dout, nullptr);
+    return rc;
+}

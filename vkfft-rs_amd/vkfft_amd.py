@@ -123,6 +123,12 @@ def lib():
         L.vkfx_planner_bluestein_padding.argtypes = [u64, u64, i32, u64, ctypes.POINTER(u64)]
         L.vkfx_planner_next_smooth.argtypes = [u64]
         L.vkfx_planner_next_smooth.restype = u64
+        L.vkfx_submit_host.argtypes = [vp, vp, u64, ctypes.POINTER(vp)]
+        L.vkfx_ticket_ready.argtypes = [vp, ctypes.POINTER(i32)]
+        L.vkfx_ticket_wait.argtypes = [vp, vp, u64]
+        L.vkfx_ticket_destroy.argtypes = [vp]
+        L.vkfx_execute_chain.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, vp, vp]
+        L.vkfx_execute_chain_host.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, u64, vp, u64]
         _lib = L
     return _lib
 
@@ -320,6 +326,53 @@ class Plan:
             pass
 
 
+class TransformTicket:
+    """NativeAsyncTransformTicket32/64 (native_runtime.rs:372-401): a submitted
+    transform; `wait()` returns the output and releases the ticket."""
+
+    def __init__(self, plan: "Plan", x: np.ndarray, out_dtype, out_count: int):
+        self.plan = plan
+        self._x = x  # kept alive until the submit has copied it
+        self._out = np.empty(out_count, dtype=out_dtype)
+        self.handle = ctypes.c_void_p()
+        _check(lib().vkfx_submit_host(plan.handle, x.ctypes.data, x.nbytes, ctypes.byref(self.handle)))
+
+    def ready(self) -> bool:
+        r = ctypes.c_int32()
+        _check(lib().vkfx_ticket_ready(self.handle, ctypes.byref(r)))
+        return bool(r.value)
+
+    def wait(self) -> np.ndarray:
+        _check(lib().vkfx_ticket_wait(self.handle, self._out.ctypes.data, self._out.nbytes))
+        self.close()
+        return self._out
+
+    def close(self):
+        if self.handle:
+            lib().vkfx_ticket_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _plan_array(plans):
+    arr = (ctypes.c_void_p * len(plans))()
+    for i, p in enumerate(plans):
+        arr[i] = p.handle
+    return arr
+
+
+def execute_chain(plans, d_in: int, d_out: int, stream: int = 0):
+    """Device-resident chain (cuda/runtime.rs:1744-1809): plans[i]'s output feeds
+    plans[i+1] on the device; raw device pointers, asynchronous on `stream`."""
+    _check(lib().vkfx_execute_chain(_plan_array(plans), len(plans), ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
+                                    ctypes.c_void_p(stream or None)))
+
+
 class HipExecutionContext:
     """`HipExecutionContext::new(device_index)` over the C ABI."""
 
@@ -361,6 +414,34 @@ class HipExecutionContext:
         if kind == TransformKind.ComplexToReal:
             return self._execute_host(ir, x, ir.complex_dtype, ir.real_dtype, ir.output_count())
         return self._execute_host(ir, x, ir.complex_dtype, ir.complex_dtype, ir.output_count())
+
+    def _io_dtypes(self, ir: TransformIr):
+        kind = ir.config.transform
+        if kind == TransformKind.RealToComplex:
+            return ir.real_dtype, ir.complex_dtype
+        if kind == TransformKind.ComplexToReal:
+            return ir.complex_dtype, ir.real_dtype
+        return ir.complex_dtype, ir.complex_dtype
+
+    def submit_transform_async(self, ir: TransformIr, x: np.ndarray) -> TransformTicket:
+        """NativeAsyncRuntime::submit_transform_f32/f64_async (native_runtime.rs:406-451)."""
+        in_dt, out_dt = self._io_dtypes(ir)
+        x = np.ascontiguousarray(x, dtype=in_dt).reshape(-1)
+        if x.size != ir.input_count():
+            raise VkFftError(-5, f"InputLengthMismatch {{ expected: {ir.input_count()}, actual: {x.size} }}")
+        return TransformTicket(self.plan(ir), x, out_dt, ir.output_count())
+
+    def execute_chain(self, irs, x: np.ndarray) -> np.ndarray:
+        """execute_program_chain_complex32_into (cuda/runtime.rs:1765-1809): host input,
+        the transforms run back to back on the device, one download."""
+        plans = [self.plan(ir) for ir in irs]
+        in_dt, _ = self._io_dtypes(irs[0])
+        _, out_dt = self._io_dtypes(irs[-1])
+        x = np.ascontiguousarray(x, dtype=in_dt).reshape(-1)
+        out = np.empty(irs[-1].output_count(), dtype=out_dt)
+        _check(lib().vkfx_execute_chain_host(_plan_array(plans), len(plans), x.ctypes.data, x.nbytes,
+                                             out.ctypes.data, out.nbytes))
+        return out
 
     def execute_transform_f32(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
         if ir.config.precision != Precision.F32:
