@@ -1,0 +1,210 @@
+"""Bit-exact addressing: the index-map test build of the library
+(libvkfft_mi355x_index.so, identity butterflies / twiddles / chirps /
+spectra / scale) against the CPU index maps of oracle/index_maps.py.
+
+Inputs are integer-tagged (exact in f32 and f64), so every output element
+must equal the input element the maps name, bit for bit: this checks the
+direct HBM stages, LDS slot arithmetic, line mappings (rows, columns, split
+axes, chunks, stream lanes), four-step transposes and Bluestein padding /
+truncation of every C2C kernel family. Real-to-complex and Rader kernels do
+arithmetic besides moving data and are checked numerically elsewhere."""
+import os
+
+import numpy as np
+import pytest
+
+import vkfft_amd as vk
+from oracle import index_maps as im
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = vk.Precision.F32, vk.Precision.F64
+FWD, INV = vk.Direction.Forward, vk.Direction.Inverse
+
+
+@pytest.fixture(scope="module")
+def idx_ctx():
+    if not os.path.exists("/dev/kfd"):
+        pytest.skip("no GPU in this container")
+    import torch
+    torch.cuda.init()
+    ctx = vk.HipExecutionContext(0, library=vk.INDEX_LIB_PATH)
+    assert b"index-map test build" in ctx._L.vkfx_version()
+    yield ctx
+    ctx.close()
+
+
+def tagged(count, prec):
+    k = np.arange(count, dtype=np.float64)
+    x = (k + 1) - 1j * ((k % 65521) + 0.5)
+    return x.astype(np.complex64 if prec == F32 else np.complex128)
+
+
+def run(ctx, dims, batch, prec, direction, x, env=None):
+    """Fresh plan (plans read the chunk budgets when built), host round trip."""
+    old = {}
+    for k, v in (env or {}).items():
+        old[k] = os.environ.get(k)
+        os.environ[k] = v
+    try:
+        cfg = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec)
+        ir = vk.TransformIr.build(cfg, direction)
+        plan = vk.Plan(ctx, ir)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    out = np.empty(ir.output_count(), dtype=x.dtype)
+    vk._check(ctx._L.vkfx_execute_host(plan.handle, x.ctypes.data, x.nbytes, out.ctypes.data, out.nbytes), ctx._L)
+    desc = plan.describe()
+    plan.close()
+    return out, desc
+
+
+def first_passes(desc):
+    """Passes of the first chunk, in launch order (labels repeat per chunk)."""
+    seen, out = set(), []
+    for p in desc["passes"]:
+        if p["kernel"] in seen and p["kernel"] not in ("stockham_rows", "stockham_columns", "split_axis_pass1",
+                                                        "split_axis_pass2", "bluestein_axis"):
+            break
+        seen.add(p["kernel"])
+        out.append(p)
+    return out
+
+
+def line_map_1d(n, desc):
+    ps = first_passes(desc)
+    names = [p["kernel"] for p in ps]
+    if names[0] == "stockham":
+        return im.stockham_perm(n, ps[0]["radices"])
+    if names[:2] == ["four_step_columns", "four_step_rows"]:
+        a, b = ps[0], ps[1]
+        return im.four_step_perm(a["fft_len"], a["radices"], b["fft_len"], b["radices"])
+    if names[0] == "bluestein_single":
+        return im.bluestein_single_perm(n, ps[0]["fft_len"], ps[0]["radices"])
+    if names[:3] == ["bluestein_columns", "bluestein_rows", "bluestein_columns_out"]:
+        a, b, c = ps[:3]
+        return im.bluestein_three_pass_perm(n, a["fft_len"], a["radices"], b["fft_len"], b["radices"],
+                                            c["radices"])
+    raise AssertionError(f"unmodelled pass list {names}")
+
+
+def check_1d(ctx, n, batch, prec, direction=FWD, env=None):
+    x = tagged(n * batch, prec)
+    out, desc = run(ctx, [n], batch, prec, direction, x, env)
+    src = line_map_1d(n, desc)
+    expect = im.gather(x, src, n, batch, n)
+    assert np.array_equal(out, expect), (n, batch, [p["kernel"] for p in desc["passes"][:4]])
+    return desc
+
+
+SINGLE = [2, 3, 5, 7, 8, 11, 13, 16, 18, 25, 27, 32, 36, 49, 60, 64, 96, 100, 121, 125, 128, 169, 243,
+          343, 360, 512, 625, 1000, 1024, 1536, 2048, 2187, 2401, 3125, 4096, 6561, 8192, 10000, 15625, 16384]
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_single_upload_lengths(idx_ctx, prec):
+    for n in SINGLE:
+        check_1d(idx_ctx, n, 3, prec)
+        check_1d(idx_ctx, n, 2, prec, INV)
+
+
+def test_config_shapes_1d(idx_ctx):
+    d = check_1d(idx_ctx, 1024, 64, F32)          # C1 kernel (fixed, two waves per line)
+    assert d["passes"][0]["fixed_shape"]
+    check_1d(idx_ctx, 1024, 33, F32, INV)
+    check_1d(idx_ctx, 4096, 5, F32)
+    check_1d(idx_ctx, 512, 9, F64)
+
+
+@pytest.mark.parametrize("n,batch,prec", [(1 << 20, 2, F32), (1 << 17, 3, F32), (3 ** 12, 1, F32),
+                                          (1 << 18, 2, F64), (5 ** 8, 1, F64)])
+def test_four_step(idx_ctx, n, batch, prec):
+    d = check_1d(idx_ctx, n, batch, prec)
+    assert [p["kernel"] for p in d["passes"][:2]] == ["four_step_columns", "four_step_rows"]
+    check_1d(idx_ctx, n, batch, prec, INV)
+
+
+def test_four_step_chunks_and_lanes(idx_ctx):
+    """Many small chunks on two stream lanes: offsets of every chunk."""
+    d = check_1d(idx_ctx, 1 << 18, 12, F32, env={"VKFX_WORK_BUDGET_MB": "4"})
+    assert d["lanes"] == 2
+    assert len(d["passes"]) == 2 * 6
+
+
+@pytest.mark.parametrize("n,prec", [(4099, F32), (65537, F32), (12289, F64), (20011, F32)])
+def test_bluestein(idx_ctx, n, prec):
+    alg, _ = vk.planner_axis(n, 4, prec)
+    if alg != vk.AlgorithmKind.Bluestein:
+        pytest.skip(f"N={n} plans as {alg.name}")
+    check_1d(idx_ctx, n, 4, prec)
+    check_1d(idx_ctx, n, 3, prec, INV)
+
+
+ND = [([64, 48], 2, F32), ([256, 256], 2, F32), ([8, 4096], 2, F32), ([4096, 8], 1, F32), ([1024, 6], 2, F32),
+      ([512, 8], 2, F64), ([8, 512], 2, F64), ([16, 12, 10], 2, F64), ([6, 20, 64, 40], 1, F32),
+      ([64, 64, 64], 1, F64), ([3, 768, 5], 2, F32), ([4099, 4], 1, F32)]
+
+
+def nd_axis_maps(dims, desc):
+    """Per-axis line maps from the pass list: axes run last to first, one pass
+    each, two for a split strided axis."""
+    passes = desc["passes"]
+    maps = [None] * len(dims)
+    i = 0
+    for ax in range(len(dims) - 1, -1, -1):
+        n = dims[ax]
+        if n == 1:
+            continue
+        p = passes[i]
+        if p["kernel"] in ("stockham_rows", "stockham_columns"):
+            maps[ax] = im.stockham_perm(n, p["radices"])
+            i += 1
+        elif p["kernel"] == "split_axis_pass1":
+            q = passes[i + 1]
+            maps[ax] = im.four_step_perm(p["fft_len"], p["radices"], q["fft_len"], q["radices"])
+            i += 2
+        elif p["kernel"] == "bluestein_axis":
+            src = im.bluestein_single_perm(n, p["fft_len"], p["radices"])
+            maps[ax] = src
+            i += 1
+        else:
+            raise AssertionError(f"unmodelled pass {p['kernel']}")
+    return maps
+
+
+@pytest.mark.parametrize("dims,batch,prec", ND)
+def test_nd(idx_ctx, dims, batch, prec):
+    count = int(np.prod(dims)) * batch
+    x = tagged(count, prec)
+    out, desc = run(idx_ctx, dims, batch, prec, FWD, x)
+    maps = nd_axis_maps(dims, desc)
+    v = x.reshape((batch,) + tuple(dims))
+    for ax, src in enumerate(maps):
+        if src is None:
+            continue
+        safe = np.where(src >= 0, src, 0)
+        v = np.take(v, safe, axis=ax + 1)
+        if (src < 0).any():
+            idx = [slice(None)] * v.ndim
+            idx[ax + 1] = np.nonzero(src < 0)[0]
+            v[tuple(idx)] = 0
+    assert np.array_equal(out, v.reshape(-1)), (dims, batch, [p["kernel"] for p in desc["passes"]])
+
+
+def test_nd_slab_chunks(idx_ctx):
+    """Slab-chunked volume (axes 1.. per slab chunk, axis 0 last)."""
+    dims, batch = [32, 64, 48], 2
+    x = tagged(int(np.prod(dims)) * batch, F64)
+    out, desc = run(idx_ctx, dims, batch, F64, FWD, x, env={"VKFX_ND_CHUNK_MB": "1"})
+    assert desc["nd"]["slabs_per_chunk"] > 0
+    rad = {}
+    for p in desc["passes"]:
+        rad.setdefault(p["fft_len"], p["radices"])
+    v = x.reshape((batch,) + tuple(dims))
+    for ax, n in enumerate(dims):
+        v = np.take(v, im.stockham_perm(n, rad[n]), axis=ax + 1)
+    assert np.array_equal(out, v.reshape(-1))

@@ -1,0 +1,77 @@
+"""Pins of the CPU index maps (oracle/index_maps.py) used by the bit-exact
+GPU addressing tests: closed forms (digit reversal), and the same maps with
+real butterflies and twiddles reproducing numpy.fft (pocketfft)."""
+import numpy as np
+import pytest
+
+from oracle import index_maps as im
+
+
+def digit_reversal(radices):
+    """Mixed-radix digit reversal: i = d0 + r0*(d1 + r1*(d2 + ...)) maps to
+    the number whose most significant digit is d0."""
+    out = []
+    for i in range(int(np.prod(radices))):
+        t, v = i, 0
+        for r in radices:
+            v = v * r + t % r
+            t //= r
+        out.append(v)
+    return np.array(out)
+
+
+@pytest.mark.parametrize("radices", [[2] * 9, [16, 8, 8], [8, 3, 7, 7, 7], [9, 9, 5], [4, 9, 9], [3, 5, 7],
+                                     [16, 16, 16], [13, 11, 2]])
+def test_identity_stockham_is_digit_reversal(radices):
+    n = int(np.prod(radices))
+    p = im.stockham_perm(n, radices)
+    assert np.array_equal(p, digit_reversal(radices))
+    assert np.array_equal(np.sort(p), np.arange(n))
+
+
+@pytest.mark.parametrize("radices", [[16, 8, 8], [8, 3, 7, 7, 7], [9, 9, 5], [4, 9, 9], [16, 16, 4], [7, 11, 13],
+                                     [2, 2, 2, 3]])
+def test_stage_maps_compute_the_dft(radices):
+    n = int(np.prod(radices))
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+    np.testing.assert_allclose(im.stockham_fft(x, radices), np.fft.fft(x), rtol=0, atol=1e-9 * np.sqrt(n))
+    np.testing.assert_allclose(im.stockham_fft(x, radices, +1), np.fft.ifft(x) * n, rtol=0, atol=1e-9 * np.sqrt(n))
+
+
+@pytest.mark.parametrize("n1,rad1,n2,rad2", [(16, [4, 4], 8, [8]), (27, [3, 9], 20, [4, 5]), (64, [8, 8], 64, [8, 8])])
+def test_four_step_map_computes_the_dft(n1, rad1, n2, rad2):
+    """Four-step with real math on the same placement as four_step_perm:
+    column FFTs over n1, twiddle exp(-2 pi i k1 n2 / M), row FFTs over n2,
+    output at k1 + n1*k2."""
+    m = n1 * n2
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal(m) + 1j * rng.standard_normal(m)
+    w = x.reshape(n1, n2).astype(np.complex128)
+    cols = np.stack([im.stockham_fft(w[:, c], rad1) for c in range(n2)], axis=1)
+    k1 = np.arange(n1)[:, None]
+    c = np.arange(n2)[None, :]
+    cols = cols * np.exp(-2j * np.pi * k1 * c / m)
+    out = np.empty(m, dtype=np.complex128)
+    for r in range(n1):
+        out[r + n1 * np.arange(n2)] = im.stockham_fft(cols[r], rad2)
+    np.testing.assert_allclose(out, np.fft.fft(x), rtol=0, atol=1e-9 * np.sqrt(m))
+    # and the identity-butterfly placement is the permutation four_step_perm describes
+    src = im.four_step_perm(n1, rad1, n2, rad2)
+    sa, sb = im.stockham_perm(n1, rad1), im.stockham_perm(n2, rad2)
+    for kk1 in range(n1):
+        for kk2 in range(n2):
+            assert src[kk1 + n1 * kk2] == sa[kk1] * n2 + sb[kk2]
+
+
+def test_bluestein_maps_zero_fill_and_truncate():
+    n, m = 11, 24
+    src = im.bluestein_single_perm(n, m, [2, 3, 4])
+    assert src.shape == (n,)
+    s = im.stockham_perm(m, [2, 3, 4])
+    for k in range(n):
+        v = s[s[k]]
+        assert src[k] == (v if v < n else -1)
+    src3 = im.bluestein_three_pass_perm(n, 6, [2, 3], 4, [4], [3, 2])
+    assert src3.shape == (n,)
+    assert ((src3 >= -1) & (src3 < n)).all()

@@ -15,6 +15,17 @@
 
 namespace vkfx {
 
+// Index-map test build (make VARIANT=index, -DVKFX_INDEX_TEST): every
+// butterfly, twiddle, chirp, spectrum and scale multiplication is the
+// identity, so a C2C kernel only moves data and its output is a permutation
+// (plus the zero fill of Bluestein padding) of its input, compared bit for
+// bit with the CPU index maps.
+#ifdef VKFX_INDEX_TEST
+constexpr bool kIndexTest = true;
+#else
+constexpr bool kIndexTest = false;
+#endif
+
 template <typename T>
 struct alignas(2 * sizeof(T)) cpx {
     T re, im;
@@ -37,11 +48,13 @@ __device__ __forceinline__ cpx<T> operator-(cpx<T> a, cpx<T> b) {
 }
 template <typename T>
 __device__ __forceinline__ cpx<T> cmul(cpx<T> a, cpx<T> b) {
+    if constexpr (kIndexTest) return a;
     return mk(a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re);
 }
 // a * conj(b)
 template <typename T>
 __device__ __forceinline__ cpx<T> cmulc(cpx<T> a, cpx<T> b) {
+    if constexpr (kIndexTest) return a;
     return mk(a.re * b.re + a.im * b.im, a.im * b.re - a.re * b.im);
 }
 template <typename T>
@@ -50,6 +63,7 @@ __device__ __forceinline__ cpx<T> conj(cpx<T> a) {
 }
 template <typename T>
 __device__ __forceinline__ cpx<T> scale(cpx<T> a, T s) {
+    if constexpr (kIndexTest) return a;
     return mk(a.re * s, a.im * s);
 }
 // (S * i) * a, S = +-1
@@ -257,7 +271,9 @@ __device__ __forceinline__ void dft_composite(cpx<T>* x) {
 
 template <int R, int S, typename T>
 __device__ __forceinline__ void dft(cpx<T>* x) {
-    if constexpr (R == 2) {
+    if constexpr (kIndexTest) {
+        return;
+    } else if constexpr (R == 2) {
         dft2<S>(x);
     } else if constexpr (R == 4) {
         dft4<S>(x[0], x[1], x[2], x[3]);

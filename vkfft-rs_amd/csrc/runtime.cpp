@@ -1141,7 +1141,11 @@ extern "C" {
 
 const char* vkfx_last_error(void) { return g_err.c_str(); }
 
+#ifdef VKFX_INDEX_TEST
+const char* vkfx_version(void) { return "vkfx-mi355x 0.1.0 (gfx950, index-map test build)"; }
+#else
 const char* vkfx_version(void) { return "vkfx-mi355x 0.1.0 (gfx950)"; }
+#endif
 
 int vkfx_context_create(int device_index, vkfx_context** out) {
     if (!out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output pointer");

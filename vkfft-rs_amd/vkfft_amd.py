@@ -21,10 +21,12 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvkfft_mi355x.so")
+# index-map test build (identity arithmetic): tests only
+INDEX_LIB_PATH = os.path.join(_HERE, "libvkfft_mi355x_index.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "vkfx.h")
 MAX_RANK = 4
 
-_lib = None
+_libs = {}
 
 
 class VkFftError(RuntimeError):
@@ -98,13 +100,14 @@ class _Profile(ctypes.Structure):
     ]
 
 
-def lib():
-    """Loads libvkfft_mi355x.so; raises if it has not been built."""
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise VkFftError(-1, f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
-        L = ctypes.CDLL(LIB_PATH)
+def lib(path: Optional[str] = None):
+    """Loads libvkfft_mi355x.so (or the library at `path`, e.g. the index-map
+    test build INDEX_LIB_PATH); raises if it has not been built."""
+    path = path or LIB_PATH
+    if path not in _libs:
+        if not os.path.exists(path):
+            raise VkFftError(-1, f"{path} is missing: build it with __graft_entry__.build()")
+        L = ctypes.CDLL(path)
         vp, u64, i32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32
         L.vkfx_last_error.restype = ctypes.c_char_p
         L.vkfx_version.restype = ctypes.c_char_p
@@ -129,13 +132,13 @@ def lib():
         L.vkfx_ticket_destroy.argtypes = [vp]
         L.vkfx_execute_chain.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, vp, vp]
         L.vkfx_execute_chain_host.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, u64, vp, u64]
-        _lib = L
-    return _lib
+        _libs[path] = L
+    return _libs[path]
 
 
-def _check(rc: int):
+def _check(rc: int, L=None):
     if rc != 0:
-        raise VkFftError(rc, lib().vkfx_last_error().decode(errors="replace"))
+        raise VkFftError(rc, (L or lib()).vkfx_last_error().decode(errors="replace"))
 
 
 def header_symbols() -> List[str]:
@@ -285,25 +288,26 @@ class Plan:
 
     def __init__(self, ctx: "HipExecutionContext", ir: TransformIr):
         self.ctx = ctx
+        self._L = ctx._L
         self.ir = ir
         self.handle = ctypes.c_void_p()
         d = ir.desc()
-        _check(lib().vkfx_plan_create(ctx.handle, ctypes.byref(d), ctypes.byref(self.handle)))
+        _check(self._L.vkfx_plan_create(ctx.handle, ctypes.byref(d), ctypes.byref(self.handle)), self._L)
         i, o, w = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
-        _check(lib().vkfx_plan_io_bytes(self.handle, ctypes.byref(i), ctypes.byref(o)))
-        _check(lib().vkfx_plan_workspace_bytes(self.handle, ctypes.byref(w)))
+        _check(self._L.vkfx_plan_io_bytes(self.handle, ctypes.byref(i), ctypes.byref(o)), self._L)
+        _check(self._L.vkfx_plan_workspace_bytes(self.handle, ctypes.byref(w)), self._L)
         self.in_bytes, self.out_bytes, self.workspace_bytes = int(i.value), int(o.value), int(w.value)
 
     def describe(self) -> dict:
-        n = lib().vkfx_plan_describe(self.handle, None, 0)
+        n = self._L.vkfx_plan_describe(self.handle, None, 0)
         buf = ctypes.create_string_buffer(n + 1)
-        lib().vkfx_plan_describe(self.handle, buf, n + 1)
+        self._L.vkfx_plan_describe(self.handle, buf, n + 1)
         return json.loads(buf.value.decode())
 
     def execute(self, d_in: int, d_out: int, d_work: int = 0, stream: int = 0):
         """Device-resident asynchronous execute (raw device pointers)."""
-        _check(lib().vkfx_execute(self.handle, ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
-                                  ctypes.c_void_p(d_work or None), ctypes.c_void_p(stream or None)))
+        _check(self._L.vkfx_execute(self.handle, ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
+                                  ctypes.c_void_p(d_work or None), ctypes.c_void_p(stream or None)), self._L)
 
     def execute_tensors(self, x, y, stream=None):
         """Execute on torch tensors already resident on the GPU."""
@@ -316,7 +320,7 @@ class Plan:
 
     def close(self):
         if self.handle:
-            lib().vkfx_plan_destroy(self.handle)
+            self._L.vkfx_plan_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
     def __del__(self):
@@ -332,24 +336,25 @@ class TransformTicket:
 
     def __init__(self, plan: "Plan", x: np.ndarray, out_dtype, out_count: int):
         self.plan = plan
+        self._L = plan._L
         self._x = x  # kept alive until the submit has copied it
         self._out = np.empty(out_count, dtype=out_dtype)
         self.handle = ctypes.c_void_p()
-        _check(lib().vkfx_submit_host(plan.handle, x.ctypes.data, x.nbytes, ctypes.byref(self.handle)))
+        _check(self._L.vkfx_submit_host(plan.handle, x.ctypes.data, x.nbytes, ctypes.byref(self.handle)), self._L)
 
     def ready(self) -> bool:
         r = ctypes.c_int32()
-        _check(lib().vkfx_ticket_ready(self.handle, ctypes.byref(r)))
+        _check(self._L.vkfx_ticket_ready(self.handle, ctypes.byref(r)), self._L)
         return bool(r.value)
 
     def wait(self) -> np.ndarray:
-        _check(lib().vkfx_ticket_wait(self.handle, self._out.ctypes.data, self._out.nbytes))
+        _check(self._L.vkfx_ticket_wait(self.handle, self._out.ctypes.data, self._out.nbytes), self._L)
         self.close()
         return self._out
 
     def close(self):
         if self.handle:
-            lib().vkfx_ticket_destroy(self.handle)
+            self._L.vkfx_ticket_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
     def __del__(self):
@@ -369,21 +374,25 @@ def _plan_array(plans):
 def execute_chain(plans, d_in: int, d_out: int, stream: int = 0):
     """Device-resident chain (cuda/runtime.rs:1744-1809): plans[i]'s output feeds
     plans[i+1] on the device; raw device pointers, asynchronous on `stream`."""
-    _check(lib().vkfx_execute_chain(_plan_array(plans), len(plans), ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
-                                    ctypes.c_void_p(stream or None)))
+    L = plans[0]._L
+    _check(L.vkfx_execute_chain(_plan_array(plans), len(plans), ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
+                                ctypes.c_void_p(stream or None)), L)
 
 
 class HipExecutionContext:
-    """`HipExecutionContext::new(device_index)` over the C ABI."""
+    """`HipExecutionContext::new(device_index)` over the C ABI. `library`
+    selects another build of the library (INDEX_LIB_PATH for the index-map
+    tests); the default is the product library."""
 
-    def __init__(self, device_index: int = 0):
+    def __init__(self, device_index: int = 0, library: Optional[str] = None):
+        self._L = lib(library)
         self.handle = ctypes.c_void_p()
-        _check(lib().vkfx_context_create(device_index, ctypes.byref(self.handle)))
+        _check(self._L.vkfx_context_create(device_index, ctypes.byref(self.handle)), self._L)
         self._plans = {}
 
     def device_profile(self) -> dict:
         p = _Profile()
-        _check(lib().vkfx_context_profile(self.handle, ctypes.byref(p)))
+        _check(self._L.vkfx_context_profile(self.handle, ctypes.byref(p)), self._L)
         return {k: (getattr(p, k).decode() if isinstance(getattr(p, k), bytes) else int(getattr(p, k)))
                 for k, _ in _Profile._fields_}
 
@@ -404,7 +413,7 @@ class HipExecutionContext:
             raise VkFftError(-5, f"InputLengthMismatch {{ expected: {ir.input_count()}, actual: {x.size} }}")
         plan = self.plan(ir)
         out = np.empty(out_count, dtype=out_dtype)
-        _check(lib().vkfx_execute_host(plan.handle, x.ctypes.data, x.nbytes, out.ctypes.data, out.nbytes))
+        _check(self._L.vkfx_execute_host(plan.handle, x.ctypes.data, x.nbytes, out.ctypes.data, out.nbytes), self._L)
         return out
 
     def execute_transform(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
@@ -439,8 +448,8 @@ class HipExecutionContext:
         _, out_dt = self._io_dtypes(irs[-1])
         x = np.ascontiguousarray(x, dtype=in_dt).reshape(-1)
         out = np.empty(irs[-1].output_count(), dtype=out_dt)
-        _check(lib().vkfx_execute_chain_host(_plan_array(plans), len(plans), x.ctypes.data, x.nbytes,
-                                             out.ctypes.data, out.nbytes))
+        _check(self._L.vkfx_execute_chain_host(_plan_array(plans), len(plans), x.ctypes.data, x.nbytes,
+                                             out.ctypes.data, out.nbytes), self._L)
         return out
 
     def execute_transform_f32(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
@@ -454,14 +463,14 @@ class HipExecutionContext:
         return self.execute_transform(ir, x)
 
     def synchronize(self):
-        _check(lib().vkfx_context_synchronize(self.handle))
+        _check(self._L.vkfx_context_synchronize(self.handle), self._L)
 
     def close(self):
         for p in self._plans.values():
             p.close()
         self._plans.clear()
         if self.handle:
-            lib().vkfx_context_destroy(self.handle)
+            self._L.vkfx_context_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
     def __del__(self):
