@@ -44,7 +44,15 @@ enum vkfx_status {
 };
 
 enum vkfx_transform { VKFX_C2C = 0, VKFX_R2C = 1, VKFX_C2R = 2 }; /* TransformKind, config.rs */
-enum vkfx_precision { VKFX_F32 = 0, VKFX_F64 = 1 };              /* Precision::{F32,F64} */
+/* Precision (src/config.rs:108-145). The caller's buffers hold the storage
+ * type; the FFT passes run on the compute type. Mixed layouts convert on the
+ * device into and out of the plan's workspace. */
+enum vkfx_precision {
+    VKFX_F32 = 0,                     /* Precision::F32 */
+    VKFX_F64 = 1,                     /* Precision::F64 */
+    VKFX_F16_STORAGE_F32_COMPUTE = 2, /* Precision::F16StorageF32Compute: binary16 buffers */
+    VKFX_F64_COMPUTE_F32_STORAGE = 3  /* Precision::F64ComputeF32Storage: f32 buffers */
+};
 enum vkfx_direction { VKFX_FORWARD = -1, VKFX_INVERSE = 1 };     /* Direction::exponent_sign */
 enum vkfx_algorithm {                                            /* AxisAlgorithm, planner.rs:46-59 */
     VKFX_ALG_STOCKHAM = 0,

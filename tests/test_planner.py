@@ -1,5 +1,6 @@
 """Planner restatement (vkfft-rs_amd/csrc/planner.cpp) pinned against values
 the reference asserts or that follow from its tables, called through the C ABI."""
+import numpy as np
 import pytest
 
 import vkfft_amd as vk
@@ -74,3 +75,33 @@ def test_f64_rader_limit_follows_lds_capacity():
 def test_next_smooth_matches_oracle():
     for t in [1, 2, 7, 11, 2061, 8197, 131073, 99991]:
         assert vk.next_smooth_at_least(t) == o.next_smooth_at_least(t)
+
+
+def test_mixed_precisions_plan_like_their_compute_type():
+    """PlannerTuning::for_device (config.rs:411-417) and the LUT rule
+    (scheduler.rs:231-239) treat F64ComputeF32Storage as F64 and
+    F16StorageF32Compute as F32."""
+    F32, F64 = vk.Precision.F32, vk.Precision.F64
+    F16S, F64C = vk.Precision.F16StorageF32Compute, vk.Precision.F64ComputeF32Storage
+    for n in (4099, 65537, 1000, 1009, 12289, 23, 31):
+        assert vk.planner_axis(n, 4, F64C) == vk.planner_axis(n, 4, F64)
+        assert vk.planner_axis(n, 4, F16S) == vk.planner_axis(n, 4, F32)
+    for n in (1000, 4099, 65537):
+        assert vk.bluestein_padding(n, 1, F64C) == vk.bluestein_padding(n, 1, F64)
+        assert vk.bluestein_padding(n, 1, F16S) == vk.bluestein_padding(n, 1, F32)
+
+
+def test_mixed_precision_host_storage_conversion():
+    ir = vk.TransformIr.build(vk.FftConfig.new([8]).with_precision(vk.Precision.F16StorageF32Compute),
+                              vk.Direction.Forward)
+    assert ir.complex_dtype == np.complex64 and ir.storage_scalar_dtype == np.float16
+    x = (np.arange(8) / 3 + 1j * np.arange(8) / 7).astype(np.complex64)
+    s = ir.to_storage(x)
+    assert s.dtype == np.float16 and s.size == 16
+    back = ir.from_storage(s, True)
+    assert back.dtype == np.complex64
+    np.testing.assert_array_equal(back.view(np.float32), x.view(np.float32).astype(np.float16).astype(np.float32))
+    ir64 = vk.TransformIr.build(vk.FftConfig.new([8]).with_precision(vk.Precision.F64ComputeF32Storage),
+                                vk.Direction.Forward)
+    assert ir64.complex_dtype == np.complex64 and ir64.storage_scalar_dtype == np.float32
+    assert ir64.to_storage(x) is x

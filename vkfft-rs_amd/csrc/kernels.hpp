@@ -112,4 +112,8 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
 // Largest dynamic LDS a block may request on this device (bytes).
 size_t max_lds_bytes();
 
+// Converts n scalars between storage and compute types (0 = binary16,
+// 1 = f32, 2 = f64) on stream s. Returns a hipError_t value.
+int launch_convert(int src, int dst, const void* in, void* out, long long n, hipStream_t s);
+
 }  // namespace vkfx

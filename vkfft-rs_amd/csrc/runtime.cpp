@@ -79,7 +79,11 @@ struct vkfx_context {
 
 namespace {
 
-enum BufSel : int { SEL_IN = 0, SEL_OUT = 1, SEL_WORK = 2 };
+// Buffers a launch reads or writes: the caller's input and output, the
+// plan's workspace (per stream lane) and, for mixed storage/compute
+// precisions, the compute-type copies of the input and output in the
+// workspace.
+enum BufSel : int { SEL_IN = 0, SEL_OUT = 1, SEL_WORK = 2, SEL_STAGE_IN = 3, SEL_STAGE_OUT = 4 };
 
 struct Launch {
     KernelKind kind;
@@ -92,6 +96,11 @@ struct Launch {
     std::string label;
     const FixedKernel* fixed;
     int chunk;  // batch chunk; chunks alternate between two stream lanes
+    // element-type conversion instead of an FFT kernel (mixed precisions):
+    // cv_count scalars from type cv_src to cv_dst (0 f16, 1 f32, 2 f64)
+    bool convert = false;
+    int cv_src = 0, cv_dst = 0;
+    long long cv_count = 0;
 };
 
 // Line geometry of one FFT length inside a kernel.
@@ -207,6 +216,7 @@ struct vkfx_plan {
     size_t work_lane = 0;   // workspace bytes of one stream lane
     int lanes = 1;          // 2: chunks alternate between the caller's stream and the aux stream
     bool serial = false;    // chunks depend on each other: one lane
+    size_t stage_in_off = 0, stage_out_off = 0;  // compute-type copies (mixed precision)
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
     std::string json;
@@ -445,6 +455,12 @@ struct Ctx {
 void note_pass(Ctx& c, const Launch& L) {
     if (!c.first_pass) c.js << ",";
     c.first_pass = false;
+    if (L.convert) {
+        static const char* kType[] = {"f16", "f32", "f64"};
+        c.js << "{\"kernel\":\"" << L.label << "\",\"from\":\"" << kType[L.cv_src] << "\",\"to\":\""
+             << kType[L.cv_dst] << "\",\"scalars\":" << L.cv_count << "}";
+        return;
+    }
     c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.a.N << ",\"lines\":" << L.a.nlines
          << ",\"grid\":" << L.grid << ",\"block\":" << L.block << ",\"lines_per_block\":" << L.a.G
          << ",\"lds_bytes\":" << L.lds << ",\"fixed_shape\":" << (L.fixed ? "true" : "false")
@@ -1235,8 +1251,9 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     if (d.batch == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "batch count must be >= 1");
     for (uint32_t i = 0; i < d.rank; ++i)
         if (d.dims[i] == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "ZeroLength: axis " + std::to_string(i));
-    if (d.precision != VKFX_F32 && d.precision != VKFX_F64)
-        return fail(VKFX_ERR_UNSUPPORTED_PRECISION, "only F32 and F64 are supported by this path");
+    if (d.precision < VKFX_F32 || d.precision > VKFX_F64_COMPUTE_F32_STORAGE)
+        return fail(VKFX_ERR_UNSUPPORTED_PRECISION,
+                    "precision must be F32, F64, F16StorageF32Compute or F64ComputeF32Storage");
     if (d.direction != VKFX_FORWARD && d.direction != VKFX_INVERSE)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "direction must be -1 or +1");
     if (d.transform == VKFX_R2C && d.direction != VKFX_FORWARD)
@@ -1246,7 +1263,10 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     if (d.transform < VKFX_C2C || d.transform > VKFX_C2R) return fail(VKFX_ERR_INVALID_ARGUMENT, "unknown transform");
     if (d.transform != VKFX_C2C && d.rank != 1)
         return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "multi-dimensional R2C/C2R is outside this path");
-    const bool f64 = d.precision == VKFX_F64;
+    // storage and compute scalar types (0 f16, 1 f32, 2 f64)
+    const bool f64 = d.precision == VKFX_F64 || d.precision == VKFX_F64_COMPUTE_F32_STORAGE;
+    const int store_t = d.precision == VKFX_F16_STORAGE_F32_COMPUTE ? 0 : d.precision == VKFX_F64 ? 2 : 1;
+    const int comp_t = f64 ? 2 : 1;
     size_t total = d.batch;
     for (uint32_t i = 0; i < d.rank; ++i) {
         if (d.dims[i] > (size_t)1 << 40 || total > ((size_t)1 << 46) / d.dims[i])
@@ -1280,7 +1300,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     const size_t cs = csize(c.prec), rs = rsize(c.prec);
     c.js << "{\"rank\":" << d.rank << ",\"dims\":[";
     for (uint32_t i = 0; i < d.rank; ++i) c.js << (i ? "," : "") << d.dims[i];
-    c.js << "],\"batch\":" << d.batch << ",\"precision\":\"" << (f64 ? "f64" : "f32") << "\",\"transform\":\""
+    static const char* kPrecName[] = {"f32", "f64", "f16_storage_f32_compute", "f64_compute_f32_storage"};
+    c.js << "],\"batch\":" << d.batch << ",\"precision\":\"" << kPrecName[d.precision] << "\",\"transform\":\""
          << (d.transform == VKFX_C2C ? "c2c" : d.transform == VKFX_R2C ? "r2c" : "c2r") << "\",\"axes\":[";
     for (uint32_t i = 0; i < d.rank; ++i) {
         const int alg = d.axis_algorithm[i];
@@ -1323,6 +1344,33 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         delete p;
         return rc;
     }
+    if (store_t != comp_t) {
+        // Mixed storage/compute: convert the caller's input into a compute-type
+        // copy in the workspace, run the passes there, convert the result out.
+        const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8, csz = comp_t == 2 ? 8 : 4;
+        const size_t cin = p->in_bytes, cout = p->out_bytes;
+        auto remap = [](int s) { return s == SEL_IN ? (int)SEL_STAGE_IN : s == SEL_OUT ? (int)SEL_STAGE_OUT : s; };
+        for (Launch& L : p->launches) {
+            L.in_sel = remap(L.in_sel);
+            L.out_sel = remap(L.out_sel);
+        }
+        Launch cv_in{};
+        cv_in.convert = true;
+        cv_in.label = "convert_in";
+        cv_in.in_sel = SEL_IN, cv_in.out_sel = SEL_STAGE_IN;
+        cv_in.cv_src = store_t, cv_in.cv_dst = comp_t, cv_in.cv_count = (long long)(cin / csz);
+        Launch cv_out = cv_in;
+        cv_out.label = "convert_out";
+        cv_out.in_sel = SEL_STAGE_OUT, cv_out.out_sel = SEL_OUT;
+        cv_out.cv_src = comp_t, cv_out.cv_dst = store_t, cv_out.cv_count = (long long)(cout / csz);
+        p->launches.insert(p->launches.begin(), cv_in);
+        p->launches.push_back(cv_out);
+        p->in_bytes = cin / csz * ssz;
+        p->out_bytes = cout / csz * ssz;
+        p->serial = true;  // the conversions bracket every chunk
+        p->stage_in_off = cin;   // provisional sizes; offsets are placed after the lanes
+        p->stage_out_off = d.transform == VKFX_C2C ? 0 : cout;  // C2C runs in place
+    }
     int nchunks = 1;
     for (const Launch& L : p->launches) nchunks = std::max(nchunks, L.chunk + 1);
     // Nontemporal roles of the fixed-shape passes: a pass reading the
@@ -1348,6 +1396,13 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     if (const char* e = getenv("VKFX_LANES")) p->lanes = (atoi(e) == 1 || p->serial) ? 1 : p->lanes;
     p->work_lane = p->work_bytes;
     p->work_bytes = p->work_lane * p->lanes;
+    if (store_t != comp_t) {
+        auto align = [](size_t v) { return (v + 255) / 256 * 256; };
+        const size_t cin = p->stage_in_off, cout = p->stage_out_off;
+        p->stage_in_off = align(p->work_bytes);
+        p->stage_out_off = cout ? p->stage_in_off + align(cin) : p->stage_in_off;
+        p->work_bytes = (cout ? p->stage_out_off + cout : p->stage_in_off + cin);
+    }
     if (p->lanes == 2) {
         hipError_t e = hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&p->ev_join, hipEventDisableTiming);
@@ -1415,7 +1470,8 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
     if (plan->work_bytes && !work) return fail(VKFX_ERR_INVALID_ARGUMENT, "plan needs a workspace");
     hipStream_t s = stream ? (hipStream_t)stream : plan->ctx->stream;
     (void)hipSetDevice(plan->ctx->device);
-    const int prec = plan->desc.precision == VKFX_F64 ? 1 : 0;
+    const int prec =
+        (plan->desc.precision == VKFX_F64 || plan->desc.precision == VKFX_F64_COMPUTE_F32_STORAGE) ? 1 : 0;
     hipStream_t lane_stream[2] = {s, plan->ctx->aux};
     if (plan->lanes == 2) {
         // fork: the aux lane starts after everything already queued on s
@@ -1427,11 +1483,19 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
         const int lane = plan->lanes == 2 ? (L.chunk & 1) : 0;
         KArgs a = L.a;
         auto sel = [&](int which, size_t off) -> char* {
-            char* base = which == SEL_IN ? (char*)d_in
-                         : which == SEL_OUT ? (char*)d_out
-                                            : (char*)work + (size_t)lane * plan->work_lane;
+            char* base = which == SEL_IN             ? (char*)d_in
+                         : which == SEL_OUT          ? (char*)d_out
+                         : which == SEL_STAGE_IN     ? (char*)work + plan->stage_in_off
+                         : which == SEL_STAGE_OUT    ? (char*)work + plan->stage_out_off
+                                                     : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };
+        if (L.convert) {
+            int e = launch_convert(L.cv_src, L.cv_dst, sel(L.in_sel, 0), sel(L.out_sel, 0), L.cv_count,
+                                   lane_stream[lane]);
+            if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
+            continue;
+        }
         a.in = sel(L.in_sel, L.in_off);
         a.out = sel(L.out_sel, L.out_off);
         int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, lane_stream[lane], L.fixed);
@@ -1485,7 +1549,7 @@ int vkfx_planner_axis(uint64_t len, uint64_t batch, int32_t precision, int32_t a
     if (!algorithm || !convolution_len) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output");
     if (len == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "ZeroLength");
     try {
-        const bool f64 = precision == VKFX_F64;
+        const bool f64 = precision == VKFX_F64 || precision == VKFX_F64_COMPUTE_F32_STORAGE;
         AxisDecision d = plan_c2c_axis(len, batch ? batch : 1, f64, axis_is_strided != 0,
                                        tuning_for_amd(f64, allow_recursive_rader != 0),
                                        planner_device(shared_memory_bytes));
@@ -1502,7 +1566,8 @@ int vkfx_planner_bluestein_padding(uint64_t len, uint64_t batch, int32_t precisi
     if (!padded) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output");
     if (len < 2) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein length must be >= 2");
     try {
-        *padded = bluestein_auto_padding(len, batch ? batch : 1, precision == VKFX_F64,
+        *padded = bluestein_auto_padding(len, batch ? batch : 1,
+                                         precision == VKFX_F64 || precision == VKFX_F64_COMPUTE_F32_STORAGE,
                                          planner_device(shared_memory_bytes));
     } catch (const std::exception& ex) {
         return fail(VKFX_ERR_INVALID_ARGUMENT, ex.what());

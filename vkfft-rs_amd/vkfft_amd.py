@@ -62,8 +62,15 @@ class TransformKind(enum.IntEnum):
 
 
 class Precision(enum.IntEnum):
+    """Precision (config.rs:108-145): storage / compute."""
     F32 = 0
     F64 = 1
+    F16StorageF32Compute = 2
+    F64ComputeF32Storage = 3
+
+
+def _f32_family(p: Precision) -> bool:
+    return p != Precision.F64
 
 
 class AlgorithmKind(enum.IntEnum):
@@ -262,11 +269,33 @@ class TransformIr:
 
     @property
     def real_dtype(self):
-        return np.float32 if self.config.precision == Precision.F32 else np.float64
+        """Host-side element type (Complex32 / f32 for every F32-family precision)."""
+        return np.float32 if _f32_family(self.config.precision) else np.float64
 
     @property
     def complex_dtype(self):
-        return np.complex64 if self.config.precision == Precision.F32 else np.complex128
+        return np.complex64 if _f32_family(self.config.precision) else np.complex128
+
+    @property
+    def storage_scalar_dtype(self):
+        """Scalar type of the device buffers (binary16 for F16StorageF32Compute)."""
+        p = self.config.precision
+        return np.float16 if p == Precision.F16StorageF32Compute else (np.float64 if p == Precision.F64
+                                                                         else np.float32)
+
+    def to_storage(self, x: np.ndarray) -> np.ndarray:
+        """Host values -> the scalars the device buffers hold (binary16 rounds to
+        nearest even, like Binary16::from_f32)."""
+        if self.config.precision != Precision.F16StorageF32Compute:
+            return x
+        scal = x.view(np.float32) if np.iscomplexobj(x) else x
+        return scal.astype(np.float16)
+
+    def from_storage(self, s: np.ndarray, complex_out: bool) -> np.ndarray:
+        if self.config.precision != Precision.F16StorageF32Compute:
+            return s
+        v = s.astype(np.float32)
+        return v.view(np.complex64) if complex_out else v
 
     def input_count(self) -> int:
         c = self.config
@@ -337,8 +366,12 @@ class TransformTicket:
     def __init__(self, plan: "Plan", x: np.ndarray, out_dtype, out_count: int):
         self.plan = plan
         self._L = plan._L
+        ir = plan.ir
+        self._complex_out = np.dtype(out_dtype).kind == "c"
+        x = np.ascontiguousarray(ir.to_storage(x))
         self._x = x  # kept alive until the submit has copied it
-        self._out = np.empty(out_count, dtype=out_dtype)
+        self._out = np.empty(out_count * (2 if self._complex_out else 1), dtype=ir.storage_scalar_dtype) \
+            if ir.config.precision == Precision.F16StorageF32Compute else np.empty(out_count, dtype=out_dtype)
         self.handle = ctypes.c_void_p()
         _check(self._L.vkfx_submit_host(plan.handle, x.ctypes.data, x.nbytes, ctypes.byref(self.handle)), self._L)
 
@@ -350,7 +383,7 @@ class TransformTicket:
     def wait(self) -> np.ndarray:
         _check(self._L.vkfx_ticket_wait(self.handle, self._out.ctypes.data, self._out.nbytes), self._L)
         self.close()
-        return self._out
+        return self.plan.ir.from_storage(self._out, self._complex_out)
 
     def close(self):
         if self.handle:
@@ -412,9 +445,13 @@ class HipExecutionContext:
         if x.size != ir.input_count():
             raise VkFftError(-5, f"InputLengthMismatch {{ expected: {ir.input_count()}, actual: {x.size} }}")
         plan = self.plan(ir)
-        out = np.empty(out_count, dtype=out_dtype)
-        _check(self._L.vkfx_execute_host(plan.handle, x.ctypes.data, x.nbytes, out.ctypes.data, out.nbytes), self._L)
-        return out
+        xs = np.ascontiguousarray(ir.to_storage(x))
+        complex_out = np.dtype(out_dtype).kind == "c"
+        out = np.empty(out_count * (2 if complex_out else 1), dtype=ir.storage_scalar_dtype) \
+            if ir.config.precision == Precision.F16StorageF32Compute else np.empty(out_count, dtype=out_dtype)
+        _check(self._L.vkfx_execute_host(plan.handle, xs.ctypes.data, xs.nbytes, out.ctypes.data, out.nbytes),
+               self._L)
+        return ir.from_storage(out, complex_out)
 
     def execute_transform(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
         kind = ir.config.transform
@@ -446,15 +483,18 @@ class HipExecutionContext:
         plans = [self.plan(ir) for ir in irs]
         in_dt, _ = self._io_dtypes(irs[0])
         _, out_dt = self._io_dtypes(irs[-1])
-        x = np.ascontiguousarray(x, dtype=in_dt).reshape(-1)
-        out = np.empty(irs[-1].output_count(), dtype=out_dt)
+        x = np.ascontiguousarray(irs[0].to_storage(np.ascontiguousarray(x, dtype=in_dt).reshape(-1)))
+        last = irs[-1]
+        complex_out = np.dtype(out_dt).kind == "c"
+        out = np.empty(last.output_count() * (2 if complex_out else 1), dtype=last.storage_scalar_dtype) \
+            if last.config.precision == Precision.F16StorageF32Compute else np.empty(last.output_count(), dtype=out_dt)
         _check(self._L.vkfx_execute_chain_host(_plan_array(plans), len(plans), x.ctypes.data, x.nbytes,
                                              out.ctypes.data, out.nbytes), self._L)
-        return out
+        return last.from_storage(out, complex_out)
 
     def execute_transform_f32(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
-        if ir.config.precision != Precision.F32:
-            raise VkFftError(-4, "execute_transform_f32 needs an F32 TransformIr")
+        if not _f32_family(ir.config.precision):
+            raise VkFftError(-4, "execute_transform_f32 needs an F32-family TransformIr")
         return self.execute_transform(ir, x)
 
     def execute_transform_f64(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
