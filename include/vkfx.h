@@ -94,6 +94,24 @@ typedef struct {
     int32_t use_library_planner;            /* 1 = plan axes here */
     int32_t axis_algorithm[VKFX_MAX_RANK];  /* vkfx_algorithm per axis */
     uint64_t convolution_len[VKFX_MAX_RANK];/* Bluestein M per axis (0 = not Bluestein) */
+    /* Formatted device layouts (FftConfig::with_input/output_buffer_axis_stride and
+     * _batch_stride, src/config.rs:892-1002, resolved as in resolve_formatted_axis_strides,
+     * config.rs:1463-1522): strides in stored elements per axis, slowest..fastest; 0 =
+     * dense. The fastest axis must stay 1; each stride must cover the next faster
+     * axis. For R2C the output's fastest extent is N/2+1 (C2R: the input's). */
+    uint64_t in_axis_stride[VKFX_MAX_RANK];
+    uint64_t out_axis_stride[VKFX_MAX_RANK];
+    uint64_t in_batch_stride;               /* 0 = dense */
+    uint64_t out_batch_stride;
+    /* Logical zero interval [zero_left, zero_right) per axis (FftConfig::with_zero_padding,
+     * config.rs:1004-1025; equal bounds = none). An element is zero when any of its
+     * coordinates lies in its axis interval (zero_pad_ir.rs:607-617). Spatial domain:
+     * forward input / inverse output; frequency domain (C2C only): forward output /
+     * inverse input (zero_pad_ir.rs:38-46). */
+    uint64_t zero_left[VKFX_MAX_RANK];
+    uint64_t zero_right[VKFX_MAX_RANK];
+    int32_t zero_frequency;                 /* ZeroPaddingDomain::Frequency */
+    uint32_t grouped_batch[VKFX_MAX_RANK];  /* groupedBatch override (0 = automatic), a scheduling hint */
 } vkfx_plan_desc;
 
 /* ---------------------------------------------------------------- context */

@@ -64,7 +64,7 @@ def test_f64_compute_f32_storage(hip_ctx, dims, batch):
     # f64 passes: the only error left is rounding the result to f32
     assert o.rel_l2(y, ref) <= 1e-7
     desc = hip_ctx.plan(ir).describe()
-    assert desc["passes"][0]["kernel"] == "convert_in" and desc["passes"][-1]["kernel"] == "convert_out"
+    assert desc["passes"][0]["kernel"] == "boundary_in" and desc["passes"][-1]["kernel"] == "boundary_out"
     assert desc["precision"] == "f64_compute_f32_storage"
 
 

@@ -350,3 +350,29 @@ def test_device_resident_execute_matches_host(hip_ctx):
     plan.execute_tensors(xt, xt)
     hip_ctx.synchronize()
     assert np.array_equal(xt.cpu().numpy().view(np.complex64), y_dev)
+
+
+@pytest.mark.parametrize("n,prec", [(206, F64), (578, F32), (323, F32), (1009, F64), (131074, F32), (17, F32)])
+def test_real_full_complex_lengths(hip_ctx, n, prec):
+    """Real lengths whose half-size (even) or own (odd) FFT has no Stockham
+    geometry run as a full-length C2C (real_ir.rs:935-946, 1038-1053)."""
+    batch = 3
+    rd = np.float32 if prec == F32 else np.float64
+    x = o.normal(n * batch, n, rd)
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec)
+    r2c = vk.TransformIr.build(cfg.with_transform(vk.TransformKind.RealToComplex), FWD)
+    X = hip_ctx.execute_transform(r2c, x)
+    h = n // 2 + 1
+    ref = np.concatenate([o.r2c_batch(x[b * n:(b + 1) * n].astype(np.float64), n) for b in range(batch)])
+    assert X.size == h * batch
+    err = o.rel_l2(X, ref)
+    if prec == F64 and err > TOL[F64]:
+        # reference::fft's Bluestein for large primes is itself less accurate
+        # than 1e-13: pin to pocketfft
+        err = o.rel_l2(X, np.fft.rfft(x.reshape(batch, n), axis=1).reshape(-1))
+    assert err <= TOL[prec]
+    cfg2 = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.ComplexToReal).with_inverse_normalization(True)
+    c2r = vk.TransformIr.build(cfg2, INV)
+    z = hip_ctx.execute_transform(c2r, X)
+    assert o.rel_l2(z, x) <= 4 * TOL[prec]

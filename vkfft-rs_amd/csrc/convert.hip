@@ -1,7 +1,11 @@
-// convert.hip -- element-type conversion passes for mixed storage/compute
-// precisions (Precision::F16StorageF32Compute and F64ComputeF32Storage,
-// src/config.rs:108-145): the caller's buffers hold the storage type, the FFT
-// passes run on the compute type in the plan's workspace.
+// convert.hip -- boundary passes around a plan's FFT passes: element-type
+// conversion for mixed storage/compute precisions (src/config.rs:108-145),
+// gathers from / scatters to formatted (strided) device layouts
+// (FftConfig::with_*_buffer_axis_stride, src/config.rs:892-1002; the formatted
+// copy passes of src/nd_ir.rs:1105-1150), the logical zero intervals of
+// zero padding (src/zero_pad_ir.rs:320-345, 607-647), and the real <-> complex
+// promotion, truncation and Hermitian expansion of full-complex real
+// transforms (src/real_ir.rs:935-946, 1038-1053).
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
@@ -9,28 +13,62 @@
 namespace vkfx {
 
 template <typename S, typename D>
-__global__ __launch_bounds__(256) void k_convert(const S* __restrict__ in, D* __restrict__ out, long long n) {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (; i < n; i += stride) out[i] = (D)in[i];
+__global__ __launch_bounds__(256) void k_boundary(const S* __restrict__ in, D* __restrict__ out, const BoundaryArgs a) {
+    const long long per = a.tensor_len;
+    const long long total = per * a.batch;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (long long)gridDim.x * blockDim.x) {
+        const long long b = i / per;
+        long long l = i - b * per;
+        long long src = b * a.src_batch, dst = b * a.dst_batch;
+        bool zero = false, conj = false;
+        if (a.mode == 1) {
+            const long long n = a.dims[0], c = l;
+            conj = 2 * c > n;
+            src += (conj ? n - c : c) * a.src_stride[0];
+            dst += c * a.dst_stride[0];
+        } else {
+            for (int ax = a.rank - 1; ax >= 0; --ax) {
+                const long long n = a.dims[ax];
+                const long long c = l % n;
+                l /= n;
+                src += c * a.src_stride[ax];
+                dst += c * a.dst_stride[ax];
+                zero |= c >= a.zero_left[ax] && c < a.zero_right[ax];
+            }
+        }
+        for (int k = 0; k < a.dst_scalars; ++k) {
+            D v = (zero || k >= a.src_scalars) ? (D)0 : (D)in[src * a.src_scalars + k];
+            if (conj && k == 1) v = -v;
+            out[dst * a.dst_scalars + k] = v;
+        }
+    }
 }
 
 template <typename S, typename D>
-static int go(const void* in, void* out, long long n, hipStream_t s) {
-    const long long blocks = (n + 255) / 256;
+static int go(const void* in, void* out, const BoundaryArgs& a, hipStream_t s) {
+    const long long total = a.tensor_len * a.batch;
+    const long long blocks = (total + 255) / 256;
     const unsigned grid = (unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
-    hipLaunchKernelGGL((k_convert<S, D>), dim3(grid), dim3(256), 0, s, (const S*)in, (D*)out, n);
+    hipLaunchKernelGGL((k_boundary<S, D>), dim3(grid), dim3(256), 0, s, (const S*)in, (D*)out, a);
     return (int)hipGetLastError();
 }
 
-// Scalar type codes: 0 = binary16 (round to nearest even), 1 = f32, 2 = f64.
-int launch_convert(int src, int dst, const void* in, void* out, long long n, hipStream_t s) {
-    if (n <= 0) return (int)hipSuccess;
-    if (src == 0 && dst == 1) return go<_Float16, float>(in, out, n, s);
-    if (src == 1 && dst == 0) return go<float, _Float16>(in, out, n, s);
-    if (src == 1 && dst == 2) return go<float, double>(in, out, n, s);
-    if (src == 2 && dst == 1) return go<double, float>(in, out, n, s);
-    return (int)hipErrorInvalidValue;
+int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_t s) {
+    if (a.tensor_len <= 0 || a.batch <= 0) return (int)hipSuccess;
+    if (a.rank < 1 || a.rank > kMaxBoundaryRank || a.src_scalars < 1 || a.src_scalars > 2 || a.dst_scalars < 1 ||
+        a.dst_scalars > 2 || (a.mode == 1 && a.rank != 1))
+        return (int)hipErrorInvalidValue;
+    const int code = a.src_type * 3 + a.dst_type;
+    switch (code) {
+        case 0 * 3 + 1: return go<_Float16, float>(in, out, a, s);
+        case 1 * 3 + 0: return go<float, _Float16>(in, out, a, s);
+        case 1 * 3 + 1: return go<float, float>(in, out, a, s);
+        case 1 * 3 + 2: return go<float, double>(in, out, a, s);
+        case 2 * 3 + 1: return go<double, float>(in, out, a, s);
+        case 2 * 3 + 2: return go<double, double>(in, out, a, s);
+        default: return (int)hipErrorInvalidValue;
+    }
 }
 
 }  // namespace vkfx

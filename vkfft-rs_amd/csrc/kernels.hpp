@@ -112,8 +112,26 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
 // Largest dynamic LDS a block may request on this device (bytes).
 size_t max_lds_bytes();
 
-// Converts n scalars between storage and compute types (0 = binary16,
-// 1 = f32, 2 = f64) on stream s. Returns a hipError_t value.
-int launch_convert(int src, int dst, const void* in, void* out, long long n, hipStream_t s);
+// Boundary pass: for every logical element (b, c_0..c_{rank-1}) of a batch
+// of tensors, out[dst] = zero ? 0 : (D)in[src] with src / dst the strided
+// offsets of the two layouts and zero set when any coordinate lies in its
+// axis interval [zero_left, zero_right). Scalar types: 0 = binary16,
+// 1 = f32, 2 = f64; src_scalars / dst_scalars = 2 for complex elements, 1
+// for real (real -> complex fills the imaginary part with 0, complex -> real
+// keeps the real part). mode 1 (rank 1): Hermitian expansion of N/2+1 bins
+// to N, out[c] = c <= N/2 ? in[c] : conj(in[N - c]) with N = dims[0].
+constexpr int kMaxBoundaryRank = 4;
+struct BoundaryArgs {
+    int rank = 1;
+    int src_scalars = 2, dst_scalars = 2;
+    int mode = 0;
+    int src_type = 1, dst_type = 1;
+    long long batch = 0, tensor_len = 0;
+    long long dims[kMaxBoundaryRank] = {1, 1, 1, 1};
+    long long src_stride[kMaxBoundaryRank] = {0, 0, 0, 0}, dst_stride[kMaxBoundaryRank] = {0, 0, 0, 0};
+    long long src_batch = 0, dst_batch = 0;
+    long long zero_left[kMaxBoundaryRank] = {0, 0, 0, 0}, zero_right[kMaxBoundaryRank] = {0, 0, 0, 0};
+};
+int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_t s);
 
 }  // namespace vkfx

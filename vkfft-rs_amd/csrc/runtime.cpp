@@ -82,8 +82,9 @@ namespace {
 // Buffers a launch reads or writes: the caller's input and output, the
 // plan's workspace (per stream lane) and, for mixed storage/compute
 // precisions, the compute-type copies of the input and output in the
-// workspace.
-enum BufSel : int { SEL_IN = 0, SEL_OUT = 1, SEL_WORK = 2, SEL_STAGE_IN = 3, SEL_STAGE_OUT = 4 };
+// workspace; SEL_FULL is the N-point complex copy of a real transform run
+// through a full-length C2C plan.
+enum BufSel : int { SEL_IN = 0, SEL_OUT = 1, SEL_WORK = 2, SEL_STAGE_IN = 3, SEL_STAGE_OUT = 4, SEL_FULL = 5 };
 
 struct Launch {
     KernelKind kind;
@@ -96,11 +97,10 @@ struct Launch {
     std::string label;
     const FixedKernel* fixed;
     int chunk;  // batch chunk; chunks alternate between two stream lanes
-    // element-type conversion instead of an FFT kernel (mixed precisions):
-    // cv_count scalars from type cv_src to cv_dst (0 f16, 1 f32, 2 f64)
-    bool convert = false;
-    int cv_src = 0, cv_dst = 0;
-    long long cv_count = 0;
+    // boundary pass instead of an FFT kernel (type conversion, formatted
+    // layouts, zero padding; convert.hip)
+    bool boundary = false;
+    BoundaryArgs ba;
 };
 
 // Line geometry of one FFT length inside a kernel.
@@ -216,7 +216,10 @@ struct vkfx_plan {
     size_t work_lane = 0;   // workspace bytes of one stream lane
     int lanes = 1;          // 2: chunks alternate between the caller's stream and the aux stream
     bool serial = false;    // chunks depend on each other: one lane
-    size_t stage_in_off = 0, stage_out_off = 0;  // compute-type copies (mixed precision)
+    size_t stage_in_off = 0, stage_out_off = 0;  // dense compute-type copies behind boundary passes
+    size_t stage_in_bytes = 0, stage_out_bytes = 0;
+    bool stage_shared = false;  // C2C with both sides staged runs in place on one copy
+    size_t full_off = 0, full_bytes = 0;  // SEL_FULL region (full-complex real transforms)
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
     std::string json;
@@ -455,10 +458,20 @@ struct Ctx {
 void note_pass(Ctx& c, const Launch& L) {
     if (!c.first_pass) c.js << ",";
     c.first_pass = false;
-    if (L.convert) {
+    if (L.boundary) {
         static const char* kType[] = {"f16", "f32", "f64"};
-        c.js << "{\"kernel\":\"" << L.label << "\",\"from\":\"" << kType[L.cv_src] << "\",\"to\":\""
-             << kType[L.cv_dst] << "\",\"scalars\":" << L.cv_count << "}";
+        bool zero = false, strided = false;
+        for (int i = 0; i < L.ba.rank; ++i) zero |= L.ba.zero_right[i] > L.ba.zero_left[i];
+        long long dense = 1;
+        for (int i = L.ba.rank - 1; i >= 0; --i) {
+            strided |= L.ba.src_stride[i] != dense || L.ba.dst_stride[i] != dense;
+            dense *= L.ba.dims[i];
+        }
+        strided |= L.ba.src_batch != dense || L.ba.dst_batch != dense;
+        c.js << "{\"kernel\":\"" << L.label << "\",\"from\":\"" << kType[L.ba.src_type] << "\",\"to\":\""
+             << kType[L.ba.dst_type] << "\",\"elements\":" << L.ba.tensor_len * L.ba.batch
+             << ",\"formatted\":" << (strided ? "true" : "false") << ",\"zero_padding\":" << (zero ? "true" : "false")
+             << "}";
         return;
     }
     c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.a.N << ",\"lines\":" << L.a.nlines
@@ -970,6 +983,72 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
 
 // ---- real ------------------------------------------------------------------
 
+PlannerDevice planner_device(uint64_t shared) {
+    PlannerDevice d;
+    if (shared) {
+        d.shared_memory_bytes = shared;
+        size_t p2 = 1;
+        while (p2 * 2 <= shared) p2 *= 2;
+        d.shared_memory_pow2_bytes = p2;
+    }
+    return d;
+}
+
+// Real transform through a full-length C2C plan (the FullComplex shape,
+// src/real_ir.rs:935-946, 1038-1053, 1124-1213), for lengths whose half-size
+// or odd-length FFT has no Stockham geometry: R2C promotes x to complex,
+// runs the N-point C2C (Stockham, Rader or Bluestein as the planner decides)
+// and keeps N/2+1 bins; C2R expands the Hermitian bins to N, runs the
+// inverse C2C and keeps the real part.
+int plan_real_full_complex(Ctx& c, size_t n, size_t batch, bool r2c, bool normalize) {
+    vkfx_plan* p = c.p;
+    const size_t h = n / 2 + 1;
+    const bool f64 = c.prec == 1;
+    AxisDecision ad = plan_c2c_axis(n, batch, f64, false, tuning_for_amd(f64), planner_device(c.p->ctx->profile.shared_memory_bytes));
+    p->full_bytes = batch * n * csize(c.prec);
+    p->serial = true;
+    c.js << "\"real\":{\"len\":" << n << ",\"algorithm\":\"full_complex\",\"c2c\":\""
+         << (ad.algorithm == Algorithm::Stockham ? "stockham" : ad.algorithm == Algorithm::Rader ? "rader" : "bluestein")
+         << "\"},";
+    auto boundary = [&](int in_sel, int out_sel, long long len, long long src_batch, long long dst_batch, int ss, int ds,
+                        int mode, const char* label) {
+        Launch L{};
+        L.boundary = true;
+        L.label = label;
+        L.in_sel = in_sel, L.out_sel = out_sel;
+        BoundaryArgs& a = L.ba;
+        a.rank = 1;
+        a.dims[0] = len;
+        a.src_stride[0] = a.dst_stride[0] = 1;
+        a.tensor_len = len;
+        a.batch = (long long)batch;
+        a.src_batch = src_batch, a.dst_batch = dst_batch;
+        a.src_scalars = ss, a.dst_scalars = ds;
+        a.mode = mode;
+        a.src_type = a.dst_type = c.prec ? 2 : 1;
+        p->launches.push_back(L);
+    };
+    const long long N = (long long)n, H = (long long)h;
+    if (r2c)
+        boundary(SEL_IN, SEL_FULL, N, N, N, 1, 2, 0, "real_promote");
+    else
+        boundary(SEL_IN, SEL_FULL, N, H, N, 2, 2, 1, "hermitian_expand");
+    const size_t first = p->launches.size();
+    int rc = plan_c2c_1d(c, n, batch, r2c ? -1 : 1, !r2c && normalize, ad.algorithm,
+                         ad.algorithm == Algorithm::Bluestein ? ad.convolution_len : 0);
+    if (rc) return rc;
+    for (size_t i = first; i < p->launches.size(); ++i) {
+        Launch& L = p->launches[i];
+        if (L.in_sel == SEL_IN || L.in_sel == SEL_OUT) L.in_sel = SEL_FULL;
+        if (L.out_sel == SEL_IN || L.out_sel == SEL_OUT) L.out_sel = SEL_FULL;
+    }
+    if (r2c)
+        boundary(SEL_FULL, SEL_OUT, H, N, H, 2, 2, 0, "truncate");
+    else
+        boundary(SEL_FULL, SEL_OUT, N, N, N, 2, 1, 0, "real_part");
+    return VKFX_OK;
+}
+
 int plan_r2c(Ctx& c, size_t n, size_t batch) {
     vkfx_plan* p = c.p;
     const int prec = c.prec;
@@ -977,7 +1056,7 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     const size_t h = n / 2 + 1;
     if (n % 2) {
         Geometry g0 = geometry(n, prec, 1, c.lds_max, c.lds_max);
-        if (!g0.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "odd R2C length needs a single-upload smooth length");
+        if (!g0.ok) return plan_real_full_complex(c, n, batch, true, false);
         Geometry g = geometry(n, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
         KArgs a = blank();
         a.in_es = a.out_es = 1;
@@ -1005,8 +1084,7 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
                           "r2c_even_half");
     }
     size_t n1, n2;
-    if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
-        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for R2C half length");
+    if (!four_step_split(M, prec, c.lds_max, &n1, &n2)) return plan_real_full_complex(c, n, batch, true, false);
     // the mirror-row pass needs N1 divisible by 2H; H lines + H mirrors per block
     Geometry gb1 = geometry(n2, prec, 1, c.lds_max, c.lds_max);
     int H = prec ? 4 : 8;
@@ -1060,7 +1138,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     const double sc = normalize ? 1.0 / (double)n : 1.0;
     if (n % 2) {
         Geometry g0 = geometry(n, prec, 1, c.lds_max, c.lds_max);
-        if (!g0.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "odd C2R length needs a single-upload smooth length");
+        if (!g0.ok) return plan_real_full_complex(c, n, batch, false, normalize);
         Geometry g = geometry(n, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
         KArgs a = blank();
         a.in_es = a.out_es = 1;
@@ -1089,8 +1167,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
                           "c2r_even_half");
     }
     size_t n1, n2;
-    if (!four_step_split(M, prec, c.lds_max, &n1, &n2))
-        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no four-step split for C2R half length");
+    if (!four_step_split(M, prec, c.lds_max, &n1, &n2)) return plan_real_full_complex(c, n, batch, false, normalize);
     // take the orientation whose two passes have fixed shapes registered
     if (!find_fixed(KK_FS_A_C2R, prec, 1, (int)n1, true) && find_fixed(KK_FS_A_C2R, prec, 1, (int)n2, true) &&
         find_fixed(KK_FS_B, prec, 1, (int)n1, false))
@@ -1136,17 +1213,6 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
         if (rc) return rc;
     }
     return VKFX_OK;
-}
-
-PlannerDevice planner_device(uint64_t shared) {
-    PlannerDevice d;
-    if (shared) {
-        d.shared_memory_bytes = shared;
-        size_t p2 = 1;
-        while (p2 * 2 <= shared) p2 *= 2;
-        d.shared_memory_pow2_bytes = p2;
-    }
-    return d;
 }
 
 }  // namespace
@@ -1344,32 +1410,118 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         delete p;
         return rc;
     }
-    if (store_t != comp_t) {
-        // Mixed storage/compute: convert the caller's input into a compute-type
-        // copy in the workspace, run the passes there, convert the result out.
-        const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8, csz = comp_t == 2 ? 8 : 4;
-        const size_t cin = p->in_bytes, cout = p->out_bytes;
-        auto remap = [](int s) { return s == SEL_IN ? (int)SEL_STAGE_IN : s == SEL_OUT ? (int)SEL_STAGE_OUT : s; };
+    {
+        // Boundary passes: type conversion (mixed precisions), formatted
+        // layouts and zero padding sit between the caller's buffers and dense
+        // compute-type copies in the workspace that the FFT passes use.
+        const bool real_in = d.transform == VKFX_R2C, real_out = d.transform == VKFX_C2R;
+        const size_t rank = d.rank;
+        long long in_dims[VKFX_MAX_RANK], out_dims[VKFX_MAX_RANK];
+        for (size_t i = 0; i < rank; ++i) in_dims[i] = out_dims[i] = (long long)d.dims[i];
+        if (d.transform == VKFX_R2C) out_dims[rank - 1] = (long long)(d.dims[rank - 1] / 2 + 1);
+        if (d.transform == VKFX_C2R) in_dims[rank - 1] = (long long)(d.dims[rank - 1] / 2 + 1);
+        // resolve_formatted_axis_strides / _batch_stride (config.rs:1463-1522)
+        auto resolve = [&](const long long* dims, const uint64_t* over, uint64_t batch_over, long long* st,
+                           long long* bst, bool* formatted, const char* side) -> int {
+            *formatted = false;
+            st[rank - 1] = 1;
+            if (over[rank - 1] && over[rank - 1] != 1)
+                return fail(VKFX_ERR_INVALID_ARGUMENT,
+                            std::string(side) + ": formatted fastest-axis stride must remain one stored element");
+            for (int ax = (int)rank - 2; ax >= 0; --ax) {
+                const long long minimum = st[ax + 1] * dims[ax + 1];
+                st[ax] = over[ax] ? (long long)over[ax] : minimum;
+                if (st[ax] < minimum)
+                    return fail(VKFX_ERR_INVALID_ARGUMENT,
+                                std::string(side) + ": formatted axis stride overlaps the next faster logical axis");
+                *formatted |= st[ax] != minimum;
+            }
+            const long long minimum = st[0] * dims[0];
+            *bst = batch_over ? (long long)batch_over : minimum;
+            if (*bst < minimum)
+                return fail(VKFX_ERR_INVALID_ARGUMENT, std::string(side) + ": formatted batch stride overlaps the logical tensor");
+            *formatted |= *bst != minimum;
+            return VKFX_OK;
+        };
+        long long in_st[VKFX_MAX_RANK], out_st[VKFX_MAX_RANK], in_bst = 0, out_bst = 0;
+        bool fmt_in = false, fmt_out = false;
+        int brc = resolve(in_dims, d.in_axis_stride, d.in_batch_stride, in_st, &in_bst, &fmt_in, "input");
+        if (!brc) brc = resolve(out_dims, d.out_axis_stride, d.out_batch_stride, out_st, &out_bst, &fmt_out, "output");
+        // zero padding ranges and the boundary that owns them (zero_pad_ir.rs:38-46)
+        bool any_zero = false;
+        for (size_t i = 0; i < rank && !brc; ++i) {
+            if (d.zero_left[i] > d.zero_right[i] || d.zero_right[i] > d.dims[i])
+                brc = fail(VKFX_ERR_INVALID_ARGUMENT, "InvalidZeroPaddingRange on axis " + std::to_string(i));
+            any_zero |= d.zero_right[i] > d.zero_left[i];
+        }
+        if (!brc && any_zero && d.zero_frequency && d.transform != VKFX_C2C)
+            brc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "frequency-domain zero padding is C2C only");
+        for (size_t i = 0; i < rank && !brc; ++i)
+            if (d.grouped_batch[i] > d.batch)
+                brc = fail(VKFX_ERR_INVALID_ARGUMENT, "groupedBatch exceeds the batch count");
+        if (brc) {
+            delete p;
+            return brc;
+        }
+        const bool fwd = d.direction == VKFX_FORWARD;
+        const bool zp_in = any_zero && (d.zero_frequency ? !fwd : fwd);
+        const bool zp_out = any_zero && !zp_in;
+        const bool mixed = store_t != comp_t;
+        const bool need_in = mixed || fmt_in || zp_in, need_out = mixed || fmt_out || zp_out;
+        const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
+        const size_t cin = p->in_bytes, cout = p->out_bytes;  // dense compute-type bytes
+        const int in_scal = real_in ? 1 : 2, out_scal = real_out ? 1 : 2;
+        auto make = [&](bool in_side) {
+            Launch L{};
+            L.boundary = true;
+            BoundaryArgs& a = L.ba;
+            a.rank = (int)rank;
+            a.batch = (long long)d.batch;
+            const long long* dims = in_side ? in_dims : out_dims;
+            long long dense = 1;
+            for (int ax = (int)rank - 1; ax >= 0; --ax) {
+                a.dims[ax] = dims[ax];
+                const long long phys = in_side ? in_st[ax] : out_st[ax];
+                a.src_stride[ax] = in_side ? phys : dense;
+                a.dst_stride[ax] = in_side ? dense : phys;
+                dense *= dims[ax];
+                if (in_side ? zp_in : zp_out) {
+                    a.zero_left[ax] = (long long)d.zero_left[ax];
+                    a.zero_right[ax] = (long long)d.zero_right[ax];
+                }
+            }
+            a.tensor_len = dense;
+            a.src_batch = in_side ? in_bst : dense;
+            a.dst_batch = in_side ? dense : out_bst;
+            a.src_scalars = a.dst_scalars = in_side ? in_scal : out_scal;
+            a.src_type = in_side ? store_t : comp_t;
+            a.dst_type = in_side ? comp_t : store_t;
+            L.label = in_side ? "boundary_in" : "boundary_out";
+            L.in_sel = in_side ? SEL_IN : SEL_STAGE_OUT;
+            L.out_sel = in_side ? SEL_STAGE_IN : SEL_OUT;
+            return L;
+        };
         for (Launch& L : p->launches) {
+            auto remap = [&](int s) {
+                return (need_in && s == SEL_IN) ? (int)SEL_STAGE_IN : (need_out && s == SEL_OUT) ? (int)SEL_STAGE_OUT : s;
+            };
             L.in_sel = remap(L.in_sel);
             L.out_sel = remap(L.out_sel);
         }
-        Launch cv_in{};
-        cv_in.convert = true;
-        cv_in.label = "convert_in";
-        cv_in.in_sel = SEL_IN, cv_in.out_sel = SEL_STAGE_IN;
-        cv_in.cv_src = store_t, cv_in.cv_dst = comp_t, cv_in.cv_count = (long long)(cin / csz);
-        Launch cv_out = cv_in;
-        cv_out.label = "convert_out";
-        cv_out.in_sel = SEL_STAGE_OUT, cv_out.out_sel = SEL_OUT;
-        cv_out.cv_src = comp_t, cv_out.cv_dst = store_t, cv_out.cv_count = (long long)(cout / csz);
-        p->launches.insert(p->launches.begin(), cv_in);
-        p->launches.push_back(cv_out);
-        p->in_bytes = cin / csz * ssz;
-        p->out_bytes = cout / csz * ssz;
-        p->serial = true;  // the conversions bracket every chunk
-        p->stage_in_off = cin;   // provisional sizes; offsets are placed after the lanes
-        p->stage_out_off = d.transform == VKFX_C2C ? 0 : cout;  // C2C runs in place
+        if (need_in) p->launches.insert(p->launches.begin(), make(true));
+        if (need_out) p->launches.push_back(make(false));
+        p->in_bytes = (size_t)in_bst * d.batch * in_scal * ssz;
+        p->out_bytes = (size_t)out_bst * d.batch * out_scal * ssz;
+        if (need_in || need_out) p->serial = true;  // the boundary passes bracket every chunk
+        p->stage_in_bytes = need_in ? cin : 0;
+        // C2C runs in place on one copy when both sides are staged
+        p->stage_shared = need_out && need_in && d.transform == VKFX_C2C;
+        p->stage_out_bytes = need_out && !p->stage_shared ? cout : 0;
+        c.js << "\"boundary\":{\"input\":" << (need_in ? "true" : "false") << ",\"output\":"
+             << (need_out ? "true" : "false") << ",\"zero_padding\":\""
+             << (!any_zero ? "none" : d.zero_frequency ? "frequency" : "spatial") << "\",\"grouped_batch\":[";
+        for (size_t i = 0; i < rank; ++i) c.js << (i ? "," : "") << d.grouped_batch[i];
+        c.js << "]},";
     }
     int nchunks = 1;
     for (const Launch& L : p->launches) nchunks = std::max(nchunks, L.chunk + 1);
@@ -1396,12 +1548,17 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     if (const char* e = getenv("VKFX_LANES")) p->lanes = (atoi(e) == 1 || p->serial) ? 1 : p->lanes;
     p->work_lane = p->work_bytes;
     p->work_bytes = p->work_lane * p->lanes;
-    if (store_t != comp_t) {
+    if (p->full_bytes) {
+        p->full_off = (p->work_bytes + 255) / 256 * 256;
+        p->work_bytes = p->full_off + p->full_bytes;
+    }
+    if (p->stage_in_bytes || p->stage_out_bytes) {
+        // workspace: [lane work][full complex][stage in][stage out]
         auto align = [](size_t v) { return (v + 255) / 256 * 256; };
-        const size_t cin = p->stage_in_off, cout = p->stage_out_off;
+        const bool shared = p->stage_shared;
         p->stage_in_off = align(p->work_bytes);
-        p->stage_out_off = cout ? p->stage_in_off + align(cin) : p->stage_in_off;
-        p->work_bytes = (cout ? p->stage_out_off + cout : p->stage_in_off + cin);
+        p->stage_out_off = shared ? p->stage_in_off : p->stage_in_off + align(p->stage_in_bytes);
+        p->work_bytes = shared ? p->stage_in_off + p->stage_in_bytes : p->stage_out_off + p->stage_out_bytes;
     }
     if (p->lanes == 2) {
         hipError_t e = hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming);
@@ -1487,12 +1644,12 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
                          : which == SEL_OUT          ? (char*)d_out
                          : which == SEL_STAGE_IN     ? (char*)work + plan->stage_in_off
                          : which == SEL_STAGE_OUT    ? (char*)work + plan->stage_out_off
+                         : which == SEL_FULL         ? (char*)work + plan->full_off
                                                      : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };
-        if (L.convert) {
-            int e = launch_convert(L.cv_src, L.cv_dst, sel(L.in_sel, 0), sel(L.out_sel, 0), L.cv_count,
-                                   lane_stream[lane]);
+        if (L.boundary) {
+            int e = launch_boundary(L.ba, sel(L.in_sel, 0), sel(L.out_sel, 0), lane_stream[lane]);
             if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
             continue;
         }

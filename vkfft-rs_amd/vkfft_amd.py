@@ -73,6 +73,12 @@ def _f32_family(p: Precision) -> bool:
     return p != Precision.F64
 
 
+class ZeroPaddingDomain(enum.IntEnum):
+    """ZeroPaddingDomain (config.rs): which boundary owns the zero interval."""
+    Spatial = 0
+    Frequency = 1
+
+
 class AlgorithmKind(enum.IntEnum):
     Stockham = 0
     Rader = 1
@@ -91,6 +97,14 @@ class _PlanDesc(ctypes.Structure):
         ("use_library_planner", ctypes.c_int32),
         ("axis_algorithm", ctypes.c_int32 * MAX_RANK),
         ("convolution_len", ctypes.c_uint64 * MAX_RANK),
+        ("in_axis_stride", ctypes.c_uint64 * MAX_RANK),
+        ("out_axis_stride", ctypes.c_uint64 * MAX_RANK),
+        ("in_batch_stride", ctypes.c_uint64),
+        ("out_batch_stride", ctypes.c_uint64),
+        ("zero_left", ctypes.c_uint64 * MAX_RANK),
+        ("zero_right", ctypes.c_uint64 * MAX_RANK),
+        ("zero_frequency", ctypes.c_int32),
+        ("grouped_batch", ctypes.c_uint32 * MAX_RANK),
     ]
 
 
@@ -190,6 +204,13 @@ class FftConfig:
     transform: TransformKind = TransformKind.ComplexToComplex
     normalize_inverse: bool = False
     allow_recursive_fft_rader: bool = False
+    input_buffer_axis_strides: List[int] = field(default_factory=lambda: [0] * MAX_RANK)
+    output_buffer_axis_strides: List[int] = field(default_factory=lambda: [0] * MAX_RANK)
+    input_buffer_batch_stride: int = 0
+    output_buffer_batch_stride: int = 0
+    zero_padding: List[Optional[tuple]] = field(default_factory=lambda: [None] * MAX_RANK)
+    zero_padding_domain: ZeroPaddingDomain = ZeroPaddingDomain.Spatial
+    grouped_batch: List[int] = field(default_factory=lambda: [0] * MAX_RANK)
 
     @staticmethod
     def new(dimensions: Sequence[int]) -> "FftConfig":
@@ -209,6 +230,47 @@ class FftConfig:
 
     def with_inverse_normalization(self, normalize: bool = True) -> "FftConfig":
         self.normalize_inverse = bool(normalize)
+        return self
+
+    def _axis(self, axis: int, field_name: str) -> int:
+        if not 0 <= axis < len(self.dimensions):
+            raise VkFftError(-7, f"ValueOutOfRange {{ field: {field_name!r} }}")
+        return axis
+
+    def with_input_buffer_axis_stride(self, axis: int, stride: int) -> "FftConfig":
+        """Formatted input stride in stored elements (config.rs:892-905); 0 clears."""
+        self.input_buffer_axis_strides[self._axis(axis, "formatted input axis stride")] = int(stride)
+        return self
+
+    def with_output_buffer_axis_stride(self, axis: int, stride: int) -> "FftConfig":
+        self.output_buffer_axis_strides[self._axis(axis, "formatted output axis stride")] = int(stride)
+        return self
+
+    def with_input_buffer_batch_stride(self, stride: int) -> "FftConfig":
+        self.input_buffer_batch_stride = int(stride)
+        return self
+
+    def with_output_buffer_batch_stride(self, stride: int) -> "FftConfig":
+        self.output_buffer_batch_stride = int(stride)
+        return self
+
+    def with_zero_padding(self, axis: int, left: int, right: int) -> "FftConfig":
+        """Logical zero interval [left, right) on one axis (config.rs:1004-1025)."""
+        if not 0 <= axis < len(self.dimensions):
+            raise VkFftError(-7, f"InvalidZeroPaddingRange {{ axis: {axis}, left: {left}, right: {right}, length: 0 }}")
+        n = self.dimensions[axis]
+        if left > right or right > n:
+            raise VkFftError(-7, f"InvalidZeroPaddingRange {{ axis: {axis}, left: {left}, right: {right}, length: {n} }}")
+        self.zero_padding[axis] = (int(left), int(right)) if left != right else None
+        return self
+
+    def with_zero_padding_domain(self, domain: ZeroPaddingDomain) -> "FftConfig":
+        self.zero_padding_domain = ZeroPaddingDomain(domain)
+        return self
+
+    def with_grouped_batch(self, axis: int, grouped_batch: int) -> "FftConfig":
+        """configuration.groupedBatch[axis] override (config.rs:869-880); 0 clears."""
+        self.grouped_batch[self._axis(axis, "groupedBatch axis")] = int(grouped_batch)
         return self
 
     def validate(self):
@@ -265,7 +327,78 @@ class TransformIr:
         for i, (a, m) in enumerate(zip(self.axis_algorithms, self.convolution_lens)):
             d.axis_algorithm[i] = int(a)
             d.convolution_len[i] = m
+        for i in range(len(c.dimensions)):
+            d.in_axis_stride[i] = c.input_buffer_axis_strides[i]
+            d.out_axis_stride[i] = c.output_buffer_axis_strides[i]
+            d.grouped_batch[i] = c.grouped_batch[i]
+            if c.zero_padding[i] is not None:
+                d.zero_left[i], d.zero_right[i] = c.zero_padding[i]
+        d.in_batch_stride = c.input_buffer_batch_stride
+        d.out_batch_stride = c.output_buffer_batch_stride
+        d.zero_frequency = int(c.zero_padding_domain == ZeroPaddingDomain.Frequency)
         return d
+
+    # ---- formatted layouts (the host-side pack/unpack of the reference's
+    # runtime boundary, nd_ir.rs:1115-1150, 1191-1260)
+    def _side_dims(self, output: bool) -> List[int]:
+        c = self.config
+        dims = list(c.dimensions)
+        if (c.transform == TransformKind.RealToComplex and output) or \
+                (c.transform == TransformKind.ComplexToReal and not output):
+            dims[-1] = dims[-1] // 2 + 1
+        return dims
+
+    def _side_strides(self, output: bool):
+        """resolve_formatted_axis_strides / _batch_stride (config.rs:1463-1522)."""
+        c = self.config
+        dims = self._side_dims(output)
+        over = c.output_buffer_axis_strides if output else c.input_buffer_axis_strides
+        rank = len(dims)
+        if over[rank - 1] not in (0, 1):
+            raise VkFftError(-7, "formatted fastest-axis stride must remain one stored element")
+        st = [1] * rank
+        for ax in range(rank - 2, -1, -1):
+            minimum = st[ax + 1] * dims[ax + 1]
+            st[ax] = over[ax] or minimum
+            if st[ax] < minimum:
+                raise VkFftError(-7, "formatted axis stride overlaps the next faster logical axis")
+        b = (c.output_buffer_batch_stride if output else c.input_buffer_batch_stride) or st[0] * dims[0]
+        if b < st[0] * dims[0]:
+            raise VkFftError(-7, "formatted batch stride overlaps the logical tensor")
+        return dims, st, b
+
+    def _physical_index(self, output: bool) -> np.ndarray:
+        dims, st, b = self._side_strides(output)
+        idx = np.zeros((self.config.batch_count,) + tuple(dims), dtype=np.int64)
+        idx += (np.arange(self.config.batch_count) * b).reshape((-1,) + (1,) * len(dims))
+        for ax, (n, s) in enumerate(zip(dims, st)):
+            shape = [1] * (len(dims) + 1)
+            shape[ax + 1] = n
+            idx += (np.arange(n) * s).reshape(shape)
+        return idx.reshape(-1), self.config.batch_count * b
+
+    def is_formatted(self, output: bool) -> bool:
+        dims, st, b = self._side_strides(output)
+        dense = [int(np.prod(dims[ax + 1:])) for ax in range(len(dims))]
+        return st != dense or b != int(np.prod(dims))
+
+    def pack_input(self, x: np.ndarray) -> np.ndarray:
+        """Logical input -> the formatted physical buffer (gaps zero)."""
+        if not self.is_formatted(False):
+            return x
+        idx, n = self._physical_index(False)
+        out = np.zeros(n, dtype=x.dtype)
+        out[idx] = x
+        return out
+
+    def unpack_output(self, y: np.ndarray) -> np.ndarray:
+        if not self.is_formatted(True):
+            return y
+        idx, _ = self._physical_index(True)
+        return y[idx]
+
+    def physical_output_count(self) -> int:
+        return self._physical_index(True)[1] if self.is_formatted(True) else self.output_count()
 
     @property
     def real_dtype(self):
@@ -368,8 +501,9 @@ class TransformTicket:
         self._L = plan._L
         ir = plan.ir
         self._complex_out = np.dtype(out_dtype).kind == "c"
-        x = np.ascontiguousarray(ir.to_storage(x))
+        x = np.ascontiguousarray(ir.to_storage(ir.pack_input(x)))
         self._x = x  # kept alive until the submit has copied it
+        out_count = ir.physical_output_count()
         self._out = np.empty(out_count * (2 if self._complex_out else 1), dtype=ir.storage_scalar_dtype) \
             if ir.config.precision == Precision.F16StorageF32Compute else np.empty(out_count, dtype=out_dtype)
         self.handle = ctypes.c_void_p()
@@ -383,7 +517,8 @@ class TransformTicket:
     def wait(self) -> np.ndarray:
         _check(self._L.vkfx_ticket_wait(self.handle, self._out.ctypes.data, self._out.nbytes), self._L)
         self.close()
-        return self.plan.ir.from_storage(self._out, self._complex_out)
+        ir = self.plan.ir
+        return ir.unpack_output(ir.from_storage(self._out, self._complex_out))
 
     def close(self):
         if self.handle:
@@ -433,9 +568,12 @@ class HipExecutionContext:
         return self.device_profile()["name"]
 
     def plan(self, ir: TransformIr) -> Plan:
-        key = (tuple(ir.config.dimensions), ir.config.batch_count, int(ir.config.precision),
-               int(ir.config.transform), ir.config.normalize_inverse, int(ir.direction),
-               tuple(int(a) for a in ir.axis_algorithms), tuple(ir.convolution_lens))
+        c = ir.config
+        key = (tuple(c.dimensions), c.batch_count, int(c.precision), int(c.transform), c.normalize_inverse,
+               int(ir.direction), tuple(int(a) for a in ir.axis_algorithms), tuple(ir.convolution_lens),
+               tuple(c.input_buffer_axis_strides), tuple(c.output_buffer_axis_strides),
+               c.input_buffer_batch_stride, c.output_buffer_batch_stride, tuple(c.zero_padding),
+               int(c.zero_padding_domain), tuple(c.grouped_batch))
         if key not in self._plans:
             self._plans[key] = Plan(self, ir)
         return self._plans[key]
@@ -445,13 +583,17 @@ class HipExecutionContext:
         if x.size != ir.input_count():
             raise VkFftError(-5, f"InputLengthMismatch {{ expected: {ir.input_count()}, actual: {x.size} }}")
         plan = self.plan(ir)
-        xs = np.ascontiguousarray(ir.to_storage(x))
+        xs = np.ascontiguousarray(ir.to_storage(ir.pack_input(x)))
+        logical_count = out_count
+        out_count = ir.physical_output_count()
         complex_out = np.dtype(out_dtype).kind == "c"
         out = np.empty(out_count * (2 if complex_out else 1), dtype=ir.storage_scalar_dtype) \
             if ir.config.precision == Precision.F16StorageF32Compute else np.empty(out_count, dtype=out_dtype)
         _check(self._L.vkfx_execute_host(plan.handle, xs.ctypes.data, xs.nbytes, out.ctypes.data, out.nbytes),
                self._L)
-        return ir.from_storage(out, complex_out)
+        y = ir.unpack_output(ir.from_storage(out, complex_out))
+        assert y.size == logical_count
+        return y
 
     def execute_transform(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
         kind = ir.config.transform
@@ -483,14 +625,16 @@ class HipExecutionContext:
         plans = [self.plan(ir) for ir in irs]
         in_dt, _ = self._io_dtypes(irs[0])
         _, out_dt = self._io_dtypes(irs[-1])
-        x = np.ascontiguousarray(irs[0].to_storage(np.ascontiguousarray(x, dtype=in_dt).reshape(-1)))
+        x = np.ascontiguousarray(irs[0].to_storage(irs[0].pack_input(np.ascontiguousarray(x, dtype=in_dt)
+                                                                                 .reshape(-1))))
         last = irs[-1]
         complex_out = np.dtype(out_dt).kind == "c"
-        out = np.empty(last.output_count() * (2 if complex_out else 1), dtype=last.storage_scalar_dtype) \
-            if last.config.precision == Precision.F16StorageF32Compute else np.empty(last.output_count(), dtype=out_dt)
+        n_out = last.physical_output_count()
+        out = np.empty(n_out * (2 if complex_out else 1), dtype=last.storage_scalar_dtype) \
+            if last.config.precision == Precision.F16StorageF32Compute else np.empty(n_out, dtype=out_dt)
         _check(self._L.vkfx_execute_chain_host(_plan_array(plans), len(plans), x.ctypes.data, x.nbytes,
                                              out.ctypes.data, out.nbytes), self._L)
-        return last.from_storage(out, complex_out)
+        return last.unpack_output(last.from_storage(out, complex_out))
 
     def execute_transform_f32(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
         if not _f32_family(ir.config.precision):
