@@ -43,7 +43,23 @@ enum vkfx_status {
     VKFX_ERR_ARITHMETIC_OVERFLOW = -8      /* ArithmeticOverflow */
 };
 
-enum vkfx_transform { VKFX_C2C = 0, VKFX_R2C = 1, VKFX_C2R = 2 }; /* TransformKind, config.rs */
+/* TransformKind (src/config.rs:35-41); DCT / DST types I-IV are FFTW's
+ * REDFT00/10/01/11 and RODFT00/10/01/11 (src/r2r_ir.rs:2351-2434), real in
+ * and real out, both directions (inverse = the type's inverse partner, scaled
+ * by 1/2(N-1), 1/2(N+1) or 1/2N when normalized; r2r_ir.rs:2318-2346). */
+enum vkfx_transform {
+    VKFX_C2C = 0,
+    VKFX_R2C = 1,
+    VKFX_C2R = 2,
+    VKFX_DCT_I = 3,
+    VKFX_DCT_II = 4,
+    VKFX_DCT_III = 5,
+    VKFX_DCT_IV = 6,
+    VKFX_DST_I = 7,
+    VKFX_DST_II = 8,
+    VKFX_DST_III = 9,
+    VKFX_DST_IV = 10
+};
 /* Precision (src/config.rs:108-145). The caller's buffers hold the storage
  * type; the FFT passes run on the compute type. Mixed layouts convert on the
  * device into and out of the plan's workspace. */

@@ -42,6 +42,7 @@ def lib():
                                     ctypes.c_int]
         L.vko_r2c_batch.argtypes = [_c_double_p, _c_double_p, sz, sz, ctypes.c_int]
         L.vko_c2r_batch.argtypes = [_c_double_p, _c_double_p, sz, sz, ctypes.c_int, ctypes.c_int]
+        L.vko_r2r_batch.argtypes = [_c_double_p, _c_double_p, sz, sz, ctypes.c_int, ctypes.c_int]
         L.vko_fft_nd.argtypes = [_c_double_p, _c_double_p, _c_size_p, sz, sz, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_int]
         L.vko_next_smooth_at_least.argtypes = [sz, _c_size_p, sz]
@@ -127,6 +128,18 @@ def c2r_batch(x, n: int, normalize=False, threads=1) -> np.ndarray:
     batch = x.size // h
     out = np.empty(batch * n, dtype=np.float64)
     _check(lib().vko_c2r_batch(_dp(x), _dp(out), n, batch, int(normalize), int(threads)), "c2r")
+    return out
+
+
+R2R_KINDS = {"dct1": 0, "dct2": 1, "dct3": 2, "dct4": 3, "dst1": 4, "dst2": 5, "dst3": 6, "dst4": 7}
+
+
+def r2r_batch(x, n: int, kind: str, threads=1) -> np.ndarray:
+    """Direct DCT/DST (FFTW REDFT/RODFT, unnormalized; src/r2r_ir.rs:2351-2434)."""
+    x = np.ascontiguousarray(x, dtype=np.float64).reshape(-1)
+    batch = x.size // n
+    out = np.empty(batch * n, dtype=np.float64)
+    _check(lib().vko_r2r_batch(_dp(x), _dp(out), n, batch, R2R_KINDS[kind], int(threads)), "r2r")
     return out
 
 

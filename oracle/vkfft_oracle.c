@@ -285,16 +285,61 @@ int vko_fft(const double *in, double *out, size_t n, int sign, int normalize) {
 /* ------------------------------------------------------- batch drivers */
 
 typedef struct {
-    int kind; /* 0 c2c, 1 r2c, 2 c2r */
+    int kind; /* 0 c2c, 1 r2c, 2 c2r, 3 r2r (sign = DCT/DST kind) */
     const double *in;
     double *out;
     size_t n, first, last;
     int sign, normalize, rc;
 } job_t;
 
+/* One DCT/DST bin, FFTW's unnormalized definitions (src/r2r_ir.rs:2351-2434).
+ * kind 0..3 DCT-I..IV (REDFT00/10/01/11), 4..7 DST-I..IV (RODFT00/10/01/11). */
+static double r2r_bin(int kind, const double *x, size_t n, size_t k) {
+    double sum = 0.0;
+    const double dk = (double)k;
+    switch (kind) {
+        case 0: /* REDFT00 */
+            sum = x[0] + ((k % 2 == 0) ? x[n - 1] : -x[n - 1]);
+            for (size_t j = 1; j + 1 < n; ++j) sum += 2.0 * x[j] * cos(VKO_PI * (double)j * dk / (double)(n - 1));
+            return sum;
+        case 1: /* REDFT10 */
+            for (size_t j = 0; j < n; ++j) sum += 2.0 * x[j] * cos(VKO_PI * ((double)j + 0.5) * dk / (double)n);
+            return sum;
+        case 2: /* REDFT01 */
+            sum = x[0];
+            for (size_t j = 1; j < n; ++j) sum += 2.0 * x[j] * cos(VKO_PI * (double)j * (dk + 0.5) / (double)n);
+            return sum;
+        case 3: /* REDFT11 */
+            for (size_t j = 0; j < n; ++j)
+                sum += 2.0 * x[j] * cos(VKO_PI * ((double)j + 0.5) * (dk + 0.5) / (double)n);
+            return sum;
+        case 4: /* RODFT00 */
+            for (size_t j = 0; j < n; ++j)
+                sum += 2.0 * x[j] * sin(VKO_PI * (double)(j + 1) * (double)(k + 1) / (double)(n + 1));
+            return sum;
+        case 5: /* RODFT10 */
+            for (size_t j = 0; j < n; ++j)
+                sum += 2.0 * x[j] * sin(VKO_PI * ((double)j + 0.5) * (double)(k + 1) / (double)n);
+            return sum;
+        case 6: /* RODFT01 */
+            sum = (k % 2 == 0) ? x[n - 1] : -x[n - 1];
+            for (size_t j = 0; j + 1 < n; ++j)
+                sum += 2.0 * x[j] * sin(VKO_PI * (double)(j + 1) * (dk + 0.5) / (double)n);
+            return sum;
+        default: /* RODFT11 */
+            for (size_t j = 0; j < n; ++j)
+                sum += 2.0 * x[j] * sin(VKO_PI * ((double)j + 0.5) * (dk + 0.5) / (double)n);
+            return sum;
+    }
+}
+
 static int run_one(job_t *j, size_t t) {
     size_t n = j->n, h = n / 2 + 1;
     if (j->kind == 0) return vko_fft(j->in + 2 * n * t, j->out + 2 * n * t, n, j->sign, j->normalize);
+    if (j->kind == 3) {
+        for (size_t k = 0; k < n; ++k) j->out[n * t + k] = r2r_bin(j->sign, j->in + n * t, n, k);
+        return 0;
+    }
     cplx *buf = (cplx *)calloc(n * 2, sizeof(cplx));
     if (!buf) return -1;
     cplx *full = buf, *res = buf + n;
@@ -371,6 +416,12 @@ static int run_batch(int kind, const double *in, double *out, size_t n, size_t b
 int vko_fft_batch(const double *in, double *out, size_t n, size_t batch, int sign, int normalize,
                   int threads) {
     return run_batch(0, in, out, n, batch, sign, normalize, threads);
+}
+
+int vko_r2r_batch(const double *in, double *out, size_t n, size_t batch, int kind, int threads) {
+    if (kind < 0 || kind > 7) return -1;
+    if (kind == 0 && n < 2) return -1; /* DCT-I needs two points */
+    return run_batch(3, in, out, n, batch, kind, 0, threads);
 }
 
 int vko_r2c_batch(const double *in, double *out, size_t n, size_t batch, int threads) {

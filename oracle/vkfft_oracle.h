@@ -43,6 +43,12 @@ int vko_c2r_batch(const double *in, double *out, size_t n, size_t batch, int nor
 /* Separable N-D C2C (src/nd_ir.rs:1303-1337): axes processed last to first,
  * each line packed, transformed with vko_fft and scattered back. dims are in
  * vkfft-rs order (slowest to fastest). */
+/* Direct DCT/DST bins, FFTW REDFT00/10/01/11 and RODFT00/10/01/11
+ * (src/r2r_ir.rs:2351-2434 evaluate_bin), unnormalized; kind 0..3 = DCT-I..IV,
+ * 4..7 = DST-I..IV. O(N^2) per line, batch lines back to back, threads > 1
+ * splits the batch. */
+int vko_r2r_batch(const double *in, double *out, size_t n, size_t batch, int kind, int threads);
+
 int vko_fft_nd(const double *in, double *out, const size_t *dims, size_t rank, size_t batch,
                int sign, int normalize, int threads);
 

@@ -181,3 +181,35 @@ def test_precision_metrics_follow_reference_definition():
     m = o.precision_metrics([1 + 0j, 2, 0], [1 + 0j, 1, 0])
     assert m["max_difference"] == 1 and m["avg_difference"] == pytest.approx(1 / 3)
     assert m["max_eps"] == 1 and m["avg_eps"] == pytest.approx(1 / 3)
+
+
+@pytest.mark.parametrize("kind", ["dct1", "dct2", "dct3", "dct4", "dst1", "dst2", "dst3", "dst4"])
+@pytest.mark.parametrize("n", [2, 3, 7, 16, 33, 100])
+def test_r2r_matches_scipy(kind, n):
+    """The oracle's DCT/DST bins (r2r_ir.rs:2351-2434, FFTW REDFT/RODFT) against
+    scipy.fft (pocketfft, FFTW's unnormalized conventions), a library routine."""
+    import scipy.fft as sf
+    if kind == "dct1" and n < 2:
+        pytest.skip("DCT-I needs two points")
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((3, n))
+    t = int(kind[-1])
+    ref = (sf.dct if kind.startswith("dct") else sf.dst)(x, type=t, axis=1)
+    got = o.r2r_batch(x, n, kind, threads=2).reshape(3, n)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-12 * n)
+
+
+def test_r2r_inverse_pairs_and_closed_forms():
+    """DCT-II/III and DST-II/III are inverse pairs up to 2N; DCT-I, DCT-IV,
+    DST-I, DST-IV are their own inverses up to 2(N-1), 2N, 2(N+1), 2N
+    (inverse_pair_scale, r2r_ir.rs:2318-2346); a constant input has DCT-II
+    2N at bin 0 and zero elsewhere."""
+    n = 12
+    x = np.random.default_rng(1).standard_normal(n)
+    for fwd, inv, den in [("dct2", "dct3", 2 * n), ("dct3", "dct2", 2 * n), ("dst2", "dst3", 2 * n),
+                          ("dst3", "dst2", 2 * n), ("dct1", "dct1", 2 * (n - 1)), ("dct4", "dct4", 2 * n),
+                          ("dst1", "dst1", 2 * (n + 1)), ("dst4", "dst4", 2 * n)]:
+        y = o.r2r_batch(o.r2r_batch(x, n, fwd), n, inv) / den
+        np.testing.assert_allclose(y, x, rtol=0, atol=1e-12)
+    c = o.r2r_batch(np.ones(n), n, "dct2")
+    assert abs(c[0] - 2 * n) < 1e-12 and np.max(np.abs(c[1:])) < 1e-12

@@ -134,4 +134,17 @@ struct BoundaryArgs {
 };
 int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_t s);
 
+// DCT / DST pre and post passes around a length-L complex FFT (r2r.hip):
+//   a[m] = w(m) x[m - off] exp(-i pi m ph / (2n))  (m - off in [0, n), else 0)
+//   X[k] = s * (im ? -Im : Re)(exp(-i pi (k + q2/2) pq / (2n)) A[k + r])
+// wmode: 0 all 1; 1 DCT-I ends 1, else 2; 2 DCT-III first 1, else 2;
+// 3 DST-III m == n 1, else 2.
+struct R2rArgs {
+    long long n = 0, L = 0, batch = 0;
+    int off = 0, ph = 0, wmode = 0;
+    int r = 0, pq = 0, q2 = 0, im = 0;
+    double s = 1.0;
+};
+int launch_r2r(bool pre, int prec, const R2rArgs& p, const void* in, void* out, hipStream_t s);
+
 }  // namespace vkfx

@@ -101,6 +101,9 @@ struct Launch {
     // layouts, zero padding; convert.hip)
     bool boundary = false;
     BoundaryArgs ba;
+    // DCT / DST pre (1) or post (2) pass instead of an FFT kernel (r2r.hip)
+    int r2r = 0;
+    R2rArgs ra;
 };
 
 // Line geometry of one FFT length inside a kernel.
@@ -458,6 +461,10 @@ struct Ctx {
 void note_pass(Ctx& c, const Launch& L) {
     if (!c.first_pass) c.js << ",";
     c.first_pass = false;
+    if (L.r2r) {
+        c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.ra.L << ",\"len\":" << L.ra.n << "}";
+        return;
+    }
     if (L.boundary) {
         static const char* kType[] = {"f16", "f32", "f64"};
         bool zero = false, strided = false;
@@ -1049,6 +1056,83 @@ int plan_real_full_complex(Ctx& c, size_t n, size_t batch, bool r2c, bool normal
     return VKFX_OK;
 }
 
+// DCT / DST of length n as one complex FFT of length L between a pre and a
+// post pass (r2r.hip). Parameters per effective type, with every cosine or
+// sine sum written as the real or imaginary part of a zero-padded DFT:
+//   DCT-I   L = 2(n-1): a_j = w_j x_j (w = 1 at the ends, 2 inside), X_k = Re A_k
+//   DCT-II  L = 2n:     a_j = x_j, X_k = 2 Re(e^{-i pi k/2n} A_k)
+//   DCT-III L = 2n:     a_j = w_j x_j e^{-i pi j/2n} (w_0 = 1, else 2), X_k = Re A_k
+//   DCT-IV  L = 2n:     a_j = x_j e^{-i pi j/2n}, X_k = 2 Re(e^{-i pi (k+1/2)/2n} A_k)
+//   DST-I   L = 2(n+1): a_{j+1} = x_j, X_k = -2 Im A_{k+1}
+//   DST-II  L = 2n:     a_j = x_j, X_k = -2 Im(e^{-i pi (k+1)/2n} A_{k+1})
+//   DST-III L = 2n:     a_{j+1} = w x_j e^{-i pi (j+1)/2n} (w = 2, 1 at j = n-1), X_k = -Im A_k
+//   DST-IV  L = 2n:     a_j = x_j e^{-i pi j/2n}, X_k = -2 Im(e^{-i pi (k+1/2)/2n} A_k)
+// The inverse direction runs the type's inverse partner (II <-> III,
+// r2r_ir.rs:2308-2316), scaled when normalized (inverse_pair_scale,
+// r2r_ir.rs:2318-2346).
+int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize) {
+    vkfx_plan* p = c.p;
+    // kind: 0..3 DCT-I..IV, 4..7 DST-I..IV
+    int eff = kind;
+    if (dir > 0) {
+        if (kind == 1) eff = 2;
+        else if (kind == 2) eff = 1;
+        else if (kind == 5) eff = 6;
+        else if (kind == 6) eff = 5;
+    }
+    double scale = 1.0;
+    if (dir > 0 && normalize) {
+        const double den = kind == 0 ? 2.0 * (double)(n - 1) : kind == 4 ? 2.0 * (double)(n + 1) : 2.0 * (double)n;
+        scale = 1.0 / den;
+    }
+    R2rArgs a;
+    a.n = (long long)n;
+    a.batch = (long long)batch;
+    switch (eff) {
+        case 0: a.L = 2 * (a.n - 1); a.wmode = 1; break;
+        case 1: a.L = 2 * a.n; a.pq = 1; a.s = 2.0; break;
+        case 2: a.L = 2 * a.n; a.ph = 1; a.wmode = 2; break;
+        case 3: a.L = 2 * a.n; a.ph = 1; a.pq = 1; a.q2 = 1; a.s = 2.0; break;
+        case 4: a.L = 2 * (a.n + 1); a.off = 1; a.r = 1; a.im = 1; a.s = 2.0; break;
+        case 5: a.L = 2 * a.n; a.r = 1; a.pq = 1; a.q2 = 2; a.im = 1; a.s = 2.0; break;
+        case 6: a.L = 2 * a.n; a.off = 1; a.ph = 1; a.wmode = 3; a.im = 1; break;
+        default: a.L = 2 * a.n; a.ph = 1; a.pq = 1; a.q2 = 1; a.im = 1; a.s = 2.0; break;
+    }
+    a.s *= scale;
+    const size_t L = (size_t)a.L;
+    const bool f64 = c.prec == 1;
+    AxisDecision ad = plan_c2c_axis(L, batch, f64, false, tuning_for_amd(f64),
+                                    planner_device(p->ctx->profile.shared_memory_bytes));
+    p->full_bytes = batch * L * csize(c.prec);
+    p->serial = true;
+    static const char* kNames[] = {"dct1", "dct2", "dct3", "dct4", "dst1", "dst2", "dst3", "dst4"};
+    c.js << "\"r2r\":{\"type\":\"" << kNames[kind] << "\",\"runs\":\"" << kNames[eff] << "\",\"fft_len\":" << L
+         << ",\"c2c\":\""
+         << (ad.algorithm == Algorithm::Stockham ? "stockham" : ad.algorithm == Algorithm::Rader ? "rader" : "bluestein")
+         << "\"},";
+    Launch pre{};
+    pre.r2r = 1;
+    pre.ra = a;
+    pre.label = "r2r_pre";
+    pre.in_sel = SEL_IN, pre.out_sel = SEL_FULL;
+    p->launches.push_back(pre);
+    const size_t first = p->launches.size();
+    int rc = plan_c2c_1d(c, L, batch, -1, false, ad.algorithm,
+                         ad.algorithm == Algorithm::Bluestein ? ad.convolution_len : 0);
+    if (rc) return rc;
+    for (size_t i = first; i < p->launches.size(); ++i) {
+        Launch& L2 = p->launches[i];
+        if (L2.in_sel == SEL_IN || L2.in_sel == SEL_OUT) L2.in_sel = SEL_FULL;
+        if (L2.out_sel == SEL_IN || L2.out_sel == SEL_OUT) L2.out_sel = SEL_FULL;
+    }
+    Launch post = pre;
+    post.r2r = 2;
+    post.label = "r2r_post";
+    post.in_sel = SEL_FULL, post.out_sel = SEL_OUT;
+    p->launches.push_back(post);
+    return VKFX_OK;
+}
+
 int plan_r2c(Ctx& c, size_t n, size_t batch) {
     vkfx_plan* p = c.p;
     const int prec = c.prec;
@@ -1326,9 +1410,13 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         return fail(VKFX_ERR_INVALID_ARGUMENT, "R2C requires Direction::Forward");
     if (d.transform == VKFX_C2R && d.direction != VKFX_INVERSE)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "C2R requires Direction::Inverse");
-    if (d.transform < VKFX_C2C || d.transform > VKFX_C2R) return fail(VKFX_ERR_INVALID_ARGUMENT, "unknown transform");
+    if (d.transform < VKFX_C2C || d.transform > VKFX_DST_IV) return fail(VKFX_ERR_INVALID_ARGUMENT, "unknown transform");
+    const bool r2r = d.transform >= VKFX_DCT_I;
     if (d.transform != VKFX_C2C && d.rank != 1)
-        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "multi-dimensional R2C/C2R is outside this path");
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                    r2r ? "multi-dimensional DCT/DST is outside this path" : "multi-dimensional R2C/C2R is outside this path");
+    if (d.transform == VKFX_DCT_I && d.dims[0] < 2)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "InvalidTransformLength { axis: 0, transform: DCT-I, length: 1 }");
     // storage and compute scalar types (0 f16, 1 f32, 2 f64)
     const bool f64 = d.precision == VKFX_F64 || d.precision == VKFX_F64_COMPUTE_F32_STORAGE;
     const int store_t = d.precision == VKFX_F16_STORAGE_F32_COMPUTE ? 0 : d.precision == VKFX_F64 ? 2 : 1;
@@ -1368,7 +1456,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     for (uint32_t i = 0; i < d.rank; ++i) c.js << (i ? "," : "") << d.dims[i];
     static const char* kPrecName[] = {"f32", "f64", "f16_storage_f32_compute", "f64_compute_f32_storage"};
     c.js << "],\"batch\":" << d.batch << ",\"precision\":\"" << kPrecName[d.precision] << "\",\"transform\":\""
-         << (d.transform == VKFX_C2C ? "c2c" : d.transform == VKFX_R2C ? "r2c" : "c2r") << "\",\"axes\":[";
+         << (d.transform == VKFX_C2C ? "c2c" : d.transform == VKFX_R2C ? "r2c" : d.transform == VKFX_C2R ? "c2r" : "r2r")
+         << "\",\"axes\":[";
     for (uint32_t i = 0; i < d.rank; ++i) {
         const int alg = d.axis_algorithm[i];
         c.js << (i ? "," : "") << "{\"len\":" << d.dims[i] << ",\"algorithm\":\""
@@ -1392,6 +1481,10 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             } else {
                 rc = plan_c2c_nd(c, d);
             }
+        } else if (r2r) {
+            const size_t n = d.dims[0];
+            p->in_bytes = p->out_bytes = d.batch * n * rs;
+            rc = plan_r2r(c, n, d.batch, d.transform - VKFX_DCT_I, d.direction, d.normalize != 0);
         } else if (d.transform == VKFX_R2C) {
             const size_t n = d.dims[0];
             p->in_bytes = d.batch * n * rs;
@@ -1414,7 +1507,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         // Boundary passes: type conversion (mixed precisions), formatted
         // layouts and zero padding sit between the caller's buffers and dense
         // compute-type copies in the workspace that the FFT passes use.
-        const bool real_in = d.transform == VKFX_R2C, real_out = d.transform == VKFX_C2R;
+        const bool real_in = d.transform == VKFX_R2C || r2r, real_out = d.transform == VKFX_C2R || r2r;
         const size_t rank = d.rank;
         long long in_dims[VKFX_MAX_RANK], out_dims[VKFX_MAX_RANK];
         for (size_t i = 0; i < rank; ++i) in_dims[i] = out_dims[i] = (long long)d.dims[i];
@@ -1621,7 +1714,7 @@ int vkfx_plan_describe(const vkfx_plan* plan, char* buf, size_t cap) {
 int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, void* stream) {
     if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
     if (!d_in || !d_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null device buffer");
-    if (plan->desc.transform != VKFX_C2C && d_in == d_out)
+    if ((plan->desc.transform == VKFX_R2C || plan->desc.transform == VKFX_C2R) && d_in == d_out)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "R2C/C2R cannot run in place");
     void* work = d_work ? d_work : plan->work.p;
     if (plan->work_bytes && !work) return fail(VKFX_ERR_INVALID_ARGUMENT, "plan needs a workspace");
@@ -1648,6 +1741,11 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
                                                      : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };
+        if (L.r2r) {
+            int e = launch_r2r(L.r2r == 1, prec, L.ra, sel(L.in_sel, 0), sel(L.out_sel, 0), lane_stream[lane]);
+            if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
+            continue;
+        }
         if (L.boundary) {
             int e = launch_boundary(L.ba, sel(L.in_sel, 0), sel(L.out_sel, 0), lane_stream[lane]);
             if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());

@@ -56,9 +56,31 @@ class Direction(enum.IntEnum):
 
 
 class TransformKind(enum.IntEnum):
+    """TransformKind (config.rs:35-41); Dct(DctType::I..IV) and Dst(DstType::I..IV)
+    are flattened to one value each."""
     ComplexToComplex = 0
     RealToComplex = 1
     ComplexToReal = 2
+    DctI = 3
+    DctII = 4
+    DctIII = 5
+    DctIV = 6
+    DstI = 7
+    DstII = 8
+    DstIII = 9
+    DstIV = 10
+
+    @staticmethod
+    def dct(t: int) -> "TransformKind":
+        return TransformKind(2 + t)
+
+    @staticmethod
+    def dst(t: int) -> "TransformKind":
+        return TransformKind(6 + t)
+
+    @property
+    def is_r2r(self) -> bool:
+        return self >= TransformKind.DctI
 
 
 class Precision(enum.IntEnum):
@@ -597,6 +619,8 @@ class HipExecutionContext:
 
     def execute_transform(self, ir: TransformIr, x: np.ndarray) -> np.ndarray:
         kind = ir.config.transform
+        if kind.is_r2r:
+            return self._execute_host(ir, x, ir.real_dtype, ir.real_dtype, ir.output_count())
         if kind == TransformKind.RealToComplex:
             return self._execute_host(ir, x, ir.real_dtype, ir.complex_dtype, ir.output_count())
         if kind == TransformKind.ComplexToReal:
@@ -605,6 +629,8 @@ class HipExecutionContext:
 
     def _io_dtypes(self, ir: TransformIr):
         kind = ir.config.transform
+        if kind.is_r2r:
+            return ir.real_dtype, ir.real_dtype
         if kind == TransformKind.RealToComplex:
             return ir.real_dtype, ir.complex_dtype
         if kind == TransformKind.ComplexToReal:
