@@ -128,6 +128,25 @@ typedef struct {
     uint64_t zero_right[VKFX_MAX_RANK];
     int32_t zero_frequency;                 /* ZeroPaddingDomain::Frequency */
     uint32_t grouped_batch[VKFX_MAX_RANK];  /* groupedBatch override (0 = automatic), a scheduling hint */
+    /* Convolution, C2C only (FftConfig::with_convolution and the convolution knobs,
+     * src/config.rs:595-800; ConvolutionIr / NdConvolutionIr, src/convolution_ir.rs):
+     * forward FFT of every [batch][coordinate] tensor, multiply by the kernel
+     * spectrum, normalized inverse FFT. The input holds batch x coordinates
+     * tensors; the output holds kernel_count x coordinates tensors when
+     * kernel_count > 1 (one-input fan-out, batch must be 1), else batch x
+     * coordinates. kernel_spectrum: host complex values of the compute precision,
+     * laid out [kernel][plane][tensor], planes = M*M (matrix), M(M+1)/2 (symmetric
+     * matrix), coordinates (independent_coordinates) or 1; copied at plan time. */
+    int32_t perform_convolution;
+    int32_t conjugate_sequence;             /* ConvolutionConjugation::Sequence */
+    int32_t cross_power_normalize;          /* cross_power_spectrum_normalization */
+    uint32_t coordinate_features;           /* 0 or 1 = one coordinate */
+    uint32_t matrix_convolution;            /* 0 or 1 = none; 2 or 3 = M x M matrix */
+    int32_t symmetric_kernel;
+    int32_t independent_coordinates;
+    uint32_t kernel_count;                  /* 0 or 1 = one kernel */
+    const void *kernel_spectrum;
+    uint64_t kernel_spectrum_bytes;
 } vkfx_plan_desc;
 
 /* ---------------------------------------------------------------- context */
@@ -148,6 +167,7 @@ int vkfx_context_profile(const vkfx_context *ctx, vkfx_device_profile *out);
  * 2109-2195): builds the kernel-launch list, uploads twiddle/chirp/spectrum
  * tables and allocates the plan's workspace once. */
 int vkfx_plan_create(vkfx_context *ctx, const vkfx_plan_desc *desc, vkfx_plan **out);
+/* Destroy every plan before the context it was created on. */
 int vkfx_plan_destroy(vkfx_plan *plan);
 
 /* Byte sizes of one execute's input and output buffers, and of the scratch

@@ -153,6 +153,63 @@ def fft_nd(x, dims, batch=1, direction="forward", normalize=False, threads=1) ->
     return out
 
 
+def conv_plane_index(m: int, symmetric: bool, out_coord: int, in_coord: int) -> int:
+    """ConvolutionMatrixLayout::kernel_plane_index (src/convolution_ir.rs:128-147):
+    row-major M*M planes, or the upper triangle row by row when symmetric."""
+    if not symmetric:
+        return out_coord * m + in_coord
+    j, l = out_coord, in_coord
+    return l * m - l * l + j if l < j else j * m - j * j + l
+
+
+def convolution(x, spectrum, dims, batch=1, matrix=0, symmetric=False, kernel_count=1,
+                conj_sequence=False, cross_power=False, threads=1, backend="oracle") -> np.ndarray:
+    """performConvolution (execute_convolution_ir / execute_nd_convolution_ir,
+    src/convolution_ir.rs:4252-4440): forward FFT of every [system][coordinate]
+    tensor, multiply by the kernel spectrum [kernel][plane][tensor]
+    (ConvolutionMultiplyPolicy::apply, :58-80: conj of the sequence, then
+    division by the modulus with no zero guard), normalized inverse FFT.
+    A matrix layout sums over input coordinates and normalizes the row sum.
+    backend "numpy" runs the two transforms with numpy.fft (pocketfft) instead
+    of the oracle's restatement, for f64 checks below the oracle's own error."""
+    dims = list(dims)
+    t = int(np.prod(dims))
+    coords = matrix if matrix else 1
+    x = _as_c128(x).reshape(-1)
+    k = _as_c128(spectrum).reshape(-1)
+    nd = len(dims) > 1
+
+    def transform(v, systems, direction, normalize):
+        if backend == "numpy":
+            a = v.reshape((systems,) + tuple(dims))
+            axes = tuple(range(1, len(dims) + 1))
+            r = np.fft.fftn(a, axes=axes) if direction == "forward" else np.fft.ifftn(a, axes=axes)
+            return r.reshape(-1)
+        if nd:
+            return fft_nd(v, dims, systems, direction, normalize, threads)
+        return fft_batch(v, dims[0], direction, normalize, threads)
+
+    spec = transform(x, batch * coords, "forward", False).reshape(batch, coords, t)
+    out_systems = kernel_count if kernel_count > 1 else batch
+    planes = (matrix * (matrix + 1) // 2 if symmetric else matrix * matrix) if matrix else 1
+    kern = k.reshape(kernel_count, planes, t)
+    seq = np.conj(spec) if conj_sequence else spec
+    prod = np.zeros((out_systems, coords, t), dtype=np.complex128)
+    for s in range(out_systems):
+        s_in, kid = (0, s) if kernel_count > 1 else (s, 0)
+        for o in range(coords):
+            if matrix:
+                acc = np.zeros(t, dtype=np.complex128)
+                for i in range(coords):
+                    acc += seq[s_in, i] * kern[kid, conv_plane_index(matrix, symmetric, o, i)]
+            else:
+                acc = seq[s_in, o] * kern[kid, 0]
+            if cross_power:
+                acc = acc * (1.0 / np.sqrt(acc.real ** 2 + acc.imag ** 2))
+            prod[s, o] = acc
+    return transform(prod.reshape(-1), out_systems * coords, "inverse", True)
+
+
 def next_smooth_at_least(target: int, primes=(2, 3, 5, 7)) -> int:
     p = (ctypes.c_size_t * len(primes))(*primes)
     return int(lib().vko_next_smooth_at_least(target, p, len(primes)))

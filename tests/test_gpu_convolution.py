@@ -1,0 +1,167 @@
+"""performConvolution through the C ABI (ConvolutionIr / NdConvolutionIr,
+src/convolution_ir.rs:2583-3110, 3642-3760; multiply rules :4252-4440;
+ownership rules of FftConfig::validate, src/config.rs:1156-1300): forward C2C,
+kernel-spectrum multiply, normalized inverse C2C, against the oracle's
+restatement (itself pinned to brute-force circular convolution)."""
+import numpy as np
+import pytest
+
+import vkfft_amd as vk
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = vk.Precision.F32, vk.Precision.F64
+# two chained transforms (forward, normalized inverse), each within the
+# transform bar of 1e-5 (f32) or 1e-13 (f64)
+TOL = {F32: 1e-5, F64: 2e-13}
+
+
+def conv_cfg(dims, batch, prec, matrix=1, symmetric=False, kernels=1, conj=False, cross=False):
+    c = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec).with_convolution(True) \
+        .with_convolution_kernel_count(kernels)
+    if matrix > 1:
+        c = c.with_matrix_convolution(matrix).with_symmetric_convolution_kernel(symmetric)
+    if conj:
+        c = c.with_convolution_conjugation(vk.ConvolutionConjugation.Sequence)
+    if cross:
+        c = c.with_cross_power_spectrum_normalization(True)
+    return c
+
+
+def planes(matrix, symmetric):
+    if matrix <= 1:
+        return 1
+    return matrix * (matrix + 1) // 2 if symmetric else matrix * matrix
+
+
+def run_case(ctx, dims, batch, prec, matrix=1, symmetric=False, kernels=1, conj=False, cross=False, seed=0):
+    t = int(np.prod(dims))
+    coords = matrix if matrix > 1 else 1
+    dt = np.complex64 if prec == F32 else np.complex128
+    x = o.complex_uniform(batch * coords * t, 100 + seed, dt)
+    k = o.complex_uniform(kernels * planes(matrix, symmetric) * t, 200 + seed, dt)
+    conv = vk.ConvolutionIr.build(conv_cfg(dims, batch, prec, matrix, symmetric, kernels, conj, cross), k)
+    y = ctx.execute_convolution(conv, x)
+    # f64 against pocketfft transforms: the oracle's own f64 error is near 1e-13
+    ref = o.convolution(x, k, dims, batch, matrix if matrix > 1 else 0, symmetric, kernels, conj, cross, threads=8,
+                        backend="numpy" if prec == F64 else "oracle")
+    assert y.size == conv.output_count() == ref.size
+    err = o.rel_l2(y, ref)
+    assert err <= TOL[prec], (dims, batch, prec, matrix, kernels, err)
+    return conv, x, y
+
+
+@pytest.mark.parametrize("dims,batch,prec", [([1024], 8, F32), ([2048], 4, F64), ([4099], 3, F32),
+                                             ([1009], 2, F64), ([1 << 20], 1, F32), ([360], 5, F32),
+                                             ([64, 48], 2, F32), ([16, 12, 10], 2, F64), ([256, 256], 1, F32)])
+def test_scalar_kernel(hip_ctx, dims, batch, prec):
+    conv, _, _ = run_case(hip_ctx, dims, batch, prec)
+    desc = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    labels = [p["kernel"] for p in desc["passes"]]
+    assert "convolution_multiply" in labels
+    assert desc["convolution"]["kernels"] == 1 and desc["convolution"]["matrix"] == 0
+
+
+@pytest.mark.parametrize("dims,prec", [([1024], F32), ([4099], F32), ([32, 40], F64)])
+def test_multi_kernel_fan_out(hip_ctx, dims, prec):
+    run_case(hip_ctx, dims, 1, prec, kernels=3, seed=1)
+
+
+@pytest.mark.parametrize("matrix,symmetric,batch,kernels,prec",
+                         [(2, False, 3, 1, F32), (3, False, 2, 1, F64), (2, True, 4, 1, F64), (3, False, 1, 2, F32),
+                          (2, True, 1, 3, F32)])
+def test_matrix_1d(hip_ctx, matrix, symmetric, batch, kernels, prec):
+    run_case(hip_ctx, [512], batch, prec, matrix, symmetric, kernels, seed=2)
+
+
+def test_matrix_nd_batch1(hip_ctx):
+    run_case(hip_ctx, [16, 32], 1, F32, matrix=2, seed=3)
+    run_case(hip_ctx, [8, 8, 8], 1, F64, matrix=3, seed=4)
+
+
+@pytest.mark.parametrize("conj,cross", [(True, False), (False, True), (True, True)])
+def test_conjugation_and_cross_power(hip_ctx, conj, cross):
+    run_case(hip_ctx, [1000], 3, F64, conj=conj, cross=cross, seed=5)
+    run_case(hip_ctx, [1024], 2, F32, conj=conj, cross=cross, seed=6)
+
+
+def test_phase_correlation_finds_shift(hip_ctx):
+    """Cross-power spectrum of x and a shifted copy: a delta at the shift."""
+    dims, shift = [128, 96], (37, 11)
+    x = o.complex_uniform(128 * 96, 7, np.complex64)
+    k = np.fft.fft2(np.roll(x.reshape(dims), shift, axis=(0, 1))).astype(np.complex64)
+    cfg = conv_cfg(dims, 1, F32, conj=True, cross=True)
+    y = hip_ctx.execute_convolution(vk.ConvolutionIr.build(cfg, k), x).reshape(dims)
+    assert np.unravel_index(np.argmax(np.abs(y)), dims) == shift
+    e = np.zeros(dims)
+    e[shift] = 1
+    assert np.max(np.abs(y - e)) <= 1e-5
+
+
+def test_mixed_storage_scalar(hip_ctx):
+    n = 4096
+    x = o.complex_uniform(n, 8, np.complex64)
+    k = o.complex_uniform(n, 9, np.complex128)
+    for prec, tol in ((vk.Precision.F64ComputeF32Storage, 1e-7), (vk.Precision.F16StorageF32Compute, 2e-3)):
+        conv = vk.ConvolutionIr.build(conv_cfg([n], 1, prec), k)
+        y = hip_ctx.execute_convolution(conv, x)
+        xin = x if prec == vk.Precision.F64ComputeF32Storage else \
+            x.view(np.float32).astype(np.float16).astype(np.float32).view(np.complex64)
+        kin = k if prec == vk.Precision.F64ComputeF32Storage else k.astype(np.complex64)
+        assert o.rel_l2(y, o.convolution(xin, kin, [n], 1)) <= tol, prec
+
+
+def test_device_resident_in_place(hip_ctx):
+    import torch
+    n, batch = 1024, 6
+    x = o.complex_uniform(n * batch, 10, np.complex64)
+    k = o.complex_uniform(n, 11, np.complex64)
+    conv = vk.ConvolutionIr.build(conv_cfg([n], batch, F32), k)
+    plan = vk.Plan(hip_ctx, conv.ir, desc=conv.desc())
+    assert plan.in_bytes == plan.out_bytes == n * batch * 8
+    d = torch.from_numpy(x.view(np.float32).copy()).cuda()
+    plan.execute(d.data_ptr(), d.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    y = d.cpu().numpy().view(np.complex64)
+    assert np.array_equal(y, hip_ctx.execute_convolution(conv, x))
+
+
+def _rejects(ctx, cfg, k, status=None):
+    with pytest.raises(vk.VkFftError) as ei:
+        conv = vk.ConvolutionIr.build(cfg, k)  # keeps the kernel spectrum alive through plan creation
+        vk.Plan(ctx, conv.ir, desc=conv.desc())
+    if status is not None:
+        assert ei.value.status == status
+    return ei.value
+
+
+def test_fail_closed_layouts(hip_ctx):
+    k1 = o.complex_uniform(256, 12, np.complex64)
+    unsupported = -3
+    # kernel spectrum length must match the plane layout
+    _rejects(hip_ctx, conv_cfg([256], 1, F32, kernels=2), k1)
+    # numberKernels is a one-input fan-out
+    _rejects(hip_ctx, conv_cfg([256], 2, F32, kernels=2), np.tile(k1, 2), unsupported)
+    # coordinates without a matrix belong to real application convolution
+    _rejects(hip_ctx, conv_cfg([256], 1, F32).with_coordinate_features(2), np.tile(k1, 2), unsupported)
+    # 3x3 symmetric aliases two planes upstream
+    _rejects(hip_ctx, conv_cfg([256], 1, F32, matrix=3, symmetric=True), np.tile(k1, 6), unsupported)
+    # N-D matrix needs batch 1
+    _rejects(hip_ctx, conv_cfg([16, 16], 2, F32, matrix=2), np.tile(k1, 4), unsupported)
+    # non-finite kernel values
+    bad = k1.copy()
+    bad[7] = np.nan
+    _rejects(hip_ctx, conv_cfg([256], 1, F32), bad)
+    # zero padding and formatted strides are real-application features
+    _rejects(hip_ctx, conv_cfg([256], 1, F32).with_zero_padding(0, 10, 20), k1, unsupported)
+    _rejects(hip_ctx, conv_cfg([256], 1, F32).with_input_buffer_batch_stride(300), k1, unsupported)
+    # mixed storage only for the batch-1 scalar K=1 default policy
+    _rejects(hip_ctx, conv_cfg([256], 2, vk.Precision.F64ComputeF32Storage), k1.astype(np.complex128), unsupported)
+    # kernel conjugation has no executable codegen upstream
+    with pytest.raises(vk.VkFftError):
+        vk.ConvolutionIr.build(conv_cfg([256], 1, F32).with_convolution_conjugation(vk.ConvolutionConjugation.Kernel),
+                               k1)
+    # a convolution config run as a plain transform has no kernel spectrum
+    with pytest.raises(vk.VkFftError):
+        hip_ctx.plan(vk.TransformIr.build(conv_cfg([256], 1, F32), vk.Direction.Forward))

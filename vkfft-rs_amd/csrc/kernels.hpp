@@ -147,4 +147,14 @@ struct R2rArgs {
 };
 int launch_r2r(bool pre, int prec, const R2rArgs& p, const void* in, void* out, hipStream_t s);
 
+// Convolution multiply (conv.hip): spectra [system][coordinate][T], kernel
+// [kernel][plane][T]; matrix = 0 (none), 2 or 3.
+struct ConvArgs {
+    long long T = 0, systems_out = 0;
+    int coords = 1, planes = 1, kernel_count = 1;
+    int matrix = 0, symmetric = 0, independent = 0;
+    int conj_seq = 0, cross_norm = 0;
+};
+int launch_conv(int prec, const ConvArgs& a, const void* x, const void* k, void* y, hipStream_t s);
+
 }  // namespace vkfx

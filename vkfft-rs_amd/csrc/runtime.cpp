@@ -104,6 +104,10 @@ struct Launch {
     // DCT / DST pre (1) or post (2) pass instead of an FFT kernel (r2r.hip)
     int r2r = 0;
     R2rArgs ra;
+    // convolution multiply instead of an FFT kernel (conv.hip)
+    bool conv = false;
+    ConvArgs ca;
+    const void* conv_kernel = nullptr;
 };
 
 // Line geometry of one FFT length inside a kernel.
@@ -463,6 +467,11 @@ void note_pass(Ctx& c, const Launch& L) {
     c.first_pass = false;
     if (L.r2r) {
         c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.ra.L << ",\"len\":" << L.ra.n << "}";
+        return;
+    }
+    if (L.conv) {
+        c.js << "{\"kernel\":\"" << L.label << "\",\"tensor\":" << L.ca.T << ",\"coordinates\":" << L.ca.coords
+             << ",\"systems\":" << L.ca.systems_out << ",\"planes\":" << L.ca.planes << "}";
         return;
     }
     if (L.boundary) {
@@ -1056,6 +1065,62 @@ int plan_real_full_complex(Ctx& c, size_t n, size_t batch, bool r2c, bool normal
     return VKFX_OK;
 }
 
+// Convolution (performConvolution, src/convolution_ir.rs:4252-4344): forward
+// C2C of every [batch][coordinate] tensor into the SEL_FULL copy, the
+// frequency-domain multiply into the output, normalized inverse C2C in place.
+int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d);
+int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_systems, const ConvArgs& ca,
+                     const void* kernel) {
+    vkfx_plan* p = c.p;
+    size_t T = 1;
+    for (uint32_t i = 0; i < d.rank; ++i) T *= d.dims[i];
+    const size_t cs = csize(c.prec);
+    p->full_bytes = d.batch * coords * T * cs;
+    p->serial = true;
+    auto transform = [&](size_t batch, int dir, bool normalize, int in_to, int out_to) -> int {
+        const size_t first = p->launches.size();
+        int rc;
+        if (d.rank == 1) {
+            const int alg = d.axis_algorithm[0];
+            Algorithm a = alg == VKFX_ALG_STOCKHAM ? Algorithm::Stockham
+                          : alg == VKFX_ALG_RADER  ? Algorithm::Rader
+                                                   : Algorithm::Bluestein;
+            rc = plan_c2c_1d(c, d.dims[0], batch, dir, normalize, a, alg == VKFX_ALG_RADER ? 0 : d.convolution_len[0]);
+        } else {
+            vkfx_plan_desc e = d;
+            e.batch = batch;
+            e.direction = dir;
+            e.normalize = normalize ? 1 : 0;
+            rc = plan_c2c_nd(c, e);
+        }
+        if (rc) return rc;
+        for (size_t i = first; i < p->launches.size(); ++i) {
+            Launch& L = p->launches[i];
+            if (L.in_sel == SEL_IN) L.in_sel = in_to;
+            else if (L.in_sel == SEL_OUT) L.in_sel = out_to;
+            if (L.out_sel == SEL_OUT) L.out_sel = out_to;
+        }
+        return VKFX_OK;
+    };
+    int rc = transform(d.batch * coords, -1, false, SEL_IN, SEL_FULL);
+    if (rc) return rc;
+    Launch m{};
+    m.conv = true;
+    m.ca = ca;
+    m.conv_kernel = kernel;
+    m.label = "convolution_multiply";
+    m.in_sel = SEL_FULL, m.out_sel = SEL_OUT;
+    p->launches.push_back(m);
+    // the inverse child is always normalized (convolution_ir.rs:4449-4451)
+    rc = transform(out_systems * coords, 1, true, SEL_OUT, SEL_OUT);
+    if (rc) return rc;
+    c.js << "\"convolution\":{\"coordinates\":" << coords << ",\"kernels\":" << ca.kernel_count << ",\"matrix\":"
+         << ca.matrix << ",\"symmetric\":" << (ca.symmetric ? "true" : "false") << ",\"independent\":"
+         << (ca.independent ? "true" : "false") << ",\"conjugate_sequence\":" << (ca.conj_seq ? "true" : "false")
+         << ",\"cross_power_normalize\":" << (ca.cross_norm ? "true" : "false") << "},";
+    return VKFX_OK;
+}
+
 // DCT / DST of length n as one complex FFT of length L between a pre and a
 // post pass (r2r.hip). Parameters per effective type, with every cosine or
 // sine sum written as the real or imaginary part of a zero-padded DFT:
@@ -1467,8 +1532,94 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     }
     c.js << "],";
     int rc = VKFX_OK;
+    // convolution geometry (validated before any planning)
+    size_t conv_coords = 1, conv_out_systems = d.batch;
+    ConvArgs conv_args;
+    const void* conv_kernel = nullptr;
+    if (d.perform_convolution) {
+        if (d.transform != VKFX_C2C) rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "convolution is C2C only on this path");
+        const int M = d.matrix_convolution > 1 ? (int)d.matrix_convolution : 0;
+        if (!rc && M && M != 2 && M != 3)
+            rc = fail(VKFX_ERR_INVALID_ARGUMENT, "matrix convolution IR requires a 2x2 or 3x3 matrix");
+        if (!rc && M == 3 && d.symmetric_kernel)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "3x3 symmetric-kernel matrix convolution is not executable (convolution_ir.rs:112-117)");
+        if (!rc && d.symmetric_kernel && !M)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "symmetricKernel requires matrixConvolution > 1");
+        conv_coords = M ? (size_t)M : std::max<uint32_t>(1, d.coordinate_features);
+        const size_t K = std::max<uint32_t>(1, d.kernel_count);
+        // ownership rules of FftConfig::validate for C2C (config.rs:1156-1300)
+        if (!rc && K > 1 && d.batch != 1)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "numberKernels is a one-input fan-out: multi-kernel convolution takes batch 1");
+        if (!rc && !M && conv_coords != 1)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "coordinateFeatures > 1 without matrixConvolution is only materialized for real application "
+                      "convolution");
+        if (!rc && M && (size_t)std::max<uint32_t>(1, d.coordinate_features) != (size_t)M)
+            rc = fail(VKFX_ERR_INVALID_ARGUMENT, "matrix convolution coordinate count must equal its matrix size");
+        if (!rc && d.rank > 1 && M && (d.batch != 1 || K != 1))
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "multidimensional performConvolution supports scalar K=1/K>1 layouts or a batch1/K1 matrix "
+                      "layout");
+        bool formatted = d.in_batch_stride || d.out_batch_stride, padded = false;
+        for (uint32_t i = 0; i < d.rank; ++i) {
+            formatted = formatted || d.in_axis_stride[i] || d.out_axis_stride[i];
+            padded = padded || d.zero_left[i] != d.zero_right[i];
+        }
+        if (!rc && formatted)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "formatted performConvolution requires a real application");
+        if (!rc && padded)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "performConvolution zero padding requires a multidimensional real application");
+        const bool mixed = d.precision == VKFX_F16_STORAGE_F32_COMPUTE || d.precision == VKFX_F64_COMPUTE_F32_STORAGE;
+        if (!rc && mixed &&
+            (d.rank != 1 || d.batch != 1 || conv_coords != 1 || K != 1 || d.conjugate_sequence ||
+             d.cross_power_normalize))
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "mixed-storage performConvolution requires dense default-policy 1D C2C batch1 scalar K1");
+        conv_out_systems = K > 1 ? K : d.batch;
+        size_t T = 1;
+        for (uint32_t i = 0; i < d.rank; ++i) T *= d.dims[i];
+        const size_t planes = M ? (d.symmetric_kernel ? (size_t)(M * (M + 1) / 2) : (size_t)(M * M))
+                                : (d.independent_coordinates ? conv_coords : 1);
+        const size_t need = K * planes * T * (f64 ? 16 : 8);
+        if (!rc && (!d.kernel_spectrum || d.kernel_spectrum_bytes != need))
+            rc = fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "convolution kernel spectrum: expected " + std::to_string(need) +
+                                                          " bytes, got " + std::to_string(d.kernel_spectrum_bytes));
+        if (!rc) {
+            // non-finite kernel values are rejected (convolution_ir.rs:347-355)
+            bool finite = true;
+            const size_t nv = need / (f64 ? 8 : 4);
+            for (size_t i = 0; i < nv && finite; ++i)
+                finite = f64 ? std::isfinite(((const double*)d.kernel_spectrum)[i])
+                             : std::isfinite(((const float*)d.kernel_spectrum)[i]);
+            if (!finite) rc = fail(VKFX_ERR_INVALID_ARGUMENT, "convolution kernel spectrum contains non-finite values");
+        }
+        if (!rc) rc = upload(p, "conv_kernel", d.kernel_spectrum, need, &conv_kernel);
+        conv_args.T = (long long)T;
+        conv_args.systems_out = (long long)conv_out_systems;
+        conv_args.coords = (int)conv_coords;
+        conv_args.planes = (int)planes;
+        conv_args.kernel_count = (int)K;
+        conv_args.matrix = M;
+        conv_args.symmetric = d.symmetric_kernel ? 1 : 0;
+        conv_args.independent = d.independent_coordinates ? 1 : 0;
+        conv_args.conj_seq = d.conjugate_sequence ? 1 : 0;
+        conv_args.cross_norm = d.cross_power_normalize ? 1 : 0;
+        if (rc) {
+            delete p;
+            return rc;
+        }
+    }
     try {
-        if (d.transform == VKFX_C2C) {
+        if (d.perform_convolution) {
+            size_t T = 1;
+            for (uint32_t i = 0; i < d.rank; ++i) T *= d.dims[i];
+            p->in_bytes = d.batch * conv_coords * T * cs;
+            p->out_bytes = conv_out_systems * conv_coords * T * cs;
+            rc = plan_convolution(c, d, conv_coords, conv_out_systems, conv_args, conv_kernel);
+        } else if (d.transform == VKFX_C2C) {
             p->in_bytes = p->out_bytes = total * cs;
             if (d.rank == 1) {
                 const int alg = d.axis_algorithm[0];
@@ -1569,7 +1720,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             L.boundary = true;
             BoundaryArgs& a = L.ba;
             a.rank = (int)rank;
-            a.batch = (long long)d.batch;
+            a.batch = (long long)((in_side ? d.batch : conv_out_systems) * conv_coords);
             const long long* dims = in_side ? in_dims : out_dims;
             long long dense = 1;
             for (int ax = (int)rank - 1; ax >= 0; --ax) {
@@ -1603,8 +1754,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         }
         if (need_in) p->launches.insert(p->launches.begin(), make(true));
         if (need_out) p->launches.push_back(make(false));
-        p->in_bytes = (size_t)in_bst * d.batch * in_scal * ssz;
-        p->out_bytes = (size_t)out_bst * d.batch * out_scal * ssz;
+        p->in_bytes = (size_t)in_bst * d.batch * conv_coords * in_scal * ssz;
+        p->out_bytes = (size_t)out_bst * conv_out_systems * conv_coords * out_scal * ssz;
         if (need_in || need_out) p->serial = true;  // the boundary passes bracket every chunk
         p->stage_in_bytes = need_in ? cin : 0;
         // C2C runs in place on one copy when both sides are staged
@@ -1741,6 +1892,11 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
                                                      : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };
+        if (L.conv) {
+            int e = launch_conv(prec, L.ca, sel(L.in_sel, 0), L.conv_kernel, sel(L.out_sel, 0), lane_stream[lane]);
+            if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
+            continue;
+        }
         if (L.r2r) {
             int e = launch_r2r(L.r2r == 1, prec, L.ra, sel(L.in_sel, 0), sel(L.out_sel, 0), lane_stream[lane]);
             if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());

@@ -14,6 +14,7 @@ import ctypes
 import enum
 import json
 import os
+import weakref
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
 
@@ -101,6 +102,13 @@ class ZeroPaddingDomain(enum.IntEnum):
     Frequency = 1
 
 
+class ConvolutionConjugation(enum.IntEnum):
+    """configuration.conjugateConvolution (config.rs:595-612)."""
+    Off = 0
+    Sequence = 1
+    Kernel = 2
+
+
 class AlgorithmKind(enum.IntEnum):
     Stockham = 0
     Rader = 1
@@ -127,6 +135,16 @@ class _PlanDesc(ctypes.Structure):
         ("zero_right", ctypes.c_uint64 * MAX_RANK),
         ("zero_frequency", ctypes.c_int32),
         ("grouped_batch", ctypes.c_uint32 * MAX_RANK),
+        ("perform_convolution", ctypes.c_int32),
+        ("conjugate_sequence", ctypes.c_int32),
+        ("cross_power_normalize", ctypes.c_int32),
+        ("coordinate_features", ctypes.c_uint32),
+        ("matrix_convolution", ctypes.c_uint32),
+        ("symmetric_kernel", ctypes.c_int32),
+        ("independent_coordinates", ctypes.c_int32),
+        ("kernel_count", ctypes.c_uint32),
+        ("kernel_spectrum", ctypes.c_void_p),
+        ("kernel_spectrum_bytes", ctypes.c_uint64),
     ]
 
 
@@ -233,6 +251,13 @@ class FftConfig:
     zero_padding: List[Optional[tuple]] = field(default_factory=lambda: [None] * MAX_RANK)
     zero_padding_domain: ZeroPaddingDomain = ZeroPaddingDomain.Spatial
     grouped_batch: List[int] = field(default_factory=lambda: [0] * MAX_RANK)
+    perform_convolution: bool = False
+    convolution_conjugation: ConvolutionConjugation = ConvolutionConjugation.Off
+    cross_power_spectrum_normalization: bool = False
+    coordinate_features: int = 1
+    matrix_convolution: int = 1
+    symmetric_convolution_kernel: bool = False
+    convolution_kernel_count: int = 1
 
     @staticmethod
     def new(dimensions: Sequence[int]) -> "FftConfig":
@@ -288,6 +313,37 @@ class FftConfig:
 
     def with_zero_padding_domain(self, domain: ZeroPaddingDomain) -> "FftConfig":
         self.zero_padding_domain = ZeroPaddingDomain(domain)
+        return self
+
+    # convolution knobs (config.rs:734-800)
+    def with_convolution(self, enabled: bool = True) -> "FftConfig":
+        self.perform_convolution = bool(enabled)
+        return self
+
+    def with_convolution_conjugation(self, conjugation: ConvolutionConjugation) -> "FftConfig":
+        self.convolution_conjugation = ConvolutionConjugation(conjugation)
+        return self
+
+    def with_cross_power_spectrum_normalization(self, enabled: bool = True) -> "FftConfig":
+        self.cross_power_spectrum_normalization = bool(enabled)
+        return self
+
+    def with_coordinate_features(self, n: int) -> "FftConfig":
+        self.coordinate_features = int(n)
+        return self
+
+    def with_matrix_convolution(self, matrix_size: int) -> "FftConfig":
+        self.matrix_convolution = int(matrix_size)
+        if matrix_size > 1:
+            self.coordinate_features = int(matrix_size)
+        return self
+
+    def with_symmetric_convolution_kernel(self, symmetric: bool = True) -> "FftConfig":
+        self.symmetric_convolution_kernel = bool(symmetric)
+        return self
+
+    def with_convolution_kernel_count(self, kernel_count: int) -> "FftConfig":
+        self.convolution_kernel_count = int(kernel_count)
         return self
 
     def with_grouped_batch(self, axis: int, grouped_batch: int) -> "FftConfig":
@@ -358,6 +414,8 @@ class TransformIr:
         d.in_batch_stride = c.input_buffer_batch_stride
         d.out_batch_stride = c.output_buffer_batch_stride
         d.zero_frequency = int(c.zero_padding_domain == ZeroPaddingDomain.Frequency)
+        # a convolution config without its kernel spectrum fails at plan time
+        d.perform_convolution = int(c.perform_convolution)
         return d
 
     # ---- formatted layouts (the host-side pack/unpack of the reference's
@@ -470,13 +528,14 @@ class TransformIr:
 class Plan:
     """A built plan: launch list, tables and workspace on one device."""
 
-    def __init__(self, ctx: "HipExecutionContext", ir: TransformIr):
+    def __init__(self, ctx: "HipExecutionContext", ir: TransformIr, desc: Optional[_PlanDesc] = None):
         self.ctx = ctx
         self._L = ctx._L
         self.ir = ir
         self.handle = ctypes.c_void_p()
-        d = ir.desc()
+        d = desc if desc is not None else ir.desc()
         _check(self._L.vkfx_plan_create(ctx.handle, ctypes.byref(d), ctypes.byref(self.handle)), self._L)
+        ctx._live_plans.add(self)
         i, o, w = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
         _check(self._L.vkfx_plan_io_bytes(self.handle, ctypes.byref(i), ctypes.byref(o)), self._L)
         _check(self._L.vkfx_plan_workspace_bytes(self.handle, ctypes.byref(w)), self._L)
@@ -503,15 +562,66 @@ class Plan:
         self.execute(x.data_ptr(), y.data_ptr(), 0, s)
 
     def close(self):
-        if self.handle:
+        # a plan outliving its context only drops its handle: the context's
+        # close already destroyed it (vkfx_plan_destroy needs a live context)
+        if self.handle and self.ctx.handle:
             self._L.vkfx_plan_destroy(self.handle)
-            self.handle = ctypes.c_void_p()
+        self.handle = ctypes.c_void_p()
 
     def __del__(self):
         try:
             self.close()
         except Exception:
             pass
+
+
+class ConvolutionIr:
+    """ConvolutionIr / NdConvolutionIr (convolution_ir.rs): forward C2C of every
+    [batch][coordinate] tensor, multiply by `kernel_spectrum` (frequency domain,
+    [kernel][plane][tensor]), normalized inverse C2C."""
+
+    def __init__(self, config: FftConfig, kernel_spectrum: np.ndarray):
+        if config.convolution_conjugation == ConvolutionConjugation.Kernel:
+            raise VkFftError(-3, "kernel-conjugated convolution is not executable in the pinned VkFFT codegen")
+        cfg = FftConfig(**{k: (list(v) if isinstance(v, list) else v) for k, v in config.__dict__.items()})
+        cfg.perform_convolution = True
+        self.ir = TransformIr.build(cfg, Direction.Forward)
+        self.config = cfg
+        dt = self.ir.complex_dtype if cfg.precision != Precision.F64ComputeF32Storage else np.complex128
+        self.kernel = np.ascontiguousarray(kernel_spectrum, dtype=dt).reshape(-1)
+        m = cfg.matrix_convolution if cfg.matrix_convolution > 1 else 0
+        self.coordinates = m if m else max(1, cfg.coordinate_features)
+        self.kernel_count = max(1, cfg.convolution_kernel_count)
+        self.independent = (not m) and self.coordinates > 1
+
+    @staticmethod
+    def build(config: FftConfig, kernel_spectrum: np.ndarray) -> "ConvolutionIr":
+        return ConvolutionIr(config, kernel_spectrum)
+
+    def tensor_len(self) -> int:
+        return int(np.prod(self.config.dimensions))
+
+    def input_count(self) -> int:
+        return self.config.batch_count * self.coordinates * self.tensor_len()
+
+    def output_count(self) -> int:
+        systems = self.kernel_count if self.kernel_count > 1 else self.config.batch_count
+        return systems * self.coordinates * self.tensor_len()
+
+    def desc(self) -> _PlanDesc:
+        d = self.ir.desc()
+        c = self.config
+        d.perform_convolution = 1
+        d.conjugate_sequence = int(c.convolution_conjugation == ConvolutionConjugation.Sequence)
+        d.cross_power_normalize = int(c.cross_power_spectrum_normalization)
+        d.coordinate_features = self.coordinates
+        d.matrix_convolution = c.matrix_convolution if c.matrix_convolution > 1 else 0
+        d.symmetric_kernel = int(c.symmetric_convolution_kernel)
+        d.independent_coordinates = int(self.independent)
+        d.kernel_count = self.kernel_count
+        d.kernel_spectrum = self.kernel.ctypes.data
+        d.kernel_spectrum_bytes = self.kernel.nbytes
+        return d
 
 
 class TransformTicket:
@@ -579,6 +689,7 @@ class HipExecutionContext:
         self.handle = ctypes.c_void_p()
         _check(self._L.vkfx_context_create(device_index, ctypes.byref(self.handle)), self._L)
         self._plans = {}
+        self._live_plans = weakref.WeakSet()  # every Plan built on this context
 
     def device_profile(self) -> dict:
         p = _Profile()
@@ -626,6 +737,24 @@ class HipExecutionContext:
         if kind == TransformKind.ComplexToReal:
             return self._execute_host(ir, x, ir.complex_dtype, ir.real_dtype, ir.output_count())
         return self._execute_host(ir, x, ir.complex_dtype, ir.complex_dtype, ir.output_count())
+
+    def execute_convolution(self, conv: ConvolutionIr, x: np.ndarray) -> np.ndarray:
+        """Host round trip of a convolution (the plan is built once per ConvolutionIr)."""
+        ir = conv.ir
+        x = np.ascontiguousarray(x, dtype=ir.complex_dtype).reshape(-1)
+        if x.size != conv.input_count():
+            raise VkFftError(-5, f"InputLengthMismatch {{ expected: {conv.input_count()}, actual: {x.size} }}")
+        plan = getattr(conv, "_plan", None)
+        if plan is None or plan.ctx is not self:
+            plan = Plan(self, ir, desc=conv.desc())
+            conv._plan = plan
+        xs = np.ascontiguousarray(ir.to_storage(x))
+        n_out = conv.output_count()
+        f16 = ir.config.precision == Precision.F16StorageF32Compute
+        out = np.empty(2 * n_out, dtype=np.float16) if f16 else np.empty(n_out, dtype=ir.complex_dtype)
+        _check(self._L.vkfx_execute_host(plan.handle, xs.ctypes.data, xs.nbytes, out.ctypes.data, out.nbytes),
+               self._L)
+        return ir.from_storage(out, True)
 
     def _io_dtypes(self, ir: TransformIr):
         kind = ir.config.transform
@@ -676,7 +805,7 @@ class HipExecutionContext:
         _check(self._L.vkfx_context_synchronize(self.handle), self._L)
 
     def close(self):
-        for p in self._plans.values():
+        for p in list(self._live_plans):
             p.close()
         self._plans.clear()
         if self.handle:
