@@ -65,6 +65,19 @@ struct FixDims {
     static __device__ __forceinline__ constexpr int PS(const KArgs&) { return PS_; }
 };
 
+// Group of lines handled by this block. Workgroups are dispatched round-robin
+// over the 8 XCDs; with KF_XCD_GROUPS each XCD gets a contiguous range of
+// groups instead, so neighbouring groups whose HBM segments share cache lines
+// (unaligned pitches, narrow strided segments) meet in the same L2.
+__device__ __forceinline__ long long group_index(const KArgs& a) {
+    const long long i = blockIdx.x;
+    if (!(a.flags & KF_XCD_GROUPS)) return i;
+    constexpr long long X = 8;
+    const long long n = gridDim.x, q = n / X, r = n % X;
+    const long long x = i % X, k = i / X;
+    return x * q + (x < r ? x : r) + k;
+}
+
 __device__ __forceinline__ LineInfo line_default(const KArgs& a, long long blk, int g) {
     LineInfo L;
     long long line = blk * a.G + g;
@@ -433,6 +446,12 @@ struct IoFsAC2R : IoFsA {
         }
         staged_load<IoPlain, D>(a, lds, li, false);  // X of the 2H columns, each element once
         __syncthreads();
+        pair_fixup<T, D>(a, lds, li);
+    }
+    // (X[k], X[M-k]) -> (Z[k], Z[M-k]) in LDS for the mirror-pair layout
+    template <typename T, class D>
+    static __device__ void pair_fixup(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        if (!(a.flags & KF_MIRROR_PAIRS)) return;
         const int N1 = D::N(a), H = D::G(a) / 2, LS = D::LS(a), PS = D::PS(a);
         const long long N2 = a.N2;
         const bool first = li[0].c == 0;  // the block holding columns 0 and N2/2
@@ -728,7 +747,7 @@ __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
     __shared__ LineInfo li[kMaxLinesPerBlock];
     const int tid = threadIdx.x;
-    if (tid < a.G) li[tid] = IO::line(a, blockIdx.x, tid);
+    if (tid < a.G) li[tid] = IO::line(a, group_index(a), tid);
     __syncthreads();
     IO::template prologue<T, DynDims>(a, lds, li);
     __syncthreads();
@@ -931,7 +950,7 @@ template <typename T, int S, class IO, class Sh>
 __global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ LineInfo li[Sh::G];
-    fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blockIdx.x);
+    fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, group_index(a));
 }
 
 // Variant shapes for tuning: a waves-per-EU occupancy hint and nontemporal IO.
@@ -946,7 +965,7 @@ __global__ __launch_bounds__(Sh::G* Sh::TT) __attribute__((amdgpu_waves_per_eu(S
     const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ LineInfo li[Sh::G];
-    fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blockIdx.x);
+    fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, group_index(a));
 }
 
 // Persistent variant: a grid sized to the resident capacity walks the groups

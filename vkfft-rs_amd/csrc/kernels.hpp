@@ -35,6 +35,7 @@ enum KFlags : int {
     KF_IN_ROWMAJOR = 1,   // a line's elements are contiguous in the input
     KF_OUT_ROWMAJOR = 2,  // a line's elements are contiguous in the output
     KF_MIRROR_PAIRS = 4,  // C2R column pass: a block owns columns and their mirrors
+    KF_XCD_GROUPS = 8,    // deal line groups to XCDs in contiguous ranges
 };
 
 struct KArgs {

@@ -9,8 +9,8 @@ namespace vkfx {
 
 static const FixedKernel kTable[] = {
     // 4096-point rows, first pass of a chunk
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 5, 4224, false, true, false, 16, 16, 16),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 5, 4224, false, true, false, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 4, 4352, false, true, false, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 4, 4352, false, true, false, 16, 16, 16),
     // split 4096 column axis: the 64-point column pass in the middle, the
     // 64-point row-of-columns pass last
     VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 64, 8, 32, 30, 65, true, false, false, 8, 8),
@@ -18,12 +18,12 @@ static const FixedKernel kTable[] = {
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 64, 8, 32, 30, 65, true, false, true, 8, 8),
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 64, 8, 32, 30, 65, true, false, true, 8, 8),
     // f64 512: rows first, columns in the middle or last
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 4, 544, false, true, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 4, 544, false, true, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 3, 578, true, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 3, 578, true, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 3, 578, true, false, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 3, 578, true, false, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 3, 576, false, true, false, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 3, 576, false, true, false, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 30, 513, true, false, false, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 30, 513, true, false, false, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 30, 513, true, false, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 30, 513, true, false, true, 8, 8, 8),
 };
 
 const FixedKernel* fixed_table_nd(int* count) {

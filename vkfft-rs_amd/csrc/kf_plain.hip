@@ -7,21 +7,23 @@ namespace vkfx {
 static const FixedKernel kTable[] = {
     // 1-D rows of 1024 (C1): two waves per line, 8 elements per thread in the
     // radix-8 stages (16 in the radix-16 load stage)
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 5, 1056, false, true, true, 16, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 1024, 128, 1, 5, 1056, false, true, true, 16, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 4, 1088, false, true, true, 16, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 1024, 128, 1, 4, 1088, false, true, true, 16, 8, 8),
     // one wave per line (VKFX_FIXED_PICK=1)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
+    // the previous padding (one slot per 32; VKFX_FIXED_PICK=2)
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 5, 1056, false, true, true, 16, 8, 8),
     // rows of 4096 (C3 axis 1)
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 5, 4224, false, true, true, 16, 16, 16),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 5, 4224, false, true, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 4, 4352, false, true, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 4, 4352, false, true, true, 16, 16, 16),
     // columns of 4096 (C3 axis 0): 4 adjacent columns per block
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 128, 4, 4, 4360, true, true, true, 16, 16, 16),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 128, 4, 4, 4360, true, true, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 128, 4, 4, 4356, true, true, true, 16, 16, 16),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 128, 4, 4, 4356, true, true, true, 16, 16, 16),
     // f64 512 rows and columns (C4)
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 4, 544, false, true, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 4, 544, false, true, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 3, 578, true, true, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 3, 578, true, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 3, 576, false, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 3, 576, false, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 30, 513, true, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 30, 513, true, true, true, 8, 8, 8),
     // 64-point column passes of a split strided axis (4096 = 64 x 64): 32
     // adjacent columns per block, 256-byte row segments
     VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 64, 8, 32, 30, 65, true, true, true, 8, 8),

@@ -57,22 +57,22 @@ const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool co
     if (disabled) return nullptr;
     int total = 0;
     const FixedKernel* all = registry(&total);
-    // VKFX_FIXED_PICK=k selects the k-th registered variant of a shape key
-    // (tuning runs); the default is the first.
+    // VKFX_FIXED_PICK=k selects the k-th registered variant of a shape key,
+    // or its last one if it has fewer (tuning runs); the default is the first.
     static const int pick = [] {
         const char* e = getenv("VKFX_FIXED_PICK");
         return e ? atoi(e) : 0;
     }();
-    const FixedKernel* first = nullptr;
+    const FixedKernel* last = nullptr;
     int seen = 0;
     for (int i = 0; i < total; ++i) {
         const FixedKernel& f = all[i];
         if (f.kind == kind && f.prec == prec && f.dir == dir && f.N == N && f.col == col) {
-            if (!first) first = &f;
+            last = &f;
             if (seen++ == pick) return &f;
         }
     }
-    return first;
+    return last;
 }
 
 const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto) {
@@ -117,6 +117,23 @@ static int persist_blocks_per_cu() {
     return v;
 }
 
+// Launches whose blocks share HBM cache lines with their neighbours get their
+// groups dealt to XCDs in contiguous ranges: the four-step passes that read
+// or write the N/2+1-pitch real-transform spectra (unaligned 128-byte
+// segments) and the Bluestein passes over pitch-N lines. Measured on C2: the
+// C2R column pass reads 1.0x its bytes instead of 2.0x and the R2C row pass
+// writes 1.0x instead of 1.19x. VKFX_XCD_GROUPS=0/1 forces it off/on for
+// every launch (tuning runs).
+static bool xcd_groups(KernelKind kind) {
+    static const int forced = [] {
+        const char* e = getenv("VKFX_XCD_GROUPS");
+        return e ? (e[0] == '1' ? 1 : 0) : -1;
+    }();
+    if (forced >= 0) return forced == 1;
+    return kind == KK_FS_B_R2C || kind == KK_FS_A_C2R || kind == KK_FS_A_BLUE || kind == KK_BLUE_B ||
+           kind == KK_FS_C_BLUE;
+}
+
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block, size_t lds_bytes,
            hipStream_t stream, const FixedKernel* fixed) {
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1))
@@ -149,6 +166,7 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     if (!fn) return (int)hipErrorInvalidValue;
     KArgs args = a;
     args.nblk = grid;
+    if (xcd_groups(kind)) args.flags |= KF_XCD_GROUPS;
     if (fixed && persist_blocks_per_cu() > 0) {
         // persistent launch: at most the resident capacity, groups by grid stride
         static int cus = 0;
