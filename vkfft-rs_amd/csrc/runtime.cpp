@@ -83,8 +83,17 @@ namespace {
 // plan's workspace (per stream lane) and, for mixed storage/compute
 // precisions, the compute-type copies of the input and output in the
 // workspace; SEL_FULL is the N-point complex copy of a real transform run
-// through a full-length C2C plan.
-enum BufSel : int { SEL_IN = 0, SEL_OUT = 1, SEL_WORK = 2, SEL_STAGE_IN = 3, SEL_STAGE_OUT = 4, SEL_FULL = 5 };
+// through a full-length C2C plan; SEL_AUX the compact spectrum between the
+// complex axes and the real axis of an N-D C2R.
+enum BufSel : int {
+    SEL_IN = 0,
+    SEL_OUT = 1,
+    SEL_WORK = 2,
+    SEL_STAGE_IN = 3,
+    SEL_STAGE_OUT = 4,
+    SEL_FULL = 5,
+    SEL_AUX = 6
+};
 
 struct Launch {
     KernelKind kind;
@@ -227,6 +236,7 @@ struct vkfx_plan {
     size_t stage_in_bytes = 0, stage_out_bytes = 0;
     bool stage_shared = false;  // C2C with both sides staged runs in place on one copy
     size_t full_off = 0, full_bytes = 0;  // SEL_FULL region (full-complex real transforms)
+    size_t aux_off = 0, aux_bytes = 0;    // SEL_AUX region (N-D C2R compact spectrum)
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
     std::string json;
@@ -830,7 +840,9 @@ bool split_strided_axis(size_t len, int prec, size_t lds_budget, size_t* l1, siz
     return true;
 }
 
-int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
+// Axes whose bit is set in `omit` are left untransformed (the real axis of an
+// N-D real transform).
+int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d, uint32_t omit) {
     const int prec = c.prec;
     const int dir = d.direction;
     const size_t cs = csize(prec);
@@ -840,9 +852,10 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
     // intermediate between its axis passes.
     size_t chunk = d.batch;
     bool any_split = false;
+    auto active = [&](uint32_t ax) { return d.dims[ax] > 1 && !(omit >> ax & 1u); };
     for (uint32_t ax = 0; ax + 1 < d.rank; ++ax) {
         size_t l1, l2;
-        if (d.axis_algorithm[ax] == VKFX_ALG_STOCKHAM && d.dims[ax] > 1 &&
+        if (d.axis_algorithm[ax] == VKFX_ALG_STOCKHAM && active(ax) &&
             split_strided_axis(d.dims[ax], prec, c.lds_budget, &l1, &l2))
             any_split = true;
     }
@@ -855,9 +868,9 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
     // then axis 0 over the whole volume.
     const size_t slab = per_batch / d.dims[0];
     int slab_axes = 0;
-    for (uint32_t ax = 1; ax < d.rank; ++ax) slab_axes += d.dims[ax] > 1;
+    for (uint32_t ax = 1; ax < d.rank; ++ax) slab_axes += active(ax);
     size_t slabs = 0;
-    if (chunk == 1 && per_batch * cs > chunk_budget && d.dims[0] > 1 && slab_axes >= 2)
+    if (chunk == 1 && per_batch * cs > chunk_budget && active(0) && slab_axes >= 2)
         slabs = std::max<size_t>(1, chunk_budget / (slab * cs));
     c.js << "\"nd\":{\"chunk\":" << chunk << ",\"slabs_per_chunk\":" << slabs << "},";
 
@@ -967,7 +980,7 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
                 const size_t ns = std::min(slabs, d.dims[0] - s0);
                 bool sfirst = true;
                 for (int ax = (int)d.rank - 1; ax >= 1; --ax) {
-                    if (d.dims[ax] == 1) continue;
+                    if (!active(ax)) continue;
                     int rc = axis_pass(ax, ns * slab, off + s0 * slab * cs, sfirst ? SEL_IN : SEL_OUT);
                     if (rc) return rc;
                     sfirst = false;
@@ -981,7 +994,7 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d) {
         c.cur_chunk = next_chunk++;
         bool first = true;
         for (int ax = (int)d.rank - 1; ax >= 0; --ax) {
-            if (d.dims[ax] == 1) continue;
+            if (!active(ax)) continue;
             int rc = axis_pass(ax, total, off, first ? SEL_IN : SEL_OUT);
             if (rc) return rc;
             first = false;
@@ -1065,10 +1078,62 @@ int plan_real_full_complex(Ctx& c, size_t n, size_t batch, bool r2c, bool normal
     return VKFX_OK;
 }
 
+int plan_r2c(Ctx& c, size_t n, size_t batch);
+int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize);
+
+// N-D real transform (NdRealFftIr, src/nd_real_ir.rs:754-870): the real
+// axis (the fastest) as a 1-D R2C/C2R over every row, the other axes as
+// C2C over the compact [.., N/2+1] spectrum. R2C runs the real axis into
+// the output and the complex axes in place there; C2R runs the complex axes
+// from the (read-only) input into the SEL_AUX copy and the real axis from
+// there into the output. The inverse normalizes every axis by its length.
+int plan_real_nd(Ctx& c, const vkfx_plan_desc& d, bool r2c) {
+    vkfx_plan* p = c.p;
+    const uint32_t r = d.rank;
+    const size_t n = d.dims[r - 1], h = n / 2 + 1;
+    size_t outer = 1;
+    for (uint32_t i = 0; i + 1 < r; ++i) outer *= d.dims[i];
+    const size_t rows = d.batch * outer;
+    vkfx_plan_desc e = d;
+    e.transform = VKFX_C2C;
+    e.dims[r - 1] = h;
+    e.direction = r2c ? VKFX_FORWARD : VKFX_INVERSE;
+    e.normalize = r2c ? 0 : d.normalize;
+    const uint32_t omit = 1u << (r - 1);
+    int rc;
+    if (r2c) {
+        rc = plan_r2c(c, n, rows);
+        if (rc) return rc;
+        const size_t first = p->launches.size();
+        rc = plan_c2c_nd(c, e, omit);
+        if (rc) return rc;
+        for (size_t i = first; i < p->launches.size(); ++i)
+            if (p->launches[i].in_sel == SEL_IN) p->launches[i].in_sel = SEL_OUT;
+    } else {
+        p->aux_bytes = rows * h * csize(c.prec);
+        const size_t first = p->launches.size();
+        rc = plan_c2c_nd(c, e, omit);
+        if (rc) return rc;
+        for (size_t i = first; i < p->launches.size(); ++i) {
+            Launch& L = p->launches[i];
+            if (L.in_sel == SEL_OUT) L.in_sel = SEL_AUX;
+            if (L.out_sel == SEL_OUT) L.out_sel = SEL_AUX;
+        }
+        const size_t mid = p->launches.size();
+        rc = plan_c2r(c, n, rows, d.normalize != 0);
+        if (rc) return rc;
+        for (size_t i = mid; i < p->launches.size(); ++i)
+            if (p->launches[i].in_sel == SEL_IN) p->launches[i].in_sel = SEL_AUX;
+    }
+    p->serial = true;
+    c.js << "\"real_nd\":{\"real_axis\":" << n << ",\"rows\":" << rows << "},";
+    return VKFX_OK;
+}
+
 // Convolution (performConvolution, src/convolution_ir.rs:4252-4344): forward
 // C2C of every [batch][coordinate] tensor into the SEL_FULL copy, the
 // frequency-domain multiply into the output, normalized inverse C2C in place.
-int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d);
+int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d, uint32_t omit = 0);
 int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_systems, const ConvArgs& ca,
                      const void* kernel) {
     vkfx_plan* p = c.p;
@@ -1477,9 +1542,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         return fail(VKFX_ERR_INVALID_ARGUMENT, "C2R requires Direction::Inverse");
     if (d.transform < VKFX_C2C || d.transform > VKFX_DST_IV) return fail(VKFX_ERR_INVALID_ARGUMENT, "unknown transform");
     const bool r2r = d.transform >= VKFX_DCT_I;
-    if (d.transform != VKFX_C2C && d.rank != 1)
-        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
-                    r2r ? "multi-dimensional DCT/DST is outside this path" : "multi-dimensional R2C/C2R is outside this path");
+    if (r2r && d.rank != 1)
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "multi-dimensional DCT/DST is outside this path");
     if (d.transform == VKFX_DCT_I && d.dims[0] < 2)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "InvalidTransformLength { axis: 0, transform: DCT-I, length: 1 }");
     // storage and compute scalar types (0 f16, 1 f32, 2 f64)
@@ -1636,16 +1700,16 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             const size_t n = d.dims[0];
             p->in_bytes = p->out_bytes = d.batch * n * rs;
             rc = plan_r2r(c, n, d.batch, d.transform - VKFX_DCT_I, d.direction, d.normalize != 0);
-        } else if (d.transform == VKFX_R2C) {
-            const size_t n = d.dims[0];
-            p->in_bytes = d.batch * n * rs;
-            p->out_bytes = d.batch * (n / 2 + 1) * cs;
-            rc = plan_r2c(c, n, d.batch);
         } else {
-            const size_t n = d.dims[0];
-            p->in_bytes = d.batch * (n / 2 + 1) * cs;
-            p->out_bytes = d.batch * n * rs;
-            rc = plan_c2r(c, n, d.batch, d.normalize != 0);
+            const size_t n = d.dims[d.rank - 1];
+            const size_t real_elems = total, compact_elems = total / n * (n / 2 + 1);
+            const bool r2c_kind = d.transform == VKFX_R2C;
+            p->in_bytes = r2c_kind ? real_elems * rs : compact_elems * cs;
+            p->out_bytes = r2c_kind ? compact_elems * cs : real_elems * rs;
+            if (d.rank > 1)
+                rc = plan_real_nd(c, d, r2c_kind);
+            else
+                rc = r2c_kind ? plan_r2c(c, n, d.batch) : plan_c2r(c, n, d.batch, d.normalize != 0);
         }
     } catch (const std::exception& ex) {
         rc = fail(VKFX_ERR_INVALID_ARGUMENT, std::string("plan: ") + ex.what());
@@ -1796,8 +1860,12 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->full_off = (p->work_bytes + 255) / 256 * 256;
         p->work_bytes = p->full_off + p->full_bytes;
     }
+    if (p->aux_bytes) {
+        p->aux_off = (p->work_bytes + 255) / 256 * 256;
+        p->work_bytes = p->aux_off + p->aux_bytes;
+    }
     if (p->stage_in_bytes || p->stage_out_bytes) {
-        // workspace: [lane work][full complex][stage in][stage out]
+        // workspace: [lane work][full complex][aux][stage in][stage out]
         auto align = [](size_t v) { return (v + 255) / 256 * 256; };
         const bool shared = p->stage_shared;
         p->stage_in_off = align(p->work_bytes);
@@ -1889,6 +1957,7 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
                          : which == SEL_STAGE_IN     ? (char*)work + plan->stage_in_off
                          : which == SEL_STAGE_OUT    ? (char*)work + plan->stage_out_off
                          : which == SEL_FULL         ? (char*)work + plan->full_off
+                         : which == SEL_AUX          ? (char*)work + plan->aux_off
                                                      : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };

@@ -511,18 +511,12 @@ class TransformIr:
         return v.view(np.complex64) if complex_out else v
 
     def input_count(self) -> int:
-        c = self.config
-        n = int(np.prod(c.dimensions)) * c.batch_count
-        if c.transform == TransformKind.ComplexToReal:
-            return c.batch_count * (c.dimensions[-1] // 2 + 1)
-        return n
+        """Logical input elements: the compact [.., N/2+1] spectrum for C2R."""
+        return int(np.prod(self._side_dims(False))) * self.config.batch_count
 
     def output_count(self) -> int:
-        c = self.config
-        n = int(np.prod(c.dimensions)) * c.batch_count
-        if c.transform == TransformKind.RealToComplex:
-            return c.batch_count * (c.dimensions[-1] // 2 + 1)
-        return n
+        """Logical output elements: the compact [.., N/2+1] spectrum for R2C."""
+        return int(np.prod(self._side_dims(True))) * self.config.batch_count
 
 
 class Plan:
