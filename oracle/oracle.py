@@ -210,6 +210,40 @@ def convolution(x, spectrum, dims, batch=1, matrix=0, symmetric=False, kernel_co
     return transform(prod.reshape(-1), out_systems * coords, "inverse", True)
 
 
+def convolution_real(x, spectrum, dims, coords=1, matrix=0, symmetric=False, kernel_count=1,
+                     conj_sequence=False, cross_power=False) -> np.ndarray:
+    """Real-application performConvolution (execute_nd_real_convolution_ir,
+    src/convolution_ir.rs:4185-4251), batch 1: rfftn of the `coords` real
+    tensors, multiply over the compact [.., N/2+1] spectra (matrix: output
+    (k, o) sums input i with plane (k, plane(o, i)); otherwise output (k, c)
+    uses plane (k, c)), normalized irfftn of the K * coords products. The
+    transforms are numpy's (pocketfft); the kernel spectrum must be Hermitian
+    (the rfftn of real kernels) for the inverse to be well defined."""
+    dims = list(dims)
+    axes = tuple(range(1, len(dims) + 1))
+    h = dims[-1] // 2 + 1
+    t = int(np.prod(dims[:-1])) * h
+    xs = np.asarray(x, dtype=np.float64).reshape((coords,) + tuple(dims))
+    spec = np.fft.rfftn(xs, axes=axes).reshape(coords, t)
+    seq = np.conj(spec) if conj_sequence else spec
+    planes = (matrix * (matrix + 1) // 2 if symmetric else matrix * matrix) if matrix else coords
+    kern = np.asarray(spectrum, dtype=np.complex128).reshape(kernel_count, planes, t)
+    prod = np.zeros((kernel_count, coords, t), dtype=np.complex128)
+    for kid in range(kernel_count):
+        for o in range(coords):
+            if matrix:
+                acc = np.zeros(t, dtype=np.complex128)
+                for i in range(coords):
+                    acc += seq[i] * kern[kid, conv_plane_index(matrix, symmetric, o, i)]
+            else:
+                acc = seq[o] * kern[kid, o]
+            if cross_power:
+                acc = acc * (1.0 / np.sqrt(acc.real ** 2 + acc.imag ** 2))
+            prod[kid, o] = acc
+    shaped = prod.reshape((kernel_count * coords,) + tuple(dims[:-1]) + (h,))
+    return np.fft.irfftn(shaped, s=dims, axes=axes).reshape(-1)
+
+
 def next_smooth_at_least(target: int, primes=(2, 3, 5, 7)) -> int:
     p = (ctypes.c_size_t * len(primes))(*primes)
     return int(lib().vko_next_smooth_at_least(target, p, len(primes)))

@@ -165,3 +165,103 @@ def test_fail_closed_layouts(hip_ctx):
     # a convolution config run as a plain transform has no kernel spectrum
     with pytest.raises(vk.VkFftError):
         hip_ctx.plan(vk.TransformIr.build(conv_cfg([256], 1, F32), vk.Direction.Forward))
+
+
+# ---- real application (NdRealConvolutionIr, convolution_ir.rs:3884-4251) ----
+
+def real_conv_cfg(dims, prec, coords=1, matrix=1, symmetric=False, kernels=1, conj=False, cross=False):
+    c = conv_cfg(dims, 1, prec, matrix, symmetric, kernels, conj, cross).with_transform(vk.TransformKind.RealToComplex)
+    if matrix <= 1:
+        c = c.with_coordinate_features(coords)
+    return c
+
+
+def run_real_case(ctx, dims, prec, coords=1, matrix=1, symmetric=False, kernels=1, conj=False, cross=False, seed=0):
+    rd = np.float32 if prec == F32 else np.float64
+    cd = np.complex64 if prec == F32 else np.complex128
+    coords = matrix if matrix > 1 else coords
+    n = int(np.prod(dims))
+    x = o.normal(coords * n, 300 + seed, rd)
+    pl = planes(matrix, symmetric) if matrix > 1 else coords
+    hk = o.normal(kernels * pl * n, 400 + seed, np.float64).reshape((kernels * pl,) + tuple(dims))
+    k = np.fft.rfftn(hk, axes=tuple(range(1, len(dims) + 1))).astype(cd).reshape(-1)  # Hermitian spectra
+    conv = vk.ConvolutionIr.build(real_conv_cfg(dims, prec, coords, matrix, symmetric, kernels, conj, cross), k)
+    assert conv.real and conv.input_count() == coords * n and conv.output_count() == kernels * coords * n
+    y = ctx.execute_convolution(conv, x)
+    assert y.dtype == rd
+    ref = o.convolution_real(x, k, dims, coords, matrix if matrix > 1 else 0, symmetric, kernels, conj, cross)
+    err = o.rel_l2(y, ref)
+    assert err <= TOL[prec], (dims, prec, coords, matrix, kernels, err)
+    return conv
+
+
+@pytest.mark.parametrize("dims,prec,coords,kernels", [([64, 48], F32, 1, 1), ([32, 40], F64, 3, 1),
+                                                      ([16, 12, 10], F32, 2, 3), ([128, 130], F32, 1, 2),
+                                                      ([1, 64], F64, 1, 1), ([4096, 4096], F32, 1, 1)])
+def test_real_convolution_independent(hip_ctx, dims, prec, coords, kernels):
+    conv = run_real_case(hip_ctx, dims, prec, coords=coords, kernels=kernels)
+    desc = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    assert desc["convolution"]["real"] and "convolution_multiply" in [p["kernel"] for p in desc["passes"]]
+
+
+@pytest.mark.parametrize("matrix,symmetric,kernels,prec", [(2, False, 1, F32), (3, False, 2, F64), (2, True, 1, F64)])
+def test_real_convolution_matrix(hip_ctx, matrix, symmetric, kernels, prec):
+    run_real_case(hip_ctx, [24, 32], prec, matrix=matrix, symmetric=symmetric, kernels=kernels, seed=1)
+
+
+def test_real_convolution_policies_and_mixed(hip_ctx):
+    run_real_case(hip_ctx, [48, 40], F64, conj=True, seed=2)
+    run_real_case(hip_ctx, [48, 40], F64, conj=True, cross=True, seed=3)
+    # mixed storage: scalar ownership and independent-coordinate K>1 fan-out
+    dims, n = [32, 36], 32 * 36
+    x = o.normal(n, 5, np.float32)
+    hk = o.normal(n, 6, np.float64).reshape(dims)
+    k = np.fft.rfftn(hk).reshape(-1)
+    for prec, tol in ((vk.Precision.F64ComputeF32Storage, 1e-7), (vk.Precision.F16StorageF32Compute, 3e-3)):
+        kk = k if prec == vk.Precision.F64ComputeF32Storage else k.astype(np.complex64)
+        y = hip_ctx.execute_convolution(vk.ConvolutionIr.build(real_conv_cfg(dims, prec), kk), x)
+        xin = x if prec == vk.Precision.F64ComputeF32Storage else x.astype(np.float16).astype(np.float32)
+        assert o.rel_l2(y, o.convolution_real(xin, kk, dims)) <= tol, prec
+
+
+def test_real_convolution_zero_padding_and_layout(hip_ctx):
+    """Spatial zero padding masks the input of the forward R2C and the output
+    of the inverse C2R; formatted strides for scalar K=1 ownership."""
+    dims, n = [40, 36], 40 * 36
+    x = o.normal(2 * n, 7, np.float64)
+    hk = o.normal(4 * n, 8, np.float64).reshape(4, 40, 36)
+    k = np.fft.rfftn(hk, axes=(1, 2)).reshape(-1)
+    c = real_conv_cfg(dims, F64, matrix=2).with_zero_padding(0, 30, 40).with_zero_padding(1, 20, 36)
+    y = hip_ctx.execute_convolution(vk.ConvolutionIr.build(c, k), x).reshape(2, 40, 36)
+    mask = np.zeros((40, 36), dtype=bool)
+    mask[30:, :] = True
+    mask[:, 20:] = True
+    xm = x.reshape(2, 40, 36).copy()
+    xm[:, mask] = 0
+    ref = o.convolution_real(xm, k, dims, 2, 2).reshape(2, 40, 36)
+    ref[:, mask] = 0
+    assert (y[:, mask] == 0).all()
+    assert o.rel_l2(y, ref) <= TOL[F64]
+    # formatted input / output row strides (scalar, K = 1)
+    k1 = k[:40 * 19]
+    cf = real_conv_cfg(dims, F64).with_input_buffer_axis_stride(0, 40).with_output_buffer_axis_stride(0, 38)
+    conv = vk.ConvolutionIr.build(cf, k1)
+    yf = hip_ctx.execute_convolution(conv, x[:n])
+    assert o.rel_l2(yf, o.convolution_real(x[:n], k1, dims)) <= TOL[F64]
+
+
+def test_real_convolution_fail_closed(hip_ctx):
+    dims = [16, 16]
+    k1 = np.fft.rfftn(np.ones(dims)).astype(np.complex64).reshape(-1)
+    unsupported = -3
+    _rejects(hip_ctx, real_conv_cfg(dims, F32).with_batch_count(2), k1, unsupported)
+    _rejects(hip_ctx, real_conv_cfg(dims, F32, matrix=2, symmetric=True).with_zero_padding(0, 8, 16),
+             np.tile(k1, 3), unsupported)
+    _rejects(hip_ctx, real_conv_cfg(dims, F32, coords=2).with_output_buffer_batch_stride(300), np.tile(k1, 2),
+             unsupported)
+    # mixed storage: a 2x2 matrix is not among the pinned real ownerships
+    _rejects(hip_ctx, real_conv_cfg(dims, vk.Precision.F64ComputeF32Storage, matrix=2), np.tile(k1, 4).astype(np.complex128),
+             unsupported)
+    # 1-D real convolution is not a real application
+    with pytest.raises(vk.VkFftError):
+        hip_ctx.execute_convolution(vk.ConvolutionIr.build(real_conv_cfg([64], F32), k1[:33]), np.ones(64, np.float32))

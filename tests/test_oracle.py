@@ -293,3 +293,32 @@ def test_convolution_backends_agree():
         a = o.convolution(x, k, dims, batch, conj_sequence=True, cross_power=True)
         b = o.convolution(x, k, dims, batch, conj_sequence=True, cross_power=True, backend="numpy")
         assert o.rel_l2(a, b) <= 1e-12
+
+
+def _circ_conv2(x, h):
+    """Brute-force 2-D circular convolution."""
+    n0, n1 = x.shape
+    y = np.zeros_like(x)
+    for a in range(n0):
+        for b in range(n1):
+            y[a, b] = sum(x[p, q] * h[(a - p) % n0, (b - q) % n1] for p in range(n0) for q in range(n1))
+    return y
+
+
+def test_real_convolution_is_circular_convolution():
+    """The real-application convolution with kernel spectra rfftn(h) convolves
+    each coordinate (independent: plane (k, c)) or sums a matrix row."""
+    rng = np.random.default_rng(9)
+    dims = [5, 6]
+    xs = rng.standard_normal((2, 5, 6))
+    hs = rng.standard_normal((2, 2, 5, 6))  # [kernel][coordinate]
+    spec = np.fft.rfftn(hs, axes=(2, 3)).reshape(-1)
+    y = o.convolution_real(xs, spec, dims, coords=2, kernel_count=2).reshape(2, 2, 5, 6)
+    for k in range(2):
+        for c in range(2):
+            assert np.allclose(y[k, c], _circ_conv2(xs[c], hs[k, c]), atol=1e-12)
+    hm = rng.standard_normal((4, 5, 6))  # 2x2 matrix planes, row-major
+    ym = o.convolution_real(xs, np.fft.rfftn(hm, axes=(1, 2)).reshape(-1), dims, coords=2, matrix=2).reshape(2, 5, 6)
+    for oc in range(2):
+        ref = _circ_conv2(xs[0], hm[2 * oc]) + _circ_conv2(xs[1], hm[2 * oc + 1])
+        assert np.allclose(ym[oc], ref, atol=1e-12)

@@ -92,7 +92,9 @@ enum BufSel : int {
     SEL_STAGE_IN = 3,
     SEL_STAGE_OUT = 4,
     SEL_FULL = 5,
-    SEL_AUX = 6
+    SEL_AUX = 6,
+    SEL_CONV_A = 7,  // real-application convolution: forward spectrum
+    SEL_CONV_B = 8   // real-application convolution: multiplied spectrum
 };
 
 struct Launch {
@@ -237,6 +239,7 @@ struct vkfx_plan {
     bool stage_shared = false;  // C2C with both sides staged runs in place on one copy
     size_t full_off = 0, full_bytes = 0;  // SEL_FULL region (full-complex real transforms)
     size_t aux_off = 0, aux_bytes = 0;    // SEL_AUX region (N-D C2R compact spectrum)
+    size_t conv_a_off = 0, conv_a_bytes = 0, conv_b_off = 0, conv_b_bytes = 0;  // SEL_CONV_A / SEL_CONV_B
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
     std::string json;
@@ -1130,6 +1133,55 @@ int plan_real_nd(Ctx& c, const vkfx_plan_desc& d, bool r2c) {
     return VKFX_OK;
 }
 
+// Real-application convolution (NdRealConvolutionIr, execute_nd_real_convolution_ir,
+// src/convolution_ir.rs:3884-4251): the N-D R2C of the `coords` input
+// tensors into SEL_CONV_A, the kernel-spectrum multiply over the compact
+// spectra into SEL_CONV_B (K * coords systems), the normalized N-D C2R of
+// those into the output.
+int plan_convolution_real(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t kernels, const ConvArgs& ca,
+                          const void* kernel) {
+    vkfx_plan* p = c.p;
+    const size_t T = (size_t)ca.T;
+    p->conv_a_bytes = coords * T * csize(c.prec);
+    p->conv_b_bytes = kernels * coords * T * csize(c.prec);
+    vkfx_plan_desc e = d;
+    e.perform_convolution = 0;
+    e.batch = coords;
+    e.transform = VKFX_R2C;
+    e.direction = VKFX_FORWARD;
+    e.normalize = 0;
+    size_t first = p->launches.size();
+    int rc = plan_real_nd(c, e, true);
+    if (rc) return rc;
+    for (size_t i = first; i < p->launches.size(); ++i) {
+        Launch& L = p->launches[i];
+        if (L.in_sel == SEL_OUT) L.in_sel = SEL_CONV_A;
+        if (L.out_sel == SEL_OUT) L.out_sel = SEL_CONV_A;
+    }
+    Launch m{};
+    m.conv = true;
+    m.ca = ca;
+    m.conv_kernel = kernel;
+    m.label = "convolution_multiply";
+    m.in_sel = SEL_CONV_A, m.out_sel = SEL_CONV_B;
+    p->launches.push_back(m);
+    vkfx_plan_desc f = e;
+    f.batch = kernels * coords;
+    f.transform = VKFX_C2R;
+    f.direction = VKFX_INVERSE;
+    f.normalize = 1;  // the inverse child is always normalized
+    first = p->launches.size();
+    rc = plan_real_nd(c, f, false);
+    if (rc) return rc;
+    for (size_t i = first; i < p->launches.size(); ++i)
+        if (p->launches[i].in_sel == SEL_IN) p->launches[i].in_sel = SEL_CONV_B;
+    c.js << "\"convolution\":{\"real\":true,\"coordinates\":" << coords << ",\"kernels\":" << kernels
+         << ",\"matrix\":" << ca.matrix << ",\"symmetric\":" << (ca.symmetric ? "true" : "false")
+         << ",\"conjugate_sequence\":" << (ca.conj_seq ? "true" : "false") << ",\"cross_power_normalize\":"
+         << (ca.cross_norm ? "true" : "false") << "},";
+    return VKFX_OK;
+}
+
 // Convolution (performConvolution, src/convolution_ir.rs:4252-4344): forward
 // C2C of every [batch][coordinate] tensor into the SEL_FULL copy, the
 // frequency-domain multiply into the output, normalized inverse C2C in place.
@@ -1600,8 +1652,15 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     size_t conv_coords = 1, conv_out_systems = d.batch;
     ConvArgs conv_args;
     const void* conv_kernel = nullptr;
+    const bool conv_real = d.perform_convolution && d.transform == VKFX_R2C && d.rank > 1;
     if (d.perform_convolution) {
-        if (d.transform != VKFX_C2C) rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "convolution is C2C only on this path");
+        if (d.transform != VKFX_C2C && !conv_real)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "performConvolution supports C2C plus multidimensional R2C application transforms");
+        if (!rc && conv_real && d.batch != 1)
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "multidimensional real performConvolution supports batch1 independent-coordinate or matrix "
+                      "K=1/K>1 layouts");
         const int M = d.matrix_convolution > 1 ? (int)d.matrix_convolution : 0;
         if (!rc && M && M != 2 && M != 3)
             rc = fail(VKFX_ERR_INVALID_ARGUMENT, "matrix convolution IR requires a 2x2 or 3x3 matrix");
@@ -1616,13 +1675,13 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         if (!rc && K > 1 && d.batch != 1)
             rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
                       "numberKernels is a one-input fan-out: multi-kernel convolution takes batch 1");
-        if (!rc && !M && conv_coords != 1)
+        if (!rc && !conv_real && !M && conv_coords != 1)
             rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
                       "coordinateFeatures > 1 without matrixConvolution is only materialized for real application "
                       "convolution");
         if (!rc && M && (size_t)std::max<uint32_t>(1, d.coordinate_features) != (size_t)M)
             rc = fail(VKFX_ERR_INVALID_ARGUMENT, "matrix convolution coordinate count must equal its matrix size");
-        if (!rc && d.rank > 1 && M && (d.batch != 1 || K != 1))
+        if (!rc && !conv_real && d.rank > 1 && M && (d.batch != 1 || K != 1))
             rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
                       "multidimensional performConvolution supports scalar K=1/K>1 layouts or a batch1/K1 matrix "
                       "layout");
@@ -1631,22 +1690,35 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             formatted = formatted || d.in_axis_stride[i] || d.out_axis_stride[i];
             padded = padded || d.zero_left[i] != d.zero_right[i];
         }
-        if (!rc && formatted)
-            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "formatted performConvolution requires a real application");
-        if (!rc && padded)
+        // formatted: scalar batch1 K1 real ownership; zero padding: real with
+        // a nonsymmetric matrix or no matrix (config.rs:1273-1300)
+        if (!rc && formatted && !(conv_real && conv_coords == 1 && K == 1 && !M))
             rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
-                      "performConvolution zero padding requires a multidimensional real application");
+                      conv_real ? "multidimensional real formatted performConvolution currently requires scalar batch1 K1"
+                                : "formatted performConvolution requires a real application");
+        if (!rc && padded && !(conv_real && !(M && d.symmetric_kernel)))
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      conv_real ? "multidimensional real performConvolution zero padding requires batch1/K1 "
+                                  "nonsymmetric matrix ownership"
+                                : "performConvolution zero padding requires a multidimensional real application");
         const bool mixed = d.precision == VKFX_F16_STORAGE_F32_COMPUTE || d.precision == VKFX_F64_COMPUTE_F32_STORAGE;
-        if (!rc && mixed &&
+        if (!rc && mixed && !conv_real &&
             (d.rank != 1 || d.batch != 1 || conv_coords != 1 || K != 1 || d.conjugate_sequence ||
              d.cross_power_normalize))
             rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
                       "mixed-storage performConvolution requires dense default-policy 1D C2C batch1 scalar K1");
+        // config.rs:1244-1272: unformatted real ownership (scalar, independent K>1 fan-out, 3x3 matrix)
+        if (!rc && mixed && conv_real &&
+            !((conv_coords == 1 && !M) || (conv_coords > 1 && !M && K > 1) || (M == 3 && conv_coords == 3)))
+            rc = fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                      "mixed-storage real performConvolution requires scalar, independent-coordinate K>1 or 3x3 "
+                      "matrix ownership");
         conv_out_systems = K > 1 ? K : d.batch;
-        size_t T = 1;
-        for (uint32_t i = 0; i < d.rank; ++i) T *= d.dims[i];
+        size_t T = 1;  // tensor length of the spectra: compact for the real application
+        for (uint32_t i = 0; i < d.rank; ++i) T *= (conv_real && i + 1 == d.rank) ? d.dims[i] / 2 + 1 : d.dims[i];
+        const bool independent = conv_real ? !M : d.independent_coordinates != 0;
         const size_t planes = M ? (d.symmetric_kernel ? (size_t)(M * (M + 1) / 2) : (size_t)(M * M))
-                                : (d.independent_coordinates ? conv_coords : 1);
+                                : (independent ? conv_coords : 1);
         const size_t need = K * planes * T * (f64 ? 16 : 8);
         if (!rc && (!d.kernel_spectrum || d.kernel_spectrum_bytes != need))
             rc = fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "convolution kernel spectrum: expected " + std::to_string(need) +
@@ -1668,7 +1740,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         conv_args.kernel_count = (int)K;
         conv_args.matrix = M;
         conv_args.symmetric = d.symmetric_kernel ? 1 : 0;
-        conv_args.independent = d.independent_coordinates ? 1 : 0;
+        conv_args.independent = independent ? 1 : 0;
         conv_args.conj_seq = d.conjugate_sequence ? 1 : 0;
         conv_args.cross_norm = d.cross_power_normalize ? 1 : 0;
         if (rc) {
@@ -1677,7 +1749,11 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         }
     }
     try {
-        if (d.perform_convolution) {
+        if (conv_real) {
+            p->in_bytes = conv_coords * total * rs;
+            p->out_bytes = conv_out_systems * conv_coords * total * rs;
+            rc = plan_convolution_real(c, d, conv_coords, conv_out_systems, conv_args, conv_kernel);
+        } else if (d.perform_convolution) {
             size_t T = 1;
             for (uint32_t i = 0; i < d.rank; ++i) T *= d.dims[i];
             p->in_bytes = d.batch * conv_coords * T * cs;
@@ -1722,11 +1798,12 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         // Boundary passes: type conversion (mixed precisions), formatted
         // layouts and zero padding sit between the caller's buffers and dense
         // compute-type copies in the workspace that the FFT passes use.
-        const bool real_in = d.transform == VKFX_R2C || r2r, real_out = d.transform == VKFX_C2R || r2r;
+        const bool real_in = d.transform == VKFX_R2C || r2r,
+                   real_out = d.transform == VKFX_C2R || r2r || conv_real;
         const size_t rank = d.rank;
         long long in_dims[VKFX_MAX_RANK], out_dims[VKFX_MAX_RANK];
         for (size_t i = 0; i < rank; ++i) in_dims[i] = out_dims[i] = (long long)d.dims[i];
-        if (d.transform == VKFX_R2C) out_dims[rank - 1] = (long long)(d.dims[rank - 1] / 2 + 1);
+        if (d.transform == VKFX_R2C && !conv_real) out_dims[rank - 1] = (long long)(d.dims[rank - 1] / 2 + 1);
         if (d.transform == VKFX_C2R) in_dims[rank - 1] = (long long)(d.dims[rank - 1] / 2 + 1);
         // resolve_formatted_axis_strides / _batch_stride (config.rs:1463-1522)
         auto resolve = [&](const long long* dims, const uint64_t* over, uint64_t batch_over, long long* st,
@@ -1772,8 +1849,10 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             return brc;
         }
         const bool fwd = d.direction == VKFX_FORWARD;
-        const bool zp_in = any_zero && (d.zero_frequency ? !fwd : fwd);
-        const bool zp_out = any_zero && !zp_in;
+        // a real-application convolution masks its input (forward R2C) and
+        // its output (inverse C2R): spatial padding on both children
+        const bool zp_in = any_zero && (conv_real || (d.zero_frequency ? !fwd : fwd));
+        const bool zp_out = any_zero && (conv_real || !zp_in);
         const bool mixed = store_t != comp_t;
         const bool need_in = mixed || fmt_in || zp_in, need_out = mixed || fmt_out || zp_out;
         const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
@@ -1864,8 +1943,13 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->aux_off = (p->work_bytes + 255) / 256 * 256;
         p->work_bytes = p->aux_off + p->aux_bytes;
     }
+    if (p->conv_a_bytes) {
+        p->conv_a_off = (p->work_bytes + 255) / 256 * 256;
+        p->conv_b_off = (p->conv_a_off + p->conv_a_bytes + 255) / 256 * 256;
+        p->work_bytes = p->conv_b_off + p->conv_b_bytes;
+    }
     if (p->stage_in_bytes || p->stage_out_bytes) {
-        // workspace: [lane work][full complex][aux][stage in][stage out]
+        // workspace: [lane work][full complex][aux][conv a][conv b][stage in][stage out]
         auto align = [](size_t v) { return (v + 255) / 256 * 256; };
         const bool shared = p->stage_shared;
         p->stage_in_off = align(p->work_bytes);
@@ -1958,6 +2042,8 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
                          : which == SEL_STAGE_OUT    ? (char*)work + plan->stage_out_off
                          : which == SEL_FULL         ? (char*)work + plan->full_off
                          : which == SEL_AUX          ? (char*)work + plan->aux_off
+                         : which == SEL_CONV_A       ? (char*)work + plan->conv_a_off
+                         : which == SEL_CONV_B       ? (char*)work + plan->conv_b_off
                                                      : (char*)work + (size_t)lane * plan->work_lane;
             return base + off;
         };

@@ -570,9 +570,12 @@ class Plan:
 
 
 class ConvolutionIr:
-    """ConvolutionIr / NdConvolutionIr (convolution_ir.rs): forward C2C of every
-    [batch][coordinate] tensor, multiply by `kernel_spectrum` (frequency domain,
-    [kernel][plane][tensor]), normalized inverse C2C."""
+    """ConvolutionIr / NdConvolutionIr / NdRealConvolutionIr (convolution_ir.rs):
+    forward transform of every [batch][coordinate] tensor, multiply by
+    `kernel_spectrum` (frequency domain, [kernel][plane][tensor]), normalized
+    inverse. C2C configs convolve complex tensors; an N-D RealToComplex config
+    (batch 1) is the real application: R2C, multiply over the compact
+    [.., N/2+1] spectra, C2R, real tensors on both sides."""
 
     def __init__(self, config: FftConfig, kernel_spectrum: np.ndarray):
         if config.convolution_conjugation == ConvolutionConjugation.Kernel:
@@ -587,13 +590,31 @@ class ConvolutionIr:
         self.coordinates = m if m else max(1, cfg.coordinate_features)
         self.kernel_count = max(1, cfg.convolution_kernel_count)
         self.independent = (not m) and self.coordinates > 1
+        self.real = cfg.transform == TransformKind.RealToComplex
+        # caller-side layouts: `coordinates` input tensors, K * coordinates
+        # output tensors, full (real or complex) dims on both sides
+        systems_out = self.kernel_count if self.kernel_count > 1 else cfg.batch_count
+        self._sides = []
+        for systems in (cfg.batch_count * self.coordinates, systems_out * self.coordinates):
+            side = FftConfig(**{k: (list(v) if isinstance(v, list) else v) for k, v in cfg.__dict__.items()})
+            side.transform = TransformKind.ComplexToComplex
+            side.batch_count = systems
+            self._sides.append(TransformIr(side, Direction.Forward))
 
     @staticmethod
     def build(config: FftConfig, kernel_spectrum: np.ndarray) -> "ConvolutionIr":
         return ConvolutionIr(config, kernel_spectrum)
 
     def tensor_len(self) -> int:
+        """Elements of one input / output tensor (real for the real application)."""
         return int(np.prod(self.config.dimensions))
+
+    def spectrum_len(self) -> int:
+        """Elements of one kernel-spectrum plane (compact for the real application)."""
+        dims = list(self.config.dimensions)
+        if self.real:
+            dims[-1] = dims[-1] // 2 + 1
+        return int(np.prod(dims))
 
     def input_count(self) -> int:
         return self.config.batch_count * self.coordinates * self.tensor_len()
@@ -735,20 +756,23 @@ class HipExecutionContext:
     def execute_convolution(self, conv: ConvolutionIr, x: np.ndarray) -> np.ndarray:
         """Host round trip of a convolution (the plan is built once per ConvolutionIr)."""
         ir = conv.ir
-        x = np.ascontiguousarray(x, dtype=ir.complex_dtype).reshape(-1)
+        vdt = ir.real_dtype if conv.real else ir.complex_dtype
+        x = np.ascontiguousarray(x, dtype=vdt).reshape(-1)
         if x.size != conv.input_count():
             raise VkFftError(-5, f"InputLengthMismatch {{ expected: {conv.input_count()}, actual: {x.size} }}")
         plan = getattr(conv, "_plan", None)
         if plan is None or plan.ctx is not self:
             plan = Plan(self, ir, desc=conv.desc())
             conv._plan = plan
-        xs = np.ascontiguousarray(ir.to_storage(x))
-        n_out = conv.output_count()
+        side_in, side_out = conv._sides
+        xs = np.ascontiguousarray(ir.to_storage(side_in.pack_input(x)))
+        n_out = side_out.physical_output_count()
         f16 = ir.config.precision == Precision.F16StorageF32Compute
-        out = np.empty(2 * n_out, dtype=np.float16) if f16 else np.empty(n_out, dtype=ir.complex_dtype)
+        scal = 1 if conv.real else 2
+        out = np.empty(scal * n_out, dtype=np.float16) if f16 else np.empty(n_out, dtype=vdt)
         _check(self._L.vkfx_execute_host(plan.handle, xs.ctypes.data, xs.nbytes, out.ctypes.data, out.nbytes),
                self._L)
-        return ir.from_storage(out, True)
+        return side_out.unpack_output(ir.from_storage(out, not conv.real))
 
     def _io_dtypes(self, ir: TransformIr):
         kind = ir.config.transform
