@@ -147,6 +147,9 @@ typedef struct {
     uint32_t kernel_count;                  /* 0 or 1 = one kernel */
     const void *kernel_spectrum;
     uint64_t kernel_spectrum_bytes;
+    /* FftConfig::omit_dimension (config.rs:651, 844-853, 1053-1067): bit i set
+     * leaves axis i untransformed (rank > 1; never the real axis of R2C/C2R). */
+    uint32_t omit_dimension;
 } vkfx_plan_desc;
 
 /* ---------------------------------------------------------------- context */

@@ -1102,7 +1102,7 @@ int plan_real_nd(Ctx& c, const vkfx_plan_desc& d, bool r2c) {
     e.dims[r - 1] = h;
     e.direction = r2c ? VKFX_FORWARD : VKFX_INVERSE;
     e.normalize = r2c ? 0 : d.normalize;
-    const uint32_t omit = 1u << (r - 1);
+    const uint32_t omit = d.omit_dimension | 1u << (r - 1);
     int rc;
     if (r2c) {
         rc = plan_r2c(c, n, rows);
@@ -1596,6 +1596,16 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     const bool r2r = d.transform >= VKFX_DCT_I;
     if (r2r && d.rank != 1)
         return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "multi-dimensional DCT/DST is outside this path");
+    // omitDimension (config.rs:1053-1067)
+    if (d.omit_dimension >> d.rank)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "omitDimension metadata must match the FFT dimensionality");
+    if (d.omit_dimension && d.rank == 1)
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "omitDimension currently supports multidimensional transforms only");
+    if ((d.transform == VKFX_R2C || d.transform == VKFX_C2R) && (d.omit_dimension >> (d.rank - 1) & 1u))
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "omitDimension cannot disable the contiguous R2C/C2R axis");
+    if (d.omit_dimension && d.perform_convolution)
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
+                    "performConvolution currently requires active dimensions without omitDimension");
     if (d.transform == VKFX_DCT_I && d.dims[0] < 2)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "InvalidTransformLength { axis: 0, transform: DCT-I, length: 1 }");
     // storage and compute scalar types (0 f16, 1 f32, 2 f64)
@@ -1770,7 +1780,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 if (alg == VKFX_ALG_RADER) conv = 0;  // Bluestein fallback uses M = next smooth >= 2N-1
                 rc = plan_c2c_1d(c, d.dims[0], d.batch, d.direction, d.normalize != 0, a, conv);
             } else {
-                rc = plan_c2c_nd(c, d);
+                rc = plan_c2c_nd(c, d, d.omit_dimension);
             }
         } else if (r2r) {
             const size_t n = d.dims[0];

@@ -145,6 +145,7 @@ class _PlanDesc(ctypes.Structure):
         ("kernel_count", ctypes.c_uint32),
         ("kernel_spectrum", ctypes.c_void_p),
         ("kernel_spectrum_bytes", ctypes.c_uint64),
+        ("omit_dimension", ctypes.c_uint32),
     ]
 
 
@@ -258,6 +259,7 @@ class FftConfig:
     matrix_convolution: int = 1
     symmetric_convolution_kernel: bool = False
     convolution_kernel_count: int = 1
+    omit_dimension: List[bool] = field(default_factory=lambda: [False] * MAX_RANK)
 
     @staticmethod
     def new(dimensions: Sequence[int]) -> "FftConfig":
@@ -313,6 +315,13 @@ class FftConfig:
 
     def with_zero_padding_domain(self, domain: ZeroPaddingDomain) -> "FftConfig":
         self.zero_padding_domain = ZeroPaddingDomain(domain)
+        return self
+
+    def with_omit_dimension(self, axis: int, omit: bool = True) -> "FftConfig":
+        """config.rs:844-853: leave `axis` untransformed."""
+        if not 0 <= axis < len(self.dimensions):
+            raise VkFftError(-7, "ValueOutOfRange { field: omitDimension axis }")
+        self.omit_dimension[axis] = bool(omit)
         return self
 
     # convolution knobs (config.rs:734-800)
@@ -416,6 +425,7 @@ class TransformIr:
         d.zero_frequency = int(c.zero_padding_domain == ZeroPaddingDomain.Frequency)
         # a convolution config without its kernel spectrum fails at plan time
         d.perform_convolution = int(c.perform_convolution)
+        d.omit_dimension = sum(1 << i for i in range(len(c.dimensions)) if c.omit_dimension[i])
         return d
 
     # ---- formatted layouts (the host-side pack/unpack of the reference's
@@ -716,12 +726,8 @@ class HipExecutionContext:
         return self.device_profile()["name"]
 
     def plan(self, ir: TransformIr) -> Plan:
-        c = ir.config
-        key = (tuple(c.dimensions), c.batch_count, int(c.precision), int(c.transform), c.normalize_inverse,
-               int(ir.direction), tuple(int(a) for a in ir.axis_algorithms), tuple(ir.convolution_lens),
-               tuple(c.input_buffer_axis_strides), tuple(c.output_buffer_axis_strides),
-               c.input_buffer_batch_stride, c.output_buffer_batch_stride, tuple(c.zero_padding),
-               int(c.zero_padding_domain), tuple(c.grouped_batch))
+        # keyed on every field the library sees
+        key = bytes(ir.desc())
         if key not in self._plans:
             self._plans[key] = Plan(self, ir)
         return self._plans[key]
