@@ -114,3 +114,67 @@ def test_r2r_mixed_precision_and_device_in_place(hip_ctx):
 def test_dct1_length_one_rejected(hip_ctx):
     with pytest.raises(vk.VkFftError):
         hip_ctx.plan(r2r_ir("dct1", 1, 1, F32))
+
+
+# ---- N-D (NdR2rIr, src/r2r_ir.rs:1769-1990, execute_nd_r2r_ir :2216-2300) ----
+
+def oracle_nd(x, dims, batch, name, axes):
+    """The oracle's 1-D direct sums along each axis in `axes`."""
+    v = x.reshape((batch,) + tuple(dims)).astype(np.float64)
+    for ax in axes:
+        moved = np.moveaxis(v, ax + 1, -1)
+        shp = moved.shape
+        out = o.r2r_batch(np.ascontiguousarray(moved).reshape(-1), shp[-1], name, threads=8).reshape(shp)
+        v = np.moveaxis(out, -1, ax + 1)
+    return v.reshape(-1)
+
+
+def r2r_nd_cfg(name, dims, batch, prec, normalize=False):
+    return vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec).with_transform(kind_of(name)) \
+        .with_inverse_normalization(normalize)
+
+
+@pytest.mark.parametrize("name", KINDS)
+def test_r2r_nd_forward(hip_ctx, name):
+    import scipy.fft as sf
+    dims, batch = [12, 10, 6], 2
+    x = o.uniform(int(np.prod(dims)) * batch, 51, np.float64)
+    y = hip_ctx.execute_transform(vk.TransformIr.build(r2r_nd_cfg(name, dims, batch, F64), FWD), x)
+    f = sf.dctn if name.startswith("dct") else sf.dstn
+    ref = f(x.reshape((batch,) + tuple(dims)), type=int(name[-1]), axes=(1, 2, 3)).reshape(-1)
+    assert o.rel_l2(y, ref) <= 1e-13
+    dims32 = [64, 48]
+    x32 = o.uniform(64 * 48 * 3, 52, np.float32)
+    y32 = hip_ctx.execute_transform(vk.TransformIr.build(r2r_nd_cfg(name, dims32, 3, F32), FWD), x32)
+    assert o.rel_l2(y32, oracle_nd(x32, dims32, 3, name, (0, 1))) <= 1e-5
+
+
+@pytest.mark.parametrize("name", ["dct1", "dct2", "dst3", "dst4"])
+def test_r2r_nd_round_trip_and_omit(hip_ctx, name):
+    import scipy.fft as sf
+    dims, batch = [20, 1, 36], 2
+    x = o.uniform(20 * 36 * batch, 53, np.float64)
+    y = hip_ctx.execute_transform(vk.TransformIr.build(r2r_nd_cfg(name, dims, batch, F64), FWD), x)
+    z = hip_ctx.execute_transform(vk.TransformIr.build(r2r_nd_cfg(name, dims, batch, F64, True), INV), y)
+    assert o.rel_l2(z, x) <= 1e-13
+    # omitting axis 0 transforms axis 2 only
+    c = r2r_nd_cfg(name, dims, batch, F64).with_omit_dimension(0, True)
+    yo = hip_ctx.execute_transform(vk.TransformIr.build(c, FWD), x)
+    f = sf.dct if name.startswith("dct") else sf.dst
+    ref = f(x.reshape(batch, 20, 1, 36), type=int(name[-1]), axis=3).reshape(-1)
+    assert o.rel_l2(yo, ref) <= 1e-13
+
+
+def test_r2r_nd_layouts(hip_ctx):
+    import scipy.fft as sf
+    dims, batch = [24, 30], 2
+    x = o.uniform(24 * 30 * batch, 54, np.float64)
+    c = r2r_nd_cfg("dct2", dims, batch, F64).with_zero_padding(1, 25, 30).with_output_buffer_batch_stride(24 * 30 + 7)
+    y = hip_ctx.execute_transform(vk.TransformIr.build(c, FWD), x)
+    xm = x.reshape(batch, 24, 30).copy()
+    xm[:, :, 25:] = 0
+    assert o.rel_l2(y, sf.dctn(xm, type=2, axes=(1, 2)).reshape(-1)) <= 1e-13
+    irm = vk.TransformIr.build(r2r_nd_cfg("dst2", dims, batch, vk.Precision.F64ComputeF32Storage), FWD)
+    ym = hip_ctx.execute_transform(irm, x.astype(np.float32))
+    assert o.rel_l2(ym, sf.dstn(x.astype(np.float32).astype(np.float64).reshape(batch, 24, 30), type=2,
+                                axes=(1, 2)).reshape(-1)) <= 1e-7

@@ -142,6 +142,7 @@ int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_
 // 3 DST-III m == n 1, else 2.
 struct R2rArgs {
     long long n = 0, L = 0, batch = 0;
+    long long inner = 1;  // element stride of a line (lines of a strided axis)
     int off = 0, ph = 0, wmode = 0;
     int r = 0, pq = 0, q2 = 0, im = 0;
     double s = 1.0;

@@ -3,7 +3,8 @@
 // between a pre pass and a post pass:
 //   a[m] = w(m) x[m - off] exp(-i pi m ph / (2N)),  m - off in [0, N), else 0
 //   X[k] = s * sel( exp(-i pi (k + q) pq / (2N)) A[k + r] ),  A = FFT_L(a)
-// with sel = Re or -Im. The per-type parameters (runtime.cpp, r2r_params)
+// with sel = Re or -Im. Lines of a strided axis (N-D transforms) are read
+// and written in place with element stride `inner`. The per-type parameters (runtime.cpp, r2r_params)
 // follow from writing each cosine / sine sum as the real or imaginary part
 // of a zero-padded DFT.
 #include <hip/hip_runtime.h>
@@ -27,13 +28,15 @@ __global__ __launch_bounds__(256) void k_r2r_pre(const T* __restrict__ x, T* __r
          i += (long long)gridDim.x * blockDim.x) {
         const long long b = i / p.L, m = i - b * p.L;
         const long long j = m - p.off;
+        // line b of the axis: element j at (b / inner) * n * inner + b % inner + j * inner
+        const long long bo = b / p.inner, bc = b - bo * p.inner;
         double re = 0.0, im = 0.0;
         if (j >= 0 && j < p.n) {
             double w = 1.0;
             if (p.wmode == 1) w = (j == 0 || j == p.n - 1) ? 1.0 : 2.0;      // DCT-I
             else if (p.wmode == 2) w = j == 0 ? 1.0 : 2.0;                    // DCT-III
             else if (p.wmode == 3) w = m == p.n ? 1.0 : 2.0;                  // DST-III
-            const double v = w * (double)x[b * p.n + j];
+            const double v = w * (double)x[bo * p.n * p.inner + bc + j * p.inner];
             if (p.ph) {
                 double c, s;
                 phase((double)m, 2.0 * (double)p.n, &c, &s);
@@ -63,7 +66,8 @@ __global__ __launch_bounds__(256) void k_r2r_post(const T* __restrict__ A, T* __
             re = r2;
             im = i2;
         }
-        X[i] = (T)(p.s * (p.im ? -im : re));
+        const long long bo = b / p.inner, bc = b - bo * p.inner;
+        X[bo * p.n * p.inner + bc + k * p.inner] = (T)(p.s * (p.im ? -im : re));
     }
 }
 
@@ -80,7 +84,7 @@ static int go(bool pre, const R2rArgs& p, const void* in, void* out, hipStream_t
 }
 
 int launch_r2r(bool pre, int prec, const R2rArgs& p, const void* in, void* out, hipStream_t s) {
-    if (p.n <= 0 || p.L <= 0 || p.batch <= 0) return (int)hipErrorInvalidValue;
+    if (p.n <= 0 || p.L <= 0 || p.batch <= 0 || p.inner <= 0 || p.batch % p.inner) return (int)hipErrorInvalidValue;
     return prec ? go<double>(pre, p, in, out, s) : go<float>(pre, p, in, out, s);
 }
 

@@ -1252,7 +1252,8 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
 // The inverse direction runs the type's inverse partner (II <-> III,
 // r2r_ir.rs:2308-2316), scaled when normalized (inverse_pair_scale,
 // r2r_ir.rs:2318-2346).
-int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize) {
+int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize, size_t inner = 1,
+             int in_sel = SEL_IN) {
     vkfx_plan* p = c.p;
     // kind: 0..3 DCT-I..IV, 4..7 DST-I..IV
     int eff = kind;
@@ -1270,6 +1271,7 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize) 
     R2rArgs a;
     a.n = (long long)n;
     a.batch = (long long)batch;
+    a.inner = (long long)inner;
     switch (eff) {
         case 0: a.L = 2 * (a.n - 1); a.wmode = 1; break;
         case 1: a.L = 2 * a.n; a.pq = 1; a.s = 2.0; break;
@@ -1285,7 +1287,7 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize) 
     const bool f64 = c.prec == 1;
     AxisDecision ad = plan_c2c_axis(L, batch, f64, false, tuning_for_amd(f64),
                                     planner_device(p->ctx->profile.shared_memory_bytes));
-    p->full_bytes = batch * L * csize(c.prec);
+    p->full_bytes = std::max(p->full_bytes, batch * L * csize(c.prec));
     p->serial = true;
     static const char* kNames[] = {"dct1", "dct2", "dct3", "dct4", "dst1", "dst2", "dst3", "dst4"};
     c.js << "\"r2r\":{\"type\":\"" << kNames[kind] << "\",\"runs\":\"" << kNames[eff] << "\",\"fft_len\":" << L
@@ -1296,7 +1298,7 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize) 
     pre.r2r = 1;
     pre.ra = a;
     pre.label = "r2r_pre";
-    pre.in_sel = SEL_IN, pre.out_sel = SEL_FULL;
+    pre.in_sel = in_sel, pre.out_sel = SEL_FULL;
     p->launches.push_back(pre);
     const size_t first = p->launches.size();
     int rc = plan_c2c_1d(c, L, batch, -1, false, ad.algorithm,
@@ -1312,6 +1314,49 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize) 
     post.label = "r2r_post";
     post.in_sel = SEL_FULL, post.out_sel = SEL_OUT;
     p->launches.push_back(post);
+    return VKFX_OK;
+}
+
+// N-D DCT / DST (NdR2rIr, src/r2r_ir.rs:1769-1990, execute_nd_r2r_ir
+// :2216-2300): the same type along every active axis, fastest first; each
+// axis is the 1-D pre pass / C2C / post pass over its lines, read and written
+// in place with the axis stride. Axes of length 1 and omitted axes are left
+// as they are; the inverse normalizes each axis by its own factor.
+int plan_r2r_nd(Ctx& c, const vkfx_plan_desc& d) {
+    vkfx_plan* p = c.p;
+    size_t per = 1;
+    for (uint32_t i = 0; i < d.rank; ++i) per *= d.dims[i];
+    bool first = true;
+    for (int ax = (int)d.rank - 1; ax >= 0; --ax) {
+        const size_t n = d.dims[ax];
+        if (n == 1 || (d.omit_dimension >> ax & 1u)) continue;
+        if (d.transform == VKFX_DCT_I && n < 2)
+            return fail(VKFX_ERR_INVALID_ARGUMENT, "InvalidTransformLength: DCT-I axis of length 1");
+        size_t inner = 1;
+        for (uint32_t j = ax + 1; j < d.rank; ++j) inner *= d.dims[j];
+        const int rc = plan_r2r(c, n, d.batch * (per / n), d.transform - VKFX_DCT_I, d.direction, d.normalize != 0,
+                                inner, first ? SEL_IN : SEL_OUT);
+        if (rc) return rc;
+        first = false;
+    }
+    if (first) {
+        // no active axis: the transform is a copy
+        Launch L{};
+        L.boundary = true;
+        L.label = "copy";
+        L.in_sel = SEL_IN, L.out_sel = SEL_OUT;
+        BoundaryArgs& a = L.ba;
+        a.rank = 1;
+        a.dims[0] = (long long)per;
+        a.src_stride[0] = a.dst_stride[0] = 1;
+        a.tensor_len = (long long)per;
+        a.batch = (long long)d.batch;
+        a.src_batch = a.dst_batch = (long long)per;
+        a.src_scalars = a.dst_scalars = 1;
+        a.src_type = a.dst_type = c.prec ? 2 : 1;
+        p->launches.push_back(L);
+    }
+    p->serial = true;
     return VKFX_OK;
 }
 
@@ -1594,8 +1639,6 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         return fail(VKFX_ERR_INVALID_ARGUMENT, "C2R requires Direction::Inverse");
     if (d.transform < VKFX_C2C || d.transform > VKFX_DST_IV) return fail(VKFX_ERR_INVALID_ARGUMENT, "unknown transform");
     const bool r2r = d.transform >= VKFX_DCT_I;
-    if (r2r && d.rank != 1)
-        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "multi-dimensional DCT/DST is outside this path");
     // omitDimension (config.rs:1053-1067)
     if (d.omit_dimension >> d.rank)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "omitDimension metadata must match the FFT dimensionality");
@@ -1606,7 +1649,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     if (d.omit_dimension && d.perform_convolution)
         return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH,
                     "performConvolution currently requires active dimensions without omitDimension");
-    if (d.transform == VKFX_DCT_I && d.dims[0] < 2)
+    if (d.transform == VKFX_DCT_I && d.rank == 1 && d.dims[0] < 2)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "InvalidTransformLength { axis: 0, transform: DCT-I, length: 1 }");
     // storage and compute scalar types (0 f16, 1 f32, 2 f64)
     const bool f64 = d.precision == VKFX_F64 || d.precision == VKFX_F64_COMPUTE_F32_STORAGE;
@@ -1783,9 +1826,11 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 rc = plan_c2c_nd(c, d, d.omit_dimension);
             }
         } else if (r2r) {
-            const size_t n = d.dims[0];
-            p->in_bytes = p->out_bytes = d.batch * n * rs;
-            rc = plan_r2r(c, n, d.batch, d.transform - VKFX_DCT_I, d.direction, d.normalize != 0);
+            p->in_bytes = p->out_bytes = total * rs;
+            if (d.rank == 1)
+                rc = plan_r2r(c, d.dims[0], d.batch, d.transform - VKFX_DCT_I, d.direction, d.normalize != 0);
+            else
+                rc = plan_r2r_nd(c, d);
         } else {
             const size_t n = d.dims[d.rank - 1];
             const size_t real_elems = total, compact_elems = total / n * (n / 2 + 1);
