@@ -230,6 +230,17 @@ int vkfx_ticket_wait(vkfx_ticket *ticket, void *h_out, uint64_t out_bytes);
  * context's pools. */
 int vkfx_ticket_destroy(vkfx_ticket *ticket);
 
+/* HipExecutionContext::cached_transient_buffer_count / pooled_stream_count
+ * (src/backend/hip/runtime.rs:1828-1840) and the in-flight submission count
+ * that guards clear_runtime_caches (:2275-2284). Any pointer may be NULL. */
+int vkfx_context_cache_stats(vkfx_context *ctx, uint64_t *transient_buffers, uint64_t *pooled_streams,
+                             uint64_t *in_flight);
+/* HipExecutionContext::clear_runtime_caches (src/backend/hip/runtime.rs:2275-2330):
+ * frees the pooled transient buffers and streams of the ticket and chain
+ * calls; fails (VKFX_ERR_NATIVE_RUNTIME) while tickets are in flight.
+ * Plans keep their own tables and workspace until vkfx_plan_destroy. */
+int vkfx_context_clear_caches(vkfx_context *ctx);
+
 /* Device-resident chain, the HIP counterpart of
  * CudaExecutionContext::execute_program_chain_complex32
  * (src/backend/cuda/runtime.rs:1744-1809): plans[i]'s output is plans[i+1]'s

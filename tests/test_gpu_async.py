@@ -136,3 +136,30 @@ def test_chain_transition_mismatch(hip_ctx):
     with pytest.raises(vk.VkFftError) as ei:
         hip_ctx.execute_chain([a], o.complex_uniform(100, 1, np.complex64))
     assert ei.value.status == -5
+
+
+def test_runtime_caches_and_clear(hip_ctx):
+    """hip/runtime.rs:3038-3095, 3225-3343: with two tickets in flight the
+    caches cannot be cleared; afterwards the pooled streams and transient
+    buffers are counted, clearing empties them and later submissions work."""
+    a = (c2c_ir([64], 1), o.complex_uniform(64, 6, np.complex64))
+    b = (c2c_ir([96], 1), o.complex_uniform(96, 7, np.complex64))
+    ta = hip_ctx.submit_transform_async(*a)
+    tb = hip_ctx.submit_transform_async(*b)
+    assert hip_ctx.in_flight_submission_count() == 2
+    with pytest.raises(vk.VkFftError):
+        hip_ctx.clear_runtime_caches()
+    yb, ya = tb.wait(), ta.wait()
+    tb.close()
+    ta.close()
+    assert hip_ctx.in_flight_submission_count() == 0
+    assert hip_ctx.pooled_stream_count() >= 2
+    assert hip_ctx.cached_transient_buffer_count() > 0
+    for (ir, x), y in ((a, ya), (b, yb)):
+        ref = o.fft_batch(x.astype(np.complex128), ir.config.dimensions[0], "forward", False)
+        assert np.max(np.abs(y - ref)) <= 2e-3 * x.size  # the reference test's bound
+    hip_ctx.clear_runtime_caches()
+    assert hip_ctx.pooled_stream_count() == 0 and hip_ctx.cached_transient_buffer_count() == 0
+    t = hip_ctx.submit_transform_async(*a)
+    assert np.array_equal(t.wait(), ya)
+    t.close()

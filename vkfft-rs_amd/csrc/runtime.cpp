@@ -13,6 +13,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -75,6 +76,8 @@ struct vkfx_context {
     vkfx_device_profile profile{};
     std::vector<PoolBuf> dev_pool, host_pool;  // free buffers
     std::vector<hipStream_t> stream_pool;      // free streams for tickets
+    std::mutex mu;                             // guards the pools and `active`
+    int active = 0;                            // tickets submitted and not yet destroyed
 };
 
 namespace {
@@ -2214,6 +2217,7 @@ namespace {
 // allocates one. When `s` is given and the buffer carries a release event,
 // s waits on it before the buffer is touched.
 int pool_take(vkfx_context* ctx, bool host, size_t bytes, hipStream_t s, PoolBuf* out) {
+    std::lock_guard<std::mutex> lock(ctx->mu);
     std::vector<PoolBuf>& pool = host ? ctx->host_pool : ctx->dev_pool;
     for (size_t i = 0; i < pool.size(); ++i) {
         if (pool[i].bytes != bytes) continue;
@@ -2238,6 +2242,7 @@ int pool_take(vkfx_context* ctx, bool host, size_t bytes, hipStream_t s, PoolBuf
 // there so the next user waits for the work already queued on it.
 void pool_give(vkfx_context* ctx, bool host, PoolBuf b, hipStream_t s) {
     if (!b.p) return;
+    std::lock_guard<std::mutex> lock(ctx->mu);
     if (s) {
         if (!b.ready && hipEventCreateWithFlags(&b.ready, hipEventDisableTiming) != hipSuccess) b.ready = nullptr;
         if (b.ready && hipEventRecord(b.ready, s) != hipSuccess) {
@@ -2314,16 +2319,23 @@ int vkfx_submit_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, vkfx_
         pool_give(ctx, false, t->d_work, nullptr);
         pool_give(ctx, true, t->h_in, nullptr);
         pool_give(ctx, true, t->h_out, nullptr);
-        if (t->stream) ctx->stream_pool.push_back(t->stream);
+        if (t->stream) {
+            std::lock_guard<std::mutex> lock(ctx->mu);
+            ctx->stream_pool.push_back(t->stream);
+        }
         if (t->done) (void)hipEventDestroy(t->done);
         delete t;
         return rc;
     };
     hipError_t e = hipSuccess;
-    if (!ctx->stream_pool.empty()) {
-        t->stream = ctx->stream_pool.back();
-        ctx->stream_pool.pop_back();
-    } else {
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        if (!ctx->stream_pool.empty()) {
+            t->stream = ctx->stream_pool.back();
+            ctx->stream_pool.pop_back();
+        }
+    }
+    if (!t->stream) {
         e = hipStreamCreate(&t->stream);  // default priority
         if (e != hipSuccess) {
             t->stream = nullptr;
@@ -2349,6 +2361,10 @@ int vkfx_submit_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, vkfx_
     e = hipMemcpyAsync(t->h_out.p, t->d_out.p, plan->out_bytes, hipMemcpyDeviceToHost, t->stream);
     if (e == hipSuccess) e = hipEventRecord(t->done, t->stream);
     if (e != hipSuccess) return cleanup(hip_fail(e, "ticket enqueue"));
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        ++ctx->active;
+    }
     *out = t;
     return VKFX_OK;
 }
@@ -2388,10 +2404,54 @@ int vkfx_ticket_destroy(vkfx_ticket* t) {
     pool_give(ctx, false, t->d_work, nullptr);
     pool_give(ctx, true, t->h_in, nullptr);
     pool_give(ctx, true, t->h_out, nullptr);
-    ctx->stream_pool.push_back(t->stream);
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        ctx->stream_pool.push_back(t->stream);
+        --ctx->active;
+    }
     (void)hipEventDestroy(t->done);
     delete t;
     return e == hipSuccess ? VKFX_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int vkfx_context_cache_stats(vkfx_context* ctx, uint64_t* transient_buffers, uint64_t* pooled_streams,
+                             uint64_t* in_flight) {
+    if (!ctx) return fail(VKFX_ERR_INVALID_ARGUMENT, "null context");
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (transient_buffers) *transient_buffers = ctx->dev_pool.size() + ctx->host_pool.size();
+    if (pooled_streams) *pooled_streams = ctx->stream_pool.size();
+    if (in_flight) *in_flight = (uint64_t)ctx->active;
+    return VKFX_OK;
+}
+
+int vkfx_context_clear_caches(vkfx_context* ctx) {
+    if (!ctx) return fail(VKFX_ERR_INVALID_ARGUMENT, "null context");
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (ctx->active)
+        return fail(VKFX_ERR_NATIVE_RUNTIME, "cannot clear HIP runtime caches while " + std::to_string(ctx->active) +
+                                                 " submission(s) are in flight");
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->aux);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    for (PoolBuf& b : ctx->dev_pool) {
+        if (b.ready) (void)hipEventDestroy(b.ready);
+        e = hipFree(b.p);
+        if (e != hipSuccess) return hip_fail(e, "hipFree");
+    }
+    ctx->dev_pool.clear();
+    for (PoolBuf& b : ctx->host_pool) {
+        if (b.ready) (void)hipEventDestroy(b.ready);
+        e = hipHostFree(b.p);
+        if (e != hipSuccess) return hip_fail(e, "hipHostFree");
+    }
+    ctx->host_pool.clear();
+    for (hipStream_t s : ctx->stream_pool) {
+        (void)hipStreamSynchronize(s);
+        (void)hipStreamDestroy(s);
+    }
+    ctx->stream_pool.clear();
+    return VKFX_OK;
 }
 
 int vkfx_execute_chain(vkfx_plan* const* plans, uint32_t count, const void* d_in, void* d_out, void* stream) {

@@ -192,6 +192,8 @@ def lib(path: Optional[str] = None):
         L.vkfx_ticket_ready.argtypes = [vp, ctypes.POINTER(i32)]
         L.vkfx_ticket_wait.argtypes = [vp, vp, u64]
         L.vkfx_ticket_destroy.argtypes = [vp]
+        L.vkfx_context_cache_stats.argtypes = [vp, ctypes.POINTER(u64), ctypes.POINTER(u64), ctypes.POINTER(u64)]
+        L.vkfx_context_clear_caches.argtypes = [vp]
         L.vkfx_execute_chain.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, vp, vp]
         L.vkfx_execute_chain_host.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, u64, vp, u64]
         _libs[path] = L
@@ -678,9 +680,11 @@ class TransformTicket:
         return ir.unpack_output(ir.from_storage(self._out, self._complex_out))
 
     def close(self):
-        if self.handle:
+        # a ticket outliving its context was already synchronised by the
+        # context's teardown; vkfx_ticket_destroy needs a live context
+        if self.handle and self.plan.ctx.handle:
             self._L.vkfx_ticket_destroy(self.handle)
-            self.handle = ctypes.c_void_p()
+        self.handle = ctypes.c_void_p()
 
     def __del__(self):
         try:
@@ -827,6 +831,27 @@ class HipExecutionContext:
 
     def synchronize(self):
         _check(self._L.vkfx_context_synchronize(self.handle), self._L)
+
+    def _cache_stats(self):
+        b, s, a = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        _check(self._L.vkfx_context_cache_stats(self.handle, ctypes.byref(b), ctypes.byref(s), ctypes.byref(a)),
+               self._L)
+        return int(b.value), int(s.value), int(a.value)
+
+    def cached_transient_buffer_count(self) -> int:
+        """hip/runtime.rs:1828-1833: pooled device and pinned buffers."""
+        return self._cache_stats()[0]
+
+    def pooled_stream_count(self) -> int:
+        """hip/runtime.rs:1835-1840."""
+        return self._cache_stats()[1]
+
+    def in_flight_submission_count(self) -> int:
+        return self._cache_stats()[2]
+
+    def clear_runtime_caches(self):
+        """hip/runtime.rs:2275-2330: fails while tickets are in flight."""
+        _check(self._L.vkfx_context_clear_caches(self.handle), self._L)
 
     def close(self):
         for p in list(self._live_plans):
