@@ -94,6 +94,16 @@ typedef struct {
     char arch[64];
 } vkfx_device_profile;
 
+/* PlannerTuning (src/config.rs:367-380): Rader ranges and the recursive-Rader
+ * opt-in. */
+typedef struct {
+    uint64_t min_rader_direct_prime;
+    uint64_t max_rader_direct_prime; /* exclusive */
+    uint64_t min_rader_fft_prime;
+    uint64_t max_rader_fft_prime; /* exclusive */
+    int32_t allow_recursive_fft_rader;
+} vkfx_planner_tuning;
+
 /* Plan descriptor: the part of `TransformIr` (src/application.rs:48-167) the
  * kernels need, plus the planner's per-axis decision so the library executes
  * exactly what vkfft-rs planned (src/planner.rs:168-241). With
@@ -150,6 +160,10 @@ typedef struct {
     /* FftConfig::omit_dimension (config.rs:651, 844-853, 1053-1067): bit i set
      * leaves axis i untransformed (rank > 1; never the real axis of R2C/C2R). */
     uint32_t omit_dimension;
+    /* FftConfig::with_tuning (config.rs:820-824): with custom_tuning = 0 the
+     * library planner uses the AMD device tuning (PlannerTuning::for_device). */
+    int32_t custom_tuning;
+    vkfx_planner_tuning tuning;
 } vkfx_plan_desc;
 
 /* ---------------------------------------------------------------- context */
@@ -272,6 +286,12 @@ const char *vkfx_version(void);
 int vkfx_planner_axis(uint64_t len, uint64_t batch, int32_t precision, int32_t axis_is_strided,
                       int32_t allow_recursive_rader, uint64_t shared_memory_bytes,
                       int32_t *algorithm, uint64_t *convolution_len);
+
+/* vkfx_planner_axis with an explicit PlannerTuning (NULL: the AMD device
+ * tuning), as plan_c2c_axis_algorithm_for_device with FftConfig::with_tuning. */
+int vkfx_planner_axis_tuned(uint64_t len, uint64_t batch, int32_t precision, int32_t axis_is_strided,
+                            const vkfx_planner_tuning *tuning, uint64_t shared_memory_bytes, int32_t *algorithm,
+                            uint64_t *convolution_len);
 
 /* upstream_bluestein_auto_padding for HIP/AMD (src/scheduler.rs:225-373). */
 int vkfx_planner_bluestein_padding(uint64_t len, uint64_t batch, int32_t precision,

@@ -105,3 +105,23 @@ def test_mixed_precision_host_storage_conversion():
                                 vk.Direction.Forward)
     assert ir64.complex_dtype == np.complex64 and ir64.storage_scalar_dtype == np.float32
     assert ir64.to_storage(x) is x
+
+
+def test_tuned_planner_and_kernel_preparation_rules():
+    """PlannerTuning moves a Rader prime to Bluestein above max_rader_fft_prime
+    (config.rs:367-420); kernelConvolution is a forward-only preparation of
+    coordinate_features * batch systems with the pinned ownerships
+    (config.rs:806-818, 1101-1136)."""
+    assert vk.planner_axis(1009)[0] == vk.AlgorithmKind.Rader
+    assert vk.planner_axis(1009, tuning=vk.PlannerTuning(max_rader_fft_prime=1000))[0] == vk.AlgorithmKind.Bluestein
+    assert vk.planner_axis(4099, tuning=vk.PlannerTuning().with_recursive_fft_rader())[0] == vk.AlgorithmKind.Rader
+    ir = vk.TransformIr.build(vk.FftConfig.new([64]).with_batch_count(3).with_coordinate_features(2)
+                              .with_kernel_convolution(True), vk.Direction.Forward)
+    assert ir.input_count() == ir.output_count() == 64 * 6 and ir.desc().batch == 6
+def test_kernel_preparation_rejections():
+    with pytest.raises(vk.VkFftError):
+        vk.TransformIr.build(vk.FftConfig.new([64]).with_kernel_convolution(True), vk.Direction.Inverse)
+    with pytest.raises(vk.VkFftError):
+        vk.TransformIr.build(vk.FftConfig.new([64, 32]).with_kernel_convolution(True), vk.Direction.Forward)  # 2-D C2C
+    with pytest.raises(vk.VkFftError):
+        vk.TransformIr.build(vk.FftConfig.new([64]).with_kernel_convolution(True).with_convolution(True), vk.Direction.Forward)

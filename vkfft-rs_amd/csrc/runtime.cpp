@@ -468,10 +468,21 @@ bool four_step_split(size_t M, int prec, size_t lds_max, size_t* n1, size_t* n2)
     return true;
 }
 
+PlannerTuning tuning_from(const vkfx_planner_tuning& t) {
+    PlannerTuning p;
+    p.min_rader_direct_prime = (size_t)t.min_rader_direct_prime;
+    p.max_rader_direct_prime = (size_t)t.max_rader_direct_prime;
+    p.min_rader_fft_prime = (size_t)t.min_rader_fft_prime;
+    p.max_rader_fft_prime = (size_t)t.max_rader_fft_prime;
+    p.allow_recursive_fft_rader = t.allow_recursive_fft_rader != 0;
+    return p;
+}
+
 struct Ctx {
     vkfx_plan* p;
     int prec;
     size_t lds_max;
+    PlannerTuning tuning;  // the plan's planner tuning (device default or FftConfig::with_tuning)
     size_t lds_budget = 80 * 1024;
     std::ostringstream js;
     bool first_pass = true;
@@ -1039,7 +1050,7 @@ int plan_real_full_complex(Ctx& c, size_t n, size_t batch, bool r2c, bool normal
     vkfx_plan* p = c.p;
     const size_t h = n / 2 + 1;
     const bool f64 = c.prec == 1;
-    AxisDecision ad = plan_c2c_axis(n, batch, f64, false, tuning_for_amd(f64), planner_device(c.p->ctx->profile.shared_memory_bytes));
+    AxisDecision ad = plan_c2c_axis(n, batch, f64, false, c.tuning, planner_device(c.p->ctx->profile.shared_memory_bytes));
     p->full_bytes = batch * n * csize(c.prec);
     p->serial = true;
     c.js << "\"real\":{\"len\":" << n << ",\"algorithm\":\"full_complex\",\"c2c\":\""
@@ -1288,7 +1299,7 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize, 
     a.s *= scale;
     const size_t L = (size_t)a.L;
     const bool f64 = c.prec == 1;
-    AxisDecision ad = plan_c2c_axis(L, batch, f64, false, tuning_for_amd(f64),
+    AxisDecision ad = plan_c2c_axis(L, batch, f64, false, c.tuning,
                                     planner_device(p->ctx->profile.shared_memory_bytes));
     p->full_bytes = std::max(p->full_bytes, batch * L * csize(c.prec));
     p->serial = true;
@@ -1666,6 +1677,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     }
     PlannerDevice pdev = planner_device(ctx->profile.shared_memory_bytes);
     PlannerTuning tuning = tuning_for_amd(f64);
+    if (d.custom_tuning) tuning = tuning_from(d.tuning);
     try {
         if (d.use_library_planner) {
             for (uint32_t i = 0; i < d.rank; ++i) {
@@ -1685,7 +1697,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     auto* p = new vkfx_plan();
     p->ctx = ctx;
     p->desc = d;
-    Ctx c{p, f64 ? 1 : 0, lds_max_for(ctx)};
+    Ctx c{p, f64 ? 1 : 0, lds_max_for(ctx), tuning};
     if (const char* e = getenv("VKFX_LDS_BUDGET_KB")) c.lds_budget = (size_t)atoll(e) << 10;
 
     const size_t cs = csize(c.prec), rs = rsize(c.prec);
@@ -2176,6 +2188,24 @@ int vkfx_planner_axis(uint64_t len, uint64_t batch, int32_t precision, int32_t a
         const bool f64 = precision == VKFX_F64 || precision == VKFX_F64_COMPUTE_F32_STORAGE;
         AxisDecision d = plan_c2c_axis(len, batch ? batch : 1, f64, axis_is_strided != 0,
                                        tuning_for_amd(f64, allow_recursive_rader != 0),
+                                       planner_device(shared_memory_bytes));
+        *algorithm = (int32_t)d.algorithm;
+        *convolution_len = d.convolution_len;
+    } catch (const std::exception& ex) {
+        return fail(VKFX_ERR_INVALID_ARGUMENT, ex.what());
+    }
+    return VKFX_OK;
+}
+
+int vkfx_planner_axis_tuned(uint64_t len, uint64_t batch, int32_t precision, int32_t axis_is_strided,
+                            const vkfx_planner_tuning* tuning, uint64_t shared_memory_bytes, int32_t* algorithm,
+                            uint64_t* convolution_len) {
+    if (!algorithm || !convolution_len) return fail(VKFX_ERR_INVALID_ARGUMENT, "null output");
+    if (len == 0) return fail(VKFX_ERR_INVALID_ARGUMENT, "ZeroLength");
+    try {
+        const bool f64 = precision == VKFX_F64 || precision == VKFX_F64_COMPUTE_F32_STORAGE;
+        const PlannerTuning t = tuning ? tuning_from(*tuning) : tuning_for_amd(f64);
+        AxisDecision d = plan_c2c_axis(len, batch ? batch : 1, f64, axis_is_strided != 0, t,
                                        planner_device(shared_memory_bytes));
         *algorithm = (int32_t)d.algorithm;
         *convolution_len = d.convolution_len;

@@ -115,6 +115,16 @@ class AlgorithmKind(enum.IntEnum):
     Bluestein = 2
 
 
+class _PlannerTuning(ctypes.Structure):
+    _fields_ = [
+        ("min_rader_direct_prime", ctypes.c_uint64),
+        ("max_rader_direct_prime", ctypes.c_uint64),
+        ("min_rader_fft_prime", ctypes.c_uint64),
+        ("max_rader_fft_prime", ctypes.c_uint64),
+        ("allow_recursive_fft_rader", ctypes.c_int32),
+    ]
+
+
 class _PlanDesc(ctypes.Structure):
     _fields_ = [
         ("rank", ctypes.c_uint32),
@@ -146,6 +156,8 @@ class _PlanDesc(ctypes.Structure):
         ("kernel_spectrum", ctypes.c_void_p),
         ("kernel_spectrum_bytes", ctypes.c_uint64),
         ("omit_dimension", ctypes.c_uint32),
+        ("custom_tuning", ctypes.c_int32),
+        ("tuning", _PlannerTuning),
     ]
 
 
@@ -185,6 +197,8 @@ def lib(path: Optional[str] = None):
         L.vkfx_execute.argtypes = [vp, vp, vp, vp, vp]
         L.vkfx_execute_host.argtypes = [vp, vp, u64, vp, u64]
         L.vkfx_planner_axis.argtypes = [u64, u64, i32, i32, i32, u64, ctypes.POINTER(i32), ctypes.POINTER(u64)]
+        L.vkfx_planner_axis_tuned.argtypes = [u64, u64, i32, i32, ctypes.POINTER(_PlannerTuning), u64,
+                                              ctypes.POINTER(i32), ctypes.POINTER(u64)]
         L.vkfx_planner_bluestein_padding.argtypes = [u64, u64, i32, u64, ctypes.POINTER(u64)]
         L.vkfx_planner_next_smooth.argtypes = [u64]
         L.vkfx_planner_next_smooth.restype = u64
@@ -214,12 +228,43 @@ def header_symbols() -> List[str]:
 
 # ------------------------------------------------------------------ planner
 
+@dataclass
+class PlannerTuning:
+    """PlannerTuning (src/config.rs:367-420): Rader ranges (max bounds exclusive)
+    and the recursive-Rader opt-in."""
+    min_rader_direct_prime: int = 17
+    max_rader_direct_prime: int = 89
+    min_rader_fft_prime: int = 17
+    max_rader_fft_prime: int = 16_384
+    allow_recursive_fft_rader: bool = False
+
+    @staticmethod
+    def portable() -> "PlannerTuning":
+        return PlannerTuning()
+
+    def with_recursive_fft_rader(self, enabled: bool = True) -> "PlannerTuning":
+        self.allow_recursive_fft_rader = bool(enabled)
+        return self
+
+    def _c(self) -> _PlannerTuning:
+        return _PlannerTuning(self.min_rader_direct_prime, self.max_rader_direct_prime, self.min_rader_fft_prime,
+                              self.max_rader_fft_prime, int(self.allow_recursive_fft_rader))
+
+
 def planner_axis(length: int, batch: int = 1, precision: Precision = Precision.F32, strided: bool = False,
-                 recursive_rader: bool = False, shared_memory_bytes: int = 160 * 1024):
-    """plan_c2c_axis_algorithm_for_device on the HIP/AMD profile (planner.rs:349-440)."""
+                 recursive_rader: bool = False, shared_memory_bytes: int = 160 * 1024,
+                 tuning: Optional[PlannerTuning] = None):
+    """plan_c2c_axis_algorithm_for_device on the HIP/AMD profile (planner.rs:349-440),
+    with the device tuning or an explicit PlannerTuning."""
     alg, m = ctypes.c_int32(), ctypes.c_uint64()
-    _check(lib().vkfx_planner_axis(length, batch, int(precision), int(strided), int(recursive_rader),
-                                   shared_memory_bytes, ctypes.byref(alg), ctypes.byref(m)))
+    if tuning is None:
+        _check(lib().vkfx_planner_axis(length, batch, int(precision), int(strided), int(recursive_rader),
+                                       shared_memory_bytes, ctypes.byref(alg), ctypes.byref(m)))
+    else:
+        t = tuning._c()
+        t.allow_recursive_fft_rader = int(tuning.allow_recursive_fft_rader or recursive_rader)
+        _check(lib().vkfx_planner_axis_tuned(length, batch, int(precision), int(strided), ctypes.byref(t),
+                                             shared_memory_bytes, ctypes.byref(alg), ctypes.byref(m)))
     return AlgorithmKind(alg.value), int(m.value)
 
 
@@ -262,6 +307,8 @@ class FftConfig:
     symmetric_convolution_kernel: bool = False
     convolution_kernel_count: int = 1
     omit_dimension: List[bool] = field(default_factory=lambda: [False] * MAX_RANK)
+    kernel_convolution: bool = False
+    tuning: Optional["PlannerTuning"] = None  # None: the device tuning
 
     @staticmethod
     def new(dimensions: Sequence[int]) -> "FftConfig":
@@ -319,6 +366,22 @@ class FftConfig:
         self.zero_padding_domain = ZeroPaddingDomain(domain)
         return self
 
+    def with_tuning(self, tuning: "PlannerTuning") -> "FftConfig":
+        """config.rs:820-824: explicit planner tuning."""
+        self.tuning = tuning
+        return self
+
+    def with_device_tuning(self) -> "FftConfig":
+        """config.rs:828-832: back to the device/precision defaults."""
+        self.tuning = None
+        return self
+
+    def with_kernel_convolution(self, enabled: bool = True) -> "FftConfig":
+        """config.rs:746-749: a forward transform that prepares a convolution
+        kernel spectrum over coordinate_features * batch_count systems."""
+        self.kernel_convolution = bool(enabled)
+        return self
+
     def with_omit_dimension(self, axis: int, omit: bool = True) -> "FftConfig":
         """config.rs:844-853: leave `axis` untransformed."""
         if not 0 <= axis < len(self.dimensions):
@@ -371,6 +434,36 @@ class FftConfig:
                 raise VkFftError(-7, f"ZeroLength {{ axis: {axis} }}")
         if self.batch_count <= 0:
             raise VkFftError(-7, "batch_count must be >= 1")
+        if self.coordinate_features <= 0:
+            raise VkFftError(-7, "ValueOutOfRange { field: coordinateFeatures }")
+        if self.kernel_convolution:
+            # config.rs:1101-1136: the pinned kernel-preparation ownerships
+            rank = len(self.dimensions)
+            padded = [z is not None for z in self.zero_padding[:rank]]
+            real = self.transform == TransformKind.RealToComplex
+            dense_1d = rank == 1 and not any(padded)
+            s52 = real and rank == 2 and self.batch_count == 2 and self.coordinate_features == 2 and not any(padded)
+            s51 = real and rank == 3 and self.batch_count == 1 and self.coordinate_features == 9 and all(padded) \
+                and self.zero_padding_domain == ZeroPaddingDomain.Spatial
+            formatted = any(self.input_buffer_axis_strides[:rank]) or any(self.output_buffer_axis_strides[:rank]) \
+                or bool(self.input_buffer_batch_stride) or bool(self.output_buffer_batch_stride)
+            if self.perform_convolution:
+                raise VkFftError(-3, "kernelConvolution prepares a kernel spectrum and must not be combined with "
+                                     "performConvolution")
+            if self.transform not in (TransformKind.ComplexToComplex, TransformKind.RealToComplex) \
+                    or not (dense_1d or s52 or s51) or self.matrix_convolution != 1 \
+                    or self.symmetric_convolution_kernel or self.convolution_kernel_count != 1 \
+                    or self.precision not in (Precision.F32, Precision.F64) or formatted \
+                    or self.convolution_conjugation != ConvolutionConjugation.Off \
+                    or self.cross_power_spectrum_normalization:
+                raise VkFftError(-3, "kernelConvolution currently requires dense 1D C2C/R2C independent "
+                                     "batch/coordinate K1 preparation, sample_52-style 2D R2C B2/C2 preparation, "
+                                     "or sample_51-style batch1 3D R2C C9 Spatial-padding preparation in F32/F64")
+
+    def system_count(self) -> int:
+        """Independent transforms of a plan: coordinate_features * batch_count
+        for kernel preparation (config.rs:806-818), else batch_count."""
+        return self.batch_count * (self.coordinate_features if self.kernel_convolution else 1)
 
 
 @dataclass
@@ -389,12 +482,14 @@ class TransformIr:
             raise VkFftError(-7, "RealToComplex requires Direction::Forward")
         if config.transform == TransformKind.ComplexToReal and direction != Direction.Inverse:
             raise VkFftError(-7, "ComplexToReal requires Direction::Inverse")
+        if config.kernel_convolution and direction != Direction.Forward:
+            raise VkFftError(-3, "kernelConvolution prepares a kernel spectrum with a forward transform")
         ir = TransformIr(config, direction)
         rank = len(config.dimensions)
         for axis, n in enumerate(config.dimensions):
             if config.transform == TransformKind.ComplexToComplex:
-                alg, m = planner_axis(n, config.batch_count, config.precision, strided=axis + 1 != rank,
-                                      recursive_rader=config.allow_recursive_fft_rader)
+                alg, m = planner_axis(n, config.system_count(), config.precision, strided=axis + 1 != rank,
+                                      recursive_rader=config.allow_recursive_fft_rader, tuning=config.tuning)
             else:
                 alg, m = AlgorithmKind.Stockham, 0
             ir.axis_algorithms.append(alg)
@@ -428,6 +523,12 @@ class TransformIr:
         # a convolution config without its kernel spectrum fails at plan time
         d.perform_convolution = int(c.perform_convolution)
         d.omit_dimension = sum(1 << i for i in range(len(c.dimensions)) if c.omit_dimension[i])
+        if c.tuning is not None:
+            d.custom_tuning = 1
+            d.tuning = c.tuning._c()
+            d.tuning.allow_recursive_fft_rader = int(c.tuning.allow_recursive_fft_rader or c.allow_recursive_fft_rader)
+        if c.kernel_convolution:
+            d.batch = c.system_count()
         return d
 
     # ---- formatted layouts (the host-side pack/unpack of the reference's
@@ -524,11 +625,11 @@ class TransformIr:
 
     def input_count(self) -> int:
         """Logical input elements: the compact [.., N/2+1] spectrum for C2R."""
-        return int(np.prod(self._side_dims(False))) * self.config.batch_count
+        return int(np.prod(self._side_dims(False))) * self.config.system_count()
 
     def output_count(self) -> int:
         """Logical output elements: the compact [.., N/2+1] spectrum for R2C."""
-        return int(np.prod(self._side_dims(True))) * self.config.batch_count
+        return int(np.prod(self._side_dims(True))) * self.config.system_count()
 
 
 class Plan:
