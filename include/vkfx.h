@@ -187,6 +187,26 @@ int vkfx_plan_create(vkfx_context *ctx, const vkfx_plan_desc *desc, vkfx_plan **
 /* Destroy every plan before the context it was created on. */
 int vkfx_plan_destroy(vkfx_plan *plan);
 
+/* Resources of one distinct pass of a plan (NativeRuntime::
+ * compiled_pass_resource_reports / theoretical_occupancy_reports,
+ * src/backend/native_runtime.rs:96-131, 166-183; HIP metrics of
+ * hip/runtime.rs:1849-1870): the attributes of the compiled kernel and the
+ * blocks of this launch that fit on one CU. */
+typedef struct {
+    char pass[48];                   /* launch label (as in vkfx_plan_describe) */
+    uint32_t registers_per_thread;   /* hipFuncAttributes::numRegs */
+    uint32_t static_shared_bytes;    /* hipFuncAttributes::sharedSizeBytes */
+    uint32_t dynamic_shared_bytes;   /* LDS the launch requests */
+    uint32_t local_bytes_per_thread; /* hipFuncAttributes::localSizeBytes (scratch) */
+    uint32_t max_threads_per_block;  /* hipFuncAttributes::maxThreadsPerBlock */
+    uint32_t block_threads;
+    uint32_t resident_blocks_per_cu; /* hipOccupancyMaxActiveBlocksPerMultiprocessor */
+    uint32_t waves_per_cu;           /* resident_blocks_per_cu * ceil(block_threads / 64) */
+} vkfx_pass_resources;
+/* Writes up to `capacity` reports (distinct passes in launch order) and the
+ * total count into *count. */
+int vkfx_plan_resources(const vkfx_plan *plan, vkfx_pass_resources *out, uint32_t capacity, uint32_t *count);
+
 /* Byte sizes of one execute's input and output buffers, and of the scratch
  * a caller may pass to vkfx_execute (0 when the plan needs none). */
 int vkfx_plan_io_bytes(const vkfx_plan *plan, uint64_t *in_bytes, uint64_t *out_bytes);

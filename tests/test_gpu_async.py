@@ -163,3 +163,22 @@ def test_runtime_caches_and_clear(hip_ctx):
     t = hip_ctx.submit_transform_async(*a)
     assert np.array_equal(t.wait(), ya)
     t.close()
+
+
+def test_pass_resource_reports(hip_ctx):
+    """compiled_pass_resource_reports / theoretical_occupancy_reports
+    (native_runtime.rs:96-131): one report per distinct pass, with the
+    compiled kernel's registers and the blocks of the launch that fit a CU."""
+    c1 = hip_ctx.plan(c2c_ir([1024], 8192)).resources()
+    assert len(c1) == 1 and c1[0]["pass"] == "stockham"
+    r = c1[0]
+    assert 0 < r["registers_per_thread"] <= 512 and r["local_bytes_per_thread"] == 0
+    assert r["block_threads"] == 128 and r["dynamic_shared_bytes"] >= 1024 * 8
+    assert 1 <= r["resident_blocks_per_cu"] and r["waves_per_cu"] <= 64
+    real = hip_ctx.plan(real_irs(1 << 20, 4)[0]).resources()
+    assert [p["pass"] for p in real] == ["r2c_four_step_columns", "r2c_four_step_rows"] or len(real) == 2
+    assert all(p["resident_blocks_per_cu"] >= 1 for p in real)
+    mixed = vk.TransformIr.build(vk.FftConfig.new([1024]).with_batch_count(4)
+                                 .with_precision(vk.Precision.F64ComputeF32Storage), FWD)
+    names = [p["pass"] for p in hip_ctx.plan(mixed).resources()]
+    assert names[0] == "boundary_in" and names[-1] == "boundary_out"

@@ -54,6 +54,8 @@ __global__ __launch_bounds__(256) void k_conv(const T* __restrict__ X, const T* 
     }
 }
 
+const void* conv_kernel_fn(int prec) { return prec ? (const void*)k_conv<double> : (const void*)k_conv<float>; }
+
 int launch_conv(int prec, const ConvArgs& a, const void* x, const void* k, void* y, hipStream_t s) {
     const long long total = a.T * a.coords * a.systems_out;
     if (total <= 0 || a.coords < 1 || a.planes < 1) return (int)hipErrorInvalidValue;

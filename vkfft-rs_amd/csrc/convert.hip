@@ -54,6 +54,18 @@ static int go(const void* in, void* out, const BoundaryArgs& a, hipStream_t s) {
     return (int)hipGetLastError();
 }
 
+const void* boundary_kernel_fn(int src_type, int dst_type) {
+    switch (src_type * 3 + dst_type) {
+        case 0 * 3 + 1: return (const void*)k_boundary<_Float16, float>;
+        case 1 * 3 + 0: return (const void*)k_boundary<float, _Float16>;
+        case 1 * 3 + 1: return (const void*)k_boundary<float, float>;
+        case 1 * 3 + 2: return (const void*)k_boundary<float, double>;
+        case 2 * 3 + 1: return (const void*)k_boundary<double, float>;
+        case 2 * 3 + 2: return (const void*)k_boundary<double, double>;
+        default: return nullptr;
+    }
+}
+
 int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_t s) {
     if (a.tensor_len <= 0 || a.batch <= 0) return (int)hipSuccess;
     if (a.rank < 1 || a.rank > kMaxBoundaryRank || a.src_scalars < 1 || a.src_scalars > 2 || a.dst_scalars < 1 ||

@@ -159,4 +159,11 @@ struct ConvArgs {
 };
 int launch_conv(int prec, const ConvArgs& a, const void* x, const void* k, void* y, hipStream_t s);
 
+// Device functions a launch runs, for resource queries (hipFuncGetAttributes,
+// occupancy): the same selection as the launch functions make.
+const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed);
+const void* boundary_kernel_fn(int src_type, int dst_type);
+const void* r2r_kernel_fn(bool pre, int prec);
+const void* conv_kernel_fn(int prec);
+
 }  // namespace vkfx

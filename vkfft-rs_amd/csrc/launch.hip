@@ -134,6 +134,14 @@ static bool xcd_groups(KernelKind kind) {
            kind == KK_FS_C_BLUE;
 }
 
+const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed) {
+    if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1)) return nullptr;
+    if (fixed) return (const void*)fixed->fn;
+    KernelFn fn = prec == 0 ? (dir < 0 ? pick_f32_fwd(kind) : pick_f32_inv(kind))
+                            : (dir < 0 ? pick_f64_fwd(kind) : pick_f64_inv(kind));
+    return (const void*)fn;
+}
+
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block, size_t lds_bytes,
            hipStream_t stream, const FixedKernel* fixed) {
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1))

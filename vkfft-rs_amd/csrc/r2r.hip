@@ -83,6 +83,11 @@ static int go(bool pre, const R2rArgs& p, const void* in, void* out, hipStream_t
     return (int)hipGetLastError();
 }
 
+const void* r2r_kernel_fn(bool pre, int prec) {
+    if (prec) return pre ? (const void*)k_r2r_pre<double> : (const void*)k_r2r_post<double>;
+    return pre ? (const void*)k_r2r_pre<float> : (const void*)k_r2r_post<float>;
+}
+
 int launch_r2r(bool pre, int prec, const R2rArgs& p, const void* in, void* out, hipStream_t s) {
     if (p.n <= 0 || p.L <= 0 || p.batch <= 0 || p.inner <= 0 || p.batch % p.inner) return (int)hipErrorInvalidValue;
     return prec ? go<double>(pre, p, in, out, s) : go<float>(pre, p, in, out, s);

@@ -2061,6 +2061,62 @@ int vkfx_plan_destroy(vkfx_plan* plan) {
     return VKFX_OK;
 }
 
+int vkfx_plan_resources(const vkfx_plan* plan, vkfx_pass_resources* out, uint32_t capacity, uint32_t* count) {
+    if (!plan || !count || (capacity && !out)) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    (void)hipSetDevice(plan->ctx->device);
+    const int prec =
+        (plan->desc.precision == VKFX_F64 || plan->desc.precision == VKFX_F64_COMPUTE_F32_STORAGE) ? 1 : 0;
+    std::vector<std::pair<std::string, const void*>> seen;
+    uint32_t n = 0;
+    for (const Launch& L : plan->launches) {
+        const void* fn = nullptr;
+        unsigned block = 256;
+        size_t lds = 0;
+        if (L.boundary) {
+            fn = boundary_kernel_fn(L.ba.src_type, L.ba.dst_type);
+        } else if (L.r2r) {
+            fn = r2r_kernel_fn(L.r2r == 1, prec);
+        } else if (L.conv) {
+            fn = conv_kernel_fn(prec);
+        } else {
+            fn = fft_kernel_fn(L.kind, prec, L.dir, L.fixed);
+            block = L.block;
+            lds = L.lds;
+        }
+        if (!fn) return fail(VKFX_ERR_NATIVE_RUNTIME, "no device function for pass " + L.label);
+        bool dup = false;
+        for (const auto& s : seen) dup = dup || (s.first == L.label && s.second == fn);
+        if (dup) continue;
+        seen.emplace_back(L.label, fn);
+        if (n < capacity) {
+            hipFuncAttributes attr{};
+            hipError_t e = hipFuncGetAttributes(&attr, fn);
+            if (e != hipSuccess) return hip_fail(e, "hipFuncGetAttributes");
+            if (lds > 65536) {
+                e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute");
+            }
+            int blocks = 0;
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, (int)block, lds);
+            if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+            vkfx_pass_resources& r = out[n];
+            std::memset(&r, 0, sizeof r);
+            std::snprintf(r.pass, sizeof r.pass, "%s", L.label.c_str());
+            r.registers_per_thread = (uint32_t)attr.numRegs;
+            r.static_shared_bytes = (uint32_t)attr.sharedSizeBytes;
+            r.dynamic_shared_bytes = (uint32_t)lds;
+            r.local_bytes_per_thread = (uint32_t)attr.localSizeBytes;
+            r.max_threads_per_block = (uint32_t)attr.maxThreadsPerBlock;
+            r.block_threads = block;
+            r.resident_blocks_per_cu = (uint32_t)blocks;
+            r.waves_per_cu = (uint32_t)blocks * ((block + 63) / 64);
+        }
+        ++n;
+    }
+    *count = n;
+    return VKFX_OK;
+}
+
 int vkfx_plan_io_bytes(const vkfx_plan* plan, uint64_t* in_bytes, uint64_t* out_bytes) {
     if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
     if (in_bytes) *in_bytes = plan->in_bytes;

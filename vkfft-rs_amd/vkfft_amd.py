@@ -115,6 +115,20 @@ class AlgorithmKind(enum.IntEnum):
     Bluestein = 2
 
 
+class _PassResources(ctypes.Structure):
+    _fields_ = [
+        ("pass_", ctypes.c_char * 48),
+        ("registers_per_thread", ctypes.c_uint32),
+        ("static_shared_bytes", ctypes.c_uint32),
+        ("dynamic_shared_bytes", ctypes.c_uint32),
+        ("local_bytes_per_thread", ctypes.c_uint32),
+        ("max_threads_per_block", ctypes.c_uint32),
+        ("block_threads", ctypes.c_uint32),
+        ("resident_blocks_per_cu", ctypes.c_uint32),
+        ("waves_per_cu", ctypes.c_uint32),
+    ]
+
+
 class _PlannerTuning(ctypes.Structure):
     _fields_ = [
         ("min_rader_direct_prime", ctypes.c_uint64),
@@ -208,6 +222,8 @@ def lib(path: Optional[str] = None):
         L.vkfx_ticket_destroy.argtypes = [vp]
         L.vkfx_context_cache_stats.argtypes = [vp, ctypes.POINTER(u64), ctypes.POINTER(u64), ctypes.POINTER(u64)]
         L.vkfx_context_clear_caches.argtypes = [vp]
+        L.vkfx_plan_resources.argtypes = [vp, ctypes.POINTER(_PassResources), ctypes.c_uint32,
+                                          ctypes.POINTER(ctypes.c_uint32)]
         L.vkfx_execute_chain.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, vp, vp]
         L.vkfx_execute_chain_host.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, u64, vp, u64]
         _libs[path] = L
@@ -647,6 +663,20 @@ class Plan:
         _check(self._L.vkfx_plan_io_bytes(self.handle, ctypes.byref(i), ctypes.byref(o)), self._L)
         _check(self._L.vkfx_plan_workspace_bytes(self.handle, ctypes.byref(w)), self._L)
         self.in_bytes, self.out_bytes, self.workspace_bytes = int(i.value), int(o.value), int(w.value)
+
+    def resources(self) -> List[dict]:
+        """compiled_pass_resource_reports + theoretical_occupancy_reports
+        (native_runtime.rs:96-131): one entry per distinct pass."""
+        count = ctypes.c_uint32()
+        _check(self._L.vkfx_plan_resources(self.handle, None, 0, ctypes.byref(count)), self._L)
+        arr = (_PassResources * max(1, count.value))()
+        _check(self._L.vkfx_plan_resources(self.handle, arr, count.value, ctypes.byref(count)), self._L)
+        out = []
+        for r in arr[:count.value]:
+            d = {name: getattr(r, name) for name, _ in _PassResources._fields_ if name != "pass_"}
+            d["pass"] = r.pass_.decode()
+            out.append(d)
+        return out
 
     def describe(self) -> dict:
         n = self._L.vkfx_plan_describe(self.handle, None, 0)
