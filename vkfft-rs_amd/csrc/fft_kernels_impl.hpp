@@ -484,6 +484,15 @@ struct IoFsAC2R : IoFsA {
     }
 };
 
+// C2R column pass with direct loads: with KF_MIRROR_PAIRS the block owns
+// columns and their mirrors, and every element reads its own X[k] and its
+// partner X[M-k] (load_elem): the partner's second read is served by the
+// L1/L2 of the same CU, and the staged prologue with its LDS pair pass and
+// barrier goes away.
+struct IoFsAC2RDirect : IoFsAC2R {
+    static constexpr int kLoad = LAY_COL;
+};
+
 // Four-step row pass. Line = row k1 (C = N1), contiguous in the scratch;
 // FFT over n2 (length N2); store X[k1 + N1*k2] (column-coalesced).
 struct IoFsB : IoPlain {

@@ -13,6 +13,7 @@ static const FixedKernel kTable[] = {
     VKFX_FIXED_NT(KK_FS_B_R2C, IoFsBR2C, float, 0, -1, 512, 32, 32, 4, 543, false, false, false, 8, 8, 8),
     // C2R, M = 512 x 1024: 16 columns of 512 beside their 16 mirror columns
     // (preprocess fused), then 16 rows of 1024
+    VKFX_FIXED_NT(KK_FS_A_C2R, IoFsAC2RDirect, float, 0, 1, 512, 32, 32, 3, 577, true, false, false, 8, 8, 8),
     VKFX_FIXED_NT(KK_FS_A_C2R, IoFsAC2R, float, 0, 1, 512, 32, 32, 3, 577, true, false, false, 8, 8, 8),
     VKFX_FIXED_NT(KK_FS_B, IoFsB, float, 0, 1, 1024, 64, 16, 4, 1089, false, false, false, 16, 16, 4),
     // row pass of the C2C four-step of 2^20 = 1024 x 1024 (its column pass is the first entry)
