@@ -8,9 +8,9 @@ namespace vkfx {
 static const FixedKernel kTable[] = {
     VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
     VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 448, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
-    VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 406, true, true, false, 9, 9, 5),
+    VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, false, false, 4, 9, 9),
-    VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 406, true, false, true, 9, 9, 5),
+    VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 407, true, false, true, 9, 9, 5),
 };
 
 const FixedKernel* fixed_table_blue(int* count) {

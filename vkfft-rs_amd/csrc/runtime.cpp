@@ -2145,6 +2145,8 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
     if (!d_in || !d_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null device buffer");
     if ((plan->desc.transform == VKFX_R2C || plan->desc.transform == VKFX_C2R) && d_in == d_out)
         return fail(VKFX_ERR_INVALID_ARGUMENT, "R2C/C2R cannot run in place");
+    if (d_in == d_out && plan->in_bytes != plan->out_bytes)
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "in-place execution needs equal input and output sizes");
     void* work = d_work ? d_work : plan->work.p;
     if (plan->work_bytes && !work) return fail(VKFX_ERR_INVALID_ARGUMENT, "plan needs a workspace");
     hipStream_t s = stream ? (hipStream_t)stream : plan->ctx->stream;
