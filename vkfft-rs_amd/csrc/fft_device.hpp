@@ -341,8 +341,11 @@ __device__ __forceinline__ void root_powers(cpx<T> w, cpx<T>* p) {
 
 // One Stockham stage over a line held in LDS, in place: every thread first
 // loads all of its butterfly inputs, the block synchronises, then writes.
+// Not inlined: the runtime-radix loop dispatches to one of these per stage,
+// and inlined cases share no registers (a dozen radix cases in one body need
+// more than 256 VGPRs and spill to scratch).
 template <typename T, int S, int R>
-__device__ __forceinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
+__device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
                                           const int TT, const int t, const int ps, const StageTw& tw) {
     constexpr int MJ = max_butterflies_per_thread<R>();
     const int NB = N / R;
