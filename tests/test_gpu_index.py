@@ -146,7 +146,10 @@ def test_bluestein(idx_ctx, n, prec):
 
 ND = [([64, 48], 2, F32), ([256, 256], 2, F32), ([8, 4096], 2, F32), ([4096, 8], 1, F32), ([1024, 6], 2, F32),
       ([512, 8], 2, F64), ([8, 512], 2, F64), ([16, 12, 10], 2, F64), ([6, 20, 64, 40], 1, F32),
-      ([64, 64, 64], 1, F64), ([3, 768, 5], 2, F32), ([4099, 4], 1, F32)]
+      ([64, 64, 64], 1, F64), ([3, 768, 5], 2, F32), ([4099, 4], 1, F32),
+      # power-of-two column shapes and split strided axes (32 x 32, 64 x 32, 128 x 64)
+      ([32, 16, 8], 3, F32), ([128, 64], 2, F64), ([16, 128], 5, F32), ([256, 3], 2, F64),
+      ([1024, 4], 1, F64), ([2048, 3], 1, F32), ([8192, 2], 1, F32), ([8192, 2], 1, F64)]
 
 
 def nd_axis_maps(dims, desc):

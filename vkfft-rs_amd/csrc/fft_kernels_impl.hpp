@@ -247,6 +247,14 @@ struct IoPlain {
     }
 };
 
+// IoPlain with both ends staged through LDS (coalesced cooperative copies):
+// for short rows, whose first and last Stockham stages would otherwise touch
+// HBM in segments narrower than 128 bytes.
+struct IoPlainStaged : IoPlain {
+    static constexpr int kLoad = LAY_STAGED;
+    static constexpr int kStore = LAY_STAGED;
+};
+
 struct IoR2CFull : IoPlain {
     static constexpr bool kPtrLoad = false, kPtrStore = false;
     template <class D>
@@ -1023,6 +1031,14 @@ KernelFn pick(KernelKind kind) {
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                               \
             (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>), \
             (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)              \
+    }
+// A shape without the persistent variant (it launches as one block per group
+// under VKFX_PERSIST_BLOCKS_PER_CU as well).
+#define VKFX_SHAPE(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                                \
+    FixedKernel {                                                                                      \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                               \
+            (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>), \
+            nullptr                                                                                    \
     }
 // The same shape with nontemporal HBM streaming (inputs read once, outputs
 // written once).

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <string>
 
 #include "kernels.hpp"
 
@@ -15,6 +16,8 @@ const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
 const FixedKernel* fixed_table_blue(int* count);
 const FixedKernel* fixed_table_nd(int* count);
+const FixedKernel* fixed_table_pow2_f32(int* count);
+const FixedKernel* fixed_table_pow2_f64(int* count);
 
 // All registered fixed-shape instantiations, merged once (thread-safe
 // static initialisation).
@@ -25,7 +28,7 @@ static const FixedKernel* registry(int* count) {
     };
     static const Merged m = [] {
         const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_real, fixed_table_blue,
-                                                fixed_table_nd};
+                                                fixed_table_nd, fixed_table_pow2_f32, fixed_table_pow2_f64};
         constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
         int counts[kTables], sum = 0;
         const FixedKernel* ptrs[kTables];
@@ -59,10 +62,23 @@ const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool co
     const FixedKernel* all = registry(&total);
     // VKFX_FIXED_PICK=k selects the k-th registered variant of a shape key,
     // or its last one if it has fewer (tuning runs); the default is the first.
-    static const int pick = [] {
+    // VKFX_FIXED_PICK_K<kind>=k does the same for one KernelKind only.
+    static const int pick_all = [] {
         const char* e = getenv("VKFX_FIXED_PICK");
         return e ? atoi(e) : 0;
     }();
+    static const auto pick_kind = [] {
+        struct Picks {
+            int v[KK_COUNT];
+        } p;
+        for (int k = 0; k < KK_COUNT; ++k) {
+            const std::string name = "VKFX_FIXED_PICK_K" + std::to_string(k);
+            const char* e = getenv(name.c_str());
+            p.v[k] = e ? atoi(e) : pick_all;
+        }
+        return p;
+    }();
+    const int pick = (kind >= 0 && kind < KK_COUNT) ? pick_kind.v[kind] : pick_all;
     const FixedKernel* last = nullptr;
     int seen = 0;
     for (int i = 0; i < total; ++i) {
@@ -175,7 +191,7 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     KArgs args = a;
     args.nblk = grid;
     if (xcd_groups(kind)) args.flags |= KF_XCD_GROUPS;
-    if (fixed && persist_blocks_per_cu() > 0) {
+    if (fixed && fixed->fn_persist && persist_blocks_per_cu() > 0) {
         // persistent launch: at most the resident capacity, groups by grid stride
         static int cus = 0;
         if (!cus) {
