@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "kernels.hpp"
 #include "radix_constants.hpp"
 
 namespace vkfx {
@@ -294,13 +295,6 @@ __device__ __forceinline__ void dft(cpx<T>* x) {
     }
 }
 
-// Butterflies per thread per stage held in registers. The host picks the
-// threads per line so that ceil((N/R)/threads) never exceeds this bound.
-template <int R>
-__host__ __device__ constexpr int max_butterflies_per_thread() {
-    return R <= 2 ? 16 : R <= 3 ? 10 : R <= 4 ? 8 : R <= 5 ? 6 : R <= 8 ? 4 : R <= 13 ? 2 : 2;
-}
-
 // LDS element index of element e in a line (one pad slot every 2^ps).
 __device__ __forceinline__ int lpad(int e, int ps) { return e + (e >> ps); }
 
@@ -344,10 +338,16 @@ __device__ __forceinline__ void root_powers(cpx<T> w, cpx<T>* p) {
 // Not inlined: the runtime-radix loop dispatches to one of these per stage,
 // and inlined cases share no registers (a dozen radix cases in one body need
 // more than 256 VGPRs and spill to scratch).
-template <typename T, int S, int R>
+template <typename T, int S, int R, bool WIDE>
 __device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
                                           const int TT, const int t, const int ps, const StageTw& tw) {
-    constexpr int MJ = max_butterflies_per_thread<R>();
+    // `line` always points into LDS; without this a non-inlined function
+    // addresses it with flat instructions instead of ds_read / ds_write
+    // (the builtin exists in the device pass only)
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
+#endif
+    constexpr int MJ = dyn_butterflies_per_thread(R, WIDE);
     const int NB = N / R;
     cpx<T> v[MJ][R];
 #pragma unroll
@@ -381,7 +381,7 @@ __device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, c
 }
 
 // Runs every stage of a runtime radix list over the line at `line`.
-template <typename T, int S>
+template <typename T, int S, bool WIDE>
 __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int N, const int TT,
                                            const int t, const int ps, const int nst,
                                            const int* __restrict__ radix, const StageTw& tw) {
@@ -389,19 +389,19 @@ __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int 
     for (int s = 0; s < nst; ++s) {
         const int R = radix[s];
         switch (R) {
-            case 2: stage_lds<T, S, 2>(line, N, P, TT, t, ps, tw); break;
-            case 3: stage_lds<T, S, 3>(line, N, P, TT, t, ps, tw); break;
-            case 4: stage_lds<T, S, 4>(line, N, P, TT, t, ps, tw); break;
-            case 5: stage_lds<T, S, 5>(line, N, P, TT, t, ps, tw); break;
-            case 7: stage_lds<T, S, 7>(line, N, P, TT, t, ps, tw); break;
-            case 6: stage_lds<T, S, 6>(line, N, P, TT, t, ps, tw); break;
-            case 8: stage_lds<T, S, 8>(line, N, P, TT, t, ps, tw); break;
-            case 9: stage_lds<T, S, 9>(line, N, P, TT, t, ps, tw); break;
-            case 10: stage_lds<T, S, 10>(line, N, P, TT, t, ps, tw); break;
-            case 12: stage_lds<T, S, 12>(line, N, P, TT, t, ps, tw); break;
-            case 11: stage_lds<T, S, 11>(line, N, P, TT, t, ps, tw); break;
-            case 13: stage_lds<T, S, 13>(line, N, P, TT, t, ps, tw); break;
-            case 16: stage_lds<T, S, 16>(line, N, P, TT, t, ps, tw); break;
+            case 2: stage_lds<T, S, 2, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 3: stage_lds<T, S, 3, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 4: stage_lds<T, S, 4, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 5: stage_lds<T, S, 5, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 7: stage_lds<T, S, 7, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 6: stage_lds<T, S, 6, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 8: stage_lds<T, S, 8, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 9: stage_lds<T, S, 9, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 10: stage_lds<T, S, 10, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 12: stage_lds<T, S, 12, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 11: stage_lds<T, S, 11, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 13: stage_lds<T, S, 13, WIDE>(line, N, P, TT, t, ps, tw); break;
+            case 16: stage_lds<T, S, 16, WIDE>(line, N, P, TT, t, ps, tw); break;
             default: break;
         }
         P *= R;

@@ -758,7 +758,7 @@ __global__ __launch_bounds__(512) void k_rader_direct(const KArgs a) {
 
 // ------------------------------------------------------- dynamic kernel
 
-template <typename T, int S, class IO>
+template <typename T, int S, class IO, bool WIDE>
 __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
@@ -771,11 +771,11 @@ __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     const int g = tid / a.TT, t = tid - g * a.TT;
     cpx<T>* line = lds + g * a.LS;
     const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
-    run_stages<T, S>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
+    run_stages<T, S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
     if constexpr (IO::kTwoPass) {
         IO::template mid<T, DynDims>(a, lds, li);
         __syncthreads();
-        run_stages<T, -S>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
+        run_stages<T, -S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
     }
     IO::template epilogue<T, S, DynDims>(a, lds, li);
 }
@@ -1000,26 +1000,30 @@ __global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix_persist(const KArgs a) {
 
 // ------------------------------------------------------------- selection
 
-template <typename T, int S>
-KernelFn pick(KernelKind kind) {
+template <typename T, int S, bool W>
+KernelFn pick_dyn(KernelKind kind) {
     switch (kind) {
-        case KK_PLAIN: return k_dyn<T, S, IoPlain>;
-        case KK_R2C_FULL: return k_dyn<T, S, IoR2CFull>;
-        case KK_C2R_FULL: return k_dyn<T, S, IoC2RFull>;
-        case KK_R2C_HALF: return k_dyn<T, S, IoR2CHalf>;
-        case KK_C2R_HALF: return k_dyn<T, S, IoC2RHalf>;
-        case KK_FS_A: return k_dyn<T, S, IoFsA>;
-        case KK_FS_A_BLUE: return k_dyn<T, S, IoFsABlue>;
-        case KK_FS_A_C2R: return k_dyn<T, S, IoFsAC2R>;
-        case KK_FS_B: return k_dyn<T, S, IoFsB>;
-        case KK_FS_B_R2C: return k_dyn<T, S, IoFsBR2C>;
-        case KK_BLUE_B: return k_dyn<T, S, IoBlueB>;
-        case KK_FS_C_BLUE: return k_dyn<T, S, IoFsCBlue>;
-        case KK_BLUE_1: return k_dyn<T, S, IoBlue1>;
-        case KK_RADER_FFT: return k_dyn<T, S, IoRader>;
+        case KK_PLAIN: return k_dyn<T, S, IoPlain, W>;
+        case KK_R2C_FULL: return k_dyn<T, S, IoR2CFull, W>;
+        case KK_C2R_FULL: return k_dyn<T, S, IoC2RFull, W>;
+        case KK_R2C_HALF: return k_dyn<T, S, IoR2CHalf, W>;
+        case KK_C2R_HALF: return k_dyn<T, S, IoC2RHalf, W>;
+        case KK_FS_A: return k_dyn<T, S, IoFsA, W>;
+        case KK_FS_A_BLUE: return k_dyn<T, S, IoFsABlue, W>;
+        case KK_FS_A_C2R: return k_dyn<T, S, IoFsAC2R, W>;
+        case KK_FS_B: return k_dyn<T, S, IoFsB, W>;
+        case KK_FS_B_R2C: return k_dyn<T, S, IoFsBR2C, W>;
+        case KK_BLUE_B: return k_dyn<T, S, IoBlueB, W>;
+        case KK_FS_C_BLUE: return k_dyn<T, S, IoFsCBlue, W>;
+        case KK_BLUE_1: return k_dyn<T, S, IoBlue1, W>;
+        case KK_RADER_FFT: return k_dyn<T, S, IoRader, W>;
         case KK_RADER_DIRECT: return k_rader_direct<T>;
         default: return nullptr;
     }
+}
+template <typename T, int S>
+KernelFn pick(KernelKind kind, bool wide) {
+    return wide ? pick_dyn<T, S, true>(kind) : pick_dyn<T, S, false>(kind);
 }
 
 }  // namespace vkfx

@@ -3,5 +3,5 @@
 #include "fft_kernels_impl.hpp"
 
 namespace vkfx {
-KernelFn pick_f32_inv(KernelKind kind) { return pick<float, 1>(kind); }
+KernelFn pick_f32_inv(KernelKind kind, bool wide) { return pick<float, 1>(kind, wide); }
 }  // namespace vkfx

@@ -36,7 +36,19 @@ enum KFlags : int {
     KF_OUT_ROWMAJOR = 2,  // a line's elements are contiguous in the output
     KF_MIRROR_PAIRS = 4,  // C2R column pass: a block owns columns and their mirrors
     KF_XCD_GROUPS = 8,    // deal line groups to XCDs in contiguous ranges
+    KF_DYN_WIDE = 16,     // runtime-shape kernel holding up to 32 elements per thread per stage
 };
+
+// Butterflies per thread in one radix-R stage of the runtime-shape kernel
+// (the host sizes threads per line with the same rule, so that
+// threads * butterflies covers every butterfly of every stage). The narrow
+// variant holds at most 16 elements per thread and needs about half the
+// registers of the wide one, which doubles the waves resident per CU; the
+// wide variant serves lengths whose narrow geometry exceeds 512 threads.
+constexpr int dyn_butterflies_per_thread(int R, bool wide) {
+    return wide ? (R <= 2 ? 16 : R <= 3 ? 10 : R <= 4 ? 8 : R <= 5 ? 6 : R <= 8 ? 4 : 2)
+                : (R <= 16 && 16 / R > 1 ? 16 / R : 1);
+}
 
 struct KArgs {
     const void* in;
@@ -161,7 +173,7 @@ int launch_conv(int prec, const ConvArgs& a, const void* x, const void* k, void*
 
 // Device functions a launch runs, for resource queries (hipFuncGetAttributes,
 // occupancy): the same selection as the launch functions make.
-const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed);
+const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed, int flags);
 const void* boundary_kernel_fn(int src_type, int dst_type);
 const void* r2r_kernel_fn(bool pre, int prec);
 const void* conv_kernel_fn(int prec);

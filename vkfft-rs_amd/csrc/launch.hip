@@ -8,10 +8,10 @@
 
 namespace vkfx {
 
-KernelFn pick_f32_fwd(KernelKind kind);
-KernelFn pick_f32_inv(KernelKind kind);
-KernelFn pick_f64_fwd(KernelKind kind);
-KernelFn pick_f64_inv(KernelKind kind);
+KernelFn pick_f32_fwd(KernelKind kind, bool wide);
+KernelFn pick_f32_inv(KernelKind kind, bool wide);
+KernelFn pick_f64_fwd(KernelKind kind, bool wide);
+KernelFn pick_f64_inv(KernelKind kind, bool wide);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
 const FixedKernel* fixed_table_blue(int* count);
@@ -150,12 +150,15 @@ static bool xcd_groups(KernelKind kind) {
            kind == KK_FS_C_BLUE;
 }
 
-const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed) {
+static KernelFn pick_kernel(KernelKind kind, int prec, int dir, bool wide) {
+    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide) : pick_f32_inv(kind, wide))
+                     : (dir < 0 ? pick_f64_fwd(kind, wide) : pick_f64_inv(kind, wide));
+}
+
+const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed, int flags) {
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1)) return nullptr;
     if (fixed) return (const void*)fixed->fn;
-    KernelFn fn = prec == 0 ? (dir < 0 ? pick_f32_fwd(kind) : pick_f32_inv(kind))
-                            : (dir < 0 ? pick_f64_fwd(kind) : pick_f64_inv(kind));
-    return (const void*)fn;
+    return (const void*)pick_kernel(kind, prec, dir, (flags & KF_DYN_WIDE) != 0);
 }
 
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block, size_t lds_bytes,
@@ -175,8 +178,7 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         return (int)hipErrorInvalidConfiguration;
     if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))
         return (int)hipErrorInvalidConfiguration;
-    KernelFn fn = prec == 0 ? (dir < 0 ? pick_f32_fwd(kind) : pick_f32_inv(kind))
-                            : (dir < 0 ? pick_f64_fwd(kind) : pick_f64_inv(kind));
+    KernelFn fn = pick_kernel(kind, prec, dir, (a.flags & KF_DYN_WIDE) != 0);
     if (fixed) {
         // the fixed shape must be launched with exactly its own geometry
         if (fixed->kind != kind || fixed->prec != prec || fixed->dir != dir || fixed->N != a.N ||

@@ -130,12 +130,9 @@ struct Geometry {
     std::vector<int> radix;
     size_t lds = 0;
     bool ok = false;
+    bool wide = false;  // runtime-shape kernel with up to 32 elements per thread per stage
     const FixedKernel* fixed = nullptr;
 };
-
-int max_bpt(int r) {
-    return r <= 2 ? 16 : r <= 3 ? 10 : r <= 4 ? 8 : r <= 5 ? 6 : r <= 8 ? 4 : 2;
-}
 
 // Stage radices: power-of-two part split into ceil(p/4) stages as evenly as
 // possible (radix 16/8/4/2), pairs of 3 as radix 9, then one stage per
@@ -174,10 +171,20 @@ Geometry geometry(size_t n, int prec, int want_g, size_t lds_max, size_t lds_bud
     if (!radix_schedule(n, g.radix)) return g;
     if ((int)g.radix.size() > kMaxStages) return g;
     g.N = (int)n;
-    int tt = 1;
-    for (int r : g.radix) {
-        int nb = (int)n / r;
-        tt = std::max(tt, (nb + max_bpt(r) - 1) / max_bpt(r));
+    // threads per line: the narrow kernel (at most 16 elements per thread,
+    // twice the resident waves) unless it would need more than 512 threads
+    auto threads = [&](bool wide) {
+        int tt = 1;
+        for (int r : g.radix) {
+            const int nb = (int)n / r, bpt = dyn_butterflies_per_thread(r, wide);
+            tt = std::max(tt, (nb + bpt - 1) / bpt);
+        }
+        return tt;
+    };
+    int tt = threads(false);
+    if (tt > 512) {
+        g.wide = true;
+        tt = threads(true);
     }
     if (tt > 512) return g;
     g.TT = tt;
@@ -537,6 +544,7 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     a.nstages = (int)g.radix.size();
     for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
     a.nlines = nlines;
+    if (!g.fixed && g.wide) a.flags |= KF_DYN_WIDE;
     int rc = stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
     rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
@@ -2079,7 +2087,7 @@ int vkfx_plan_resources(const vkfx_plan* plan, vkfx_pass_resources* out, uint32_
         } else if (L.conv) {
             fn = conv_kernel_fn(prec);
         } else {
-            fn = fft_kernel_fn(L.kind, prec, L.dir, L.fixed);
+            fn = fft_kernel_fn(L.kind, prec, L.dir, L.fixed, L.a.flags);
             block = L.block;
             lds = L.lds;
         }
