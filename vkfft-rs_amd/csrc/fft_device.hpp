@@ -308,12 +308,20 @@ struct StageTw {
     const void* hi;
     int shift;
 };
+// Entry i of a complex table in global memory. The explicit address space
+// keeps loads in out-of-line functions (whose pointer arguments are generic)
+// on global_load instead of flat_load.
+template <typename T>
+__device__ __forceinline__ cpx<T> ld_table(const void* p, int i) {
+    typedef T v2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) v2* gptr;
+    const v2 x = ((gptr)p)[i];
+    return mk(x.x, x.y);
+}
 template <typename T>
 __device__ __forceinline__ cpx<T> stage_root(const StageTw& w, int m, bool scattered) {
-    if (!scattered) return ((const cpx<T>*)w.full)[m];
-    const cpx<T>* L = (const cpx<T>*)w.lo;
-    const cpx<T>* H = (const cpx<T>*)w.hi;
-    return cmul(H[m >> w.shift], L[m & ((1 << w.shift) - 1)]);
+    if (!scattered) return ld_table<T>(w.full, m);
+    return cmul(ld_table<T>(w.hi, m >> w.shift), ld_table<T>(w.lo, m & ((1 << w.shift) - 1)));
 }
 constexpr int kScatterP = 32;  // stages with P >= this use the two-level tables
 
@@ -340,7 +348,7 @@ __device__ __forceinline__ void root_powers(cpx<T> w, cpx<T>* p) {
 // more than 256 VGPRs and spill to scratch).
 template <typename T, int S, int R, bool WIDE>
 __device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
-                                          const int TT, const int t, const int ps, const StageTw& tw) {
+                                          const int TT, const int t, const int ps, const StageTw tw) {
     // `line` always points into LDS; without this a non-inlined function
     // addresses it with flat instructions instead of ds_read / ds_write
     // (the builtin exists in the device pass only)

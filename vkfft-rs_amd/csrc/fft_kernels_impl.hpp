@@ -108,19 +108,28 @@ __device__ __forceinline__ LineInfo line_default(const KArgs& a, long long blk, 
 }
 
 // Visits (g, e) for g < G, e < n with consecutive threads on consecutive
-// addresses: e fastest when lines are contiguous, g fastest otherwise.
+// addresses: e fastest when lines are contiguous, g fastest otherwise. The
+// (slow, fast) pair of idx = slow * d + fast advances by the block size with
+// one division up front instead of one per element.
 template <class F>
 __device__ __forceinline__ void coop_for(int G, int n, bool rowmajor, F&& f) {
     const int total = G * n;
-    if (rowmajor) {
-        for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-            const int g = idx / n;
-            f(g, idx - g * n);
+    const int d = rowmajor ? n : G;
+    const int step = (int)blockDim.x;
+    const int dq = step / d, dr = step - dq * d;
+    int slow = (int)threadIdx.x / d;
+    int fast = (int)threadIdx.x - slow * d;
+    for (int idx = threadIdx.x; idx < total; idx += step) {
+        if (rowmajor) {
+            f(slow, fast);
+        } else {
+            f(fast, slow);
         }
-    } else {
-        for (int idx = threadIdx.x; idx < total; idx += blockDim.x) {
-            const int e = idx / G;
-            f(idx - e * G, e);
+        slow += dq;
+        fast += dr;
+        if (fast >= d) {
+            fast -= d;
+            ++slow;
         }
     }
 }
