@@ -949,13 +949,19 @@ __device__ __forceinline__ void fix_body(const KArgs& a, cpx<T>* lds, LineInfo* 
     constexpr bool LD = Direct<IO, Sh::COL>::load;
     constexpr bool SD = Direct<IO, Sh::COL>::store;
     const int tid = threadIdx.x;
-    if (tid < Sh::G) li[tid] = IO::line(a, blk, tid);
-    __syncthreads();
     const int g = Sh::COL ? tid % Sh::G : tid / Sh::TT;
     const int t = Sh::COL ? tid / Sh::G : tid % Sh::TT;
+    // A pass that reads and writes HBM only from its own registers needs
+    // nothing but its own line's placement: every thread computes it, with no
+    // shared table and no barrier before the first loads.
+    constexpr bool kOwnLine = LD && SD && !IO::kTwoPass;
+    if constexpr (!kOwnLine) {
+        if (tid < Sh::G) li[tid] = IO::line(a, blk, tid);
+        __syncthreads();
+    }
     cpx<T>* line = lds + g * Sh::LS;
     const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
-    const LineInfo L = li[g];
+    const LineInfo L = kOwnLine ? IO::line(a, blk, g) : li[g];
     if constexpr (!LD) {
         IO::template prologue<T, D>(a, lds, li);
         __syncthreads();
