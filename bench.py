@@ -145,7 +145,7 @@ def run_gpu(cfg, steps, warmup, rotate):
 def plain_copy_bandwidth(nbytes=1 << 30, reps=10):
     """The library's own copy (a transform whose only axis has length 1:
     dims [1], f64, 1 GiB) on device buffers. Its kernel
-    (k_dyn<double, -1, IoPlain>) moves 8-16 bytes per lane like the FFT
+    (k_dyn<double, -1, IoPlain, false>) moves 8-16 bytes per lane like the FFT
     kernels, so its FETCH_SIZE / WRITE_SIZE counters calibrate theirs."""
     import torch
 
@@ -221,7 +221,7 @@ def cpu_baseline(cfg, budget_s=15.0):
 
 
 COPY_BYTES = 1 << 30  # plain_copy_bandwidth(): 1 GiB read + 1 GiB written per launch
-CALIBRATION_KERNEL = "k_dyn<double, -1, vkfx::IoPlain>"
+CALIBRATION_KERNEL = "k_dyn<double, -1, vkfx::IoPlain, false>"
 
 
 def rocprof_summary(dirs, workload_kernel="vkfx"):
