@@ -212,6 +212,7 @@ __device__ __forceinline__ void staged_store(const KArgs& a, const cpx<T>* lds, 
 
 struct IoPlain {
     static constexpr bool kTwoPass = false;
+    static constexpr bool kMidFused = false;  // two-pass: mid_elem applied in the first FFT's last stage
     static constexpr bool kStoreTw = false;  // store multiplies by a per-element pass twiddle
     static constexpr int kLoad = LAY_ANY;
     static constexpr int kStore = LAY_ANY;
@@ -603,6 +604,11 @@ struct IoBlueB : IoPlain {
             v = cmul(v, spec[li[g].c * D::N(a) + e]);
         });
     }
+    static constexpr bool kMidFused = true;
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> mid_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        return cmul(v, ((const cpx<T>*)a.spec)[L.c * a.N + e]);
+    }
     static constexpr bool kStoreTw = true;
     template <typename T>
     static __device__ __forceinline__ cpx<T> tw_root(const KArgs& a, long long m) {
@@ -674,6 +680,11 @@ struct IoBlue1 : IoPlain {
             cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
             v = cmul(v, spec[e]);
         });
+    }
+    static constexpr bool kMidFused = true;
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> mid_elem(const KArgs& a, const LineInfo&, int e, cpx<T> v) {
+        return cmul(v, ((const cpx<T>*)a.spec)[e]);
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -841,7 +852,10 @@ __device__ __forceinline__ int lds_out(int base, int q) {
 
 // One stage with compile-time geometry. SRC/DST: 0 = the line in LDS,
 // 1 = HBM through the IO policy's element functions.
-template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST, bool NTI, bool NTO>
+// MID: this stage ends the first FFT of a two-pass kernel and applies the
+// policy's pointwise product (IO::mid_elem) to its outputs on the way to LDS.
+template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST, bool NTI, bool NTO,
+          bool MID = false>
 __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line, const LineInfo& L, int t,
                                        const StageTw& tw) {
     constexpr int NB = N / R;
@@ -918,7 +932,11 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                     if constexpr (DST) {
                         if (L.valid) IO::template store_elem<T, S, NTO>(a, L, base + q * P, v[j][q]);
                     } else {
-                        line[lds_out<PS, P, R>(base, q)] = v[j][q];
+                        if constexpr (MID) {
+                            line[lds_out<PS, P, R>(base, q)] = IO::template mid_elem<T>(a, L, base + q * P, v[j][q]);
+                        } else {
+                            line[lds_out<PS, P, R>(base, q)] = v[j][q];
+                        }
                     }
                 }
             }
@@ -927,13 +945,13 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
     if constexpr (!DST) __syncthreads();
 }
 
-template <typename T, int S, class IO, class Sh, int SRC0, int DSTL, int P, int R, int... Rest>
+template <typename T, int S, class IO, class Sh, int SRC0, int DSTL, bool MIDL, int P, int R, int... Rest>
 __device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, const LineInfo& L, int t,
                                         const StageTw& tw, RList<R, Rest...>) {
     constexpr bool last = sizeof...(Rest) == 0;
-    fstage<T, S, IO, Sh::N, P, R, Sh::TT, Sh::PS, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO>(
-        a, line, L, t, tw);
-    if constexpr (!last) fstages<T, S, IO, Sh, SRC0, DSTL, P * R>(a, line, L, t, tw, RList<Rest...>{});
+    fstage<T, S, IO, Sh::N, P, R, Sh::TT, Sh::PS, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO,
+           last && MIDL && !DSTL>(a, line, L, t, tw);
+    if constexpr (!last) fstages<T, S, IO, Sh, SRC0, DSTL, MIDL, P * R>(a, line, L, t, tw, RList<Rest...>{});
 }
 
 template <class IO, bool COL>
@@ -967,12 +985,14 @@ __device__ __forceinline__ void fix_body(const KArgs& a, cpx<T>* lds, LineInfo* 
         __syncthreads();
     }
     if constexpr (IO::kTwoPass) {
-        fstages<T, S, IO, Sh, LD ? 1 : 0, 0, 1>(a, line, L, t, tw, typename Sh::Radices{});
-        IO::template mid<T, D>(a, lds, li);
-        __syncthreads();
-        fstages<T, -S, IO, Sh, 0, SD ? 1 : 0, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        fstages<T, S, IO, Sh, LD ? 1 : 0, 0, IO::kMidFused, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        if constexpr (!IO::kMidFused) {
+            IO::template mid<T, D>(a, lds, li);
+            __syncthreads();
+        }
+        fstages<T, -S, IO, Sh, 0, SD ? 1 : 0, false, 1>(a, line, L, t, tw, typename Sh::Radices{});
     } else {
-        fstages<T, S, IO, Sh, LD ? 1 : 0, SD ? 1 : 0, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        fstages<T, S, IO, Sh, LD ? 1 : 0, SD ? 1 : 0, false, 1>(a, line, L, t, tw, typename Sh::Radices{});
     }
     if constexpr (!SD) IO::template epilogue<T, S, D>(a, lds, li);
 }
