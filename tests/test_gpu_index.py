@@ -102,7 +102,9 @@ def check_1d(ctx, n, batch, prec, direction=FWD, env=None):
 
 
 SINGLE = [2, 3, 5, 7, 8, 11, 13, 16, 18, 25, 27, 32, 36, 49, 60, 64, 96, 100, 121, 125, 128, 169, 243,
-          343, 360, 512, 625, 1000, 1024, 1536, 2048, 2187, 2401, 3125, 4096, 6561, 8192, 10000, 15625, 16384]
+          343, 360, 512, 625, 1000, 1024, 1536, 2048, 2187, 2401, 3125, 4096, 6561, 8192, 10000, 15625, 16384,
+          # the 3*2^k / 5*2^k fixed families
+          12, 20, 24, 40, 48, 80, 160, 192, 320, 384, 640, 768, 1280, 2560, 3072, 5120, 6144, 10240, 12288]
 
 
 @pytest.mark.parametrize("prec", [F32, F64])

@@ -84,6 +84,23 @@ def test_c2c_length_sweep(hip_ctx, prec, direction):
 
 
 @pytest.mark.parametrize("prec", [F32, F64])
+def test_many_lines_per_block(hip_ctx, prec):
+    """Short lengths at batch 70 and 133: blocks of up to 64 lines, partial
+    last blocks, every line checked (the line placement of the cooperative
+    copies and of each thread's butterflies), against pocketfft."""
+    bad = {}
+    for n in list(range(2, 70)) + [96, 100, 120, 125, 128, 130]:
+        for batch in (70, 133):
+            x = rand(n * batch, 7 * n + batch, prec)
+            y, _ = c2c(hip_ctx, [n], batch, x, prec)
+            ref = np.fft.fft(x.reshape(batch, n).astype(np.complex128), axis=1)
+            lines = np.linalg.norm(y.reshape(batch, n) - ref, axis=1) / np.linalg.norm(ref, axis=1)
+            if lines.max() > 4 * TOL[prec]:
+                bad[(n, batch)] = np.nonzero(lines > 4 * TOL[prec])[0][:8].tolist()
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
 def test_c1_shape_sampled_full_size(hip_ctx, prec):
     """C1: N=1024, batch 8192; every 97th transform against the oracle, all
     of them through a forward/inverse round trip."""
