@@ -151,7 +151,10 @@ ND = [([64, 48], 2, F32), ([256, 256], 2, F32), ([8, 4096], 2, F32), ([4096, 8],
       ([64, 64, 64], 1, F64), ([3, 768, 5], 2, F32), ([4099, 4], 1, F32),
       # power-of-two column shapes and split strided axes (32 x 32, 64 x 32, 128 x 64)
       ([32, 16, 8], 3, F32), ([128, 64], 2, F64), ([16, 128], 5, F32), ([256, 3], 2, F64),
-      ([1024, 4], 1, F64), ([2048, 3], 1, F32), ([8192, 2], 1, F32), ([8192, 2], 1, F64)]
+      ([1024, 4], 1, F64), ([2048, 3], 1, F32), ([8192, 2], 1, F32), ([8192, 2], 1, F64),
+      # 3*2^k / 5*2^k / 10^k / 360 column shapes
+      ([96, 20], 2, F32), ([360, 12], 1, F64), ([100, 40, 6], 1, F32), ([640, 3], 2, F32), ([640, 3], 1, F64),
+      ([80, 160, 2], 1, F64), ([384, 24], 1, F32), ([12, 48, 5], 2, F64)]
 
 
 def nd_axis_maps(dims, desc):
