@@ -228,6 +228,31 @@ def test_r2c_c2r(hip_ctx, n, prec):
     assert o.rel_l2(xr, back) <= TOL[prec] * (1 if prec == F32 else 10)
 
 
+HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 320],
+              F64: [64, 128, 160, 192, 256, 320, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096]}
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_r2c_c2r_fixed_half_lengths(hip_ctx, prec):
+    """Even lengths whose half-size FFT has a fixed shape, at batch 37 (several
+    lines per block, a partial last block), every line against pocketfft."""
+    rdt = np.float32 if prec == F32 else np.float64
+    cdt = _cdtype(prec)
+    bad = {}
+    for m in HALF_FIXED[prec]:
+        n, batch = 2 * m, 37
+        x = o.normal(n * batch, m, rdt).reshape(batch, n)
+        X, ir = r2c(hip_ctx, n, batch, x.reshape(-1), prec)
+        assert hip_ctx.plan(ir).describe()["passes"][0]["fixed_shape"], n
+        ref = np.fft.rfft(x.astype(np.float64), axis=1)
+        e1 = o.rel_l2(X, ref.reshape(-1))
+        xr, _ = c2r(hip_ctx, n, batch, ref.astype(cdt).reshape(-1), prec)
+        e2 = o.rel_l2(xr, x.astype(np.float64).reshape(-1))
+        if max(e1, e2) > TOL[prec] * (1 if prec == F32 else 10):
+            bad[n] = (e1, e2)
+    assert not bad, bad
+
+
 def test_c2_shape_round_trip_full_size(hip_ctx):
     """C2: R2C N=2^20 batch 256 then C2R with normalization; two sampled
     transforms against the oracle, the whole batch through the round trip."""

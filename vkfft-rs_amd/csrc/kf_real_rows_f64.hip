@@ -1,0 +1,88 @@
+// Fixed shapes of the one-upload even-length real transforms, f64: the
+// half-size packed FFT of R2C (postprocess fused into the staged store) and of
+// C2R (preprocess fused into the direct loads) for half lengths M that have a
+// fixed C2C row shape (powers of two and the 3*2^k / 5*2^k families), with the
+// same radices, threads, lines per block and LDS strides as those rows. R2C is
+// registered for the caller's input with or without the caller's output, C2R
+// for the caller's output with or without the caller's input.
+#include "fft_kernels_impl.hpp"
+
+namespace vkfx {
+
+static const FixedKernel kTable[] = {
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 64, 8, 32, 3, 71, false, true, true, 8, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 64, 8, 32, 3, 71, false, true, false, 8, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 64, 8, 32, 3, 71, false, true, true, 8, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 64, 8, 32, 3, 71, false, false, true, 8, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 128, 16, 16, 4, 135, false, true, true, 16, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 128, 16, 16, 4, 135, false, true, false, 16, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 128, 16, 16, 4, 135, false, true, true, 16, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 128, 16, 16, 4, 135, false, false, true, 16, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 256, 16, 16, 4, 271, false, true, true, 16, 16),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 256, 16, 16, 4, 271, false, true, false, 16, 16),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 256, 16, 16, 4, 271, false, true, true, 16, 16),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 256, 16, 16, 4, 271, false, false, true, 16, 16),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 512, 64, 2, 3, 576, false, true, true, 8, 8, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 512, 64, 2, 3, 576, false, true, false, 8, 8, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 512, 64, 2, 3, 576, false, true, true, 8, 8, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 512, 64, 2, 3, 576, false, false, true, 8, 8, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 1024, 128, 2, 4, 1087, false, true, true, 16, 8, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 1024, 128, 2, 4, 1087, false, true, false, 16, 8, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 1024, 128, 2, 4, 1087, false, true, true, 16, 8, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 1024, 128, 2, 4, 1087, false, false, true, 16, 8, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 2048, 256, 1, 4, 2175, false, true, true, 16, 16, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 2048, 256, 1, 4, 2175, false, true, false, 16, 16, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 2048, 256, 1, 4, 2175, false, true, true, 16, 16, 8),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 2048, 256, 1, 4, 2175, false, false, true, 16, 16, 8),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 4096, 256, 1, 4, 4351, false, true, true, 16, 16, 16),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 4096, 256, 1, 4, 4351, false, true, false, 16, 16, 16),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 4096, 256, 1, 4, 4351, false, true, true, 16, 16, 16),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 4096, 256, 1, 4, 4351, false, false, true, 16, 16, 16),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 192, 12, 21, 4, 204, false, true, true, 16, 12),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 192, 12, 21, 4, 204, false, true, false, 16, 12),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 192, 12, 21, 4, 204, false, true, true, 16, 12),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 192, 12, 21, 4, 204, false, false, true, 16, 12),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 384, 24, 10, 4, 407, false, true, true, 16, 8, 3),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 384, 24, 10, 4, 407, false, true, false, 16, 8, 3),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 384, 24, 10, 4, 407, false, true, true, 16, 8, 3),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 384, 24, 10, 4, 407, false, false, true, 16, 8, 3),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 768, 48, 5, 4, 815, false, true, true, 16, 16, 3),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 768, 48, 5, 4, 815, false, true, false, 16, 16, 3),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 768, 48, 5, 4, 815, false, true, true, 16, 16, 3),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 768, 48, 5, 4, 815, false, false, true, 16, 16, 3),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 1536, 96, 2, 4, 1631, false, true, true, 16, 16, 6),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 1536, 96, 2, 4, 1631, false, true, false, 16, 16, 6),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 1536, 96, 2, 4, 1631, false, true, true, 16, 16, 6),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 1536, 96, 2, 4, 1631, false, false, true, 16, 16, 6),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 3072, 192, 1, 4, 3263, false, true, true, 16, 16, 12),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 3072, 192, 1, 4, 3263, false, true, false, 16, 16, 12),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 3072, 192, 1, 4, 3263, false, true, true, 16, 16, 12),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 3072, 192, 1, 4, 3263, false, false, true, 16, 16, 12),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 160, 10, 25, 4, 170, false, true, true, 16, 10),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 160, 10, 25, 4, 170, false, true, false, 16, 10),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 160, 10, 25, 4, 170, false, true, true, 16, 10),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 160, 10, 25, 4, 170, false, false, true, 16, 10),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 320, 40, 6, 3, 359, false, true, true, 8, 8, 5),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 320, 40, 6, 3, 359, false, true, false, 8, 8, 5),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 320, 40, 6, 3, 359, false, true, true, 8, 8, 5),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 320, 40, 6, 3, 359, false, false, true, 8, 8, 5),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 640, 40, 6, 4, 679, false, true, true, 16, 8, 5),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 640, 40, 6, 4, 679, false, true, false, 16, 8, 5),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 640, 40, 6, 4, 679, false, true, true, 16, 8, 5),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 640, 40, 6, 4, 679, false, false, true, 16, 8, 5),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 1280, 80, 3, 4, 1359, false, true, true, 16, 16, 5),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 1280, 80, 3, 4, 1359, false, true, false, 16, 16, 5),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 1280, 80, 3, 4, 1359, false, true, true, 16, 16, 5),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 1280, 80, 3, 4, 1359, false, false, true, 16, 16, 5),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 2560, 160, 1, 4, 2719, false, true, true, 16, 16, 10),
+    VKFX_SHAPE(KK_R2C_HALF, IoR2CHalf, double, 1, -1, 2560, 160, 1, 4, 2719, false, true, false, 16, 16, 10),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 2560, 160, 1, 4, 2719, false, true, true, 16, 16, 10),
+    VKFX_SHAPE(KK_C2R_HALF, IoC2RHalf, double, 1, 1, 2560, 160, 1, 4, 2719, false, false, true, 16, 16, 10),
+};
+
+const FixedKernel* fixed_table_real_rows_f64(int* count) {
+    *count = (int)(sizeof(kTable) / sizeof(kTable[0]));
+    return kTable;
+}
+
+}  // namespace vkfx
