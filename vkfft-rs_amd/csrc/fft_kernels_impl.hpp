@@ -213,6 +213,8 @@ __device__ __forceinline__ void staged_store(const KArgs& a, const cpx<T>* lds, 
 struct IoPlain {
     static constexpr bool kTwoPass = false;
     static constexpr bool kMidFused = false;  // two-pass: mid_elem applied in the first FFT's last stage
+    // direct first stage: load_tw(e, w) with w = ltw_root(b) * ltw_root(NB, step)^i for e = b + i*NB
+    static constexpr bool kLoadTw = false;
     static constexpr bool kStoreTw = false;  // store multiplies by a per-element pass twiddle
     static constexpr int kLoad = LAY_ANY;
     static constexpr int kStore = LAY_ANY;
@@ -345,11 +347,20 @@ struct IoC2RHalf : IoPlain {
     static constexpr int kStore = LAY_ROW;
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int k) {
+        return load_tw<T, NTIO>(a, L, k, tw2<T>(a.rlo, a.rhi, a.rshift, k));
+    }
+    // w = W_N^k = exp(-2 pi i k / 2M)
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_tw(const KArgs& a, const LineInfo& L, int k, cpx<T> w) {
         const cpx<T>* in = (const cpx<T>*)a.in;
         cpx<T> X = ldg_in<NTIO>(a, in + L.ib + k * a.in_es);
         cpx<T> Xm = conj(ldg_in<NTIO>(a, in + L.ib + (a.N - k) * a.in_es));
-        cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
         return (X + Xm) + muli<1>(cmulc(X - Xm, w));
+    }
+    static constexpr bool kLoadTw = true;
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> ltw_root(const KArgs& a, const LineInfo&, int m, bool = false) {
+        return tw2<T>(a.rlo, a.rhi, a.rshift, m);
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -440,11 +451,15 @@ struct IoFsAC2R : IoFsA {
     // Z[k] = (X[k] + conj X[M-k]) + i (X[k] - conj X[M-k]) conj(w_k), w_k = exp(-2 pi i k / 2M)
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        return load_tw<T, NTIO>(a, L, e, tw2<T>(a.rlo, a.rhi, a.rshift, L.c + (long long)e * a.N2));
+    }
+    // w = W_N^k for k = c + e*N2
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_tw(const KArgs& a, const LineInfo& L, int e, cpx<T> w) {
         const cpx<T>* in = (const cpx<T>*)a.in;
         const long long k = L.c + (long long)e * a.N2;
         cpx<T> X = ldg_in<NTIO>(a, in + L.ib + e * a.in_es);
         cpx<T> Xm = conj(in[L.o * a.in_os + (a.M - k)]);
-        cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
         return (X + Xm) + muli<1>(cmulc(X - Xm, w));
     }
     // Both members of a pair from A = X[k], B = X[M-k]; w_(M-k) = -conj(w_k).
@@ -509,6 +524,12 @@ struct IoFsAC2R : IoFsA {
 // barrier goes away.
 struct IoFsAC2RDirect : IoFsAC2R {
     static constexpr int kLoad = LAY_COL;
+    static constexpr bool kLoadTw = true;
+    // root(c + b*N2) for butterfly b; the step NB advances k by NB*N2
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> ltw_root(const KArgs& a, const LineInfo& L, int m, bool step = false) {
+        return tw2<T>(a.rlo, a.rhi, a.rshift, (step ? 0 : L.c) + (long long)m * a.N2);
+    }
 };
 
 // Four-step row pass. Line = row k1 (C = N1), contiguous in the scratch;
@@ -873,6 +894,19 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                 const long long st = (long long)NB * a.in_es;
 #pragma unroll
                 for (int i = 0; i < R; ++i) v[j][i] = ldg_in<NTI>(a, p + i * st);
+            } else if constexpr (SRC && IO::kLoadTw) {
+                // inputs b + i*NB carry the load twiddle root(b) * root(NB)^i
+                if (L.valid) {
+                    const cpx<T> wb = IO::template ltw_root<T>(a, L, b);
+                    cpx<T> sp[R];
+                    root_powers<R>(IO::template ltw_root<T>(a, L, NB, true), sp);
+#pragma unroll
+                    for (int i = 0; i < R; ++i)
+                        v[j][i] = IO::template load_tw<T, NTI>(a, L, b + i * NB, cmul(wb, sp[i]));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < R; ++i) v[j][i] = zero<T>();
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < R; ++i) {
