@@ -579,33 +579,45 @@ struct IoFsBR2C : IoPlain {
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
         staged_load<IoPlain, D>(a, lds, li, true);
     }
+    // Column-major over (row g, bin k2) with the block size a multiple of G:
+    // each thread keeps its row and steps k2 by blockDim/G, so the twiddle
+    // W_N^k (k = k1 + N1*k2) advances by one multiplication with W_N^(N1*dk)
+    // (at most 32 steps per thread) instead of two table loads per element.
     template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
         cpx<T>* out = (cpx<T>*)a.out;
         const int G = D::G(a), H = G / 2;
         const int N2 = D::N(a);
-        coop_for(G, N2, false, [&](int g, int k2) {
-            if (!li[g].valid) return;
-            const long long k1 = li[g].c;
-            int gp, k2m;
-            if (k1 == 0) {
-                gp = g;
-                k2m = k2 == 0 ? 0 : N2 - k2;
-            } else if (2 * k1 == a.N1) {
-                gp = g;
-                k2m = N2 - 1 - k2;
-            } else {
-                gp = g < H ? g + H : g - H;
-                k2m = N2 - 1 - k2;
-            }
+        const int g = (int)threadIdx.x % G;
+        const int dk = (int)blockDim.x / G;
+        if (!li[g].valid) return;
+        const long long k1 = li[g].c;
+        const cpx<T>* row = lds + g * D::LS(a);
+        int gp, mirror;  // mirror partner: row gp, bin (mirror - k2) or N2 - k2 for row 0
+        if (k1 == 0) {
+            gp = g;
+            mirror = N2;
+        } else if (2 * k1 == a.N1) {
+            gp = g;
+            mirror = N2 - 1;
+        } else {
+            gp = g < H ? g + H : g - H;
+            mirror = N2 - 1;
+        }
+        const cpx<T>* prow = lds + gp * D::LS(a);
+        int k2 = (int)threadIdx.x / G;
+        cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k1 + a.N1 * (long long)k2);
+        const cpx<T> wstep = tw2<T>(a.rlo, a.rhi, a.rshift, a.N1 * (long long)dk);
+        for (; k2 < N2; k2 += dk) {
+            const int k2m = (k1 == 0 && k2 == 0) ? 0 : mirror - k2;
             const long long k = k1 + a.N1 * k2;
-            cpx<T> A = lds[g * D::LS(a) + lpad(k2, D::PS(a))];
-            cpx<T> B = conj(lds[gp * D::LS(a) + lpad(k2m, D::PS(a))]);
-            cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
+            cpx<T> A = row[lpad(k2, D::PS(a))];
+            cpx<T> B = conj(prow[lpad(k2m, D::PS(a))]);
             cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
             stg_out<D::NTO>(a, out + li[g].ob + k, scale(X, (T)0.5));
             if (k == 0) out[li[g].ob + a.M] = mk(A.re - A.im, (T)0);
-        });
+            w = cmul(w, wstep);
+        }
     }
 };
 
