@@ -25,12 +25,6 @@ static const FixedKernel kTable[] = {
     VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 1024, 64, 16, 4, 1090, true, false, false, 16, 16, 4),
     VKFX_FIXED_NT(KK_FS_B_R2C, IoFsBR2C, float, 0, -1, 512, 32, 32, 3, 577, false, false, false, 8, 8, 8),
     VKFX_FIXED_NT(KK_FS_B, IoFsB, float, 0, 1, 1024, 64, 16, 5, 1058, false, false, false, 16, 16, 4),
-    // half-size blocks, two resident per CU (VKFX_FIXED_PICK_K<kind>=3 / 2)
-    VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 1024, 64, 8, 4, 1090, true, false, false, 16, 16, 4),
-    VKFX_FIXED_NT(KK_FS_B_R2C, IoFsBR2C, float, 0, -1, 512, 32, 16, 4, 543, false, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_FS_A_C2R, IoFsAC2RDirect, float, 0, 1, 512, 32, 16, 30, 513, true, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_FS_A_C2R, IoFsAC2RDirect, float, 0, 1, 512, 32, 32, 30, 513, true, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_FS_B, IoFsB, float, 0, 1, 1024, 64, 8, 4, 1090, false, false, false, 16, 16, 4),
 };
 
 const FixedKernel* fixed_table_real(int* count) {
