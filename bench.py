@@ -1,6 +1,6 @@
 """Benchmark of the MI355X batched-FFT path (one JSON line on stdout).
 
-Default workload (BASELINE metric "batched f32 C2C effective HBM GB/s"):
+Default workload (metric "batched f32 C2C effective HBM GB/s"):
 C1 = 1-D C2C forward, f32, N=1024, batch 8192, inputs resident in HBM.
 A step is one execute of the plan over one batch. Buffers rotate over 8
 input/output pairs (1 GiB) so the 256 MB Infinity Cache cannot hold the
@@ -12,7 +12,7 @@ working set between steps.
   cpu_baseline = the oracle (a port of vkfft-rs src/reference.rs) timed on
                this host's cores over a bounded sample of the same workload
 
---config selects another BASELINE config (c2, c3, c4, c5a, c5b) for
+--config selects another benchmark configuration (c2, c3, c4, c5a, c5b) for
 measurement runs; --all prints one line per config.
 """
 from __future__ import annotations
@@ -43,7 +43,7 @@ CONFIGS = {
 }
 
 
-# BASELINE's metric for the default workload; the other configs report the
+# The metric of the default workload; the other configs report the
 # same quantities for their own transform.
 METRICS = {
     "c1": "batched f32 C2C effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
@@ -57,7 +57,8 @@ METRICS = {
 
 def algorithmic(cfg):
     """(bytes, flops) of one step: one read + one write of the logical data
-    (BASELINE.md section 2); flops 5 N log2 N per transform (logical N)."""
+    (for R2C/C2R: N*4 + (N/2+1)*8 bytes per direction and transform); flops
+    5 N log2 N per transform (logical N)."""
     n = 1
     for d in cfg["dims"]:
         n *= d
@@ -290,7 +291,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c1", choices=sorted(CONFIGS))
-    ap.add_argument("--all", action="store_true", help="one line per BASELINE config")
+    ap.add_argument("--all", action="store_true", help="one line per benchmark configuration")
     ap.add_argument("--rotate", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch (tuning runs)")
@@ -301,7 +302,7 @@ def main():
         print(rocprof_summary(args.rocprof_summary))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md).",
+        print("bench.py measures one GPU only: this build has no multi-GPU path.",
               file=sys.stderr)
         sys.exit(2)
     names = list(CONFIGS) if args.all else [args.config]

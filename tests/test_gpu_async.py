@@ -4,7 +4,7 @@ resident program chains, src/backend/cuda/runtime.rs:1744-1809).
 
 Results of a ticket or a chain must equal the synchronous execute of the same
 plans bit for bit (same kernels, own buffers), and the oracle within the
-BASELINE tolerances."""
+parity tolerances (f32 relative L2 1e-5, f64 1e-13)."""
 import numpy as np
 import pytest
 

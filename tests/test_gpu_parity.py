@@ -1,7 +1,7 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle
 (restated src/reference.rs) on identical seeded inputs.
 
-Tolerances (BASELINE): f32 relative L2 <= 1e-5 against the f64 oracle of the
+Tolerances: f32 relative L2 <= 1e-5 against the f64 oracle of the
 same f32-rounded input; f64 <= 1e-13. Where the oracle's own algorithm is
 less accurate than 1e-13 (reference::fft's Bluestein at large N), f64 is
 checked against pocketfft at 1e-13 and against the oracle within its own

@@ -1,5 +1,5 @@
 // Fixed-shape C2C kernels for the contiguous and strided axes of the
-// BASELINE configurations (1024 and 4096 f32, 512 f64).
+// benchmark configurations (1024 and 4096 f32, 512 f64).
 #include "fft_kernels_impl.hpp"
 
 namespace vkfx {

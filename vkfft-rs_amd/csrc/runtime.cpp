@@ -756,8 +756,9 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
         if (rc || done) return rc;
     }
     if (alg == Algorithm::Rader) c.js << "\"rader_fallback\":\"bluestein\",";
-    // Bluestein (also Rader axes that need the recursive extension or have
-    // composite length).
+    // Bluestein (also Rader axes that need the recursive extension, and
+    // composite lengths with a Rader prime factor, which the reference folds
+    // into a mixed-radix tree).
     const size_t M = conv_len ? conv_len : next_smooth_at_least(2 * n - 1, {2, 3, 5, 7});
     if (M < 2 * n - 1) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein convolution length below 2N-1");
     Geometry g = kernel_geometry(KK_BLUE_1, prec, -1, M, false, 1, c.lds_max, c.lds_max);
