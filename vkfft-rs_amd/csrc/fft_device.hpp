@@ -341,20 +341,34 @@ __device__ __forceinline__ void root_powers(cpx<T> w, cpx<T>* p) {
     }
 }
 
-// One Stockham stage over a line held in LDS, in place: every thread first
-// loads all of its butterfly inputs, the block synchronises, then writes.
+// Where a runtime-shape stage reads its inputs and writes its outputs.
+enum StageMode : int {
+    SM_LDS = 0,    // LDS -> LDS, in place
+    SM_FIRST = 1,  // the line's contiguous HBM elements -> LDS
+    SM_LAST = 2,   // LDS -> the line's contiguous HBM elements (scaled)
+};
+
+// One Stockham stage of the runtime-shape kernels. SM_LDS reads every input
+// of the thread's butterflies from LDS, synchronises the block and writes in
+// place; SM_FIRST loads from HBM and SM_LAST stores to HBM (lines contiguous
+// there, consecutive threads on consecutive elements), with no barrier
+// between their reads and writes (the two sides are different memories).
 // Not inlined: the runtime-radix loop dispatches to one of these per stage,
 // and inlined cases share no registers (a dozen radix cases in one body need
 // more than 256 VGPRs and spill to scratch).
-template <typename T, int S, int R, bool WIDE>
-__device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, const int P,
-                                          const int TT, const int t, const int ps, const StageTw tw) {
+template <typename T, int S, int R, bool WIDE, int MODE>
+__device__ __noinline__ void stage_rt(cpx<T>* __restrict__ line, const int N, const int P, const int TT,
+                                      const int t, const int ps, const StageTw tw, const cpx<T>* gsrc,
+                                      cpx<T>* gdst, const int valid, const T sc) {
     // `line` always points into LDS; without this a non-inlined function
     // addresses it with flat instructions instead of ds_read / ds_write
     // (the builtin exists in the device pass only)
 #if defined(__HIP_DEVICE_COMPILE__)
     __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
 #endif
+    typedef T v2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) v2* gsrc_t;
+    typedef __attribute__((address_space(1))) v2* gdst_t;
     constexpr int MJ = dyn_butterflies_per_thread(R, WIDE);
     const int NB = N / R;
     cpx<T> v[MJ][R];
@@ -363,10 +377,17 @@ __device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, c
         const int b = t + j * TT;
         if (b < NB) {
 #pragma unroll
-            for (int i = 0; i < R; ++i) v[j][i] = line[lpad(b + i * NB, ps)];
+            for (int i = 0; i < R; ++i) {
+                if constexpr (MODE == SM_FIRST) {
+                    const v2 x = ((gsrc_t)gsrc)[b + i * NB];
+                    v[j][i] = mk(x.x, x.y);
+                } else {
+                    v[j][i] = line[lpad(b + i * NB, ps)];
+                }
+            }
         }
     }
-    __syncthreads();
+    if constexpr (MODE == SM_LDS) __syncthreads();
     const int step = N / (P * R);
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
@@ -382,38 +403,81 @@ __device__ __noinline__ void stage_lds(cpx<T>* __restrict__ line, const int N, c
             dft<R, S>(v[j]);
             const int base = (b - k) * R + k;
 #pragma unroll
-            for (int q = 0; q < R; ++q) line[lpad(base + q * P, ps)] = v[j][q];
+            for (int q = 0; q < R; ++q) {
+                if constexpr (MODE == SM_LAST) {
+                    if (valid) {
+                        const cpx<T> y = scale(v[j][q], sc);
+                        v2 x;
+                        x.x = y.re;
+                        x.y = y.im;
+                        ((gdst_t)gdst)[base + q * P] = x;
+                    }
+                } else {
+                    line[lpad(base + q * P, ps)] = v[j][q];
+                }
+            }
         }
     }
-    __syncthreads();
+    if constexpr (MODE != SM_LAST) __syncthreads();
 }
 
-// Runs every stage of a runtime radix list over the line at `line`.
+// Dispatch of one stage on its runtime radix. Radix-2 HBM stages are not
+// built (their hoisted loads would raise the register count of every
+// runtime-shape kernel); the host gives such lines the staged kernel.
+template <typename T, int S, bool WIDE, int MODE>
+__device__ __forceinline__ void stage_rt_radix(int R, cpx<T>* __restrict__ line, const int N, const int P,
+                                               const int TT, const int t, const int ps, const StageTw& tw,
+                                               const cpx<T>* gsrc, cpx<T>* gdst, const int valid, const T sc) {
+#define VKFX_STAGE_CASE(RR) \
+    case RR: stage_rt<T, S, RR, WIDE, MODE>(line, N, P, TT, t, ps, tw, gsrc, gdst, valid, sc); break;
+    switch (R) {
+        case 2:
+            if constexpr (MODE == SM_LDS) stage_rt<T, S, 2, WIDE, MODE>(line, N, P, TT, t, ps, tw, gsrc, gdst, valid, sc);
+            break;
+        VKFX_STAGE_CASE(3)
+        VKFX_STAGE_CASE(4)
+        VKFX_STAGE_CASE(5)
+        VKFX_STAGE_CASE(6)
+        VKFX_STAGE_CASE(7)
+        VKFX_STAGE_CASE(8)
+        VKFX_STAGE_CASE(9)
+        VKFX_STAGE_CASE(10)
+        VKFX_STAGE_CASE(11)
+        VKFX_STAGE_CASE(12)
+        VKFX_STAGE_CASE(13)
+        VKFX_STAGE_CASE(16)
+        default: break;
+    }
+#undef VKFX_STAGE_CASE
+}
+
+// Runs every stage of a runtime radix list over the line at `line` (in LDS).
 template <typename T, int S, bool WIDE>
 __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int N, const int TT,
                                            const int t, const int ps, const int nst,
                                            const int* __restrict__ radix, const StageTw& tw) {
     int P = 1;
     for (int s = 0; s < nst; ++s) {
-        const int R = radix[s];
-        switch (R) {
-            case 2: stage_lds<T, S, 2, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 3: stage_lds<T, S, 3, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 4: stage_lds<T, S, 4, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 5: stage_lds<T, S, 5, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 7: stage_lds<T, S, 7, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 6: stage_lds<T, S, 6, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 8: stage_lds<T, S, 8, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 9: stage_lds<T, S, 9, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 10: stage_lds<T, S, 10, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 12: stage_lds<T, S, 12, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 11: stage_lds<T, S, 11, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 13: stage_lds<T, S, 13, WIDE>(line, N, P, TT, t, ps, tw); break;
-            case 16: stage_lds<T, S, 16, WIDE>(line, N, P, TT, t, ps, tw); break;
-            default: break;
-        }
-        P *= R;
+        stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, nullptr, 0, (T)1);
+        P *= radix[s];
     }
+}
+
+// The same with the first stage reading the line from HBM (`src`) and the
+// last writing it, times `sc`, to HBM (`dst`, skipped when !valid): at least
+// two stages, neither end of radix 2.
+template <typename T, int S, bool WIDE>
+__device__ __forceinline__ void run_stages_direct(cpx<T>* __restrict__ line, const int N, const int TT,
+                                                  const int t, const int ps, const int nst,
+                                                  const int* __restrict__ radix, const StageTw& tw,
+                                                  const cpx<T>* src, cpx<T>* dst, int valid, T sc) {
+    stage_rt_radix<T, S, WIDE, SM_FIRST>(radix[0], line, N, 1, TT, t, ps, tw, src, dst, valid, sc);
+    int P = radix[0];
+    for (int s = 1; s + 1 < nst; ++s) {
+        stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, src, dst, valid, sc);
+        P *= radix[s];
+    }
+    stage_rt_radix<T, S, WIDE, SM_LAST>(radix[nst - 1], line, N, P, TT, t, ps, tw, src, dst, valid, sc);
 }
 
 }  // namespace vkfx

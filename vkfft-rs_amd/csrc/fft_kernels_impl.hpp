@@ -833,6 +833,24 @@ __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     IO::template epilogue<T, S, DynDims>(a, lds, li);
 }
 
+// Runtime-shape C2C over lines contiguous in HBM (KF_DYN_DIRECT, chosen by
+// the host): the first stage loads the line straight from HBM into registers
+// and the last stage stores registers straight to HBM (threads of a line are
+// adjacent lanes), so the line passes through LDS only between stages. Each
+// thread computes its own line placement; lines past the end map onto line 0
+// (loads in bounds, stores skipped).
+template <typename T, int S, bool WIDE>
+__global__ __launch_bounds__(512) void k_dyn_direct(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
+    const int tid = threadIdx.x;
+    const int g = tid / a.TT, t = tid - g * a.TT;
+    const LineInfo L = line_default(a, group_index(a), g);
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
+    run_stages_direct<T, S, WIDE>(lds + g * a.LS, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw,
+                                  (const cpx<T>*)a.in + L.ib, (cpx<T>*)a.out + L.ob, L.valid, (T)a.scale);
+}
+
 // -------------------------------------------------- fixed-shape kernel
 
 template <int... R>
@@ -1103,7 +1121,8 @@ KernelFn pick_dyn(KernelKind kind) {
     }
 }
 template <typename T, int S>
-KernelFn pick(KernelKind kind, bool wide) {
+KernelFn pick(KernelKind kind, bool wide, bool direct) {
+    if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
     return wide ? pick_dyn<T, S, true>(kind) : pick_dyn<T, S, false>(kind);
 }
 

@@ -8,10 +8,10 @@
 
 namespace vkfx {
 
-KernelFn pick_f32_fwd(KernelKind kind, bool wide);
-KernelFn pick_f32_inv(KernelKind kind, bool wide);
-KernelFn pick_f64_fwd(KernelKind kind, bool wide);
-KernelFn pick_f64_inv(KernelKind kind, bool wide);
+KernelFn pick_f32_fwd(KernelKind kind, bool wide, bool direct);
+KernelFn pick_f32_inv(KernelKind kind, bool wide, bool direct);
+KernelFn pick_f64_fwd(KernelKind kind, bool wide, bool direct);
+KernelFn pick_f64_inv(KernelKind kind, bool wide, bool direct);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
 const FixedKernel* fixed_table_blue(int* count);
@@ -156,15 +156,16 @@ static bool xcd_groups(KernelKind kind) {
            kind == KK_FS_C_BLUE;
 }
 
-static KernelFn pick_kernel(KernelKind kind, int prec, int dir, bool wide) {
-    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide) : pick_f32_inv(kind, wide))
-                     : (dir < 0 ? pick_f64_fwd(kind, wide) : pick_f64_inv(kind, wide));
+static KernelFn pick_kernel(KernelKind kind, int prec, int dir, int flags) {
+    const bool wide = (flags & KF_DYN_WIDE) != 0, direct = (flags & KF_DYN_DIRECT) != 0;
+    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide, direct) : pick_f32_inv(kind, wide, direct))
+                     : (dir < 0 ? pick_f64_fwd(kind, wide, direct) : pick_f64_inv(kind, wide, direct));
 }
 
 const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed, int flags) {
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1)) return nullptr;
     if (fixed) return (const void*)fixed->fn;
-    return (const void*)pick_kernel(kind, prec, dir, (flags & KF_DYN_WIDE) != 0);
+    return (const void*)pick_kernel(kind, prec, dir, flags);
 }
 
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block, size_t lds_bytes,
@@ -184,7 +185,13 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         return (int)hipErrorInvalidConfiguration;
     if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))
         return (int)hipErrorInvalidConfiguration;
-    KernelFn fn = pick_kernel(kind, prec, dir, (a.flags & KF_DYN_WIDE) != 0);
+    KernelFn fn = pick_kernel(kind, prec, dir, a.flags);
+    // the direct runtime-shape kernel reads and writes contiguous lines of at
+    // least two stages with no radix-2 stage at either end
+    if (!fixed && (a.flags & KF_DYN_DIRECT) &&
+        (kind != KK_PLAIN || a.in_es != 1 || a.out_es != 1 || a.nstages < 2 || a.radix[0] == 2 ||
+         a.radix[a.nstages - 1] == 2))
+        return (int)hipErrorInvalidConfiguration;
     if (fixed) {
         // the fixed shape must be launched with exactly its own geometry
         if (fixed->kind != kind || fixed->prec != prec || fixed->dir != dir || fixed->N != a.N ||

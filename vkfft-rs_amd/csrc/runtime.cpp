@@ -545,6 +545,10 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
     a.nlines = nlines;
     if (!g.fixed && g.wide) a.flags |= KF_DYN_WIDE;
+    // runtime-shape C2C over contiguous lines: HBM-direct first and last stages
+    if (!g.fixed && kind == KK_PLAIN && (a.flags & KF_IN_ROWMAJOR) && (a.flags & KF_OUT_ROWMAJOR) &&
+        a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && a.radix[a.nstages - 1] != 2)
+        a.flags |= KF_DYN_DIRECT;
     int rc = stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
     rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
