@@ -868,6 +868,8 @@ struct Shape {
     static constexpr int N = N_, TT = TT_, G = G_, PS = PS_, LS = LS_;
     static constexpr bool COL = COL_;
     static_assert(LS_ >= N_ + ((N_ - 1) >> PS_), "LDS line stride too small");
+    static_assert((R * ... * 1) == N_, "radices must multiply to the length");
+    static_assert(G_ >= 1 && G_ <= kMaxLinesPerBlock && TT_ >= 1 && G_ * TT_ <= 1024, "block shape");
     using Radices = RList<R...>;
     using Dims = FixDims<N_, G_, LS_, PS_>;
 };
