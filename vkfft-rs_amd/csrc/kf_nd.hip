@@ -20,10 +20,10 @@ static const FixedKernel kTable[] = {
     // f64 512: rows first, columns in the middle or last
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 3, 576, false, true, false, 8, 8, 8),
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 3, 576, false, true, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 30, 513, true, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 30, 513, true, false, false, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 30, 513, true, false, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 30, 513, true, false, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 16, 30, 513, true, false, false, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 16, 30, 513, true, false, false, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 16, 30, 513, true, false, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 16, 30, 513, true, false, true, 8, 8, 8),
 };
 
 const FixedKernel* fixed_table_nd(int* count) {

@@ -22,8 +22,8 @@ static const FixedKernel kTable[] = {
     // f64 512 rows and columns (C4)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 2, 3, 576, false, true, true, 8, 8, 8),
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 2, 3, 576, false, true, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 8, 30, 513, true, true, true, 8, 8, 8),
-    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 8, 30, 513, true, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, -1, 512, 64, 16, 30, 513, true, true, true, 8, 8, 8),
+    VKFX_FIXED_NT(KK_PLAIN, IoPlain, double, 1, 1, 512, 64, 16, 30, 513, true, true, true, 8, 8, 8),
     // 64-point column passes of a split strided axis (4096 = 64 x 64): 32
     // adjacent columns per block, 256-byte row segments
     VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 64, 8, 32, 30, 65, true, true, true, 8, 8),
