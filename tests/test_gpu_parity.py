@@ -61,7 +61,9 @@ def test_hip_round_trip_n4096_batch8(hip_ctx):
 # ------------------------------------------------------- 1-D C2C sweep
 
 SMALL = list(range(1, 65)) + [96, 100, 121, 125, 128, 169, 192, 243, 343, 360, 512, 625, 1000, 1024, 1536,
-                             2048, 2187, 2401, 3125, 4096, 6561, 8192, 10000, 15625, 16384]
+                             2048, 2187, 2401, 3125, 4096, 6561, 8192, 10000, 15625, 16384,
+                             # fixed 3*2^k / 5*2^k family lengths
+                             80, 160, 320, 384, 640, 768, 1280, 2560, 3072, 5120, 6144, 10240, 12288]
 
 
 @pytest.mark.parametrize("prec", [F32, F64])
