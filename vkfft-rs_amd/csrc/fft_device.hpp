@@ -463,6 +463,21 @@ __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int 
     }
 }
 
+// The same with only the first stage reading the line from HBM (`src`); the
+// result stays in LDS for a staged epilogue. The first radix must not be 2.
+template <typename T, int S, bool WIDE>
+__device__ __forceinline__ void run_stages_direct_in(cpx<T>* __restrict__ line, const int N, const int TT,
+                                                     const int t, const int ps, const int nst,
+                                                     const int* __restrict__ radix, const StageTw& tw,
+                                                     const cpx<T>* src) {
+    stage_rt_radix<T, S, WIDE, SM_FIRST>(radix[0], line, N, 1, TT, t, ps, tw, src, nullptr, 0, (T)1);
+    int P = radix[0];
+    for (int s = 1; s < nst; ++s) {
+        stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, src, nullptr, 0, (T)1);
+        P *= radix[s];
+    }
+}
+
 // The same with the first stage reading the line from HBM (`src`) and the
 // last writing it, times `sc`, to HBM (`dst`, skipped when !valid): at least
 // two stages, neither end of radix 2.

@@ -851,6 +851,24 @@ __global__ __launch_bounds__(512) void k_dyn_direct(const KArgs a) {
                                   (const cpx<T>*)a.in + L.ib, (cpx<T>*)a.out + L.ob, L.valid, (T)a.scale);
 }
 
+// Runtime-shape even R2C of one upload (KF_DYN_DIRECT): the first stage loads
+// the real input pairs straight from HBM (contiguous lines), the postprocess
+// stays the staged epilogue of IoR2CHalf.
+template <typename T, int S, bool WIDE>
+__global__ __launch_bounds__(512) void k_dyn_r2c_direct(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
+    __shared__ LineInfo li[kMaxLinesPerBlock];
+    const int tid = threadIdx.x;
+    if (tid < a.G) li[tid] = IoR2CHalf::line(a, group_index(a), tid);
+    __syncthreads();
+    const int g = tid / a.TT, t = tid - g * a.TT;
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
+    run_stages_direct_in<T, S, WIDE>(lds + g * a.LS, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw,
+                                     (const cpx<T>*)a.in + li[g].ib);
+    IoR2CHalf::template epilogue<T, S, DynDims>(a, lds, li);
+}
+
 // -------------------------------------------------- fixed-shape kernel
 
 template <int... R>
@@ -1125,6 +1143,8 @@ KernelFn pick_dyn(KernelKind kind) {
 template <typename T, int S>
 KernelFn pick(KernelKind kind, bool wide, bool direct) {
     if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
+    if (direct && kind == KK_R2C_HALF)
+        return wide ? k_dyn_r2c_direct<T, S, true> : k_dyn_r2c_direct<T, S, false>;
     return wide ? pick_dyn<T, S, true>(kind) : pick_dyn<T, S, false>(kind);
 }
 
