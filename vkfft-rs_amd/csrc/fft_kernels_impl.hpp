@@ -869,6 +869,25 @@ __global__ __launch_bounds__(512) void k_dyn_r2c_direct(const KArgs a) {
     IoR2CHalf::template epilogue<T, S, DynDims>(a, lds, li);
 }
 
+// Runtime-shape even C2R of one upload (KF_DYN_DIRECT): the preprocess (bin k
+// paired with N/2-k) stays the staged prologue of IoC2RHalf, the last stage
+// stores the real output pairs straight to HBM (contiguous lines).
+template <typename T, int S, bool WIDE>
+__global__ __launch_bounds__(512) void k_dyn_c2r_direct(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
+    __shared__ LineInfo li[kMaxLinesPerBlock];
+    const int tid = threadIdx.x;
+    if (tid < a.G) li[tid] = IoC2RHalf::line(a, group_index(a), tid);
+    __syncthreads();
+    IoC2RHalf::template prologue<T, DynDims>(a, lds, li);
+    __syncthreads();
+    const int g = tid / a.TT, t = tid - g * a.TT;
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
+    run_stages_direct_out<T, S, WIDE>(lds + g * a.LS, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw,
+                                      (cpx<T>*)a.out + li[g].ob, li[g].valid, (T)a.scale);
+}
+
 // -------------------------------------------------- fixed-shape kernel
 
 template <int... R>
@@ -1145,6 +1164,8 @@ KernelFn pick(KernelKind kind, bool wide, bool direct) {
     if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
     if (direct && kind == KK_R2C_HALF)
         return wide ? k_dyn_r2c_direct<T, S, true> : k_dyn_r2c_direct<T, S, false>;
+    if (direct && kind == KK_C2R_HALF)
+        return wide ? k_dyn_c2r_direct<T, S, true> : k_dyn_c2r_direct<T, S, false>;
     return wide ? pick_dyn<T, S, true>(kind) : pick_dyn<T, S, false>(kind);
 }
 

@@ -553,6 +553,9 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     if (!g.fixed && kind == KK_R2C_HALF && (a.flags & KF_IN_ROWMAJOR) && a.in_es == 1 && a.nstages >= 1 &&
         a.radix[0] != 2)
         a.flags |= KF_DYN_DIRECT;
+    // runtime-shape even C2R: staged preprocess, HBM-direct last stage
+    if (!g.fixed && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2)
+        a.flags |= KF_DYN_DIRECT;
     int rc = stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
     rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
