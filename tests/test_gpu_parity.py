@@ -230,6 +230,26 @@ def test_r2c_c2r(hip_ctx, n, prec):
     assert o.rel_l2(xr, back) <= TOL[prec] * (1 if prec == F32 else 10)
 
 
+@pytest.mark.parametrize("n", [6, 18, 22, 26, 200, 686, 1000, 3000, 6000, 9000])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_r2c_c2r_runtime_lengths(hip_ctx, n, prec):
+    """Even lengths without a registered shape (runtime-radix kernels whose
+    first R2C stage loads, and last C2R stage stores, HBM directly), over a
+    batch that leaves the last block of lines partly empty."""
+    batch = 37
+    rdt = np.float32 if prec == F32 else np.float64
+    x = o.normal(n * batch, 4000 + n, rdt)
+    X, _ = r2c(hip_ctx, n, batch, x, prec)
+    ref = o.r2c_batch(x.astype(np.float64), n, threads=8)
+    assert o.rel_l2(X, ref) <= TOL[prec] * (1 if prec == F32 else 10)
+    xr, _ = c2r(hip_ctx, n, batch, ref.astype(_cdtype(prec)), prec)
+    back = o.c2r_batch(ref, n, normalize=True, threads=8)
+    assert o.rel_l2(xr, back) <= TOL[prec] * (1 if prec == F32 else 10)
+    # unnormalized C2R of the R2C output returns n * x
+    xu, _ = c2r(hip_ctx, n, batch, X, prec, normalize=False)
+    assert o.rel_l2(xu, n * x.astype(np.float64)) <= TOL[prec] * (1 if prec == F32 else 10)
+
+
 HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 320],
               F64: [64, 128, 160, 192, 256, 320, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096]}
 
