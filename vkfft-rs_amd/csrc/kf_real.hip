@@ -8,9 +8,15 @@ namespace vkfx {
 
 static const FixedKernel kTable[] = {
     // R2C, M = 1024 x 512: 16 columns of 1024 per block, then 16 rows of 512
-    // beside their 16 mirror rows (postprocess fused)
+    // beside their 16 mirror rows (postprocess fused); the planner takes the
+    // 512 x 1024 pair below when both are registered, these serve the C2C
+    // four-step and VKFX_FIXED_PICK comparisons
     VKFX_FIXED_NT(KK_FS_A, IoFsA, float, 0, -1, 1024, 64, 16, 30, 1025, true, false, false, 16, 16, 4),
     VKFX_FIXED_NT(KK_FS_B_R2C, IoFsBR2C, float, 0, -1, 512, 32, 32, 4, 543, false, false, false, 8, 8, 8),
+    // R2C, M = 512 x 1024: 32 columns of 512 per block (256-byte row
+    // segments), then 8 rows of 1024 beside their 8 mirror rows
+    VKFX_SHAPE(KK_FS_A, IoFsA, float, 0, -1, 512, 32, 32, 3, 577, true, false, false, 8, 8, 8),
+    VKFX_SHAPE(KK_FS_B_R2C, IoFsBR2C, float, 0, -1, 1024, 64, 16, 4, 1089, false, false, false, 16, 16, 4),
     // C2R, M = 512 x 1024: 16 columns of 512 beside their 16 mirror columns
     // (preprocess fused), then 16 rows of 1024
     VKFX_FIXED_NT(KK_FS_A_C2R, IoFsAC2RDirect, float, 0, 1, 512, 32, 32, 3, 577, true, false, false, 8, 8, 8),

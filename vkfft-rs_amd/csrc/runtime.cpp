@@ -1430,6 +1430,12 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     }
     size_t n1, n2;
     if (!four_step_split(M, prec, c.lds_max, &n1, &n2)) return plan_real_full_complex(c, n, batch, true, false);
+    // the shorter factor goes to the column pass when both passes have fixed
+    // shapes that way round: more columns per block, wider row segments
+    // (M = 2^19: 32 columns of 512, 256-byte segments, instead of 16 of 1024)
+    if (n1 != n2 && kernel_geometry(KK_FS_A, prec, -1, n2, true, 1, c.lds_max, c.lds_budget).fixed &&
+        kernel_geometry(KK_FS_B_R2C, prec, -1, n1, false, 1, c.lds_max, c.lds_max).fixed)
+        std::swap(n1, n2);
     // the mirror-row pass needs N1 divisible by 2H; H lines + H mirrors per block
     Geometry gb1 = geometry(n2, prec, 1, c.lds_max, c.lds_max);
     int H = prec ? 4 : 8;
