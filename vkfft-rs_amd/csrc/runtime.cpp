@@ -896,8 +896,11 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d, uint32_t omit) {
             split_strided_axis(d.dims[ax], prec, c.lds_budget, &l1, &l2))
             any_split = true;
     }
-    size_t chunk_budget = 128ull << 20;
-    if (const char* e = getenv("VKFX_ND_CHUNK_MB")) chunk_budget = (size_t)atoll(e) << 20;
+    // batch chunks of 128 MB (C3: one 4096^2 f32 image in flight, 2.04 ms per
+    // step against 2.40 ms with 256 MB); slab chunks of 256 MB (C4: 2.32 ms
+    // against 2.40 ms at 128 MB and 2.47-2.54 ms at 384 MB and above)
+    size_t chunk_budget = 128ull << 20, slab_budget = 256ull << 20;
+    if (const char* e = getenv("VKFX_ND_CHUNK_MB")) chunk_budget = slab_budget = (size_t)atoll(e) << 20;
     chunk = std::max<size_t>(1, std::min(d.batch, chunk_budget / std::max<size_t>(per_batch * cs, 1)));
     if (any_split) c.p->work_bytes = std::max(c.p->work_bytes, chunk * per_batch * cs);
     // A volume larger than the chunk budget runs its axes 1.. (which stay
@@ -908,7 +911,7 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d, uint32_t omit) {
     for (uint32_t ax = 1; ax < d.rank; ++ax) slab_axes += active(ax);
     size_t slabs = 0;
     if (chunk == 1 && per_batch * cs > chunk_budget && active(0) && slab_axes >= 2)
-        slabs = std::max<size_t>(1, chunk_budget / (slab * cs));
+        slabs = std::max<size_t>(1, slab_budget / (slab * cs));
     c.js << "\"nd\":{\"chunk\":" << chunk << ",\"slabs_per_chunk\":" << slabs << "},";
 
     // Launches of one axis over `total` elements at byte offset `off`.
