@@ -440,3 +440,28 @@ def test_real_full_complex_lengths(hip_ctx, n, prec):
     c2r = vk.TransformIr.build(cfg2, INV)
     z = hip_ctx.execute_transform(c2r, X)
     assert o.rel_l2(z, x) <= 4 * TOL[prec]
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_length_sweep_sampled_against_numpy(hip_ctx, prec):
+    """Every 7th length through the planner's kernel choice (registered
+    shapes, runtime-radix kernels with HBM-direct stages, Rader, Bluestein,
+    four-step): even R2C/C2R lengths 2..4096 and C2C lengths 1..2048, batch 3,
+    against numpy's float64 FFT (a full sweep of every length passes the same
+    bounds)."""
+    rdt, cdt = (np.float32, np.complex64) if prec == F32 else (np.float64, np.complex128)
+    tol = 2e-5 if prec == F32 else 2e-13
+    rng = np.random.default_rng(11)
+    batch = 3
+    for n in range(2, 4097, 14):
+        x = rng.standard_normal(n * batch).astype(rdt)
+        X, _ = r2c(hip_ctx, n, batch, x, prec)
+        ref = np.fft.rfft(x.astype(np.float64).reshape(batch, n), axis=1).reshape(-1)
+        assert o.rel_l2(X, ref) <= tol, ("r2c", n)
+        xr, _ = c2r(hip_ctx, n, batch, ref.astype(cdt), prec)
+        assert o.rel_l2(xr, x.astype(np.float64)) <= tol, ("c2r", n)
+    for n in range(1, 2049, 7):
+        z = (rng.standard_normal(n * batch) + 1j * rng.standard_normal(n * batch)).astype(cdt)
+        y = c2c(hip_ctx, [n], batch, z, prec)[0]
+        ref = np.fft.fft(z.astype(np.complex128).reshape(batch, n), axis=1).reshape(-1)
+        assert o.rel_l2(y, ref) <= tol, ("c2c", n)
