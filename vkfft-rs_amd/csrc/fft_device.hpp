@@ -478,22 +478,6 @@ __device__ __forceinline__ void run_stages_direct_in(cpx<T>* __restrict__ line, 
     }
 }
 
-// The same with only the last stage writing the line, times `sc`, to HBM
-// (`dst`, skipped when !valid); the line starts in LDS from a staged
-// prologue. The last radix must not be 2.
-template <typename T, int S, bool WIDE>
-__device__ __forceinline__ void run_stages_direct_out(cpx<T>* __restrict__ line, const int N, const int TT,
-                                                      const int t, const int ps, const int nst,
-                                                      const int* __restrict__ radix, const StageTw& tw,
-                                                      cpx<T>* dst, int valid, T sc) {
-    int P = 1;
-    for (int s = 0; s + 1 < nst; ++s) {
-        stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, dst, valid, sc);
-        P *= radix[s];
-    }
-    stage_rt_radix<T, S, WIDE, SM_LAST>(radix[nst - 1], line, N, P, TT, t, ps, tw, nullptr, dst, valid, sc);
-}
-
 // The same with the first stage reading the line from HBM (`src`) and the
 // last writing it, times `sc`, to HBM (`dst`, skipped when !valid): at least
 // two stages, neither end of radix 2.

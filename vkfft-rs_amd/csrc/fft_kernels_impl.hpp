@@ -869,11 +869,108 @@ __global__ __launch_bounds__(512) void k_dyn_r2c_direct(const KArgs a) {
     IoR2CHalf::template epilogue<T, S, DynDims>(a, lds, li);
 }
 
-// Runtime-shape even C2R of one upload (KF_DYN_DIRECT): the preprocess (bin k
-// paired with N/2-k) stays the staged prologue of IoC2RHalf, the last stage
-// stores the real output pairs straight to HBM (contiguous lines).
+// First stage of the runtime-shape even C2R (P = 1), loading its inputs
+// straight from HBM: element e of the half-length line is the preprocessed
+// Z[e] = (X[e] + conj X[N-e]) + i (X[e] - conj X[N-e]) conj(w_e), from bins e
+// and N-e of the N+1-bin input spectrum at `gsrc` (IoC2RHalf::load_tw, w_e
+// from the two-level table of exp(-i pi e / N)). Written to LDS, then a
+// barrier.
+template <typename T, int S, int R, bool WIDE>
+__device__ __noinline__ void stage_c2r_first(cpx<T>* __restrict__ line, const int N, const int TT, const int t,
+                                             const int ps, const cpx<T>* gsrc, const void* rlo, const void* rhi,
+                                             const int rshift) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
+#endif
+    typedef T v2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) v2* gsrc_t;
+    constexpr int MJ = dyn_butterflies_per_thread(R, WIDE);
+    const int NB = N / R;
+    const int mask = (1 << rshift) - 1;
+    cpx<T> v[MJ][R];
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int b = t + j * TT;
+        if (b < NB) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int e = b + i * NB;
+                const v2 x = ((gsrc_t)gsrc)[e];
+                const v2 y = ((gsrc_t)gsrc)[N - e];
+                const cpx<T> X = mk(x.x, x.y), Xm = mk(y.x, -y.y);
+                const cpx<T> w = cmul(ld_table<T>(rhi, e >> rshift), ld_table<T>(rlo, e & mask));
+                v[j][i] = (X + Xm) + muli<1>(cmulc(X - Xm, w));
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MJ; ++j) {
+        const int b = t + j * TT;
+        if (b < NB) {
+            dft<R, S>(v[j]);
+#pragma unroll
+            for (int q = 0; q < R; ++q) line[lpad(b * R + q, ps)] = v[j][q];
+        }
+    }
+    __syncthreads();
+}
+
+template <typename T, int S, bool WIDE>
+__device__ __forceinline__ void stage_c2r_first_radix(int R, cpx<T>* __restrict__ line, const int N, const int TT,
+                                                      const int t, const int ps, const cpx<T>* gsrc,
+                                                      const void* rlo, const void* rhi, const int rshift) {
+#define VKFX_C2R_CASE(RR) \
+    case RR: stage_c2r_first<T, S, RR, WIDE>(line, N, TT, t, ps, gsrc, rlo, rhi, rshift); break;
+    switch (R) {
+        VKFX_C2R_CASE(3)
+        VKFX_C2R_CASE(4)
+        VKFX_C2R_CASE(5)
+        VKFX_C2R_CASE(6)
+        VKFX_C2R_CASE(7)
+        VKFX_C2R_CASE(8)
+        VKFX_C2R_CASE(9)
+        VKFX_C2R_CASE(10)
+        VKFX_C2R_CASE(11)
+        VKFX_C2R_CASE(12)
+        VKFX_C2R_CASE(13)
+        VKFX_C2R_CASE(16)
+        default: break;
+    }
+#undef VKFX_C2R_CASE
+}
+
+// Runtime-shape even C2R of one upload (KF_DYN_DIRECT): the first stage forms
+// the preprocessed line from the input spectrum in HBM, the last stage stores
+// the real output pairs straight to HBM (contiguous lines), so the line passes
+// through LDS only between stages. At least two stages, neither end of radix
+// 2. Lines past the end map onto line 0 (loads in bounds, stores skipped).
 template <typename T, int S, bool WIDE>
 __global__ __launch_bounds__(512) void k_dyn_c2r_direct(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
+    const int tid = threadIdx.x;
+    const int g = tid / a.TT, t = tid - g * a.TT;
+    const LineInfo L = IoC2RHalf::line(a, group_index(a), g);
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
+    cpx<T>* line = lds + g * a.LS;
+    stage_c2r_first_radix<T, S, WIDE>(a.radix[0], line, a.N, a.TT, t, a.PS, (const cpx<T>*)a.in + L.ib, a.rlo,
+                                      a.rhi, a.rshift);
+    int P = a.radix[0];
+    for (int s = 1; s + 1 < a.nstages; ++s) {
+        stage_rt_radix<T, S, WIDE, SM_LDS>(a.radix[s], line, a.N, P, a.TT, t, a.PS, tw, nullptr, nullptr, 0, (T)1);
+        P *= a.radix[s];
+    }
+    stage_rt_radix<T, S, WIDE, SM_LAST>(a.radix[a.nstages - 1], line, a.N, P, a.TT, t, a.PS, tw, nullptr,
+                                        (cpx<T>*)a.out + L.ob, L.valid, (T)a.scale);
+}
+
+// The f32 form of the runtime-shape even C2R (KF_DYN_DIRECT): staged
+// preprocess (IoC2RHalf prologue), last stage stored straight to HBM. (The
+// preprocess-in-registers kernel above measured 8-13% slower than this one
+// for f32 at lengths 256, 2000, 6000 and 12000 and faster at 200, 1000,
+// 3000 and 9000; for f64 it is faster at every measured length.)
+template <typename T, int S, bool WIDE>
+__global__ __launch_bounds__(512) void k_dyn_c2r_direct_out(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
     __shared__ LineInfo li[kMaxLinesPerBlock];
@@ -884,8 +981,14 @@ __global__ __launch_bounds__(512) void k_dyn_c2r_direct(const KArgs a) {
     __syncthreads();
     const int g = tid / a.TT, t = tid - g * a.TT;
     const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
-    run_stages_direct_out<T, S, WIDE>(lds + g * a.LS, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw,
-                                      (cpx<T>*)a.out + li[g].ob, li[g].valid, (T)a.scale);
+    cpx<T>* line = lds + g * a.LS;
+    int P = 1;
+    for (int s = 0; s + 1 < a.nstages; ++s) {
+        stage_rt_radix<T, S, WIDE, SM_LDS>(a.radix[s], line, a.N, P, a.TT, t, a.PS, tw, nullptr, nullptr, 0, (T)1);
+        P *= a.radix[s];
+    }
+    stage_rt_radix<T, S, WIDE, SM_LAST>(a.radix[a.nstages - 1], line, a.N, P, a.TT, t, a.PS, tw, nullptr,
+                                        (cpx<T>*)a.out + li[g].ob, li[g].valid, (T)a.scale);
 }
 
 // -------------------------------------------------- fixed-shape kernel
@@ -1164,8 +1267,12 @@ KernelFn pick(KernelKind kind, bool wide, bool direct) {
     if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
     if (direct && kind == KK_R2C_HALF)
         return wide ? k_dyn_r2c_direct<T, S, true> : k_dyn_r2c_direct<T, S, false>;
-    if (direct && kind == KK_C2R_HALF)
-        return wide ? k_dyn_c2r_direct<T, S, true> : k_dyn_c2r_direct<T, S, false>;
+    if (direct && kind == KK_C2R_HALF) {
+        if constexpr (std::is_same<T, double>::value)
+            return wide ? k_dyn_c2r_direct<T, S, true> : k_dyn_c2r_direct<T, S, false>;
+        else
+            return wide ? k_dyn_c2r_direct_out<T, S, true> : k_dyn_c2r_direct_out<T, S, false>;
+    }
     return wide ? pick_dyn<T, S, true>(kind) : pick_dyn<T, S, false>(kind);
 }
 

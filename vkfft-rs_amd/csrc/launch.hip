@@ -186,13 +186,15 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))
         return (int)hipErrorInvalidConfiguration;
     KernelFn fn = pick_kernel(kind, prec, dir, a.flags);
-    // the direct runtime-shape kernels read (C2C and even R2C) and write (C2C
-    // and even C2R) contiguous lines, with no radix-2 stage at a direct end
+    // the direct runtime-shape kernels read (C2C, even R2C, f64 even C2R) and
+    // write (C2C, even C2R) contiguous lines, with no radix-2 stage at a direct end
     if (!fixed && (a.flags & KF_DYN_DIRECT) &&
         !(kind == KK_PLAIN && a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 &&
           a.radix[a.nstages - 1] != 2) &&
         !(kind == KK_R2C_HALF && a.in_es == 1 && a.nstages >= 1 && a.radix[0] != 2) &&
-        !(kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2))
+        !(kind == KK_C2R_HALF && prec == 0 && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2) &&
+        !(kind == KK_C2R_HALF && prec == 1 && a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 &&
+          a.radix[a.nstages - 1] != 2))
         return (int)hipErrorInvalidConfiguration;
     if (fixed) {
         // the fixed shape must be launched with exactly its own geometry
