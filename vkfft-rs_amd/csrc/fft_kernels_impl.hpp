@@ -964,11 +964,12 @@ __global__ __launch_bounds__(512) void k_dyn_c2r_direct(const KArgs a) {
                                         (cpx<T>*)a.out + L.ob, L.valid, (T)a.scale);
 }
 
-// The f32 form of the runtime-shape even C2R (KF_DYN_DIRECT): staged
-// preprocess (IoC2RHalf prologue), last stage stored straight to HBM. (The
-// preprocess-in-registers kernel above measured 8-13% slower than this one
-// for f32 at lengths 256, 2000, 6000 and 12000 and faster at 200, 1000,
-// 3000 and 9000; for f64 it is faster at every measured length.)
+// Runtime-shape even C2R with KF_DYN_DIRECT but not KF_DYN_PRE: staged
+// preprocess (IoC2RHalf prologue), last stage stored straight to HBM. The
+// host takes it for f32 lines whose first radix is above 4 (there the
+// preprocess-in-registers kernel above measured 8-13% slower; with radix 4
+// first it is 6-14% faster, and in f64 faster at every measured length) and
+// for lines whose first stage cannot load directly.
 template <typename T, int S, bool WIDE>
 __global__ __launch_bounds__(512) void k_dyn_c2r_direct_out(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -1263,16 +1264,14 @@ KernelFn pick_dyn(KernelKind kind) {
     }
 }
 template <typename T, int S>
-KernelFn pick(KernelKind kind, bool wide, bool direct) {
+KernelFn pick(KernelKind kind, bool wide, int direct) {
     if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
     if (direct && kind == KK_R2C_HALF)
         return wide ? k_dyn_r2c_direct<T, S, true> : k_dyn_r2c_direct<T, S, false>;
-    if (direct && kind == KK_C2R_HALF) {
-        if constexpr (std::is_same<T, double>::value)
-            return wide ? k_dyn_c2r_direct<T, S, true> : k_dyn_c2r_direct<T, S, false>;
-        else
-            return wide ? k_dyn_c2r_direct_out<T, S, true> : k_dyn_c2r_direct_out<T, S, false>;
-    }
+    if (direct == 2 && kind == KK_C2R_HALF)
+        return wide ? k_dyn_c2r_direct<T, S, true> : k_dyn_c2r_direct<T, S, false>;
+    if (direct && kind == KK_C2R_HALF)
+        return wide ? k_dyn_c2r_direct_out<T, S, true> : k_dyn_c2r_direct_out<T, S, false>;
     return wide ? pick_dyn<T, S, true>(kind) : pick_dyn<T, S, false>(kind);
 }
 

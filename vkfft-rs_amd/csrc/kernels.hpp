@@ -38,6 +38,7 @@ enum KFlags : int {
     KF_XCD_GROUPS = 8,    // deal line groups to XCDs in contiguous ranges
     KF_DYN_WIDE = 16,     // runtime-shape kernel holding up to 32 elements per thread per stage
     KF_DYN_DIRECT = 32,   // runtime-shape C2C with HBM-direct first and last stages (contiguous lines)
+    KF_DYN_PRE = 64,      // with KF_DYN_DIRECT, even C2R: the first stage forms the preprocess from HBM
 };
 
 // Butterflies per thread in one radix-R stage of the runtime-shape kernel

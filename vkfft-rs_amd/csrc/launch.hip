@@ -8,10 +8,10 @@
 
 namespace vkfx {
 
-KernelFn pick_f32_fwd(KernelKind kind, bool wide, bool direct);
-KernelFn pick_f32_inv(KernelKind kind, bool wide, bool direct);
-KernelFn pick_f64_fwd(KernelKind kind, bool wide, bool direct);
-KernelFn pick_f64_inv(KernelKind kind, bool wide, bool direct);
+KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct);
+KernelFn pick_f32_inv(KernelKind kind, bool wide, int direct);
+KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct);
+KernelFn pick_f64_inv(KernelKind kind, bool wide, int direct);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
 const FixedKernel* fixed_table_blue(int* count);
@@ -157,7 +157,8 @@ static bool xcd_groups(KernelKind kind) {
 }
 
 static KernelFn pick_kernel(KernelKind kind, int prec, int dir, int flags) {
-    const bool wide = (flags & KF_DYN_WIDE) != 0, direct = (flags & KF_DYN_DIRECT) != 0;
+    const bool wide = (flags & KF_DYN_WIDE) != 0;
+    const int direct = (flags & KF_DYN_DIRECT) ? ((flags & KF_DYN_PRE) ? 2 : 1) : 0;
     return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide, direct) : pick_f32_inv(kind, wide, direct))
                      : (dir < 0 ? pick_f64_fwd(kind, wide, direct) : pick_f64_inv(kind, wide, direct));
 }
@@ -186,15 +187,15 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))
         return (int)hipErrorInvalidConfiguration;
     KernelFn fn = pick_kernel(kind, prec, dir, a.flags);
-    // the direct runtime-shape kernels read (C2C, even R2C, f64 even C2R) and
-    // write (C2C, even C2R) contiguous lines, with no radix-2 stage at a direct end
+    // the direct runtime-shape kernels read (C2C, even R2C, even C2R with
+    // KF_DYN_PRE) and write (C2C, even C2R) contiguous lines, with no radix-2
+    // stage at a direct end
     if (!fixed && (a.flags & KF_DYN_DIRECT) &&
         !(kind == KK_PLAIN && a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 &&
           a.radix[a.nstages - 1] != 2) &&
         !(kind == KK_R2C_HALF && a.in_es == 1 && a.nstages >= 1 && a.radix[0] != 2) &&
-        !(kind == KK_C2R_HALF && prec == 0 && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2) &&
-        !(kind == KK_C2R_HALF && prec == 1 && a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 &&
-          a.radix[a.nstages - 1] != 2))
+        !(kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2 &&
+          (!(a.flags & KF_DYN_PRE) || (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2))))
         return (int)hipErrorInvalidConfiguration;
     if (fixed) {
         // the fixed shape must be launched with exactly its own geometry

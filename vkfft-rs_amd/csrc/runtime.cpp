@@ -553,13 +553,17 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     if (!g.fixed && kind == KK_R2C_HALF && (a.flags & KF_IN_ROWMAJOR) && a.in_es == 1 && a.nstages >= 1 &&
         a.radix[0] != 2)
         a.flags |= KF_DYN_DIRECT;
-    // runtime-shape even C2R, HBM-direct last stage. f64: the preprocess is
-    // loaded by the first stage too, whose loads must span at least 128
-    // contiguous bytes per line (shorter lines keep the staged, coalesced
-    // prologue); f32: staged preprocess (faster at half the tested lengths)
-    if (!g.fixed && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2 &&
-        (c.prec == 0 || (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && (g.N / a.radix[0]) * 16 >= 128)))
+    // runtime-shape even C2R, HBM-direct last stage; KF_DYN_PRE: the first
+    // stage also forms the preprocess from HBM, when its loads span at least
+    // 128 contiguous bytes per line, in f64, and in f32 with a first radix of
+    // at most 4 (f32 lines with radix 8 or 16 first measured 8-13% slower
+    // that way, radix-4 ones 6-14% faster; f64 7-29% faster)
+    if (!g.fixed && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2) {
         a.flags |= KF_DYN_DIRECT;
+        if (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && (c.prec == 1 || a.radix[0] <= 4) &&
+            (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128)
+            a.flags |= KF_DYN_PRE;
+    }
     int rc = stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
     rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
