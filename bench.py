@@ -12,8 +12,16 @@ working set between steps.
   cpu_baseline = the oracle (a port of vkfft-rs src/reference.rs) timed on
                this host's cores over a bounded sample of the same workload
 
+The default line also carries `configs`: every BASELINE configuration
+(C1-C5b) timed in the same process (5 steps each after 2 warmups), with its
+effective GB/s, % of 8 TB/s, HBM sweeps per step and the relative L2 error of a
+sampled slice of its timed output against the oracle. `accuracy` is the same
+check for the headline's timed output (plus the sample-11 metrics of
+vkfft-rs src/precision.rs:31-101).
+
 --config selects another benchmark configuration (c2, c3, c4, c5a, c5b) for
-measurement runs; --all prints one line per config.
+measurement runs; --all prints one line per config; --headline-only skips
+the `configs` field.
 """
 from __future__ import annotations
 
@@ -84,7 +92,10 @@ def build_plans(vk, ctx, cfg):
     return [ctx.plan(ir)]
 
 
-def run_gpu(cfg, steps, warmup, rotate):
+def run_gpu(cfg, steps, warmup, rotate, check=None):
+    """Times `steps` steps after `warmup` untimed ones; returns (ms per step,
+    ms per launch of the first plan, info). `check(bufs, pairs, steps)` runs
+    on the timed output before the buffers are released."""
     import torch
 
     torch.cuda.init()  # torch's HIP runtime first: the library then binds to the same one
@@ -99,10 +110,15 @@ def run_gpu(cfg, steps, warmup, rotate):
     in_bytes, out_bytes = plans[0].in_bytes, plans[0].out_bytes
     pairs = max(1, min(rotate, (1 << 30) // max(in_bytes + out_bytes, 1) + 1)) if in_bytes + out_bytes < (1 << 30) else 1
     bufs = []
+    fdt = torch.float32 if cfg["prec"] == "f32" else torch.float64
+    fsz = 4 if cfg["prec"] == "f32" else 8
     for _ in range(pairs):
-        x = torch.rand(in_bytes // 4, device="cuda", generator=gen, dtype=torch.float32) * 2 - 1
-        y = torch.empty(out_bytes // 4, device="cuda", dtype=torch.float32)
-        z = torch.empty(in_bytes // 4, device="cuda", dtype=torch.float32) if len(plans) == 2 else None
+        if cfg["kind"] == "r2c_c2r":  # BASELINE C2: i.i.d. normal(0,1) real samples
+            x = torch.randn(in_bytes // fsz, device="cuda", generator=gen, dtype=fdt)
+        else:                         # uniform[-1,1) re and im
+            x = torch.rand(in_bytes // fsz, device="cuda", generator=gen, dtype=fdt) * 2 - 1
+        y = torch.empty(out_bytes // fsz, device="cuda", dtype=fdt)
+        z = torch.empty(in_bytes // fsz, device="cuda", dtype=fdt) if len(plans) == 2 else None
         bufs.append((x, y, z))
     s = stream.cuda_stream
 
@@ -139,7 +155,13 @@ def run_gpu(cfg, steps, warmup, rotate):
         torch.cuda.synchronize()
         per_launch = [a.elapsed_time(b) for a, b in evs]
     info = {"device": ctx.device_name(), "profile": ctx.device_profile(), "plans": launches, "pairs": pairs}
+    if check is not None:
+        # the last timed step's pair still holds its output (the per-launch
+        # timing above rewrote the same inputs' outputs with the same plan)
+        info["accuracy"] = check(bufs, pairs, steps)
+    del bufs
     ctx.close()
+    torch.cuda.empty_cache()
     return total_ms / steps, sum(per_launch) / len(per_launch), info
 
 
@@ -189,23 +211,111 @@ def copy_bandwidth(nbytes=1 << 30, reps=20):
     return 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
 
 
-def cpu_baseline(cfg, budget_s=15.0):
-    """The oracle (C port of reference.rs, f64) on a bounded sample: the
-    config's own batch, repeated until about budget_s of CPU work is done."""
+def _host(t, complex_=True):
+    import numpy as np
+    a = t.detach().cpu().numpy()
+    if not complex_:
+        return a
+    return a.view(np.complex64 if a.dtype == np.float32 else np.complex128)
+
+
+def _partial_dft_weights(n, k):
+    """exp(-2 pi i (j k mod n) / n) for j < n, with the index product reduced
+    exactly in integers before the float conversion."""
+    import numpy as np
+    j = (np.arange(n, dtype=np.int64) * k) % n
+    return np.exp(-2j * np.pi * j.astype(np.float64) / n)
+
+
+def make_check(cfg, threads):
+    """Checker of a sampled slice of the timed output against the oracle (the
+    C port of vkfft-rs src/reference.rs, f64): relative L2 over the slice."""
     import numpy as np
 
     from oracle import oracle as o
 
-    threads = min(16, os.cpu_count() or 1)
+    dims, kind = cfg["dims"], cfg["kind"]
+    tol = 1e-5 if cfg["prec"] == "f32" else 1e-13
+
+    def check(bufs, pairs, steps):
+        x, y, z = bufs[(steps - 1) % pairs]
+        if kind == "r2c_c2r":
+            n = dims[0]
+            h = n // 2 + 1
+            xr = _host(x[:n], False).astype(np.float64)
+            X = _host(y[: 2 * h])
+            ref = o.r2c_batch(xr, n, threads=threads)
+            back = o.c2r_batch(X.astype(np.complex128), n, normalize=True, threads=threads)
+            zr = _host(z[:n], False)
+            e1, e2 = o.rel_l2(X, ref), o.rel_l2(zr, back)
+            return {"rel_l2": max(e1, e2), "rel_l2_r2c": e1, "rel_l2_c2r": e2, "tolerance": tol,
+                    "sample": "batch 0: R2C vs oracle r2c, C2R (of the GPU spectrum) vs oracle c2r"}
+        if len(dims) == 1:
+            n = dims[0]
+            lines = 16 if n <= 8192 else 2
+            xs = _host(x[: 2 * n * lines]).astype(np.complex128)
+            ys = _host(y[: 2 * n * lines])
+            ref = o.fft_batch(xs, n, threads=threads)
+            out = {"rel_l2": o.rel_l2(ys, ref), "tolerance": tol,
+                   "sample": f"first {lines} of {cfg['batch']} lines vs oracle fft"}
+            out.update(o.precision_metrics(ys, ref))
+            return out
+        # N-D: output planes k0 along the slowest axis of batch 0 equal the
+        # oracle's (rank-1)-D FFT of the direct axis-0 DFT sum of the input
+        n0, rest = dims[0], int(np.prod(dims[1:]))
+        xs = _host(x[: 2 * n0 * rest]).astype(np.complex128).reshape(n0, rest)
+        ys = _host(y[: 2 * n0 * rest]).reshape(n0, rest)
+        ks = [0, 1, n0 // 3, n0 - 1]
+        num = den = 0.0
+        for k in ks:
+            plane = _partial_dft_weights(n0, k) @ xs
+            ref = o.fft_nd(plane, dims[1:], 1, threads=threads) if len(dims) > 2 else o.fft(plane)
+            num += float(np.sum(np.abs(ys[k] - ref) ** 2))
+            den += float(np.sum(np.abs(ref) ** 2))
+        return {"rel_l2": math.sqrt(num / den), "tolerance": tol,
+                "sample": f"batch 0, planes k0={ks} of axis 0: direct axis-0 DFT sum, then the oracle's "
+                          f"{len(dims) - 1}-D FFT"}
+
+    return check
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, budget_s=15.0):
+    """The oracle (C port of reference.rs, f64) on a bounded sample of the
+    config: one thread (the reference is single-threaded) for about 2 s, then
+    batch-parallel on this GPU's share of the host cores for about budget_s
+    of CPU work."""
+    import numpy as np
+
+    from oracle import oracle as o
+
+    nproc = os.cpu_count() or 1
+    threads = min(16, nproc)  # one GPU's share of the box's cores
     n = 1
     for d in cfg["dims"]:
         n *= d
     if len(cfg["dims"]) > 1 or cfg["kind"] != "c2c":
         return None
-    x1 = o.complex_uniform(n, 1, np.complex128)
-    t0 = time.perf_counter()
-    o.fft(x1)
-    per = max(time.perf_counter() - t0, 1e-6)          # CPU seconds per transform
+    es = 8 if cfg["prec"] == "f32" else 16
+    x1 = o.complex_uniform(n * 64, 1, np.complex128)
+    o.fft_batch(x1[:n], n)
+    # single thread
+    done1, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 2.0:
+        o.fft_batch(x1, n, threads=1)
+        done1 += 64
+    wall1 = time.perf_counter() - t0
+    per = wall1 / done1
+    # all of this GPU's share of the cores
     batch = min(cfg["batch"], max(threads, int(budget_s / per)))
     reps = max(1, int(round(budget_s / (per * batch))))
     x = o.complex_uniform(n * batch, 2, np.complex128)
@@ -214,11 +324,54 @@ def cpu_baseline(cfg, budget_s=15.0):
         o.fft_batch(x, n, threads=threads)
     wall = time.perf_counter() - t0
     done = batch * reps
-    bytes_done = 2 * n * done * (8 if cfg["prec"] == "f32" else 16)
+    bytes_done = 2 * n * done * es
     return {"value": round(bytes_done / wall / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} x {batch} transforms of N={n} (of batch {cfg['batch']}) through the oracle "
-                      f"(C port of reference.rs, f64), {wall:.2f} s wall on {threads} threads, "
-                      f"~{per * done:.1f} s CPU work"}
+            "host_nproc": nproc, "cpu_model": _cpu_model(),
+            "single_thread": {"us_per_transform": round(per * 1e6, 2),
+                              "value": round(2 * n * es / per / 1e9, 4), "unit": "GB/s",
+                              "transforms": done1},
+            "all_cores_us_per_transform": round(wall / done * 1e6, 3),
+            "sample": f"1 thread: {done1} transforms of N={n} in {wall1:.2f} s; {threads} threads: {reps} x {batch} "
+                      f"transforms (of batch {cfg['batch']}) in {wall:.2f} s wall, ~{per * done:.1f} s CPU work; "
+                      f"the oracle (C port of reference.rs, f64)"}
+
+
+def hbm_sweeps(info, cfg):
+    """HBM sweeps of one step: the data the plan's FFT passes read and write,
+    over one read + write of the step's logical data. A pass over L lines of
+    length F counts L * F; a Bluestein pass reads or writes the logical N on
+    the side that faces the caller and M on the workspace side (N + M over
+    two). A single-pass transform counts 1.0."""
+    n = 1
+    for d in cfg["dims"]:
+        n *= d
+    if cfg["kind"] == "r2c_c2r":
+        logical = n // 2 * cfg["batch"] * 2          # half-length complex lines, both directions
+    else:
+        logical = n * cfg["batch"] * len(info["plans"])
+    moved = 0.0
+    for plan in info["plans"]:
+        for p in plan.get("passes", []):
+            if "lines" not in p or "fft_len" not in p:
+                continue
+            lines, m, k = p["lines"], p["fft_len"], p["kernel"]
+            if k == "bluestein_single":
+                moved += lines * n
+            elif k in ("bluestein_columns", "bluestein_columns_out"):
+                # a column pass over the chunk's M-point lines: the caller-facing
+                # side holds N of every M points
+                moved += lines * m * 0.5 * (1 + n / _plan_m(plan))
+            else:
+                moved += lines * m
+    return round(moved / logical, 3) if logical else None
+
+
+def _plan_m(plan):
+    """Bluestein convolution length of a 1-D plan (its axes entry)."""
+    for ax in plan.get("axes", []):
+        if ax.get("convolution_len"):
+            return ax["convolution_len"]
+    return 1
 
 
 COPY_BYTES = 1 << 30  # plain_copy_bandwidth(): 1 GiB read + 1 GiB written per launch
@@ -294,6 +447,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="one line per benchmark configuration")
     ap.add_argument("--rotate", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true", help="skip the oracle check of the timed output")
+    ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch (tuning runs)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
                     help="print a markdown summary of rocprofv3 CSV output directories and exit")
@@ -305,15 +460,18 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path.",
               file=sys.stderr)
         sys.exit(2)
+    threads = min(16, os.cpu_count() or 1)
     names = list(CONFIGS) if args.all else [args.config]
     copy_gbs = plain_gbs = None
+    lines_out = []
     for name in names:
         cfg = dict(CONFIGS[name])
         if args.batch:
             cfg["batch"] = args.batch
             cfg["workload"] += f"_batch_override_{args.batch}"
         steps = args.steps if name == "c1" else max(5, min(args.steps, 30))
-        ms, launch_ms, info = run_gpu(cfg, steps, args.warmup, args.rotate)
+        ms, launch_ms, info = run_gpu(cfg, steps, args.warmup, args.rotate,
+                                      check=None if args.no_check else make_check(cfg, threads))
         if copy_gbs is None:
             copy_gbs = copy_bandwidth()
             plain_gbs = plain_copy_bandwidth()
@@ -331,7 +489,9 @@ def main():
             "metric": METRICS[name],
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32" if cfg["prec"] == "f32" else "f64", "data": "synthetic uniform[-1,1) (torch, seeded)",
+            "dtype": "f32" if cfg["prec"] == "f32" else "f64",
+            "data": "synthetic, torch-seeded: " + ("normal(0,1) reals" if cfg["kind"] == "r2c_c2r"
+                                                   else "uniform[-1,1) re/im"),
             "config": {"workload": cfg["workload"], "dims": cfg["dims"], "batch": cfg["batch"],
                        "buffer_pairs": info["pairs"]},
             "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
@@ -339,10 +499,38 @@ def main():
             "hbm_plain_copy_gbs": round(plain_gbs, 1),
             "pct_of_copy": round(100 * value / copy_gbs, 2),
             "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
+            "hbm_sweeps": hbm_sweeps(info, cfg),
+            "accuracy": info.get("accuracy"),
             "roofline": roof,
-            "cpu_baseline": None if (args.no_cpu or name != "c1") else cpu_baseline(cfg),
+            "cpu_baseline": None,
             "device": info["device"],
         }
+        lines_out.append((name, out))
+    if not args.all and args.config == "c1" and not args.headline_only:
+        # every BASELINE configuration beside the headline, same process
+        table = {}
+        for name in CONFIGS:
+            if name == "c1":
+                continue
+            cfg = dict(CONFIGS[name])
+            ms, _, info = run_gpu(cfg, 5, 2, args.rotate,
+                                  check=None if args.no_check else make_check(cfg, threads))
+            nbytes, flops = algorithmic(cfg)
+            v = nbytes / (ms * 1e-3) / 1e9
+            table[name] = {"workload": cfg["workload"], "ms_per_step": round(ms, 5), "value": round(v, 2),
+                           "unit": "GB/s", "pct_of_peak": round(100 * v / PEAK_HBM_GBS, 2),
+                           "gflops": round(flops / (ms * 1e-3) / 1e9, 1), "steps": 5, "warmup": 2,
+                           "hbm_sweeps": hbm_sweeps(info, cfg),
+                           "rel_l2": (info.get("accuracy") or {}).get("rel_l2"),
+                           "accuracy_sample": (info.get("accuracy") or {}).get("sample")}
+            print(f"# {name}: {table[name]['ms_per_step']} ms, {table[name]['value']} GB/s", file=sys.stderr,
+                  flush=True)
+        lines_out[0][1]["configs"] = table
+    if not args.no_cpu:
+        for name, out in lines_out:
+            if name == "c1":
+                out["cpu_baseline"] = cpu_baseline(CONFIGS["c1"])
+    for _, out in lines_out:
         print(json.dumps(out), flush=True)
 
 

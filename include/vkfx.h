@@ -184,7 +184,12 @@ int vkfx_context_profile(const vkfx_context *ctx, vkfx_device_profile *out);
  * 2109-2195): builds the kernel-launch list, uploads twiddle/chirp/spectrum
  * tables and allocates the plan's workspace once. */
 int vkfx_plan_create(vkfx_context *ctx, const vkfx_plan_desc *desc, vkfx_plan **out);
-/* Destroy every plan before the context it was created on. */
+/* Destroy every ticket of a plan before the plan, and every plan before the
+ * context it was created on: vkfx_plan_destroy fails (VKFX_ERR_NATIVE_RUNTIME)
+ * while tickets of the plan are alive, and vkfx_context_destroy fails while
+ * plans or tickets of the context are alive (HipExecutionContext owns its
+ * pools and streams, src/backend/hip/runtime.rs:1643-1656; tickets borrow it,
+ * native_runtime.rs:406-451). */
 int vkfx_plan_destroy(vkfx_plan *plan);
 
 /* Resources of one distinct pass of a plan (NativeRuntime::
@@ -211,6 +216,16 @@ int vkfx_plan_resources(const vkfx_plan *plan, vkfx_pass_resources *out, uint32_
  * a caller may pass to vkfx_execute (0 when the plan needs none). */
 int vkfx_plan_io_bytes(const vkfx_plan *plan, uint64_t *in_bytes, uint64_t *out_bytes);
 int vkfx_plan_workspace_bytes(const vkfx_plan *plan, uint64_t *out);
+
+/* Output kind of a plan for the async binding. NativeProgramTicket32/64::wait
+ * returns Vec<Complex32/64> for every TransformIr, and
+ * finish_transform_output32/64 (src/backend/native_runtime.rs:2045-2087)
+ * takes `.re` of it for C2R and DCT/DST. *real_output = 1 when the plan's
+ * output holds reals (C2R, DCT/DST, real-application convolution);
+ * *widened_bytes is the size of the output with every real v widened to the
+ * pair {v, 0} of the storage scalar (= the output bytes for complex outputs).
+ * Either pointer may be NULL. */
+int vkfx_plan_output_info(const vkfx_plan *plan, int32_t *real_output, uint64_t *widened_bytes);
 
 /* Writes a JSON description of the plan (axes, algorithms, Bluestein M,
  * four-step splits, kernel passes with grid/block/LDS) into buf. Returns the
@@ -258,6 +273,13 @@ int vkfx_ticket_ready(const vkfx_ticket *ticket, int32_t *ready);
  * h_out (out_bytes must equal the plan's output bytes). The ticket stays
  * valid (wait may be repeated) until destroyed. */
 int vkfx_ticket_wait(vkfx_ticket *ticket, void *h_out, uint64_t out_bytes);
+
+/* NativeProgramTicket32/64::wait for the Rust binding
+ * (src/backend/native_runtime.rs:372-401, 2045-2087): as vkfx_ticket_wait,
+ * but a real-output plan's values are written as {v, 0} pairs of the storage
+ * scalar, so out_bytes must equal vkfx_plan_output_info's widened_bytes. For
+ * complex-output plans this is vkfx_ticket_wait. */
+int vkfx_ticket_wait_complex(vkfx_ticket *ticket, void *h_out, uint64_t out_bytes);
 
 /* Drop of a ticket (src/backend/hip/runtime.rs:1610-1619): synchronises if
  * the work is still running, then returns its buffers and stream to the

@@ -55,3 +55,22 @@ def test_null_arguments_are_rejected():
     assert b"null" in lib.vkfx_last_error()
     out = ctypes.c_uint64()
     assert lib.vkfx_planner_bluestein_padding(1, 1, 0, 0, ctypes.byref(out)) == -7
+
+
+def test_integration_rust_extern_block_declares_every_symbol():
+    """The Rust binding shown in INTEGRATION.md declares every function of
+    include/vkfx.h, so a maintainer copying it has the whole ABI."""
+    import re
+    text = open(os.path.join(os.path.dirname(vk.HEADER_PATH), "..", "INTEGRATION.md")).read()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    declared = set(re.findall(r"pub fn (vkfx_[a-z_0-9]+)\(", block))
+    assert declared == set(vk.header_symbols())
+
+
+def test_lifetime_guards_without_gpu():
+    lib = vk.lib()
+    assert lib.vkfx_plan_destroy(None) == 0
+    assert lib.vkfx_context_destroy(None) == 0
+    assert lib.vkfx_plan_output_info(None, None, None) == -7
+    assert lib.vkfx_ticket_wait_complex(None, None, 0) == -7

@@ -182,3 +182,89 @@ def test_pass_resource_reports(hip_ctx):
                                  .with_precision(vk.Precision.F64ComputeF32Storage), FWD)
     names = [p["pass"] for p in hip_ctx.plan(mixed).resources()]
     assert names[0] == "boundary_in" and names[-1] == "boundary_out"
+
+
+def _shim_ticket_wait(ctx, ir, x):
+    """What the Rust shim's Mi355xTicket32/64 does: submit the
+    plan's input bytes, size the wait buffer from vkfx_plan_output_info's
+    widened bytes as Complex32/64 elements, wait with exactly that byte count
+    and hand the complex vector on (finish_transform_output32/64 then takes
+    `.re` for real outputs, native_runtime.rs:2045-2087)."""
+    import ctypes
+    L = ctx._L
+    plan = ctx.plan(ir)
+    xs = np.ascontiguousarray(x)
+    assert xs.nbytes == plan.in_bytes
+    real = ctypes.c_int32()
+    widened = ctypes.c_uint64()
+    vk._check(L.vkfx_plan_output_info(plan.handle, ctypes.byref(real), ctypes.byref(widened)), L)
+    cdt = np.complex64 if ir.config.precision == F32 else np.complex128
+    out_len = int(widened.value) // np.dtype(cdt).itemsize  # Vec<Complex32>::len
+    t = ctypes.c_void_p()
+    vk._check(L.vkfx_submit_host(plan.handle, xs.ctypes.data, xs.nbytes, ctypes.byref(t)), L)
+    try:
+        # the size the round-1 shim passed (out_len * 8 of a real output) is refused
+        if real.value:
+            bad = np.empty(plan.out_bytes // np.dtype(cdt).itemsize // 2 + 1, dtype=cdt)
+            rc = L.vkfx_ticket_wait_complex(t, bad.ctypes.data, bad.nbytes)
+            assert rc == -5
+        out = np.empty(out_len, dtype=cdt)
+        vk._check(L.vkfx_ticket_wait_complex(t, out.ctypes.data, out_len * np.dtype(cdt).itemsize), L)
+    finally:
+        vk._check(L.vkfx_ticket_destroy(t), L)
+    return bool(real.value), out
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_shim_real_output_tickets(hip_ctx, prec):
+    rd = np.float32 if prec == F32 else np.float64
+    tol = 1e-5 if prec == F32 else 1e-12
+    # C2R: widened to {v, 0}; .re is the oracle's C2R
+    n, batch = 4096, 3
+    x = o.normal(n * batch, 31, rd)
+    r2c = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec)
+                               .with_transform(vk.TransformKind.RealToComplex), FWD)
+    c2r = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec)
+                               .with_transform(vk.TransformKind.ComplexToReal), INV)
+    real, X = _shim_ticket_wait(hip_ctx, r2c, x)
+    assert not real and X.size == batch * (n // 2 + 1)
+    assert o.rel_l2(X, o.r2c_batch(x.astype(np.float64), n, threads=8)) <= tol
+    real, y = _shim_ticket_wait(hip_ctx, c2r, X)
+    assert real and y.size == n * batch
+    assert np.all(y.imag == 0)
+    ref = o.c2r_batch(X.astype(np.complex128), n, threads=8)
+    assert o.rel_l2(y.real, ref) <= tol
+    assert np.array_equal(y.real, hip_ctx.execute_transform(c2r, X))
+    # DCT-II: real in, real out, widened the same way
+    m, mb = 256, 8
+    xr = o.uniform(m * mb, 32, rd)
+    dct = vk.TransformIr.build(vk.FftConfig.new([m]).with_batch_count(mb).with_precision(prec)
+                               .with_transform(vk.TransformKind.dct(2)), FWD)
+    real, z = _shim_ticket_wait(hip_ctx, dct, xr)
+    assert real and z.size == m * mb and np.all(z.imag == 0)
+    assert o.rel_l2(z.real, o.r2r_batch(xr.astype(np.float64), m, "dct2", threads=8)) <= tol
+
+
+def test_context_close_releases_tickets_and_plans():
+    """Closing a context with a live ticket destroys the ticket and its plan
+    first; the ticket then refuses to wait instead of reading freed memory.
+    The C ABI refuses to destroy a plan with live tickets or a context with
+    live plans."""
+    import ctypes
+    import os
+    if not os.path.exists("/dev/kfd"):
+        pytest.skip("no GPU in this container")
+    ctx = vk.HipExecutionContext(0)
+    ir = c2c_ir([1024], 8)
+    x = o.complex_uniform(1024 * 8, 33, np.complex64)
+    t = ctx.submit_transform_async(ir, x)
+    L = ctx._L
+    plan = ctx.plan(ir)
+    assert L.vkfx_plan_destroy(plan.handle) == -2       # its ticket is alive
+    assert L.vkfx_context_destroy(ctx.handle) == -2     # plans and tickets are alive
+    ctx.close()
+    assert not ctx.handle and not plan.handle
+    with pytest.raises(vk.VkFftError):
+        t.wait()
+    with pytest.raises(vk.VkFftError):
+        t.ready()

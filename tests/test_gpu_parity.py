@@ -230,7 +230,7 @@ def test_r2c_c2r(hip_ctx, n, prec):
     assert o.rel_l2(xr, back) <= TOL[prec] * (1 if prec == F32 else 10)
 
 
-@pytest.mark.parametrize("n", [6, 18, 22, 26, 200, 686, 1000, 3000, 6000, 9000])
+@pytest.mark.parametrize("n", [6, 18, 22, 26, 200, 210, 686, 1000, 3000, 6000, 9000, 18018])
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_r2c_c2r_runtime_lengths(hip_ctx, n, prec):
     """Even lengths without a registered shape (runtime-radix kernels whose
@@ -248,6 +248,31 @@ def test_r2c_c2r_runtime_lengths(hip_ctx, n, prec):
     # unnormalized C2R of the R2C output returns n * x
     xu, _ = c2r(hip_ctx, n, batch, X, prec, normalize=False)
     assert o.rel_l2(xu, n * x.astype(np.float64)) <= TOL[prec] * (1 if prec == F32 else 10)
+
+
+def test_c2r_runtime_variants_covered(hip_ctx):
+    """The host rule for the runtime-shape C2R half-length kernels: HBM-direct
+    last stage always; the first stage forms the preprocess from HBM in f64,
+    and in f32 only when the first radix is 4 (n=210, radix 3 first, keeps the
+    staged preprocess). n=18018 (M=9009) needs the wide geometry. Each case
+    named here also runs in test_r2c_c2r_runtime_lengths."""
+    def c2r_launch(n, prec):
+        cfg = vk.FftConfig.new([n]).with_batch_count(37).with_precision(prec) \
+            .with_transform(vk.TransformKind.ComplexToReal).with_inverse_normalization(True)
+        plan = hip_ctx.plan(vk.TransformIr.build(cfg, INV))
+        ls = [L for L in plan.describe()["passes"] if "runtime_variant" in L and not L["fixed_shape"]]
+        assert len(ls) == 1, plan.describe()
+        return ls[0]
+    L = c2r_launch(210, F32)
+    assert L["radices"][0] == 3 and L["runtime_variant"]["hbm_direct"]
+    assert not L["runtime_variant"]["direct_preprocess"]
+    L = c2r_launch(210, F64)
+    assert L["radices"][0] == 3 and L["runtime_variant"]["direct_preprocess"]
+    L = c2r_launch(18018, F32)
+    assert L["runtime_variant"]["wide"] and L["runtime_variant"]["hbm_direct"]
+    assert not L["runtime_variant"]["direct_preprocess"]
+    L = c2r_launch(1000, F32)
+    assert L["radices"][0] == 4 and L["runtime_variant"]["direct_preprocess"]
 
 
 HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 320],

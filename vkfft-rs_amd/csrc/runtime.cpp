@@ -76,8 +76,9 @@ struct vkfx_context {
     vkfx_device_profile profile{};
     std::vector<PoolBuf> dev_pool, host_pool;  // free buffers
     std::vector<hipStream_t> stream_pool;      // free streams for tickets
-    std::mutex mu;                             // guards the pools and `active`
+    std::mutex mu;                             // guards the pools, `active` and `plans`
     int active = 0;                            // tickets submitted and not yet destroyed
+    int plans = 0;                             // plans created and not yet destroyed
 };
 
 namespace {
@@ -252,11 +253,18 @@ struct vkfx_plan {
     size_t conv_a_off = 0, conv_a_bytes = 0, conv_b_off = 0, conv_b_bytes = 0;  // SEL_CONV_A / SEL_CONV_B
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     size_t in_bytes = 0, out_bytes = 0;
+    bool real_out = false;    // output holds reals (C2R, DCT/DST, real-application convolution)
+    int tickets = 0;          // live tickets of this plan (guarded by ctx->mu)
     std::string json;
     DevBuf host_in, host_out;  // staging for vkfx_execute_host
 };
 
 namespace {
+
+// Bytes of one scalar of the caller-visible storage type.
+size_t storage_scalar_bytes(int32_t precision) {
+    return precision == VKFX_F64 ? 8 : precision == VKFX_F16_STORAGE_F32_COMPUTE ? 2 : 4;
+}
 
 // Dynamic LDS a plan may give one block: the device limit minus the kernels'
 // static per-line bookkeeping (kMaxLinesPerBlock LineInfo records).
@@ -529,6 +537,9 @@ void note_pass(Ctx& c, const Launch& L) {
          << ",\"lds_bytes\":" << L.lds << ",\"fixed_shape\":" << (L.fixed ? "true" : "false")
          << ",\"nontemporal\":[" << (L.fixed && L.fixed->nti ? "true" : "false") << ","
          << (L.fixed && L.fixed->nto ? "true" : "false") << "]"
+         << ",\"runtime_variant\":{\"wide\":" << ((L.a.flags & KF_DYN_WIDE) ? "true" : "false")
+         << ",\"hbm_direct\":" << ((L.a.flags & KF_DYN_DIRECT) ? "true" : "false")
+         << ",\"direct_preprocess\":" << ((L.a.flags & KF_DYN_PRE) ? "true" : "false") << "}"
          << ",\"radices\":[";
     for (int i = 0; i < L.a.nstages; ++i) c.js << (i ? "," : "") << L.a.radix[i];
     c.js << "]}";
@@ -556,11 +567,12 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     // runtime-shape even C2R, HBM-direct last stage; KF_DYN_PRE: the first
     // stage also forms the preprocess from HBM, when its loads span at least
     // 128 contiguous bytes per line, in f64, and in f32 with a first radix of
-    // at most 4 (f32 lines with radix 8 or 16 first measured 8-13% slower
-    // that way, radix-4 ones 6-14% faster; f64 7-29% faster)
+    // exactly 4 (f32 lines with radix 8 or 16 first measured 8-13% slower
+    // that way, radix-4 ones 6-14% faster; f64 7-29% faster; radix 3, 5, 7
+    // first were not measured in f32 and keep the staged preprocess)
     if (!g.fixed && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2) {
         a.flags |= KF_DYN_DIRECT;
-        if (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && (c.prec == 1 || a.radix[0] <= 4) &&
+        if (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && (c.prec == 1 || a.radix[0] == 4) &&
             (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128)
             a.flags |= KF_DYN_PRE;
     }
@@ -1452,13 +1464,15 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
         kernel_geometry(KK_FS_B_R2C, prec, -1, n1, false, 1, c.lds_max, c.lds_max).fixed)
         std::swap(n1, n2);
     // the mirror-row pass needs N1 divisible by 2H; H lines + H mirrors per block
+    if (n1 % 2 != 0 && n2 % 2 == 0) std::swap(n1, n2);
+    // both factors odd (M odd, e.g. 9009): the full-length complex plan
+    if (n1 % 2 != 0) return plan_real_full_complex(c, n, batch, true, false);
     Geometry gb1 = geometry(n2, prec, 1, c.lds_max, c.lds_max);
     int H = prec ? 4 : 8;
     while (H > 1 && (n1 % (2 * H) != 0)) H /= 2;
-    if (n1 % (2 * H) != 0) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "R2C four-step rows must be even");
     Geometry gb = kernel_geometry(KK_FS_B_R2C, prec, -1, n2, false, 2 * H, c.lds_max, c.lds_max);
     if (gb.fixed && n1 % gb.G == 0) H = gb.G / 2;
-    if (!gb1.ok || gb.G != 2 * H) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "R2C four-step row geometry");
+    if (!gb1.ok || gb.G != 2 * H) return plan_real_full_complex(c, n, batch, true, false);
     Geometry ga = kernel_geometry(KK_FS_A, prec, -1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
     const void *tlo, *thi;
     int tsh;
@@ -1540,7 +1554,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
         std::swap(n1, n2);
     Geometry ga = kernel_geometry(KK_FS_A_C2R, prec, 1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
     Geometry gb = kernel_geometry(KK_FS_B, prec, 1, n2, false, prec ? 8 : 16, c.lds_max, c.lds_budget);
-    if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "C2R four-step geometry");
+    if (!ga.ok || !gb.ok) return plan_real_full_complex(c, n, batch, false, normalize);
     // columns beside their mirrors in one block when the groups tile N2 evenly
     const bool pairs = ga.G % 2 == 0 && n2 % 2 == 0 && n2 % (size_t)ga.G == 0;
     const void *tlo, *thi;
@@ -1641,6 +1655,13 @@ int vkfx_context_create(int device_index, vkfx_context** out) {
 
 int vkfx_context_destroy(vkfx_context* ctx) {
     if (!ctx) return VKFX_OK;
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        if (ctx->active || ctx->plans)
+            return fail(VKFX_ERR_NATIVE_RUNTIME, "cannot destroy a context with " + std::to_string(ctx->plans) +
+                                                     " live plan(s) and " + std::to_string(ctx->active) +
+                                                     " live ticket(s); destroy them first");
+    }
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamSynchronize(ctx->aux);
@@ -1911,6 +1932,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         // compute-type copies in the workspace that the FFT passes use.
         const bool real_in = d.transform == VKFX_R2C || r2r,
                    real_out = d.transform == VKFX_C2R || r2r || conv_real;
+        p->real_out = real_out;
         const size_t rank = d.rank;
         long long in_dims[VKFX_MAX_RANK], out_dims[VKFX_MAX_RANK];
         for (size_t i = 0; i < rank; ++i) in_dims[i] = out_dims[i] = (long long)d.dims[i];
@@ -2087,12 +2109,23 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         }
         p->work.bytes = p->work_bytes;
     }
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        ++ctx->plans;
+    }
     *out = p;
     return VKFX_OK;
 }
 
 int vkfx_plan_destroy(vkfx_plan* plan) {
     if (!plan) return VKFX_OK;
+    {
+        std::lock_guard<std::mutex> lock(plan->ctx->mu);
+        if (plan->tickets)
+            return fail(VKFX_ERR_NATIVE_RUNTIME, "cannot destroy a plan while " + std::to_string(plan->tickets) +
+                                                     " of its ticket(s) are alive; destroy them first");
+        --plan->ctx->plans;
+    }
     (void)hipSetDevice(plan->ctx->device);
     (void)hipStreamSynchronize(plan->ctx->stream);
     (void)hipStreamSynchronize(plan->ctx->aux);
@@ -2155,6 +2188,13 @@ int vkfx_plan_resources(const vkfx_plan* plan, vkfx_pass_resources* out, uint32_
         ++n;
     }
     *count = n;
+    return VKFX_OK;
+}
+
+int vkfx_plan_output_info(const vkfx_plan* plan, int32_t* real_output, uint64_t* widened_bytes) {
+    if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
+    if (real_output) *real_output = plan->real_out ? 1 : 0;
+    if (widened_bytes) *widened_bytes = plan->real_out ? 2 * plan->out_bytes : plan->out_bytes;
     return VKFX_OK;
 }
 
@@ -2426,6 +2466,10 @@ int chain_run(vkfx_plan* const* plans, uint32_t count, const void* d_in, void* d
 
 struct vkfx_ticket {
     vkfx_plan* plan = nullptr;
+    vkfx_context* ctx = nullptr;
+    size_t out_bytes = 0;   // the plan's output bytes, copied at submit
+    bool real_out = false;  // the plan's output holds reals
+    size_t scalar_bytes = 0;
     hipStream_t stream = nullptr;
     hipEvent_t done = nullptr;
     PoolBuf d_in, d_out, d_work, h_in, h_out;
@@ -2441,6 +2485,10 @@ int vkfx_submit_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, vkfx_
     (void)hipSetDevice(ctx->device);
     auto* t = new vkfx_ticket();
     t->plan = plan;
+    t->ctx = ctx;
+    t->out_bytes = plan->out_bytes;
+    t->real_out = plan->real_out;
+    t->scalar_bytes = storage_scalar_bytes(plan->desc.precision);
     auto cleanup = [&](int rc) {
         if (t->stream) (void)hipStreamSynchronize(t->stream);
         pool_give(ctx, false, t->d_in, nullptr);
@@ -2493,6 +2541,7 @@ int vkfx_submit_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, vkfx_
     {
         std::lock_guard<std::mutex> lock(ctx->mu);
         ++ctx->active;
+        ++plan->tickets;
     }
     *out = t;
     return VKFX_OK;
@@ -2514,8 +2563,8 @@ int vkfx_ticket_ready(const vkfx_ticket* t, int32_t* ready) {
 
 int vkfx_ticket_wait(vkfx_ticket* t, void* h_out, uint64_t out_bytes) {
     if (!t || !h_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
-    if (out_bytes != t->plan->out_bytes)
-        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "output buffer: expected " + std::to_string(t->plan->out_bytes) +
+    if (out_bytes != t->out_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "output buffer: expected " + std::to_string(t->out_bytes) +
                                                         " bytes, got " + std::to_string(out_bytes));
     hipError_t e = hipEventSynchronize(t->done);
     if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
@@ -2523,9 +2572,29 @@ int vkfx_ticket_wait(vkfx_ticket* t, void* h_out, uint64_t out_bytes) {
     return VKFX_OK;
 }
 
+int vkfx_ticket_wait_complex(vkfx_ticket* t, void* h_out, uint64_t out_bytes) {
+    if (!t || !h_out) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    if (!t->real_out) return vkfx_ticket_wait(t, h_out, out_bytes);
+    if (out_bytes != 2 * t->out_bytes)
+        return fail(VKFX_ERR_INPUT_LENGTH_MISMATCH, "complex-widened output buffer: expected " +
+                                                        std::to_string(2 * t->out_bytes) + " bytes, got " +
+                                                        std::to_string(out_bytes));
+    hipError_t e = hipEventSynchronize(t->done);
+    if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    // {v, 0} per real value, in the storage scalar type
+    const size_t sb = t->scalar_bytes, n = t->out_bytes / sb;
+    const unsigned char* src = (const unsigned char*)t->h_out.p;
+    unsigned char* dst = (unsigned char*)h_out;
+    for (size_t i = 0; i < n; ++i) {
+        std::memcpy(dst + 2 * i * sb, src + i * sb, sb);
+        std::memset(dst + (2 * i + 1) * sb, 0, sb);
+    }
+    return VKFX_OK;
+}
+
 int vkfx_ticket_destroy(vkfx_ticket* t) {
     if (!t) return VKFX_OK;
-    vkfx_context* ctx = t->plan->ctx;
+    vkfx_context* ctx = t->ctx;
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(t->stream);
     pool_give(ctx, false, t->d_in, nullptr);
@@ -2537,6 +2606,7 @@ int vkfx_ticket_destroy(vkfx_ticket* t) {
         std::lock_guard<std::mutex> lock(ctx->mu);
         ctx->stream_pool.push_back(t->stream);
         --ctx->active;
+        --t->plan->tickets;
     }
     (void)hipEventDestroy(t->done);
     delete t;

@@ -219,6 +219,8 @@ def lib(path: Optional[str] = None):
         L.vkfx_submit_host.argtypes = [vp, vp, u64, ctypes.POINTER(vp)]
         L.vkfx_ticket_ready.argtypes = [vp, ctypes.POINTER(i32)]
         L.vkfx_ticket_wait.argtypes = [vp, vp, u64]
+        L.vkfx_ticket_wait_complex.argtypes = [vp, vp, u64]
+        L.vkfx_plan_output_info.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(u64)]
         L.vkfx_ticket_destroy.argtypes = [vp]
         L.vkfx_context_cache_stats.argtypes = [vp, ctypes.POINTER(u64), ctypes.POINTER(u64), ctypes.POINTER(u64)]
         L.vkfx_context_clear_caches.argtypes = [vp]
@@ -702,7 +704,10 @@ class Plan:
         # a plan outliving its context only drops its handle: the context's
         # close already destroyed it (vkfx_plan_destroy needs a live context)
         if self.handle and self.ctx.handle:
-            self._L.vkfx_plan_destroy(self.handle)
+            for t in list(self.ctx._live_tickets):  # a plan's tickets go first
+                if t.plan is self:
+                    t.close()
+            _check(self._L.vkfx_plan_destroy(self.handle), self._L)
         self.handle = ctypes.c_void_p()
 
     def __del__(self):
@@ -798,22 +803,29 @@ class TransformTicket:
             if ir.config.precision == Precision.F16StorageF32Compute else np.empty(out_count, dtype=out_dtype)
         self.handle = ctypes.c_void_p()
         _check(self._L.vkfx_submit_host(plan.handle, x.ctypes.data, x.nbytes, ctypes.byref(self.handle)), self._L)
+        plan.ctx._live_tickets.add(self)
+
+    def _live(self):
+        if not self.handle:
+            raise VkFftError(-2, "ticket was released (waited, closed, or its context was closed)")
 
     def ready(self) -> bool:
+        self._live()
         r = ctypes.c_int32()
         _check(self._L.vkfx_ticket_ready(self.handle, ctypes.byref(r)), self._L)
         return bool(r.value)
 
     def wait(self) -> np.ndarray:
+        self._live()
         _check(self._L.vkfx_ticket_wait(self.handle, self._out.ctypes.data, self._out.nbytes), self._L)
         self.close()
         ir = self.plan.ir
         return ir.unpack_output(ir.from_storage(self._out, self._complex_out))
 
     def close(self):
-        # a ticket outliving its context was already synchronised by the
-        # context's teardown; vkfx_ticket_destroy needs a live context
-        if self.handle and self.plan.ctx.handle:
+        # the context's close destroys its live tickets first, so a ticket
+        # never outlives the plan and context it references
+        if self.handle:
             self._L.vkfx_ticket_destroy(self.handle)
         self.handle = ctypes.c_void_p()
 
@@ -850,6 +862,7 @@ class HipExecutionContext:
         _check(self._L.vkfx_context_create(device_index, ctypes.byref(self.handle)), self._L)
         self._plans = {}
         self._live_plans = weakref.WeakSet()  # every Plan built on this context
+        self._live_tickets = weakref.WeakSet()  # every TransformTicket submitted on it
 
     def device_profile(self) -> dict:
         p = _Profile()
@@ -985,11 +998,14 @@ class HipExecutionContext:
         _check(self._L.vkfx_context_clear_caches(self.handle), self._L)
 
     def close(self):
+        # tickets, then plans, then the context (the C ABI refuses any other order)
+        for t in list(self._live_tickets):
+            t.close()
         for p in list(self._live_plans):
             p.close()
         self._plans.clear()
         if self.handle:
-            self._L.vkfx_context_destroy(self.handle)
+            _check(self._L.vkfx_context_destroy(self.handle), self._L)
             self.handle = ctypes.c_void_p()
 
     def __del__(self):
