@@ -241,6 +241,18 @@ int vkfx_plan_describe(const vkfx_plan *plan, char *buf, size_t cap);
  * case the plan's own workspace is used. */
 int vkfx_execute(vkfx_plan *plan, const void *d_in, void *d_out, void *d_work, void *stream);
 
+/* No counterpart in vkfft-rs: vkfx_execute for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). It runs the plan's passes with a static device
+ * scratch array of the library (64 MiB, one copy per GPU, held until the
+ * process ends) in place of the plan's workspace, and calls no hipMalloc,
+ * hipFree or other allocating routine. Plans whose workspace exceeds 64 MiB
+ * are rejected (VKFX_ERR_RESOURCE_LIMIT); plans without a workspace run as
+ * with vkfx_execute. Every call on one GPU shares that GPU's array and leaves
+ * its last contents there: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be ordered by the caller. */
+int vkfx_execute_noalloc(vkfx_plan *plan, const void *d_in, void *d_out, void *stream);
+
 /* Host round trip, the contract of NativeRuntime::execute_transform_f32/f64
  * (src/backend/native_runtime.rs:339-359): copies h_in to the device,
  * executes, copies the result to h_out and synchronises. Sizes are checked

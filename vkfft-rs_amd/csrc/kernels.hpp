@@ -9,6 +9,11 @@ namespace vkfx {
 
 constexpr int kMaxStages = 24;
 constexpr int kMaxLinesPerBlock = 64;
+// Bytes of the static device scratch behind vkfx_execute_noalloc (one copy
+// per GPU), and the device ordinals it tracks.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+constexpr int kMaxDevices = 64;
+hipError_t static_scratch_address(int device, void** out);
 
 // Kernel families. Each is one HBM pass over its lines; see the comments on
 // the IO policies in fft_kernels.hip for what each one loads and stores.

@@ -76,6 +76,8 @@ struct vkfx_context {
     vkfx_device_profile profile{};
     std::vector<PoolBuf> dev_pool, host_pool;  // free buffers
     std::vector<hipStream_t> stream_pool;      // free streams for tickets
+    void* scratch = nullptr;                   // this device's static scratch (vkfx_execute_noalloc)
+    hipError_t scratch_err = hipSuccess;       // why `scratch` is null, if it is
     std::mutex mu;                             // guards the pools, `active` and `plans`
     int active = 0;                            // tickets submitted and not yet destroyed
     int plans = 0;                             // plans created and not yet destroyed
@@ -1625,6 +1627,9 @@ int vkfx_context_create(int device_index, vkfx_context** out) {
     if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
     auto* ctx = new vkfx_context();
     ctx->device = device_index;
+    // once per device, with the device current: the address of its copy of
+    // the static scratch (a failure only disables vkfx_execute_noalloc)
+    ctx->scratch_err = vkfx::static_scratch_address(device_index, &ctx->scratch);
     e = hipStreamCreate(&ctx->stream);
     if (e == hipSuccess) e = hipStreamCreate(&ctx->aux);
     if (e != hipSuccess) {
@@ -2283,6 +2288,20 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
         if (e != hipSuccess) return hip_fail(e, "stream join");
     }
     return VKFX_OK;
+}
+
+int vkfx_execute_noalloc(vkfx_plan* plan, const void* d_in, void* d_out, void* stream) {
+    if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
+    if (plan->work_bytes > vkfx::kStaticScratchBytes)
+        return fail(VKFX_ERR_RESOURCE_LIMIT, "plan workspace of " + std::to_string(plan->work_bytes) +
+                                                 " bytes exceeds the static scratch of " +
+                                                 std::to_string(vkfx::kStaticScratchBytes) +
+                                                 " bytes; use vkfx_execute with a workspace");
+    if (plan->work_bytes && !plan->ctx->scratch)
+        return hip_fail(plan->ctx->scratch_err, "hipGetSymbolAddress(static scratch)");
+    // the plan's passes write every scratch element before reading it, so
+    // the array needs no clearing between calls
+    return vkfx_execute(plan, d_in, d_out, plan->work_bytes ? plan->ctx->scratch : nullptr, stream);
 }
 
 int vkfx_execute_host(vkfx_plan* plan, const void* h_in, uint64_t in_bytes, void* h_out, uint64_t out_bytes) {

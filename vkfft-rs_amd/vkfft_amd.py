@@ -209,6 +209,7 @@ def lib(path: Optional[str] = None):
         L.vkfx_plan_workspace_bytes.argtypes = [vp, ctypes.POINTER(u64)]
         L.vkfx_plan_describe.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
         L.vkfx_execute.argtypes = [vp, vp, vp, vp, vp]
+        L.vkfx_execute_noalloc.argtypes = [vp, vp, vp, vp]
         L.vkfx_execute_host.argtypes = [vp, vp, u64, vp, u64]
         L.vkfx_planner_axis.argtypes = [u64, u64, i32, i32, i32, u64, ctypes.POINTER(i32), ctypes.POINTER(u64)]
         L.vkfx_planner_axis_tuned.argtypes = [u64, u64, i32, i32, ctypes.POINTER(_PlannerTuning), u64,
@@ -690,6 +691,12 @@ class Plan:
         """Device-resident asynchronous execute (raw device pointers)."""
         _check(self._L.vkfx_execute(self.handle, ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
                                   ctypes.c_void_p(d_work or None), ctypes.c_void_p(stream or None)), self._L)
+
+    def execute_noalloc(self, d_in: int, d_out: int, stream: int = 0):
+        """vkfx_execute_noalloc: the same passes with the library's static
+        device scratch as the workspace; allocates nothing."""
+        _check(self._L.vkfx_execute_noalloc(self.handle, ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
+                                          ctypes.c_void_p(stream or None)), self._L)
 
     def execute_tensors(self, x, y, stream=None):
         """Execute on torch tensors already resident on the GPU."""
