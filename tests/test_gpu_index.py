@@ -122,6 +122,18 @@ def test_config_shapes_1d(idx_ctx):
     check_1d(idx_ctx, 512, 9, F64)
 
 
+def test_register_exchange_kernel(idx_ctx):
+    """The one-wave 1024-point kernel whose exchanges are DPP moves and
+    permlane swaps: with identity arithmetic it must apply exactly the
+    Stockham (16, 4, 16) digit-reversal permutation, for full and partial
+    blocks of 4 lines, both directions."""
+    env = {"VKFX_REGISTER_EXCHANGE": "1"}
+    for batch, direction in ((64, FWD), (33, FWD), (5, INV), (1, INV)):
+        d = check_1d(idx_ctx, 1024, batch, F32, direction, env=env)
+        (p,) = d["passes"]
+        assert p["lds_bytes"] == 0 and p["lines_per_block"] == 4 and p["radices"] == [16, 4, 16], p
+
+
 @pytest.mark.parametrize("n,batch,prec", [(1 << 20, 2, F32), (1 << 17, 3, F32), (3 ** 12, 1, F32),
                                           (1 << 18, 2, F64), (5 ** 8, 1, F64)])
 def test_four_step(idx_ctx, n, batch, prec):

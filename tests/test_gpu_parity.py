@@ -490,3 +490,71 @@ def test_length_sweep_sampled_against_numpy(hip_ctx, prec):
         y = c2c(hip_ctx, [n], batch, z, prec)[0]
         ref = np.fft.fft(z.astype(np.complex128).reshape(batch, n), axis=1).reshape(-1)
         assert o.rel_l2(y, ref) <= tol, ("c2c", n)
+
+
+def _plan_with_env(ctx, ir, env):
+    """A fresh plan built under the given environment knobs (read at plan time)."""
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return vk.Plan(ctx, ir)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def _run_plan(ctx, plan, x, out_count):
+    out = np.empty(out_count, dtype=x.dtype)
+    vk._check(ctx._L.vkfx_execute_host(plan.handle, x.ctypes.data, x.nbytes, out.ctypes.data, out.nbytes), ctx._L)
+    return out
+
+
+@pytest.mark.parametrize("batch", [1, 3, 5, 37, 8192])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_register_exchange_kernel_1024(hip_ctx, batch, direction):
+    """The one-wave register-exchange kernel (DPP and permlane exchanges, no
+    LDS) for 1024-point f32 rows, against the oracle: partial blocks of 4
+    lines, both directions, normalized inverse; bit-identical to itself on
+    repeat and within 1e-5 of the LDS-staged default."""
+    n = 1024
+    normalize = direction == INV
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_inverse_normalization(normalize)
+    ir = vk.TransformIr.build(cfg, direction)
+    plan = _plan_with_env(hip_ctx, ir, {"VKFX_REGISTER_EXCHANGE": "1"})
+    try:
+        (p,) = plan.describe()["passes"]
+        assert p["block"] == 256 and p["lines_per_block"] == 4 and p["lds_bytes"] == 0, p
+        assert p["radices"] == [16, 4, 16]
+        x = rand(n * batch, 700 + batch)
+        y = _run_plan(hip_ctx, plan, x, n * batch)
+        idx = np.arange(0, batch, max(1, batch // 64))
+        xs = x.reshape(batch, n)[idx].reshape(-1)
+        ref = o.fft_batch(xs.astype(np.complex128), n, "forward" if direction == FWD else "inverse", normalize,
+                          threads=8)
+        assert o.rel_l2(y.reshape(batch, n)[idx].reshape(-1), ref) <= TOL[F32]
+        assert np.array_equal(_run_plan(hip_ctx, plan, x, n * batch), y)
+        y_default = hip_ctx.execute_transform(ir, x)
+        assert o.rel_l2(y, y_default) <= TOL[F32]
+    finally:
+        plan.close()
+
+
+def test_register_exchange_kernel_nd_rows(hip_ctx):
+    """The register-exchange kernel as the contiguous-axis pass of N-D plans."""
+    for dims, batch in (([8, 1024], 2), ([3, 5, 1024], 1)):
+        cfg = vk.FftConfig.new(dims).with_batch_count(batch)
+        ir = vk.TransformIr.build(cfg, FWD)
+        plan = _plan_with_env(hip_ctx, ir, {"VKFX_REGISTER_EXCHANGE": "1"})
+        try:
+            assert any(p.get("lds_bytes") == 0 and p.get("fft_len") == 1024 and p.get("lines_per_block") == 4
+                       for p in plan.describe()["passes"])
+            total = int(np.prod(dims)) * batch
+            x = rand(total, 900)
+            y = _run_plan(hip_ctx, plan, x, total)
+            assert o.rel_l2(y, o.fft_nd(x, dims, batch, threads=8)) <= TOL[F32]
+        finally:
+            plan.close()

@@ -101,6 +101,14 @@ using KernelFn = void (*)(const KArgs);
 
 // A kernel instantiated for one compile-time shape (fft_kernels_impl.hpp
 // k_fix): the host must launch it with exactly this geometry.
+// Twiddle table a fixed shape reads through KArgs::tw: the stage roots
+// exp(-2 pi i k/N), k < N (FT_STAGE), or the lane-ordered table of the
+// register-exchange 1024-point kernel (FT_WAVE1024, fft_wave.hpp).
+enum FixedTable : int { FT_STAGE = 0, FT_WAVE1024 = 1 };
+// Complex entries of the FT_WAVE1024 table: 4 x 64 lane roots of the pass-1
+// twiddles, then 4 roots of the pass-2 twiddles.
+constexpr int kWave1024TableLen = 260;
+
 struct FixedKernel {
     KernelKind kind;
     int prec, dir;
@@ -111,6 +119,7 @@ struct FixedKernel {
     int radix[8];
     KernelFn fn;          // one block per group of G lines
     KernelFn fn_persist;  // grid-stride over groups, grid sized to residency
+    int table = FT_STAGE;
 };
 
 // Finds a fixed-shape kernel for (kind, precision, first-FFT direction,

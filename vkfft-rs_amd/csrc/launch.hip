@@ -12,6 +12,7 @@ KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct);
 KernelFn pick_f32_inv(KernelKind kind, bool wide, int direct);
 KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct);
 KernelFn pick_f64_inv(KernelKind kind, bool wide, int direct);
+const FixedKernel* fixed_table_wave(int* count);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
 const FixedKernel* fixed_table_blue(int* count);
@@ -31,7 +32,7 @@ static const FixedKernel* registry(int* count) {
         int total;
     };
     static const Merged m = [] {
-        const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_real, fixed_table_blue,
+        const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_wave, fixed_table_real, fixed_table_blue,
                                                 fixed_table_nd, fixed_table_pow2_f32, fixed_table_pow2_f64,
                                                 fixed_table_fam_f32, fixed_table_fam_f64, fixed_table_real_rows_f32,
                                                 fixed_table_real_rows_f64};
@@ -59,32 +60,32 @@ static const FixedKernel* registry(int* count) {
 }
 
 const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool col) {
-    static const bool disabled = [] {
-        const char* e = getenv("VKFX_DISABLE_FIXED");
-        return e && e[0] == '1';
-    }();
-    if (disabled) return nullptr;
+    // the knobs are read at each call: plans are built rarely, and a process
+    // may build plans under different settings (tests do)
+    const char* dis = getenv("VKFX_DISABLE_FIXED");
+    if (dis && dis[0] == '1') return nullptr;
     int total = 0;
     const FixedKernel* all = registry(&total);
+    // VKFX_REGISTER_EXCHANGE=1 prefers the register-exchange shape of a key
+    // (one wave per line, no LDS) where one is registered.
+    const char* rx = getenv("VKFX_REGISTER_EXCHANGE");
+    if (rx && rx[0] == '1')
+        for (int i = 0; i < total; ++i) {
+            const FixedKernel& f = all[i];
+            if (f.kind == kind && f.prec == prec && f.dir == dir && f.N == N && f.col == col &&
+                f.table == FT_WAVE1024)
+                return &f;
+        }
     // VKFX_FIXED_PICK=k selects the k-th registered variant of a shape key,
     // or its last one if it has fewer (tuning runs); the default is the first.
     // VKFX_FIXED_PICK_K<kind>=k does the same for one KernelKind only.
-    static const int pick_all = [] {
-        const char* e = getenv("VKFX_FIXED_PICK");
-        return e ? atoi(e) : 0;
-    }();
-    static const auto pick_kind = [] {
-        struct Picks {
-            int v[KK_COUNT];
-        } p;
-        for (int k = 0; k < KK_COUNT; ++k) {
-            const std::string name = "VKFX_FIXED_PICK_K" + std::to_string(k);
-            const char* e = getenv(name.c_str());
-            p.v[k] = e ? atoi(e) : pick_all;
-        }
-        return p;
-    }();
-    const int pick = (kind >= 0 && kind < KK_COUNT) ? pick_kind.v[kind] : pick_all;
+    const char* pa = getenv("VKFX_FIXED_PICK");
+    const int pick_all = pa ? atoi(pa) : 0;
+    int pick = pick_all;
+    if (kind >= 0 && kind < KK_COUNT) {
+        const std::string name = "VKFX_FIXED_PICK_K" + std::to_string((int)kind);
+        if (const char* e = getenv(name.c_str())) pick = atoi(e);
+    }
     const FixedKernel* last = nullptr;
     int seen = 0;
     for (int i = 0; i < total; ++i) {
@@ -196,6 +197,9 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         !(kind == KK_R2C_HALF && a.in_es == 1 && a.nstages >= 1 && a.radix[0] != 2) &&
         !(kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2 &&
           (!(a.flags & KF_DYN_PRE) || (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2))))
+        return (int)hipErrorInvalidConfiguration;
+    // the register-exchange kernels address contiguous lines (element stride 1)
+    if (fixed && fixed->table == FT_WAVE1024 && (a.in_es != 1 || a.out_es != 1 || !a.tw))
         return (int)hipErrorInvalidConfiguration;
     if (fixed) {
         // the fixed shape must be launched with exactly its own geometry

@@ -329,6 +329,24 @@ int stage_table(vkfx_plan* p, size_t n, int prec, const void** dev) {
     return upload(p, key, b.data(), b.size(), dev);
 }
 
+// Table of the register-exchange 1024-point kernel (fft_wave.hpp): the lane
+// roots W1024^(l 2^j), j < 4, in [j][l] order (lane fastest), then W64^m,
+// m < 4. Exponents are reduced in integers before the long-double
+// evaluation.
+int wave1024_table(vkfx_plan* p, int prec, const void** dev) {
+    const std::string key = "wave1024:" + std::to_string(prec);
+    if (p->table_cache.count(key)) {
+        *dev = p->table_cache[key];
+        return VKFX_OK;
+    }
+    std::vector<ld> re(kWave1024TableLen), im(kWave1024TableLen);
+    for (int j = 0; j < 4; ++j)
+        for (int l = 0; l < 64; ++l) root((ld)((l << j) % 1024), 1024.0L, re[j * 64 + l], im[j * 64 + l]);
+    for (int m = 0; m < 4; ++m) root((ld)m, 64.0L, re[256 + m], im[256 + m]);
+    auto b = pack(re, im, prec);
+    return upload(p, key, b.data(), b.size(), dev);
+}
+
 // Two-level table for exp(-2 pi i k/L), k <= L: lo[j] = root(j), j < 2^s;
 // hi[h] = root(h*2^s). The kernels form hi[k>>s]*lo[k&(2^s-1)].
 int two_level(vkfx_plan* p, size_t L, int prec, const void** lo, const void** hi, int* shift) {
@@ -578,7 +596,8 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
             (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128)
             a.flags |= KF_DYN_PRE;
     }
-    int rc = stage_table(c.p, g.N, c.prec, &a.tw);
+    int rc = (g.fixed && g.fixed->table == FT_WAVE1024) ? wave1024_table(c.p, c.prec, &a.tw)
+                                                        : stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
     rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
     if (rc) return rc;
