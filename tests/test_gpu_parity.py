@@ -168,14 +168,69 @@ def test_rader(hip_ctx, n, mode, prec):
     assert o.rel_l2(z, oracle_c2c(x, n, INV, True)) <= tol
 
 
-def test_rader_recursive_opt_in_falls_back_to_bluestein(hip_ctx):
-    cfg = vk.FftConfig.new([4099]).with_batch_count(2)
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_rader_recursive_opt_in_runs_the_rader_tree(hip_ctx, prec):
+    """PlannerTuning::with_recursive_fft_rader (planner.rs:414-422): 4099 is a
+    Rader prime whose convolution length 4098 = 2 * 3 * 683 has the Rader
+    prime 683 (rader_ir.rs:706-745, 1957-2101). The FFT-mode Rader kernel
+    runs its length-4098 FFTs with 683 as a Rader stage."""
+    n, batch = 4099, 3
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec)
     cfg.allow_recursive_fft_rader = True
     ir = vk.TransformIr.build(cfg, FWD)
     assert ir.axis_algorithms == [vk.AlgorithmKind.Rader]
-    assert hip_ctx.plan(ir).describe().get("rader_fallback") == "bluestein"
-    x = rand(4099 * 2, 3)
-    assert o.rel_l2(hip_ctx.execute_transform(ir, x), oracle_c2c(x, 4099)) <= TOL[F32]
+    desc = hip_ctx.plan(ir).describe()
+    assert "rader_fallback" not in desc
+    assert desc["rader"]["mode"] == "fft" and desc["rader"]["convolution_len"] == 4098
+    assert desc["rader"]["nested_rader_primes"] == [683]
+    x = rand(n * batch, 3, prec)
+    ref = oracle_c2c(x, n)
+    tol = TOL[F32] if prec == F32 else max(TOL[F64], 2 * o.rel_l2(ref, np.fft.fft(x.reshape(batch, n), axis=1)
+                                                                  .reshape(-1)))
+    assert o.rel_l2(hip_ctx.execute_transform(ir, x), ref) <= tol
+    cfg_i = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_inverse_normalization(True)
+    cfg_i.allow_recursive_fft_rader = True
+    ir_i = vk.TransformIr.build(cfg_i, INV)
+    assert o.rel_l2(hip_ctx.execute_transform(ir_i, x), oracle_c2c(x, n, INV, True)) <= tol
+
+
+# composite lengths whose prime factors above 13 are Rader primes: the
+# reference folds Rader into the mixed-radix tree (mixed_ir.rs); here each
+# such factor is a Rader stage of the Stockham sequence
+RADER_MIXED = [(17 * 64, [17]), (19 * 12, [19]), (23 * 5, [23]), (17 * 19, [17, 19]), (2 * 29 * 31, [29, 31]),
+               (47 * 4, [47]), (97 * 8, [97]), (17 * 17 * 3, [17, 17])]
+
+
+@pytest.mark.parametrize("n,primes", RADER_MIXED)
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_rader_inside_mixed_radix(hip_ctx, n, primes, prec):
+    batch = 5
+    x = rand(n * batch, n + 11, prec)
+    ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec), FWD)
+    assert ir.axis_algorithms == [vk.AlgorithmKind.Rader]
+    desc = hip_ctx.plan(ir).describe()
+    assert "rader_fallback" not in desc, desc
+    assert desc["rader_mixed"]["rader_primes"] == primes
+    ref = oracle_c2c(x, n)
+    npref = np.fft.fft(x.reshape(batch, n).astype(np.complex128), axis=1).reshape(-1)
+    tol = TOL[prec] if prec == F32 else max(TOL[F64], 2 * o.rel_l2(ref, npref))
+    assert o.rel_l2(hip_ctx.execute_transform(ir, x), ref) <= tol
+    z, _ = c2c(hip_ctx, [n], batch, x, prec, INV, normalize=True)
+    assert o.rel_l2(z, oracle_c2c(x, n, INV, True)) <= tol
+
+
+@pytest.mark.parametrize("dims", [[8, 17 * 16], [17 * 4, 32], [3, 19 * 4, 5]])
+def test_rader_inside_mixed_radix_nd(hip_ctx, dims):
+    """Composite Rader axes of N-D transforms, contiguous and strided."""
+    batch = 2
+    total = int(np.prod(dims)) * batch
+    x = rand(total, 77)
+    ir = vk.TransformIr.build(vk.FftConfig.new(dims).with_batch_count(batch), FWD)
+    assert vk.AlgorithmKind.Rader in ir.axis_algorithms
+    desc = hip_ctx.plan(ir).describe()
+    assert "rader_mixed" in desc and "rader_fallback" not in desc, desc
+    y = hip_ctx.execute_transform(ir, x)
+    assert o.rel_l2(y, o.fft_nd(x, dims, batch, threads=8)) <= TOL[F32]
 
 
 def test_bluestein_plan_uses_planner_length(hip_ctx):

@@ -53,16 +53,12 @@ def test_generic_padding_is_smooth_and_long_enough(n):
 
 
 @pytest.mark.parametrize("n,alg", [(2, A.Stockham), (13, A.Stockham), (26, A.Stockham), (34, A.Rader),
-                                   (89, A.Bluestein), (257, A.Rader), (263, A.Bluestein), (97, A.Rader)])
+                                   (89, A.Rader), (257, A.Rader), (263, A.Bluestein), (97, A.Rader)])
 def test_small_axis_classes(n, alg):
-    # direct Rader for 17 <= p < 89; FFT-Rader for safe primes (257-1 = 2^8,
-    # 97-1 = 2^5*3); Bluestein otherwise (89: 88 = 2^3*11 < 17 passes the gate?
-    # no: 89 is >= the direct cap and 88 = 8*11 has factors < 17, so FFT-Rader)
-    got = vk.planner_axis(n)[0]
-    if n == 89:
-        assert got == A.Rader
-    else:
-        assert got == alg
+    # direct Rader for 17 <= p < 89; FFT-Rader for primes whose p-1 has only
+    # factors below 17 (the safe-prime gate, planner.rs:498-503: 89-1 = 2^3*11,
+    # 97-1 = 2^5*3, 257-1 = 2^8); Bluestein otherwise (263-1 = 2*131)
+    assert vk.planner_axis(n)[0] == alg
 
 
 def test_f64_rader_limit_follows_lds_capacity():

@@ -451,14 +451,67 @@ __device__ __forceinline__ void stage_rt_radix(int R, cpx<T>* __restrict__ line,
 #undef VKFX_STAGE_CASE
 }
 
-// Runs every stage of a runtime radix list over the line at `line` (in LDS).
+// A Rader stage: prime radix p > kMaxStockhamRadix in a Stockham sequence
+// (the mixed-radix Rader of rader_ir.rs / mixed_ir.rs, with the length p-1
+// cyclic convolution by direct multiplication). Butterfly b of the stage
+// (input i at b + i N/p, j = b mod P) takes the stage twiddles
+// W_{P p}^(j i), then X[0] = sum x and X[g^m] = x0 + sum_s x[g^-s] b[m - s]
+// with b[n] = exp(S 2 pi i g^n / p), and writes X[q] to j + (b - j) p + q P.
+// The twiddled inputs go through `scr` (N more elements of LDS) in Rader
+// order; the threads of the line share the N inputs and then the N outputs.
+template <typename T, int S>
+__device__ __noinline__ void stage_rader(cpx<T>* __restrict__ line, cpx<T>* __restrict__ scr, const int N,
+                                         const int P, const int p, const int TT, const int t, const int ps,
+                                         const StageTw tw, const unsigned char* rt) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)scr));
+#endif
+    typedef const __attribute__((address_space(1))) int* gint;
+    const int L = p - 1, NB = N / p, step = N / (P * p);
+    const gint slot = (gint)rt, logq = (gint)rt + p;
+    const void* kern = rt + rader_kernel_offset(p) + (S < 0 ? 0 : (size_t)L * sizeof(cpx<T>));
+    for (int e = t; e < N; e += TT) {
+        const int i = e / NB, b = e - i * NB, j = b % P;
+        cpx<T> v = line[lpad(e, ps)];
+        if (i > 0 && j > 0) v = twmul<S>(v, stage_root<T>(tw, j * i * step, P >= kScatterP));
+        scr[b * p + slot[i]] = v;
+    }
+    __syncthreads();
+    for (int e = t; e < N; e += TT) {
+        const int b = e / p, q = e - b * p, j = b % P;
+        const cpx<T>* a = scr + b * p;
+        cpx<T> acc = a[L];
+        if (q == 0) {
+            for (int s = 0; s < L; ++s) acc = acc + a[s];
+        } else {
+            cpx<T> conv = mk((T)0, (T)0);
+            int bi = logq[q];
+            for (int s = 0; s < L; ++s) {
+                conv = conv + cmul(a[s], ld_table<T>(kern, bi));
+                bi = bi == 0 ? L - 1 : bi - 1;
+            }
+            acc = acc + conv;
+        }
+        line[lpad((b - j) * p + j + q * P, ps)] = acc;
+    }
+    __syncthreads();
+}
+
+// Runs every stage of a runtime radix list over the line at `line` (in LDS);
+// a Rader stage uses `scr` and its table block in `rtab`.
 template <typename T, int S, bool WIDE>
 __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int N, const int TT,
                                            const int t, const int ps, const int nst,
-                                           const int* __restrict__ radix, const StageTw& tw) {
+                                           const int* __restrict__ radix, const StageTw& tw,
+                                           cpx<T>* scr = nullptr, const void* rtab = nullptr,
+                                           const int* roff = nullptr) {
     int P = 1;
     for (int s = 0; s < nst; ++s) {
-        stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, nullptr, 0, (T)1);
+        if (radix[s] > kMaxStockhamRadix)
+            stage_rader<T, S>(line, scr, N, P, radix[s], TT, t, ps, tw, (const unsigned char*)rtab + roff[s]);
+        else
+            stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, nullptr, 0, (T)1);
         P *= radix[s];
     }
 }

@@ -824,11 +824,14 @@ __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     const int g = tid / a.TT, t = tid - g * a.TT;
     cpx<T>* line = lds + g * a.LS;
     const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
-    run_stages<T, S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
+    // Rader stages (radix > kMaxStockhamRadix) stage their inputs in a second
+    // region of G lines after the lines themselves
+    cpx<T>* scr = a.rtab ? lds + a.G * a.LS + g * a.LS : nullptr;
+    run_stages<T, S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw, scr, a.rtab, a.roff);
     if constexpr (IO::kTwoPass) {
         IO::template mid<T, DynDims>(a, lds, li);
         __syncthreads();
-        run_stages<T, -S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw);
+        run_stages<T, -S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw, scr, a.rtab, a.roff);
     }
     IO::template epilogue<T, S, DynDims>(a, lds, li);
 }

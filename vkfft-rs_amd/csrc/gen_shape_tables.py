@@ -1,0 +1,423 @@
+"""Shape tables of the fixed-shape kernels (kf_pow2_*.hip, kf_fam_*.hip,
+kf_real_rows_*.hip): the shape lists, the LDS bank-conflict model that chose
+each shape's LDS line stride LS and pad shift PS, and the emitter of the
+registration files.
+
+    python3 gen_shape_tables.py emit      # rewrite the six kf_*.hip tables
+    python3 gen_shape_tables.py check     # re-run the model search per shape
+
+Bank model (fitted to the SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE ratios the
+fixed kernels measured on gfx950): 32 banks of 4 bytes; an 8-byte access of a
+wave is served 16 lanes per cycle, a 16-byte access 8 lanes per cycle; a
+group costs its largest number of lanes on one bank. A shape's score is the
+cost of all its LDS accesses (Stockham stage reads and writes between the
+direct first and last stages; staged rows add the cooperative load and store
+copies) over the cost of the same accesses laid out conflict-free. `check`
+searches PS in {2, 3, 4, 5, 6, 30 (no padding)} and LS from the smallest line
+that fits upward, under the LDS cap of the shape (80 KiB for several lines
+per block, 156 KiB for one), and prints the recorded choice beside the best
+score. Real-transform rows (kf_real_rows_*) reuse the PS/LS of the C2C row of
+the same half length.
+
+Nontemporal roles registered per shape: rows -- both directions, input
+streamed, output streamed or cached; columns -- both directions, input
+cached, output cached or streamed; four-step column passes (FS_A) -- both
+directions, cached; R2C half rows -- forward, input streamed; C2R half rows
+-- inverse, output streamed.
+"""
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+# ------------------------------------------------------------ bank model
+
+BANKS = 32
+
+
+def lpad(e, ps):
+    return e + (e >> ps)
+
+
+def wave_lanes(col, G, TT, wave):
+    """(line, thread) of each lane of wave `wave` (None past the block)."""
+    out = []
+    for lane in range(64):
+        tid = wave * 64 + lane
+        if tid >= G * TT:
+            out.append(None)
+        elif col:
+            out.append((tid % G, tid // G))
+        else:
+            out.append((tid // TT, tid % TT))
+    return out
+
+
+def cost(addrs, eb):
+    """Cycles of one wave access: dword addresses (None = inactive lane)."""
+    per = BANKS * 4 // eb
+    total = 0
+    for s in range(0, 64, per):
+        cnt = {}
+        for a in addrs[s:s + per]:
+            if a is None:
+                continue
+            for w in range(eb // 4):
+                b = (a + w) % BANKS
+                cnt[b] = cnt.get(b, 0) + 1
+        total += max(cnt.values()) if cnt else 0
+    return total
+
+
+def ideal(addrs, eb):
+    return cost([None if a is None else 2 * k * (eb // 8) for k, a in enumerate(addrs)], eb)
+
+
+def stage_accesses(N, TT, G, PS, LS, col, radices, first_lds, last_lds, eb):
+    """LDS addresses of the Stockham stages (kernel_ir.rs:4565-4608 stage
+    semantics) run over G lines of length N by TT threads each."""
+    P = 1
+    waves = (G * TT + 63) // 64
+    out = []
+    for si, R in enumerate(radices):
+        NB = N // R
+        MJ = (NB + TT - 1) // TT
+        for w in range(waves):
+            lanes = wave_lanes(col, G, TT, w)
+            for j in range(MJ):
+                if si > 0 or first_lds:
+                    for i in range(R):
+                        ad = []
+                        for gt in lanes:
+                            bb = None if gt is None else gt[1] + j * TT
+                            if gt is None or bb >= NB:
+                                ad.append(None)
+                            else:
+                                ad.append((gt[0] * LS + lpad(bb + i * NB, PS)) * eb // 4)
+                        out.append(ad)
+                if si < len(radices) - 1 or last_lds:
+                    for q in range(R):
+                        ad = []
+                        for gt in lanes:
+                            bb = None if gt is None else gt[1] + j * TT
+                            if gt is None or bb >= NB:
+                                ad.append(None)
+                            else:
+                                k = bb % P
+                                ad.append((gt[0] * LS + lpad((bb - k) * R + k + q * P, PS)) * eb // 4)
+                        out.append(ad)
+        P *= R
+    return out
+
+
+def coop(G, N, PS, LS, nthreads, eb):
+    """The staged copies (coop_for over contiguous lines)."""
+    out = []
+    total = G * N
+    for base in range(0, total, nthreads):
+        for w0 in range(base, min(base + nthreads, total), 64):
+            ad = []
+            for idx in range(w0, w0 + 64):
+                if idx >= total or idx >= base + nthreads:
+                    ad.append(None)
+                else:
+                    ad.append(((idx // N) * LS + lpad(idx % N, PS)) * eb // 4)
+            out.append(ad)
+    return out
+
+
+def score(N, TT, G, PS, LS, col, radices, staged, eb):
+    if staged:
+        acc = coop(G, N, PS, LS, G * TT, eb) + stage_accesses(N, TT, G, PS, LS, col, radices, True, True, eb) + \
+            coop(G, N, PS, LS, G * TT, eb)
+    else:
+        acc = stage_accesses(N, TT, G, PS, LS, col, radices, False, False, eb)
+    a = sum(cost(x, eb) for x in acc)
+    i = sum(ideal(x, eb) for x in acc)
+    return a / i if i else 1.0
+
+
+def search(N, TT, G, col, radices, staged, eb):
+    cap = 80 * 1024 if G > 1 else 160 * 1024 - 4096
+    res = []
+    for PS in (2, 3, 4, 5, 6, 30):
+        base = N + ((N - 1) >> PS if PS < 30 else 0)
+        for LS in range(base, base + 20):
+            if G * LS * eb > cap:
+                break
+            res.append((round(score(N, TT, G, PS, LS, col, radices, staged, eb), 3), G * LS, PS, LS))
+    res.sort()
+    return res[0] if res else None
+
+
+# ------------------------------------------------------------ shape lists
+
+# (kind, io, N, threads per line, lines per block, columns?, radices, PS, LS);
+# strings are comment lines of the table
+TABLES = {
+    "kf_pow2_f32": [
+        ('PLAIN', 'PlainStaged', 8, 1, 64, False, [8], 2, 9),
+        ('PLAIN', 'PlainStaged', 16, 1, 64, False, [16], 4, 17),
+        ('PLAIN', 'PlainStaged', 32, 8, 32, False, [8, 4], 4, 36),
+        ('PLAIN', 'PlainStaged', 64, 8, 32, False, [8, 8], 4, 72),
+        ('PLAIN', 'PlainStaged', 128, 16, 16, False, [16, 8], 4, 135),
+        ('PLAIN', 'Plain', 256, 16, 16, False, [16, 16], 4, 271),
+        ('PLAIN', 'Plain', 512, 64, 4, False, [8, 8, 8], 4, 543),
+        ('PLAIN', 'Plain', 2048, 256, 1, False, [16, 16, 8], 4, 2175),
+        ('PLAIN', 'Plain', 8192, 512, 1, False, [16, 16, 8, 4], 4, 8703),
+        ('PLAIN', 'Plain', 16384, 1024, 1, False, [16, 16, 16, 4], 4, 17407),
+        ('PLAIN', 'Plain', 8, 1, 64, True, [8], 3, 8),
+        ('PLAIN', 'Plain', 16, 1, 64, True, [16], 4, 16),
+        ('PLAIN', 'Plain', 32, 8, 32, True, [8, 4], 4, 33),
+        ('PLAIN', 'Plain', 128, 16, 16, True, [16, 8], 6, 129),
+        ('PLAIN', 'Plain', 256, 16, 16, True, [16, 16], 30, 257),
+        ('PLAIN', 'Plain', 512, 64, 16, True, [8, 8, 8], 30, 513),
+        ('FS_A', 'FsA', 32, 8, 32, True, [8, 4], 4, 33),
+        ('FS_A', 'FsA', 128, 16, 16, True, [16, 8], 6, 129),
+    ],
+    "kf_pow2_f64": [
+        ('PLAIN', 'PlainStaged', 8, 1, 64, False, [8], 3, 9),
+        ('PLAIN', 'PlainStaged', 16, 1, 64, False, [16], 3, 17),
+        ('PLAIN', 'PlainStaged', 32, 8, 32, False, [8, 4], 3, 35),
+        ('PLAIN', 'Plain', 64, 8, 32, False, [8, 8], 3, 71),
+        ('PLAIN', 'Plain', 128, 16, 16, False, [16, 8], 4, 135),
+        ('PLAIN', 'Plain', 256, 16, 16, False, [16, 16], 4, 271),
+        ('PLAIN', 'Plain', 1024, 128, 2, False, [16, 8, 8], 4, 1087),
+        ('PLAIN', 'Plain', 2048, 256, 1, False, [16, 16, 8], 4, 2175),
+        ('PLAIN', 'Plain', 4096, 256, 1, False, [16, 16, 16], 4, 4351),
+        ('PLAIN', 'Plain', 8192, 512, 1, False, [16, 16, 8, 4], 4, 8703),
+        ('PLAIN', 'Plain', 8, 1, 64, True, [8], 3, 8),
+        ('PLAIN', 'Plain', 16, 1, 64, True, [16], 4, 16),
+        ('PLAIN', 'Plain', 32, 8, 32, True, [8, 4], 4, 33),
+        ('PLAIN', 'Plain', 64, 8, 32, True, [8, 8], 5, 65),
+        ('PLAIN', 'Plain', 128, 16, 16, True, [16, 8], 6, 129),
+        ('PLAIN', 'Plain', 256, 16, 16, True, [16, 16], 30, 257),
+        ('FS_A', 'FsA', 32, 8, 32, True, [8, 4], 4, 33),
+        ('FS_A', 'FsA', 64, 8, 32, True, [8, 8], 5, 65),
+        ('FS_A', 'FsA', 128, 16, 16, True, [16, 8], 6, 129),
+    ],
+    "kf_fam_f32": [
+        ('PLAIN', 'PlainStaged', 12, 3, 64, False, [4, 3], 4, 19),
+        ('PLAIN', 'PlainStaged', 24, 3, 64, False, [8, 3], 5, 35),
+        ('PLAIN', 'PlainStaged', 48, 3, 64, False, [16, 3], 4, 51),
+        ('PLAIN', 'PlainStaged', 96, 6, 42, False, [16, 6], 4, 102),
+        ('PLAIN', 'PlainStaged', 192, 12, 21, False, [16, 12], 4, 204),
+        ('PLAIN', 'Plain', 384, 24, 10, False, [16, 8, 3], 4, 409),
+        ('PLAIN', 'Plain', 768, 48, 5, False, [16, 16, 3], 4, 815),
+        ('PLAIN', 'Plain', 1536, 96, 2, False, [16, 16, 6], 4, 1631),
+        ('PLAIN', 'Plain', 3072, 192, 1, False, [16, 16, 12], 4, 3263),
+        ('PLAIN', 'Plain', 6144, 384, 1, False, [16, 16, 8, 3], 4, 6527),
+        ('PLAIN', 'Plain', 12288, 768, 1, False, [16, 16, 16, 3], 4, 13055),
+        ('PLAIN', 'PlainStaged', 20, 4, 64, False, [4, 5], 5, 20),
+        ('PLAIN', 'PlainStaged', 40, 5, 51, False, [8, 5], 5, 53),
+        ('PLAIN', 'PlainStaged', 80, 5, 51, False, [16, 5], 4, 85),
+        ('PLAIN', 'PlainStaged', 160, 10, 25, False, [16, 10], 4, 170),
+        ('PLAIN', 'Plain', 320, 40, 6, False, [8, 8, 5], 3, 360),
+        ('PLAIN', 'Plain', 640, 40, 6, False, [16, 8, 5], 4, 680),
+        ('PLAIN', 'Plain', 1280, 80, 3, False, [16, 16, 5], 4, 1359),
+        ('PLAIN', 'Plain', 2560, 160, 1, False, [16, 16, 10], 4, 2719),
+        ('PLAIN', 'Plain', 5120, 320, 1, False, [16, 16, 4, 5], 4, 5439),
+        ('PLAIN', 'Plain', 10240, 640, 1, False, [16, 16, 8, 5], 4, 10879),
+        ('PLAIN', 'PlainStaged', 100, 10, 25, False, [10, 10], 6, 106),
+        ('PLAIN', 'Plain', 1000, 100, 2, False, [10, 10, 10], 30, 1012),
+        ('PLAIN', 'Plain', 10000, 1000, 1, False, [10, 10, 10, 10], 30, 10000),
+        ('PLAIN', 'Plain', 360, 40, 6, False, [8, 9, 5], 4, 394),
+        "// strided columns (G adjacent columns per block, 128-byte or wider row segments)",
+        ('PLAIN', 'Plain', 12, 3, 64, True, [4, 3], 3, 13),
+        ('PLAIN', 'Plain', 20, 4, 64, True, [4, 5], 4, 21),
+        ('PLAIN', 'Plain', 24, 3, 64, True, [8, 3], 4, 25),
+        ('PLAIN', 'Plain', 40, 5, 64, True, [8, 5], 5, 41),
+        ('PLAIN', 'Plain', 48, 3, 64, True, [16, 3], 5, 49),
+        ('PLAIN', 'Plain', 80, 5, 64, True, [16, 5], 6, 81),
+        ('PLAIN', 'Plain', 96, 6, 64, True, [16, 6], 6, 97),
+        ('PLAIN', 'Plain', 100, 10, 32, True, [10, 10], 6, 101),
+        ('PLAIN', 'Plain', 160, 10, 32, True, [16, 10], 30, 161),
+        ('PLAIN', 'Plain', 192, 12, 32, True, [16, 12], 30, 193),
+        ('PLAIN', 'Plain', 320, 40, 16, True, [8, 8, 5], 30, 321),
+        ('PLAIN', 'Plain', 360, 40, 16, True, [8, 9, 5], 30, 361),
+        ('PLAIN', 'Plain', 384, 24, 16, True, [16, 8, 3], 30, 385),
+        ('PLAIN', 'Plain', 640, 40, 8, True, [16, 8, 5], 4, 682),
+    ],
+    "kf_fam_f64": [
+        ('PLAIN', 'PlainStaged', 12, 3, 64, False, [4, 3], 4, 19),
+        ('PLAIN', 'PlainStaged', 24, 3, 64, False, [8, 3], 3, 27),
+        ('PLAIN', 'PlainStaged', 48, 3, 64, False, [16, 3], 4, 51),
+        ('PLAIN', 'PlainStaged', 96, 6, 42, False, [16, 6], 4, 102),
+        ('PLAIN', 'Plain', 192, 12, 21, False, [16, 12], 4, 204),
+        ('PLAIN', 'Plain', 384, 24, 10, False, [16, 8, 3], 4, 407),
+        ('PLAIN', 'Plain', 768, 48, 5, False, [16, 16, 3], 4, 815),
+        ('PLAIN', 'Plain', 1536, 96, 2, False, [16, 16, 6], 4, 1631),
+        ('PLAIN', 'Plain', 3072, 192, 1, False, [16, 16, 12], 4, 3263),
+        ('PLAIN', 'Plain', 6144, 384, 1, False, [16, 16, 8, 3], 4, 6527),
+        ('PLAIN', 'PlainStaged', 20, 4, 64, False, [4, 5], 5, 20),
+        ('PLAIN', 'PlainStaged', 40, 5, 51, False, [8, 5], 3, 45),
+        ('PLAIN', 'PlainStaged', 80, 5, 51, False, [16, 5], 4, 85),
+        ('PLAIN', 'Plain', 160, 10, 25, False, [16, 10], 4, 170),
+        ('PLAIN', 'Plain', 320, 40, 6, False, [8, 8, 5], 3, 359),
+        ('PLAIN', 'Plain', 640, 40, 6, False, [16, 8, 5], 4, 679),
+        ('PLAIN', 'Plain', 1280, 80, 3, False, [16, 16, 5], 4, 1359),
+        ('PLAIN', 'Plain', 2560, 160, 1, False, [16, 16, 10], 4, 2719),
+        ('PLAIN', 'Plain', 5120, 320, 1, False, [16, 16, 4, 5], 4, 5439),
+        ('PLAIN', 'Plain', 100, 10, 25, False, [10, 10], 6, 106),
+        ('PLAIN', 'Plain', 1000, 100, 2, False, [10, 10, 10], 6, 1022),
+        ('PLAIN', 'Plain', 360, 40, 6, False, [8, 9, 5], 3, 404),
+        "// strided columns (G adjacent columns per block, 128-byte or wider row segments)",
+        ('PLAIN', 'Plain', 12, 3, 64, True, [4, 3], 3, 13),
+        ('PLAIN', 'Plain', 20, 4, 64, True, [4, 5], 4, 21),
+        ('PLAIN', 'Plain', 24, 3, 64, True, [8, 3], 4, 25),
+        ('PLAIN', 'Plain', 40, 5, 64, True, [8, 5], 5, 41),
+        ('PLAIN', 'Plain', 48, 3, 64, True, [16, 3], 5, 49),
+        ('PLAIN', 'Plain', 80, 5, 32, True, [16, 5], 6, 81),
+        ('PLAIN', 'Plain', 96, 6, 32, True, [16, 6], 6, 97),
+        ('PLAIN', 'Plain', 100, 10, 32, True, [10, 10], 6, 101),
+        ('PLAIN', 'Plain', 160, 10, 16, True, [16, 10], 30, 161),
+        ('PLAIN', 'Plain', 192, 12, 16, True, [16, 12], 30, 193),
+        ('PLAIN', 'Plain', 320, 40, 8, True, [8, 8, 5], 30, 321),
+        ('PLAIN', 'Plain', 360, 40, 8, True, [8, 9, 5], 30, 361),
+        ('PLAIN', 'Plain', 384, 24, 8, True, [16, 8, 3], 30, 385),
+        ('PLAIN', 'Plain', 640, 40, 4, True, [16, 8, 5], 4, 682),
+    ],
+    "kf_real_rows_f32": [
+        ('R2C_HALF', 'R2CHalf', 256, 16, 16, False, [16, 16], 4, 271),
+        ('C2R_HALF', 'C2RHalf', 256, 16, 16, False, [16, 16], 4, 271),
+        ('R2C_HALF', 'R2CHalf', 512, 64, 4, False, [8, 8, 8], 4, 543),
+        ('C2R_HALF', 'C2RHalf', 512, 64, 4, False, [8, 8, 8], 4, 543),
+        ('R2C_HALF', 'R2CHalf', 1024, 128, 1, False, [16, 8, 8], 4, 1088),
+        ('C2R_HALF', 'C2RHalf', 1024, 128, 1, False, [16, 8, 8], 4, 1088),
+        ('R2C_HALF', 'R2CHalf', 2048, 256, 1, False, [16, 16, 8], 4, 2175),
+        ('C2R_HALF', 'C2RHalf', 2048, 256, 1, False, [16, 16, 8], 4, 2175),
+        ('R2C_HALF', 'R2CHalf', 4096, 256, 1, False, [16, 16, 16], 4, 4352),
+        ('C2R_HALF', 'C2RHalf', 4096, 256, 1, False, [16, 16, 16], 4, 4352),
+        ('R2C_HALF', 'R2CHalf', 8192, 512, 1, False, [16, 16, 8, 4], 4, 8703),
+        ('C2R_HALF', 'C2RHalf', 8192, 512, 1, False, [16, 16, 8, 4], 4, 8703),
+        ('R2C_HALF', 'R2CHalf', 384, 24, 10, False, [16, 8, 3], 4, 409),
+        ('C2R_HALF', 'C2RHalf', 384, 24, 10, False, [16, 8, 3], 4, 409),
+        ('R2C_HALF', 'R2CHalf', 768, 48, 5, False, [16, 16, 3], 4, 815),
+        ('C2R_HALF', 'C2RHalf', 768, 48, 5, False, [16, 16, 3], 4, 815),
+        ('R2C_HALF', 'R2CHalf', 1536, 96, 2, False, [16, 16, 6], 4, 1631),
+        ('C2R_HALF', 'C2RHalf', 1536, 96, 2, False, [16, 16, 6], 4, 1631),
+        ('R2C_HALF', 'R2CHalf', 3072, 192, 1, False, [16, 16, 12], 4, 3263),
+        ('C2R_HALF', 'C2RHalf', 3072, 192, 1, False, [16, 16, 12], 4, 3263),
+        ('R2C_HALF', 'R2CHalf', 6144, 384, 1, False, [16, 16, 8, 3], 4, 6527),
+        ('C2R_HALF', 'C2RHalf', 6144, 384, 1, False, [16, 16, 8, 3], 4, 6527),
+        ('R2C_HALF', 'R2CHalf', 320, 40, 6, False, [8, 8, 5], 3, 360),
+        ('C2R_HALF', 'C2RHalf', 320, 40, 6, False, [8, 8, 5], 3, 360),
+        ('R2C_HALF', 'R2CHalf', 640, 40, 6, False, [16, 8, 5], 4, 680),
+        ('C2R_HALF', 'C2RHalf', 640, 40, 6, False, [16, 8, 5], 4, 680),
+        ('R2C_HALF', 'R2CHalf', 1280, 80, 3, False, [16, 16, 5], 4, 1359),
+        ('C2R_HALF', 'C2RHalf', 1280, 80, 3, False, [16, 16, 5], 4, 1359),
+        ('R2C_HALF', 'R2CHalf', 2560, 160, 1, False, [16, 16, 10], 4, 2719),
+        ('C2R_HALF', 'C2RHalf', 2560, 160, 1, False, [16, 16, 10], 4, 2719),
+        ('R2C_HALF', 'R2CHalf', 5120, 320, 1, False, [16, 16, 4, 5], 4, 5439),
+        ('C2R_HALF', 'C2RHalf', 5120, 320, 1, False, [16, 16, 4, 5], 4, 5439),
+    ],
+    "kf_real_rows_f64": [
+        ('R2C_HALF', 'R2CHalf', 64, 8, 32, False, [8, 8], 3, 71),
+        ('C2R_HALF', 'C2RHalf', 64, 8, 32, False, [8, 8], 3, 71),
+        ('R2C_HALF', 'R2CHalf', 128, 16, 16, False, [16, 8], 4, 135),
+        ('C2R_HALF', 'C2RHalf', 128, 16, 16, False, [16, 8], 4, 135),
+        ('R2C_HALF', 'R2CHalf', 256, 16, 16, False, [16, 16], 4, 271),
+        ('C2R_HALF', 'C2RHalf', 256, 16, 16, False, [16, 16], 4, 271),
+        ('R2C_HALF', 'R2CHalf', 512, 64, 2, False, [8, 8, 8], 3, 576),
+        ('C2R_HALF', 'C2RHalf', 512, 64, 2, False, [8, 8, 8], 3, 576),
+        ('R2C_HALF', 'R2CHalf', 1024, 128, 2, False, [16, 8, 8], 4, 1087),
+        ('C2R_HALF', 'C2RHalf', 1024, 128, 2, False, [16, 8, 8], 4, 1087),
+        ('R2C_HALF', 'R2CHalf', 2048, 256, 1, False, [16, 16, 8], 4, 2175),
+        ('C2R_HALF', 'C2RHalf', 2048, 256, 1, False, [16, 16, 8], 4, 2175),
+        ('R2C_HALF', 'R2CHalf', 4096, 256, 1, False, [16, 16, 16], 4, 4351),
+        ('C2R_HALF', 'C2RHalf', 4096, 256, 1, False, [16, 16, 16], 4, 4351),
+        ('R2C_HALF', 'R2CHalf', 192, 12, 21, False, [16, 12], 4, 204),
+        ('C2R_HALF', 'C2RHalf', 192, 12, 21, False, [16, 12], 4, 204),
+        ('R2C_HALF', 'R2CHalf', 384, 24, 10, False, [16, 8, 3], 4, 407),
+        ('C2R_HALF', 'C2RHalf', 384, 24, 10, False, [16, 8, 3], 4, 407),
+        ('R2C_HALF', 'R2CHalf', 768, 48, 5, False, [16, 16, 3], 4, 815),
+        ('C2R_HALF', 'C2RHalf', 768, 48, 5, False, [16, 16, 3], 4, 815),
+        ('R2C_HALF', 'R2CHalf', 1536, 96, 2, False, [16, 16, 6], 4, 1631),
+        ('C2R_HALF', 'C2RHalf', 1536, 96, 2, False, [16, 16, 6], 4, 1631),
+        ('R2C_HALF', 'R2CHalf', 3072, 192, 1, False, [16, 16, 12], 4, 3263),
+        ('C2R_HALF', 'C2RHalf', 3072, 192, 1, False, [16, 16, 12], 4, 3263),
+        ('R2C_HALF', 'R2CHalf', 160, 10, 25, False, [16, 10], 4, 170),
+        ('C2R_HALF', 'C2RHalf', 160, 10, 25, False, [16, 10], 4, 170),
+        ('R2C_HALF', 'R2CHalf', 320, 40, 6, False, [8, 8, 5], 3, 359),
+        ('C2R_HALF', 'C2RHalf', 320, 40, 6, False, [8, 8, 5], 3, 359),
+        ('R2C_HALF', 'R2CHalf', 640, 40, 6, False, [16, 8, 5], 4, 679),
+        ('C2R_HALF', 'C2RHalf', 640, 40, 6, False, [16, 8, 5], 4, 679),
+        ('R2C_HALF', 'R2CHalf', 1280, 80, 3, False, [16, 16, 5], 4, 1359),
+        ('C2R_HALF', 'C2RHalf', 1280, 80, 3, False, [16, 16, 5], 4, 1359),
+        ('R2C_HALF', 'R2CHalf', 2560, 160, 1, False, [16, 16, 10], 4, 2719),
+        ('C2R_HALF', 'C2RHalf', 2560, 160, 1, False, [16, 16, 10], 4, 2719),
+    ],
+}
+
+HEADS = {'kf_pow2_f32': "// Fixed shapes of the power-of-two lengths outside the benchmark\n// configurations, f32: rows of one upload (1-D batches and the contiguous\n// axis of N-D transforms), strided columns up to the length that stays one\n// upload per axis, and the first pass of split strided axes. Each shape is\n// registered for both directions and for the two nontemporal roles its pass\n// can take (rows: the caller's input, with or without the caller's output;\n// columns: cached input, with or without the caller's output). LDS strides\n// minimise bank conflicts under the 32-bank model of 8-byte accesses (16 lanes\n// served per cycle). Short rows, whose first or last Stockham stage would touch\n// HBM in segments narrower than 128 bytes, stage both ends through LDS\n// (IoPlainStaged).\n", 'kf_pow2_f64': "// Fixed shapes of the power-of-two lengths outside the benchmark\n// configurations, f64: rows of one upload (1-D batches and the contiguous\n// axis of N-D transforms), strided columns up to the length that stays one\n// upload per axis, and the first pass of split strided axes. Each shape is\n// registered for both directions and for the two nontemporal roles its pass\n// can take (rows: the caller's input, with or without the caller's output;\n// columns: cached input, with or without the caller's output). LDS strides\n// minimise bank conflicts under the 32-bank model of 8-byte accesses (16 lanes\n// served per cycle). Short rows, whose first or last Stockham stage would touch\n// HBM in segments narrower than 128 bytes, stage both ends through LDS\n// (IoPlainStaged).\n", 'kf_fam_f32': '// Fixed shapes of common lengths with factors 3 and 5, f32: 3*2^k, 5*2^k,\n// 10^k and 360, as rows of one upload (1-D batches and the contiguous axis of\n// N-D transforms) and as strided columns up to 640, each in both directions\n// and both nontemporal roles. Radix plans keep at most three or four\n// LDS-exchanged stages (composite radices 6, 10 and 12 where they save one);\n// threads per line = N / the largest radix; LDS strides minimise bank\n// conflicts under the 32-bank model of 8-byte accesses. Short rows stage both\n// ends through LDS (IoPlainStaged).\n', 'kf_fam_f64': '// Fixed shapes of common lengths with factors 3 and 5, f64: 3*2^k, 5*2^k,\n// 10^k and 360, as rows of one upload (1-D batches and the contiguous axis of\n// N-D transforms) and as strided columns up to 640, each in both directions\n// and both nontemporal roles. Radix plans keep at most three or four\n// LDS-exchanged stages (composite radices 6, 10 and 12 where they save one);\n// threads per line = N / the largest radix; LDS strides minimise bank\n// conflicts under the 32-bank model of 8-byte accesses. Short rows stage both\n// ends through LDS (IoPlainStaged).\n', 'kf_real_rows_f32': "// Fixed shapes of the one-upload even-length real transforms, f32: the\n// half-size packed FFT of R2C (postprocess fused into the staged store) and of\n// C2R (preprocess fused into the direct loads) for half lengths M that have a\n// fixed C2C row shape (powers of two and the 3*2^k / 5*2^k families), with the\n// same radices, threads, lines per block and LDS strides as those rows. R2C is\n// registered for the caller's input with or without the caller's output, C2R\n// for the caller's output with or without the caller's input.\n", 'kf_real_rows_f64': "// Fixed shapes of the one-upload even-length real transforms, f64: the\n// half-size packed FFT of R2C (postprocess fused into the staged store) and of\n// C2R (preprocess fused into the direct loads) for half lengths M that have a\n// fixed C2C row shape (powers of two and the 3*2^k / 5*2^k families), with the\n// same radices, threads, lines per block and LDS strides as those rows. R2C is\n// registered for the caller's input with or without the caller's output, C2R\n// for the caller's output with or without the caller's input.\n"}
+
+FUNCS = {'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
+
+
+def roles(kind, col):
+    """(direction, nontemporal input, nontemporal output) registered."""
+    if kind == "FS_A":
+        return [(-1, False, False), (1, False, False)]
+    if kind == "R2C_HALF":
+        return [(-1, True, True), (-1, True, False)]
+    if kind == "C2R_HALF":
+        return [(1, True, True), (1, False, True)]
+    if col:
+        return [(-1, False, False), (-1, False, True), (1, False, False), (1, False, True)]
+    return [(-1, True, True), (-1, True, False), (1, True, True), (1, True, False)]
+
+
+def b(v):
+    return "true" if v else "false"
+
+
+def render(name):
+    """Text of table file `name`.hip."""
+    prec = 1 if name.endswith("f64") else 0
+    T = "double" if prec else "float"
+    lines = [HEADS[name].rstrip("\n"),
+             "//",
+             "// Generated by gen_shape_tables.py (shape lists and LDS bank-conflict",
+             "// model); edit the lists there and run `python3 gen_shape_tables.py emit`.",
+             '#include "fft_kernels_impl.hpp"', "", "namespace vkfx {", "", "static const FixedKernel kTable[] = {"]
+    for it in TABLES[name]:
+        if isinstance(it, str):
+            lines.append("    " + it)
+            continue
+        kind, io, N, TT, G, col, rad, PS, LS = it
+        for S, nti, nto in roles(kind, col):
+            lines.append(f"    VKFX_SHAPE(KK_{kind}, Io{io}, {T}, {prec}, {S}, {N}, {TT}, {G}, {PS}, {LS}, {b(col)}, "
+                         f"{b(nti)}, {b(nto)}, {', '.join(map(str, rad))}),")
+    lines += ["};", "", f"const FixedKernel* {FUNCS[name]}(int* count) {{",
+              "    *count = (int)(sizeof(kTable) / sizeof(kTable[0]));", "    return kTable;", "}", "",
+              "}  // namespace vkfx", ""]
+    return "\n".join(lines)
+
+
+def emit(name):
+    with open(os.path.join(HERE, name + ".hip"), "w") as f:
+        f.write(render(name))
+
+
+def check():
+    for name, items in TABLES.items():
+        eb = 16 if name.endswith("f64") else 8
+        for it in items:
+            if isinstance(it, str) or it[0] in ("R2C_HALF", "C2R_HALF"):
+                continue
+            kind, io, N, TT, G, col, rad, PS, LS = it
+            staged = io == "PlainStaged"
+            cur = score(N, TT, G, PS, LS, col, rad, staged, eb)
+            best = search(N, TT, G, col, rad, staged, eb)
+            print(f"{name} {kind} N={N} {'col' if col else 'row'} TT={TT} G={G}: PS={PS} LS={LS} "
+                  f"ratio {cur:.3f}; model best {best}", flush=True)
+
+
+if __name__ == "__main__":
+    if len(sys.argv) > 1 and sys.argv[1] == "emit":
+        for n in TABLES:
+            emit(n)
+    elif len(sys.argv) > 1 and sys.argv[1] == "check":
+        check()
+    else:
+        print(__doc__)

@@ -95,7 +95,22 @@ struct KArgs {
     long long nblk;                    // line groups (persistent kernels walk them)
     const int* pin;                    // Rader gather: a[s] = x[pin[s]]
     const int* pout;                   // Rader scatter: X[pout[m]] = x0 + conv[m]
+    // Rader stages of a runtime radix list (radix > kMaxStockhamRadix): the
+    // table block of stage s starts roff[s] bytes into rtab (rader_stage_table)
+    const void* rtab;
+    int roff[kMaxStages];
 };
+
+// Radices up to this are Stockham butterflies; a larger (prime) radix in a
+// runtime radix list is a Rader stage computed by direct multiplication.
+constexpr int kMaxStockhamRadix = 16;
+
+// Byte layout of a Rader stage table for prime p (L = p - 1, generator g):
+// int slot[p] (slot[0] = L, slot[i] = s with g^-s = i), int logq[p]
+// (logq[q] = m with g^m = q), then from byte rader_kernel_offset(p) the
+// complex kernels b[n] = exp(-2 pi i g^n / p) (forward) and its conjugate
+// (inverse), L entries each.
+constexpr int rader_kernel_offset(int p) { return (2 * p * 4 + 15) / 16 * 16; }
 
 using KernelFn = void (*)(const KArgs);
 

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <limits>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -134,6 +135,7 @@ struct Geometry {
     size_t lds = 0;
     bool ok = false;
     bool wide = false;  // runtime-shape kernel with up to 32 elements per thread per stage
+    bool rader = false;  // the radix list has Rader stages (lds holds a second region of G lines)
     const FixedKernel* fixed = nullptr;
 };
 
@@ -207,6 +209,66 @@ Geometry geometry(size_t n, int prec, int want_g, size_t lds_max, size_t lds_bud
     if (G < 1) return g;
     g.G = G;
     g.lds = (size_t)G * line_bytes;
+    g.ok = true;
+    return g;
+}
+
+// Radix list of a length whose prime factors above 13 run as Rader stages
+// (the composite lengths the planner classifies as Rader, and the Rader
+// convolutions of the recursive-Rader extension): the Stockham radices of
+// the 2/3/5/7/11/13-smooth part, then one stage per larger prime factor.
+bool radix_schedule_rader(size_t n, std::vector<int>& out) {
+    size_t smooth = n;
+    std::vector<int> rader;
+    for (size_t q : prime_factorization(n))
+        if (q > 13) {
+            if (q > (size_t)std::numeric_limits<int>::max() / 2) return false;
+            rader.push_back((int)q);
+            smooth /= q;
+        }
+    if (!radix_schedule(smooth, out)) return false;
+    if (smooth == 1) out.clear();
+    out.insert(out.end(), rader.begin(), rader.end());
+    return !out.empty() && (int)out.size() <= kMaxStages;
+}
+
+// Runtime-shape geometry of a radix list with Rader stages: the threads of a
+// line cover its Stockham stages and at least min(N, 256) work items of the
+// Rader stages; LDS holds the G lines and G scratch lines. `slot` adds one
+// element after each line (the x0 slot of an FFT-mode Rader kernel).
+Geometry geometry_rader(size_t n, int prec, int want_g, size_t lds_max, size_t lds_budget, bool slot = false) {
+    Geometry g;
+    if (n < 2 || n > (1u << 20)) return g;
+    if (!radix_schedule_rader(n, g.radix)) return g;
+    bool any = false;
+    int tt = (int)std::min<size_t>(n, 256);
+    for (int r : g.radix) {
+        if (r > kMaxStockhamRadix) {
+            any = true;
+            continue;
+        }
+        const int nb = (int)n / r, bpt = dyn_butterflies_per_thread(r, false);
+        tt = std::max(tt, (nb + bpt - 1) / bpt);
+    }
+    if (!any || tt > 512) return g;
+    g.N = (int)n;
+    g.TT = tt;
+    const size_t sz = prec ? 16 : 8;
+    g.PS = prec ? 3 : 4;
+    int ls = (int)n + ((int)n >> g.PS) + (slot ? 2 : 0);
+    if (ls % 2 == 0) ls += 1;
+    g.LS = ls;
+    const size_t line_bytes = 2 * (size_t)ls * sz;  // line + scratch line
+    if (line_bytes > lds_max) return g;
+    size_t budget = std::min(std::max(lds_budget, line_bytes), lds_max);
+    int G = std::max(1, want_g);
+    G = std::min(G, 512 / tt);
+    G = std::min<int>(G, (int)(budget / line_bytes));
+    G = std::min(G, kMaxLinesPerBlock);
+    if (G < 1) return g;
+    g.G = G;
+    g.lds = (size_t)G * line_bytes;
+    g.rader = true;
     g.ok = true;
     return g;
 }
@@ -345,6 +407,59 @@ int wave1024_table(vkfx_plan* p, int prec, const void** dev) {
     for (int m = 0; m < 4; ++m) root((ld)m, 64.0L, re[256 + m], im[256 + m]);
     auto b = pack(re, im, prec);
     return upload(p, key, b.data(), b.size(), dev);
+}
+
+// Table block of a Rader stage for prime q (layout in kernels.hpp,
+// rader_kernel_offset): slot and logq from the generator's powers, then the
+// forward kernel exp(-2 pi i g^n / q) and its conjugate.
+std::vector<unsigned char> rader_stage_block(size_t q, int prec) {
+    const size_t L = q - 1, g = primitive_root(q);
+    std::vector<size_t> pw(L);
+    size_t r = 1;
+    for (size_t e = 0; e < L; ++e) {
+        pw[e] = r;
+        r = (r * g) % q;
+    }
+    const size_t koff = (size_t)rader_kernel_offset((int)q), es = prec ? 16 : 8;
+    std::vector<unsigned char> b(koff + 2 * L * es, 0);
+    int* slot = (int*)b.data();
+    int* logq = slot + q;
+    slot[0] = (int)L;
+    logq[0] = 0;
+    for (size_t e = 0; e < L; ++e) {
+        slot[pw[(L - e) % L]] = (int)e;  // g^-e
+        logq[pw[e]] = (int)e;
+    }
+    std::vector<ld> re(2 * L), im(2 * L);
+    for (size_t e = 0; e < L; ++e) {
+        root((ld)pw[e], (ld)q, re[e], im[e]);
+        re[L + e] = re[e];
+        im[L + e] = -im[e];
+    }
+    auto k = pack(re, im, prec);
+    std::memcpy(b.data() + koff, k.data(), k.size());
+    return b;
+}
+
+// Device table of every Rader stage of a radix list: rtab and per-stage byte
+// offsets (distinct primes share a block).
+int rader_stage_tables(vkfx_plan* p, const std::vector<int>& radix, int prec, KArgs& a) {
+    std::vector<unsigned char> all;
+    std::map<int, size_t> at;
+    std::string key = "rstages:" + std::to_string(prec);
+    for (size_t s = 0; s < radix.size(); ++s) {
+        if (radix[s] <= kMaxStockhamRadix) continue;
+        if (!at.count(radix[s])) {
+            at[radix[s]] = all.size();
+            auto b = rader_stage_block((size_t)radix[s], prec);
+            all.insert(all.end(), b.begin(), b.end());
+            all.resize((all.size() + 15) / 16 * 16, 0);
+            key += ":" + std::to_string(radix[s]);
+        }
+        a.roff[s] = (int)at[radix[s]];
+    }
+    if (all.empty()) return VKFX_OK;
+    return upload(p, key, all.data(), all.size(), &a.rtab);
 }
 
 // Two-level table for exp(-2 pi i k/L), k <= L: lo[j] = root(j), j < 2^s;
@@ -576,12 +691,17 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
     a.nlines = nlines;
     if (!g.fixed && g.wide) a.flags |= KF_DYN_WIDE;
+    if (g.rader) {
+        // Rader stages run in the staged runtime-shape kernel only
+        int rc = rader_stage_tables(c.p, g.radix, c.prec, a);
+        if (rc) return rc;
+    }
     // runtime-shape C2C over contiguous lines: HBM-direct first and last stages
-    if (!g.fixed && kind == KK_PLAIN && (a.flags & KF_IN_ROWMAJOR) && (a.flags & KF_OUT_ROWMAJOR) &&
+    if (!g.fixed && !g.rader && kind == KK_PLAIN && (a.flags & KF_IN_ROWMAJOR) && (a.flags & KF_OUT_ROWMAJOR) &&
         a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && a.radix[a.nstages - 1] != 2)
         a.flags |= KF_DYN_DIRECT;
     // runtime-shape even R2C: HBM-direct first stage, staged postprocess
-    if (!g.fixed && kind == KK_R2C_HALF && (a.flags & KF_IN_ROWMAJOR) && a.in_es == 1 && a.nstages >= 1 &&
+    if (!g.fixed && !g.rader && kind == KK_R2C_HALF && (a.flags & KF_IN_ROWMAJOR) && a.in_es == 1 && a.nstages >= 1 &&
         a.radix[0] != 2)
         a.flags |= KF_DYN_DIRECT;
     // runtime-shape even C2R, HBM-direct last stage; KF_DYN_PRE: the first
@@ -590,7 +710,8 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
     // exactly 4 (f32 lines with radix 8 or 16 first measured 8-13% slower
     // that way, radix-4 ones 6-14% faster; f64 7-29% faster; radix 3, 5, 7
     // first were not measured in f32 and keep the staged preprocess)
-    if (!g.fixed && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2) {
+    if (!g.fixed && !g.rader && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 &&
+        a.radix[a.nstages - 1] != 2) {
         a.flags |= KF_DYN_DIRECT;
         if (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && (c.prec == 1 || a.radix[0] == 4) &&
             (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128)
@@ -699,19 +820,39 @@ int add_rader(Ctx& c, size_t prime, int dir, KArgs a, long long lines, int in_se
         g = geometry(L, c.prec, 1, c.lds_max, c.lds_max);
         fft = g.ok;
     }
-    if (!fft && prime >= 89) return VKFX_OK;  // beyond direct multiplication: caller falls back
+    // a p-1 with prime factors above 13 (the recursive-Rader extension,
+    // planner.rs:414-422): the length p-1 FFTs run those factors as Rader
+    // stages themselves (direct multiplication inside the stage)
+    bool nested = false;
+    if (!fft && prime >= 89) {
+        g = geometry_rader(L, c.prec, 1, c.lds_max, c.lds_max, true);
+        if (!g.ok) return VKFX_OK;  // beyond one upload: the caller falls back
+        fft = nested = true;
+    }
     RaderTables t;
     int rc = rader_tables(c.p, prime, dir, c.prec, fft, &t);
     if (rc) return rc;
     a.pin = (const int*)t.pin, a.pout = (const int*)t.pout, a.spec = t.spec;
     if (fft) {
-        g = geometry(L, c.prec, std::max(1, 128 / g.TT), c.lds_max, c.lds_budget);
+        g = nested ? geometry_rader(L, c.prec, std::max(1, 128 / g.TT), c.lds_max, c.lds_budget, true)
+                   : geometry(L, c.prec, std::max(1, 128 / g.TT), c.lds_max, c.lds_budget);
         const int need = (int)L + (int)((L - 1) >> g.PS) + 2;  // x0 slot after the line
         if (g.LS < need) {
             g.LS = need | 1;
-            g.lds = (size_t)g.G * g.LS * csize(c.prec);
+            g.lds = (size_t)g.G * g.LS * csize(c.prec) * (g.rader ? 2 : 1);
         }
-        c.js << "\"rader\":{\"prime\":" << prime << ",\"mode\":\"fft\",\"convolution_len\":" << L << "},";
+        c.js << "\"rader\":{\"prime\":" << prime << ",\"mode\":\"fft\",\"convolution_len\":" << L;
+        if (nested) {
+            c.js << ",\"nested_rader_primes\":[";
+            bool first = true;
+            for (int r : g.radix)
+                if (r > kMaxStockhamRadix) {
+                    c.js << (first ? "" : ",") << r;
+                    first = false;
+                }
+            c.js << "]";
+        }
+        c.js << "},";
         rc = add_launch(c, KK_RADER_FFT, -1, g, a, lines, blocks_for(lines, g.G), in_sel, in_off, out_sel, out_off,
                         "rader_fft");
     } else {
@@ -730,6 +871,17 @@ int add_rader(Ctx& c, size_t prime, int dir, KArgs a, long long lines, int in_se
     if (rc) return rc;
     *done = true;
     return VKFX_OK;
+}
+
+void note_rader_mixed(Ctx& c, size_t n, const Geometry& g) {
+    c.js << "\"rader_mixed\":{\"len\":" << n << ",\"rader_primes\":[";
+    bool first = true;
+    for (int r : g.radix)
+        if (r > kMaxStockhamRadix) {
+            c.js << (first ? "" : ",") << r;
+            first = false;
+        }
+    c.js << "]},";
 }
 
 // ---- 1-D complex -----------------------------------------------------------
@@ -811,10 +963,24 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
         int rc = add_rader(c, n, dir, a, (long long)batch, SEL_IN, 0, SEL_OUT, 0, &done);
         if (rc || done) return rc;
     }
+    if (alg == Algorithm::Rader && !is_prime(n)) {
+        // composite length with Rader prime factors: one upload of Stockham
+        // stages plus a Rader stage per such factor (mixed_ir.rs)
+        Geometry g0 = geometry_rader(n, prec, 1, c.lds_max, c.lds_max);
+        if (g0.ok) {
+            Geometry g = geometry_rader(n, prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+            KArgs a = blank();
+            a.in_es = a.out_es = 1;
+            a.in_os = a.out_os = (long long)n;
+            a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR;
+            a.scale = sc;
+            note_rader_mixed(c, n, g);
+            return add_launch(c, KK_PLAIN, dir, g, a, (long long)batch, blocks_for(batch, g.G), SEL_IN, 0, SEL_OUT, 0,
+                              "rader_mixed");
+        }
+    }
     if (alg == Algorithm::Rader) c.js << "\"rader_fallback\":\"bluestein\",";
-    // Bluestein (also Rader axes that need the recursive extension, and
-    // composite lengths with a Rader prime factor, which the reference folds
-    // into a mixed-radix tree).
+    // Bluestein (also Rader axes beyond one upload).
     const size_t M = conv_len ? conv_len : next_smooth_at_least(2 * n - 1, {2, 3, 5, 7});
     if (M < 2 * n - 1) return fail(VKFX_ERR_INVALID_ARGUMENT, "Bluestein convolution length below 2N-1");
     Geometry g = kernel_geometry(KK_BLUE_1, prec, -1, M, false, 1, c.lds_max, c.lds_max);
@@ -1026,6 +1192,16 @@ int plan_c2c_nd(Ctx& c, const vkfx_plan_desc& d, uint32_t omit) {
                 rc = add_rader(c, len, dir, a, lines, in_sel, off, SEL_OUT, off, &done);
                 if (rc) return rc;
                 if (done) return VKFX_OK;
+            }
+            if (alg == VKFX_ALG_RADER && !is_prime(len)) {
+                Geometry g0 = geometry_rader(len, prec, 1, c.lds_max, c.lds_max);
+                if (g0.ok) {
+                    const int want = contiguous ? std::max(1, 256 / g0.TT) : (prec ? 8 : 16);
+                    Geometry g = geometry_rader(len, prec, want, c.lds_max, c.lds_budget);
+                    note_rader_mixed(c, len, g);
+                    return add_launch(c, KK_PLAIN, dir, g, a, lines, blocks_for(lines, g.G), in_sel, off, SEL_OUT,
+                                      off, "rader_mixed_axis");
+                }
             }
             const size_t M = d.convolution_len[ax] ? d.convolution_len[ax]
                                                    : next_smooth_at_least(2 * len - 1, {2, 3, 5, 7});
