@@ -178,3 +178,18 @@ def test_r2r_nd_layouts(hip_ctx):
     ym = hip_ctx.execute_transform(irm, x.astype(np.float32))
     assert o.rel_l2(ym, sf.dstn(x.astype(np.float32).astype(np.float64).reshape(batch, 24, 30), type=2,
                                 axes=(1, 2)).reshape(-1)) <= 1e-7
+
+
+@pytest.mark.parametrize("name", KINDS)
+def test_r2r_fft_lengths_follow_reference_reductions(hip_ctx, name):
+    """The complex FFT inside each type has the length of the reference's
+    reduction (r2r_ir.rs:76-110): 2(N-1) for DCT-I, 2(N+1) for DST-I, N for
+    types II and III, N/2 for even type IV and 2N for odd type IV; both
+    directions (the inverse runs the partner type)."""
+    for n in (64, 63):
+        for direction in (FWD, INV):
+            d = hip_ctx.plan(r2r_ir(name, n, 2, F32, direction)).describe()["r2r"]
+            t = int(name[-1])
+            expect = {1: 2 * (n - 1) if name.startswith("dct") else 2 * (n + 1), 2: n, 3: n,
+                      4: n // 2 if n % 2 == 0 else 2 * n}[t]
+            assert d["fft_len"] == expect, (name, n, direction, d)

@@ -183,11 +183,20 @@ int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_
 //   X[k] = s * (im ? -Im : Re)(exp(-i pi (k + q2/2) pq / (2n)) A[k + r])
 // wmode: 0 all 1; 1 DCT-I ends 1, else 2; 2 DCT-III first 1, else 2;
 // 3 DST-III m == n 1, else 2.
+// DCT / DST pre and post passes around a complex FFT of length L (r2r.hip).
+// op selects the reduction: R2R_EXTEND writes each type as the real or
+// imaginary part of a zero-padded DFT of length L = 2(N-1), 2(N+1) or 2N
+// (types I, and odd IV); R2R_REORDER / R2R_SPECTRUM are the length-N forms of
+// types II / III (Makhoul's even-odd reordering); R2R_HALF packs even type IV
+// into L = N/2 complex points. flip: the DST form of II / III / IV (input sign
+// or reversal, output reversal or sign).
+enum R2rOp : int { R2R_EXTEND = 0, R2R_REORDER = 1, R2R_SPECTRUM = 2, R2R_HALF = 3 };
 struct R2rArgs {
     long long n = 0, L = 0, batch = 0;
     long long inner = 1;  // element stride of a line (lines of a strided axis)
     int off = 0, ph = 0, wmode = 0;
     int r = 0, pq = 0, q2 = 0, im = 0;
+    int op = R2R_EXTEND, flip = 0;
     double s = 1.0;
 };
 int launch_r2r(bool pre, int prec, const R2rArgs& p, const void* in, void* out, hipStream_t s);

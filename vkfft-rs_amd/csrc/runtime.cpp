@@ -1530,15 +1530,31 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize, 
     a.n = (long long)n;
     a.batch = (long long)batch;
     a.inner = (long long)inner;
+    // FFT lengths of the reference's reductions (r2r_ir.rs:76-110): 2(N-1)
+    // for DCT-I, 2(N+1) for DST-I, N for types II and III, N/2 for even type
+    // IV (2N for odd type IV)
+    int fft_dir = -1;
     switch (eff) {
         case 0: a.L = 2 * (a.n - 1); a.wmode = 1; break;
-        case 1: a.L = 2 * a.n; a.pq = 1; a.s = 2.0; break;
-        case 2: a.L = 2 * a.n; a.ph = 1; a.wmode = 2; break;
-        case 3: a.L = 2 * a.n; a.ph = 1; a.pq = 1; a.q2 = 1; a.s = 2.0; break;
+        case 1: a.L = a.n; a.op = R2R_REORDER; break;
+        case 2: a.L = a.n; a.op = R2R_SPECTRUM; fft_dir = 1; break;
+        case 3:
+            if (a.n % 2 == 0) {
+                a.L = a.n / 2; a.op = R2R_HALF;
+            } else {
+                a.L = 2 * a.n; a.ph = 1; a.pq = 1; a.q2 = 1; a.s = 2.0;
+            }
+            break;
         case 4: a.L = 2 * (a.n + 1); a.off = 1; a.r = 1; a.im = 1; a.s = 2.0; break;
-        case 5: a.L = 2 * a.n; a.r = 1; a.pq = 1; a.q2 = 2; a.im = 1; a.s = 2.0; break;
-        case 6: a.L = 2 * a.n; a.off = 1; a.ph = 1; a.wmode = 3; a.im = 1; break;
-        default: a.L = 2 * a.n; a.ph = 1; a.pq = 1; a.q2 = 1; a.im = 1; a.s = 2.0; break;
+        case 5: a.L = a.n; a.op = R2R_REORDER; a.flip = 1; break;
+        case 6: a.L = a.n; a.op = R2R_SPECTRUM; a.flip = 1; fft_dir = 1; break;
+        default:
+            if (a.n % 2 == 0) {
+                a.L = a.n / 2; a.op = R2R_HALF; a.flip = 1;
+            } else {
+                a.L = 2 * a.n; a.ph = 1; a.pq = 1; a.q2 = 1; a.im = 1; a.s = 2.0;
+            }
+            break;
     }
     a.s *= scale;
     const size_t L = (size_t)a.L;
@@ -1559,7 +1575,7 @@ int plan_r2r(Ctx& c, size_t n, size_t batch, int kind, int dir, bool normalize, 
     pre.in_sel = in_sel, pre.out_sel = SEL_FULL;
     p->launches.push_back(pre);
     const size_t first = p->launches.size();
-    int rc = plan_c2c_1d(c, L, batch, -1, false, ad.algorithm,
+    int rc = plan_c2c_1d(c, L, batch, fft_dir, false, ad.algorithm,
                          ad.algorithm == Algorithm::Bluestein ? ad.convolution_len : 0);
     if (rc) return rc;
     for (size_t i = first; i < p->launches.size(); ++i) {
