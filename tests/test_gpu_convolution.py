@@ -59,8 +59,20 @@ def test_scalar_kernel(hip_ctx, dims, batch, prec):
     conv, _, _ = run_case(hip_ctx, dims, batch, prec)
     desc = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
     labels = [p["kernel"] for p in desc["passes"]]
-    assert "convolution_multiply" in labels
+    if dims in ([1024], [2048], [360]):
+        # one upload: forward FFT, multiply and normalized inverse in one pass
+        assert desc["convolution"]["fused"] and labels == ["convolution_fused"], labels
+    else:
+        assert not desc["convolution"]["fused"] and "convolution_multiply" in labels
     assert desc["convolution"]["kernels"] == 1 and desc["convolution"]["matrix"] == 0
+
+
+@pytest.mark.parametrize("conj,cross,batch", [(True, False, 3), (False, True, 2), (True, True, 5)])
+def test_fused_convolution_policies(hip_ctx, conj, cross, batch):
+    """Sequence conjugation and cross-power normalization inside the fused
+    one-pass kernel, against the oracle's three-step definition."""
+    conv, _, _ = run_case(hip_ctx, [1536], batch, F32, conj=conj, cross=cross, seed=5)
+    assert vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()["convolution"]["fused"]
 
 
 @pytest.mark.parametrize("dims,prec", [([1024], F32), ([4099], F32), ([32, 40], F64)])

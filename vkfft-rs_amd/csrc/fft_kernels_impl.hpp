@@ -729,6 +729,34 @@ struct IoBlue1 : IoPlain {
     }
 };
 
+// Convolution of one tensor line in one kernel (performConvolution,
+// convolution_ir.rs:4252-4440, with the multiply that the reference fuses
+// into its last forward / first inverse upload): staged load, forward FFT,
+// spectrum multiply in LDS, inverse FFT, store scaled by 1/N (the inverse
+// child is always normalized). Every line (a scalar convolution: one
+// coordinate, one kernel) is multiplied by the one kernel-spectrum plane.
+struct IoConv1 : IoPlain {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
+    static constexpr bool kTwoPass = true;
+    static constexpr int kLoad = LAY_STAGED;
+    static constexpr int kStore = LAY_STAGED;
+    template <typename T, class D>
+    static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        const cpx<T>* spec = (const cpx<T>*)a.spec;
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
+            cpx<T> x = v;
+            if (a.flags & KF_CONV_CONJ) x = conj(x);
+            cpx<T> y = cmul(x, spec[e]);
+            if (a.flags & KF_CONV_CROSS) {
+                const T r = (T)1 / sqrt(y.re * y.re + y.im * y.im);
+                y = mk(y.re * r, y.im * r);
+            }
+            v = y;
+        });
+    }
+};
+
 // Rader, FFT convolution (rader_ir.rs:1957-2101): a[s] = x[g^-s] gathered
 // into LDS, FFT of length p-1 (= N here), multiply by FFT(b)/(p-1) with
 // b[n] = exp(dir 2 pi i g^n / p), inverse FFT, X[g^m] = x0 + conv[m] and
@@ -1263,6 +1291,7 @@ KernelFn pick_dyn(KernelKind kind) {
         case KK_BLUE_1: return k_dyn<T, S, IoBlue1, W>;
         case KK_RADER_FFT: return k_dyn<T, S, IoRader, W>;
         case KK_RADER_DIRECT: return k_rader_direct<T>;
+        case KK_CONV_1: return k_dyn<T, S, IoConv1, W>;
         default: return nullptr;
     }
 }

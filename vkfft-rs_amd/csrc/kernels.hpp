@@ -33,6 +33,7 @@ enum KernelKind : int {
     KK_BLUE_1,         // Bluestein in one kernel (convolution fits LDS)
     KK_RADER_FFT,      // prime length p: gather, FFT(p-1), kernel multiply, IFFT, scatter
     KK_RADER_DIRECT,   // prime length p: gather, O(p^2) cyclic convolution, scatter
+    KK_CONV_1,         // convolution in one kernel: FFT, kernel-spectrum multiply, normalized IFFT
     KK_COUNT
 };
 
@@ -44,6 +45,8 @@ enum KFlags : int {
     KF_DYN_WIDE = 16,     // runtime-shape kernel holding up to 32 elements per thread per stage
     KF_DYN_DIRECT = 32,   // runtime-shape C2C with HBM-direct first and last stages (contiguous lines)
     KF_DYN_PRE = 64,      // with KF_DYN_DIRECT, even C2R: the first stage forms the preprocess from HBM
+    KF_CONV_CONJ = 128,   // KK_CONV_1: conjugate the sequence spectrum (ConvolutionConjugation::Sequence)
+    KF_CONV_CROSS = 256,  // KK_CONV_1: cross-power-spectrum normalization of the product
 };
 
 // Butterflies per thread in one radix-R stage of the runtime-shape kernel

@@ -183,6 +183,7 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     if (a.nstages < 0 || a.nstages > kMaxStages) return (int)hipErrorInvalidValue;
     if (lds_bytes < (size_t)a.G * (size_t)a.LS * (prec ? 16 : 8) || lds_bytes > (size_t)lds_limit_bytes())
         return (int)hipErrorInvalidConfiguration;
+    if (kind == KK_CONV_1 && !a.spec) return (int)hipErrorInvalidConfiguration;
     if (kind == KK_RADER_DIRECT && (a.TT != a.N || a.LS < a.N + 1 || a.N < 1 || !a.pin || !a.pout))
         return (int)hipErrorInvalidConfiguration;
     if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))

@@ -1477,6 +1477,35 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
         }
         return VKFX_OK;
     };
+    c.js << "\"convolution\":{\"coordinates\":" << coords << ",\"kernels\":" << ca.kernel_count << ",\"matrix\":"
+         << ca.matrix << ",\"symmetric\":" << (ca.symmetric ? "true" : "false") << ",\"independent\":"
+         << (ca.independent ? "true" : "false") << ",\"conjugate_sequence\":" << (ca.conj_seq ? "true" : "false")
+         << ",\"cross_power_normalize\":" << (ca.cross_norm ? "true" : "false");
+    // one line per tensor, no coordinate mixing, one upload: the forward FFT,
+    // the multiply and the normalized inverse FFT in one kernel, one HBM pass
+    // (the reference fuses the multiply into its last forward / first inverse
+    // upload, convolution_ir.rs:4252-4440)
+    if (d.rank == 1 && !ca.matrix && ca.kernel_count <= 1 && coords == 1 && d.axis_algorithm[0] == VKFX_ALG_STOCKHAM) {
+        const size_t n = d.dims[0];
+        Geometry g0 = geometry(n, c.prec, 1, c.lds_max, c.lds_max);
+        if (g0.ok) {
+            Geometry g = geometry(n, c.prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+            KArgs a = blank();
+            a.in_es = a.out_es = 1;
+            a.in_os = a.out_os = (long long)n;
+            a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR | (ca.conj_seq ? KF_CONV_CONJ : 0) |
+                      (ca.cross_norm ? KF_CONV_CROSS : 0);
+            a.scale = 1.0 / (double)n;
+            a.spec = kernel;
+            p->full_bytes = 0;
+            p->serial = false;
+            c.js << ",\"fused\":true},";
+            const long long lines = (long long)(d.batch * coords);
+            return add_launch(c, KK_CONV_1, -1, g, a, lines, blocks_for(lines, g.G), SEL_IN, 0, SEL_OUT, 0,
+                              "convolution_fused");
+        }
+    }
+    c.js << ",\"fused\":false},";
     int rc = transform(d.batch * coords, -1, false, SEL_IN, SEL_FULL);
     if (rc) return rc;
     Launch m{};
@@ -1489,24 +1518,20 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
     // the inverse child is always normalized (convolution_ir.rs:4449-4451)
     rc = transform(out_systems * coords, 1, true, SEL_OUT, SEL_OUT);
     if (rc) return rc;
-    c.js << "\"convolution\":{\"coordinates\":" << coords << ",\"kernels\":" << ca.kernel_count << ",\"matrix\":"
-         << ca.matrix << ",\"symmetric\":" << (ca.symmetric ? "true" : "false") << ",\"independent\":"
-         << (ca.independent ? "true" : "false") << ",\"conjugate_sequence\":" << (ca.conj_seq ? "true" : "false")
-         << ",\"cross_power_normalize\":" << (ca.cross_norm ? "true" : "false") << "},";
     return VKFX_OK;
 }
 
 // DCT / DST of length n as one complex FFT of length L between a pre and a
-// post pass (r2r.hip). Parameters per effective type, with every cosine or
-// sine sum written as the real or imaginary part of a zero-padded DFT:
-//   DCT-I   L = 2(n-1): a_j = w_j x_j (w = 1 at the ends, 2 inside), X_k = Re A_k
-//   DCT-II  L = 2n:     a_j = x_j, X_k = 2 Re(e^{-i pi k/2n} A_k)
-//   DCT-III L = 2n:     a_j = w_j x_j e^{-i pi j/2n} (w_0 = 1, else 2), X_k = Re A_k
-//   DCT-IV  L = 2n:     a_j = x_j e^{-i pi j/2n}, X_k = 2 Re(e^{-i pi (k+1/2)/2n} A_k)
-//   DST-I   L = 2(n+1): a_{j+1} = x_j, X_k = -2 Im A_{k+1}
-//   DST-II  L = 2n:     a_j = x_j, X_k = -2 Im(e^{-i pi (k+1)/2n} A_{k+1})
-//   DST-III L = 2n:     a_{j+1} = w x_j e^{-i pi (j+1)/2n} (w = 2, 1 at j = n-1), X_k = -Im A_k
-//   DST-IV  L = 2n:     a_j = x_j e^{-i pi j/2n}, X_k = -2 Im(e^{-i pi (k+1/2)/2n} A_k)
+// post pass (r2r.hip, which states the algebra of each reduction):
+//   DCT-I   L = 2(n-1): even extension (w = 1 at the ends, 2 inside), Re
+//   DST-I   L = 2(n+1): odd extension, -2 Im
+//   DCT-II  L = n:      Makhoul reordering, 2 Re(e^{-i pi k/2n} V_k)
+//   DCT-III L = n:      V_j = e^{i pi j/2n} (x_j - i x_{n-j}), inverse FFT, un-reorder
+//   DCT-IV  L = n/2 (even n): z_j = (x_2j + i x_{n-1-2j}) e^{-i pi (4j+1)/4n},
+//           outputs 2 Re / -2 Im of e^{-i pi j/n} Z_j; odd n: L = 2n extension
+//   DST-II/III/IV: the DCT forms with the input sign or reversal and the
+//           output reversal or sign (DST-II_k = DCT-II((-1)^j x)_{n-1-k},
+//           DST-III_k = (-1)^k DCT-III(reversed x)_k, same for type IV)
 // The inverse direction runs the type's inverse partner (II <-> III,
 // r2r_ir.rs:2308-2316), scaled when normalized (inverse_pair_scale,
 // r2r_ir.rs:2318-2346).
