@@ -134,6 +134,16 @@ def test_register_exchange_kernel(idx_ctx):
         assert p["lds_bytes"] == 0 and p["lines_per_block"] == 4 and p["radices"] == [16, 4, 16], p
 
 
+@pytest.mark.parametrize("n,kind,pick", [(1024, 0, 0), (1024, 0, 1), (4099, 12, 0), (4099, 12, 1), (4099, 12, 2)])
+def test_fixed_shape_variants(idx_ctx, n, kind, pick):
+    """Per-stage twiddle tables and pads, ping-pong LDS buffers and the
+    product-tree forms of the C1 and M = 8232 shapes move the same elements."""
+    env = {f"VKFX_FIXED_PICK_K{kind}": str(pick)}
+    for batch, direction in ((5, FWD), (3, INV)):
+        d = check_1d(idx_ctx, n, batch, F32, direction, env=env)
+        assert d["passes"][0]["fixed_shape"]
+
+
 @pytest.mark.parametrize("n,batch,prec", [(1 << 20, 2, F32), (1 << 17, 3, F32), (3 ** 12, 1, F32),
                                           (1 << 18, 2, F64), (5 ** 8, 1, F64)])
 def test_four_step(idx_ctx, n, batch, prec):

@@ -598,6 +598,30 @@ def test_register_exchange_kernel_1024(hip_ctx, batch, direction):
         plan.close()
 
 
+@pytest.mark.parametrize("n,batch,kind,pick,lds", [
+    (1024, 37, 0, 0, 1088 * 8), (1024, 37, 0, 1, 1088 * 8), (1024, 37, 0, 3, 1056 * 8),
+    (4099, 6, 12, 0, 9261 * 8), (4099, 6, 12, 1, 2 * 9261 * 8), (4099, 6, 12, 2, 8489 * 8)])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_fixed_shape_variants(hip_ctx, n, batch, kind, pick, lds, direction):
+    """Each registered variant of the C1 and M = 8232 Bluestein shapes
+    (per-stage twiddle tables and pads, ping-pong LDS buffers, product-tree
+    twiddles with one uniform pad) against the oracle, both directions."""
+    if n == 1024 and pick == 3 and direction == INV:
+        pytest.skip("the one-slot-per-32 padding is registered for the forward direction only")
+    normalize = direction == INV
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_inverse_normalization(normalize)
+    ir = vk.TransformIr.build(cfg, direction)
+    plan = _plan_with_env(hip_ctx, ir, {f"VKFX_FIXED_PICK_K{kind}": str(pick)})
+    try:
+        (p,) = plan.describe()["passes"]
+        assert p["fixed_shape"] and p["lds_bytes"] == lds, p
+        x = rand(n * batch, 300 + pick)
+        y = _run_plan(hip_ctx, plan, x, n * batch)
+        assert o.rel_l2(y, oracle_c2c(x, n, direction, normalize)) <= TOL[F32]
+    finally:
+        plan.close()
+
+
 def test_register_exchange_kernel_nd_rows(hip_ctx):
     """The register-exchange kernel as the contiguous-axis pass of N-D plans."""
     for dims, batch in (([8, 1024], 2), ([3, 5, 1024], 1)):

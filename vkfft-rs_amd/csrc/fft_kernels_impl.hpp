@@ -1037,6 +1037,9 @@ template <int N_, int TT_, int G_, int PS_, int LS_, bool COL_, int... R>
 struct Shape {
     static constexpr int WPE = 0;  // waves-per-EU hint (0 = compiler default)
     static constexpr bool NTI = false, NTO = false;  // nontemporal HBM loads / stores
+    static constexpr bool PP = false;  // ping-pong LDS buffers (see PingPong)
+    static constexpr bool TWT = false;  // per-stage twiddle tables (see StageTables)
+    static constexpr bool SPAD = false;  // per-stage LDS pads (see StagePads)
     static constexpr int N = N_, TT = TT_, G = G_, PS = PS_, LS = LS_;
     static constexpr bool COL = COL_;
     static_assert(LS_ >= N_ + ((N_ - 1) >> PS_), "LDS line stride too small");
@@ -1079,10 +1082,19 @@ __device__ __forceinline__ int lds_out(int base, int q) {
 // 1 = HBM through the IO policy's element functions.
 // MID: this stage ends the first FFT of a two-pass kernel and applies the
 // policy's pointwise product (IO::mid_elem) to its outputs on the way to LDS.
+// PP: ping-pong; the stage reads `line` and writes `out` (a second LDS
+// buffer), so no barrier separates its reads from its writes. Otherwise it
+// works in place on `line` (`out` is unused).
+// TOFF >= 0: the stage's twiddles W_{PR}^(k i), i = 1..R-1, are entries
+// TOFF + k (R - 1) + i - 1 of the per-stage table at tw.full (FT_STAGE_PR
+// layout); otherwise one root per butterfly from the W_N table and a product
+// tree for its powers.
+// PS: pad shift of the LDS buffer the stage reads; PSO: of the one it writes.
 template <typename T, int S, class IO, int N, int P, int R, int TT, int PS, int SRC, int DST, bool NTI, bool NTO,
-          bool MID = false>
-__device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line, const LineInfo& L, int t,
-                                       const StageTw& tw) {
+          bool MID = false, bool PP = false, int TOFF = -1, int PSO = PS>
+__device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line, cpx<T>* __restrict__ out,
+                                       const LineInfo& L, int t, const StageTw& tw) {
+    cpx<T>* __restrict__ dst = PP ? out : line;
     constexpr int NB = N / R;
     constexpr int MJ = (NB + TT - 1) / TT;
     constexpr bool EXACT = (NB % TT) == 0;
@@ -1123,7 +1135,7 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
             }
         }
     }
-    if constexpr (!SRC) __syncthreads();
+    if constexpr (!SRC && !PP) __syncthreads();
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
         const int b = t + j * TT;
@@ -1132,7 +1144,12 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
             if constexpr (P > 1) {
                 constexpr int step = N / (P * R);
                 cpx<T> wp[R];
-                root_powers<R>(stage_root<T>(tw, k * step, P >= kScatterP), wp);
+                if constexpr (TOFF >= 0) {
+#pragma unroll
+                    for (int i = 1; i < R; ++i) wp[i] = ld_table<T>(tw.full, TOFF + k * (R - 1) + i - 1);
+                } else {
+                    root_powers<R>(stage_root<T>(tw, k * step, P >= kScatterP), wp);
+                }
 #pragma unroll
                 for (int i = 1; i < R; ++i) v[j][i] = twmul<S>(v[j][i], wp[i]);
             }
@@ -1171,9 +1188,9 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                         if (L.valid) IO::template store_elem<T, S, NTO>(a, L, base + q * P, v[j][q]);
                     } else {
                         if constexpr (MID) {
-                            line[lds_out<PS, P, R>(base, q)] = IO::template mid_elem<T>(a, L, base + q * P, v[j][q]);
+                            dst[lds_out<PSO, P, R>(base, q)] = IO::template mid_elem<T>(a, L, base + q * P, v[j][q]);
                         } else {
-                            line[lds_out<PS, P, R>(base, q)] = v[j][q];
+                            dst[lds_out<PSO, P, R>(base, q)] = v[j][q];
                         }
                     }
                 }
@@ -1183,13 +1200,43 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
     if constexpr (!DST) __syncthreads();
 }
 
-template <typename T, int S, class IO, class Sh, int SRC0, int DSTL, bool MIDL, int P, int R, int... Rest>
-__device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, const LineInfo& L, int t,
+// Runs the stages of Sh over one line. With ping-pong buffers stage k
+// (1-based) writes `alt` when k is odd and `line` when k is even.
+template <int R, int... Rest>
+constexpr int rlist_head(RList<R, Rest...>) {
+    return R;
+}
+// Per-stage pad of a stage's output buffer (StagePads shapes): the first
+// stage (P = 1) writes its R outputs R slots apart across lanes, which one
+// pad slot every R elements spreads over the banks when R is a power of two
+// and the next stage's input stride N/Rn is a multiple of R (its reads then
+// keep compile-time offsets); every other Stockham write and read is
+// contiguous across lanes up to block steps that stay bank-distinct, so
+// those buffers carry no pad (and no per-element pad arithmetic).
+template <int N, int P, int R, int Rn>
+constexpr int stage_pad() {
+    return (P == 1 && Rn > 0 && (R & (R - 1)) == 0 && (N / Rn) % R == 0) ? (R == 2 ? 1 : R == 4 ? 2 : R == 8 ? 3 : 4)
+                                                                         : 30;
+}
+
+// TO: offset of this stage's block in the per-stage twiddle table (stages
+// with P > 1 hold P (R - 1) entries each, in radix order). PSI: pad of the
+// buffer the stage reads.
+template <typename T, int S, class IO, class Sh, int SRC0, int DSTL, bool MIDL, int P, int TO = 0,
+          int PSI = (Sh::SPAD ? 30 : Sh::PS), int R, int... Rest>
+__device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, cpx<T>* alt, const LineInfo& L, int t,
                                         const StageTw& tw, RList<R, Rest...>) {
     constexpr bool last = sizeof...(Rest) == 0;
-    fstage<T, S, IO, Sh::N, P, R, Sh::TT, Sh::PS, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO,
-           last && MIDL && !DSTL>(a, line, L, t, tw);
-    if constexpr (!last) fstages<T, S, IO, Sh, SRC0, DSTL, MIDL, P * R>(a, line, L, t, tw, RList<Rest...>{});
+    constexpr int PSO = !Sh::SPAD ? Sh::PS : last ? 30 : stage_pad<Sh::N, P, R, rlist_head(RList<Rest..., 0>{})>();
+    fstage<T, S, IO, Sh::N, P, R, Sh::TT, PSI, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO,
+           last && MIDL && !DSTL, Sh::PP, Sh::TWT ? TO : -1, PSO>(a, line, alt, L, t, tw);
+    if constexpr (!last)
+        fstages<T, S, IO, Sh, SRC0, DSTL, MIDL, P * R, TO + (P > 1 ? P * (R - 1) : 0), PSO>(
+            a, Sh::PP ? alt : line, Sh::PP ? line : alt, L, t, tw, RList<Rest...>{});
+}
+template <int... R>
+constexpr int rlist_size(RList<R...>) {
+    return (int)sizeof...(R);
 }
 
 template <class IO, bool COL>
@@ -1216,6 +1263,14 @@ __device__ __forceinline__ void fix_body(const KArgs& a, cpx<T>* lds, LineInfo* 
         __syncthreads();
     }
     cpx<T>* line = lds + g * Sh::LS;
+    // ping-pong shapes hold a second buffer of G lines behind the first; the
+    // prologue fills the first, the stages alternate and the last stage
+    // stores to HBM, so the policy's LDS-wide steps never see the second
+    static_assert(!Sh::PP || (SD && (!IO::kTwoPass || IO::kMidFused)),
+                  "ping-pong shapes need a direct last stage and a fused mid product");
+    static_assert(!Sh::SPAD || (LD && SD && (!IO::kTwoPass || IO::kMidFused)),
+                  "per-stage pads need direct first and last stages and a fused mid product");
+    cpx<T>* alt = Sh::PP ? lds + (Sh::G + g) * Sh::LS : line;
     const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
     const LineInfo L = kOwnLine ? IO::line(a, blk, g) : li[g];
     if constexpr (!LD) {
@@ -1223,14 +1278,17 @@ __device__ __forceinline__ void fix_body(const KArgs& a, cpx<T>* lds, LineInfo* 
         __syncthreads();
     }
     if constexpr (IO::kTwoPass) {
-        fstages<T, S, IO, Sh, LD ? 1 : 0, 0, IO::kMidFused, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        fstages<T, S, IO, Sh, LD ? 1 : 0, 0, IO::kMidFused, 1>(a, line, alt, L, t, tw, typename Sh::Radices{});
         if constexpr (!IO::kMidFused) {
             IO::template mid<T, D>(a, lds, li);
             __syncthreads();
         }
-        fstages<T, -S, IO, Sh, 0, SD ? 1 : 0, false, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        // the first FFT's output sits in `alt` after an odd number of stages
+        constexpr bool odd = (rlist_size(typename Sh::Radices{}) & 1) != 0;
+        fstages<T, -S, IO, Sh, 0, SD ? 1 : 0, false, 1>(a, Sh::PP && odd ? alt : line, Sh::PP && odd ? line : alt,
+                                                        L, t, tw, typename Sh::Radices{});
     } else {
-        fstages<T, S, IO, Sh, LD ? 1 : 0, SD ? 1 : 0, false, 1>(a, line, L, t, tw, typename Sh::Radices{});
+        fstages<T, S, IO, Sh, LD ? 1 : 0, SD ? 1 : 0, false, 1>(a, line, alt, L, t, tw, typename Sh::Radices{});
     }
     if constexpr (!SD) IO::template epilogue<T, S, D>(a, lds, li);
 }
@@ -1242,6 +1300,29 @@ __global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix(const KArgs a) {
     __shared__ LineInfo li[Sh::G];
     fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, group_index(a));
 }
+
+// Two LDS buffers of G lines each: every stage reads one and writes the
+// other, one barrier per stage instead of two (for shapes whose LDS use
+// leaves room for the second buffer at the residency they already have).
+template <class Base>
+struct PingPong : Base {
+    static constexpr bool PP = true;
+};
+
+// Stage twiddles read from a per-stage table (FT_STAGE_PR) instead of one
+// root and a product tree per butterfly: R-1 loads in place of R-2 complex
+// multiplications (and the two-level lookup of large P).
+template <class Base>
+struct StageTables : Base {
+    static constexpr bool TWT = true;
+};
+
+// Each stage's output buffer carries its own pad (stage_pad); Sh::PS is the
+// smallest pad any stage uses, so LS covers every buffer.
+template <class Base>
+struct StagePads : Base {
+    static constexpr bool SPAD = true;
+};
 
 // Variant shapes for tuning: a waves-per-EU occupancy hint and nontemporal IO.
 template <class Base, int W, bool NTIN, bool NTOUT>
@@ -1316,6 +1397,44 @@ KernelFn pick(KernelKind kind, bool wide, int direct) {
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                               \
             (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>), \
             (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)              \
+    }
+// A ping-pong shape (two LDS buffers per line, lds_mult 2).
+#define VKFX_FIXED_PP(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                              \
+    FixedKernel {                                                                                              \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
+            (KernelFn)(k_fix_occ<T, S, IO, PingPong<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>), \
+            nullptr, FT_STAGE, 2                                                                               \
+    }
+// Ping-pong with per-stage twiddle tables.
+#define VKFX_FIXED_PPT(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                            \
+    FixedKernel {                                                                                              \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
+            (KernelFn)(k_fix_occ<T, S, IO,                                                                     \
+                                 StageTables<PingPong<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>>), \
+            nullptr, FT_STAGE_PR, 2                                                                            \
+    }
+// Ping-pong with per-stage twiddle tables and per-stage pads.
+#define VKFX_FIXED_PPTS(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                           \
+    FixedKernel {                                                                                              \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
+            (KernelFn)(k_fix_occ<T, S, IO,                                                                     \
+                                 StagePads<StageTables<PingPong<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>>>), \
+            nullptr, FT_STAGE_PR, 2                                                                            \
+    }
+// In place with per-stage twiddle tables (the shape's own pad).
+#define VKFX_FIXED_T(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                               \
+    FixedKernel {                                                                                              \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
+            (KernelFn)(k_fix_occ<T, S, IO, StageTables<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>), \
+            nullptr, FT_STAGE_PR, 1                                                                            \
+    }
+// In place (one LDS buffer) with per-stage twiddle tables and pads, and a
+// waves-per-EU hint W.
+#define VKFX_FIXED_TS(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, W, NTI, NTO, ...)                           \
+    FixedKernel {                                                                                              \
+        KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
+            (KernelFn)(k_fix_occ<T, S, IO, StagePads<StageTables<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>>>), \
+            nullptr, FT_STAGE_PR, 1                                                                            \
     }
 // A shape without the persistent variant (it launches as one block per group
 // under VKFX_PERSIST_BLOCKS_PER_CU as well).

@@ -122,7 +122,10 @@ using KernelFn = void (*)(const KArgs);
 // Twiddle table a fixed shape reads through KArgs::tw: the stage roots
 // exp(-2 pi i k/N), k < N (FT_STAGE), or the lane-ordered table of the
 // register-exchange 1024-point kernel (FT_WAVE1024, fft_wave.hpp).
-enum FixedTable : int { FT_STAGE = 0, FT_WAVE1024 = 1 };
+// FT_STAGE_PR: per-stage blocks in radix order, one per stage with P > 1
+// (P = product of the earlier radices), P (R - 1) entries each: entry
+// k (R - 1) + i - 1 = exp(-2 pi i k i / (P R)).
+enum FixedTable : int { FT_STAGE = 0, FT_WAVE1024 = 1, FT_STAGE_PR = 2 };
 // Complex entries of the FT_WAVE1024 table: 4 x 64 lane roots of the pass-1
 // twiddles, then 4 roots of the pass-2 twiddles.
 constexpr int kWave1024TableLen = 260;
@@ -138,6 +141,7 @@ struct FixedKernel {
     KernelFn fn;          // one block per group of G lines
     KernelFn fn_persist;  // grid-stride over groups, grid sized to residency
     int table = FT_STAGE;
+    int lds_mult = 1;  // 2: ping-pong shapes hold two LDS buffers of G lines
 };
 
 // Finds a fixed-shape kernel for (kind, precision, first-FFT direction,

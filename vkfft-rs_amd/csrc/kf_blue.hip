@@ -1,13 +1,18 @@
-// Fixed-shape Bluestein kernels (C5): N = 4099 with M = 8232 in one kernel
-// (686 threads per line; VKFX_FIXED_PICK=1 selects 448),
-// N = 65537 with M = 131220 = 405 x 324 in three passes.
+// Fixed-shape Bluestein kernels: M = 8232 (N = 4099) in one kernel of 686
+// threads per line, M = 131220 = 405 x 324 (N = 65537) in three passes.
 #include "fft_kernels_impl.hpp"
 
 namespace vkfx {
 
 static const FixedKernel kTable[] = {
+    // M = 8232: in place with per-stage twiddle tables and pads, 80 VGPRs so
+    // two 74 KiB blocks share a CU; then the ping-pong form (one block per
+    // CU, one barrier per stage) and the in-place form with product-tree
+    // twiddles and one uniform pad (VKFX_FIXED_PICK_K12=1, 2)
+    VKFX_FIXED_TS(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 3, 9261, false, 6, true, true, 8, 3, 7, 7, 7),
+    VKFX_FIXED_PPTS(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 3, 9261, false, true, true, 8, 3, 7, 7, 7),
     VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
-    VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 448, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
+    // M = 131220: product-tree twiddles (per-stage tables measured 4% slower)
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, false, false, 4, 9, 9),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 407, true, false, true, 9, 9, 5),

@@ -106,7 +106,7 @@ const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto) {
         const FixedKernel& v = all[i];
         if (v.kind != f->kind || v.prec != f->prec || v.dir != f->dir || v.N != f->N || v.col != f->col ||
             v.TT != f->TT || v.G != f->G || v.PS != f->PS || v.LS != f->LS || v.nst != f->nst || v.nti != nti ||
-            v.nto != nto)
+            v.nto != nto || v.table != f->table || v.lds_mult != f->lds_mult)
             continue;
         bool same = true;
         for (int s = 0; s < v.nst; ++s) same = same && v.radix[s] == f->radix[s];
@@ -181,7 +181,8 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         (unsigned)(a.G * a.TT) != block)
         return (int)hipErrorInvalidConfiguration;
     if (a.nstages < 0 || a.nstages > kMaxStages) return (int)hipErrorInvalidValue;
-    if (lds_bytes < (size_t)a.G * (size_t)a.LS * (prec ? 16 : 8) || lds_bytes > (size_t)lds_limit_bytes())
+    if (lds_bytes < (size_t)a.G * (size_t)a.LS * (prec ? 16 : 8) * (fixed ? fixed->lds_mult : 1) ||
+        lds_bytes > (size_t)lds_limit_bytes())
         return (int)hipErrorInvalidConfiguration;
     if (kind == KK_CONV_1 && !a.spec) return (int)hipErrorInvalidConfiguration;
     if (kind == KK_RADER_DIRECT && (a.TT != a.N || a.LS < a.N + 1 || a.N < 1 || !a.pin || !a.pout))
@@ -202,6 +203,7 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     // the register-exchange kernels address contiguous lines (element stride 1)
     if (fixed && fixed->table == FT_WAVE1024 && (a.in_es != 1 || a.out_es != 1 || !a.tw))
         return (int)hipErrorInvalidConfiguration;
+    if (fixed && fixed->table == FT_STAGE_PR && !a.tw) return (int)hipErrorInvalidConfiguration;
     if (fixed) {
         // the fixed shape must be launched with exactly its own geometry
         if (fixed->kind != kind || fixed->prec != prec || fixed->dir != dir || fixed->N != a.N ||

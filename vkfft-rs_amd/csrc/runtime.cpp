@@ -287,7 +287,7 @@ Geometry kernel_geometry(KernelKind kind, int prec, int dir, size_t n, bool col,
             g.PS = f->PS;
             g.LS = f->LS;
             g.radix.assign(f->radix, f->radix + f->nst);
-            g.lds = (size_t)g.G * g.LS * (prec ? 16 : 8);
+            g.lds = (size_t)g.G * g.LS * (prec ? 16 : 8) * f->lds_mult;
             g.fixed = f;
             g.ok = g.lds <= lds_max;
             if (g.ok) return g;
@@ -405,6 +405,36 @@ int wave1024_table(vkfx_plan* p, int prec, const void** dev) {
     for (int j = 0; j < 4; ++j)
         for (int l = 0; l < 64; ++l) root((ld)((l << j) % 1024), 1024.0L, re[j * 64 + l], im[j * 64 + l]);
     for (int m = 0; m < 4; ++m) root((ld)m, 64.0L, re[256 + m], im[256 + m]);
+    auto b = pack(re, im, prec);
+    return upload(p, key, b.data(), b.size(), dev);
+}
+
+// Per-stage twiddle blocks of a fixed shape (FT_STAGE_PR layout, kernels.hpp).
+int stage_pr_table(vkfx_plan* p, const FixedKernel* f, int prec, const void** dev) {
+    std::string key = "stage_pr:" + std::to_string(prec);
+    for (int s = 0; s < f->nst; ++s) key += ":" + std::to_string(f->radix[s]);
+    if (p->table_cache.count(key)) {
+        *dev = p->table_cache[key];
+        return VKFX_OK;
+    }
+    std::vector<ld> re, im;
+    long long P = 1;
+    for (int s = 0; s < f->nst; ++s) {
+        const long long R = f->radix[s];
+        if (P > 1)
+            for (long long k = 0; k < P; ++k)
+                for (long long i = 1; i < R; ++i) {
+                    ld x, y;
+                    root((ld)((k * i) % (P * R)), (ld)(P * R), x, y);
+                    re.push_back(x);
+                    im.push_back(y);
+                }
+        P *= R;
+    }
+    if (re.empty()) {
+        re.push_back(1.0L);
+        im.push_back(0.0L);
+    }
     auto b = pack(re, im, prec);
     return upload(p, key, b.data(), b.size(), dev);
 }
@@ -717,8 +747,9 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
             (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128)
             a.flags |= KF_DYN_PRE;
     }
-    int rc = (g.fixed && g.fixed->table == FT_WAVE1024) ? wave1024_table(c.p, c.prec, &a.tw)
-                                                        : stage_table(c.p, g.N, c.prec, &a.tw);
+    int rc = (g.fixed && g.fixed->table == FT_WAVE1024)   ? wave1024_table(c.p, c.prec, &a.tw)
+             : (g.fixed && g.fixed->table == FT_STAGE_PR) ? stage_pr_table(c.p, g.fixed, c.prec, &a.tw)
+                                                          : stage_table(c.p, g.N, c.prec, &a.tw);
     if (rc) return rc;
     rc = two_level(c.p, g.N, c.prec, &a.swlo, &a.swhi, &a.swshift);
     if (rc) return rc;
