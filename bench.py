@@ -289,51 +289,83 @@ def _cpu_model():
     return "unknown"
 
 
-def cpu_baseline(cfg, budget_s=15.0):
+def cpu_baseline(cfg, budget_s=15.0, single_s=2.0):
     """The oracle (C port of reference.rs, f64) on a bounded sample of the
-    config: one thread (the reference is single-threaded) for about 2 s, then
-    batch-parallel on this GPU's share of the host cores for about budget_s
-    of CPU work."""
+    config, as effective GB/s of the config's own byte count: one thread (the
+    reference is single-threaded) for about single_s, then batch-parallel on
+    this GPU's share of the host cores for about budget_s of CPU work. A unit
+    of work is one transform of a 1-D C2C line, one R2C + C2R round trip of a
+    real line, or, for N-D transforms, the line FFTs of every axis (the
+    separable driver's work per tensor, timed on contiguous lines of each axis
+    length; its strided gathers are not included, so the CPU figure is an
+    upper bound)."""
     import numpy as np
 
     from oracle import oracle as o
 
     nproc = os.cpu_count() or 1
     threads = min(16, nproc)  # one GPU's share of the box's cores
+    dims = cfg["dims"]
     n = 1
-    for d in cfg["dims"]:
+    for d in dims:
         n *= d
-    if len(cfg["dims"]) > 1 or cfg["kind"] != "c2c":
-        return None
     es = 8 if cfg["prec"] == "f32" else 16
-    x1 = o.complex_uniform(n * 64, 1, np.complex128)
-    o.fft_batch(x1[:n], n)
-    # single thread
-    done1, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 2.0:
-        o.fft_batch(x1, n, threads=1)
-        done1 += 64
-    wall1 = time.perf_counter() - t0
-    per = wall1 / done1
-    # all of this GPU's share of the cores
-    batch = min(cfg["batch"], max(threads, int(budget_s / per)))
-    reps = max(1, int(round(budget_s / (per * batch))))
-    x = o.complex_uniform(n * batch, 2, np.complex128)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        o.fft_batch(x, n, threads=threads)
-    wall = time.perf_counter() - t0
-    done = batch * reps
-    bytes_done = 2 * n * done * es
-    return {"value": round(bytes_done / wall / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+    nbytes, _ = algorithmic(dict(cfg, batch=1))  # bytes of one tensor / transform
+
+    def pool(length):  # lines of input held for the timing calls
+        return max(threads, 4) if length > 65536 else 64
+
+    # per axis length: (lines of that length per tensor, line-unit runner)
+    if cfg["kind"] == "r2c_c2r":
+        def runner(length):
+            r = o.normal(length * pool(length), 3)
+
+            def go(lines, th):
+                spec = o.r2c_batch(r[:length * lines], length, threads=th)
+                o.c2r_batch(spec, length, True, threads=th)
+            return go
+        axes = [(dims[0], 1)]
+    else:
+        def runner(length):
+            x = o.complex_uniform(length * pool(length), 1, np.complex128)
+
+            def go(lines, th):
+                xs = x if lines * length <= x.size else np.resize(x, lines * length)
+                o.fft_batch(xs[:lines * length], length, threads=th)
+            return go
+        axes = [(d, n // d) for d in dims]
+
+    def rate(th, seconds, min_lines):
+        """seconds per tensor with `th` threads, timing each axis length for
+        its share of `seconds`"""
+        per_tensor, lines_done = 0.0, 0
+        for length, lines_per_tensor in axes:
+            go = runner(length)
+            lines = max(min_lines, 1)
+            go(1, 1)  # warm
+            done, t0 = 0, time.perf_counter()
+            while True:
+                go(lines, th)
+                done += lines
+                if time.perf_counter() - t0 >= seconds / len(axes):
+                    break
+            per_line = (time.perf_counter() - t0) / done
+            per_tensor += per_line * lines_per_tensor
+            lines_done += done
+        return per_tensor, lines_done
+
+    per1, lines1 = rate(1, single_s, 1)
+    perT, linesT = rate(threads, budget_s / threads, threads)
+    unit = "transform" if len(dims) == 1 else "tensor"
+    return {"value": round(nbytes / perT / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "host_nproc": nproc, "cpu_model": _cpu_model(),
-            "single_thread": {"us_per_transform": round(per * 1e6, 2),
-                              "value": round(2 * n * es / per / 1e9, 4), "unit": "GB/s",
-                              "transforms": done1},
-            "all_cores_us_per_transform": round(wall / done * 1e6, 3),
-            "sample": f"1 thread: {done1} transforms of N={n} in {wall1:.2f} s; {threads} threads: {reps} x {batch} "
-                      f"transforms (of batch {cfg['batch']}) in {wall:.2f} s wall, ~{per * done:.1f} s CPU work; "
-                      f"the oracle (C port of reference.rs, f64)"}
+            "single_thread": {"us_per_" + unit: round(per1 * 1e6, 2), "value": round(nbytes / per1 / 1e9, 4),
+                              "unit": "GB/s", "lines": lines1},
+            "all_cores_us_per_" + unit: round(perT * 1e6, 3),
+            "sample": f"1 thread: {lines1} lines in ~{single_s:.0f} s; {threads} threads: {linesT} lines in "
+                      f"~{budget_s / threads:.1f} s wall (~{budget_s:.0f} s CPU work); axis lengths "
+                      f"{[a for a, _ in axes]}; the oracle (C port of reference.rs, f64)"
+                      + ("; N-D: per-axis line FFTs only" if len(dims) > 1 else "")}
 
 
 def hbm_sweeps(info, cfg):
@@ -528,8 +560,12 @@ def main():
         lines_out[0][1]["configs"] = table
     if not args.no_cpu:
         for name, out in lines_out:
-            if name == "c1":
-                out["cpu_baseline"] = cpu_baseline(CONFIGS["c1"])
+            out["cpu_baseline"] = cpu_baseline(CONFIGS[name], 15.0 if name == "c1" else 6.0,
+                                               2.0 if name == "c1" else 1.0)
+            for other, row in (out.get("configs") or {}).items():
+                cb = cpu_baseline(CONFIGS[other], 4.0, 1.0)
+                row["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+                row["cpu_baseline"]["single_thread_gbs"] = cb["single_thread"]["value"]
     for _, out in lines_out:
         print(json.dumps(out), flush=True)
 
