@@ -13,6 +13,8 @@ out[k] = in[src[k]] (src = -1: a zero of Bluestein padding).
   826-864, 1042-1238): a line of M = N1*N2 is the matrix x[n1*N2 + n2]; the
   column pass transforms over n1 for each n2 and keeps the layout, the row
   pass transforms over n2 for each k1 and stores X[k1 + N1*k2].
+- Three uploads (FourStepThreeUpload, src/kernel_ir.rs:1206-1236): the same
+  four-step with each row of N2 = M1*M2 transformed by a four-step of its own.
 - Bluestein (src/bluestein_ir.rs:933-1089): a = x zero-padded to M, FFT_M,
   spectrum multiply, inverse FFT_M, truncation to N.
 
@@ -74,6 +76,20 @@ def four_step_perm(n1: int, rad1, n2: int, rad2) -> np.ndarray:
     k2 = np.arange(n2)[None, :]
     src = np.empty(n1 * n2, dtype=np.int64)
     src[(k1 + n1 * k2).reshape(-1)] = (sa[k1] * n2 + sb[k2]).reshape(-1)
+    return src
+
+
+def three_pass_perm(n1: int, rad1, m1: int, rad2, m2: int, rad3) -> np.ndarray:
+    """src of a three-upload line of M = n1*n2, n2 = m1*m2 (FourStepThreeUpload,
+    src/kernel_ir.rs:1206-1236, as a four-step whose rows are four-steps):
+    X[k1 + n1*k2] = x[sa[k1]*n2 + sub[k2]], sub = four_step_perm(m1, m2)."""
+    n2 = m1 * m2
+    sa = stockham_perm(n1, rad1)
+    sub = four_step_perm(m1, rad2, m2, rad3)
+    k1 = np.arange(n1)[:, None]
+    k2 = np.arange(n2)[None, :]
+    src = np.empty(n1 * n2, dtype=np.int64)
+    src[(k1 + n1 * k2).reshape(-1)] = (sa[k1] * n2 + sub[k2]).reshape(-1)
     return src
 
 

@@ -83,6 +83,10 @@ def line_map_1d(n, desc):
     if names[:2] == ["four_step_columns", "four_step_rows"]:
         a, b = ps[0], ps[1]
         return im.four_step_perm(a["fft_len"], a["radices"], b["fft_len"], b["radices"])
+    if names[:3] == ["three_upload_pass1", "three_upload_pass2", "three_upload_pass3"]:
+        a, b, c = ps[:3]
+        return im.three_pass_perm(a["fft_len"], a["radices"], b["fft_len"], b["radices"], c["fft_len"],
+                                  c["radices"])
     if names[0] == "bluestein_single":
         return im.bluestein_single_perm(n, ps[0]["fft_len"], ps[0]["radices"])
     if names[:3] == ["bluestein_columns", "bluestein_rows", "bluestein_columns_out"]:
@@ -132,6 +136,17 @@ def test_register_exchange_kernel(idx_ctx):
         d = check_1d(idx_ctx, 1024, batch, F32, direction, env=env)
         (p,) = d["passes"]
         assert p["lds_bytes"] == 0 and p["lines_per_block"] == 4 and p["radices"] == [16, 4, 16], p
+
+
+@pytest.mark.parametrize("n,cap,prec", [(4096, 16, F32), (2187, 27, F64), (3072, 16, F32), (1 << 20, 128, F32)])
+def test_three_upload(idx_ctx, n, cap, prec):
+    """Lengths with no two-upload split (forced by capping the one-upload
+    length): three passes, every chunk and lane."""
+    env = {"VKFX_MAX_UPLOAD": str(cap)}
+    for batch, direction in ((3, FWD), (2, INV)):
+        d = check_1d(idx_ctx, n, batch, prec, direction, env=env)
+        assert d["four_step"]["uploads"] == 3, d["four_step"]
+    d = check_1d(idx_ctx, n, 9, prec, env=dict(env, VKFX_WORK_BUDGET_MB="0"))
 
 
 @pytest.mark.parametrize("n,kind,pick", [(1024, 0, 0), (1024, 0, 1), (4099, 12, 0), (4099, 12, 1), (4099, 12, 2)])

@@ -622,6 +622,71 @@ def test_fixed_shape_variants(hip_ctx, n, batch, kind, pick, lds, direction):
         plan.close()
 
 
+@pytest.mark.parametrize("n,cap,prec", [(4096, 16, F32), (2187, 27, F64), (3072, 16, F32), (1 << 20, 128, F64)])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_three_upload_four_step(hip_ctx, n, cap, prec, direction):
+    """Three-upload four-step (FourStepThreeUpload, kernel_ir.rs:1206-1236,
+    recursive_ir.rs:756-893) forced at small sizes by capping the one-upload
+    length, against the oracle; normalized inverse."""
+    batch = 3
+    normalize = direction == INV
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_inverse_normalization(normalize)
+    ir = vk.TransformIr.build(cfg, direction)
+    plan = _plan_with_env(hip_ctx, ir, {"VKFX_MAX_UPLOAD": str(cap)})
+    try:
+        fs = plan.describe()["four_step"]
+        assert fs["uploads"] == 3 and fs["n1"] * fs["m1"] * fs["m2"] == n and max(fs["n1"], fs["m1"], fs["m2"]) <= cap
+        x = rand(n * batch, 40 + n % 97, prec)
+        y = _run_plan(hip_ctx, plan, x, n * batch)
+        ref = oracle_c2c(x, n, direction, normalize)
+        tol = TOL[prec] if prec == F32 else max(TOL[F64], 4 * o.rel_l2(ref, (np.fft.fft if direction == FWD else
+                                                                              np.fft.ifft)(x.reshape(batch, n).astype(np.complex128), axis=1).reshape(-1)))
+        assert o.rel_l2(y, ref) <= tol
+    finally:
+        plan.close()
+
+
+@pytest.mark.parametrize("log2n,prec,tol", [(29, F32, 1e-5), (27, F64, 1e-12)])
+def test_three_upload_full_length(hip_ctx, log2n, prec, tol):
+    """Lengths past the two-upload limit (f32 2^29, f64 2^27: one line of
+    4 and 2 GiB): three uploads without a cap. Input = three tones, whose
+    spectrum is N a_t at bin f_t and zero elsewhere (closed form); then the
+    normalized inverse returns the input."""
+    import torch
+    n = 1 << log2n
+    cdt = torch.complex64 if prec == F32 else torch.complex128
+    freqs, amps = [3, 12345, n - 77], [1.0, 0.5 - 0.25j, -0.75j]
+    k = torch.arange(n, device="cuda", dtype=torch.int64)
+    x = torch.zeros(n, device="cuda", dtype=torch.complex128)
+    one = torch.ones(n, device="cuda", dtype=torch.float64)
+    for f, a in zip(freqs, amps):
+        # exact integer reduction of the phase f k / n before the float conversion
+        x += a * torch.polar(one, (2 * np.pi / n) * ((k * f) % n).to(torch.float64))
+    del k, one
+    x = x.to(cdt)
+    ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_precision(prec), FWD)
+    plan = hip_ctx.plan(ir)
+    assert plan.describe()["four_step"]["uploads"] == 3
+    y = torch.empty_like(x)
+    plan.execute_tensors(x, y)
+    torch.cuda.synchronize()
+    ref_norm = n * float(np.sqrt(sum(abs(a) ** 2 for a in amps)))
+    err = y.clone()
+    for f, a in zip(freqs, amps):
+        err[f] -= n * a
+    assert float(torch.linalg.vector_norm(err.to(torch.complex128))) / ref_norm <= tol
+    del err
+    plan.close()
+    iir = vk.TransformIr.build(vk.FftConfig.new([n]).with_precision(prec).with_inverse_normalization(True), INV)
+    iplan = hip_ctx.plan(iir)
+    z = torch.empty_like(x)
+    iplan.execute_tensors(y, z)
+    torch.cuda.synchronize()
+    rel = float(torch.linalg.vector_norm((z - x).to(torch.complex128)) / torch.linalg.vector_norm(x.to(torch.complex128)))
+    assert rel <= tol
+    iplan.close()
+
+
 def test_register_exchange_kernel_nd_rows(hip_ctx):
     """The register-exchange kernel as the contiguous-axis pass of N-D plans."""
     for dims, batch in (([8, 1024], 2), ([3, 5, 1024], 1)):

@@ -64,6 +64,36 @@ def test_four_step_map_computes_the_dft(n1, rad1, n2, rad2):
             assert src[kk1 + n1 * kk2] == sa[kk1] * n2 + sb[kk2]
 
 
+def _four_step_fft(x, n1, rad1, n2, rad2, row_fft=None):
+    m = n1 * n2
+    w = x.reshape(n1, n2).astype(np.complex128)
+    cols = np.stack([im.stockham_fft(w[:, c], rad1) for c in range(n2)], axis=1)
+    cols = cols * np.exp(-2j * np.pi * np.arange(n1)[:, None] * np.arange(n2)[None, :] / m)
+    out = np.empty(m, dtype=np.complex128)
+    for r in range(n1):
+        out[r + n1 * np.arange(n2)] = row_fft(cols[r]) if row_fft else im.stockham_fft(cols[r], rad2)
+    return out
+
+
+@pytest.mark.parametrize("n1,rad1,m1,rad2,m2,rad3", [(16, [4, 4], 16, [16], 16, [4, 4]), (27, [3, 9], 9, [9], 9, [3, 3]),
+                                                     (12, [3, 4], 8, [8], 4, [4])])
+def test_three_pass_map_computes_the_dft(n1, rad1, m1, rad2, m2, rad3):
+    """Three uploads with real math on the placement of three_pass_perm: a
+    four-step over n1 x n2 whose row FFTs are four-steps over m1 x m2."""
+    n2 = m1 * m2
+    m = n1 * n2
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal(m) + 1j * rng.standard_normal(m)
+    out = _four_step_fft(x, n1, rad1, n2, None, row_fft=lambda r: _four_step_fft(r, m1, rad2, m2, rad3))
+    np.testing.assert_allclose(out, np.fft.fft(x), rtol=0, atol=1e-9 * np.sqrt(m))
+    src = im.three_pass_perm(n1, rad1, m1, rad2, m2, rad3)
+    assert np.array_equal(np.sort(src), np.arange(m))
+    sa, sub = im.stockham_perm(n1, rad1), im.four_step_perm(m1, rad2, m2, rad3)
+    for kk1 in range(0, n1, 3):
+        for kk2 in range(0, n2, 5):
+            assert src[kk1 + n1 * kk2] == sa[kk1] * n2 + sub[kk2]
+
+
 def test_bluestein_maps_zero_fill_and_truncate():
     n, m = 11, 24
     src = im.bluestein_single_perm(n, m, [2, 3, 4])

@@ -626,16 +626,28 @@ int bluestein_tables(vkfx_plan* p, size_t N, size_t M, int sign, int prec, size_
 size_t csize(int prec) { return prec ? 16 : 8; }
 size_t rsize(int prec) { return prec ? 8 : 4; }
 
+// Longest line planned as one upload (VKFX_MAX_UPLOAD, 0 = no cap beyond
+// LDS): lets tests reach the multi-upload plans at small sizes.
+size_t upload_cap() {
+    const char* e = getenv("VKFX_MAX_UPLOAD");
+    const long long v = e ? atoll(e) : 0;
+    return v > 0 ? (size_t)v : SIZE_MAX;
+}
+
+// A length one kernel can hold (single upload), within the cap.
+bool one_upload(size_t n, int prec, size_t lds_max) {
+    return n <= upload_cap() && geometry(n, prec, 1, lds_max, lds_max).ok;
+}
+
 // Chooses M = N1 * N2 with both factors feasible single-upload lengths,
-// minimising max(N1, N2) (N1 >= N2 on ties). need_even_rows: N1 % (2*h) == 0
-// for the mirror-row R2C pass.
+// minimising max(N1, N2) (N1 >= N2 on ties).
 bool four_step_split(size_t M, int prec, size_t lds_max, size_t* n1, size_t* n2) {
     size_t best1 = 0, best2 = 0, bestmax = SIZE_MAX;
     for (size_t a = 2; a * a <= M; ++a) {
         if (M % a) continue;
         const size_t b = M / a;
         const size_t hi = std::max(a, b), lo = std::min(a, b);
-        if (!geometry(hi, prec, 1, lds_max, lds_max).ok || !geometry(lo, prec, 1, lds_max, lds_max).ok) continue;
+        if (!one_upload(hi, prec, lds_max) || !one_upload(lo, prec, lds_max)) continue;
         if (hi < bestmax) {
             bestmax = hi;
             best1 = hi;
@@ -646,6 +658,25 @@ bool four_step_split(size_t M, int prec, size_t lds_max, size_t* n1, size_t* n2)
     *n1 = best1;
     *n2 = best2;
     return true;
+}
+
+// Three uploads for lengths with no two-upload split: M = N1 * (M1 * M2),
+// N1 one upload (the first column pass over the whole line) and the rows of
+// N2 = M1 * M2 a two-upload four-step of their own; minimises the largest
+// of the three factors.
+bool three_step_split(size_t M, int prec, size_t lds_max, size_t* n1, size_t* m1, size_t* m2) {
+    size_t best = SIZE_MAX;
+    for (size_t a = 2; a <= M / 4 && a <= (1u << 20); ++a) {
+        if (M % a || !one_upload(a, prec, lds_max)) continue;
+        size_t b1, b2;
+        if (!four_step_split(M / a, prec, lds_max, &b1, &b2)) continue;
+        const size_t hi = std::max(a, std::max(b1, b2));
+        if (hi < best) {
+            best = hi;
+            *n1 = a, *m1 = b1, *m2 = b2;
+        }
+    }
+    return best != SIZE_MAX;
 }
 
 PlannerTuning tuning_from(const vkfx_planner_tuning& t) {
@@ -917,6 +948,76 @@ void note_rader_mixed(Ctx& c, size_t n, const Geometry& g) {
 
 // ---- 1-D complex -----------------------------------------------------------
 
+// Three-upload four-step of one 1-D axis (the reference's FourStepThreeUpload
+// plans, recursive_ir.rs:756-893, kernel_ir.rs:1206-1236): a line of
+// M = N1 * N2 is the matrix x[i1 * N2 + i2]; pass 1 transforms the N2 columns
+// over i1 with the twiddle W_M^(i2 k1) (workspace, same layout); the rows of
+// N2 = M1 * M2 are then a four-step of their own, in place on the workspace:
+// pass 2 transforms each row's M2 columns over j1 (i2 = j2 + M2 j1) with
+// W_N2^(j2 l1), pass 3 transforms the contiguous M2-runs over j2 and stores
+// X[k1 + N1 (l1 + M1 l2)] (line (b, k1, l1): input b M + k1 N2 + l1 M2,
+// output b M + k1 + l1 N1, element stride N1 M1).
+int plan_c2c_three_upload(Ctx& c, size_t n, size_t batch, int dir, double sc) {
+    vkfx_plan* p = c.p;
+    const int prec = c.prec;
+    const size_t cs = csize(prec);
+    size_t n1, m1, m2;
+    if (!three_step_split(n, prec, c.lds_max, &n1, &m1, &m2))
+        return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no three-upload four-step split for length " + std::to_string(n));
+    const size_t n2 = m1 * m2;
+    Geometry ga = kernel_geometry(KK_FS_A, prec, dir, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gb = kernel_geometry(KK_FS_A, prec, dir, m1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    Geometry gc = kernel_geometry(KK_FS_B, prec, dir, m2, false, prec ? 8 : 16, c.lds_max, c.lds_budget);
+    if (!ga.ok || !gb.ok || !gc.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "three-upload geometry");
+    const size_t chunk = chunk_for(batch, n * cs, 64);
+    p->work_bytes = std::max(p->work_bytes, chunk * n * cs);
+    const void *alo, *ahi, *blo, *bhi;
+    int ash, bsh;
+    int rc = two_level(p, n, prec, &alo, &ahi, &ash);
+    if (rc) return rc;
+    rc = two_level(p, n2, prec, &blo, &bhi, &bsh);
+    if (rc) return rc;
+    c.js << "\"four_step\":{\"len\":" << n << ",\"uploads\":3,\"n1\":" << n1 << ",\"n2\":" << n2 << ",\"m1\":" << m1
+         << ",\"m2\":" << m2 << ",\"chunk\":" << chunk << "},";
+    for (size_t b0 = 0; b0 < batch; b0 += chunk) {
+        c.cur_chunk = (int)(b0 / chunk);
+        const size_t cb = std::min(chunk, batch - b0);
+        KArgs a = blank();
+        a.C = (long long)n2;
+        a.in_es = (long long)n2, a.in_cs = 1, a.in_os = (long long)n;
+        a.out_es = (long long)n2, a.out_cs = 1, a.out_os = (long long)n;
+        a.tlo = alo, a.thi = ahi, a.tshift = ash;
+        a.M = (long long)n, a.N1 = (long long)n1, a.N2 = (long long)n2;
+        long long lines = (long long)(cb * n2);
+        rc = add_launch(c, KK_FS_A, dir, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * n * cs, SEL_WORK, 0,
+                        "three_upload_pass1");
+        if (rc) return rc;
+        KArgs b = blank();
+        b.C = (long long)m2;
+        b.in_es = (long long)m2, b.in_cs = 1, b.in_os = (long long)n2;
+        b.out_es = (long long)m2, b.out_cs = 1, b.out_os = (long long)n2;
+        b.tlo = blo, b.thi = bhi, b.tshift = bsh;
+        b.M = (long long)n2, b.N1 = (long long)m1, b.N2 = (long long)m2;
+        lines = (long long)(cb * n1 * m2);
+        rc = add_launch(c, KK_FS_A, dir, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_WORK, 0,
+                        "three_upload_pass2");
+        if (rc) return rc;
+        KArgs d = blank();
+        d.C = (long long)m1;
+        d.C1 = (long long)n1;
+        d.in_es = 1, d.in_cs = (long long)m2, d.in_os1 = (long long)n2, d.in_os = (long long)n;
+        d.out_es = (long long)(n1 * m1), d.out_cs = (long long)n1, d.out_os1 = 1, d.out_os = (long long)n;
+        d.flags = KF_IN_ROWMAJOR;
+        d.scale = sc;
+        d.M = (long long)n2, d.N1 = (long long)m1, d.N2 = (long long)m2;
+        lines = (long long)(cb * n1 * m1);
+        rc = add_launch(c, KK_FS_B, dir, gc, d, lines, blocks_for(lines, gc.G), SEL_WORK, 0, SEL_OUT, b0 * n * cs,
+                        "three_upload_pass3");
+        if (rc) return rc;
+    }
+    return VKFX_OK;
+}
+
 int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorithm alg, size_t conv_len) {
     vkfx_plan* p = c.p;
     const int prec = c.prec;
@@ -924,7 +1025,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     const double sc = (dir > 0 && normalize) ? 1.0 / (double)n : 1.0;
     if (alg == Algorithm::Stockham) {
         Geometry g = geometry(n, prec, 256, c.lds_max, c.lds_budget);
-        if (g.ok) {
+        if (g.ok && n <= upload_cap()) {
             g = kernel_geometry(KK_PLAIN, prec, dir, n, false, std::max(1, 256 / g.TT), c.lds_max, c.lds_budget);
             // one launch by default (VKFX_SPLIT=k splits the batch for tuning runs)
             size_t parts = 1;
@@ -945,8 +1046,7 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
             return VKFX_OK;
         }
         size_t n1, n2;
-        if (!four_step_split(n, prec, c.lds_max, &n1, &n2))
-            return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no two-upload four-step split for length " + std::to_string(n));
+        if (!four_step_split(n, prec, c.lds_max, &n1, &n2)) return plan_c2c_three_upload(c, n, batch, dir, sc);
         Geometry ga = kernel_geometry(KK_FS_A, prec, dir, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
         Geometry gb = kernel_geometry(KK_FS_B, prec, dir, n2, false, prec ? 8 : 16, c.lds_max, c.lds_budget);
         if (!ga.ok || !gb.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "four-step geometry");
