@@ -57,8 +57,57 @@ def test_formatted_1d_batch_strides(hip_ctx, prec):
     tol = 1e-5 if prec == F32 else 1e-13
     assert o.rel_l2(y, ref_c2c(x, [n], batch)) <= tol
     desc = hip_ctx.plan(ir).describe()
-    assert desc["boundary"]["input"] and desc["boundary"]["output"]
+    # a 1-D batch stride is the passes' own per-transform stride: no boundary pass
+    assert not desc["boundary"]["input"] and not desc["boundary"]["output"]
+    assert desc["boundary"]["fused_batch_stride"] == [True, True]
     assert hip_ctx.plan(ir).in_bytes == 1100 * batch * np.dtype(dt).itemsize
+
+
+@pytest.mark.parametrize("n,batch,prec,env", [
+    (1024, 7, F32, {}), (1024, 9, F32, {"VKFX_REGISTER_EXCHANGE": "1"}), (1000, 5, F32, {}), (1000, 5, F64, {}),
+    (1 << 18, 5, F32, {"VKFX_WORK_BUDGET_MB": "2"}), (4096, 4, F32, {"VKFX_MAX_UPLOAD": "16"}),
+    (4099, 3, F32, {}), (65537, 2, F32, {}), (97, 6, F32, {}), (47, 6, F64, {})])
+def test_formatted_1d_batch_strides_fused(hip_ctx, n, batch, prec, env):
+    """1-D C2C with formatted batch strides on both sides, read and written
+    by the FFT passes themselves (one-upload, runtime-shape, register-exchange,
+    four-step over several chunks and lanes, three-upload, Bluestein one- and
+    three-pass, Rader FFT and direct): results against numpy, and the gaps of
+    the output layout keep their contents."""
+    import os
+
+    import torch
+    dt = np.complex64 if prec == F32 else np.complex128
+    sin, sout = n + 13, n + 5
+    c = cfg([n], batch, prec).with_input_buffer_batch_stride(sin).with_output_buffer_batch_stride(sout)
+    ir = build(c)
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        plan = vk.Plan(hip_ctx, ir)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    try:
+        desc = plan.describe()
+        assert desc["boundary"]["fused_batch_stride"] == [True, True], desc["boundary"]
+        assert not any(p.get("kernel", "").startswith("boundary") for p in desc["passes"])
+        x = o.complex_uniform(n * batch, 60 + n % 89, dt)
+        xin = np.zeros(sin * batch, dtype=dt)
+        xin.reshape(batch, sin)[:, :n] = x.reshape(batch, n)
+        rdt = torch.float32 if prec == F32 else torch.float64
+        dx = torch.from_numpy(xin.view(np.float32 if prec == F32 else np.float64).copy()).cuda()
+        dy = torch.full((sout * batch * 2,), float("nan"), device="cuda", dtype=rdt)
+        plan.execute_tensors(dx, dy)
+        torch.cuda.synchronize()
+        y = dy.cpu().numpy().view(dt).reshape(batch, sout)
+        assert np.isnan(y[:, n:].real).all() and np.isnan(y[:, n:].imag).all()
+        tol = 1e-5 if prec == F32 else 1e-12
+        assert o.rel_l2(y[:, :n].reshape(-1), ref_c2c(x, [n], batch)) <= tol
+    finally:
+        plan.close()
 
 
 def test_formatted_2d_axis_and_batch_strides(hip_ctx):

@@ -2359,7 +2359,38 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         const bool zp_in = any_zero && (conv_real || (d.zero_frequency ? !fwd : fwd));
         const bool zp_out = any_zero && (conv_real || !zp_in);
         const bool mixed = store_t != comp_t;
-        const bool need_in = mixed || fmt_in || zp_in, need_out = mixed || fmt_out || zp_out;
+        // 1-D C2C whose only boundary work is a formatted batch stride: the
+        // passes that read the caller's input or write its output take that
+        // stride as their per-transform stride, so no boundary pass runs
+        // (the reference keeps layouts inside its passes). Every such pass
+        // must address transform b at b * n (in_os / out_os = n, chunk
+        // offsets multiples of n elements).
+        auto fuse_batch_stride = [&](bool in_side, long long bst) {
+            const long long n = (long long)d.dims[0];
+            const size_t unit = (size_t)n * csize(c.prec);
+            for (const Launch& L : p->launches) {
+                if (L.boundary || L.r2r) return false;
+                if (in_side && L.in_sel == SEL_IN && (L.a.in_os != n || L.in_off % unit)) return false;
+                if (!in_side && L.out_sel == SEL_OUT && (L.a.out_os != n || L.out_off % unit)) return false;
+            }
+            for (Launch& L : p->launches) {
+                if (in_side && L.in_sel == SEL_IN) {
+                    L.a.in_os = bst;
+                    L.in_off = L.in_off / unit * (size_t)bst * csize(c.prec);
+                }
+                if (!in_side && L.out_sel == SEL_OUT) {
+                    L.a.out_os = bst;
+                    L.out_off = L.out_off / unit * (size_t)bst * csize(c.prec);
+                }
+            }
+            return true;
+        };
+        const bool plain_1d = d.transform == VKFX_C2C && !d.perform_convolution && rank == 1 && !mixed && !any_zero;
+        bool fused_in = false, fused_out = false;
+        if (plain_1d && fmt_in) fused_in = fuse_batch_stride(true, in_bst);
+        if (plain_1d && fmt_out) fused_out = fuse_batch_stride(false, out_bst);
+        const bool need_in = mixed || (fmt_in && !fused_in) || zp_in;
+        const bool need_out = mixed || (fmt_out && !fused_out) || zp_out;
         const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
         const size_t cin = p->in_bytes, cout = p->out_bytes;  // dense compute-type bytes
         const int in_scal = real_in ? 1 : 2, out_scal = real_out ? 1 : 2;
@@ -2410,7 +2441,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->stage_shared = need_out && need_in && d.transform == VKFX_C2C;
         p->stage_out_bytes = need_out && !p->stage_shared ? cout : 0;
         c.js << "\"boundary\":{\"input\":" << (need_in ? "true" : "false") << ",\"output\":"
-             << (need_out ? "true" : "false") << ",\"zero_padding\":\""
+             << (need_out ? "true" : "false") << ",\"fused_batch_stride\":[" << (fused_in ? "true" : "false")
+             << "," << (fused_out ? "true" : "false") << "],\"zero_padding\":\""
              << (!any_zero ? "none" : d.zero_frequency ? "frequency" : "spatial") << "\",\"grouped_batch\":[";
         for (size_t i = 0; i < rank; ++i) c.js << (i ? "," : "") << d.grouped_batch[i];
         c.js << "]},";
