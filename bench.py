@@ -167,9 +167,9 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
 
 def plain_copy_bandwidth(nbytes=1 << 30, reps=10):
     """The library's own copy (a transform whose only axis has length 1:
-    dims [1], f64, 1 GiB) on device buffers. Its kernel
-    (k_dyn<double, -1, IoPlain, false>) moves 8-16 bytes per lane like the FFT
-    kernels, so its FETCH_SIZE / WRITE_SIZE counters calibrate theirs."""
+    dims [1], f64, 1 GiB) on device buffers. Its kernel (k_copy16, 16-byte
+    nontemporal loads and stores) streams HBM like the FFT kernels' direct
+    stages, so its FETCH_SIZE / WRITE_SIZE counters calibrate theirs."""
     import torch
 
     torch.cuda.init()
@@ -407,7 +407,7 @@ def _plan_m(plan):
 
 
 COPY_BYTES = 1 << 30  # plain_copy_bandwidth(): 1 GiB read + 1 GiB written per launch
-CALIBRATION_KERNEL = "k_dyn<double, -1, vkfx::IoPlain, false>"
+CALIBRATION_KERNEL = "k_copy16"
 
 
 def rocprof_summary(dirs, workload_kernel="vkfx"):

@@ -687,6 +687,22 @@ def test_three_upload_full_length(hip_ctx, log2n, prec, tol):
     iplan.close()
 
 
+@pytest.mark.parametrize("prec", [F32, F64])
+@pytest.mark.parametrize("batch", [1, 3, 4096, 100003])
+def test_length_one_is_a_copy(hip_ctx, prec, batch):
+    """A transform whose only axis has length 1 is X[0] = x[0] in both
+    directions (normalized or not): one copy pass, 16-byte body and 8-byte
+    tail, bit-exact."""
+    x = rand(batch, 5 + batch % 7, prec)
+    for direction, normalize in ((FWD, False), (INV, True), (INV, False)):
+        cfg = vk.FftConfig.new([1]).with_batch_count(batch).with_precision(prec).with_inverse_normalization(normalize)
+        ir = vk.TransformIr.build(cfg, direction)
+        plan = hip_ctx.plan(ir)
+        assert [p["kernel"] for p in plan.describe()["passes"]] == ["copy"]
+        y = hip_ctx.execute_transform(ir, x)
+        assert np.array_equal(y, x)
+
+
 def test_register_exchange_kernel_nd_rows(hip_ctx):
     """The register-exchange kernel as the contiguous-axis pass of N-D plans."""
     for dims, batch in (([8, 1024], 2), ([3, 5, 1024], 1)):

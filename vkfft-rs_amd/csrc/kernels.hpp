@@ -184,6 +184,9 @@ struct BoundaryArgs {
     long long zero_left[kMaxBoundaryRank] = {0, 0, 0, 0}, zero_right[kMaxBoundaryRank] = {0, 0, 0, 0};
 };
 int launch_boundary(const BoundaryArgs& a, const void* in, void* out, hipStream_t s);
+// Copy of `bytes` (a multiple of 8) for transforms of length 1 (convert.hip).
+int launch_copy(const void* in, void* out, size_t bytes, hipStream_t s);
+const void* copy_kernel_fn();
 
 // DCT / DST pre and post passes around a length-L complex FFT (r2r.hip):
 //   a[m] = w(m) x[m - off] exp(-i pi m ph / (2n))  (m - off in [0, n), else 0)

@@ -73,7 +73,6 @@ struct PoolBuf {
 struct vkfx_context {
     int device = 0;
     hipStream_t stream = nullptr;
-    hipStream_t aux = nullptr;  // second lane for chunked plans (default priority)
     vkfx_device_profile profile{};
     std::vector<PoolBuf> dev_pool, host_pool;  // free buffers
     std::vector<hipStream_t> stream_pool;      // free streams for tickets
@@ -118,6 +117,9 @@ struct Launch {
     // boundary pass instead of an FFT kernel (type conversion, formatted
     // layouts, zero padding; convert.hip)
     bool boundary = false;
+    // plain copy of copy_bytes (a transform of length 1; convert.hip)
+    bool copy = false;
+    size_t copy_bytes = 0;
     BoundaryArgs ba;
     // DCT / DST pre (1) or post (2) pass instead of an FFT kernel (r2r.hip)
     int r2r = 0;
@@ -307,7 +309,7 @@ struct vkfx_plan {
     DevBuf work;
     size_t work_bytes = 0;  // per lane while planning; total after plan_create
     size_t work_lane = 0;   // workspace bytes of one stream lane
-    int lanes = 1;          // 2: chunks alternate between the caller's stream and the aux stream
+    int lanes = 1;          // 2: chunks alternate between the caller's stream and the plan's aux stream
     bool serial = false;    // chunks depend on each other: one lane
     size_t stage_in_off = 0, stage_out_off = 0;  // dense compute-type copies behind boundary passes
     size_t stage_in_bytes = 0, stage_out_bytes = 0;
@@ -316,6 +318,7 @@ struct vkfx_plan {
     size_t aux_off = 0, aux_bytes = 0;    // SEL_AUX region (N-D C2R compact spectrum)
     size_t conv_a_off = 0, conv_a_bytes = 0, conv_b_off = 0, conv_b_bytes = 0;  // SEL_CONV_A / SEL_CONV_B
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    hipStream_t aux = nullptr;  // the plan's second lane (two-lane plans; default priority)
     size_t in_bytes = 0, out_bytes = 0;
     bool real_out = false;    // output holds reals (C2R, DCT/DST, real-application convolution)
     int tickets = 0;          // live tickets of this plan (guarded by ctx->mu)
@@ -707,6 +710,10 @@ void note_pass(Ctx& c, const Launch& L) {
         c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.ra.L << ",\"len\":" << L.ra.n << "}";
         return;
     }
+    if (L.copy) {
+        c.js << "{\"kernel\":\"" << L.label << "\",\"bytes\":" << L.copy_bytes << "}";
+        return;
+    }
     if (L.conv) {
         c.js << "{\"kernel\":\"" << L.label << "\",\"tensor\":" << L.ca.T << ",\"coordinates\":" << L.ca.coords
              << ",\"systems\":" << L.ca.systems_out << ",\"planes\":" << L.ca.planes << "}";
@@ -1023,6 +1030,16 @@ int plan_c2c_1d(Ctx& c, size_t n, size_t batch, int dir, bool normalize, Algorit
     const int prec = c.prec;
     const size_t cs = csize(prec);
     const double sc = (dir > 0 && normalize) ? 1.0 / (double)n : 1.0;
+    if (n == 1) {
+        // X[0] = x[0] (the scale of a normalized inverse is 1/1): one copy
+        Launch L{};
+        L.copy = true;
+        L.copy_bytes = batch * cs;
+        L.in_sel = SEL_IN, L.out_sel = SEL_OUT;
+        L.label = "copy";
+        p->launches.push_back(L);
+        return VKFX_OK;
+    }
     if (alg == Algorithm::Stockham) {
         Geometry g = geometry(n, prec, 256, c.lds_max, c.lds_budget);
         if (g.ok && n <= upload_cap()) {
@@ -1998,9 +2015,7 @@ int vkfx_context_create(int device_index, vkfx_context** out) {
     // the static scratch (a failure only disables vkfx_execute_noalloc)
     ctx->scratch_err = vkfx::static_scratch_address(device_index, &ctx->scratch);
     e = hipStreamCreate(&ctx->stream);
-    if (e == hipSuccess) e = hipStreamCreate(&ctx->aux);
     if (e != hipSuccess) {
-        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return hip_fail(e, "hipStreamCreate");
     }
@@ -2017,7 +2032,6 @@ int vkfx_context_create(int device_index, vkfx_context** out) {
     std::snprintf(pr.arch, sizeof(pr.arch), "%s", prop.gcnArchName);
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         (void)hipStreamDestroy(ctx->stream);
-        (void)hipStreamDestroy(ctx->aux);
         delete ctx;
         return fail(VKFX_ERR_NATIVE_UNAVAILABLE, std::string("library built for gfx950, device is ") + prop.gcnArchName);
     }
@@ -2036,7 +2050,6 @@ int vkfx_context_destroy(vkfx_context* ctx) {
     }
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    (void)hipStreamSynchronize(ctx->aux);
     for (hipStream_t s : ctx->stream_pool) {
         (void)hipStreamSynchronize(s);
         (void)hipStreamDestroy(s);
@@ -2050,7 +2063,6 @@ int vkfx_context_destroy(vkfx_context* ctx) {
         (void)hipHostFree(b.p);
     }
     (void)hipStreamDestroy(ctx->stream);
-    (void)hipStreamDestroy(ctx->aux);
     delete ctx;
     return VKFX_OK;
 }
@@ -2064,7 +2076,6 @@ int vkfx_context_profile(const vkfx_context* ctx, vkfx_device_profile* out) {
 int vkfx_context_synchronize(vkfx_context* ctx) {
     if (!ctx) return fail(VKFX_ERR_INVALID_ARGUMENT, "null context");
     hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->aux);
     return e == hipSuccess ? VKFX_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
@@ -2369,7 +2380,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
             const long long n = (long long)d.dims[0];
             const size_t unit = (size_t)n * csize(c.prec);
             for (const Launch& L : p->launches) {
-                if (L.boundary || L.r2r) return false;
+                if (L.boundary || L.r2r || L.copy) return false;
                 if (in_side && L.in_sel == SEL_IN && (L.a.in_os != n || L.in_off % unit)) return false;
                 if (!in_side && L.out_sel == SEL_OUT && (L.a.out_os != n || L.out_off % unit)) return false;
             }
@@ -2494,11 +2505,16 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->work_bytes = shared ? p->stage_in_off + p->stage_in_bytes : p->stage_out_off + p->stage_out_bytes;
     }
     if (p->lanes == 2) {
+        // each two-lane plan forks onto a stream of its own, so plans on
+        // different caller streams do not serialize their odd chunks
         hipError_t e = hipEventCreateWithFlags(&p->ev_fork, hipEventDisableTiming);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&p->ev_join, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipStreamCreate(&p->aux);
         if (e != hipSuccess) {
+            if (p->ev_fork) (void)hipEventDestroy(p->ev_fork);
+            if (p->ev_join) (void)hipEventDestroy(p->ev_join);
             delete p;
-            return hip_fail(e, "hipEventCreate");
+            return hip_fail(e, "plan stream lane");
         }
     }
     c.js << "\"lanes\":" << p->lanes << ",\"workspace_bytes\":" << p->work_bytes << ",\"passes\":[";
@@ -2532,7 +2548,10 @@ int vkfx_plan_destroy(vkfx_plan* plan) {
     }
     (void)hipSetDevice(plan->ctx->device);
     (void)hipStreamSynchronize(plan->ctx->stream);
-    (void)hipStreamSynchronize(plan->ctx->aux);
+    if (plan->aux) {
+        (void)hipStreamSynchronize(plan->aux);
+        (void)hipStreamDestroy(plan->aux);
+    }
     if (plan->ev_fork) (void)hipEventDestroy(plan->ev_fork);
     if (plan->ev_join) (void)hipEventDestroy(plan->ev_join);
     delete plan;
@@ -2556,6 +2575,8 @@ int vkfx_plan_resources(const vkfx_plan* plan, vkfx_pass_resources* out, uint32_
             fn = r2r_kernel_fn(L.r2r == 1, prec);
         } else if (L.conv) {
             fn = conv_kernel_fn(prec);
+        } else if (L.copy) {
+            fn = copy_kernel_fn();
         } else {
             fn = fft_kernel_fn(L.kind, prec, L.dir, L.fixed, L.a.flags);
             block = L.block;
@@ -2638,11 +2659,11 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
     (void)hipSetDevice(plan->ctx->device);
     const int prec =
         (plan->desc.precision == VKFX_F64 || plan->desc.precision == VKFX_F64_COMPUTE_F32_STORAGE) ? 1 : 0;
-    hipStream_t lane_stream[2] = {s, plan->ctx->aux};
+    hipStream_t lane_stream[2] = {s, plan->aux};
     if (plan->lanes == 2) {
         // fork: the aux lane starts after everything already queued on s
         hipError_t e = hipEventRecord(plan->ev_fork, s);
-        if (e == hipSuccess) e = hipStreamWaitEvent(plan->ctx->aux, plan->ev_fork, 0);
+        if (e == hipSuccess) e = hipStreamWaitEvent(plan->aux, plan->ev_fork, 0);
         if (e != hipSuccess) return hip_fail(e, "stream fork");
     }
     for (const Launch& L : plan->launches) {
@@ -2675,6 +2696,11 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
             if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
             continue;
         }
+        if (L.copy) {
+            int e = launch_copy(sel(L.in_sel, L.in_off), sel(L.out_sel, L.out_off), L.copy_bytes, lane_stream[lane]);
+            if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
+            continue;
+        }
         a.in = sel(L.in_sel, L.in_off);
         a.out = sel(L.out_sel, L.out_off);
         int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, lane_stream[lane], L.fixed);
@@ -2682,7 +2708,7 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
     }
     if (plan->lanes == 2) {
         // join: s continues only after the aux lane's work
-        hipError_t e = hipEventRecord(plan->ev_join, plan->ctx->aux);
+        hipError_t e = hipEventRecord(plan->ev_join, plan->aux);
         if (e == hipSuccess) e = hipStreamWaitEvent(s, plan->ev_join, 0);
         if (e != hipSuccess) return hip_fail(e, "stream join");
     }
@@ -3049,7 +3075,6 @@ int vkfx_context_clear_caches(vkfx_context* ctx) {
                                                  " submission(s) are in flight");
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->aux);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     for (PoolBuf& b : ctx->dev_pool) {
         if (b.ready) (void)hipEventDestroy(b.ready);
