@@ -149,7 +149,8 @@ def test_three_upload(idx_ctx, n, cap, prec):
     d = check_1d(idx_ctx, n, 9, prec, env=dict(env, VKFX_WORK_BUDGET_MB="0"))
 
 
-@pytest.mark.parametrize("n,kind,pick", [(1024, 0, 0), (1024, 0, 1), (4099, 12, 0), (4099, 12, 1), (4099, 12, 2)])
+@pytest.mark.parametrize("n,kind,pick", [(1024, 0, 0), (1024, 0, 1), (4099, 12, 0), (4099, 12, 1), (4099, 12, 2),
+                                         (4115, 12, 0)])
 def test_fixed_shape_variants(idx_ctx, n, kind, pick):
     """Per-stage twiddle tables and pads, ping-pong LDS buffers and the
     product-tree forms of the C1 and M = 8232 shapes move the same elements."""

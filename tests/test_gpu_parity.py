@@ -600,7 +600,8 @@ def test_register_exchange_kernel_1024(hip_ctx, batch, direction):
 
 @pytest.mark.parametrize("n,batch,kind,pick,lds", [
     (1024, 37, 0, 0, 1088 * 8), (1024, 37, 0, 1, 1088 * 8), (1024, 37, 0, 3, 1056 * 8),
-    (4099, 6, 12, 0, 9261 * 8), (4099, 6, 12, 1, 2 * 9261 * 8), (4099, 6, 12, 2, 8489 * 8)])
+    (4099, 6, 12, 0, 9261 * 8), (4099, 6, 12, 1, 2 * 9261 * 8), (4099, 6, 12, 2, 8489 * 8),
+    (4115, 5, 12, 0, 9261 * 8)])
 @pytest.mark.parametrize("direction", [FWD, INV])
 def test_fixed_shape_variants(hip_ctx, n, batch, kind, pick, lds, direction):
     """Each registered variant of the C1 and M = 8232 Bluestein shapes
