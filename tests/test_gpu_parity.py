@@ -369,6 +369,11 @@ def test_c2_shape_round_trip_full_size(hip_ctx):
         assert o.rel_l2(X[b * h:(b + 1) * h], ref) <= TOL[F32]
     xr, _ = c2r(hip_ctx, n, batch, X)
     assert o.rel_l2(xr, x) <= 2 * TOL[F32]
+    # the full-size C2R itself on sampled lines: the oracle's C2R of the same
+    # (f32) spectrum the GPU consumed
+    for b in (0, 131, 255):
+        back = o.c2r_batch(X[b * h:(b + 1) * h].astype(np.complex128), n, normalize=True)
+        assert o.rel_l2(xr[b * n:(b + 1) * n], back) <= TOL[F32]
 
 
 # ------------------------------------------------------------------ N-D

@@ -295,6 +295,27 @@ __device__ __forceinline__ void dft(cpx<T>* x) {
     }
 }
 
+// DFT of even length R whose inputs R/2..R-1 are zero: the even outputs are
+// the R/2-point DFT of x[0..R/2), the odd ones that of x[m] exp(S 2 pi i m / R).
+template <int R, int S, typename T>
+__device__ __forceinline__ void dft_upper_zero(cpx<T>* x) {
+    if constexpr (kIndexTest) return;
+    constexpr int H = R / 2;
+    cpx<T> e[H], o[H];
+#pragma unroll
+    for (int m = 0; m < H; ++m) {
+        e[m] = x[m];
+        o[m] = m == 0 ? x[0] : 4 * m == R ? muli<S>(x[m]) : cmul(x[m], unit_root<R, S, T>(m));
+    }
+    dft<H, S>(e);
+    dft<H, S>(o);
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+        x[2 * j] = e[j];
+        x[2 * j + 1] = o[j];
+    }
+}
+
 // LDS element index of element e in a line (one pad slot every 2^ps).
 __device__ __forceinline__ int lpad(int e, int ps) { return e + (e >> ps); }
 

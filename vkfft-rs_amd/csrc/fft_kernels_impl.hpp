@@ -218,6 +218,10 @@ struct IoPlain {
     static constexpr bool kStoreTw = false;  // store multiplies by a per-element pass twiddle
     static constexpr int kLoad = LAY_ANY;
     static constexpr int kStore = LAY_ANY;
+    // elements at or beyond kZeroFrom(N) of a length-N line are known zeros
+    // (Bluestein padding); the direct first stage skips their loads and,
+    // when a butterfly's upper half is all zeros, uses the half butterfly
+    static constexpr int kZeroFrom(int N) { return N; }
     static __device__ LineInfo line(const KArgs& a, long long blk, int g) { return line_default(a, blk, g); }
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return D::N(a); }
@@ -694,6 +698,8 @@ struct IoFsCBlue : IoPlain {
 struct IoBlue1 : IoPlain {
     static constexpr bool kPtrLoad = false, kPtrStore = false;
     static constexpr bool kTwoPass = true;
+    // M >= 2 N - 1: inputs from (M + 1) / 2 on are padding
+    static constexpr int kZeroFrom(int M) { return (M + 1) / 2; }
     template <class D>
     static __device__ __forceinline__ int out_count(const KArgs& a) { return (int)a.nout; }
     template <typename T, bool NTIO = false>
@@ -1127,7 +1133,8 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
 #pragma unroll
                 for (int i = 0; i < R; ++i) {
                     if constexpr (SRC) {
-                        v[j][i] = L.valid ? IO::template load_elem<T, NTI>(a, L, b + i * NB) : zero<T>();
+                        v[j][i] = (L.valid && i * NB < IO::kZeroFrom(N)) ? IO::template load_elem<T, NTI>(a, L, b + i * NB)
+                                                                          : zero<T>();
                     } else {
                         v[j][i] = line[lds_step<PS, NB>(b, i)];
                     }
@@ -1153,7 +1160,12 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
 #pragma unroll
                 for (int i = 1; i < R; ++i) v[j][i] = twmul<S>(v[j][i], wp[i]);
             }
-            dft<R, S>(v[j]);
+            // a direct first stage whose inputs b + i NB, i >= R/2, are all padding
+            constexpr bool kHalf = SRC && P == 1 && (R == 8 || R == 16) && (R / 2) * NB >= IO::kZeroFrom(N);
+            if constexpr (kHalf)
+                dft_upper_zero<R, S>(v[j]);
+            else
+                dft<R, S>(v[j]);
             const int base = (b - k) * R + k;
             if constexpr (DST && IO::kStoreTw) {
                 // last stage: outputs o = b + q*N/R carry the pass twiddle
