@@ -17,7 +17,8 @@ static const FixedKernel kTable[] = {
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
     // the previous padding (one slot per 32; VKFX_FIXED_PICK=3)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 5, 1056, false, true, true, 16, 8, 8),
-    // rows of 4096 (C3 axis 1)
+    // rows of 4096 (C3 axis 1; per-stage twiddle tables measured 6% slower here: 15 table loads per
+    // radix-16 butterfly against the product tree's 14 multiplications)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 4096, 256, 1, 4, 4352, false, true, true, 16, 16, 16),
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 4096, 256, 1, 4, 4352, false, true, true, 16, 16, 16),
     // columns of 4096 (C3 axis 0): 4 adjacent columns per block

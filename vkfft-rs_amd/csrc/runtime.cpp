@@ -738,6 +738,12 @@ void note_pass(Ctx& c, const Launch& L) {
     c.js << "{\"kernel\":\"" << L.label << "\",\"fft_len\":" << L.a.N << ",\"lines\":" << L.a.nlines
          << ",\"grid\":" << L.grid << ",\"block\":" << L.block << ",\"lines_per_block\":" << L.a.G
          << ",\"lds_bytes\":" << L.lds << ",\"fixed_shape\":" << (L.fixed ? "true" : "false")
+         << ",\"twiddles\":\""
+         << (!L.fixed                            ? "stage_roots"
+             : L.fixed->table == FT_STAGE_PR     ? "per_stage_tables"
+             : L.fixed->table == FT_WAVE1024     ? "lane_table"
+                                                 : "stage_roots")
+         << "\""
          << ",\"nontemporal\":[" << (L.fixed && L.fixed->nti ? "true" : "false") << ","
          << (L.fixed && L.fixed->nto ? "true" : "false") << "]"
          << ",\"runtime_variant\":{\"wide\":" << ((L.a.flags & KF_DYN_WIDE) ? "true" : "false")
