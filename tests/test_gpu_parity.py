@@ -307,9 +307,10 @@ def test_r2c_c2r_runtime_lengths(hip_ctx, n, prec):
 
 def test_c2r_runtime_variants_covered(hip_ctx):
     """The host rule for the runtime-shape C2R half-length kernels: HBM-direct
-    last stage always; the first stage forms the preprocess from HBM in f64,
-    and in f32 only when the first radix is 4 (n=210, radix 3 first, keeps the
-    staged preprocess). n=18018 (M=9009) needs the wide geometry. Each case
+    last stage always; the first stage forms the preprocess from HBM whenever
+    its loads span 128 bytes or more (any first radix but 2, both precisions;
+    n=210 has radix 3 first), else the staged preprocess (f64 n=6, 18: one
+    stage or a short span). n=18018 (M=9009) needs the wide geometry. Each case
     named here also runs in test_r2c_c2r_runtime_lengths."""
     def c2r_launch(n, prec):
         cfg = vk.FftConfig.new([n]).with_batch_count(37).with_precision(prec) \
@@ -318,16 +319,18 @@ def test_c2r_runtime_variants_covered(hip_ctx):
         ls = [L for L in plan.describe()["passes"] if "runtime_variant" in L and not L["fixed_shape"]]
         assert len(ls) == 1, plan.describe()
         return ls[0]
-    L = c2r_launch(210, F32)
-    assert L["radices"][0] == 3 and L["runtime_variant"]["hbm_direct"]
-    assert not L["runtime_variant"]["direct_preprocess"]
-    L = c2r_launch(210, F64)
-    assert L["radices"][0] == 3 and L["runtime_variant"]["direct_preprocess"]
+    for prec in (F32, F64):
+        L = c2r_launch(210, prec)
+        assert L["radices"][0] == 3 and L["runtime_variant"]["hbm_direct"]
+        assert L["runtime_variant"]["direct_preprocess"]
     L = c2r_launch(18018, F32)
     assert L["runtime_variant"]["wide"] and L["runtime_variant"]["hbm_direct"]
-    assert not L["runtime_variant"]["direct_preprocess"]
-    L = c2r_launch(1000, F32)
-    assert L["radices"][0] == 4 and L["runtime_variant"]["direct_preprocess"]
+    assert L["runtime_variant"]["direct_preprocess"]
+    L = c2r_launch(2000, F32)
+    assert L["radices"][0] == 8 and L["runtime_variant"]["direct_preprocess"]
+    for n in (6, 18):
+        L = c2r_launch(n, F64)
+        assert L["runtime_variant"]["hbm_direct"] and not L["runtime_variant"]["direct_preprocess"]
 
 
 HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 320],

@@ -924,18 +924,24 @@ __device__ __noinline__ void stage_c2r_first(cpx<T>* __restrict__ line, const in
     constexpr int MJ = dyn_butterflies_per_thread(R, WIDE);
     const int NB = N / R;
     const int mask = (1 << rshift) - 1;
+    // w_e for e = b + i NB is w_b (w_NB)^i: one two-level lookup per
+    // butterfly and the powers of w_NB once per thread, instead of a lookup
+    // per element
+    cpx<T> sp[R];
+    root_powers<R>(cmul(ld_table<T>(rhi, NB >> rshift), ld_table<T>(rlo, NB & mask)), sp);
     cpx<T> v[MJ][R];
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
         const int b = t + j * TT;
         if (b < NB) {
+            const cpx<T> wb = cmul(ld_table<T>(rhi, b >> rshift), ld_table<T>(rlo, b & mask));
 #pragma unroll
             for (int i = 0; i < R; ++i) {
                 const int e = b + i * NB;
                 const v2 x = ((gsrc_t)gsrc)[e];
                 const v2 y = ((gsrc_t)gsrc)[N - e];
                 const cpx<T> X = mk(x.x, x.y), Xm = mk(y.x, -y.y);
-                const cpx<T> w = cmul(ld_table<T>(rhi, e >> rshift), ld_table<T>(rlo, e & mask));
+                const cpx<T> w = i == 0 ? wb : cmul(wb, sp[i]);
                 v[j][i] = (X + Xm) + muli<1>(cmulc(X - Xm, w));
             }
         }
@@ -1003,10 +1009,8 @@ __global__ __launch_bounds__(512) void k_dyn_c2r_direct(const KArgs a) {
 
 // Runtime-shape even C2R with KF_DYN_DIRECT but not KF_DYN_PRE: staged
 // preprocess (IoC2RHalf prologue), last stage stored straight to HBM. The
-// host takes it for f32 lines whose first radix is above 4 (there the
-// preprocess-in-registers kernel above measured 8-13% slower; with radix 4
-// first it is 6-14% faster, and in f64 faster at every measured length) and
-// for lines whose first stage cannot load directly.
+// host takes it for lines whose first stage cannot load directly (one stage,
+// a radix-2 first stage, or first-stage loads spanning under 128 bytes).
 template <typename T, int S, bool WIDE>
 __global__ __launch_bounds__(512) void k_dyn_c2r_direct_out(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];

@@ -779,17 +779,19 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
         a.radix[0] != 2)
         a.flags |= KF_DYN_DIRECT;
     // runtime-shape even C2R, HBM-direct last stage; KF_DYN_PRE: the first
-    // stage also forms the preprocess from HBM, when its loads span at least
-    // 128 contiguous bytes per line, in f64, and in f32 with a first radix of
-    // exactly 4 (f32 lines with radix 8 or 16 first measured 8-13% slower
-    // that way, radix-4 ones 6-14% faster; f64 7-29% faster; radix 3, 5, 7
-    // first were not measured in f32 and keep the staged preprocess)
+    // stage also forms the preprocess from HBM when its loads span at least
+    // 128 contiguous bytes per line (the preprocess twiddle of element
+    // b + i N/R is w_b (w_(N/R))^i: one table lookup per butterfly). Measured
+    // 8-30% over the staged preprocess in both precisions and every first
+    // radix (f32 256, 2000, 6000, 12000, 200-9000; f64 2000-12000).
     if (!g.fixed && !g.rader && kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 &&
         a.radix[a.nstages - 1] != 2) {
         a.flags |= KF_DYN_DIRECT;
-        if (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 && (c.prec == 1 || a.radix[0] == 4) &&
-            (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128)
-            a.flags |= KF_DYN_PRE;
+        bool pre = a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2 &&
+                   (long long)(g.N / a.radix[0]) * (c.prec ? 16 : 8) >= 128;
+        // VKFX_C2R_PRE=0 keeps the staged preprocess (comparison runs)
+        if (const char* e = getenv("VKFX_C2R_PRE")) pre = pre && e[0] != '0';
+        if (pre) a.flags |= KF_DYN_PRE;
     }
     int rc = (g.fixed && g.fixed->table == FT_WAVE1024)   ? wave1024_table(c.p, c.prec, &a.tw)
              : (g.fixed && g.fixed->table == FT_STAGE_PR) ? stage_pr_table(c.p, g.fixed, c.prec, &a.tw)
