@@ -6,13 +6,13 @@ namespace vkfx {
 
 static const FixedKernel kTable[] = {
     // 1-D rows of 1024 (C1): two waves per line, 8 elements per thread in the
-    // radix-8 stages (16 in the radix-16 load stage); per-stage twiddle
-    // tables and pads (1.5-2% over product trees, half the rounding error)
-    VKFX_FIXED_TS(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 4, 1088, false, 0, true, true, 16, 8, 8),
-    VKFX_FIXED_TS(KK_PLAIN, IoPlain, float, 0, 1, 1024, 128, 1, 4, 1088, false, 0, true, true, 16, 8, 8),
-    // product-tree twiddles, one pad (VKFX_FIXED_PICK=1)
+    // radix-8 stages (16 in the radix-16 load stage), product-tree twiddles
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 4, 1088, false, true, true, 16, 8, 8),
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, 1, 1024, 128, 1, 4, 1088, false, true, true, 16, 8, 8),
+    // per-stage twiddle tables and pads (VKFX_FIXED_PICK=1): half the rounding
+    // error, 7% slower on two boxes (26.1 against 28.0 us)
+    VKFX_FIXED_TS(KK_PLAIN, IoPlain, float, 0, -1, 1024, 128, 1, 4, 1088, false, 0, true, true, 16, 8, 8),
+    VKFX_FIXED_TS(KK_PLAIN, IoPlain, float, 0, 1, 1024, 128, 1, 4, 1088, false, 0, true, true, 16, 8, 8),
     // one wave per line (VKFX_FIXED_PICK=2)
     VKFX_FIXED_NT(KK_PLAIN, IoPlain, float, 0, -1, 1024, 64, 1, 5, 1056, false, true, true, 16, 16, 4),
     // the previous padding (one slot per 32; VKFX_FIXED_PICK=3)
