@@ -14,12 +14,16 @@ static const FixedKernel kTable[] = {
     VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
     // M = 131220: product-tree twiddles (per-stage tables measured 4% slower).
     // Column passes of 405 with 45 threads per column (one radix-9 butterfly
-    // each, 1.3% over 27 threads, the second variant); the 324-point row
-    // pass keeps 27 threads per row (36 threads, 16 rows per block: 4% slower)
+    // each: 1.3% over 27 threads, the second variant); the 324-point row pass
+    // with 36 threads per row (radix 4, 9, 9: one radix-9 butterfly per thread,
+    // three radix-4 rounds) and 8 rows per block, 6-7% over 27 threads per row
+    // (the second variant) on two boxes; 16 rows per block or an LDS pad of one
+    // per 16 ran slower
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 45, 16, 30, 405, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 45, 16, 30, 405, true, false, true, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 407, true, false, true, 9, 9, 5),
+    VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 36, 8, 30, 324, false, false, false, 4, 9, 9),
     VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, false, false, 4, 9, 9),
 };
 
