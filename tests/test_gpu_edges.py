@@ -1,0 +1,129 @@
+"""Boundary work inside the FFT passes (KF_EDGE): the storage conversion of
+mixed precisions (src/config.rs:108-145) and the zero intervals of 1-D zero
+padding (src/zero_pad_ir.rs:320-345, 607-647) in the first pass's loads and
+the last pass's stores of C2C plans made of one-upload Stockham passes. Each
+case runs with the fused passes and with the boundary passes
+(VKFX_FUSED_EDGES=0) and both are checked against the oracle; the fused plan
+must have no boundary pass. Every test takes the session context first so
+that torch's HIP runtime is the one the library binds to."""
+import numpy as np
+import pytest
+
+import vkfft_amd as vk
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+F32, F64 = vk.Precision.F32, vk.Precision.F64
+F16S, F64C = vk.Precision.F16StorageF32Compute, vk.Precision.F64ComputeF32Storage
+FWD, INV = vk.Direction.Forward, vk.Direction.Inverse
+SPATIAL, FREQ = vk.ZeroPaddingDomain.Spatial, vk.ZeroPaddingDomain.Frequency
+
+
+def f16(v):
+    """Binary16 rounding of complex64 values (round to nearest even)."""
+    return v.view(np.float32).astype(np.float16).astype(np.float32).view(np.complex64)
+
+
+def ref_c2c(x, dims, batch, direction, normalize=False):
+    v = x.reshape((batch,) + tuple(dims)).astype(np.complex128)
+    if len(dims) == 1:
+        y = o.fft_batch(v.reshape(-1), dims[0], "forward" if direction == FWD else "inverse", normalize, threads=8)
+        return np.asarray(y).reshape(-1)
+    axes = tuple(range(1, len(dims) + 1))
+    if direction == FWD:
+        return np.fft.fftn(v, axes=axes).reshape(-1)
+    return (np.fft.ifftn(v, axes=axes) * (1 if normalize else int(np.prod(dims)))).reshape(-1)
+
+
+def run_both(monkeypatch, c, direction, x):
+    """(fused output, fused describe, boundary-pass output)."""
+    out = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("VKFX_FUSED_EDGES", fused)
+        ctx = vk.HipExecutionContext(0)  # own plan cache: plans read the switch when built
+        try:
+            ir = vk.TransformIr.build(c, direction)
+            y = ctx.execute_transform(ir, x)
+            desc = ctx.plan(ir).describe()
+        finally:
+            ctx.close()
+        assert desc["boundary"]["fused_edges"] == (fused == "1")
+        kernels = [p["kernel"] for p in desc["passes"]]
+        assert ("boundary_in" in kernels or "boundary_out" in kernels) == (fused == "0"), kernels
+        out.append((y, desc))
+    return out[0][0], out[0][1], out[1][0]
+
+
+@pytest.mark.parametrize("dims,batch", [([1024], 7), ([4096], 3), ([720], 5), ([16, 24, 40], 2), ([64, 48], 3),
+                                        ([6, 10, 12, 14], 1)])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_mixed_storage_fused(hip_ctx, monkeypatch, dims, batch, direction):
+    count = int(np.prod(dims)) * batch
+    x = o.complex_uniform(count, count % 983, np.complex64)
+    for prec, tol in ((F64C, 1e-7), (F16S, 1e-3)):
+        c = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec).with_inverse_normalization(True)
+        y, desc, yb = run_both(monkeypatch, c, direction, x)
+        xin = f16(x) if prec == F16S else x
+        ref = ref_c2c(xin, dims, batch, direction, normalize=True)
+        assert o.rel_l2(y, ref) <= tol, prec
+        assert o.rel_l2(yb, ref) <= tol, prec
+        if prec == F16S:
+            assert np.array_equal(y, f16(y))
+        # one pass per axis; the passes between the first and the last run
+        # on a compute-type copy
+        assert len(desc["passes"]) == len(dims)
+
+
+@pytest.mark.parametrize("direction,domain", [(FWD, SPATIAL), (INV, SPATIAL), (FWD, FREQ), (INV, FREQ)])
+@pytest.mark.parametrize("n,left,right", [(1024, 100, 300), (720, 0, 1), (4096, 4000, 4096), (1000, 0, 1000)])
+def test_zero_padding_fused(hip_ctx, monkeypatch, direction, domain, n, left, right):
+    batch = 3
+    x = o.complex_uniform(n * batch, n + left, np.complex64)
+    for prec, dt, tol in ((F32, np.complex64, 1e-5), (F64, np.complex128, 1e-13), (F16S, np.complex64, 1e-3)):
+        xs = x.astype(dt)
+        c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+            .with_zero_padding(0, left, right).with_zero_padding_domain(domain)
+        y, desc, yb = run_both(monkeypatch, c, direction, xs)
+        mask = np.zeros((batch, n), dtype=bool)
+        mask[:, left:right] = True
+        mask = mask.reshape(-1)
+        input_side = (direction == FWD) == (domain == SPATIAL)
+        xin = f16(xs) if prec == F16S else xs
+        xin = np.where(mask, 0, xin) if input_side else xin
+        expect = ref_c2c(xin, [n], batch, direction)
+        if not input_side:
+            expect = np.where(mask, 0, expect)
+            assert (y[mask] == 0).all() and (yb[mask] == 0).all()
+        if left == 0 and right == n:
+            # the whole axis is zero on one side: the result is exactly zero
+            assert (y == 0).all() and (yb == 0).all()
+            continue
+        assert o.rel_l2(y, expect) <= tol, prec
+        assert o.rel_l2(yb, expect) <= tol, prec
+
+
+def test_fused_edges_device_resident_and_chunks(hip_ctx, monkeypatch):
+    """Device-resident f16 buffers through the fused plan, a batch large
+    enough for several chunks, and a plan that does not qualify (four-step)
+    keeping its boundary passes."""
+    import torch
+    n, batch = 1024, 4096
+    x = o.complex_uniform(n * batch, 31, np.complex64)
+    ctx = vk.HipExecutionContext(0)
+    try:
+        ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(F16S), FWD)
+        plan = ctx.plan(ir)
+        assert plan.describe()["boundary"]["fused_edges"]
+        xs = torch.from_numpy(x.view(np.float32).astype(np.float16)).cuda()
+        ys = torch.empty_like(xs)
+        plan.execute_tensors(xs, ys)
+        torch.cuda.synchronize()
+        y = ys.cpu().numpy().astype(np.float32).view(np.complex64)
+        for b in (0, 1, 2047, 4095):
+            ref = o.fft(f16(x[b * n:(b + 1) * n]).astype(np.complex128))
+            assert o.rel_l2(y[b * n:(b + 1) * n], ref) <= 1e-3, b
+        big = vk.TransformIr.build(vk.FftConfig.new([1 << 20]).with_batch_count(2).with_precision(F16S), FWD)
+        assert not ctx.plan(big).describe()["boundary"]["fused_edges"]
+    finally:
+        ctx.close()

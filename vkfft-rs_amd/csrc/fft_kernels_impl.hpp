@@ -271,6 +271,59 @@ struct IoPlainStaged : IoPlain {
     static constexpr int kStore = LAY_STAGED;
 };
 
+// Storage type of half the compute precision (F16StorageF32Compute,
+// F64ComputeF32Storage: src/config.rs:108-145).
+template <typename T>
+struct Narrow;
+template <>
+struct Narrow<float> {
+    using type = _Float16;
+};
+template <>
+struct Narrow<double> {
+    using type = float;
+};
+
+// IoPlain with the plan's boundary work in its loads and stores (KF_EDGE):
+// NI / NO read / write storage of half the compute precision (converted on
+// load, rounded to nearest on store), and the element interval [zl, zr) of
+// each line reads as zero (KF_ZERO_IN) or is written as zero (KF_ZERO_OUT),
+// the logical zero intervals of src/zero_pad_ir.rs:320-345, 607-647. Line
+// strides count elements of the storage type.
+template <bool NI, bool NO>
+struct IoEdge : IoPlain {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        if ((a.flags & KF_ZERO_IN) && e >= a.zl && e < a.zr) return zero<T>();
+        if constexpr (NI) {
+            using U = typename Narrow<T>::type;
+            const cpx<U> v = ldg_in<NTIO>(a, (const cpx<U>*)a.in + L.ib + e * a.in_es);
+            return mk((T)v.re, (T)v.im);
+        } else {
+            return ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es);
+        }
+    }
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        v = ((a.flags & KF_ZERO_OUT) && e >= a.zl && e < a.zr) ? zero<T>() : scale(v, (T)a.scale);
+        if constexpr (NO) {
+            using U = typename Narrow<T>::type;
+            stg_out<NTIO>(a, (cpx<U>*)a.out + L.ob + e * a.out_es, mk((U)v.re, (U)v.im));
+        } else {
+            stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, v);
+        }
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoEdge, D>(a, lds, li, a.flags & KF_IN_ROWMAJOR);
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoEdge, D, T, S>(a, lds, li, a.flags & KF_OUT_ROWMAJOR);
+    }
+};
+
 struct IoR2CFull : IoPlain {
     static constexpr bool kPtrLoad = false, kPtrStore = false;
     template <class D>
@@ -1392,8 +1445,20 @@ KernelFn pick_dyn(KernelKind kind) {
         default: return nullptr;
     }
 }
+// KK_PLAIN with boundary work (KF_EDGE): edge = 1 + narrow input + 2 * narrow output
+template <typename T, int S, bool W>
+KernelFn pick_edge(int edge) {
+    switch (edge) {
+        case 1: return k_dyn<T, S, IoEdge<false, false>, W>;
+        case 2: return k_dyn<T, S, IoEdge<true, false>, W>;
+        case 3: return k_dyn<T, S, IoEdge<false, true>, W>;
+        case 4: return k_dyn<T, S, IoEdge<true, true>, W>;
+        default: return nullptr;
+    }
+}
 template <typename T, int S>
-KernelFn pick(KernelKind kind, bool wide, int direct) {
+KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
+    if (edge) return kind == KK_PLAIN && !direct ? (wide ? pick_edge<T, S, true>(edge) : pick_edge<T, S, false>(edge)) : nullptr;
     if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
     if (direct && kind == KK_R2C_HALF)
         return wide ? k_dyn_r2c_direct<T, S, true> : k_dyn_r2c_direct<T, S, false>;

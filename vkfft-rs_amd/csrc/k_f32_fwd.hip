@@ -3,5 +3,7 @@
 #include "fft_kernels_impl.hpp"
 
 namespace vkfx {
-KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct) { return pick<float, -1>(kind, wide, direct); }
+KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct, int edge) {
+    return pick<float, -1>(kind, wide, direct, edge);
+}
 }  // namespace vkfx

@@ -3,5 +3,7 @@
 #include "fft_kernels_impl.hpp"
 
 namespace vkfx {
-KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct) { return pick<double, -1>(kind, wide, direct); }
+KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct, int edge) {
+    return pick<double, -1>(kind, wide, direct, edge);
+}
 }  // namespace vkfx

@@ -47,6 +47,15 @@ enum KFlags : int {
     KF_DYN_PRE = 64,      // with KF_DYN_DIRECT, even C2R: the first stage forms the preprocess from HBM
     KF_CONV_CONJ = 128,   // KK_CONV_1: conjugate the sequence spectrum (ConvolutionConjugation::Sequence)
     KF_CONV_CROSS = 256,  // KK_CONV_1: cross-power-spectrum normalization of the product
+    // KK_PLAIN in the staged runtime-shape kernel with the plan's boundary
+    // work inside its loads and stores (IoEdge): storage of half the compute
+    // precision on the input / output side, and the zero interval [zl, zr) of
+    // a line's elements read as zero / written as zero
+    KF_EDGE = 512,
+    KF_NARROW_IN = 1024,
+    KF_NARROW_OUT = 2048,
+    KF_ZERO_IN = 4096,
+    KF_ZERO_OUT = 8192,
 };
 
 // Butterflies per thread in one radix-R stage of the runtime-shape kernel
@@ -102,6 +111,7 @@ struct KArgs {
     // table block of stage s starts roff[s] bytes into rtab (rader_stage_table)
     const void* rtab;
     int roff[kMaxStages];
+    long long zl, zr;                  // KF_ZERO_IN / KF_ZERO_OUT element interval of a line
 };
 
 // Radices up to this are Stockham butterflies; a larger (prime) radix in a

@@ -8,10 +8,10 @@
 
 namespace vkfx {
 
-KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct);
-KernelFn pick_f32_inv(KernelKind kind, bool wide, int direct);
-KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct);
-KernelFn pick_f64_inv(KernelKind kind, bool wide, int direct);
+KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct, int edge);
+KernelFn pick_f32_inv(KernelKind kind, bool wide, int direct, int edge);
+KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct, int edge);
+KernelFn pick_f64_inv(KernelKind kind, bool wide, int direct, int edge);
 const FixedKernel* fixed_table_wave(int* count);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
@@ -160,8 +160,10 @@ static bool xcd_groups(KernelKind kind) {
 static KernelFn pick_kernel(KernelKind kind, int prec, int dir, int flags) {
     const bool wide = (flags & KF_DYN_WIDE) != 0;
     const int direct = (flags & KF_DYN_DIRECT) ? ((flags & KF_DYN_PRE) ? 2 : 1) : 0;
-    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide, direct) : pick_f32_inv(kind, wide, direct))
-                     : (dir < 0 ? pick_f64_fwd(kind, wide, direct) : pick_f64_inv(kind, wide, direct));
+    const int edge =
+        (flags & KF_EDGE) ? 1 + ((flags & KF_NARROW_IN) ? 1 : 0) + ((flags & KF_NARROW_OUT) ? 2 : 0) : 0;
+    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide, direct, edge) : pick_f32_inv(kind, wide, direct, edge))
+                     : (dir < 0 ? pick_f64_fwd(kind, wide, direct, edge) : pick_f64_inv(kind, wide, direct, edge));
 }
 
 const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed, int flags) {
@@ -199,6 +201,11 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         !(kind == KK_R2C_HALF && a.in_es == 1 && a.nstages >= 1 && a.radix[0] != 2) &&
         !(kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2 &&
           (!(a.flags & KF_DYN_PRE) || (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2))))
+        return (int)hipErrorInvalidConfiguration;
+    // boundary work runs in the staged runtime-shape C2C kernel only
+    if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE))
+        return (int)hipErrorInvalidValue;
+    if ((a.flags & KF_EDGE) && (fixed || kind != KK_PLAIN || (a.flags & KF_DYN_DIRECT) || a.zl > a.zr))
         return (int)hipErrorInvalidConfiguration;
     // the register-exchange kernels address contiguous lines (element stride 1)
     if (fixed && fixed->table == FT_WAVE1024 && (a.in_es != 1 || a.out_es != 1 || !a.tw))

@@ -807,6 +807,38 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
 
 unsigned blocks_for(long long lines, int G) { return (unsigned)((lines + G - 1) / G); }
 
+// Moves a KK_PLAIN launch onto the staged runtime-shape kernel (the only
+// kernel that carries boundary work): a fixed shape is replaced by the
+// runtime geometry of its length (rows: about 256 threads per block,
+// columns: 8 / 16 lines per block as for strided axes), the HBM-direct ends
+// are dropped.
+int to_staged_dynamic(Ctx& c, Launch& L) {
+    KArgs& a = L.a;
+    a.flags &= ~(KF_DYN_DIRECT | KF_DYN_PRE);
+    if (!L.fixed) return VKFX_OK;
+    const bool rows = (a.flags & KF_IN_ROWMAJOR) != 0;
+    const Geometry g0 = geometry((size_t)a.N, c.prec, 1, c.lds_max, c.lds_max);
+    if (!g0.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
+    const Geometry g = geometry((size_t)a.N, c.prec, rows ? std::max(1, 256 / g0.TT) : (c.prec ? 8 : 16),
+                                c.lds_max, c.lds_budget);
+    if (!g.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
+    a.TT = g.TT;
+    a.G = g.G;
+    a.LS = g.LS;
+    a.PS = g.PS;
+    a.nstages = (int)g.radix.size();
+    for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
+    a.flags &= ~KF_DYN_WIDE;
+    if (g.wide) a.flags |= KF_DYN_WIDE;
+    int rc = stage_table(c.p, g.N, c.prec, &a.tw);
+    if (rc) return rc;
+    L.grid = blocks_for(a.nlines, g.G);
+    L.block = (unsigned)(g.G * g.TT);
+    L.lds = g.lds;
+    L.fixed = nullptr;
+    return VKFX_OK;
+}
+
 KArgs blank() {
     KArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -2408,8 +2440,66 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         bool fused_in = false, fused_out = false;
         if (plain_1d && fmt_in) fused_in = fuse_batch_stride(true, in_bst);
         if (plain_1d && fmt_out) fused_out = fuse_batch_stride(false, out_bst);
-        const bool need_in = mixed || (fmt_in && !fused_in) || zp_in;
-        const bool need_out = mixed || (fmt_out && !fused_out) || zp_out;
+        // C2C whose passes are all one-upload Stockham line passes (1-D, or
+        // N-D without split axes or slab chunks) in chunks of the form: the
+        // first pass reads the caller's input, the others run in place on the
+        // output, the last one leaves the result there. The storage
+        // conversion (and, for rank 1, the zero interval: a line is then the
+        // whole axis) then happens in the first pass's loads and the last
+        // pass's stores, and the passes between run on a compute-type copy;
+        // no boundary pass runs (the reference keeps both inside its passes,
+        // src/zero_pad_ir.rs:607-617). VKFX_FUSED_EDGES=0 keeps the boundary
+        // passes (comparison runs).
+        auto edges_fusable = [&]() {
+            const char* e = getenv("VKFX_FUSED_EDGES");
+            if (e && e[0] == '0') return false;
+            if (d.transform != VKFX_C2C || d.perform_convolution || fmt_in || fmt_out || !(mixed || any_zero))
+                return false;
+            if (any_zero && rank != 1) return false;
+            int prev_chunk = -1;
+            for (size_t i = 0; i < p->launches.size(); ++i) {
+                const Launch& L = p->launches[i];
+                if (L.boundary || L.copy || L.r2r || L.conv || L.kind != KK_PLAIN || L.a.rtab) return false;
+                const bool first = L.chunk != prev_chunk;
+                if (L.chunk < prev_chunk || L.in_sel != (first ? SEL_IN : SEL_OUT) || L.out_sel != SEL_OUT)
+                    return false;
+                prev_chunk = L.chunk;
+            }
+            return !p->launches.empty();
+        };
+        const bool fused_edges = edges_fusable();
+        bool edge_stage = false;  // passes between the first and the last run on a compute-type copy
+        if (fused_edges) {
+            int prev_chunk = -1;
+            for (size_t i = 0; i < p->launches.size(); ++i) {
+                Launch& L = p->launches[i];
+                const bool first = L.chunk != prev_chunk;
+                const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
+                prev_chunk = L.chunk;
+                int rc = to_staged_dynamic(c, L);
+                if (rc) {
+                    delete p;
+                    return rc;
+                }
+                L.a.flags |= KF_EDGE;
+                if (any_zero) L.a.zl = (long long)d.zero_left[0], L.a.zr = (long long)d.zero_right[0];
+                if (first) {
+                    if (mixed) L.a.flags |= KF_NARROW_IN, L.in_off /= 2;
+                    if (zp_in) L.a.flags |= KF_ZERO_IN;
+                } else {
+                    L.in_sel = SEL_STAGE_OUT;
+                }
+                if (last) {
+                    if (mixed) L.a.flags |= KF_NARROW_OUT, L.out_off /= 2;
+                    if (zp_out) L.a.flags |= KF_ZERO_OUT;
+                } else {
+                    L.out_sel = SEL_STAGE_OUT;
+                    edge_stage = true;
+                }
+            }
+        }
+        const bool need_in = !fused_edges && (mixed || (fmt_in && !fused_in) || zp_in);
+        const bool need_out = !fused_edges && (mixed || (fmt_out && !fused_out) || zp_out);
         const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
         const size_t cin = p->in_bytes, cout = p->out_bytes;  // dense compute-type bytes
         const int in_scal = real_in ? 1 : 2, out_scal = real_out ? 1 : 2;
@@ -2458,10 +2548,11 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->stage_in_bytes = need_in ? cin : 0;
         // C2C runs in place on one copy when both sides are staged
         p->stage_shared = need_out && need_in && d.transform == VKFX_C2C;
-        p->stage_out_bytes = need_out && !p->stage_shared ? cout : 0;
+        p->stage_out_bytes = (need_out && !p->stage_shared) || edge_stage ? cout : 0;
         c.js << "\"boundary\":{\"input\":" << (need_in ? "true" : "false") << ",\"output\":"
              << (need_out ? "true" : "false") << ",\"fused_batch_stride\":[" << (fused_in ? "true" : "false")
-             << "," << (fused_out ? "true" : "false") << "],\"zero_padding\":\""
+             << "," << (fused_out ? "true" : "false") << "],\"fused_edges\":" << (fused_edges ? "true" : "false")
+             << ",\"zero_padding\":\""
              << (!any_zero ? "none" : d.zero_frequency ? "frequency" : "spatial") << "\",\"grouped_batch\":[";
         for (size_t i = 0; i < rank; ++i) c.js << (i ? "," : "") << d.grouped_batch[i];
         c.js << "]},";
