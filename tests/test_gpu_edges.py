@@ -37,11 +37,14 @@ def ref_c2c(x, dims, batch, direction, normalize=False):
 
 
 def run_both(monkeypatch, c, direction, x):
-    """(fused output, fused describe, boundary-pass output)."""
+    """(fused output, fused describe, boundary-pass output); the fused plan
+    also runs with staged ends only (VKFX_EDGE_DIRECT=0) and must give the
+    same values as with HBM-direct ends up to rounding."""
     out = []
-    for fused in ("1", "0"):
+    for fused, direct in (("1", "1"), ("1", "0"), ("0", "1")):
         monkeypatch.setenv("VKFX_FUSED_EDGES", fused)
-        ctx = vk.HipExecutionContext(0)  # own plan cache: plans read the switch when built
+        monkeypatch.setenv("VKFX_EDGE_DIRECT", direct)
+        ctx = vk.HipExecutionContext(0)  # own plan cache: plans read the switches when built
         try:
             ir = vk.TransformIr.build(c, direction)
             y = ctx.execute_transform(ir, x)
@@ -52,7 +55,11 @@ def run_both(monkeypatch, c, direction, x):
         kernels = [p["kernel"] for p in desc["passes"]]
         assert ("boundary_in" in kernels or "boundary_out" in kernels) == (fused == "0"), kernels
         out.append((y, desc))
-    return out[0][0], out[0][1], out[1][0]
+    (y, desc), (ys, _), (yb, _) = out
+    scale = max(float(np.max(np.abs(y))), 1e-30)
+    tol = {F16S: 2e-3, F32: 1e-5, F64C: 1e-6, F64: 1e-12}[c.precision]
+    assert float(np.max(np.abs(y - ys))) <= tol * scale
+    return y, desc, yb
 
 
 @pytest.mark.parametrize("dims,batch", [([1024], 7), ([4096], 3), ([720], 5), ([16, 24, 40], 2), ([64, 48], 3),

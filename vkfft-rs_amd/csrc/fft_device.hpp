@@ -377,19 +377,9 @@ enum StageMode : int {
 // Not inlined: the runtime-radix loop dispatches to one of these per stage,
 // and inlined cases share no registers (a dozen radix cases in one body need
 // more than 256 VGPRs and spill to scratch).
-template <typename T, int S, int R, bool WIDE, int MODE>
-__device__ __noinline__ void stage_rt(cpx<T>* __restrict__ line, const int N, const int P, const int TT,
-                                      const int t, const int ps, const StageTw tw, const cpx<T>* gsrc,
-                                      cpx<T>* gdst, const int valid, const T sc) {
-    // `line` always points into LDS; without this a non-inlined function
-    // addresses it with flat instructions instead of ds_read / ds_write
-    // (the builtin exists in the device pass only)
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
-#endif
-    typedef T v2 __attribute__((ext_vector_type(2)));
-    typedef const __attribute__((address_space(1))) v2* gsrc_t;
-    typedef __attribute__((address_space(1))) v2* gdst_t;
+template <typename T, int S, int R, bool WIDE, int MODE, class Ld, class St>
+__device__ __forceinline__ void stage_rt_body(cpx<T>* __restrict__ line, const int N, const int P, const int TT,
+                                              const int t, const int ps, const StageTw& tw, Ld&& ld, St&& st) {
     constexpr int MJ = dyn_butterflies_per_thread(R, WIDE);
     const int NB = N / R;
     cpx<T> v[MJ][R];
@@ -400,8 +390,7 @@ __device__ __noinline__ void stage_rt(cpx<T>* __restrict__ line, const int N, co
 #pragma unroll
             for (int i = 0; i < R; ++i) {
                 if constexpr (MODE == SM_FIRST) {
-                    const v2 x = ((gsrc_t)gsrc)[b + i * NB];
-                    v[j][i] = mk(x.x, x.y);
+                    v[j][i] = ld(b + i * NB);
                 } else {
                     v[j][i] = line[lpad(b + i * NB, ps)];
                 }
@@ -426,13 +415,7 @@ __device__ __noinline__ void stage_rt(cpx<T>* __restrict__ line, const int N, co
 #pragma unroll
             for (int q = 0; q < R; ++q) {
                 if constexpr (MODE == SM_LAST) {
-                    if (valid) {
-                        const cpx<T> y = scale(v[j][q], sc);
-                        v2 x;
-                        x.x = y.re;
-                        x.y = y.im;
-                        ((gdst_t)gdst)[base + q * P] = x;
-                    }
+                    st(base + q * P, v[j][q]);
                 } else {
                     line[lpad(base + q * P, ps)] = v[j][q];
                 }
@@ -440,6 +423,68 @@ __device__ __noinline__ void stage_rt(cpx<T>* __restrict__ line, const int N, co
         }
     }
     if constexpr (MODE != SM_LAST) __syncthreads();
+}
+
+template <typename T, int S, int R, bool WIDE, int MODE>
+__device__ __noinline__ void stage_rt(cpx<T>* __restrict__ line, const int N, const int P, const int TT,
+                                      const int t, const int ps, const StageTw tw, const cpx<T>* gsrc,
+                                      cpx<T>* gdst, const int valid, const T sc) {
+    // `line` always points into LDS; without this a non-inlined function
+    // addresses it with flat instructions instead of ds_read / ds_write
+    // (the builtin exists in the device pass only)
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
+#endif
+    typedef T v2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) v2* gsrc_t;
+    typedef __attribute__((address_space(1))) v2* gdst_t;
+    stage_rt_body<T, S, R, WIDE, MODE>(
+        line, N, P, TT, t, ps, tw,
+        [&](int e) {
+            const v2 x = ((gsrc_t)gsrc)[e];
+            return mk(x.x, x.y);
+        },
+        [&](int o, cpx<T> v) {
+            if (valid) {
+                const cpx<T> y = scale(v, sc);
+                v2 x;
+                x.x = y.re;
+                x.y = y.im;
+                ((gdst_t)gdst)[o] = x;
+            }
+        });
+}
+
+// The HBM end of a runtime-shape direct C2C stage with the plan's boundary
+// work (KF_EDGE): the HBM side holds storage type U (converted on load,
+// rounded to nearest on store), and elements of [zl, zr) read as zero
+// (SM_FIRST) or are written as zero (SM_LAST).
+template <typename T, int S, int R, bool WIDE, int MODE, typename U>
+__device__ __noinline__ void stage_rt_edge(cpx<T>* __restrict__ line, const int N, const int P, const int TT,
+                                           const int t, const int ps, const StageTw tw, const cpx<U>* gsrc,
+                                           cpx<U>* gdst, const int valid, const T sc, const int zl, const int zr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)line));
+#endif
+    typedef U u2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(1))) u2* gsrc_t;
+    typedef __attribute__((address_space(1))) u2* gdst_t;
+    stage_rt_body<T, S, R, WIDE, MODE>(
+        line, N, P, TT, t, ps, tw,
+        [&](int e) {
+            if (e >= zl && e < zr) return mk((T)0, (T)0);
+            const u2 x = ((gsrc_t)gsrc)[e];
+            return mk((T)x.x, (T)x.y);
+        },
+        [&](int o, cpx<T> v) {
+            if (valid) {
+                const cpx<T> y = (o >= zl && o < zr) ? mk((T)0, (T)0) : scale(v, sc);
+                u2 x;
+                x.x = (U)y.re;
+                x.y = (U)y.im;
+                ((gdst_t)gdst)[o] = x;
+            }
+        });
 }
 
 // Dispatch of one stage on its runtime radix. Radix-2 HBM stages are not
@@ -567,6 +612,53 @@ __device__ __forceinline__ void run_stages_direct(cpx<T>* __restrict__ line, con
         P *= radix[s];
     }
     stage_rt_radix<T, S, WIDE, SM_LAST>(radix[nst - 1], line, N, P, TT, t, ps, tw, src, dst, valid, sc);
+}
+
+// Dispatch of an HBM end with boundary work on its runtime radix (no radix 2,
+// as for the plain direct ends).
+template <typename T, int S, bool WIDE, int MODE, typename U>
+__device__ __forceinline__ void stage_rt_edge_radix(int R, cpx<T>* __restrict__ line, const int N, const int P,
+                                                    const int TT, const int t, const int ps, const StageTw& tw,
+                                                    const cpx<U>* gsrc, cpx<U>* gdst, const int valid, const T sc,
+                                                    const int zl, const int zr) {
+#define VKFX_STAGE_CASE(RR) \
+    case RR: stage_rt_edge<T, S, RR, WIDE, MODE, U>(line, N, P, TT, t, ps, tw, gsrc, gdst, valid, sc, zl, zr); break;
+    switch (R) {
+        VKFX_STAGE_CASE(3)
+        VKFX_STAGE_CASE(4)
+        VKFX_STAGE_CASE(5)
+        VKFX_STAGE_CASE(6)
+        VKFX_STAGE_CASE(7)
+        VKFX_STAGE_CASE(8)
+        VKFX_STAGE_CASE(9)
+        VKFX_STAGE_CASE(10)
+        VKFX_STAGE_CASE(11)
+        VKFX_STAGE_CASE(12)
+        VKFX_STAGE_CASE(13)
+        VKFX_STAGE_CASE(16)
+        default: break;
+    }
+#undef VKFX_STAGE_CASE
+}
+
+// run_stages_direct with boundary work at both HBM ends: the first stage
+// reads storage type UI with the input zero interval [zil, zir), the last
+// writes storage type UO with the output zero interval [zol, zor).
+template <typename T, int S, bool WIDE, typename UI, typename UO>
+__device__ __forceinline__ void run_stages_direct_edge(cpx<T>* __restrict__ line, const int N, const int TT,
+                                                       const int t, const int ps, const int nst,
+                                                       const int* __restrict__ radix, const StageTw& tw,
+                                                       const cpx<UI>* src, cpx<UO>* dst, int valid, T sc,
+                                                       int zil, int zir, int zol, int zor) {
+    stage_rt_edge_radix<T, S, WIDE, SM_FIRST, UI>(radix[0], line, N, 1, TT, t, ps, tw, src, nullptr, valid, sc, zil,
+                                                  zir);
+    int P = radix[0];
+    for (int s = 1; s + 1 < nst; ++s) {
+        stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, nullptr, 0, (T)1);
+        P *= radix[s];
+    }
+    stage_rt_edge_radix<T, S, WIDE, SM_LAST, UO>(radix[nst - 1], line, N, P, TT, t, ps, tw, nullptr, dst, valid, sc,
+                                                 zol, zor);
 }
 
 }  // namespace vkfx

@@ -34,6 +34,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "fft_device.hpp"
 #include "kernels.hpp"
 
@@ -941,6 +943,27 @@ __global__ __launch_bounds__(512) void k_dyn_direct(const KArgs a) {
                                   (const cpx<T>*)a.in + L.ib, (cpx<T>*)a.out + L.ob, L.valid, (T)a.scale);
 }
 
+// k_dyn_direct with the plan's boundary work at its HBM ends (KF_EDGE):
+// storage of half the compute precision on the input (NI) / output (NO)
+// side, the zero interval [zl, zr) on the input (KF_ZERO_IN) or the output
+// (KF_ZERO_OUT) side.
+template <typename T, int S, bool WIDE, bool NI, bool NO>
+__global__ __launch_bounds__(512) void k_dyn_direct_edge(const KArgs a) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
+    using UI = std::conditional_t<NI, typename Narrow<T>::type, T>;
+    using UO = std::conditional_t<NO, typename Narrow<T>::type, T>;
+    const int tid = threadIdx.x;
+    const int g = tid / a.TT, t = tid - g * a.TT;
+    const LineInfo L = line_default(a, group_index(a), g);
+    const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
+    const bool zi = (a.flags & KF_ZERO_IN) != 0, zo = (a.flags & KF_ZERO_OUT) != 0;
+    run_stages_direct_edge<T, S, WIDE, UI, UO>(lds + g * a.LS, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw,
+                                               (const cpx<UI>*)a.in + L.ib, (cpx<UO>*)a.out + L.ob, L.valid,
+                                               (T)a.scale, zi ? (int)a.zl : 0, zi ? (int)a.zr : 0,
+                                               zo ? (int)a.zl : 0, zo ? (int)a.zr : 0);
+}
+
 // Runtime-shape even R2C of one upload (KF_DYN_DIRECT): the first stage loads
 // the real input pairs straight from HBM (contiguous lines), the postprocess
 // stays the staged epilogue of IoR2CHalf.
@@ -1445,20 +1468,24 @@ KernelFn pick_dyn(KernelKind kind) {
         default: return nullptr;
     }
 }
-// KK_PLAIN with boundary work (KF_EDGE): edge = 1 + narrow input + 2 * narrow output
+// KK_PLAIN with boundary work (KF_EDGE): edge = 1 + narrow input + 2 * narrow
+// output; staged ends, or HBM-direct ends over contiguous lines
 template <typename T, int S, bool W>
-KernelFn pick_edge(int edge) {
+KernelFn pick_edge(int edge, bool direct) {
     switch (edge) {
-        case 1: return k_dyn<T, S, IoEdge<false, false>, W>;
-        case 2: return k_dyn<T, S, IoEdge<true, false>, W>;
-        case 3: return k_dyn<T, S, IoEdge<false, true>, W>;
-        case 4: return k_dyn<T, S, IoEdge<true, true>, W>;
+        case 1: return direct ? k_dyn_direct_edge<T, S, W, false, false> : k_dyn<T, S, IoEdge<false, false>, W>;
+        case 2: return direct ? k_dyn_direct_edge<T, S, W, true, false> : k_dyn<T, S, IoEdge<true, false>, W>;
+        case 3: return direct ? k_dyn_direct_edge<T, S, W, false, true> : k_dyn<T, S, IoEdge<false, true>, W>;
+        case 4: return direct ? k_dyn_direct_edge<T, S, W, true, true> : k_dyn<T, S, IoEdge<true, true>, W>;
         default: return nullptr;
     }
 }
 template <typename T, int S>
 KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
-    if (edge) return kind == KK_PLAIN && !direct ? (wide ? pick_edge<T, S, true>(edge) : pick_edge<T, S, false>(edge)) : nullptr;
+    if (edge) {
+        if (kind != KK_PLAIN || direct > 1) return nullptr;
+        return wide ? pick_edge<T, S, true>(edge, direct == 1) : pick_edge<T, S, false>(edge, direct == 1);
+    }
     if (direct && kind == KK_PLAIN) return wide ? k_dyn_direct<T, S, true> : k_dyn_direct<T, S, false>;
     if (direct && kind == KK_R2C_HALF)
         return wide ? k_dyn_r2c_direct<T, S, true> : k_dyn_r2c_direct<T, S, false>;

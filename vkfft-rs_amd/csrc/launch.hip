@@ -202,10 +202,12 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
         !(kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2 &&
           (!(a.flags & KF_DYN_PRE) || (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2))))
         return (int)hipErrorInvalidConfiguration;
-    // boundary work runs in the staged runtime-shape C2C kernel only
+    // boundary work runs in the runtime-shape C2C kernels only (staged, or
+    // HBM-direct under the direct kernel's own conditions below)
     if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE))
         return (int)hipErrorInvalidValue;
-    if ((a.flags & KF_EDGE) && (fixed || kind != KK_PLAIN || (a.flags & KF_DYN_DIRECT) || a.zl > a.zr))
+    if ((a.flags & KF_EDGE) && (fixed || kind != KK_PLAIN || (a.flags & KF_DYN_PRE) || a.zl > a.zr || a.zl < 0 ||
+                                a.zr > a.N))
         return (int)hipErrorInvalidConfiguration;
     // the register-exchange kernels address contiguous lines (element stride 1)
     if (fixed && fixed->table == FT_WAVE1024 && (a.in_es != 1 || a.out_es != 1 || !a.tw))

@@ -807,35 +807,43 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
 
 unsigned blocks_for(long long lines, int G) { return (unsigned)((lines + G - 1) / G); }
 
-// Moves a KK_PLAIN launch onto the staged runtime-shape kernel (the only
-// kernel that carries boundary work): a fixed shape is replaced by the
-// runtime geometry of its length (rows: about 256 threads per block,
-// columns: 8 / 16 lines per block as for strided axes), the HBM-direct ends
-// are dropped.
-int to_staged_dynamic(Ctx& c, Launch& L) {
+// Moves a KK_PLAIN launch onto the runtime-shape kernels (the only kernels
+// that carry boundary work): a fixed shape is replaced by the runtime
+// geometry of its length (rows: about 256 threads per block, columns: 8 / 16
+// lines per block as for strided axes). Contiguous lines keep HBM-direct ends
+// under the direct kernel's conditions; the others run staged.
+int to_edge_kernel(Ctx& c, Launch& L) {
     KArgs& a = L.a;
+    if (L.fixed) {
+        const bool rows = (a.flags & KF_IN_ROWMAJOR) != 0;
+        const Geometry g0 = geometry((size_t)a.N, c.prec, 1, c.lds_max, c.lds_max);
+        if (!g0.ok)
+            return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
+        const Geometry g = geometry((size_t)a.N, c.prec, rows ? std::max(1, 256 / g0.TT) : (c.prec ? 8 : 16),
+                                    c.lds_max, c.lds_budget);
+        if (!g.ok)
+            return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
+        a.TT = g.TT;
+        a.G = g.G;
+        a.LS = g.LS;
+        a.PS = g.PS;
+        a.nstages = (int)g.radix.size();
+        for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
+        a.flags &= ~KF_DYN_WIDE;
+        if (g.wide) a.flags |= KF_DYN_WIDE;
+        int rc = stage_table(c.p, g.N, c.prec, &a.tw);
+        if (rc) return rc;
+        L.grid = blocks_for(a.nlines, g.G);
+        L.block = (unsigned)(g.G * g.TT);
+        L.lds = g.lds;
+        L.fixed = nullptr;
+    }
     a.flags &= ~(KF_DYN_DIRECT | KF_DYN_PRE);
-    if (!L.fixed) return VKFX_OK;
-    const bool rows = (a.flags & KF_IN_ROWMAJOR) != 0;
-    const Geometry g0 = geometry((size_t)a.N, c.prec, 1, c.lds_max, c.lds_max);
-    if (!g0.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
-    const Geometry g = geometry((size_t)a.N, c.prec, rows ? std::max(1, 256 / g0.TT) : (c.prec ? 8 : 16),
-                                c.lds_max, c.lds_budget);
-    if (!g.ok) return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
-    a.TT = g.TT;
-    a.G = g.G;
-    a.LS = g.LS;
-    a.PS = g.PS;
-    a.nstages = (int)g.radix.size();
-    for (int i = 0; i < a.nstages; ++i) a.radix[i] = g.radix[i];
-    a.flags &= ~KF_DYN_WIDE;
-    if (g.wide) a.flags |= KF_DYN_WIDE;
-    int rc = stage_table(c.p, g.N, c.prec, &a.tw);
-    if (rc) return rc;
-    L.grid = blocks_for(a.nlines, g.G);
-    L.block = (unsigned)(g.G * g.TT);
-    L.lds = g.lds;
-    L.fixed = nullptr;
+    const char* de = getenv("VKFX_EDGE_DIRECT");  // 0: staged ends only (comparison runs)
+    const bool direct_on = !(de && de[0] == '0');
+    if (direct_on && (a.flags & KF_IN_ROWMAJOR) && (a.flags & KF_OUT_ROWMAJOR) && a.in_es == 1 && a.out_es == 1 &&
+        a.nstages >= 2 && a.radix[0] != 2 && a.radix[a.nstages - 1] != 2)
+        a.flags |= KF_DYN_DIRECT;
     return VKFX_OK;
 }
 
@@ -2476,7 +2484,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 const bool first = L.chunk != prev_chunk;
                 const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
                 prev_chunk = L.chunk;
-                int rc = to_staged_dynamic(c, L);
+                int rc = to_edge_kernel(c, L);
                 if (rc) {
                     delete p;
                     return rc;
