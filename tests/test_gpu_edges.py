@@ -51,7 +51,7 @@ def run_both(monkeypatch, c, direction, x):
             desc = ctx.plan(ir).describe()
         finally:
             ctx.close()
-        assert desc["boundary"]["fused_edges"] == (fused == "1")
+        assert (desc["boundary"]["fused_edges"] or desc["boundary"]["fused_layout"]) == (fused == "1")
         kernels = [p["kernel"] for p in desc["passes"]]
         assert ("boundary_in" in kernels or "boundary_out" in kernels) == (fused == "0"), kernels
         out.append((y, desc))
@@ -62,8 +62,7 @@ def run_both(monkeypatch, c, direction, x):
     return y, desc, yb
 
 
-@pytest.mark.parametrize("dims,batch", [([1024], 7), ([4096], 3), ([720], 5), ([16, 24, 40], 2), ([64, 48], 3),
-                                        ([6, 10, 12, 14], 1)])
+@pytest.mark.parametrize("dims,batch", [([1024], 7), ([4096], 3), ([720], 5), ([1000], 2)])
 @pytest.mark.parametrize("direction", [FWD, INV])
 def test_mixed_storage_fused(hip_ctx, monkeypatch, dims, batch, direction):
     count = int(np.prod(dims)) * batch
@@ -77,9 +76,25 @@ def test_mixed_storage_fused(hip_ctx, monkeypatch, dims, batch, direction):
         assert o.rel_l2(yb, ref) <= tol, prec
         if prec == F16S:
             assert np.array_equal(y, f16(y))
-        # one pass per axis; the passes between the first and the last run
-        # on a compute-type copy
-        assert len(desc["passes"]) == len(dims)
+        assert [p["kernel"] for p in desc["passes"]] == ["stockham"]
+
+
+@pytest.mark.parametrize("dims,batch", [([16, 24, 40], 2), ([64, 48], 3), ([6, 10, 12, 14], 1), ([4096, 16], 2),
+                                        ([8, 2048, 24], 1), ([8, 97, 40], 1)])
+def test_mixed_storage_nd_flat_boundary(hip_ctx, dims, batch):
+    """N-D mixed storage keeps its fixed-shape passes between two boundary
+    passes, which are flat vectorized conversions for dense layouts."""
+    count = int(np.prod(dims)) * batch
+    x = o.complex_uniform(count, count % 983, np.complex64)
+    for prec, tol in ((F64C, 1e-7), (F16S, 1e-3)):
+        c = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec)
+        ir = vk.TransformIr.build(c, FWD)
+        y = hip_ctx.execute_transform(ir, x)
+        desc = hip_ctx.plan(ir).describe()
+        kernels = [p["kernel"] for p in desc["passes"]]
+        assert kernels[0] == "boundary_in" and kernels[-1] == "boundary_out", kernels
+        xin = f16(x) if prec == F16S else x
+        assert o.rel_l2(y, ref_c2c(xin, dims, batch, FWD)) <= tol, prec
 
 
 @pytest.mark.parametrize("direction,domain", [(FWD, SPATIAL), (INV, SPATIAL), (FWD, FREQ), (INV, FREQ)])
@@ -134,3 +149,74 @@ def test_fused_edges_device_resident_and_chunks(hip_ctx, monkeypatch):
         assert not ctx.plan(big).describe()["boundary"]["fused_edges"]
     finally:
         ctx.close()
+
+
+def layout_cfg(dims, batch, prec, fmt_in, fmt_out):
+    """Formatted strides on the chosen sides: every axis but the fastest
+    padded by a few elements, and the batch stride padded too."""
+    c = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec)
+    for side, on in (("input", fmt_in), ("output", fmt_out)):
+        if not on:
+            continue
+        st = 1
+        for ax in range(len(dims) - 1, -1, -1):
+            if ax < len(dims) - 1:
+                st = st + 3 + ax
+                c = getattr(c, f"with_{side}_buffer_axis_stride")(ax, st)
+            st *= dims[ax]
+        c = getattr(c, f"with_{side}_buffer_batch_stride")(st + 5)
+    return c
+
+
+@pytest.mark.parametrize("dims,batch", [([1024], 3), ([32, 48], 3), ([8, 12, 40], 2), ([64, 64], 2), ([4, 300], 2),
+                                        ([3, 5, 512], 2)])
+@pytest.mark.parametrize("sides", [(True, False), (False, True), (True, True)])
+def test_formatted_layout_fused(hip_ctx, monkeypatch, dims, batch, sides):
+    """Formatted strides read and written by the first and last passes
+    (rank <= 3): alone, and together with storage conversion."""
+    count = int(np.prod(dims)) * batch
+    x = o.complex_uniform(count, count % 887, np.complex64)
+    for prec, tol in ((F32, 1e-5), (F64, 1e-12), (F16S, 1e-3), (F64C, 1e-7)):
+        if len(dims) == 1 and prec in (F32, F64):
+            continue  # the 1-D batch stride alone is the passes' own stride (test_gpu_layout)
+        xs = x.astype(np.complex128) if prec == F64 else x
+        c = layout_cfg(dims, batch, prec, *sides)
+        if len(dims) > 1 and prec in (F16S, F64C):
+            # N-D mixed storage: boundary passes carry both the layout and the conversion
+            ir = vk.TransformIr.build(c, FWD)
+            y = hip_ctx.execute_transform(ir, xs)
+            assert not hip_ctx.plan(ir).describe()["boundary"]["fused_layout"]
+            assert o.rel_l2(y, ref_c2c(f16(xs) if prec == F16S else xs, dims, batch, FWD)) <= tol, prec
+            continue
+        y, desc, yb = run_both(monkeypatch, c, FWD, xs)
+        assert desc["boundary"]["fused_layout"], desc["boundary"]
+        xin = f16(xs) if prec == F16S else xs
+        ref = ref_c2c(xin, dims, batch, FWD)
+        assert o.rel_l2(y, ref) <= tol, prec
+        assert o.rel_l2(yb, ref) <= tol, prec
+
+
+@pytest.mark.parametrize("dims,prec", [([8, 12, 40], F32), ([1000], F16S)])
+def test_formatted_layout_fused_gaps_untouched(hip_ctx, dims, prec):
+    """The fused last pass writes only the logical positions of a formatted
+    output (gaps keep their NaN), from a formatted input."""
+    import torch
+    batch = 2
+    c = layout_cfg(dims, batch, prec, True, True)
+    ir = vk.TransformIr.build(c, FWD)
+    plan = hip_ctx.plan(ir)
+    assert plan.describe()["boundary"]["fused_layout"]
+    x = o.complex_uniform(int(np.prod(dims)) * batch, 41, np.complex64)
+    xs = ir.to_storage(ir.pack_input(x))
+    tdt = torch.float16 if prec == F16S else torch.float32
+    dx = torch.from_numpy(np.ascontiguousarray(xs).view(np.float16 if prec == F16S else np.float32)).cuda()
+    dy = torch.full((plan.out_bytes // (2 if prec == F16S else 4),), float("nan"), device="cuda", dtype=tdt)
+    plan.execute_tensors(dx, dy)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().astype(np.float32).view(np.complex64)
+    idx, _ = ir._physical_index(True)
+    gaps = np.ones(y.size, dtype=bool)
+    gaps[idx] = False
+    assert gaps.any() and np.isnan(y[gaps].real).all() and np.isnan(y[gaps].imag).all()
+    xin = f16(x) if prec == F16S else x
+    assert o.rel_l2(y[idx], ref_c2c(xin, dims, batch, FWD)) <= (1e-3 if prec == F16S else 1e-5)

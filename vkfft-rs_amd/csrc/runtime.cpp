@@ -2448,66 +2448,148 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         bool fused_in = false, fused_out = false;
         if (plain_1d && fmt_in) fused_in = fuse_batch_stride(true, in_bst);
         if (plain_1d && fmt_out) fused_out = fuse_batch_stride(false, out_bst);
-        // C2C whose passes are all one-upload Stockham line passes (1-D, or
-        // N-D without split axes or slab chunks) in chunks of the form: the
-        // first pass reads the caller's input, the others run in place on the
-        // output, the last one leaves the result there. The storage
-        // conversion (and, for rank 1, the zero interval: a line is then the
-        // whole axis) then happens in the first pass's loads and the last
-        // pass's stores, and the passes between run on a compute-type copy;
-        // no boundary pass runs (the reference keeps both inside its passes,
-        // src/zero_pad_ir.rs:607-617). VKFX_FUSED_EDGES=0 keeps the boundary
-        // passes (comparison runs).
-        auto edges_fusable = [&]() {
-            const char* e = getenv("VKFX_FUSED_EDGES");
-            if (e && e[0] == '0') return false;
-            if (d.transform != VKFX_C2C || d.perform_convolution || fmt_in || fmt_out || !(mixed || any_zero))
-                return false;
-            if (any_zero && rank != 1) return false;
+        // C2C plans in chunks of the form: the first pass (a plain one-upload
+        // line pass) reads the caller's input, the passes between run in
+        // place on the output and the workspace, the last (a plain one-upload
+        // line pass) leaves the result in the output. The boundary work then
+        // happens inside the first pass's loads and the last pass's stores,
+        // and no boundary pass runs (the reference keeps it inside its
+        // passes, src/zero_pad_ir.rs:607-617):
+        //  - rank 1, one pass per chunk: storage conversion and the zero
+        //    interval (a line is the whole axis) on runtime-shape kernels
+        //    with KF_EDGE;
+        //  - formatted layouts of rank <= 3 with every axis active and one
+        //    pass per axis: the first pass's lines (batch, axis 0, axis 1)
+        //    and the last pass's lines (batch, axis 1, axis 2) take the
+        //    caller's strides (three line levels), on any kernel.
+        // When the output is narrower or formatted, the passes between the
+        // first and the last run on a compute-type copy in the workspace.
+        // VKFX_FUSED_EDGES=0 keeps the boundary passes (comparison runs).
+        const char* fe = getenv("VKFX_FUSED_EDGES");
+        const bool fuse_on = !(fe && fe[0] == '0');
+        bool all_active = true;
+        for (size_t i = 0; i < rank; ++i) all_active &= d.dims[i] > 1 && !(d.omit_dimension >> i & 1u);
+        // the first and last passes of a chunk are plain one-upload line
+        // passes; the passes between (split-axis and Bluestein axis passes
+        // included) touch only the output, in place, and the workspace
+        auto chunks_fusable = [&]() {
+            if (d.transform != VKFX_C2C || d.perform_convolution || p->launches.empty()) return false;
             int prev_chunk = -1;
             for (size_t i = 0; i < p->launches.size(); ++i) {
                 const Launch& L = p->launches[i];
-                if (L.boundary || L.copy || L.r2r || L.conv || L.kind != KK_PLAIN || L.a.rtab) return false;
+                if (L.boundary || L.copy || L.r2r || L.conv || L.chunk < prev_chunk) return false;
                 const bool first = L.chunk != prev_chunk;
-                if (L.chunk < prev_chunk || L.in_sel != (first ? SEL_IN : SEL_OUT) || L.out_sel != SEL_OUT)
+                const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
+                const bool plain = L.kind == KK_PLAIN && !L.a.rtab;
+                if ((first || last) && !plain) return false;
+                if ((L.in_sel == SEL_IN) != first || (first && L.out_sel != SEL_OUT && !last)) return false;
+                if (last && L.out_sel != SEL_OUT) return false;
+                if ((L.in_sel != SEL_IN && L.in_sel != SEL_OUT && L.in_sel != SEL_WORK) ||
+                    (L.out_sel != SEL_OUT && L.out_sel != SEL_WORK))
                     return false;
                 prev_chunk = L.chunk;
             }
-            return !p->launches.empty();
+            return true;
         };
-        const bool fused_edges = edges_fusable();
+        // one launch per active axis and chunk, rows first and axis 0 last
+        auto layout_fusable = [&]() {
+            if (rank > 3 || !all_active) return false;
+            size_t run = 0;
+            for (size_t i = 0; i < p->launches.size(); ++i) {
+                ++run;
+                if (i + 1 == p->launches.size() || p->launches[i + 1].chunk != p->launches[i].chunk) {
+                    if (run != rank) return false;
+                    run = 0;
+                }
+            }
+            return true;
+        };
+        const bool shape_ok = fuse_on && chunks_fusable();
+        const bool want_layout = (fmt_in && !fused_in) || (fmt_out && !fused_out);
+        const bool layout_ok = want_layout && shape_ok && layout_fusable();
+        // Edges ride on runtime-shape kernels, which pay where a 1-D line is
+        // the whole transform (mixed 1024 x 8192: 33.5 us against 94.8 with
+        // boundary passes) but not on N-D column passes (F16 2048^2 x 4: the
+        // runtime-shape column pass with the conversion 145 us against 35 us
+        // for the fixed shape plus 40 us for a flat conversion pass).
+        const bool fused_edges = shape_ok && (mixed || any_zero) && rank == 1 && (!want_layout || layout_ok);
+        const bool fused_layout = layout_ok && (fused_edges || !(mixed || any_zero));
         bool edge_stage = false;  // passes between the first and the last run on a compute-type copy
-        if (fused_edges) {
+        if (fused_edges || fused_layout) {
+            const bool stage_mid = mixed || (fmt_out && !fused_out);
+            const size_t cs = csize(c.prec);
+            const size_t scs = (store_t == 0 ? 2 : store_t == 1 ? 4 : 8) * 2;  // storage bytes per complex element
+            long long per_batch = 1;
+            for (size_t i = 0; i < rank; ++i) per_batch *= (long long)d.dims[i];
+            const long long* dm = in_dims;
             int prev_chunk = -1;
             for (size_t i = 0; i < p->launches.size(); ++i) {
                 Launch& L = p->launches[i];
                 const bool first = L.chunk != prev_chunk;
                 const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
                 prev_chunk = L.chunk;
-                int rc = to_edge_kernel(c, L);
-                if (rc) {
-                    delete p;
-                    return rc;
+                if (fused_edges && (first || last)) {
+                    int rc = to_edge_kernel(c, L);
+                    if (rc) {
+                        delete p;
+                        return rc;
+                    }
+                    L.a.flags |= KF_EDGE;
+                    if (any_zero) L.a.zl = (long long)d.zero_left[0], L.a.zr = (long long)d.zero_right[0];
+                    if (first && mixed) L.a.flags |= KF_NARROW_IN;
+                    if (first && zp_in) L.a.flags |= KF_ZERO_IN;
+                    if (last && mixed) L.a.flags |= KF_NARROW_OUT;
+                    if (last && zp_out) L.a.flags |= KF_ZERO_OUT;
                 }
-                L.a.flags |= KF_EDGE;
-                if (any_zero) L.a.zl = (long long)d.zero_left[0], L.a.zr = (long long)d.zero_right[0];
+                KArgs& a = L.a;
                 if (first) {
-                    if (mixed) L.a.flags |= KF_NARROW_IN, L.in_off /= 2;
-                    if (zp_in) L.a.flags |= KF_ZERO_IN;
-                } else {
+                    const long long b0 = (long long)(L.in_off / ((size_t)per_batch * cs));
+                    const bool fmt = fmt_in && fused_layout;
+                    const long long bst = fmt ? in_bst : per_batch;
+                    L.in_off = (size_t)(b0 * bst) * (mixed ? scs : cs);
+                    if (fmt && rank == 1) {
+                        a.in_os = bst;
+                    } else if (fmt) {
+                        // rows: lines (batch, i0[, i1]) at the caller's strides; dense on the output side
+                        a.C = rank == 3 ? dm[1] : 1;
+                        a.in_cs = rank == 3 ? in_st[1] : 1;
+                        a.out_cs = rank == 3 ? dm[2] : 1;
+                        a.C1 = dm[0];
+                        a.in_os1 = in_st[0];
+                        a.out_os1 = rank == 3 ? dm[1] * dm[2] : dm[1];
+                        a.in_os = bst;
+                        a.out_os = per_batch;
+                    }
+                } else if (stage_mid && L.in_sel == SEL_OUT) {
                     L.in_sel = SEL_STAGE_OUT;
                 }
                 if (last) {
-                    if (mixed) L.a.flags |= KF_NARROW_OUT, L.out_off /= 2;
-                    if (zp_out) L.a.flags |= KF_ZERO_OUT;
-                } else {
+                    const long long b0 = (long long)(L.out_off / ((size_t)per_batch * cs));
+                    const bool fmt = fmt_out && fused_layout;
+                    const long long bst = fmt ? out_bst : per_batch;
+                    L.out_off = (size_t)(b0 * bst) * (mixed ? scs : cs);
+                    if (fmt && rank == 1) {
+                        a.out_os = bst;
+                    } else if (fmt) {
+                        // axis 0 columns: lines (batch, i1[, i2]) at the caller's strides; dense input
+                        a.C = rank == 3 ? dm[2] : dm[1];
+                        a.in_cs = a.out_cs = 1;
+                        a.C1 = rank == 3 ? dm[1] : 1;
+                        a.in_os1 = rank == 3 ? dm[2] : 0;
+                        a.out_os1 = rank == 3 ? out_st[1] : 0;
+                        a.out_es = out_st[0];
+                        a.in_os = per_batch;
+                        a.out_os = bst;
+                    }
+                } else if (stage_mid && L.out_sel == SEL_OUT) {
                     L.out_sel = SEL_STAGE_OUT;
                     edge_stage = true;
                 }
             }
         }
-        const bool need_in = !fused_edges && (mixed || (fmt_in && !fused_in) || zp_in);
-        const bool need_out = !fused_edges && (mixed || (fmt_out && !fused_out) || zp_out);
+        const bool fused_all = fused_edges || fused_layout;
+        const bool need_in = !fused_all && (mixed || (fmt_in && !fused_in) || zp_in);
+        const bool need_out = !fused_all && (mixed || (fmt_out && !fused_out) || zp_out);
         const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
         const size_t cin = p->in_bytes, cout = p->out_bytes;  // dense compute-type bytes
         const int in_scal = real_in ? 1 : 2, out_scal = real_out ? 1 : 2;
@@ -2560,6 +2642,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         c.js << "\"boundary\":{\"input\":" << (need_in ? "true" : "false") << ",\"output\":"
              << (need_out ? "true" : "false") << ",\"fused_batch_stride\":[" << (fused_in ? "true" : "false")
              << "," << (fused_out ? "true" : "false") << "],\"fused_edges\":" << (fused_edges ? "true" : "false")
+             << ",\"fused_layout\":" << (fused_layout ? "true" : "false")
              << ",\"zero_padding\":\""
              << (!any_zero ? "none" : d.zero_frequency ? "frequency" : "spatial") << "\",\"grouped_batch\":[";
         for (size_t i = 0; i < rank; ++i) c.js << (i ? "," : "") << d.grouped_batch[i];
