@@ -812,15 +812,18 @@ unsigned blocks_for(long long lines, int G) { return (unsigned)((lines + G - 1) 
 // geometry of its length (rows: about 256 threads per block, columns: 8 / 16
 // lines per block as for strided axes). Contiguous lines keep HBM-direct ends
 // under the direct kernel's conditions; the others run staged.
+Geometry edge_geometry(const Ctx& c, const KArgs& a) {
+    const Geometry g0 = geometry((size_t)a.N, c.prec, 1, c.lds_max, c.lds_max);
+    if (!g0.ok) return g0;
+    const bool rows = (a.flags & KF_IN_ROWMAJOR) != 0;
+    return geometry((size_t)a.N, c.prec, rows ? std::max(1, 256 / g0.TT) : (c.prec ? 8 : 16), c.lds_max,
+                    c.lds_budget);
+}
+
 int to_edge_kernel(Ctx& c, Launch& L) {
     KArgs& a = L.a;
     if (L.fixed) {
-        const bool rows = (a.flags & KF_IN_ROWMAJOR) != 0;
-        const Geometry g0 = geometry((size_t)a.N, c.prec, 1, c.lds_max, c.lds_max);
-        if (!g0.ok)
-            return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
-        const Geometry g = geometry((size_t)a.N, c.prec, rows ? std::max(1, 256 / g0.TT) : (c.prec ? 8 : 16),
-                                    c.lds_max, c.lds_budget);
+        const Geometry g = edge_geometry(c, a);
         if (!g.ok)
             return fail(VKFX_ERR_UNSUPPORTED_KERNEL_PATH, "no runtime geometry for length " + std::to_string(a.N));
         a.TT = g.TT;
@@ -2482,6 +2485,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
                 const bool plain = L.kind == KK_PLAIN && !L.a.rtab;
                 if ((first || last) && !plain) return false;
+                // a fixed shape that would carry edges needs a runtime geometry of its length
+                if ((first || last) && (mixed || any_zero) && L.fixed && !edge_geometry(c, L.a).ok) return false;
                 if ((L.in_sel == SEL_IN) != first || (first && L.out_sel != SEL_OUT && !last)) return false;
                 if (last && L.out_sel != SEL_OUT) return false;
                 if ((L.in_sel != SEL_IN && L.in_sel != SEL_OUT && L.in_sel != SEL_WORK) ||
