@@ -254,3 +254,71 @@ def test_nd_slab_chunks(idx_ctx):
     for ax, n in enumerate(dims):
         v = np.take(v, im.stockham_perm(n, rad[n]), axis=ax + 1)
     assert np.array_equal(out, v.reshape(-1))
+
+
+def _padded_layout(c, dims):
+    """Formatted strides on both sides: every axis but the fastest padded by a
+    few elements, and the batch stride padded too."""
+    for side in ("input", "output"):
+        st = 1
+        for ax in range(len(dims) - 1, -1, -1):
+            if ax < len(dims) - 1:
+                st = st + 3 + ax
+                c = getattr(c, f"with_{side}_buffer_axis_stride")(ax, st)
+            st *= dims[ax]
+        c = getattr(c, f"with_{side}_buffer_batch_stride")(st + 5)
+    return c
+
+
+@pytest.mark.parametrize("dims,batch", [([32, 48], 2), ([8, 12, 40], 2), ([4, 300], 3)])
+def test_formatted_layout_in_passes(idx_ctx, dims, batch):
+    """Formatted input and output read and written by the first and last
+    passes (three line levels): every logical element lands where the
+    per-axis Stockham maps send it, through the caller's strides."""
+    cfg = _padded_layout(vk.FftConfig.new(dims).with_batch_count(batch).with_precision(F64), dims)
+    ir = vk.TransformIr.build(cfg, FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        assert desc["boundary"]["fused_layout"] and not desc["boundary"]["input"]
+        x = tagged(int(np.prod(dims)) * batch, F64)
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    rad = {}
+    for p in desc["passes"]:
+        rad.setdefault(p["fft_len"], p["radices"])
+    v = x.reshape((batch,) + tuple(dims))
+    for ax, n in enumerate(dims):
+        v = np.take(v, im.stockham_perm(n, rad[n]), axis=ax + 1)
+    assert np.array_equal(out, v.reshape(-1))
+
+
+@pytest.mark.parametrize("n,left,right,domain", [(1024, 100, 300, "spatial"), (1000, 0, 7, "frequency"),
+                                                 (720, 700, 720, "spatial")])
+def test_storage_and_zero_interval_in_pass(idx_ctx, n, left, right, domain):
+    """1-D F64ComputeF32Storage with a zero interval, converted and masked
+    inside the one pass (HBM-direct ends): f32 tags survive the f64 pass
+    exactly; the input interval reads as zero (spatial, forward) or the
+    output interval is written as zero (frequency, forward)."""
+    batch = 3
+    zd = vk.ZeroPaddingDomain.Spatial if domain == "spatial" else vk.ZeroPaddingDomain.Frequency
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(vk.Precision.F64ComputeF32Storage) \
+        .with_zero_padding(0, left, right).with_zero_padding_domain(zd)
+    ir = vk.TransformIr.build(cfg, FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        assert desc["boundary"]["fused_edges"] and [p["kernel"] for p in desc["passes"]] == ["stockham"]
+        x = tagged(n * batch, F32)
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    perm = im.stockham_perm(n, desc["passes"][0]["radices"])
+    v = x.reshape(batch, n).copy()
+    if domain == "spatial":
+        v[:, left:right] = 0
+    v = v[:, perm]
+    if domain == "frequency":
+        v[:, left:right] = 0
+    assert np.array_equal(out, v.reshape(-1))
