@@ -5,9 +5,13 @@ spectra / scale) against the CPU index maps of oracle/index_maps.py.
 Inputs are integer-tagged (exact in f32 and f64), so every output element
 must equal the input element the maps name, bit for bit: this checks the
 direct HBM stages, LDS slot arithmetic, line mappings (rows, columns, split
-axes, chunks, stream lanes), four-step transposes and Bluestein padding /
-truncation of every C2C kernel family. Real-to-complex and Rader kernels do
-arithmetic besides moving data and are checked numerically elsewhere."""
+axes, chunks, stream lanes, formatted layouts), four-step transposes and
+Bluestein padding / truncation of every C2C kernel family. The even R2C / C2R
+kernels (one upload and four-step) combine each element with its mirror:
+with random integer tags their identity-arithmetic results (sums and
+differences of the paired elements) are exact, so the pairing and placement
+are checked bit for bit too. Rader kernels are checked numerically
+elsewhere."""
 import os
 
 import numpy as np
@@ -322,3 +326,138 @@ def test_storage_and_zero_interval_in_pass(idx_ctx, n, left, right, domain):
     if domain == "frequency":
         v[:, left:right] = 0
     assert np.array_equal(out, v.reshape(-1))
+
+
+def _muli(v, s):
+    """(s i) * v, s = +-1 (fft_device.hpp muli)."""
+    return (-v.imag + 1j * v.real) if s > 0 else (v.imag - 1j * v.real)
+
+
+@pytest.mark.parametrize("n", [64, 210, 1000, 1024, 4096, 6000, 8192])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_r2c_half_addressing(idx_ctx, n, prec):
+    """Even one-upload R2C (real pairs -> half-length FFT -> postprocess):
+    with identity butterflies and twiddles the postprocess computes
+    (A + conj Z[M-k]) - i (A - conj Z[M-k]) from A = Z[k] (k = 0 and M both
+    take Z[0]). Random integer tags make a wrong pairing or placement show:
+    the result must match bit for bit."""
+    batch, M = 3, n // 2
+    rng = np.random.default_rng(n)
+    x = rng.integers(0, 1 << 18, n * batch).astype(np.float32 if prec == F32 else np.float64)
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.RealToComplex)
+    ir = vk.TransformIr.build(cfg, FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    assert len(desc["passes"]) == 1, desc["passes"]
+    z = (x[0::2] + 1j * x[1::2]).reshape(batch, M)
+    z = z[:, im.stockham_perm(M, desc["passes"][0]["radices"])]
+    k = np.arange(M + 1)
+    a = z[:, np.where(k == M, 0, k)]
+    b = np.conj(z[:, np.where(k == 0, 0, M - k)])
+    expect = (a + b) + _muli(a - b, -1)
+    assert np.array_equal(out.reshape(batch, M + 1), expect.astype(out.dtype))
+
+
+@pytest.mark.parametrize("n", [64, 210, 1000, 1024, 4096, 6000, 8192])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_c2r_half_addressing(idx_ctx, n, prec):
+    """Even one-upload C2R (preprocess -> half-length inverse FFT -> real
+    pairs): with identity arithmetic Z[k] = (X[k] + conj X[M-k]) +
+    i (X[k] - conj X[M-k]) for k < M, then the Stockham map, then the
+    complex results as real pairs; random integer tags, bit for bit."""
+    batch, M = 3, n // 2
+    rng = np.random.default_rng(n + 1)
+    re = rng.integers(0, 1 << 18, (M + 1) * batch)
+    im_ = rng.integers(0, 1 << 18, (M + 1) * batch)
+    X = (re + 1j * im_).astype(np.complex64 if prec == F32 else np.complex128)
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.ComplexToReal)
+    ir = vk.TransformIr.build(cfg, INV)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, X)
+    finally:
+        plan.close()
+    assert len(desc["passes"]) == 1, desc["passes"]
+    Xb = X.reshape(batch, M + 1).astype(np.complex128)
+    k = np.arange(M)
+    xk = Xb[:, k]
+    xm = np.conj(Xb[:, M - k])
+    z = (xk + xm) + _muli(xk - xm, 1)
+    z = z[:, im.stockham_perm(M, desc["passes"][0]["radices"])]
+    expect = np.empty((batch, n))
+    expect[:, 0::2] = z.real
+    expect[:, 1::2] = z.imag
+    assert np.array_equal(out.reshape(batch, n), expect.astype(out.dtype))
+
+
+def _real_four_step(desc, first, second):
+    names = [p["kernel"] for p in desc["passes"]]
+    assert names[:2] == [first, second], names
+    a, b = desc["passes"][0], desc["passes"][1]
+    return im.four_step_perm(a["fft_len"], a["radices"], b["fft_len"], b["radices"])
+
+
+@pytest.mark.parametrize("n,batch", [(1 << 17, 3), (1 << 20, 2), (3 << 16, 2)])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_r2c_four_step_addressing(idx_ctx, n, batch, prec):
+    """Two-upload R2C (column pass, then the row pass with the postprocess
+    of each row beside its mirror row): X[k] from Z[k] and Z[(M-k) mod M] of
+    the four-step map, X[M] = Re Z[0] - Im Z[0]; integer tags, bit for bit."""
+    M = n // 2
+    rng = np.random.default_rng(n + batch)
+    x = rng.integers(0, 1 << 18, n * batch).astype(np.float32 if prec == F32 else np.float64)
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.RealToComplex)
+    ir = vk.TransformIr.build(cfg, FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    src = _real_four_step(desc, "r2c_columns", "r2c_rows_post")
+    z = (x[0::2] + 1j * x[1::2]).reshape(batch, M)[:, src]
+    k = np.arange(M)
+    a = z
+    b = np.conj(z[:, (M - k) % M])
+    expect = np.empty((batch, M + 1), dtype=np.complex128)
+    expect[:, :M] = (a + b) + _muli(a - b, -1)
+    expect[:, M] = z[:, 0].real - z[:, 0].imag
+    assert np.array_equal(out.reshape(batch, M + 1), expect.astype(out.dtype))
+
+
+@pytest.mark.parametrize("n,batch", [(1 << 17, 3), (1 << 20, 2), (3 << 16, 2)])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_c2r_four_step_addressing(idx_ctx, n, batch, prec):
+    """Two-upload C2R (column pass forming the preprocess from X[k] and
+    X[M-k], then the row pass): the four-step map of Z, as real pairs;
+    integer tags, bit for bit."""
+    M = n // 2
+    rng = np.random.default_rng(n + batch + 7)
+    X = (rng.integers(0, 1 << 18, (M + 1) * batch) + 1j * rng.integers(0, 1 << 18, (M + 1) * batch))
+    X = X.astype(np.complex64 if prec == F32 else np.complex128)
+    cfg = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_transform(vk.TransformKind.ComplexToReal)
+    ir = vk.TransformIr.build(cfg, INV)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, X)
+    finally:
+        plan.close()
+    src = _real_four_step(desc, "c2r_columns_pre", "c2r_rows")
+    Xb = X.reshape(batch, M + 1).astype(np.complex128)
+    k = np.arange(M)
+    xk, xm = Xb[:, k], np.conj(Xb[:, M - k])
+    z = ((xk + xm) + _muli(xk - xm, 1))[:, src]
+    expect = np.empty((batch, n))
+    expect[:, 0::2] = z.real
+    expect[:, 1::2] = z.imag
+    assert np.array_equal(out.reshape(batch, n), expect.astype(out.dtype))

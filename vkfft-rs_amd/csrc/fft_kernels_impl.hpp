@@ -392,7 +392,7 @@ struct IoR2CHalf : IoPlain {
             cpx<T> A = Z[lpad(k0, D::PS(a))];
             cpx<T> B = conj(Z[lpad(km, D::PS(a))]);
             cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
-            cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
+            cpx<T> X = (A + B) + muli<-1>(cmul(A - B, w));
             stg_out<D::NTO>(a, out + li[g].ob + k * a.out_es, scale(X, (T)0.5));
         });
     }
@@ -521,12 +521,13 @@ struct IoFsAC2R : IoFsA {
         cpx<T> Xm = conj(in[L.o * a.in_os + (a.M - k)]);
         return (X + Xm) + muli<1>(cmulc(X - Xm, w));
     }
-    // Both members of a pair from A = X[k], B = X[M-k]; w_(M-k) = -conj(w_k).
+    // Both members of a pair from A = X[k], B = X[M-k]; w_(M-k) = -conj(w_k)
+    // (both in the form of load_tw, data operand first).
     template <typename T>
     static __device__ __forceinline__ void pair(const KArgs& a, long long k, cpx<T>& A, cpx<T>& B) {
         const cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
         const cpx<T> zk = (A + conj(B)) + muli<1>(cmulc(A - conj(B), w));
-        const cpx<T> zm = (B + conj(A)) - muli<1>(cmul(B - conj(A), w));
+        const cpx<T> zm = (B + conj(A)) + muli<1>(cmulc(B - conj(A), mk(-w.re, w.im)));
         A = zk;
         B = zm;
     }
@@ -672,7 +673,7 @@ struct IoFsBR2C : IoPlain {
             const long long k = k1 + a.N1 * k2;
             cpx<T> A = row[lpad(k2, D::PS(a))];
             cpx<T> B = conj(prow[lpad(k2m, D::PS(a))]);
-            cpx<T> X = (A + B) + muli<-1>(cmul(w, A - B));
+            cpx<T> X = (A + B) + muli<-1>(cmul(A - B, w));
             stg_out<D::NTO>(a, out + li[g].ob + k, scale(X, (T)0.5));
             if (k == 0) out[li[g].ob + a.M] = mk(A.re - A.im, (T)0);
             w = cmul(w, wstep);
