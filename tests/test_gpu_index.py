@@ -10,8 +10,10 @@ Bluestein padding / truncation of every C2C kernel family. The even R2C / C2R
 kernels (one upload and four-step) combine each element with its mirror:
 with random integer tags their identity-arithmetic results (sums and
 differences of the paired elements) are exact, so the pairing and placement
-are checked bit for bit too. Rader kernels are checked numerically
-elsewhere."""
+are checked bit for bit too, and likewise the FFT-mode Rader kernel's
+gather, slot-0 sum and scatter. The direct-multiplication Rader kernel sums
+every input into every output under identity arithmetic and is checked
+numerically elsewhere."""
 import os
 
 import numpy as np
@@ -461,3 +463,40 @@ def test_c2r_four_step_addressing(idx_ctx, n, batch, prec):
     expect[:, 0::2] = z.real
     expect[:, 1::2] = z.imag
     assert np.array_equal(out.reshape(batch, n), expect.astype(out.dtype))
+
+
+@pytest.mark.parametrize("p", [97, 193, 257, 769, 3457])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_rader_fft_addressing(idx_ctx, p, prec):
+    """FFT-mode Rader of a prime p (rader_ir.rs, lut.rs:374-435): gather
+    a[s] = x[g^-s], length p-1 FFT, kernel multiply, inverse FFT, scatter to
+    g^m plus x[0], and X[0] = x[0] + (the FFT's slot 0). With identity
+    arithmetic both FFTs are the Stockham map of the plan's radices, so
+    X[0] = x0 + a[P[0]] and X[g^m] = x0 + a[P[P[m]]]; random integer tags,
+    bit for bit."""
+    from oracle import oracle as orc
+    batch, L = 3, p - 1
+    rng = np.random.default_rng(p)
+    x = (rng.integers(0, 1 << 18, p * batch) + 1j * rng.integers(0, 1 << 18, p * batch))
+    x = x.astype(np.complex64 if prec == F32 else np.complex128)
+    cfg = vk.FftConfig.new([p]).with_batch_count(batch).with_precision(prec)
+    ir = vk.TransformIr.build(cfg, FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    assert [q["kernel"] for q in desc["passes"]] == ["rader_fft"], desc["passes"]
+    g = orc.primitive_root(p)
+    pw = np.array([pow(g, e, p) for e in range(L)])
+    pin = pw[(L - np.arange(L)) % L]
+    perm = im.stockham_perm(L, desc["passes"][0]["radices"])
+    xb = x.reshape(batch, p).astype(np.complex128)
+    a = xb[:, pin]
+    f = a[:, perm]
+    h = f[:, perm]
+    expect = np.empty((batch, p), dtype=np.complex128)
+    expect[:, 0] = xb[:, 0] + f[:, 0]
+    expect[:, pw] = xb[:, :1] + h
+    assert np.array_equal(out.reshape(batch, p), expect.astype(out.dtype))
