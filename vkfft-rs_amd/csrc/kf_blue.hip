@@ -17,8 +17,9 @@ static const FixedKernel kTable[] = {
     // each: 1.3% over 27 threads, the second variant); the 324-point row pass
     // with 36 threads per row (radix 4, 9, 9: one radix-9 butterfly per thread,
     // three radix-4 rounds) and 8 rows per block, 6-7% over 27 threads per row
-    // (the second variant) on two boxes; 16 rows per block or an LDS pad of one
-    // per 16 ran slower
+    // (the second variant) on two boxes; 16 rows per block, an LDS pad of one
+    // per 16, radix orders 9-9-4 / 9-4-9 (fewer modelled LDS bank conflicts)
+    // and 81 threads per row ran slower (5.50-6.86 ms against 5.41-5.47)
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 45, 16, 30, 405, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 45, 16, 30, 405, true, false, true, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
