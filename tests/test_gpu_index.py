@@ -117,6 +117,21 @@ SINGLE = [2, 3, 5, 7, 8, 11, 13, 16, 18, 25, 27, 32, 36, 49, 60, 64, 96, 100, 12
           12, 20, 24, 40, 48, 80, 160, 192, 320, 384, 640, 768, 1280, 2560, 3072, 5120, 6144, 10240, 12288]
 
 
+ROUND = [200, 240, 300, 400, 480, 500, 600, 720, 750, 800, 900, 960, 1200, 1500, 1600, 1800, 1920, 2000, 2400,
+         2500, 3000, 3200, 3600, 4000, 4800, 5000, 6000, 6400, 7200, 8000, 9000, 9600, 12000, 16000]
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_round_length_rows(idx_ctx, prec):
+    """The generated round-length row shapes (kf_round_*), both directions."""
+    for n in ROUND:
+        if prec == F64 and n > 8192:
+            continue
+        d = check_1d(idx_ctx, n, 3, prec)
+        assert d["passes"][0]["fixed_shape"], n
+        check_1d(idx_ctx, n, 2, prec, INV)
+
+
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_single_upload_lengths(idx_ctx, prec):
     for n in SINGLE:

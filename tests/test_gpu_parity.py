@@ -337,6 +337,26 @@ HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072,
               F64: [64, 128, 160, 192, 256, 320, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096]}
 
 
+ROUND = [200, 240, 300, 400, 480, 500, 600, 720, 750, 800, 900, 960, 1200, 1500, 1600, 1800, 1920, 2000, 2400,
+         2500, 3000, 3200, 3600, 4000, 4800, 5000, 6000, 6400, 7200, 8000, 9000, 9600, 12000, 16000]
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_round_length_fixed_rows(hip_ctx, prec):
+    """The round lengths with factors 2, 3 and 5 (kf_round_*) run on their
+    fixed row shapes, forward and inverse, against the oracle."""
+    for n in ROUND:
+        if prec == F64 and n > 8192:
+            continue  # longer f64 lines are two uploads
+        batch = 3
+        x = rand(n * batch, n, prec)
+        y, ir = c2c(hip_ctx, [n], batch, x, prec)
+        assert hip_ctx.plan(ir).describe()["passes"][0]["fixed_shape"], n
+        assert o.rel_l2(y, oracle_c2c(x, n)) <= TOL[prec], (n, prec)
+        z, _ = c2c(hip_ctx, [n], batch, y, prec, INV, normalize=True)
+        assert o.rel_l2(z, x) <= 4 * TOL[prec], (n, prec)
+
+
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_r2c_c2r_fixed_half_lengths(hip_ctx, prec):
     """Even lengths whose half-size FFT has a fixed shape, at batch 37 (several

@@ -3,8 +3,9 @@ kf_real_rows_*.hip): the shape lists, the LDS bank-conflict model that chose
 each shape's LDS line stride LS and pad shift PS, and the emitter of the
 registration files.
 
-    python3 gen_shape_tables.py emit      # rewrite the six kf_*.hip tables
+    python3 gen_shape_tables.py emit      # rewrite the eight kf_*.hip tables
     python3 gen_shape_tables.py check     # re-run the model search per shape
+    python3 gen_shape_tables.py round     # re-derive the round-length rows by rule
 
 Bank model (fitted to the SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE ratios the
 fixed kernels measured on gfx950): 32 banks of 4 bytes; an 8-byte access of a
@@ -349,9 +350,79 @@ TABLES = {
     ],
 }
 
+# Round lengths with factors 2, 3 and 5 outside the families above (common
+# decimal-like sizes), as one-upload rows built by rule: the radix plan with
+# the fewest stages from {16, 12, 10, 9, 8, 6, 5, 4, 3, 2} (then the largest
+# smallest radix, then the largest first radix), largest radix first;
+# threads per line = N / the largest radix; about 256 threads per block; LDS
+# stride and pad from the bank model's search.
+ROUND = [200, 240, 300, 400, 480, 500, 600, 720, 750, 800, 900, 960, 1200, 1500, 1600, 1800, 1920, 2000, 2400,
+         2500, 3000, 3200, 3600, 4000, 4800, 5000, 6000, 6400, 7200, 8000, 9000, 9600, 12000, 15000, 16000]
+RADICES = (16, 12, 10, 9, 8, 6, 5, 4, 3, 2)
+
+
+def radix_plan(n):
+    """Fewest stages, then the largest smallest radix, then the largest first radix."""
+    best = None
+
+    def rec(rest, start, acc):
+        nonlocal best
+        if rest == 1:
+            plan = sorted(acc, reverse=True)
+            key = (len(plan), -min(plan), -plan[0])
+            if best is None or key < best[0]:
+                best = (key, plan)
+            return
+        if len(acc) >= 5:
+            return
+        for i in range(start, len(RADICES)):
+            r = RADICES[i]
+            if rest % r == 0:
+                rec(rest // r, i, acc + [r])
+
+    rec(n, 0, [])
+    return best[1] if best else None
+
+
+def round_rows(prec):
+    eb = 16 if prec else 8
+    rows = []
+    for n in ROUND:
+        if prec and n > 8192:
+            continue  # longer f64 lines are two uploads (the runtime line with its pad exceeds the LDS)
+        rad = radix_plan(n)
+        tt = n // max(rad)
+        if tt > 1024:
+            continue
+        g = max(1, min(256 // tt, 64))
+        while g > 1 and g * (n + (n >> 2)) * eb > 80 * 1024:
+            g -= 1
+        best = search(n, tt, g, False, rad, False, eb)
+        if best is None:
+            continue
+        _, _, ps, ls = best
+        rows.append(('PLAIN', 'Plain', n, tt, g, False, rad, ps, ls))
+    return rows
+
+
+HEADS_ROUND = ("// Fixed shapes of round lengths with factors 2, 3 and 5 outside the\n"
+               "// power-of-two, 3*2^k and 5*2^k families, {p}: one-upload rows (1-D batches\n"
+               "// and the contiguous axis of N-D transforms) in both directions and both\n"
+               "// nontemporal roles. Radix plans with the fewest LDS-exchanged stages from\n"
+               "// radices 2-16 (composite 6, 9, 10, 12); threads per line = N / the largest\n"
+               "// radix; about 256 threads per block; LDS strides minimise bank conflicts\n"
+               "// under the 32-bank model of 8-byte accesses.\n")
+
 HEADS = {'kf_pow2_f32': "// Fixed shapes of the power-of-two lengths outside the benchmark\n// configurations, f32: rows of one upload (1-D batches and the contiguous\n// axis of N-D transforms), strided columns up to the length that stays one\n// upload per axis, and the first pass of split strided axes. Each shape is\n// registered for both directions and for the two nontemporal roles its pass\n// can take (rows: the caller's input, with or without the caller's output;\n// columns: cached input, with or without the caller's output). LDS strides\n// minimise bank conflicts under the 32-bank model of 8-byte accesses (16 lanes\n// served per cycle). Short rows, whose first or last Stockham stage would touch\n// HBM in segments narrower than 128 bytes, stage both ends through LDS\n// (IoPlainStaged).\n", 'kf_pow2_f64': "// Fixed shapes of the power-of-two lengths outside the benchmark\n// configurations, f64: rows of one upload (1-D batches and the contiguous\n// axis of N-D transforms), strided columns up to the length that stays one\n// upload per axis, and the first pass of split strided axes. Each shape is\n// registered for both directions and for the two nontemporal roles its pass\n// can take (rows: the caller's input, with or without the caller's output;\n// columns: cached input, with or without the caller's output). LDS strides\n// minimise bank conflicts under the 32-bank model of 8-byte accesses (16 lanes\n// served per cycle). Short rows, whose first or last Stockham stage would touch\n// HBM in segments narrower than 128 bytes, stage both ends through LDS\n// (IoPlainStaged).\n", 'kf_fam_f32': '// Fixed shapes of common lengths with factors 3 and 5, f32: 3*2^k, 5*2^k,\n// 10^k and 360, as rows of one upload (1-D batches and the contiguous axis of\n// N-D transforms) and as strided columns up to 640, each in both directions\n// and both nontemporal roles. Radix plans keep at most three or four\n// LDS-exchanged stages (composite radices 6, 10 and 12 where they save one);\n// threads per line = N / the largest radix; LDS strides minimise bank\n// conflicts under the 32-bank model of 8-byte accesses. Short rows stage both\n// ends through LDS (IoPlainStaged).\n', 'kf_fam_f64': '// Fixed shapes of common lengths with factors 3 and 5, f64: 3*2^k, 5*2^k,\n// 10^k and 360, as rows of one upload (1-D batches and the contiguous axis of\n// N-D transforms) and as strided columns up to 640, each in both directions\n// and both nontemporal roles. Radix plans keep at most three or four\n// LDS-exchanged stages (composite radices 6, 10 and 12 where they save one);\n// threads per line = N / the largest radix; LDS strides minimise bank\n// conflicts under the 32-bank model of 8-byte accesses. Short rows stage both\n// ends through LDS (IoPlainStaged).\n', 'kf_real_rows_f32': "// Fixed shapes of the one-upload even-length real transforms, f32: the\n// half-size packed FFT of R2C (postprocess fused into the staged store) and of\n// C2R (preprocess fused into the direct loads) for half lengths M that have a\n// fixed C2C row shape (powers of two and the 3*2^k / 5*2^k families), with the\n// same radices, threads, lines per block and LDS strides as those rows. R2C is\n// registered for the caller's input with or without the caller's output, C2R\n// for the caller's output with or without the caller's input.\n", 'kf_real_rows_f64': "// Fixed shapes of the one-upload even-length real transforms, f64: the\n// half-size packed FFT of R2C (postprocess fused into the staged store) and of\n// C2R (preprocess fused into the direct loads) for half lengths M that have a\n// fixed C2C row shape (powers of two and the 3*2^k / 5*2^k families), with the\n// same radices, threads, lines per block and LDS strides as those rows. R2C is\n// registered for the caller's input with or without the caller's output, C2R\n// for the caller's output with or without the caller's input.\n"}
 
-FUNCS = {'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
+# round_rows(0) / round_rows(1) (the model search takes minutes in pure
+# Python: `python3 gen_shape_tables.py round` re-derives these lists)
+TABLES['kf_round_f32'] = [('PLAIN', 'Plain', 200, 25, 10, False, [8, 5, 5], 5, 217), ('PLAIN', 'Plain', 240, 30, 8, False, [8, 6, 5], 4, 255), ('PLAIN', 'Plain', 300, 25, 10, False, [12, 5, 5], 6, 313), ('PLAIN', 'Plain', 400, 25, 10, False, [16, 5, 5], 4, 425), ('PLAIN', 'Plain', 480, 48, 5, False, [10, 8, 6], 30, 480), ('PLAIN', 'Plain', 500, 50, 5, False, [10, 10, 5], 6, 515), ('PLAIN', 'Plain', 600, 60, 4, False, [10, 10, 6], 30, 604), ('PLAIN', 'Plain', 720, 72, 3, False, [10, 9, 8], 30, 728), ('PLAIN', 'Plain', 750, 125, 2, False, [6, 5, 5, 5], 30, 765), ('PLAIN', 'Plain', 800, 80, 3, False, [10, 10, 8], 6, 812), ('PLAIN', 'Plain', 900, 90, 2, False, [10, 10, 9], 30, 906), ('PLAIN', 'Plain', 960, 80, 3, False, [12, 10, 8], 5, 989), ('PLAIN', 'Plain', 1200, 100, 2, False, [12, 10, 10], 5, 1239), ('PLAIN', 'Plain', 1500, 125, 2, False, [12, 5, 5, 5], 6, 1535), ('PLAIN', 'Plain', 1600, 100, 2, False, [16, 10, 10], 4, 1706), ('PLAIN', 'Plain', 1800, 150, 1, False, [12, 6, 5, 5], 6, 1828), ('PLAIN', 'Plain', 1920, 120, 2, False, [16, 12, 10], 4, 2047), ('PLAIN', 'Plain', 2000, 125, 2, False, [16, 5, 5, 5], 5, 2065), ('PLAIN', 'Plain', 2400, 150, 1, False, [16, 6, 5, 5], 5, 2474), ('PLAIN', 'Plain', 2500, 250, 1, False, [10, 10, 5, 5], 30, 2500), ('PLAIN', 'Plain', 3000, 250, 1, False, [12, 10, 5, 5], 6, 3046), ('PLAIN', 'Plain', 3200, 200, 1, False, [16, 8, 5, 5], 4, 3399), ('PLAIN', 'Plain', 3600, 360, 1, False, [10, 10, 6, 6], 30, 3600), ('PLAIN', 'Plain', 4000, 250, 1, False, [16, 10, 5, 5], 5, 4124), ('PLAIN', 'Plain', 4800, 480, 1, False, [10, 10, 8, 6], 6, 4874), ('PLAIN', 'Plain', 5000, 500, 1, False, [10, 10, 10, 5], 30, 5000), ('PLAIN', 'Plain', 6000, 600, 1, False, [10, 10, 10, 6], 30, 6000), ('PLAIN', 'Plain', 6400, 640, 1, False, [10, 10, 8, 8], 6, 6499), ('PLAIN', 'Plain', 7200, 720, 1, False, [10, 10, 9, 8], 30, 7200), ('PLAIN', 'Plain', 8000, 800, 1, False, [10, 10, 10, 8], 6, 8124), ('PLAIN', 'Plain', 9000, 900, 1, False, [10, 10, 10, 9], 30, 9000), ('PLAIN', 'Plain', 9600, 800, 1, False, [12, 10, 10, 8], 5, 9899), ('PLAIN', 'Plain', 12000, 1000, 1, False, [12, 10, 10, 10], 5, 12374), ('PLAIN', 'Plain', 16000, 1000, 1, False, [16, 10, 10, 10], 4, 16999)]
+TABLES['kf_round_f64'] = [('PLAIN', 'Plain', 200, 25, 10, False, [8, 5, 5], 3, 225), ('PLAIN', 'Plain', 240, 30, 8, False, [8, 6, 5], 3, 273), ('PLAIN', 'Plain', 300, 25, 10, False, [12, 5, 5], 5, 314), ('PLAIN', 'Plain', 400, 25, 10, False, [16, 5, 5], 4, 426), ('PLAIN', 'Plain', 480, 48, 5, False, [10, 8, 6], 5, 494), ('PLAIN', 'Plain', 500, 50, 5, False, [10, 10, 5], 30, 506), ('PLAIN', 'Plain', 600, 60, 4, False, [10, 10, 6], 30, 604), ('PLAIN', 'Plain', 720, 72, 3, False, [10, 9, 8], 30, 720), ('PLAIN', 'Plain', 750, 125, 2, False, [6, 5, 5, 5], 30, 757), ('PLAIN', 'Plain', 800, 80, 3, False, [10, 10, 8], 30, 800), ('PLAIN', 'Plain', 900, 90, 2, False, [10, 10, 9], 30, 906), ('PLAIN', 'Plain', 960, 80, 3, False, [12, 10, 8], 5, 989), ('PLAIN', 'Plain', 1200, 100, 2, False, [12, 10, 10], 5, 1242), ('PLAIN', 'Plain', 1500, 125, 2, False, [12, 5, 5, 5], 5, 1552), ('PLAIN', 'Plain', 1600, 100, 2, False, [16, 10, 10], 4, 1706), ('PLAIN', 'Plain', 1800, 150, 1, False, [12, 6, 5, 5], 5, 1856), ('PLAIN', 'Plain', 1920, 120, 2, False, [16, 12, 10], 4, 2039), ('PLAIN', 'Plain', 2000, 125, 2, False, [16, 5, 5, 5], 4, 2125), ('PLAIN', 'Plain', 2400, 150, 1, False, [16, 6, 5, 5], 4, 2549), ('PLAIN', 'Plain', 2500, 250, 1, False, [10, 10, 5, 5], 30, 2500), ('PLAIN', 'Plain', 3000, 250, 1, False, [12, 10, 5, 5], 5, 3093), ('PLAIN', 'Plain', 3200, 200, 1, False, [16, 8, 5, 5], 4, 3399), ('PLAIN', 'Plain', 3600, 360, 1, False, [10, 10, 6, 6], 30, 3600), ('PLAIN', 'Plain', 4000, 250, 1, False, [16, 10, 5, 5], 4, 4249), ('PLAIN', 'Plain', 4800, 480, 1, False, [10, 10, 8, 6], 30, 4800), ('PLAIN', 'Plain', 5000, 500, 1, False, [10, 10, 10, 5], 30, 5000), ('PLAIN', 'Plain', 6000, 600, 1, False, [10, 10, 10, 6], 30, 6000), ('PLAIN', 'Plain', 6400, 640, 1, False, [10, 10, 8, 8], 30, 6400), ('PLAIN', 'Plain', 7200, 720, 1, False, [10, 10, 9, 8], 30, 7200), ('PLAIN', 'Plain', 8000, 800, 1, False, [10, 10, 10, 8], 30, 8000)]
+HEADS['kf_round_f32'] = HEADS_ROUND.format(p='f32')
+HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
+
+FUNCS = {'kf_round_f32': 'fixed_table_round_f32', 'kf_round_f64': 'fixed_table_round_f64', 'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
 
 
 def roles(kind, col):
@@ -419,5 +490,9 @@ if __name__ == "__main__":
             emit(n)
     elif len(sys.argv) > 1 and sys.argv[1] == "check":
         check()
+    elif len(sys.argv) > 1 and sys.argv[1] == "round":
+        for prec, name in ((0, "kf_round_f32"), (1, "kf_round_f64")):
+            rows = round_rows(prec)
+            print(name, "matches" if rows == TABLES[name] else "DIFFERS", rows, flush=True)
     else:
         print(__doc__)
