@@ -213,7 +213,10 @@ ND = [([64, 48], 2, F32), ([256, 256], 2, F32), ([8, 4096], 2, F32), ([4096, 8],
       ([1024, 4], 1, F64), ([2048, 3], 1, F32), ([8192, 2], 1, F32), ([8192, 2], 1, F64),
       # 3*2^k / 5*2^k / 10^k / 360 column shapes
       ([96, 20], 2, F32), ([360, 12], 1, F64), ([100, 40, 6], 1, F32), ([640, 3], 2, F32), ([640, 3], 1, F64),
-      ([80, 160, 2], 1, F64), ([384, 24], 1, F32), ([12, 48, 5], 2, F64)]
+      ([80, 160, 2], 1, F64), ([384, 24], 1, F32), ([12, 48, 5], 2, F64),
+      # round-length rows, columns and split passes (kf_round_*)
+      ([120, 120, 12], 1, F32), ([720, 30], 1, F32), ([1000, 40], 1, F64), ([2000, 6], 1, F32),
+      ([75, 45, 27], 1, F64), ([6, 10, 9, 15], 2, F32), ([625, 18], 1, F32), ([4800, 3], 1, F64)]
 
 
 def nd_axis_maps(dims, desc):

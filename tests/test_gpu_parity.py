@@ -408,7 +408,11 @@ def test_c2_shape_round_trip_full_size(hip_ctx):
                                              ([1024, 8], 2, F32), ([2048, 3], 1, F32), ([1000, 6], 1, F64),
                                              ([3, 768, 5], 2, F32),
                                              # Rader axes inside N-D transforms (contiguous and strided)
-                                             ([8, 17], 2, F32), ([47, 8], 1, F32), ([97, 6], 1, F64)])
+                                             ([8, 17], 2, F32), ([47, 8], 1, F32), ([97, 6], 1, F64),
+                                             # round-length rows, columns and split passes (kf_round_*)
+                                             ([120, 120, 12], 1, F32), ([720, 30], 1, F32), ([1000, 40], 1, F64),
+                                             ([2000, 6], 1, F32), ([75, 45, 27], 1, F64), ([6, 10, 9, 15], 2, F32),
+                                             ([625, 18], 1, F32), ([4800, 3], 1, F64)])
 def test_nd_c2c(hip_ctx, dims, batch, prec):
     count = int(np.prod(dims)) * batch
     x = rand(count, count % 1000, prec)

@@ -17,7 +17,8 @@ def _gen():
 
 
 @pytest.mark.parametrize("name", ["kf_pow2_f32", "kf_pow2_f64", "kf_fam_f32", "kf_fam_f64", "kf_real_rows_f32",
-                                  "kf_real_rows_f64", "kf_round_f32", "kf_round_f64"])
+                                  "kf_real_rows_f64", "kf_round_f32", "kf_round_f64", "kf_round_nd_f32",
+                                  "kf_round_nd_f64"])
 def test_tables_match_generator(name):
     g = _gen()
     assert open(os.path.join(CSRC, name + ".hip")).read() == g.render(name)
@@ -35,6 +36,16 @@ def test_round_rows_follow_the_rule():
             assert TT == N // max(rad) and 1 <= TT <= 1024, (name, N)
             assert G * TT <= 1024 and G * LS * eb <= (80 * 1024 if G > 1 else 156 * 1024), (name, N)
             assert LS >= N + ((N - 1) >> PS if PS < 30 else 0), (name, N)
+    for prec, name in ((0, "kf_round_nd_f32"), (1, "kf_round_nd_f64")):
+        eb = 16 if prec else 8
+        for kind, io, N, TT, G, col, rad, PS, LS in g.TABLES[name]:
+            assert rad == g.radix_plan(N) and TT == N // max(rad), (name, N)
+            assert G * TT <= 1024 and G * LS * eb <= 80 * 1024, (name, N)
+            if col:
+                assert PS == 30 and LS % 2 == 1 and LS >= N and (G == 64 or 2 * G * TT > 1024 or
+                                                                 2 * G * LS * eb > 80 * 1024), (name, N)
+            else:
+                assert io == "PlainStaged" and G == max(1, min(64, 256 // TT)), (name, N)
 
 
 def test_recorded_strides_are_model_optimal_for_small_shapes():

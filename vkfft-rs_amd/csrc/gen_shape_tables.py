@@ -3,7 +3,7 @@ kf_real_rows_*.hip): the shape lists, the LDS bank-conflict model that chose
 each shape's LDS line stride LS and pad shift PS, and the emitter of the
 registration files.
 
-    python3 gen_shape_tables.py emit      # rewrite the eight kf_*.hip tables
+    python3 gen_shape_tables.py emit      # rewrite the ten kf_*.hip tables
     python3 gen_shape_tables.py check     # re-run the model search per shape
     python3 gen_shape_tables.py round     # re-derive the round-length rows by rule
 
@@ -405,6 +405,61 @@ def round_rows(prec):
     return rows
 
 
+def _smooth(lo, hi):
+    return sorted({2 ** a * 3 ** b * 5 ** c for a in range(15) for b in range(9) for c in range(7)
+                   if lo <= 2 ** a * 3 ** b * 5 ** c <= hi})
+
+
+def _split_pair(n):
+    """The two factors a strided axis of length n > 640 is split into (the
+    runtime's split_strided_axis: the smallest larger factor)."""
+    best = None
+    a = 2
+    while a * a <= n:
+        if n % a == 0 and (best is None or max(a, n // a) < best[0]):
+            best = (max(a, n // a), min(a, n // a))
+        a += 1
+    return best
+
+
+def nd_rows(prec, have):
+    """Shapes the N-D passes of lengths with factors 2, 3 and 5 need beyond the
+    other tables (`have`: (kind, N, col) already registered): strided columns of
+    every such length up to 640 (the longest strided axis of one pass), the
+    first split pass (FS_A columns) of the longer ones, and short rows staged
+    through LDS. Columns: threads per line = N / the largest radix, the
+    largest power-of-two lines per block up to 64 within 80 KiB and 1024
+    threads, an odd LDS stride without pads (lanes walk adjacent lines);
+    short rows: about 256 threads per block, LDS stride from the model search."""
+    eb = 16 if prec else 8
+    rows = []
+
+    def col_shape(kind, io, n):
+        rad = radix_plan(n)
+        tt = n // max(rad)
+        ls = n if n % 2 else n + 1
+        G = 64
+        while G > 1 and (G * ls * eb > 80 * 1024 or G * tt > 1024):
+            G //= 2
+        return (kind, io, n, tt, G, True, rad, 30, ls)
+
+    for n in _smooth(6, 640):
+        if ('PLAIN', n, True) not in have:
+            rows.append(col_shape('PLAIN', 'Plain', n))
+    for hi in sorted({_split_pair(n)[0] for n in _smooth(641, 16384)}):
+        if ('FS_A', hi, True) not in have:
+            rows.append(col_shape('FS_A', 'FsA', hi))
+    for n in _smooth(6, 199):
+        if ('PLAIN', n, False) in have:
+            continue
+        rad = radix_plan(n)
+        tt = n // max(rad)
+        G = max(1, min(64, 256 // tt))
+        best = search(n, tt, G, False, rad, True, eb)
+        rows.append(('PLAIN', 'PlainStaged', n, tt, G, False, rad, best[2], best[3]))
+    return rows
+
+
 HEADS_ROUND = ("// Fixed shapes of round lengths with factors 2, 3 and 5 outside the\n"
                "// power-of-two, 3*2^k and 5*2^k families, {p}: one-upload rows (1-D batches\n"
                "// and the contiguous axis of N-D transforms) in both directions and both\n"
@@ -419,10 +474,24 @@ HEADS = {'kf_pow2_f32': "// Fixed shapes of the power-of-two lengths outside the
 # Python: `python3 gen_shape_tables.py round` re-derives these lists)
 TABLES['kf_round_f32'] = [('PLAIN', 'Plain', 200, 25, 10, False, [8, 5, 5], 5, 217), ('PLAIN', 'Plain', 240, 30, 8, False, [8, 6, 5], 4, 255), ('PLAIN', 'Plain', 300, 25, 10, False, [12, 5, 5], 6, 313), ('PLAIN', 'Plain', 400, 25, 10, False, [16, 5, 5], 4, 425), ('PLAIN', 'Plain', 480, 48, 5, False, [10, 8, 6], 30, 480), ('PLAIN', 'Plain', 500, 50, 5, False, [10, 10, 5], 6, 515), ('PLAIN', 'Plain', 600, 60, 4, False, [10, 10, 6], 30, 604), ('PLAIN', 'Plain', 720, 72, 3, False, [10, 9, 8], 30, 728), ('PLAIN', 'Plain', 750, 125, 2, False, [6, 5, 5, 5], 30, 765), ('PLAIN', 'Plain', 800, 80, 3, False, [10, 10, 8], 6, 812), ('PLAIN', 'Plain', 900, 90, 2, False, [10, 10, 9], 30, 906), ('PLAIN', 'Plain', 960, 80, 3, False, [12, 10, 8], 5, 989), ('PLAIN', 'Plain', 1200, 100, 2, False, [12, 10, 10], 5, 1239), ('PLAIN', 'Plain', 1500, 125, 2, False, [12, 5, 5, 5], 6, 1535), ('PLAIN', 'Plain', 1600, 100, 2, False, [16, 10, 10], 4, 1706), ('PLAIN', 'Plain', 1800, 150, 1, False, [12, 6, 5, 5], 6, 1828), ('PLAIN', 'Plain', 1920, 120, 2, False, [16, 12, 10], 4, 2047), ('PLAIN', 'Plain', 2000, 125, 2, False, [16, 5, 5, 5], 5, 2065), ('PLAIN', 'Plain', 2400, 150, 1, False, [16, 6, 5, 5], 5, 2474), ('PLAIN', 'Plain', 2500, 250, 1, False, [10, 10, 5, 5], 30, 2500), ('PLAIN', 'Plain', 3000, 250, 1, False, [12, 10, 5, 5], 6, 3046), ('PLAIN', 'Plain', 3200, 200, 1, False, [16, 8, 5, 5], 4, 3399), ('PLAIN', 'Plain', 3600, 360, 1, False, [10, 10, 6, 6], 30, 3600), ('PLAIN', 'Plain', 4000, 250, 1, False, [16, 10, 5, 5], 5, 4124), ('PLAIN', 'Plain', 4800, 480, 1, False, [10, 10, 8, 6], 6, 4874), ('PLAIN', 'Plain', 5000, 500, 1, False, [10, 10, 10, 5], 30, 5000), ('PLAIN', 'Plain', 6000, 600, 1, False, [10, 10, 10, 6], 30, 6000), ('PLAIN', 'Plain', 6400, 640, 1, False, [10, 10, 8, 8], 6, 6499), ('PLAIN', 'Plain', 7200, 720, 1, False, [10, 10, 9, 8], 30, 7200), ('PLAIN', 'Plain', 8000, 800, 1, False, [10, 10, 10, 8], 6, 8124), ('PLAIN', 'Plain', 9000, 900, 1, False, [10, 10, 10, 9], 30, 9000), ('PLAIN', 'Plain', 9600, 800, 1, False, [12, 10, 10, 8], 5, 9899), ('PLAIN', 'Plain', 12000, 1000, 1, False, [12, 10, 10, 10], 5, 12374), ('PLAIN', 'Plain', 16000, 1000, 1, False, [16, 10, 10, 10], 4, 16999)]
 TABLES['kf_round_f64'] = [('PLAIN', 'Plain', 200, 25, 10, False, [8, 5, 5], 3, 225), ('PLAIN', 'Plain', 240, 30, 8, False, [8, 6, 5], 3, 273), ('PLAIN', 'Plain', 300, 25, 10, False, [12, 5, 5], 5, 314), ('PLAIN', 'Plain', 400, 25, 10, False, [16, 5, 5], 4, 426), ('PLAIN', 'Plain', 480, 48, 5, False, [10, 8, 6], 5, 494), ('PLAIN', 'Plain', 500, 50, 5, False, [10, 10, 5], 30, 506), ('PLAIN', 'Plain', 600, 60, 4, False, [10, 10, 6], 30, 604), ('PLAIN', 'Plain', 720, 72, 3, False, [10, 9, 8], 30, 720), ('PLAIN', 'Plain', 750, 125, 2, False, [6, 5, 5, 5], 30, 757), ('PLAIN', 'Plain', 800, 80, 3, False, [10, 10, 8], 30, 800), ('PLAIN', 'Plain', 900, 90, 2, False, [10, 10, 9], 30, 906), ('PLAIN', 'Plain', 960, 80, 3, False, [12, 10, 8], 5, 989), ('PLAIN', 'Plain', 1200, 100, 2, False, [12, 10, 10], 5, 1242), ('PLAIN', 'Plain', 1500, 125, 2, False, [12, 5, 5, 5], 5, 1552), ('PLAIN', 'Plain', 1600, 100, 2, False, [16, 10, 10], 4, 1706), ('PLAIN', 'Plain', 1800, 150, 1, False, [12, 6, 5, 5], 5, 1856), ('PLAIN', 'Plain', 1920, 120, 2, False, [16, 12, 10], 4, 2039), ('PLAIN', 'Plain', 2000, 125, 2, False, [16, 5, 5, 5], 4, 2125), ('PLAIN', 'Plain', 2400, 150, 1, False, [16, 6, 5, 5], 4, 2549), ('PLAIN', 'Plain', 2500, 250, 1, False, [10, 10, 5, 5], 30, 2500), ('PLAIN', 'Plain', 3000, 250, 1, False, [12, 10, 5, 5], 5, 3093), ('PLAIN', 'Plain', 3200, 200, 1, False, [16, 8, 5, 5], 4, 3399), ('PLAIN', 'Plain', 3600, 360, 1, False, [10, 10, 6, 6], 30, 3600), ('PLAIN', 'Plain', 4000, 250, 1, False, [16, 10, 5, 5], 4, 4249), ('PLAIN', 'Plain', 4800, 480, 1, False, [10, 10, 8, 6], 30, 4800), ('PLAIN', 'Plain', 5000, 500, 1, False, [10, 10, 10, 5], 30, 5000), ('PLAIN', 'Plain', 6000, 600, 1, False, [10, 10, 10, 6], 30, 6000), ('PLAIN', 'Plain', 6400, 640, 1, False, [10, 10, 8, 8], 30, 6400), ('PLAIN', 'Plain', 7200, 720, 1, False, [10, 10, 9, 8], 30, 7200), ('PLAIN', 'Plain', 8000, 800, 1, False, [10, 10, 10, 8], 30, 8000)]
+# nd_rows(0 / 1, keys of the other tables and of kf_plain / kf_nd / kf_real /
+# kf_blue): `python3 gen_shape_tables.py round` re-derives these lists too
+TABLES['kf_round_nd_f32'] = [('PLAIN', 'Plain', 6, 1, 64, True, [6], 30, 7), ('PLAIN', 'Plain', 9, 1, 64, True, [9], 30, 9), ('PLAIN', 'Plain', 10, 1, 64, True, [10], 30, 11), ('PLAIN', 'Plain', 15, 3, 64, True, [5, 3], 30, 15), ('PLAIN', 'Plain', 18, 3, 64, True, [6, 3], 30, 19), ('PLAIN', 'Plain', 25, 5, 64, True, [5, 5], 30, 25), ('PLAIN', 'Plain', 27, 3, 64, True, [9, 3], 30, 27), ('PLAIN', 'Plain', 30, 5, 64, True, [6, 5], 30, 31), ('PLAIN', 'Plain', 36, 6, 64, True, [6, 6], 30, 37), ('PLAIN', 'Plain', 45, 5, 64, True, [9, 5], 30, 45), ('PLAIN', 'Plain', 50, 5, 64, True, [10, 5], 30, 51), ('PLAIN', 'Plain', 54, 6, 64, True, [9, 6], 30, 55), ('PLAIN', 'Plain', 60, 6, 64, True, [10, 6], 30, 61), ('PLAIN', 'Plain', 72, 8, 64, True, [9, 8], 30, 73), ('PLAIN', 'Plain', 75, 15, 64, True, [5, 5, 3], 30, 75), ('PLAIN', 'Plain', 81, 9, 64, True, [9, 9], 30, 81), ('PLAIN', 'Plain', 90, 9, 64, True, [10, 9], 30, 91), ('PLAIN', 'Plain', 108, 9, 64, True, [12, 9], 30, 109), ('PLAIN', 'Plain', 120, 10, 64, True, [12, 10], 30, 121), ('PLAIN', 'Plain', 125, 25, 32, True, [5, 5, 5], 30, 125), ('PLAIN', 'Plain', 135, 15, 64, True, [9, 5, 3], 30, 135), ('PLAIN', 'Plain', 144, 12, 64, True, [12, 12], 30, 145), ('PLAIN', 'Plain', 150, 25, 32, True, [6, 5, 5], 30, 151), ('PLAIN', 'Plain', 162, 18, 32, True, [9, 6, 3], 30, 163), ('PLAIN', 'Plain', 180, 30, 32, True, [6, 6, 5], 30, 181), ('PLAIN', 'Plain', 200, 25, 32, True, [8, 5, 5], 30, 201), ('PLAIN', 'Plain', 216, 36, 16, True, [6, 6, 6], 30, 217), ('PLAIN', 'Plain', 225, 25, 32, True, [9, 5, 5], 30, 225), ('PLAIN', 'Plain', 240, 30, 32, True, [8, 6, 5], 30, 241), ('PLAIN', 'Plain', 243, 27, 32, True, [9, 9, 3], 30, 243), ('PLAIN', 'Plain', 250, 25, 32, True, [10, 5, 5], 30, 251), ('PLAIN', 'Plain', 270, 30, 32, True, [9, 6, 5], 30, 271), ('PLAIN', 'Plain', 288, 36, 16, True, [8, 6, 6], 30, 289), ('PLAIN', 'Plain', 300, 25, 32, True, [12, 5, 5], 30, 301), ('PLAIN', 'Plain', 324, 36, 16, True, [9, 6, 6], 30, 325), ('PLAIN', 'Plain', 375, 75, 8, True, [5, 5, 5, 3], 30, 375), ('PLAIN', 'Plain', 400, 25, 16, True, [16, 5, 5], 30, 401), ('PLAIN', 'Plain', 405, 45, 16, True, [9, 9, 5], 30, 405), ('PLAIN', 'Plain', 432, 36, 16, True, [12, 6, 6], 30, 433), ('PLAIN', 'Plain', 450, 45, 16, True, [10, 9, 5], 30, 451), ('PLAIN', 'Plain', 480, 48, 16, True, [10, 8, 6], 30, 481), ('PLAIN', 'Plain', 486, 54, 16, True, [9, 9, 6], 30, 487), ('PLAIN', 'Plain', 500, 50, 16, True, [10, 10, 5], 30, 501), ('PLAIN', 'Plain', 540, 54, 16, True, [10, 9, 6], 30, 541), ('PLAIN', 'Plain', 576, 64, 16, True, [9, 8, 8], 30, 577), ('PLAIN', 'Plain', 600, 60, 16, True, [10, 10, 6], 30, 601), ('PLAIN', 'Plain', 625, 125, 8, True, [5, 5, 5, 5], 30, 625), ('FS_A', 'FsA', 27, 3, 64, True, [9, 3], 30, 27), ('FS_A', 'FsA', 30, 5, 64, True, [6, 5], 30, 31), ('FS_A', 'FsA', 36, 6, 64, True, [6, 6], 30, 37), ('FS_A', 'FsA', 40, 5, 64, True, [8, 5], 30, 41), ('FS_A', 'FsA', 45, 5, 64, True, [9, 5], 30, 45), ('FS_A', 'FsA', 48, 6, 64, True, [8, 6], 30, 49), ('FS_A', 'FsA', 50, 5, 64, True, [10, 5], 30, 51), ('FS_A', 'FsA', 54, 6, 64, True, [9, 6], 30, 55), ('FS_A', 'FsA', 60, 6, 64, True, [10, 6], 30, 61), ('FS_A', 'FsA', 72, 8, 64, True, [9, 8], 30, 73), ('FS_A', 'FsA', 75, 15, 64, True, [5, 5, 3], 30, 75), ('FS_A', 'FsA', 80, 8, 64, True, [10, 8], 30, 81), ('FS_A', 'FsA', 81, 9, 64, True, [9, 9], 30, 81), ('FS_A', 'FsA', 90, 9, 64, True, [10, 9], 30, 91), ('FS_A', 'FsA', 96, 8, 64, True, [12, 8], 30, 97), ('FS_A', 'FsA', 100, 10, 64, True, [10, 10], 30, 101), ('FS_A', 'FsA', 108, 9, 64, True, [12, 9], 30, 109), ('FS_A', 'FsA', 120, 10, 64, True, [12, 10], 30, 121), ('FS_A', 'FsA', 125, 25, 32, True, [5, 5, 5], 30, 125), ('FS_A', 'FsA', 135, 15, 64, True, [9, 5, 3], 30, 135), ('FS_A', 'FsA', 144, 12, 64, True, [12, 12], 30, 145), ('FS_A', 'FsA', 162, 18, 32, True, [9, 6, 3], 30, 163), ('PLAIN', 'PlainStaged', 6, 1, 64, False, [6], 3, 6), ('PLAIN', 'PlainStaged', 9, 1, 64, False, [9], 4, 9), ('PLAIN', 'PlainStaged', 10, 1, 64, False, [10], 4, 10), ('PLAIN', 'PlainStaged', 15, 3, 64, False, [5, 3], 4, 19), ('PLAIN', 'PlainStaged', 18, 3, 64, False, [6, 3], 5, 19), ('PLAIN', 'PlainStaged', 25, 5, 51, False, [5, 5], 5, 25), ('PLAIN', 'PlainStaged', 27, 3, 64, False, [9, 3], 5, 35), ('PLAIN', 'PlainStaged', 30, 5, 51, False, [6, 5], 5, 37), ('PLAIN', 'PlainStaged', 36, 6, 42, False, [6, 6], 6, 38), ('PLAIN', 'PlainStaged', 45, 5, 51, False, [9, 5], 6, 53), ('PLAIN', 'PlainStaged', 50, 5, 51, False, [10, 5], 6, 53), ('PLAIN', 'PlainStaged', 54, 6, 42, False, [9, 6], 6, 54), ('PLAIN', 'PlainStaged', 60, 6, 42, False, [10, 6], 6, 70), ('PLAIN', 'PlainStaged', 72, 8, 32, False, [9, 8], 30, 72), ('PLAIN', 'PlainStaged', 75, 15, 17, False, [5, 5, 3], 30, 79), ('PLAIN', 'PlainStaged', 81, 9, 28, False, [9, 9], 30, 89), ('PLAIN', 'PlainStaged', 90, 9, 28, False, [10, 9], 30, 105), ('PLAIN', 'PlainStaged', 108, 9, 28, False, [12, 9], 30, 121), ('PLAIN', 'PlainStaged', 120, 10, 25, False, [12, 10], 6, 122), ('PLAIN', 'PlainStaged', 125, 25, 10, False, [5, 5, 5], 30, 137), ('PLAIN', 'PlainStaged', 135, 15, 17, False, [9, 5, 3], 30, 143), ('PLAIN', 'PlainStaged', 144, 12, 21, False, [12, 12], 6, 156), ('PLAIN', 'PlainStaged', 150, 25, 10, False, [6, 5, 5], 30, 153), ('PLAIN', 'PlainStaged', 162, 18, 14, False, [9, 6, 3], 30, 162), ('PLAIN', 'PlainStaged', 180, 30, 8, False, [6, 6, 5], 30, 190)]
+TABLES['kf_round_nd_f64'] = [('PLAIN', 'Plain', 6, 1, 64, True, [6], 30, 7), ('PLAIN', 'Plain', 9, 1, 64, True, [9], 30, 9), ('PLAIN', 'Plain', 10, 1, 64, True, [10], 30, 11), ('PLAIN', 'Plain', 15, 3, 64, True, [5, 3], 30, 15), ('PLAIN', 'Plain', 18, 3, 64, True, [6, 3], 30, 19), ('PLAIN', 'Plain', 25, 5, 64, True, [5, 5], 30, 25), ('PLAIN', 'Plain', 27, 3, 64, True, [9, 3], 30, 27), ('PLAIN', 'Plain', 30, 5, 64, True, [6, 5], 30, 31), ('PLAIN', 'Plain', 36, 6, 64, True, [6, 6], 30, 37), ('PLAIN', 'Plain', 45, 5, 64, True, [9, 5], 30, 45), ('PLAIN', 'Plain', 50, 5, 64, True, [10, 5], 30, 51), ('PLAIN', 'Plain', 54, 6, 64, True, [9, 6], 30, 55), ('PLAIN', 'Plain', 60, 6, 64, True, [10, 6], 30, 61), ('PLAIN', 'Plain', 72, 8, 64, True, [9, 8], 30, 73), ('PLAIN', 'Plain', 75, 15, 64, True, [5, 5, 3], 30, 75), ('PLAIN', 'Plain', 81, 9, 32, True, [9, 9], 30, 81), ('PLAIN', 'Plain', 90, 9, 32, True, [10, 9], 30, 91), ('PLAIN', 'Plain', 108, 9, 32, True, [12, 9], 30, 109), ('PLAIN', 'Plain', 120, 10, 32, True, [12, 10], 30, 121), ('PLAIN', 'Plain', 125, 25, 32, True, [5, 5, 5], 30, 125), ('PLAIN', 'Plain', 135, 15, 32, True, [9, 5, 3], 30, 135), ('PLAIN', 'Plain', 144, 12, 32, True, [12, 12], 30, 145), ('PLAIN', 'Plain', 150, 25, 32, True, [6, 5, 5], 30, 151), ('PLAIN', 'Plain', 162, 18, 16, True, [9, 6, 3], 30, 163), ('PLAIN', 'Plain', 180, 30, 16, True, [6, 6, 5], 30, 181), ('PLAIN', 'Plain', 200, 25, 16, True, [8, 5, 5], 30, 201), ('PLAIN', 'Plain', 216, 36, 16, True, [6, 6, 6], 30, 217), ('PLAIN', 'Plain', 225, 25, 16, True, [9, 5, 5], 30, 225), ('PLAIN', 'Plain', 240, 30, 16, True, [8, 6, 5], 30, 241), ('PLAIN', 'Plain', 243, 27, 16, True, [9, 9, 3], 30, 243), ('PLAIN', 'Plain', 250, 25, 16, True, [10, 5, 5], 30, 251), ('PLAIN', 'Plain', 270, 30, 16, True, [9, 6, 5], 30, 271), ('PLAIN', 'Plain', 288, 36, 16, True, [8, 6, 6], 30, 289), ('PLAIN', 'Plain', 300, 25, 16, True, [12, 5, 5], 30, 301), ('PLAIN', 'Plain', 324, 36, 8, True, [9, 6, 6], 30, 325), ('PLAIN', 'Plain', 375, 75, 8, True, [5, 5, 5, 3], 30, 375), ('PLAIN', 'Plain', 400, 25, 8, True, [16, 5, 5], 30, 401), ('PLAIN', 'Plain', 405, 45, 8, True, [9, 9, 5], 30, 405), ('PLAIN', 'Plain', 432, 36, 8, True, [12, 6, 6], 30, 433), ('PLAIN', 'Plain', 450, 45, 8, True, [10, 9, 5], 30, 451), ('PLAIN', 'Plain', 480, 48, 8, True, [10, 8, 6], 30, 481), ('PLAIN', 'Plain', 486, 54, 8, True, [9, 9, 6], 30, 487), ('PLAIN', 'Plain', 500, 50, 8, True, [10, 10, 5], 30, 501), ('PLAIN', 'Plain', 540, 54, 8, True, [10, 9, 6], 30, 541), ('PLAIN', 'Plain', 576, 64, 8, True, [9, 8, 8], 30, 577), ('PLAIN', 'Plain', 600, 60, 8, True, [10, 10, 6], 30, 601), ('PLAIN', 'Plain', 625, 125, 8, True, [5, 5, 5, 5], 30, 625), ('FS_A', 'FsA', 27, 3, 64, True, [9, 3], 30, 27), ('FS_A', 'FsA', 30, 5, 64, True, [6, 5], 30, 31), ('FS_A', 'FsA', 36, 6, 64, True, [6, 6], 30, 37), ('FS_A', 'FsA', 40, 5, 64, True, [8, 5], 30, 41), ('FS_A', 'FsA', 45, 5, 64, True, [9, 5], 30, 45), ('FS_A', 'FsA', 48, 6, 64, True, [8, 6], 30, 49), ('FS_A', 'FsA', 50, 5, 64, True, [10, 5], 30, 51), ('FS_A', 'FsA', 54, 6, 64, True, [9, 6], 30, 55), ('FS_A', 'FsA', 60, 6, 64, True, [10, 6], 30, 61), ('FS_A', 'FsA', 72, 8, 64, True, [9, 8], 30, 73), ('FS_A', 'FsA', 75, 15, 64, True, [5, 5, 3], 30, 75), ('FS_A', 'FsA', 80, 8, 32, True, [10, 8], 30, 81), ('FS_A', 'FsA', 81, 9, 32, True, [9, 9], 30, 81), ('FS_A', 'FsA', 90, 9, 32, True, [10, 9], 30, 91), ('FS_A', 'FsA', 96, 8, 32, True, [12, 8], 30, 97), ('FS_A', 'FsA', 100, 10, 32, True, [10, 10], 30, 101), ('FS_A', 'FsA', 108, 9, 32, True, [12, 9], 30, 109), ('FS_A', 'FsA', 120, 10, 32, True, [12, 10], 30, 121), ('FS_A', 'FsA', 125, 25, 32, True, [5, 5, 5], 30, 125), ('FS_A', 'FsA', 135, 15, 32, True, [9, 5, 3], 30, 135), ('FS_A', 'FsA', 144, 12, 32, True, [12, 12], 30, 145), ('FS_A', 'FsA', 162, 18, 16, True, [9, 6, 3], 30, 163), ('PLAIN', 'PlainStaged', 6, 1, 64, False, [6], 3, 6), ('PLAIN', 'PlainStaged', 9, 1, 64, False, [9], 4, 9), ('PLAIN', 'PlainStaged', 10, 1, 64, False, [10], 3, 11), ('PLAIN', 'PlainStaged', 15, 3, 64, False, [5, 3], 4, 19), ('PLAIN', 'PlainStaged', 18, 3, 64, False, [6, 3], 5, 19), ('PLAIN', 'PlainStaged', 25, 5, 51, False, [5, 5], 5, 29), ('PLAIN', 'PlainStaged', 27, 3, 64, False, [9, 3], 5, 27), ('PLAIN', 'PlainStaged', 30, 5, 51, False, [6, 5], 5, 37), ('PLAIN', 'PlainStaged', 36, 6, 42, False, [6, 6], 6, 38), ('PLAIN', 'PlainStaged', 45, 5, 51, False, [9, 5], 6, 45), ('PLAIN', 'PlainStaged', 50, 5, 51, False, [10, 5], 6, 53), ('PLAIN', 'PlainStaged', 54, 6, 42, False, [9, 6], 6, 54), ('PLAIN', 'PlainStaged', 60, 6, 42, False, [10, 6], 5, 62), ('PLAIN', 'PlainStaged', 72, 8, 32, False, [9, 8], 30, 72), ('PLAIN', 'PlainStaged', 75, 15, 17, False, [5, 5, 3], 30, 79), ('PLAIN', 'PlainStaged', 81, 9, 28, False, [9, 9], 30, 81), ('PLAIN', 'PlainStaged', 90, 9, 28, False, [10, 9], 30, 97), ('PLAIN', 'PlainStaged', 108, 9, 28, False, [12, 9], 5, 113), ('PLAIN', 'PlainStaged', 120, 10, 25, False, [12, 10], 6, 122), ('PLAIN', 'PlainStaged', 125, 25, 10, False, [5, 5, 5], 30, 129), ('PLAIN', 'PlainStaged', 135, 15, 17, False, [9, 5, 3], 30, 135), ('PLAIN', 'PlainStaged', 144, 12, 21, False, [12, 12], 5, 148), ('PLAIN', 'PlainStaged', 150, 25, 10, False, [6, 5, 5], 30, 153), ('PLAIN', 'PlainStaged', 162, 18, 14, False, [9, 6, 3], 30, 162), ('PLAIN', 'PlainStaged', 180, 30, 8, False, [6, 6, 5], 30, 182)]
+HEADS_ROUND_ND = ("// Fixed shapes for the N-D passes of lengths with factors 2, 3 and 5\n"
+                  "// outside the power-of-two, 3*2^k and 5*2^k families, {p}: strided columns up\n"
+                  "// to 640 (the longest strided axis of one pass), the first pass of a split\n"
+                  "// strided axis (FS_A columns of its larger factor) and short rows staged\n"
+                  "// through LDS. Columns: threads per line = N / the largest radix, the largest\n"
+                  "// power-of-two lines per block up to 64 within 80 KiB and 1024 threads, an odd\n"
+                  "// LDS stride; rows: about 256 threads per block, LDS stride from the bank model.\n")
+HEADS['kf_round_nd_f32'] = HEADS_ROUND_ND.format(p='f32')
+HEADS['kf_round_nd_f64'] = HEADS_ROUND_ND.format(p='f64')
 HEADS['kf_round_f32'] = HEADS_ROUND.format(p='f32')
 HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 
-FUNCS = {'kf_round_f32': 'fixed_table_round_f32', 'kf_round_f64': 'fixed_table_round_f64', 'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
+FUNCS = {'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
+         'kf_round_f32': 'fixed_table_round_f32', 'kf_round_f64': 'fixed_table_round_f64', 'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
 
 
 def roles(kind, col):
@@ -493,6 +562,20 @@ if __name__ == "__main__":
     elif len(sys.argv) > 1 and sys.argv[1] == "round":
         for prec, name in ((0, "kf_round_f32"), (1, "kf_round_f64")):
             rows = round_rows(prec)
+            print(name, "matches" if rows == TABLES[name] else "DIFFERS", rows, flush=True)
+        import re
+        for prec, name in ((0, "kf_round_nd_f32"), (1, "kf_round_nd_f64")):
+            have = set()
+            for other, items in TABLES.items():
+                if other.startswith("kf_round_nd") or other.endswith("f64") != bool(prec):
+                    continue
+                have |= {(it[0], it[2], it[5]) for it in items if not isinstance(it, str)}
+            for f in ("kf_plain.hip", "kf_nd.hip", "kf_real.hip", "kf_blue.hip"):
+                pat = r"KK_(\w+), Io\w+, (float|double), (\d), -?\d, (\d+), \d+, \d+, \d+, \d+, (true|false)"
+                for m in re.finditer(pat, open(os.path.join(HERE, f)).read()):
+                    if int(m.group(3)) == prec:
+                        have.add((m.group(1), int(m.group(4)), m.group(5) == "true"))
+            rows = nd_rows(prec, have)
             print(name, "matches" if rows == TABLES[name] else "DIFFERS", rows, flush=True)
     else:
         print(__doc__)

@@ -25,6 +25,8 @@ const FixedKernel* fixed_table_real_rows_f32(int* count);
 const FixedKernel* fixed_table_real_rows_f64(int* count);
 const FixedKernel* fixed_table_round_f32(int* count);
 const FixedKernel* fixed_table_round_f64(int* count);
+const FixedKernel* fixed_table_round_nd_f32(int* count);
+const FixedKernel* fixed_table_round_nd_f64(int* count);
 
 // All registered fixed-shape instantiations, merged once (thread-safe
 // static initialisation).
@@ -37,7 +39,8 @@ static const FixedKernel* registry(int* count) {
         const FixedKernel* (*tables[])(int*) = {fixed_table_plain, fixed_table_wave, fixed_table_real, fixed_table_blue,
                                                 fixed_table_nd, fixed_table_pow2_f32, fixed_table_pow2_f64,
                                                 fixed_table_fam_f32, fixed_table_fam_f64, fixed_table_real_rows_f32,
-                                                fixed_table_real_rows_f64, fixed_table_round_f32, fixed_table_round_f64};
+                                                fixed_table_real_rows_f64, fixed_table_round_f32, fixed_table_round_f64,
+                                                fixed_table_round_nd_f32, fixed_table_round_nd_f64};
         constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
         int counts[kTables], sum = 0;
         const FixedKernel* ptrs[kTables];
