@@ -353,7 +353,7 @@ def _muli(v, s):
     return (-v.imag + 1j * v.real) if s > 0 else (v.imag - 1j * v.real)
 
 
-@pytest.mark.parametrize("n", [64, 210, 1000, 1024, 4096, 6000, 8192])
+@pytest.mark.parametrize("n", [64, 210, 1000, 1024, 4096, 6000, 8192, 2400, 16000, 20000, 32000])
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_r2c_half_addressing(idx_ctx, n, prec):
     """Even one-upload R2C (real pairs -> half-length FFT -> postprocess):
@@ -361,6 +361,8 @@ def test_r2c_half_addressing(idx_ctx, n, prec):
     (A + conj Z[M-k]) - i (A - conj Z[M-k]) from A = Z[k] (k = 0 and M both
     take Z[0]). Random integer tags make a wrong pairing or placement show:
     the result must match bit for bit."""
+    if prec == F64 and n > 16384:
+        pytest.skip("an f64 half length above 8192 runs as two uploads (the four-step addressing tests)")
     batch, M = 3, n // 2
     rng = np.random.default_rng(n)
     x = rng.integers(0, 1 << 18, n * batch).astype(np.float32 if prec == F32 else np.float64)
@@ -383,13 +385,15 @@ def test_r2c_half_addressing(idx_ctx, n, prec):
     assert np.array_equal(out.reshape(batch, M + 1), expect.astype(out.dtype))
 
 
-@pytest.mark.parametrize("n", [64, 210, 1000, 1024, 4096, 6000, 8192])
+@pytest.mark.parametrize("n", [64, 210, 1000, 1024, 4096, 6000, 8192, 2400, 16000, 20000, 32000])
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_c2r_half_addressing(idx_ctx, n, prec):
     """Even one-upload C2R (preprocess -> half-length inverse FFT -> real
     pairs): with identity arithmetic Z[k] = (X[k] + conj X[M-k]) +
     i (X[k] - conj X[M-k]) for k < M, then the Stockham map, then the
     complex results as real pairs; random integer tags, bit for bit."""
+    if prec == F64 and n > 16384:
+        pytest.skip("an f64 half length above 8192 runs as two uploads (the four-step addressing tests)")
     batch, M = 3, n // 2
     rng = np.random.default_rng(n + 1)
     re = rng.integers(0, 1 << 18, (M + 1) * batch)

@@ -285,7 +285,7 @@ def test_r2c_c2r(hip_ctx, n, prec):
     assert o.rel_l2(xr, back) <= TOL[prec] * (1 if prec == F32 else 10)
 
 
-@pytest.mark.parametrize("n", [6, 18, 22, 26, 200, 210, 686, 1000, 3000, 6000, 9000, 18018])
+@pytest.mark.parametrize("n", [6, 18, 22, 26, 196, 210, 686, 1078, 2002, 5880, 9000, 18018])
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_r2c_c2r_runtime_lengths(hip_ctx, n, prec):
     """Even lengths without a registered shape (runtime-radix kernels whose
@@ -326,15 +326,18 @@ def test_c2r_runtime_variants_covered(hip_ctx):
     L = c2r_launch(18018, F32)
     assert L["runtime_variant"]["wide"] and L["runtime_variant"]["hbm_direct"]
     assert L["runtime_variant"]["direct_preprocess"]
-    L = c2r_launch(2000, F32)
+    L = c2r_launch(2800, F32)
     assert L["radices"][0] == 8 and L["runtime_variant"]["direct_preprocess"]
     for n in (6, 18):
         L = c2r_launch(n, F64)
         assert L["runtime_variant"]["hbm_direct"] and not L["runtime_variant"]["direct_preprocess"]
 
 
-HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 320],
-              F64: [64, 128, 160, 192, 256, 320, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096]}
+HALF_FIXED = {F32: [256, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096, 5120, 6144, 8192, 320,
+                   # round half lengths and 10^k / 360 (kf_round_real_*)
+                   200, 360, 500, 750, 1000, 1200, 1500, 2400, 3000, 5000, 8000, 10000, 16000],
+              F64: [64, 128, 160, 192, 256, 320, 384, 512, 640, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096,
+                    240, 360, 600, 1000, 1800, 3000, 4800, 8000]}
 
 
 ROUND = [200, 240, 300, 400, 480, 500, 600, 720, 750, 800, 900, 960, 1200, 1500, 1600, 1800, 1920, 2000, 2400,

@@ -3,7 +3,7 @@ kf_real_rows_*.hip): the shape lists, the LDS bank-conflict model that chose
 each shape's LDS line stride LS and pad shift PS, and the emitter of the
 registration files.
 
-    python3 gen_shape_tables.py emit      # rewrite the ten kf_*.hip tables
+    python3 gen_shape_tables.py emit      # rewrite the twelve kf_*.hip tables
     python3 gen_shape_tables.py check     # re-run the model search per shape
     python3 gen_shape_tables.py round     # re-derive the round-length rows by rule
 
@@ -485,12 +485,38 @@ HEADS_ROUND_ND = ("// Fixed shapes for the N-D passes of lengths with factors 2,
                   "// through LDS. Columns: threads per line = N / the largest radix, the largest\n"
                   "// power-of-two lines per block up to 64 within 80 KiB and 1024 threads, an odd\n"
                   "// LDS stride; rows: about 256 threads per block, LDS stride from the bank model.\n")
+# Even-length real rows whose half length has a round-length or 10^k / 360 C2C
+# row shape: the same radices, threads, lines per block and LDS strides.
+def round_real_rows(prec):
+    fam = 'kf_fam_f64' if prec else 'kf_fam_f32'
+    src = list(TABLES['kf_round_f64' if prec else 'kf_round_f32'])
+    src += [it for it in TABLES[fam] if not isinstance(it, str) and it[0] == 'PLAIN' and not it[5] and
+            it[1] == 'Plain' and it[2] in (100, 360, 1000, 10000)]
+    rows = []
+    for kind, io, N, TT, G, col, rad, PS, LS in sorted(src, key=lambda r: r[2]):
+        rows.append(('R2C_HALF', 'R2CHalf', N, TT, G, False, rad, PS, LS))
+        rows.append(('C2R_HALF', 'C2RHalf', N, TT, G, False, rad, PS, LS))
+    return rows
+
+
+TABLES['kf_round_real_f32'] = round_real_rows(0)
+TABLES['kf_round_real_f64'] = round_real_rows(1)
+HEADS_ROUND_REAL = ("// Fixed shapes of the one-upload even-length real transforms whose half\n"
+                    "// length M has a round-length (kf_round_{p}) or 10^k / 360 C2C row shape, {p}:\n"
+                    "// the half-size packed FFT of R2C (postprocess fused into the staged store)\n"
+                    "// and of C2R (preprocess fused into the direct loads), with the same radices,\n"
+                    "// threads, lines per block and LDS strides as those rows. R2C is registered\n"
+                    "// for the caller's input with or without the caller's output, C2R for the\n"
+                    "// caller's output with or without the caller's input.\n")
+HEADS['kf_round_real_f32'] = HEADS_ROUND_REAL.format(p='f32')
+HEADS['kf_round_real_f64'] = HEADS_ROUND_REAL.format(p='f64')
 HEADS['kf_round_nd_f32'] = HEADS_ROUND_ND.format(p='f32')
 HEADS['kf_round_nd_f64'] = HEADS_ROUND_ND.format(p='f64')
 HEADS['kf_round_f32'] = HEADS_ROUND.format(p='f32')
 HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 
-FUNCS = {'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
+FUNCS = {'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
+         'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
          'kf_round_f32': 'fixed_table_round_f32', 'kf_round_f64': 'fixed_table_round_f64', 'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
 
 

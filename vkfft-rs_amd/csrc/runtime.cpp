@@ -1880,9 +1880,13 @@ int plan_r2c(Ctx& c, size_t n, size_t batch) {
     int rsh;
     int rc = two_level(p, n, prec, &rlo, &rhi, &rsh);
     if (rc) return rc;
+    // one upload when the half length has a runtime geometry or a fixed shape
+    // (a fixed shape without padding can hold a line the runtime one cannot)
     Geometry g0 = geometry(M, prec, 1, c.lds_max, c.lds_max);
-    if (g0.ok) {
-        Geometry g = kernel_geometry(KK_R2C_HALF, prec, -1, M, false, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+    const Geometry gh = kernel_geometry(KK_R2C_HALF, prec, -1, M, false, g0.ok ? std::max(1, 256 / g0.TT) : 1,
+                                        c.lds_max, c.lds_budget);
+    if (g0.ok || (gh.ok && gh.fixed)) {
+        const Geometry& g = gh;
         KArgs a = blank();
         a.in_es = a.out_es = 1;
         a.in_os = (long long)M, a.out_os = (long long)h;
@@ -1970,9 +1974,13 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     int rsh;
     int rc = two_level(p, n, prec, &rlo, &rhi, &rsh);
     if (rc) return rc;
+    // one upload when the half length has a runtime geometry or a fixed shape
+    // (a fixed shape without padding can hold a line the runtime one cannot)
     Geometry g0 = geometry(M, prec, 1, c.lds_max, c.lds_max);
-    if (g0.ok) {
-        Geometry g = kernel_geometry(KK_C2R_HALF, prec, 1, M, false, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+    const Geometry gh = kernel_geometry(KK_C2R_HALF, prec, 1, M, false, g0.ok ? std::max(1, 256 / g0.TT) : 1,
+                                        c.lds_max, c.lds_budget);
+    if (g0.ok || (gh.ok && gh.fixed)) {
+        const Geometry& g = gh;
         KArgs a = blank();
         a.in_es = a.out_es = 1;
         a.in_os = (long long)h, a.out_os = (long long)M;
