@@ -86,6 +86,29 @@ def test_c2c_length_sweep(hip_ctx, prec, direction):
 
 
 @pytest.mark.parametrize("prec", [F32, F64])
+def test_runtime_kernels_on_registered_lengths(hip_ctx, monkeypatch, prec):
+    """VKFX_DISABLE_FIXED=1: lengths that normally run fixed shapes go through
+    the runtime-shape kernels (rows, columns, split axes), against the oracle,
+    so the runtime path stays covered as the fixed families grow."""
+    monkeypatch.setenv("VKFX_DISABLE_FIXED", "1")
+    ctx = vk.HipExecutionContext(0)
+    try:
+        for n in (8, 12, 30, 100, 720, 1000, 1024, 2000, 4096):
+            x = rand(n * 5, n, prec)
+            y, ir = c2c(ctx, [n], 5, x, prec)
+            assert not any(p.get("fixed_shape") for p in ctx.plan(ir).describe()["passes"]), n
+            assert o.rel_l2(y, oracle_c2c(x, n)) <= TOL[prec], (n, prec)
+        for dims in ([120, 30], [1000, 6], [25, 12, 8]):
+            count = int(np.prod(dims))
+            x = rand(count * 2, count, prec)
+            y, ir = c2c(ctx, dims, 2, x, prec)
+            assert not any(p.get("fixed_shape") for p in ctx.plan(ir).describe()["passes"]), dims
+            assert o.rel_l2(y, o.fft_nd(x, dims, 2, threads=8)) <= TOL[prec], (dims, prec)
+    finally:
+        ctx.close()
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
 def test_many_lines_per_block(hip_ctx, prec):
     """Short lengths at batch 70 and 133: blocks of up to 64 lines, partial
     last blocks, every line checked (the line placement of the cooperative
