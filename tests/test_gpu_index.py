@@ -182,7 +182,10 @@ def test_fixed_shape_variants(idx_ctx, n, kind, pick):
 
 
 @pytest.mark.parametrize("n,batch,prec", [(1 << 20, 2, F32), (1 << 17, 3, F32), (3 ** 12, 1, F32),
-                                          (1 << 18, 2, F64), (5 ** 8, 1, F64)])
+                                          (1 << 18, 2, F64), (5 ** 8, 1, F64),
+                                          # kf_round_fs_* factors
+                                          (1 << 16, 2, F32), (60000, 2, F64), (100000, 2, F32),
+                                          (250000, 1, F64), (1000000, 1, F32), (4000000, 1, F32)])
 def test_four_step(idx_ctx, n, batch, prec):
     d = check_1d(idx_ctx, n, batch, prec)
     assert [p["kernel"] for p in d["passes"][:2]] == ["four_step_columns", "four_step_rows"]

@@ -150,6 +150,24 @@ def test_c2c_four_step(hip_ctx, n):
     assert o.rel_l2(z, x) <= 2 * TOL[F32]
 
 
+@pytest.mark.parametrize("n", [1 << 16, 60000, 100000, 250000, 1000000, 1 << 22, 4000000])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_c2c_four_step_round_factors(hip_ctx, n, prec):
+    """Two-upload four-step over the factors of kf_round_fs_* (fixed column
+    and row passes, both directions), against pocketfft in f64."""
+    batch = 2
+    x = rand(n * batch, n % 1009, prec)
+    y, ir = c2c(hip_ctx, [n], batch, x, prec)
+    passes = hip_ctx.plan(ir).describe()["passes"]
+    assert [p["kernel"] for p in passes[:2]] == ["four_step_columns", "four_step_rows"], passes[:2]
+    assert all(p["fixed_shape"] for p in passes), [(p["kernel"], p["fft_len"]) for p in passes]
+    ref = np.fft.fft(x.reshape(batch, n).astype(np.complex128), axis=1).reshape(-1)
+    assert o.rel_l2(y, ref) <= TOL[prec]
+    z, ir2 = c2c(hip_ctx, [n], batch, y, prec, INV, normalize=True)
+    assert all(p["fixed_shape"] for p in hip_ctx.plan(ir2).describe()["passes"])
+    assert o.rel_l2(z, x) <= 4 * TOL[prec]
+
+
 def test_c2c_four_step_f64(hip_ctx):
     n = 1 << 14
     x = rand(n * 2, 7, F64)

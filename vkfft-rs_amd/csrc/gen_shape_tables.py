@@ -3,7 +3,7 @@ kf_real_rows_*.hip): the shape lists, the LDS bank-conflict model that chose
 each shape's LDS line stride LS and pad shift PS, and the emitter of the
 registration files.
 
-    python3 gen_shape_tables.py emit      # rewrite the twelve kf_*.hip tables
+    python3 gen_shape_tables.py emit      # rewrite the fourteen kf_*.hip tables
     python3 gen_shape_tables.py check     # re-run the model search per shape
     python3 gen_shape_tables.py round     # re-derive the round-length rows by rule
 
@@ -460,6 +460,59 @@ def nd_rows(prec, have):
     return rows
 
 
+def registered_keys(prec, skip=()):
+    """(kind, N, col) of every shape of one precision registered in both
+    directions: the generated tables except `skip` (always both), and the
+    hand-written kf_plain / kf_nd / kf_real / kf_blue tables."""
+    import re
+    have = set()
+    for other, items in TABLES.items():
+        if other in skip or other.endswith("f64") != bool(prec):
+            continue
+        have |= {(it[0], it[2], it[5]) for it in items if not isinstance(it, str)}
+    dirs = {}
+    pat = r"KK_(\w+), Io\w+, (float|double), (\d), (-?\d), (\d+), \d+, \d+, \d+, \d+, (true|false)"
+    for f in ("kf_plain.hip", "kf_nd.hip", "kf_real.hip", "kf_blue.hip"):
+        for m in re.finditer(pat, open(os.path.join(HERE, f)).read()):
+            if int(m.group(3)) == prec:
+                dirs.setdefault((m.group(1), int(m.group(5)), m.group(6) == "true"), set()).add(int(m.group(4)))
+    have |= {k for k, d in dirs.items() if d == {-1, 1}}
+    return have
+
+
+# Factors of the two-upload four-step (the split four_step_split picks: the
+# smallest larger factor) for common lengths: powers of two and round ones.
+FOURSTEP = [128, 240, 250, 256, 400, 500, 512, 1000, 1024, 2000, 2048]
+
+
+def fourstep_rows(prec, have):
+    """FS_A column passes (threads per line = N / the largest radix, the
+    largest power-of-two columns per block up to 32 within 150 KiB and 1024
+    threads, odd LDS stride) and FS_B row passes (up to 16 rows per block
+    for 128-byte transposed stores, the rows' pad rule) of the FOURSTEP
+    lengths not registered yet."""
+    eb = 16 if prec else 8
+    ps_row = 3 if prec else 4
+    rows = []
+    for n in FOURSTEP:
+        rad = radix_plan(n)
+        tt = n // max(rad)
+        if ('FS_A', n, True) not in have:
+            ls = n if n % 2 else n + 1
+            G = 32
+            while G > 1 and (G * ls * eb > 150 * 1024 or G * tt > 1024):
+                G //= 2
+            rows.append(('FS_A', 'FsA', n, tt, G, True, rad, 30, ls))
+        if ('FS_B', n, False) not in have:
+            ls = n + (n >> ps_row)
+            ls += 1 - ls % 2
+            G = 16
+            while G > 1 and (G * ls * eb > 150 * 1024 or G * tt > 1024):
+                G //= 2
+            rows.append(('FS_B', 'FsB', n, tt, G, False, rad, ps_row, ls))
+    return rows
+
+
 HEADS_ROUND = ("// Fixed shapes of round lengths with factors 2, 3 and 5 outside the\n"
                "// power-of-two, 3*2^k and 5*2^k families, {p}: one-upload rows (1-D batches\n"
                "// and the contiguous axis of N-D transforms) in both directions and both\n"
@@ -508,6 +561,18 @@ HEADS_ROUND_REAL = ("// Fixed shapes of the one-upload even-length real transfor
                     "// threads, lines per block and LDS strides as those rows. R2C is registered\n"
                     "// for the caller's input with or without the caller's output, C2R for the\n"
                     "// caller's output with or without the caller's input.\n")
+# fourstep_rows(0 / 1, registered_keys(0 / 1)) before these tables existed
+TABLES['kf_round_fs_f32'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 4, 137), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 4, 255), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 4, 265), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 4, 273), ('FS_A', 'FsA', 400, 25, 32, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 4, 425), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 4, 531), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 4, 545), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 4, 1063), ('FS_A', 'FsA', 1024, 64, 16, True, [16, 8, 8], 30, 1025), ('FS_A', 'FsA', 2000, 125, 8, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 8, False, [16, 5, 5, 5], 4, 2125), ('FS_A', 'FsA', 2048, 128, 8, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 8, False, [16, 16, 8], 4, 2177)]
+TABLES['kf_round_fs_f64'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 3, 145), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 3, 271), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 3, 281), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 3, 289), ('FS_A', 'FsA', 400, 25, 16, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 3, 451), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 3, 563), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 3, 577), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 3, 1125), ('FS_A', 'FsA', 1024, 64, 8, True, [16, 8, 8], 30, 1025), ('FS_B', 'FsB', 1024, 64, 8, False, [16, 8, 8], 3, 1153), ('FS_A', 'FsA', 2000, 125, 4, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 4, False, [16, 5, 5, 5], 3, 2251), ('FS_A', 'FsA', 2048, 128, 4, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 4, False, [16, 16, 8], 3, 2305)]
+HEADS_ROUND_FS = ("// Fixed shapes of the two-upload four-step passes, {p}: FS_A column passes\n"
+                  "// (FFT over N1 + the W_M twiddle) and FS_B row passes (FFT over N2 + the\n"
+                  "// transposed store) for the factors four_step_split picks for common lengths\n"
+                  "// (powers of two and round ones: 2^16, 60000, 10^5, 250000, 10^6, 2^22,\n"
+                  "// 4*10^6, ...), both directions. Threads per line = N / the largest radix;\n"
+                  "// columns: up to 32 per block within 150 KiB, odd LDS stride; rows: up to 16\n"
+                  "// per block (128-byte transposed stores), the rows' pad rule.\n")
+HEADS['kf_round_fs_f32'] = HEADS_ROUND_FS.format(p='f32')
+HEADS['kf_round_fs_f64'] = HEADS_ROUND_FS.format(p='f64')
 HEADS['kf_round_real_f32'] = HEADS_ROUND_REAL.format(p='f32')
 HEADS['kf_round_real_f64'] = HEADS_ROUND_REAL.format(p='f64')
 HEADS['kf_round_nd_f32'] = HEADS_ROUND_ND.format(p='f32')
@@ -515,14 +580,15 @@ HEADS['kf_round_nd_f64'] = HEADS_ROUND_ND.format(p='f64')
 HEADS['kf_round_f32'] = HEADS_ROUND.format(p='f32')
 HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 
-FUNCS = {'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
+FUNCS = {'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
+         'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
          'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
          'kf_round_f32': 'fixed_table_round_f32', 'kf_round_f64': 'fixed_table_round_f64', 'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
 
 
 def roles(kind, col):
     """(direction, nontemporal input, nontemporal output) registered."""
-    if kind == "FS_A":
+    if kind in ("FS_A", "FS_B"):
         return [(-1, False, False), (1, False, False)]
     if kind == "R2C_HALF":
         return [(-1, True, True), (-1, True, False)]
@@ -602,6 +668,9 @@ if __name__ == "__main__":
                     if int(m.group(3)) == prec:
                         have.add((m.group(1), int(m.group(4)), m.group(5) == "true"))
             rows = nd_rows(prec, have)
+            print(name, "matches" if rows == TABLES[name] else "DIFFERS", rows, flush=True)
+        for prec, name in ((0, "kf_round_fs_f32"), (1, "kf_round_fs_f64")):
+            rows = fourstep_rows(prec, registered_keys(prec, skip=(name,)))
             print(name, "matches" if rows == TABLES[name] else "DIFFERS", rows, flush=True)
     else:
         print(__doc__)
