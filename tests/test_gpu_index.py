@@ -199,7 +199,9 @@ def test_four_step_chunks_and_lanes(idx_ctx):
     assert len(d["passes"]) == 2 * 6
 
 
-@pytest.mark.parametrize("n,prec", [(4099, F32), (65537, F32), (12289, F64), (20011, F32)])
+@pytest.mark.parametrize("n,prec", [(4099, F32), (65537, F32), (12289, F64), (20011, F32),
+                                    # one-kernel fixed rows: M = 256 (four lines per block), 5184, 16384, 1323, 8192
+                                    (103, F32), (2309, F32), (6131, F32), (659, F64), (4093, F64)])
 def test_bluestein(idx_ctx, n, prec):
     alg, _ = vk.planner_axis(n, 4, prec)
     if alg != vk.AlgorithmKind.Bluestein:

@@ -293,6 +293,41 @@ def test_bluestein_f64(hip_ctx, n):
     assert o.rel_l2(y, ref) <= max(1e-13, 2 * o.rel_l2(ref, npref))
 
 
+# A prime per convolution length M of the one-kernel Bluestein rows
+# (kf_blue_rows_*): the planner's padding tables give that M for the prime.
+BLUE_PRIMES = {F32: {103: 256, 137: 512, 263: 625, 317: 768, 389: 1024, 523: 1296, 653: 2048, 1031: 2187,
+                     1097: 2304, 1163: 2500, 1259: 2592, 1303: 3072, 1543: 3125, 1567: 3136, 1571: 4096,
+                     2053: 4375, 2203: 4608, 2309: 5184, 2609: 6561, 3299: 8192, 6131: 16384},
+               F64: {239: 512, 311: 625, 317: 640, 373: 750, 383: 768, 431: 875, 509: 1024, 647: 1296, 659: 1323,
+                     743: 1512, 887: 1792, 997: 2016, 1021: 2048, 1091: 2187, 1567: 3136, 1709: 3430, 1789: 3584,
+                     2039: 4096, 2153: 4375, 2239: 4480, 2351: 4704, 2551: 5103, 2687: 5376, 3023: 6048,
+                     3067: 6144, 4093: 8192}}
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_bluestein_fixed_rows(hip_ctx, prec):
+    """Primes whose Bluestein convolution length has a fixed one-kernel row
+    shape run on it (bluestein_ir.rs's single-upload path), forward and
+    inverse. f32 against the oracle; f64 against pocketfft at 1e-13 and against
+    the oracle within twice the oracle's own distance from pocketfft."""
+    for n, m in BLUE_PRIMES[prec].items():
+        batch = 3
+        x = rand(n * batch, n + 11, prec)
+        y, ir = c2c(hip_ctx, [n], batch, x, prec)
+        desc = hip_ctx.plan(ir).describe()
+        assert desc["bluestein"]["m"] == m, (n, desc["bluestein"])
+        assert desc["passes"][0]["kernel"] == "bluestein_single" and desc["passes"][0]["fixed_shape"], n
+        ref = oracle_c2c(x, n)
+        if prec == F32:
+            assert o.rel_l2(y, ref) <= TOL[F32], n
+        else:
+            npref = np.fft.fft(x.reshape(batch, n), axis=1).reshape(-1)
+            assert o.rel_l2(y, npref) <= 1e-13, n
+            assert o.rel_l2(y, ref) <= max(1e-13, 2 * o.rel_l2(ref, npref)), n
+        z, _ = c2c(hip_ctx, [n], batch, y, prec, INV, normalize=True)
+        assert o.rel_l2(z, x) <= 4 * TOL[prec], n
+
+
 # -------------------------------------------------------------- R2C / C2R
 
 def r2c(ctx, n, batch, x, prec=F32):

@@ -19,7 +19,7 @@ def _gen():
 @pytest.mark.parametrize("name", ["kf_pow2_f32", "kf_pow2_f64", "kf_fam_f32", "kf_fam_f64", "kf_real_rows_f32",
                                   "kf_real_rows_f64", "kf_round_f32", "kf_round_f64", "kf_round_nd_f32",
                                   "kf_round_nd_f64", "kf_round_real_f32", "kf_round_real_f64",
-                                  "kf_round_fs_f32", "kf_round_fs_f64"])
+                                  "kf_round_fs_f32", "kf_round_fs_f64", "kf_blue_rows_f32", "kf_blue_rows_f64"])
 def test_tables_match_generator(name):
     g = _gen()
     assert open(os.path.join(CSRC, name + ".hip")).read() == g.render(name)

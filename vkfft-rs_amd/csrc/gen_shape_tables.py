@@ -3,7 +3,7 @@ kf_real_rows_*.hip): the shape lists, the LDS bank-conflict model that chose
 each shape's LDS line stride LS and pad shift PS, and the emitter of the
 registration files.
 
-    python3 gen_shape_tables.py emit      # rewrite the fourteen kf_*.hip tables
+    python3 gen_shape_tables.py emit      # rewrite the sixteen kf_*.hip tables
     python3 gen_shape_tables.py check     # re-run the model search per shape
     python3 gen_shape_tables.py round     # re-derive the round-length rows by rule
 
@@ -361,7 +361,7 @@ ROUND = [200, 240, 300, 400, 480, 500, 600, 720, 750, 800, 900, 960, 1200, 1500,
 RADICES = (16, 12, 10, 9, 8, 6, 5, 4, 3, 2)
 
 
-def radix_plan(n):
+def radix_plan(n, radices=RADICES):
     """Fewest stages, then the largest smallest radix, then the largest first radix."""
     best = None
 
@@ -375,8 +375,8 @@ def radix_plan(n):
             return
         if len(acc) >= 5:
             return
-        for i in range(start, len(RADICES)):
-            r = RADICES[i]
+        for i in range(start, len(radices)):
+            r = radices[i]
             if rest % r == 0:
                 rec(rest // r, i, acc + [r])
 
@@ -513,6 +513,40 @@ def fourstep_rows(prec, have):
     return rows
 
 
+# The planner's most frequent Bluestein convolution lengths (the padded M of
+# the primes up to 8200 that run as Bluestein: 16384, 8192, 6561, 4096, ...)
+# Convolution lengths M >= 256 that the planner's Bluestein padding tables
+# give (f32: the AMD f32 table plus 16384, which the generic padding gives for
+# lengths 4097-8192; f64: the wide table), keeping those with a plan of
+# radices 2-16.
+BLUE_M = {0: [256, 512, 625, 768, 1024, 1296, 2048, 2187, 2304, 2500, 2592, 3072, 3125, 3136, 4096, 4375, 4608,
+              5184, 6561, 8192, 16384],
+          1: [256, 270, 512, 625, 640, 750, 756, 768, 875, 1024, 1296, 1323, 1344, 1512, 1792, 2016, 2048, 2187,
+              3136, 3430, 3584, 4096, 4375, 4480, 4704, 5103, 5376, 6048, 6144, 8192]}
+
+
+def blue_rows(prec):
+    """One-kernel Bluestein rows (chirp multiply, FFT of M, spectrum multiply
+    fused into its last stage, inverse FFT, chirp multiply and truncation):
+    the rule's radix plan, threads per line = M / the largest radix, about 256
+    threads per block, the rows' pad rule (one slot per 16 f32 / 8 f64)."""
+    eb = 16 if prec else 8
+    ps = 3 if prec else 4
+    rows = []
+    for m in BLUE_M[prec]:
+        rad = radix_plan(m, (16, 12, 10, 9, 8, 7, 6, 5, 4, 3, 2))
+        tt = m // max(rad)
+        ls = m + (m >> ps)
+        ls += 1 - ls % 2
+        if tt > 1024 or ls * eb > 156 * 1024:
+            continue
+        G = max(1, min(64, 256 // tt))
+        while G > 1 and (G * ls * eb > 80 * 1024 or G * tt > 1024):
+            G -= 1
+        rows.append(('BLUE_1', 'Blue1', m, tt, G, False, rad, ps, ls))
+    return rows
+
+
 HEADS_ROUND = ("// Fixed shapes of round lengths with factors 2, 3 and 5 outside the\n"
                "// power-of-two, 3*2^k and 5*2^k families, {p}: one-upload rows (1-D batches\n"
                "// and the contiguous axis of N-D transforms) in both directions and both\n"
@@ -561,6 +595,16 @@ HEADS_ROUND_REAL = ("// Fixed shapes of the one-upload even-length real transfor
                     "// threads, lines per block and LDS strides as those rows. R2C is registered\n"
                     "// for the caller's input with or without the caller's output, C2R for the\n"
                     "// caller's output with or without the caller's input.\n")
+TABLES['kf_blue_rows_f32'] = blue_rows(0)
+TABLES['kf_blue_rows_f64'] = blue_rows(1)
+HEADS_BLUE = ("// Fixed shapes of the one-kernel Bluestein transform, {p}, for the planner's\n"
+              "// most frequent convolution lengths M (the padded lengths of the primes up\n"
+              "// to 8200 that run as Bluestein), forward FFT direction, streamed input and\n"
+              "// output. Radix plans with the fewest stages from radices 2-16; threads per\n"
+              "// line = M / the largest radix; about 256 threads per block; one LDS pad\n"
+              "// slot per 16 (f32) / 8 (f64) elements.\n")
+HEADS['kf_blue_rows_f32'] = HEADS_BLUE.format(p='f32')
+HEADS['kf_blue_rows_f64'] = HEADS_BLUE.format(p='f64')
 # fourstep_rows(0 / 1, registered_keys(0 / 1)) before these tables existed
 TABLES['kf_round_fs_f32'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 4, 137), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 4, 255), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 4, 265), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 4, 273), ('FS_A', 'FsA', 400, 25, 32, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 4, 425), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 4, 531), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 4, 545), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 4, 1063), ('FS_A', 'FsA', 1024, 64, 16, True, [16, 8, 8], 30, 1025), ('FS_A', 'FsA', 2000, 125, 8, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 8, False, [16, 5, 5, 5], 4, 2125), ('FS_A', 'FsA', 2048, 128, 8, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 8, False, [16, 16, 8], 4, 2177)]
 TABLES['kf_round_fs_f64'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 3, 145), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 3, 271), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 3, 281), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 3, 289), ('FS_A', 'FsA', 400, 25, 16, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 3, 451), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 3, 563), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 3, 577), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 3, 1125), ('FS_A', 'FsA', 1024, 64, 8, True, [16, 8, 8], 30, 1025), ('FS_B', 'FsB', 1024, 64, 8, False, [16, 8, 8], 3, 1153), ('FS_A', 'FsA', 2000, 125, 4, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 4, False, [16, 5, 5, 5], 3, 2251), ('FS_A', 'FsA', 2048, 128, 4, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 4, False, [16, 16, 8], 3, 2305)]
@@ -580,7 +624,8 @@ HEADS['kf_round_nd_f64'] = HEADS_ROUND_ND.format(p='f64')
 HEADS['kf_round_f32'] = HEADS_ROUND.format(p='f32')
 HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 
-FUNCS = {'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
+FUNCS = {'kf_blue_rows_f32': 'fixed_table_blue_rows_f32', 'kf_blue_rows_f64': 'fixed_table_blue_rows_f64',
+         'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
          'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
          'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
          'kf_round_f32': 'fixed_table_round_f32', 'kf_round_f64': 'fixed_table_round_f64', 'kf_pow2_f32': 'fixed_table_pow2_f32', 'kf_pow2_f64': 'fixed_table_pow2_f64', 'kf_fam_f32': 'fixed_table_fam_f32', 'kf_fam_f64': 'fixed_table_fam_f64', 'kf_real_rows_f32': 'fixed_table_real_rows_f32', 'kf_real_rows_f64': 'fixed_table_real_rows_f64'}
@@ -588,6 +633,8 @@ FUNCS = {'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixe
 
 def roles(kind, col):
     """(direction, nontemporal input, nontemporal output) registered."""
+    if kind == "BLUE_1":
+        return [(-1, True, True)]
     if kind in ("FS_A", "FS_B"):
         return [(-1, False, False), (1, False, False)]
     if kind == "R2C_HALF":

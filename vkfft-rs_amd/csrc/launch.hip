@@ -31,6 +31,8 @@ const FixedKernel* fixed_table_round_real_f32(int* count);
 const FixedKernel* fixed_table_round_real_f64(int* count);
 const FixedKernel* fixed_table_round_fs_f32(int* count);
 const FixedKernel* fixed_table_round_fs_f64(int* count);
+const FixedKernel* fixed_table_blue_rows_f32(int* count);
+const FixedKernel* fixed_table_blue_rows_f64(int* count);
 
 // All registered fixed-shape instantiations, merged once (thread-safe
 // static initialisation).
@@ -46,7 +48,8 @@ static const FixedKernel* registry(int* count) {
                                                 fixed_table_real_rows_f64, fixed_table_round_f32, fixed_table_round_f64,
                                                 fixed_table_round_nd_f32, fixed_table_round_nd_f64,
                                                 fixed_table_round_real_f32, fixed_table_round_real_f64,
-                                                fixed_table_round_fs_f32, fixed_table_round_fs_f64};
+                                                fixed_table_round_fs_f32, fixed_table_round_fs_f64,
+                                                fixed_table_blue_rows_f32, fixed_table_blue_rows_f64};
         constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
         int counts[kTables], sum = 0;
         const FixedKernel* ptrs[kTables];
