@@ -218,6 +218,9 @@ struct IoPlain {
     // direct first stage: load_tw(e, w) with w = ltw_root(b) * ltw_root(NB, step)^i for e = b + i*NB
     static constexpr bool kLoadTw = false;
     static constexpr bool kStoreTw = false;  // store multiplies by a per-element pass twiddle
+    // direct first stage of a C2R column pass over mirror-pair blocks that
+    // loads each pair (X[k], X[M-k]) once for two butterflies (fstage_c2r_pairs)
+    static constexpr bool kPairFirst = false;
     static constexpr int kLoad = LAY_ANY;
     static constexpr int kStore = LAY_ANY;
     // elements at or beyond kZeroFrom(N) of a length-N line are known zeros
@@ -585,6 +588,13 @@ struct IoFsAC2R : IoFsA {
 struct IoFsAC2RDirect : IoFsAC2R {
     static constexpr int kLoad = LAY_COL;
     static constexpr bool kLoadTw = true;
+    static constexpr bool kPairFirst = true;
+    // the block holding column 0 and the stand-in column N2/2, whose pairs
+    // differ from the regular (c, e) <-> (N2 - c, N1-1-e); g = this line's
+    // slot, H = G/2 (the same answer on every thread of a block)
+    static __device__ __forceinline__ bool pair_special(const KArgs& a, const LineInfo& L, int g, int H) {
+        return g < H ? L.c == g : g == H ? L.c == a.N2 / 2 : L.c == a.N2 - (g - H);
+    }
     // root(c + b*N2) for butterfly b; the step NB advances k by NB*N2
     template <typename T>
     static __device__ __forceinline__ cpx<T> ltw_root(const KArgs& a, const LineInfo& L, int m, bool step = false) {
@@ -1312,6 +1322,49 @@ constexpr int stage_pad() {
                                                                          : 30;
 }
 
+// First stage of a C2R column pass over mirror-pair blocks (KF_MIRROR_PAIRS):
+// line g < H holds column c, line g + H its mirror N2 - c, and element e of
+// column c pairs with element N1-1-e of the mirror (X[M-k] for k = c + e*N2).
+// Thread t of line g runs butterfly t of its own line and butterfly NB-1-t
+// of the mirror line: the R pairs (X[k], X[M-k]) it loads for the first are,
+// in reverse order, the inputs of the second, so every element is read once
+// and each pair gives Z[k] and Z[M-k] from one twiddle (w_(M-k) = -conj w_k).
+template <typename T, int S, class IO, class Sh, int R, int PSO>
+__device__ __forceinline__ void fstage_c2r_pairs(const KArgs& a, cpx<T>* line, const LineInfo& L, int t) {
+    constexpr int NB = Sh::N / R, H = Sh::G / 2;
+    static_assert(Sh::COL && Sh::G % 2 == 0 && NB == 2 * Sh::TT, "mirror-pair first stage geometry");
+    const int g = threadIdx.x % Sh::G;
+    cpx<T>* mline = line + (g < H ? H : -H) * Sh::LS;
+    cpx<T> v[R], u[R];
+    if (L.valid) {
+        const cpx<T>* in = (const cpx<T>*)a.in;
+        const cpx<T>* xm = in + L.o * a.in_os + (a.M - L.c);  // X[M-k] = xm[-e*N2]
+        const cpx<T> wb = IO::template ltw_root<T>(a, L, t);
+        cpx<T> sp[R];
+        root_powers<R>(IO::template ltw_root<T>(a, L, NB, true), sp);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int e = t + i * NB;
+            const cpx<T> A = ldg_in<Sh::NTI>(a, in + L.ib + e * a.in_es);
+            const cpx<T> B = ldg_in<Sh::NTI>(a, xm - (long long)e * a.N2);
+            const cpx<T> w = cmul(wb, sp[i]);
+            v[i] = (A + conj(B)) + muli<1>(cmulc(A - conj(B), w));
+            u[R - 1 - i] = (B + conj(A)) + muli<1>(cmulc(B - conj(A), mk(-w.re, w.im)));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < R; ++i) v[i] = u[i] = zero<T>();
+    }
+    dft<R, S>(v);
+    dft<R, S>(u);
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+        line[lds_out<PSO, 1, R>(t * R, q)] = v[q];
+        mline[lds_out<PSO, 1, R>((NB - 1 - t) * R, q)] = u[q];
+    }
+    __syncthreads();
+}
+
 // TO: offset of this stage's block in the per-stage twiddle table (stages
 // with P > 1 hold P (R - 1) entries each, in radix order). PSI: pad of the
 // buffer the stage reads.
@@ -1321,8 +1374,20 @@ __device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, cpx<T>* al
                                         const StageTw& tw, RList<R, Rest...>) {
     constexpr bool last = sizeof...(Rest) == 0;
     constexpr int PSO = !Sh::SPAD ? Sh::PS : last ? 30 : stage_pad<Sh::N, P, R, rlist_head(RList<Rest..., 0>{})>();
-    fstage<T, S, IO, Sh::N, P, R, Sh::TT, PSI, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO,
-           last && MIDL && !DSTL, Sh::PP, Sh::TWT ? TO : -1, PSO>(a, line, alt, L, t, tw);
+    constexpr bool kPairs = IO::kPairFirst && P == 1 && SRC0 && !last && !Sh::PP && !Sh::SPAD && Sh::COL &&
+                            Sh::N / R == 2 * Sh::TT;
+    if constexpr (kPairs) {
+        if ((a.flags & KF_MIRROR_PAIRS) && (a.flags & KF_PAIR_LOADS) &&
+            !IO::pair_special(a, L, (int)(threadIdx.x % Sh::G), Sh::G / 2)) {
+            fstage_c2r_pairs<T, S, IO, Sh, R, PSO>(a, line, L, t);
+        } else {
+            fstage<T, S, IO, Sh::N, P, R, Sh::TT, PSI, SRC0, 0, Sh::NTI, Sh::NTO, false, false, -1, PSO>(a, line, alt,
+                                                                                                       L, t, tw);
+        }
+    } else {
+        fstage<T, S, IO, Sh::N, P, R, Sh::TT, PSI, (P == 1 ? SRC0 : 0), (last ? DSTL : 0), Sh::NTI, Sh::NTO,
+               last && MIDL && !DSTL, Sh::PP, Sh::TWT ? TO : -1, PSO>(a, line, alt, L, t, tw);
+    }
     if constexpr (!last)
         fstages<T, S, IO, Sh, SRC0, DSTL, MIDL, P * R, TO + (P > 1 ? P * (R - 1) : 0), PSO>(
             a, Sh::PP ? alt : line, Sh::PP ? line : alt, L, t, tw, RList<Rest...>{});

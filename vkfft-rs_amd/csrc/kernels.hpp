@@ -56,6 +56,9 @@ enum KFlags : int {
     KF_NARROW_OUT = 2048,
     KF_ZERO_IN = 4096,
     KF_ZERO_OUT = 8192,
+    // with KF_MIRROR_PAIRS: the direct first stage loads each (X[k], X[M-k])
+    // once for a butterfly of the column and one of its mirror
+    KF_PAIR_LOADS = 16384,
 };
 
 // Butterflies per thread in one radix-R stage of the runtime-shape kernel

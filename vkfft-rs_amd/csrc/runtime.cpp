@@ -2002,6 +2002,12 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     if (!ga.ok || !gb.ok) return plan_real_full_complex(c, n, batch, false, normalize);
     // columns beside their mirrors in one block when the groups tile N2 evenly
     const bool pairs = ga.G % 2 == 0 && n2 % 2 == 0 && n2 % (size_t)ga.G == 0;
+    // fixed shapes whose first stage can take the pair loads use them
+    // (VKFX_C2R_PAIR_LOADS=0: every element reads X[k] and X[M-k] itself)
+    static const bool pair_loads = [] {
+        const char* e = getenv("VKFX_C2R_PAIR_LOADS");
+        return !(e && e[0] == '0');
+    }();
     const void *tlo, *thi;
     int tsh;
     rc = two_level(p, M, prec, &tlo, &thi, &tsh);
@@ -2020,7 +2026,7 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
         a.tlo = tlo, a.thi = thi, a.tshift = tsh;
         a.rlo = rlo, a.rhi = rhi, a.rshift = rsh;
         a.M = (long long)M, a.N1 = (long long)n1, a.N2 = (long long)n2;
-        if (pairs) a.flags |= KF_MIRROR_PAIRS;
+        if (pairs) a.flags |= KF_MIRROR_PAIRS | (pair_loads ? KF_PAIR_LOADS : 0);
         long long lines = (long long)(cb * n2);
         rc = add_launch(c, KK_FS_A_C2R, 1, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * h * cs, SEL_WORK, 0,
                         "c2r_columns_pre");
