@@ -324,7 +324,9 @@ def test_bluestein_fixed_rows(hip_ctx, prec):
             npref = np.fft.fft(x.reshape(batch, n), axis=1).reshape(-1)
             assert o.rel_l2(y, npref) <= 1e-13, n
             assert o.rel_l2(y, ref) <= max(1e-13, 2 * o.rel_l2(ref, npref)), n
-        z, _ = c2c(hip_ctx, [n], batch, y, prec, INV, normalize=True)
+        z, iir = c2c(hip_ctx, [n], batch, y, prec, INV, normalize=True)
+        idesc = hip_ctx.plan(iir).describe()
+        assert idesc["passes"][0]["kernel"] == "bluestein_single" and idesc["passes"][0]["fixed_shape"], n
         assert o.rel_l2(z, x) <= 4 * TOL[prec], n
 
 

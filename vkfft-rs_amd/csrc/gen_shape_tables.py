@@ -599,8 +599,10 @@ TABLES['kf_blue_rows_f32'] = blue_rows(0)
 TABLES['kf_blue_rows_f64'] = blue_rows(1)
 HEADS_BLUE = ("// Fixed shapes of the one-kernel Bluestein transform, {p}, for the planner's\n"
               "// most frequent convolution lengths M (the padded lengths of the primes up\n"
-              "// to 8200 that run as Bluestein), forward FFT direction, streamed input and\n"
-              "// output. Radix plans with the fewest stages from radices 2-16; threads per\n"
+              "// to 8200 that run as Bluestein), streamed input and output. The kernel\n"
+              "// always runs its forward FFT first; the transform direction lives in the\n"
+              "// chirp and kernel-spectrum tables, so one entry serves both directions.\n"
+              "// Radix plans with the fewest stages from radices 2-16; threads per\n"
               "// line = M / the largest radix; about 256 threads per block; one LDS pad\n"
               "// slot per 16 (f32) / 8 (f64) elements.\n")
 HEADS['kf_blue_rows_f32'] = HEADS_BLUE.format(p='f32')
