@@ -58,8 +58,9 @@ def test_null_arguments_are_rejected():
 
 
 def test_integration_rust_extern_block_declares_every_symbol():
-    """The Rust binding shown in INTEGRATION.md declares every function of
-    include/vkfx.h, so a maintainer copying it has the whole ABI."""
+    """The Rust `extern "C"` block of the integration guide at the repository
+    root declares every function of include/vkfx.h, so a maintainer copying
+    it has the whole ABI."""
     import re
     text = open(os.path.join(os.path.dirname(vk.HEADER_PATH), "..", "INTEGRATION.md")).read()
     block = text[text.index('extern "C" {'):]

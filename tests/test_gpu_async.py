@@ -191,7 +191,7 @@ def test_pass_resource_reports(hip_ctx):
 
 
 def _shim_ticket_wait(ctx, ir, x):
-    """What the Rust shim's Mi355xTicket32/64 does: submit the
+    """What the reference-side Rust shim's Mi355xTicket32/64 does: submit the
     plan's input bytes, size the wait buffer from vkfx_plan_output_info's
     widened bytes as Complex32/64 elements, wait with exactly that byte count
     and hand the complex vector on (finish_transform_output32/64 then takes
