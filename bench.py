@@ -6,9 +6,12 @@ A step is one execute of the plan over one batch. Buffers rotate over 8
 input/output pairs (1 GiB) so the 256 MB Infinity Cache cannot hold the
 working set between steps.
 
-  value      = algorithmic bytes (2 * N * batch * 8) / average step time, GB/s
+  value      = algorithmic bytes (2 * N * batch * 8) / average step time, GB/s;
+               the step time is the host clock between the synchronizes that
+               bracket the K timed steps (no timing event in that region)
   roofline   = the dominant kernel's algorithmic bytes / its average launch
-               duration (HIP events on the launch stream) against 8 TB/s
+               duration (HIP events on the launch stream, over a second run of
+               the K steps) against 8 TB/s
   cpu_baseline = the oracle (a port of vkfft-rs src/reference.rs) timed on
                this host's cores over a bounded sample of the same workload
 
@@ -130,19 +133,29 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
 
     for i in range(warmup):
         step(i)
+    # The timed region: the host clock between two synchronizes around exactly
+    # `steps` steps. No timing event sits in it: with HIP timing events in the
+    # stream the same launches run slower (C1: 27-29 us against 24.5-25.5 us
+    # per step on one box), so the events that time the kernel for the
+    # roofline run over a second pass of the same steps below.
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
+    t0 = time.perf_counter()
     for i in range(steps):
         step(i)
-    end.record(stream)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    # per-launch durations of the dominant (first) kernel, events around single launches
+    total_ms = (time.perf_counter() - t0) * 1e3
+    # per-launch durations of the dominant (first) kernel from HIP events on
+    # the launch stream
     launches = [p.describe() for p in plans]
     per_launch = []
     if len(plans[0].describe()["passes"]) == 1 and len(plans) == 1:
-        per_launch = [total_ms / steps]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            step(i)
+        end.record(stream)
+        torch.cuda.synchronize()
+        per_launch = [start.elapsed_time(end) / steps]
     else:
         evs = []
         for i in range(min(steps, 20)):
@@ -516,7 +529,8 @@ def main():
             ach = dom_bytes / (launch_ms * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(cfg["workload"]),
-                    "kernel": first[0]["kernel"], "launch_ms": round(launch_ms, 5)}
+                    "kernel": first[0]["kernel"], "launch_ms": round(launch_ms, 5),
+                    "timing": "HIP events over a second run of the timed steps"}
         out = {
             "metric": METRICS[name],
             "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
