@@ -6,25 +6,35 @@ A step is one execute of the plan over one batch. Buffers rotate over 8
 input/output pairs (1 GiB) so the 256 MB Infinity Cache cannot hold the
 working set between steps.
 
-  value      = algorithmic bytes (2 * N * batch * 8) / average step time, GB/s;
+Every configuration is timed the same way, after max(3, --warmup) untimed
+steps, over three runs of the same K = max(20, --steps) steps:
+
+  value      = algorithmic bytes (2 * N * batch * 8) / mean step time, GB/s;
                the step time is the host clock between the synchronizes that
-               bracket the K timed steps (no timing event in that region)
-  roofline   = the dominant kernel's algorithmic bytes / its average launch
-               duration (HIP events on the launch stream, over a second run of
-               the K steps) against 8 TB/s
+               bracket the K steps (no timing event in that region)
+  ms_per_step_median = median of 20 host-clocked blocks of B steps each
+               (B: about 2 ms of work per block), a per-step figure robust to
+               outliers (a HIP event pair around each step slows the launches
+               it brackets, so none is used)
+  roofline   = the dominant kernel's algorithmic bytes per launch / its mean
+               duration, from HIP events bound to each kernel dispatch
+               (vkfx_plan_timing_start: hipExtLaunchKernel begin/end, the
+               durations a rocprofv3 kernel trace reports, without the gaps
+               between launches), against 8 TB/s; `traffic` is that kernel's
+               HBM bytes per launch from the committed rocprofv3 counters
   cpu_baseline = the oracle (a port of vkfft-rs src/reference.rs) timed on
                this host's cores over a bounded sample of the same workload
 
-The default line also carries `configs`: every BASELINE configuration
-(C1-C5b) timed in the same process (5 steps each after 2 warmups), with its
-effective GB/s, % of 8 TB/s, HBM sweeps per step and the relative L2 error of a
+The default line also carries `configs`: every other BASELINE configuration
+(C2-C5b) timed in the same process by the same protocol, each with its own
+roofline, HBM sweeps per step, CPU baseline and the relative L2 error of a
 sampled slice of its timed output against the oracle. `accuracy` is the same
 check for the headline's timed output (plus the sample-11 metrics of
 vkfft-rs src/precision.rs:31-101).
 
---config selects another benchmark configuration (c2, c3, c4, c5a, c5b) for
-measurement runs; --all prints one line per config; --headline-only skips
-the `configs` field.
+--config selects another benchmark configuration (c2, c3, c4, c5a, c5b,
+c5a_rader) for measurement runs; --all prints one line per config;
+--headline-only skips the `configs` field.
 """
 from __future__ import annotations
 
@@ -51,7 +61,13 @@ CONFIGS = {
                 prec="f32"),
     "c5b": dict(workload="1d_c2c_fwd_f32_n65537_b4096_bluestein", dims=[65537], batch=4096, kind="c2c",
                 prec="f32"),
+    # C5a's length under PlannerTuning::with_recursive_fft_rader (planner.rs:414-422):
+    # the FFT-Rader tree 4099 -> 4098 = 2 * 3 * 683 instead of Bluestein
+    "c5a_rader": dict(workload="1d_c2c_fwd_f32_n4099_b4096_rader", dims=[4099], batch=4096, kind="c2c",
+                      prec="f32", recursive_rader=True),
 }
+# BASELINE.json's configurations (the others are extra measurement runs)
+BASELINE_CONFIGS = ["c1", "c2", "c3", "c4", "c5a", "c5b"]
 
 
 # The metric of the default workload; the other configs report the
@@ -63,6 +79,7 @@ METRICS = {
     "c4": "f64 3-D C2C effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
     "c5a": "batched f32 C2C (Bluestein axis) effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
     "c5b": "batched f32 C2C (Bluestein axis) effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
+    "c5a_rader": "batched f32 C2C (Rader axis) effective HBM GB/s and % of peak; GFLOP/s (5NlogN); 1 GPU",
 }
 
 
@@ -90,15 +107,30 @@ def build_plans(vk, ctx, cfg):
                                  .with_transform(vk.TransformKind.ComplexToReal).with_inverse_normalization(True),
                                  vk.Direction.Inverse)
         return [ctx.plan(f), ctx.plan(i)]
-    ir = vk.TransformIr.build(vk.FftConfig.new(cfg["dims"]).with_batch_count(cfg["batch"]).with_precision(prec),
-                              vk.Direction.Forward)
+    c = vk.FftConfig.new(cfg["dims"]).with_batch_count(cfg["batch"]).with_precision(prec)
+    if cfg.get("recursive_rader"):
+        c.allow_recursive_fft_rader = True
+    ir = vk.TransformIr.build(c, vk.Direction.Forward)
     return [ctx.plan(ir)]
 
 
 def run_gpu(cfg, steps, warmup, rotate, check=None):
-    """Times `steps` steps after `warmup` untimed ones; returns (ms per step,
-    ms per launch of the first plan, info). `check(bufs, pairs, steps)` runs
-    on the timed output before the buffers are released."""
+    """Times one configuration: `warmup` untimed steps, then three runs of
+    the same `steps` steps. Returns a dict with
+      ms_mean    host clock between the synchronizes around run 1 / steps
+                 (no timing event in that region: HIP timing events in the
+                 stream slow the launches around them);
+      block_ms   run 2: mean step time of each of 20 host-clocked blocks of
+                 block_steps steps (a HIP event pair around every step slows
+                 the launches of every step it brackets, 10-15% for the
+                 multi-pass configs and 2x for C1, so none is used);
+      kernels    run 3: per-pass kernel durations from HIP events bound to
+                 each FFT kernel dispatch (vkfx_plan_timing_start), one list
+                 per plan; with --profile-region, run 3 is the region a
+                 `rocprofv3 --selected-regions` trace collects;
+      info       device, plan descriptions, buffer pairs, accuracy.
+    `check(bufs, pairs, steps)` runs on the timed output before the buffers
+    are released."""
     import torch
 
     torch.cuda.init()  # torch's HIP runtime first: the library then binds to the same one
@@ -133,49 +165,129 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
 
     for i in range(warmup):
         step(i)
-    # The timed region: the host clock between two synchronizes around exactly
-    # `steps` steps. No timing event sits in it: with HIP timing events in the
-    # stream the same launches run slower (C1: 27-29 us against 24.5-25.5 us
-    # per step on one box), so the events that time the kernel for the
-    # roofline run over a second pass of the same steps below.
+    # run 1: host clock, no event in the region
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         step(i)
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) * 1e3
-    # per-launch durations of the dominant (first) kernel from HIP events on
-    # the launch stream
+    # run 2: 20 host-clocked blocks of B steps (B chosen so a block holds
+    # about 2 ms of work), for the median per-step time; a synchronize ends
+    # each block, so its cost is spread over the block
+    per_step = total_ms / steps
+    B = max(1, int(math.ceil(2.0 / max(per_step, 1e-3))))
+    block_ms = []
+    for blk in range(MEDIAN_BLOCKS):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(B):
+            step(blk * B + i)
+        torch.cuda.synchronize()
+        block_ms.append((time.perf_counter() - t0) * 1e3 / B)
+    # run 3: kernel durations from events bound to each dispatch
     launches = [p.describe() for p in plans]
-    per_launch = []
-    if len(plans[0].describe()["passes"]) == 1 and len(plans) == 1:
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(steps):
-            step(i)
-        end.record(stream)
-        torch.cuda.synchronize()
-        per_launch = [start.elapsed_time(end) / steps]
-    else:
-        evs = []
-        for i in range(min(steps, 20)):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            x, y, _ = bufs[i % pairs]
-            a.record(stream)
-            plans[0].execute(x.data_ptr(), y.data_ptr(), 0, s)
-            b.record(stream)
-            evs.append((a, b))
-        torch.cuda.synchronize()
-        per_launch = [a.elapsed_time(b) for a, b in evs]
+    for p, d in zip(plans, launches):
+        p.timing_start(steps * max(1, len(d.get("passes", []))))
+    _profile_region(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    _profile_region(False)
+    kernels = [p.timing_stop() for p in plans]
     info = {"device": ctx.device_name(), "profile": ctx.device_profile(), "plans": launches, "pairs": pairs}
     if check is not None:
-        # the last timed step's pair still holds its output (the per-launch
-        # timing above rewrote the same inputs' outputs with the same plan)
+        # the last timed step's pair holds its output (runs 2 and 3 rewrote
+        # the same inputs' outputs with the same plans)
         info["accuracy"] = check(bufs, pairs, steps)
     del bufs
     ctx.close()
     torch.cuda.empty_cache()
-    return total_ms / steps, sum(per_launch) / len(per_launch), info
+    return {"ms_mean": total_ms / steps, "block_ms": block_ms, "block_steps": B, "kernels": kernels, "info": info}
+
+
+MEDIAN_BLOCKS = 20
+_ROCTX = {"on": False, "lib": None}
+
+
+def _profile_region(begin):
+    """roctxProfilerResume / roctxProfilerPause around the kernel-timing run
+    (only with --profile-region), so that `rocprofv3 --selected-regions`
+    traces exactly the dispatches whose durations the roofline uses."""
+    if not _ROCTX["on"]:
+        return
+    import ctypes
+    if _ROCTX["lib"] is None:
+        _ROCTX["lib"] = ctypes.CDLL("librocprofiler-sdk-roctx.so.1")
+    (_ROCTX["lib"].roctxProfilerResume if begin else _ROCTX["lib"].roctxProfilerPause)(ctypes.c_uint64(0))
+
+
+# Pass label -> the IO policy its kernels are instantiated with (the
+# rocprofv3 kernel names carry it, with the line length of fixed shapes).
+PASS_IO = {
+    "stockham": ["IoPlain", "IoPlainStaged"], "stockham_columns": ["IoPlain", "IoPlainStaged"],
+    "split_axis_pass1": ["IoFsA"], "split_axis_pass2": ["IoPlain", "IoPlainStaged"],
+    "four_step_columns": ["IoFsA"], "four_step_rows": ["IoFsB"],
+    "r2c_columns": ["IoFsA"], "r2c_rows_post": ["IoFsBR2C"],
+    "c2r_columns_pre": ["IoFsAC2R", "IoFsAC2RDirect"], "c2r_rows": ["IoFsB"],
+    "bluestein_single": ["IoBlue1"], "bluestein_columns": ["IoFsABlue"], "bluestein_rows": ["IoBlueB"],
+    "bluestein_columns_out": ["IoFsCBlue"], "rader_fft": ["IoRader"], "rader_mixed": ["IoPlain"],
+}
+
+
+def pass_bytes(rec, cfg, plan_desc):
+    """Algorithmic HBM bytes of one launch of a pass: each line's elements
+    read once and written once. A Bluestein column pass faces the caller on
+    one side, where a line holds the logical N of its M points."""
+    es = 8 if cfg["prec"] == "f32" else 16
+    elems = rec["lines"] * rec["fft_len"]
+    if rec["pass"] == "bluestein_single":
+        n = cfg["dims"][0]
+        return 2 * rec["lines"] * n * es
+    if rec["pass"] in ("bluestein_columns", "bluestein_columns_out"):
+        m = _plan_m(plan_desc)
+        return int(elems * es * (1 + cfg["dims"][-1] / m))
+    return 2 * elems * es
+
+
+def dominant_kernel(kernels, plans, cfg):
+    """The pass (label, line length, lines per launch) with the largest total
+    kernel time over the timed steps, its mean launch duration and its
+    algorithmic bytes per launch."""
+    best = None
+    for recs, desc in zip(kernels, plans):
+        for r in recs:
+            if best is None or r["total_ms"] > best[0]["total_ms"]:
+                best = (r, desc)
+    if best is None:
+        return None
+    r, desc = best
+    total = sum(x["total_ms"] for recs in kernels for x in recs)
+    grid = None
+    for p in desc.get("passes", []):
+        if p.get("kernel") == r["pass"] and p.get("fft_len") == r["fft_len"] and p.get("lines") == r["lines"]:
+            grid = p["grid"] * p["block"]
+            break
+    return {"pass": r["pass"], "fft_len": r["fft_len"], "lines_per_launch": r["lines"], "launches": r["launches"],
+            "avg_ms": r["avg_ms"], "min_ms": r["min_ms"], "max_ms": r["max_ms"],
+            "share_of_kernel_time": round(r["total_ms"] / total, 4) if total else None,
+            "bytes_per_launch": pass_bytes(r, cfg, desc), "grid_threads": grid}
+
+
+def roofline_of(dom, workload):
+    if not dom or not dom["avg_ms"]:
+        return None
+    ach = dom["bytes_per_launch"] / (dom["avg_ms"] * 1e-3) / 1e9
+    traffic, kname = profiled_traffic(workload, dom["pass"], dom["fft_len"], dom.get("grid_threads"))
+    return {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "traffic_ratio": round(traffic / dom["bytes_per_launch"], 3) if traffic else None,
+            "kernel": dom["pass"], "fft_len": dom["fft_len"], "lines_per_launch": dom["lines_per_launch"],
+            "profile_kernel": kname, "grid_threads": dom["grid_threads"], "launch_ms": round(dom["avg_ms"], 5),
+            "launches": dom["launches"],
+            "bytes_per_launch": dom["bytes_per_launch"], "share_of_kernel_time": dom["share_of_kernel_time"],
+            "timing": "HIP events bound to each dispatch of the kernel (hipExtLaunchKernel begin/end), mean over "
+                      "the timed steps"}
 
 
 def plain_copy_bandwidth(nbytes=1 << 30, reps=10):
@@ -425,9 +537,11 @@ CALIBRATION_KERNEL = "k_copy16"
 
 def rocprof_summary(dirs, workload_kernel="vkfx"):
     """Markdown summary of rocprofv3 CSV output directories: kernel stats
-    (--kernel-trace --stats) and FETCH_SIZE / WRITE_SIZE (--pmc), the latter
-    per launch and scaled by what the same counter reads for the 1 GiB plain
-    copy that plain_copy_bandwidth() runs in the same process."""
+    (--kernel-trace --stats), the library's kernels per dispatch shape (name,
+    grid size) with their mean durations and scratch bytes from the kernel
+    trace, and FETCH_SIZE / WRITE_SIZE (--pmc) per dispatch shape, scaled by
+    what the same counter reads for the 1 GiB plain copy that
+    plain_copy_bandwidth() runs in the same process."""
     import csv
     import glob
     lines = []
@@ -441,46 +555,121 @@ def rocprof_summary(dirs, workload_kernel="vkfx"):
                 lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                              f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {r['Percentage']} |")
             lines.append("")
+        for f in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+            shapes = {}
+            for r in csv.DictReader(open(f)):
+                if workload_kernel not in r["Kernel_Name"] or CALIBRATION_KERNEL in r["Kernel_Name"]:
+                    continue
+                key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+                dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                shapes.setdefault(key, []).append((dur, int(r["Scratch_Size"]), int(r["VGPR_Count"])))
+            if shapes:
+                lines.append(f"### library kernels per dispatch shape ({os.path.basename(f)})\n")
+                lines.append("| kernel | grid threads | calls | avg us | min us | max us | VGPRs | scratch B/lane |")
+                lines.append("|---|---|---|---|---|---|---|---|")
+                for (k, g), v in sorted(shapes.items(), key=lambda kv: -sum(x[0] for x in kv[1])):
+                    ds = [x[0] for x in v]
+                    lines.append(f"| `{k[:110]}` | {g} | {len(v)} | {sum(ds) / len(ds):.2f} | {min(ds):.2f} | "
+                                 f"{max(ds):.2f} | {v[0][2]} | {v[0][1]} |")
+                lines.append("")
+                for (k, g), v in shapes.items():
+                    ds = [x[0] for x in v]
+                    lines.append(f"kernel_avg_us `{k[:90]}` grid={g}: {sum(ds) / len(ds):.4f}")
+                lines.append("")
         for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
             per = {}
             for r in csv.DictReader(open(f)):
-                key = (r["Kernel_Name"], r["Counter_Name"])
+                key = (r["Kernel_Name"], int(r["Grid_Size"]), r["Counter_Name"])
                 per.setdefault(key, []).append(float(r["Counter_Value"]))
-            for (k, c), v in per.items():
+            for (k, g, c), v in per.items():
                 if CALIBRATION_KERNEL in k:
-                    traffic.setdefault(c, {}).setdefault("copy", []).append((k, max(v)))
+                    traffic.setdefault(c, {}).setdefault("copy", []).append((k, g, max(v)))
                 elif workload_kernel in k:
-                    traffic.setdefault(c, {}).setdefault("fft", []).append((k, sum(v) / len(v)))
+                    traffic.setdefault(c, {}).setdefault("fft", []).append((k, g, sum(v) / len(v)))
     if traffic:
         lines.append("### HBM traffic per launch (rocprofv3 --pmc, KiB per dispatch)\n")
-        lines.append("| counter | kernel | raw KiB/launch | plain-copy raw KiB (1 GiB moved) | scaled bytes/launch |")
-        lines.append("|---|---|---|---|---|")
+        lines.append("| counter | kernel | grid threads | raw KiB/launch | plain-copy raw KiB (1 GiB moved) | "
+                     "scaled bytes/launch |")
+        lines.append("|---|---|---|---|---|---|")
         result = {}
         for c, tags in sorted(traffic.items()):
-            copy = [v for _, v in tags.get("copy", [])]
+            copy = [v for _, _, v in tags.get("copy", [])]
             ref = max(copy) if copy else None
-            for k, v in tags.get("fft", []):
+            for k, g, v in tags.get("fft", []):
                 scaled = v / ref * COPY_BYTES if ref else None
-                lines.append(f"| {c} | `{k[:90]}` | {v:.1f} | {ref if ref else 'n/a'} | "
+                lines.append(f"| {c} | `{k[:90]}` | {g} | {v:.1f} | {ref if ref else 'n/a'} | "
                              f"{'%.4g' % scaled if scaled else 'n/a'} |")
-                result.setdefault(k, {})[c] = scaled
+                result.setdefault((k, g), {})[c] = scaled
         lines.append("")
-        for k, cs in result.items():
-            if "FETCH_SIZE" in cs and "WRITE_SIZE" in cs and cs["FETCH_SIZE"] and cs["WRITE_SIZE"]:
-                lines.append(f"traffic_bytes_per_launch `{k[:90]}`: {cs['FETCH_SIZE'] + cs['WRITE_SIZE']:.6g}")
+        for (k, g), cs in result.items():
+            if cs.get("FETCH_SIZE") and cs.get("WRITE_SIZE"):
+                lines.append(f"traffic_bytes_per_launch `{k[:90]}` grid={g}: {cs['FETCH_SIZE'] + cs['WRITE_SIZE']:.6g}")
     return "\n".join(lines)
 
 
-def profiled_traffic(workload):
-    """HBM bytes per launch of the dominant kernel, from the committed rocprof
-    summary profiles/<workload>.md (None when absent)."""
+def profiled_traffic(workload, label, fft_len, grid_threads=None):
+    """HBM bytes per launch of the kernel that runs pass `label` with line
+    length `fft_len` over `grid_threads` threads, from the committed
+    rocprofv3 summary profiles/<workload>.md: (bytes, kernel name), or
+    (None, None). The kernel is matched by its IO policy, the length of a
+    fixed shape and the dispatch's grid size."""
+    import re
     path = os.path.join(ROOT, "profiles", f"{workload}.md")
     if not os.path.exists(path):
-        return None
+        return None, None
+    ios = PASS_IO.get(label, [])
+    found = []
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch"):
-            return float(line.rsplit(":", 1)[1])
-    return None
+        if not line.startswith("traffic_bytes_per_launch"):
+            continue
+        name = line[line.index("`") + 1:line.rindex("`")]
+        val = float(line.rsplit(":", 1)[1])
+        g = re.search(r"grid=(\d+)", line[line.rindex("`"):])
+        if not any(re.search(r"vkfx::%s[,<>]" % io, name) for io in ios):
+            continue
+        m = re.search(r"Shape<(\d+),", name)
+        if m and int(m.group(1)) != fft_len:
+            continue
+        if g and grid_threads and int(g.group(1)) != grid_threads:
+            continue
+        found.append((val, name))
+    if len(found) != 1:
+        return None, None
+    return found[0]
+
+
+def summarize(name, cfg, r, steps, warmup, threads, with_cpu):
+    """One result record of a configuration from run_gpu's measurements."""
+    import statistics
+    nbytes, flops = algorithmic(cfg)
+    ms = r["ms_mean"]
+    med = statistics.median(r["block_ms"])
+    value = nbytes / (ms * 1e-3) / 1e9
+    dom = dominant_kernel(r["kernels"], r["info"]["plans"], cfg)
+    out = {
+        "metric": METRICS[name],
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32" if cfg["prec"] == "f32" else "f64",
+        "data": "synthetic, torch-seeded: " + ("normal(0,1) reals" if cfg["kind"] == "r2c_c2r"
+                                               else "uniform[-1,1) re/im"),
+        "config": {"workload": cfg["workload"], "dims": cfg["dims"], "batch": cfg["batch"],
+                   "buffer_pairs": r["info"]["pairs"]},
+        "ms_per_step_median": round(med, 5),
+        "ms_per_step_min": round(min(r["block_ms"]), 5),
+        "ms_per_step_max": round(max(r["block_ms"]), 5),
+        "median_protocol": f"median over {MEDIAN_BLOCKS} host-clocked blocks of {r['block_steps']} step(s)",
+        "value_at_median": round(nbytes / (med * 1e-3) / 1e9, 2),
+        "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
+        "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
+        "hbm_sweeps": hbm_sweeps(r["info"], cfg),
+        "accuracy": r["info"].get("accuracy"),
+        "roofline": roofline_of(dom, cfg["workload"]),
+        "kernels": [[{k: (round(v, 5) if isinstance(v, float) else v) for k, v in rec.items()} for rec in recs]
+                    for recs in r["kernels"]],
+        "cpu_baseline": None,
+    }
+    return out
 
 
 def main():
@@ -495,18 +684,23 @@ def main():
     ap.add_argument("--no-check", action="store_true", help="skip the oracle check of the timed output")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch (tuning runs)")
+    ap.add_argument("--profile-region", action="store_true",
+                    help="bracket the kernel-timing run with roctxProfilerResume/Pause (rocprofv3 --selected-regions)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
                     help="print a markdown summary of rocprofv3 CSV output directories and exit")
     args = ap.parse_args()
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary))
         return
+    _ROCTX["on"] = args.profile_region
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path.",
               file=sys.stderr)
         sys.exit(2)
     threads = min(16, os.cpu_count() or 1)
     names = list(CONFIGS) if args.all else [args.config]
+    steps = max(20, args.steps)
+    warmup = max(3, args.warmup)
     copy_gbs = plain_gbs = None
     lines_out = []
     for name in names:
@@ -514,63 +708,39 @@ def main():
         if args.batch:
             cfg["batch"] = args.batch
             cfg["workload"] += f"_batch_override_{args.batch}"
-        steps = args.steps if name == "c1" else max(5, min(args.steps, 30))
-        ms, launch_ms, info = run_gpu(cfg, steps, args.warmup, args.rotate,
-                                      check=None if args.no_check else make_check(cfg, threads))
+        r = run_gpu(cfg, steps, warmup, args.rotate, check=None if args.no_check else make_check(cfg, threads))
         if copy_gbs is None:
             copy_gbs = copy_bandwidth()
             plain_gbs = plain_copy_bandwidth()
-        nbytes, flops = algorithmic(cfg)
-        value = nbytes / (ms * 1e-3) / 1e9
-        first = info["plans"][0]["passes"]
-        dom_bytes = nbytes if (len(first) == 1 and len(info["plans"]) == 1) else None
-        roof = None
-        if dom_bytes:
-            ach = dom_bytes / (launch_ms * 1e-3) / 1e9
-            roof = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(cfg["workload"]),
-                    "kernel": first[0]["kernel"], "launch_ms": round(launch_ms, 5),
-                    "timing": "HIP events over a second run of the timed steps"}
-        out = {
-            "metric": METRICS[name],
-            "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
-            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32" if cfg["prec"] == "f32" else "f64",
-            "data": "synthetic, torch-seeded: " + ("normal(0,1) reals" if cfg["kind"] == "r2c_c2r"
-                                                   else "uniform[-1,1) re/im"),
-            "config": {"workload": cfg["workload"], "dims": cfg["dims"], "batch": cfg["batch"],
-                       "buffer_pairs": info["pairs"]},
-            "pct_of_peak": round(100 * value / PEAK_HBM_GBS, 2),
-            "hbm_copy_gbs": round(copy_gbs, 1),
-            "hbm_plain_copy_gbs": round(plain_gbs, 1),
-            "pct_of_copy": round(100 * value / copy_gbs, 2),
-            "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
-            "hbm_sweeps": hbm_sweeps(info, cfg),
-            "accuracy": info.get("accuracy"),
-            "roofline": roof,
-            "cpu_baseline": None,
-            "device": info["device"],
-        }
+        out = summarize(name, cfg, r, steps, warmup, threads, not args.no_cpu)
+        out["hbm_copy_gbs"] = round(copy_gbs, 1)
+        out["hbm_plain_copy_gbs"] = round(plain_gbs, 1)
+        out["pct_of_copy"] = round(100 * out["value"] / copy_gbs, 2)
+        out["device"] = r["info"]["device"]
+        print(f"# {name}: {out['ms_per_step']} ms mean, {out['ms_per_step_median']} ms median, "
+              f"{out['value']} GB/s", file=sys.stderr, flush=True)
         lines_out.append((name, out))
     if not args.all and args.config == "c1" and not args.headline_only:
-        # every BASELINE configuration beside the headline, same process
+        # every other configuration beside the headline, same process and protocol
         table = {}
         for name in CONFIGS:
             if name == "c1":
                 continue
             cfg = dict(CONFIGS[name])
-            ms, _, info = run_gpu(cfg, 5, 2, args.rotate,
-                                  check=None if args.no_check else make_check(cfg, threads))
-            nbytes, flops = algorithmic(cfg)
-            v = nbytes / (ms * 1e-3) / 1e9
-            table[name] = {"workload": cfg["workload"], "ms_per_step": round(ms, 5), "value": round(v, 2),
-                           "unit": "GB/s", "pct_of_peak": round(100 * v / PEAK_HBM_GBS, 2),
-                           "gflops": round(flops / (ms * 1e-3) / 1e9, 1), "steps": 5, "warmup": 2,
-                           "hbm_sweeps": hbm_sweeps(info, cfg),
-                           "rel_l2": (info.get("accuracy") or {}).get("rel_l2"),
-                           "accuracy_sample": (info.get("accuracy") or {}).get("sample")}
-            print(f"# {name}: {table[name]['ms_per_step']} ms, {table[name]['value']} GB/s", file=sys.stderr,
-                  flush=True)
+            # the other configs' steps are 1-6 ms: at most 30 keep the run short
+            ksteps = min(steps, 30)
+            r = run_gpu(cfg, ksteps, warmup, args.rotate, check=None if args.no_check else make_check(cfg, threads))
+            row = summarize(name, cfg, r, ksteps, warmup, threads, False)
+            acc = row.pop("accuracy") or {}
+            for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "data", "unit"):
+                row.pop(k, None)
+            row["workload"] = row.pop("config")["workload"]
+            row["rel_l2"] = acc.get("rel_l2")
+            row["accuracy_sample"] = acc.get("sample")
+            row["baseline_config"] = name in BASELINE_CONFIGS
+            table[name] = row
+            print(f"# {name}: {row['ms_per_step']} ms mean, {row['ms_per_step_median']} ms median, "
+                  f"{row['value']} GB/s", file=sys.stderr, flush=True)
         lines_out[0][1]["configs"] = table
     if not args.no_cpu:
         for name, out in lines_out:

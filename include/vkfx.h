@@ -212,6 +212,29 @@ typedef struct {
  * total count into *count. */
 int vkfx_plan_resources(const vkfx_plan *plan, vkfx_pass_resources *out, uint32_t capacity, uint32_t *count);
 
+/* GPU durations of a plan's FFT kernels (measurement only; no counterpart in
+ * the reference, whose HIP backend publishes no timings). After
+ * vkfx_plan_timing_start, every FFT kernel that vkfx_execute launches for the
+ * plan, up to `max_launches` of them, is dispatched with a pair of HIP events
+ * bound to that dispatch (hipExtLaunchKernel), so each pair reads the
+ * kernel's own begin and end: the duration a kernel trace reports, without
+ * the gaps between launches that a stream-level event pair also counts.
+ * Launches past `max_launches` and non-FFT passes (boundary, copy, DCT/DST,
+ * convolution multiply) run untimed. vkfx_plan_timing_stop waits for the
+ * events, disarms the plan and writes one record per distinct (pass label,
+ * line length, lines per launch), in launch order. Not for a plan that executes on several host threads at once. */
+typedef struct {
+    char pass[48];     /* launch label (as in vkfx_plan_describe) */
+    uint32_t fft_len;  /* length each line of the pass transforms */
+    uint32_t launches; /* timed launches with this label, length and line count */
+    uint64_t lines;    /* lines of each of those launches */
+    double total_ms;   /* sum of the launches' durations */
+    double min_ms;
+    double max_ms;
+} vkfx_pass_timing;
+int vkfx_plan_timing_start(vkfx_plan *plan, uint32_t max_launches);
+int vkfx_plan_timing_stop(vkfx_plan *plan, vkfx_pass_timing *out, uint32_t capacity, uint32_t *count);
+
 /* Byte sizes of one execute's input and output buffers, and of the scratch
  * a caller may pass to vkfx_execute (0 when the plan needs none). */
 int vkfx_plan_io_bytes(const vkfx_plan *plan, uint64_t *in_bytes, uint64_t *out_bytes);

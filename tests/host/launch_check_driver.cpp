@@ -1,0 +1,100 @@
+// Host-side checks of the launch validation (csrc/launch_check.cpp): each
+// case builds the KArgs of one launch and compares check_launch's verdict
+// with the expected one. Prints "ok <cases>" and exits 0 when all agree.
+#include <cstdio>
+#include <cstring>
+
+#include "kernels.hpp"
+
+using namespace vkfx;
+
+static int fails = 0, cases = 0;
+
+static void expect(const char* name, hipError_t got, hipError_t want) {
+    ++cases;
+    if (got != want) {
+        ++fails;
+        std::printf("FAIL %s: got %d, want %d\n", name, (int)got, (int)want);
+    }
+}
+
+// A runtime-shape f32 line of N = 34 = 2 * 17 with a Rader stage for 17:
+// G lines of LS elements, 34 threads per line.
+static KArgs rader_args() {
+    KArgs a;
+    std::memset(&a, 0, sizeof a);
+    a.N = 34;
+    a.TT = 34;
+    a.G = 2;
+    a.LS = 37;
+    a.PS = 4;
+    a.nstages = 2;
+    a.radix[0] = 2;
+    a.radix[1] = 17;
+    a.in_es = a.out_es = 1;
+    static const int table = 0;
+    a.rtab = &table;
+    return a;
+}
+
+int main() {
+    const size_t limit = 160 * 1024;
+    const KArgs r = rader_args();
+    const unsigned block = (unsigned)(r.G * r.TT);
+    const size_t two = 2 * (size_t)r.G * r.LS * 8, one = (size_t)r.G * r.LS * 8;
+    expect("rader staged, line + scratch region", check_launch(KK_PLAIN, 0, -1, r, block, two, limit, nullptr),
+           hipSuccess);
+    expect("rader staged, scratch region missing", check_launch(KK_PLAIN, 0, -1, r, block, one, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    expect("rader f64 sized for f32", check_launch(KK_PLAIN, 1, -1, r, block, two, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs d = r;
+    d.flags = KF_DYN_DIRECT;
+    expect("rader with HBM-direct stages", check_launch(KK_PLAIN, 0, -1, d, block, two, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs e = r;
+    e.flags = KF_EDGE;
+    e.zr = e.N;
+    expect("rader with edge work", check_launch(KK_PLAIN, 0, -1, e, block, two, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    FixedKernel fx;
+    std::memset(&fx, 0, sizeof fx);
+    fx.kind = KK_PLAIN;
+    fx.prec = 0;
+    fx.dir = -1;
+    fx.N = r.N;
+    fx.TT = r.TT;
+    fx.G = r.G;
+    fx.PS = r.PS;
+    fx.LS = r.LS;
+    fx.nst = r.nstages;
+    fx.radix[0] = 2;
+    fx.radix[1] = 17;
+    fx.lds_mult = 1;
+    expect("rader on a fixed shape", check_launch(KK_PLAIN, 0, -1, r, block, two, limit, &fx),
+           hipErrorInvalidConfiguration);
+    KArgs n = r;
+    n.rtab = nullptr;
+    expect("rader radix without its table", check_launch(KK_PLAIN, 0, -1, n, block, two, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs s = r;
+    s.radix[1] = 16;
+    s.N = 32;
+    s.TT = 16;
+    expect("table without a rader radix", check_launch(KK_PLAIN, 0, -1, s, 32, two, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    // ordinary launches around the new rules
+    KArgs p = s;
+    p.rtab = nullptr;
+    expect("plain staged", check_launch(KK_PLAIN, 0, -1, p, 32, (size_t)p.G * p.LS * 8, limit, nullptr),
+           hipSuccess);
+    expect("plain, block != G * TT", check_launch(KK_PLAIN, 0, -1, p, 64, (size_t)p.G * p.LS * 8, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    expect("plain, LDS beyond the limit", check_launch(KK_PLAIN, 0, -1, p, 32, limit + 8, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    expect("plain, bad direction", check_launch(KK_PLAIN, 0, 0, p, 32, (size_t)p.G * p.LS * 8, limit, nullptr),
+           hipErrorInvalidValue);
+    if (fails) return 1;
+    std::printf("ok %d\n", cases);
+    return 0;
+}

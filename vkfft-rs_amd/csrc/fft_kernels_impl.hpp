@@ -1497,19 +1497,6 @@ __global__ __launch_bounds__(Sh::G* Sh::TT) __attribute__((amdgpu_waves_per_eu(S
     fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, group_index(a));
 }
 
-// Persistent variant: a grid sized to the resident capacity walks the groups
-// with a grid stride, so the groups in flight stay within a compact window of
-// HBM and no workgroup is dispatched per group.
-template <typename T, int S, class IO, class Sh>
-__global__ __launch_bounds__(Sh::G* Sh::TT) void k_fix_persist(const KArgs a) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    __shared__ LineInfo li[Sh::G];
-    for (long long blk = blockIdx.x; blk < a.nblk; blk += gridDim.x) {
-        fix_body<T, S, IO, Sh>(a, reinterpret_cast<cpx<T>*>(smem_raw), li, blk);
-        __syncthreads();
-    }
-}
-
 // ------------------------------------------------------------- selection
 
 template <typename T, int S, bool W>
@@ -1569,15 +1556,14 @@ KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
 #define VKFX_FIXED_OCC(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, W, NTI, NTO, ...)                  \
     FixedKernel {                                                                                      \
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                               \
-            (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>), \
-            (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)              \
+            (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>) \
     }
 // A ping-pong shape (two LDS buffers per line, lds_mult 2).
 #define VKFX_FIXED_PP(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                              \
     FixedKernel {                                                                                              \
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
             (KernelFn)(k_fix_occ<T, S, IO, PingPong<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>), \
-            nullptr, FT_STAGE, 2                                                                               \
+            FT_STAGE, 2                                                                                        \
     }
 // Ping-pong with per-stage twiddle tables.
 #define VKFX_FIXED_PPT(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                            \
@@ -1585,7 +1571,7 @@ KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
             (KernelFn)(k_fix_occ<T, S, IO,                                                                     \
                                  StageTables<PingPong<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>>), \
-            nullptr, FT_STAGE_PR, 2                                                                            \
+            FT_STAGE_PR, 2                                                                                     \
     }
 // Ping-pong with per-stage twiddle tables and per-stage pads.
 #define VKFX_FIXED_PPTS(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                           \
@@ -1593,14 +1579,14 @@ KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
             (KernelFn)(k_fix_occ<T, S, IO,                                                                     \
                                  StagePads<StageTables<PingPong<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>>>), \
-            nullptr, FT_STAGE_PR, 2                                                                            \
+            FT_STAGE_PR, 2                                                                                     \
     }
 // In place with per-stage twiddle tables (the shape's own pad).
 #define VKFX_FIXED_T(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                               \
     FixedKernel {                                                                                              \
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
             (KernelFn)(k_fix_occ<T, S, IO, StageTables<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>>), \
-            nullptr, FT_STAGE_PR, 1                                                                            \
+            FT_STAGE_PR, 1                                                                                     \
     }
 // In place (one LDS buffer) with per-stage twiddle tables and pads, and a
 // waves-per-EU hint W.
@@ -1608,24 +1594,16 @@ KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
     FixedKernel {                                                                                              \
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                                       \
             (KernelFn)(k_fix_occ<T, S, IO, StagePads<StageTables<Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, W, NTI, NTO>>>>), \
-            nullptr, FT_STAGE_PR, 1                                                                            \
+            FT_STAGE_PR, 1                                                                                     \
     }
-// A shape without the persistent variant (it launches as one block per group
-// under VKFX_PERSIST_BLOCKS_PER_CU as well).
+// A shape with the default launch bounds hint.
 #define VKFX_SHAPE(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...)                                \
     FixedKernel {                                                                                      \
         KIND, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, 0, {__VA_ARGS__},                               \
-            (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>), \
-            nullptr                                                                                    \
+            (KernelFn)(k_fix_occ<T, S, IO, Tuned<Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>, 0, NTI, NTO>>) \
     }
 // The same shape with nontemporal HBM streaming (inputs read once, outputs
 // written once).
 // NTI / NTO: nontemporal loads of the pass input / stores of its output.
 #define VKFX_FIXED_NT(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, NTI, NTO, ...) \
     VKFX_FIXED_OCC(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, 0, NTI, NTO, __VA_ARGS__)
-#define VKFX_FIXED(KIND, IO, T, PREC, S, N, TT, G, PS, LS, COL, ...)                                   \
-    FixedKernel {                                                                                     \
-        KIND, PREC, S, N, TT, G, PS, LS, COL, false, false, 0, {__VA_ARGS__},                          \
-            (KernelFn)(k_fix<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>),                    \
-            (KernelFn)(k_fix_persist<T, S, IO, Shape<N, TT, G, PS, LS, COL, __VA_ARGS__>>)             \
-    }

@@ -107,7 +107,7 @@ struct KArgs {
     long long nvalid;                  // logical input length (zero pad beyond)
     long long nout;                    // logical output length per line (truncate)
     long long N1, N2;                  // four-step factors (M = N1*N2)
-    long long nblk;                    // line groups (persistent kernels walk them)
+    long long nblk;                    // line groups of the launch
     const int* pin;                    // Rader gather: a[s] = x[pin[s]]
     const int* pout;                   // Rader scatter: X[pout[m]] = x0 + conv[m]
     // Rader stages of a runtime radix list (radix > kMaxStockhamRadix): the
@@ -152,7 +152,6 @@ struct FixedKernel {
     int nst;
     int radix[8];
     KernelFn fn;          // one block per group of G lines
-    KernelFn fn_persist;  // grid-stride over groups, grid sized to residency
     int table = FT_STAGE;
     int lds_mult = 1;  // 2: ping-pong shapes hold two LDS buffers of G lines
 };
@@ -168,10 +167,19 @@ const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto);
 
 // Launches one kernel. prec: 0 = f32, 1 = f64. dir: -1 forward, +1 inverse
 // (direction of the first FFT the kernel runs). fixed: the fixed-shape
-// instantiation to run, or nullptr for the runtime-shape kernel. Returns a
+// instantiation to run, or nullptr for the runtime-shape kernel. t_begin /
+// t_end: when both are set, HIP events bound to this dispatch
+// (hipExtLaunchKernel) that read the kernel's own begin and end. Returns a
 // hipError_t value.
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block,
-           size_t lds_bytes, hipStream_t stream, const FixedKernel* fixed = nullptr);
+           size_t lds_bytes, hipStream_t stream, const FixedKernel* fixed = nullptr, hipEvent_t t_begin = nullptr,
+           hipEvent_t t_end = nullptr);
+
+// Validates one launch against what the kernel it selects assumes (block
+// shape, LDS size, flags, fixed-shape geometry, Rader stage scratch); no HIP
+// calls. Returns hipSuccess or the error launch() reports.
+hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned block, size_t lds_bytes,
+                        size_t lds_limit, const FixedKernel* fixed);
 
 // Largest dynamic LDS a block may request on this device (bytes).
 size_t max_lds_bytes();

@@ -11,7 +11,7 @@ namespace vkfx {
 #define VKFX_WAVE1024(S, NTI, NTO)                                                                    \
     FixedKernel {                                                                                     \
         KK_PLAIN, 0, S, 1024, 64, 4, 0, 0, false, NTI, NTO, 0, {16, 4, 16},                             \
-            (KernelFn)(k_wave1024<S, NTI, NTO>), nullptr, FT_WAVE1024                                   \
+            (KernelFn)(k_wave1024<S, NTI, NTO>), FT_WAVE1024                                            \
     }
 
 static const FixedKernel kTable[] = {

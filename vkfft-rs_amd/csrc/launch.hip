@@ -1,5 +1,6 @@
 // launch.hip -- dispatches a KernelKind to its instantiation and launches it.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cstdlib>
 #include <string>
@@ -144,16 +145,6 @@ static int lds_limit_bytes() {
 
 size_t max_lds_bytes() { return (size_t)lds_limit_bytes(); }
 
-// Blocks per CU of a persistent launch (0 = one block per group). Tuning knob:
-// VKFX_PERSIST_BLOCKS_PER_CU.
-static int persist_blocks_per_cu() {
-    static const int v = [] {
-        const char* e = getenv("VKFX_PERSIST_BLOCKS_PER_CU");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
 // Launches whose blocks share HBM cache lines with their neighbours get their
 // groups dealt to XCDs in contiguous ranges: the four-step passes that read
 // or write the N/2+1-pitch real-transform spectra (unaligned 128-byte
@@ -187,77 +178,25 @@ const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel*
 }
 
 int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, unsigned block, size_t lds_bytes,
-           hipStream_t stream, const FixedKernel* fixed) {
-    if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1))
-        return (int)hipErrorInvalidValue;
+           hipStream_t stream, const FixedKernel* fixed, hipEvent_t t_begin, hipEvent_t t_end) {
     if (grid == 0) return (int)hipSuccess;
-    // runtime-shape kernels are built for at most 512 threads, fixed shapes
-    // for exactly their own G * TT (at most 1024)
-    if (block == 0 || block > (fixed ? 1024u : 512u) || a.G < 1 || a.G > kMaxLinesPerBlock ||
-        (unsigned)(a.G * a.TT) != block)
-        return (int)hipErrorInvalidConfiguration;
-    if (a.nstages < 0 || a.nstages > kMaxStages) return (int)hipErrorInvalidValue;
-    if (lds_bytes < (size_t)a.G * (size_t)a.LS * (prec ? 16 : 8) * (fixed ? fixed->lds_mult : 1) ||
-        lds_bytes > (size_t)lds_limit_bytes())
-        return (int)hipErrorInvalidConfiguration;
-    if (kind == KK_CONV_1 && !a.spec) return (int)hipErrorInvalidConfiguration;
-    if (kind == KK_RADER_DIRECT && (a.TT != a.N || a.LS < a.N + 1 || a.N < 1 || !a.pin || !a.pout))
-        return (int)hipErrorInvalidConfiguration;
-    if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))
-        return (int)hipErrorInvalidConfiguration;
-    KernelFn fn = pick_kernel(kind, prec, dir, a.flags);
-    // the direct runtime-shape kernels read (C2C, even R2C, even C2R with
-    // KF_DYN_PRE) and write (C2C, even C2R) contiguous lines, with no radix-2
-    // stage at a direct end
-    if (!fixed && (a.flags & KF_DYN_DIRECT) &&
-        !(kind == KK_PLAIN && a.in_es == 1 && a.out_es == 1 && a.nstages >= 2 && a.radix[0] != 2 &&
-          a.radix[a.nstages - 1] != 2) &&
-        !(kind == KK_R2C_HALF && a.in_es == 1 && a.nstages >= 1 && a.radix[0] != 2) &&
-        !(kind == KK_C2R_HALF && a.out_es == 1 && a.nstages >= 1 && a.radix[a.nstages - 1] != 2 &&
-          (!(a.flags & KF_DYN_PRE) || (a.in_es == 1 && a.nstages >= 2 && a.radix[0] != 2))))
-        return (int)hipErrorInvalidConfiguration;
-    // boundary work runs in the runtime-shape C2C kernels only (staged, or
-    // HBM-direct under the direct kernel's own conditions below)
-    if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE))
-        return (int)hipErrorInvalidValue;
-    if ((a.flags & KF_EDGE) && (fixed || kind != KK_PLAIN || (a.flags & KF_DYN_PRE) || a.zl > a.zr || a.zl < 0 ||
-                                a.zr > a.N))
-        return (int)hipErrorInvalidConfiguration;
-    // the register-exchange kernels address contiguous lines (element stride 1)
-    if (fixed && fixed->table == FT_WAVE1024 && (a.in_es != 1 || a.out_es != 1 || !a.tw))
-        return (int)hipErrorInvalidConfiguration;
-    if (fixed && fixed->table == FT_STAGE_PR && !a.tw) return (int)hipErrorInvalidConfiguration;
-    if (fixed) {
-        // the fixed shape must be launched with exactly its own geometry
-        if (fixed->kind != kind || fixed->prec != prec || fixed->dir != dir || fixed->N != a.N ||
-            fixed->TT != a.TT || fixed->G != a.G || fixed->PS != a.PS || fixed->LS != a.LS ||
-            fixed->nst != a.nstages)
-            return (int)hipErrorInvalidConfiguration;
-        for (int i = 0; i < fixed->nst; ++i)
-            if (fixed->radix[i] != a.radix[i]) return (int)hipErrorInvalidConfiguration;
-        fn = fixed->fn;
-    }
+    const hipError_t bad = check_launch(kind, prec, dir, a, block, lds_bytes, (size_t)lds_limit_bytes(), fixed);
+    if (bad != hipSuccess) return (int)bad;
+    KernelFn fn = fixed ? fixed->fn : pick_kernel(kind, prec, dir, a.flags);
     if (!fn) return (int)hipErrorInvalidValue;
     KArgs args = a;
     args.nblk = grid;
     if (xcd_groups(kind)) args.flags |= KF_XCD_GROUPS;
-    if (fixed && fixed->fn_persist && persist_blocks_per_cu() > 0) {
-        // persistent launch: at most the resident capacity, groups by grid stride
-        static int cus = 0;
-        if (!cus) {
-            int dev = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-                cus = 256;
-        }
-        fn = fixed->fn_persist;
-        const unsigned cap = (unsigned)(cus * persist_blocks_per_cu());
-        if (grid > cap) grid = cap;
-    }
     if (lds_bytes > 65536) {
         hipError_t e =
             hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
         if (e != hipSuccess) return (int)e;
+    }
+    if (t_begin && t_end) {
+        void* kargs[1] = {&args};
+        hipError_t e = hipExtLaunchKernel((const void*)fn, dim3(grid), dim3(block), kargs, lds_bytes, stream, t_begin,
+                                          t_end, 0);
+        return e != hipSuccess ? (int)e : (int)hipGetLastError();
     }
     hipLaunchKernelGGL(fn, dim3(grid), dim3(block), lds_bytes, stream, args);
     return (int)hipGetLastError();

@@ -324,6 +324,13 @@ struct vkfx_plan {
     int tickets = 0;          // live tickets of this plan (guarded by ctx->mu)
     std::string json;
     DevBuf host_in, host_out;  // staging for vkfx_execute_host
+    // vkfx_plan_timing_start/stop: event pairs bound to FFT kernel dispatches
+    struct {
+        bool armed = false;
+        std::vector<hipEvent_t> ev;  // begin/end of timed launch i at 2i, 2i+1
+        std::vector<int> launch;     // index into launches of timed launch i
+        size_t used = 0, cap = 0;
+    } timing;
 };
 
 namespace {
@@ -2763,6 +2770,7 @@ int vkfx_plan_destroy(vkfx_plan* plan) {
     }
     if (plan->ev_fork) (void)hipEventDestroy(plan->ev_fork);
     if (plan->ev_join) (void)hipEventDestroy(plan->ev_join);
+    for (hipEvent_t e : plan->timing.ev) (void)hipEventDestroy(e);
     delete plan;
     return VKFX_OK;
 }
@@ -2825,6 +2833,62 @@ int vkfx_plan_resources(const vkfx_plan* plan, vkfx_pass_resources* out, uint32_
     return VKFX_OK;
 }
 
+int vkfx_plan_timing_start(vkfx_plan* plan, uint32_t max_launches) {
+    if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
+    if (max_launches == 0 || max_launches > (1u << 20))
+        return fail(VKFX_ERR_INVALID_ARGUMENT, "max_launches must be in [1, 2^20]");
+    (void)hipSetDevice(plan->ctx->device);
+    auto& tm = plan->timing;
+    while (tm.ev.size() < 2 * (size_t)max_launches) {
+        hipEvent_t e = nullptr;
+        hipError_t r = hipEventCreate(&e);  // default flags: timing enabled
+        if (r != hipSuccess) return hip_fail(r, "hipEventCreate(timing)");
+        tm.ev.push_back(e);
+    }
+    tm.launch.assign(max_launches, -1);
+    tm.cap = max_launches;
+    tm.used = 0;
+    tm.armed = true;
+    return VKFX_OK;
+}
+
+int vkfx_plan_timing_stop(vkfx_plan* plan, vkfx_pass_timing* out, uint32_t capacity, uint32_t* count) {
+    if (!plan || !count || (capacity && !out)) return fail(VKFX_ERR_INVALID_ARGUMENT, "null argument");
+    auto& tm = plan->timing;
+    if (!tm.armed) return fail(VKFX_ERR_INVALID_ARGUMENT, "plan timing was not started");
+    tm.armed = false;
+    (void)hipSetDevice(plan->ctx->device);
+    std::vector<vkfx_pass_timing> recs;
+    for (size_t i = 0; i < tm.used; ++i) {
+        hipError_t r = hipEventSynchronize(tm.ev[2 * i + 1]);
+        float ms = 0.f;
+        if (r == hipSuccess) r = hipEventElapsedTime(&ms, tm.ev[2 * i], tm.ev[2 * i + 1]);
+        if (r != hipSuccess) return hip_fail(r, "hipEventElapsedTime(timing)");
+        const Launch& L = plan->launches[(size_t)tm.launch[i]];
+        vkfx_pass_timing* rec = nullptr;
+        for (auto& x : recs)
+            if (L.label == x.pass && (uint32_t)L.a.N == x.fft_len && (uint64_t)L.a.nlines == x.lines) rec = &x;
+        if (!rec) {
+            recs.emplace_back();
+            rec = &recs.back();
+            std::memset(rec, 0, sizeof *rec);
+            std::snprintf(rec->pass, sizeof rec->pass, "%s", L.label.c_str());
+            rec->fft_len = (uint32_t)L.a.N;
+            rec->lines = (uint64_t)L.a.nlines;
+            rec->min_ms = ms;
+            rec->max_ms = ms;
+        }
+        rec->launches += 1;
+        rec->total_ms += ms;
+        rec->min_ms = std::min(rec->min_ms, (double)ms);
+        rec->max_ms = std::max(rec->max_ms, (double)ms);
+    }
+    tm.used = 0;
+    for (size_t i = 0; i < recs.size() && i < capacity; ++i) out[i] = recs[i];
+    *count = (uint32_t)recs.size();
+    return VKFX_OK;
+}
+
 int vkfx_plan_output_info(const vkfx_plan* plan, int32_t* real_output, uint64_t* widened_bytes) {
     if (!plan) return fail(VKFX_ERR_INVALID_ARGUMENT, "null plan");
     if (real_output) *real_output = plan->real_out ? 1 : 0;
@@ -2875,7 +2939,8 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
         if (e == hipSuccess) e = hipStreamWaitEvent(plan->aux, plan->ev_fork, 0);
         if (e != hipSuccess) return hip_fail(e, "stream fork");
     }
-    for (const Launch& L : plan->launches) {
+    for (size_t li = 0; li < plan->launches.size(); ++li) {
+        const Launch& L = plan->launches[li];
         const int lane = plan->lanes == 2 ? (L.chunk & 1) : 0;
         KArgs a = L.a;
         auto sel = [&](int which, size_t off) -> char* {
@@ -2912,7 +2977,14 @@ int vkfx_execute(vkfx_plan* plan, const void* d_in, void* d_out, void* d_work, v
         }
         a.in = sel(L.in_sel, L.in_off);
         a.out = sel(L.out_sel, L.out_off);
-        int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, lane_stream[lane], L.fixed);
+        hipEvent_t t0 = nullptr, t1 = nullptr;
+        auto& tm = plan->timing;
+        if (tm.armed && tm.used < tm.cap) {
+            t0 = tm.ev[2 * tm.used];
+            t1 = tm.ev[2 * tm.used + 1];
+            tm.launch[tm.used++] = (int)li;
+        }
+        int e = launch(L.kind, prec, L.dir, a, L.grid, L.block, L.lds, lane_stream[lane], L.fixed, t0, t1);
         if (e != hipSuccess) return hip_fail((hipError_t)e, ("launch " + L.label).c_str());
     }
     if (plan->lanes == 2) {

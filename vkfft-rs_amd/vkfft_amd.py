@@ -129,6 +129,18 @@ class _PassResources(ctypes.Structure):
     ]
 
 
+class _PassTiming(ctypes.Structure):
+    _fields_ = [
+        ("pass_", ctypes.c_char * 48),
+        ("fft_len", ctypes.c_uint32),
+        ("launches", ctypes.c_uint32),
+        ("lines", ctypes.c_uint64),
+        ("total_ms", ctypes.c_double),
+        ("min_ms", ctypes.c_double),
+        ("max_ms", ctypes.c_double),
+    ]
+
+
 class _PlannerTuning(ctypes.Structure):
     _fields_ = [
         ("min_rader_direct_prime", ctypes.c_uint64),
@@ -227,6 +239,9 @@ def lib(path: Optional[str] = None):
         L.vkfx_context_clear_caches.argtypes = [vp]
         L.vkfx_plan_resources.argtypes = [vp, ctypes.POINTER(_PassResources), ctypes.c_uint32,
                                           ctypes.POINTER(ctypes.c_uint32)]
+        L.vkfx_plan_timing_start.argtypes = [vp, ctypes.c_uint32]
+        L.vkfx_plan_timing_stop.argtypes = [vp, ctypes.POINTER(_PassTiming), ctypes.c_uint32,
+                                            ctypes.POINTER(ctypes.c_uint32)]
         L.vkfx_execute_chain.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, vp, vp]
         L.vkfx_execute_chain_host.argtypes = [ctypes.POINTER(vp), ctypes.c_uint32, vp, u64, vp, u64]
         _libs[path] = L
@@ -679,6 +694,26 @@ class Plan:
             d = {name: getattr(r, name) for name, _ in _PassResources._fields_ if name != "pass_"}
             d["pass"] = r.pass_.decode()
             out.append(d)
+        return out
+
+    def timing_start(self, max_launches: int):
+        """Arms kernel timing: the next `max_launches` FFT kernel dispatches
+        of this plan carry HIP events bound to the dispatch itself."""
+        _check(self._L.vkfx_plan_timing_start(self.handle, int(max_launches)), self._L)
+
+    def timing_stop(self) -> List[dict]:
+        """Waits for the timed dispatches and returns one record per (pass
+        label, line length, lines per launch), in launch order: launches and
+        total/min/max/avg kernel ms."""
+        count = ctypes.c_uint32()
+        arr = (_PassTiming * 256)()
+        _check(self._L.vkfx_plan_timing_stop(self.handle, arr, 256, ctypes.byref(count)), self._L)
+        out = []
+        for r in arr[:min(256, count.value)]:
+            out.append({"pass": r.pass_.decode(), "fft_len": int(r.fft_len), "lines": int(r.lines),
+                        "launches": int(r.launches), "total_ms": r.total_ms,
+                        "min_ms": r.min_ms, "max_ms": r.max_ms,
+                        "avg_ms": r.total_ms / r.launches if r.launches else None})
         return out
 
     def describe(self) -> dict:
