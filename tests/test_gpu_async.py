@@ -251,6 +251,49 @@ def test_shim_real_output_tickets(hip_ctx, prec):
     assert o.rel_l2(z.real, o.r2r_batch(xr.astype(np.float64), m, "dct2", threads=8)) <= tol
 
 
+def test_shim_f16_storage_tickets(hip_ctx):
+    """The shim's F16StorageF32Compute ticket path: binary16 input
+    (Binary16::from_f32), out_len = widened bytes / 4 (binary16 pairs), the
+    wait decoded to Complex32 (native_runtime.rs:1111-1120 decodes F16
+    storage on readback). Equal to the synchronous execute of the same plan;
+    C2C and C2R (a real output widened to {v, 0})."""
+    import ctypes
+    L = hip_ctx._L
+    F16 = vk.Precision.F16StorageF32Compute
+    n, batch = 4096, 3
+    cases = [
+        (vk.TransformIr.build(vk.FftConfig.new([1024]).with_batch_count(4).with_precision(F16), FWD),
+         o.complex_uniform(1024 * 4, 41, np.complex64)),
+        (vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(F16)
+                              .with_transform(vk.TransformKind.ComplexToReal).with_inverse_normalization(True), INV),
+         o.complex_uniform((n // 2 + 1) * batch, 42, np.complex64)),
+    ]
+    for ir, x in cases:
+        plan = hip_ctx.plan(ir)
+        x16 = np.ascontiguousarray(x.view(np.float32).astype(np.float16))
+        assert x16.nbytes == plan.in_bytes
+        real, widened = ctypes.c_int32(), ctypes.c_uint64()
+        vk._check(L.vkfx_plan_output_info(plan.handle, ctypes.byref(real), ctypes.byref(widened)), L)
+        out_len = int(widened.value) // 4
+        t = ctypes.c_void_p()
+        vk._check(L.vkfx_submit_host(plan.handle, x16.ctypes.data, x16.nbytes, ctypes.byref(t)), L)
+        try:
+            raw = np.empty(2 * out_len, dtype=np.float16)
+            vk._check(L.vkfx_ticket_wait_complex(t, raw.ctypes.data, raw.nbytes), L)
+        finally:
+            L.vkfx_ticket_destroy(t)
+        y = raw.astype(np.float32).view(np.complex64)
+        sync = hip_ctx.execute_transform(ir, x)
+        if real.value:
+            assert np.all(y.imag == 0) and np.array_equal(y.real, sync)
+            xin = x16.astype(np.float32).view(np.complex64).astype(np.complex128)
+            assert o.rel_l2(y.real, o.c2r_batch(xin, n, normalize=True, threads=8)) <= 2e-3
+        else:
+            assert np.array_equal(y, sync)
+            xin = x16.astype(np.float32).view(np.complex64).astype(np.complex128)
+            assert o.rel_l2(y, o.fft_batch(xin, 1024)) <= 2e-3
+
+
 def test_context_close_releases_tickets_and_plans():
     """Closing a context with a live ticket destroys the ticket and its plan
     first; the ticket then refuses to wait instead of reading freed memory.

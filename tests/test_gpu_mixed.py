@@ -127,3 +127,55 @@ def test_mixed_ticket_and_chain(hip_ctx):
     assert np.array_equal(t.wait(), hip_ctx.execute_transform_f32(fwd, x))
     z = hip_ctx.execute_chain([fwd, inv], x)
     assert o.rel_l2(z, x) <= 1e-7
+
+
+# ------------------------------------ the reference's mixed-storage FFTW corpora
+
+MIXED_CORPORA = {
+    # tests/fftw_medium_f16_storage_golden.rs:230-252: within 2 binary16 ulps or 2e-3
+    "f16": ("fftw_precision_medium_f16_storage_v1.txt", F16S, 2, 2e-3),
+    # tests/fftw_medium_f64_f32_storage_golden.rs:217-240: within 4 f32 ulps or 1e-6
+    "f64_f32": ("fftw_precision_medium_f64_f32_storage_v1.txt", F64C, 4, 1e-6),
+}
+
+
+@pytest.mark.parametrize("corpus", sorted(MIXED_CORPORA))
+@pytest.mark.parametrize("case", ["c2c-bluestein-n103", "c2c-rader-n257", "c2c-smooth-n1536",
+                                  "c2c-large-smooth-n4096", "r2c-nd-17x34", "r2c-nd-64x64", "dct2-nd-17x34"])
+def test_fftw_medium_mixed_storage_on_gpu(hip_ctx, corpus, case):
+    """run_native_medium_*_storage_fftw of the reference: the f32 input
+    formulas (rounded to binary16 by the F16 plan's storage), a forward plan
+    of the case's kind, every output scalar against FFTW's committed bits at
+    the reference's tolerances, and the planner families of the C2C cases
+    (Bluestein under max_rader_fft_prime = 100, Rader, Stockham)."""
+    import os
+
+    import golden_bits as gb
+    from conftest import GOLDEN
+    name, prec, max_ulps, max_abs = MIXED_CORPORA[corpus]
+    width, cases = gb.parse(os.path.join(GOLDEN, name))
+    c = cases[case]
+    kind = {"c2c": vk.TransformKind.ComplexToComplex, "r2c": vk.TransformKind.RealToComplex,
+            "dct2": vk.TransformKind.dct(2)}[c["kind"]]
+    cfg = vk.FftConfig.new(c["shape"]).with_precision(prec).with_transform(kind)
+    if case == "c2c-bluestein-n103":
+        t = vk.PlannerTuning.portable()
+        t.max_rader_fft_prime = 100
+        cfg = cfg.with_tuning(t)
+    ir = vk.TransformIr.build(cfg, FWD)
+    family = {"c2c-bluestein-n103": vk.AlgorithmKind.Bluestein, "c2c-rader-n257": vk.AlgorithmKind.Rader,
+              "c2c-smooth-n1536": vk.AlgorithmKind.Stockham, "c2c-large-smooth-n4096": vk.AlgorithmKind.Stockham}
+    if case in family:
+        assert ir.axis_algorithms == [family[case]]
+    n = int(np.prod(c["shape"]))
+    x = o.fixture_input("complex-f32-v1" if c["kind"] == "c2c" else "real-f32-v1", n)
+    y = hip_ctx.execute_transform_f32(ir, x)
+    got = gb.scalars(y, c["kind"]).astype(np.float32)
+    assert got.size == c["bits"].size and np.all(np.isfinite(got))
+    if width == 16:   # caller-visible binary16 storage
+        assert np.array_equal(got.astype(np.float16).astype(np.float32), got)
+    expected = gb.from_bits(c["bits"], width)
+    d = gb.ulps(gb.to_bits(got, width), c["bits"], width)
+    ok = (d <= max_ulps) | (np.abs(got - expected) <= max_abs)
+    bad = np.flatnonzero(~ok)
+    assert bad.size == 0, [(int(i), float(got[i]), float(expected[i]), int(d[i])) for i in bad[:8]]

@@ -105,3 +105,70 @@ def test_bluestein_maps_zero_fill_and_truncate():
     src3 = im.bluestein_three_pass_perm(n, 6, [2, 3], 4, [4], [3, 2])
     assert src3.shape == (n,)
     assert ((src3 >= -1) & (src3 < n)).all()
+
+
+# ------------------------------------------- Bluestein maps by brute force
+
+def _stage_moves(line, radices):
+    """One identity-butterfly Stockham pass over a list of tags, element by
+    element: the butterfly b of a radix-R stage after radices multiplying to
+    P reads in[b + i*N/R] and writes its i-th input to out[j + (b - j)*R + i*P],
+    j = b mod P (kernel_ir.rs:1486-1727)."""
+    n = len(line)
+    p = 1
+    for r in radices:
+        out = [None] * n
+        for b in range(n // r):
+            j = b % p
+            for i in range(r):
+                out[j + (b - j) * r + i * p] = line[b + i * (n // r)]
+        assert None not in out
+        line = out
+        p *= r
+    return line
+
+
+def _bluestein_single_sim(n, m, radices):
+    """x zero-padded to M (tag -1), forward FFT_M, spectrum multiply (in
+    place), inverse FFT_M with the same radices, truncation to N
+    (bluestein_ir.rs:933-1089), all by explicit moves."""
+    a = list(range(n)) + [-1] * (m - n)
+    a = _stage_moves(a, radices)
+    a = _stage_moves(a, radices)
+    return np.array(a[:n])
+
+
+def _bluestein_three_pass_sim(n, n1, rad1, n2, rad2, rad3):
+    """The same over M = n1 * n2 in three passes on the matrix a[e*n2 + c]:
+    columns (length n1, rad1) in place, rows (length n2: forward rad2,
+    multiply, inverse rad2) in place, inverse columns (rad3) in place,
+    truncation to N."""
+    m = n1 * n2
+    a = list(range(n)) + [-1] * (m - n)
+    for c in range(n2):
+        col = _stage_moves([a[e * n2 + c] for e in range(n1)], rad1)
+        for e in range(n1):
+            a[e * n2 + c] = col[e]
+    for e in range(n1):
+        row = _stage_moves(_stage_moves(a[e * n2:(e + 1) * n2], rad2), rad2)
+        a[e * n2:(e + 1) * n2] = row
+    for c in range(n2):
+        col = _stage_moves([a[e * n2 + c] for e in range(n1)], rad3)
+        for e in range(n1):
+            a[e * n2 + c] = col[e]
+    return np.array(a[:n])
+
+
+@pytest.mark.parametrize("n,m,radices", [(11, 24, [2, 3, 4]), (11, 24, [4, 3, 2]), (5, 9, [3, 3]),
+                                         (13, 32, [2, 4, 4]), (7, 16, [16]), (17, 45, [5, 3, 3])])
+def test_bluestein_single_map_by_simulation(n, m, radices):
+    assert np.array_equal(im.bluestein_single_perm(n, m, radices), _bluestein_single_sim(n, m, radices))
+
+
+@pytest.mark.parametrize("n,n1,rad1,n2,rad2,rad3", [(11, 6, [2, 3], 4, [4], [3, 2]),
+                                                    (13, 4, [4], 8, [2, 4], [2, 2]),
+                                                    (23, 9, [3, 3], 6, [3, 2], [3, 3]),
+                                                    (29, 10, [5, 2], 6, [2, 3], [2, 5])])
+def test_bluestein_three_pass_map_by_simulation(n, n1, rad1, n2, rad2, rad3):
+    got = im.bluestein_three_pass_perm(n, n1, rad1, n2, rad2, rad3)
+    assert np.array_equal(got, _bluestein_three_pass_sim(n, n1, rad1, n2, rad2, rad3))

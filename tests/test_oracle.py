@@ -322,3 +322,31 @@ def test_real_convolution_is_circular_convolution():
     for oc in range(2):
         ref = _circ_conv2(xs[0], hm[2 * oc]) + _circ_conv2(xs[1], hm[2 * oc + 1])
         assert np.allclose(ym[oc], ref, atol=1e-12)
+
+
+# ------------------------------------------- mixed-storage FFTW corpora
+
+@pytest.mark.parametrize("corpus", ["fftw_precision_medium_f16_storage_v1.txt",
+                                    "fftw_precision_medium_f64_f32_storage_v1.txt"])
+def test_mixed_storage_corpora_pin_the_oracle(corpus):
+    """As the reference's CPU half of these corpora
+    (fftw_medium_f16_storage_golden.rs:264-300, ..._f64_f32_storage_golden.rs:
+    264-300): the f64 oracle on the storage-rounded inputs, rounded to the
+    storage type, reproduces FFTW's committed bits. Exact for all but values
+    within the oracle's f64 error of a rounding boundary: at most 1 ulp apart
+    (or, for the bins FFTW returns as exact zeros, within the oracle's f64
+    error of 2e-10 * N, the reference's CPU fixture tolerance) and at least
+    99.5% identical over the corpus."""
+    import golden_bits as gb
+    width, cases = gb.parse(os.path.join(GOLDEN, corpus))
+    total = exact = 0
+    for name, case in cases.items():
+        x = gb.storage_input(case, width)
+        got = gb.to_bits(gb.scalars(gb.oracle_output(case, x), case["kind"]), width)
+        d = gb.ulps(got, case["bits"], width)
+        n = int(np.prod(case["shape"]))
+        near = np.abs(gb.from_bits(got, width) - gb.from_bits(case["bits"], width)) <= 2e-10 * n
+        assert np.all((d <= 1) | near), (name, int(d.max()))
+        total += d.size
+        exact += int(np.sum(d == 0))
+    assert exact >= 0.995 * total, (exact, total)

@@ -16,7 +16,7 @@ import json
 import os
 import weakref
 from dataclasses import dataclass, field
-from typing import List, Optional, Sequence
+from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -530,6 +530,61 @@ class TransformIr:
             ir.convolution_lens.append(m)
         return ir
 
+    def lower(self):
+        """The IR variant TransformIr::build makes for this config
+        (application.rs:48-167), with the fields the HIP boundary reads."""
+        c = self.config
+        prec = c.precision
+        scalar = ScalarType.F64 if prec in (Precision.F64, Precision.F64ComputeF32Storage) else ScalarType.F32
+        storage = {Precision.F32: ScalarType.F32, Precision.F64: ScalarType.F64,
+                   Precision.F16StorageF32Compute: ScalarType.F16,
+                   Precision.F64ComputeF32Storage: ScalarType.F32}[prec]
+        if c.perform_convolution or c.kernel_convolution:
+            raise VkFftError(-3, "convolutions lower to ConvolutionIr, not TransformIr")
+        rank = len(c.dimensions)
+        zeros = tuple(ZeroPadPassIr(z[0], z[1], c.zero_padding_domain == ZeroPaddingDomain.Frequency)
+                      if z is not None else None for z in c.zero_padding[:rank])
+        norm = bool(c.normalize_inverse) and self.direction == Direction.Inverse
+        tun = None
+        if c.tuning is not None:
+            t = c.tuning
+            tun = (t.min_rader_direct_prime, t.max_rader_direct_prime, t.min_rader_fft_prime,
+                   t.max_rader_fft_prime, bool(t.allow_recursive_fft_rader or c.allow_recursive_fft_rader))
+
+        def one_dim(axis, n, batch):
+            alg, m = self.axis_algorithms[axis], self.convolution_lens[axis]
+            if alg == AlgorithmKind.Bluestein:
+                return BluesteinPipelineIr(n, m, batch, self.direction, scalar, storage, norm,
+                                           zeros[axis] if rank == 1 else None)
+            primes = tuple(p for p in _prime_factors(n) if p > 13) if alg == AlgorithmKind.Rader else ()
+            return RecursiveFftIr(n, batch, self.direction, scalar, storage, norm, primes, tun,
+                                  zeros[axis] if rank == 1 else None)
+
+        dense = all(v == 0 for v in c.input_buffer_axis_strides[:rank] + c.output_buffer_axis_strides[:rank]) and \
+            not c.input_buffer_batch_stride and not c.output_buffer_batch_stride
+        if c.transform == TransformKind.ComplexToComplex:
+            if rank == 1 and dense and not any(c.omit_dimension[:1]):
+                return one_dim(0, c.dimensions[0], c.batch_count)
+            return NdFftIr(tuple(c.dimensions), c.batch_count, self.direction, scalar, storage,
+                           tuple(NdAxisIr(i, one_dim(i, n, 1)) for i, n in enumerate(c.dimensions)),
+                           tuple(c.input_buffer_axis_strides[:rank]), tuple(c.output_buffer_axis_strides[:rank]),
+                           c.input_buffer_batch_stride, c.output_buffer_batch_stride,
+                           tuple(bool(o) for o in c.omit_dimension[:rank]), zeros)
+        if c.transform in (TransformKind.RealToComplex, TransformKind.ComplexToReal):
+            r2c = c.transform == TransformKind.RealToComplex
+            real_norm = bool(c.normalize_inverse) and not r2c
+            if rank == 1 and dense:
+                return RealFftIr(c.transform, c.dimensions[0], c.batch_count, scalar, storage, storage, real_norm,
+                                 zeros[0])
+            return NdRealFftIr(c.transform, tuple(c.dimensions), c.batch_count, scalar, storage, storage, real_norm,
+                               tuple(c.input_buffer_axis_strides[:rank]), tuple(c.output_buffer_axis_strides[:rank]),
+                               c.input_buffer_batch_stride, c.output_buffer_batch_stride,
+                               tuple(bool(o) for o in c.omit_dimension[:rank]), zeros)
+        if rank == 1 and dense:
+            return R2rIr(c.transform, c.dimensions[0], c.batch_count, self.direction, scalar, storage,
+                         bool(c.normalize_inverse) and self.direction == Direction.Inverse, zeros[0])
+        raise VkFftError(-3, "N-D or formatted DCT/DST IRs are planned from FftConfig here")
+
     def desc(self) -> _PlanDesc:
         c = self.config
         d = _PlanDesc()
@@ -891,6 +946,367 @@ def execute_chain(plans, d_in: int, d_out: int, stream: int = 0):
     L = plans[0]._L
     _check(L.vkfx_execute_chain(_plan_array(plans), len(plans), ctypes.c_void_p(d_in), ctypes.c_void_p(d_out),
                                 ctypes.c_void_p(stream or None)), L)
+
+
+# ------------------------------------------------- IR-driven runtime boundary
+#
+# vkfft-rs's NativeRuntime entry points receive only the built IR:
+# execute_transform_f32/f64(&TransformIr, input) (src/backend/native_runtime.rs:
+# 339-359) and submit_transform_f32/f64_async (:458-529), and callers build that
+# IR with TransformIr::build (e.g. native_runtime.rs:2206-2220). The classes
+# below mirror the fields of the IR variants the HIP boundary reads; desc_from_ir
+# derives the library's plan descriptor from those fields alone, and
+# NativeRuntime plans each IR on first use, keyed by the IR itself.
+
+class ScalarType(enum.IntEnum):
+    """ScalarType of the IRs (src/precision.rs): compute `scalar` and the
+    caller-visible storage scalar."""
+    F16 = 0
+    F32 = 1
+    F64 = 2
+
+
+@dataclass(frozen=True)
+class ZeroPadPassIr:
+    """ZeroPadPassIr (src/zero_pad_ir.rs:50-64): the zero interval [left, right)
+    of the logical axis and its domain (spatial: forward input / inverse
+    output; frequency: forward output / inverse input, zero_pad_ir.rs:38-46)."""
+    left: int
+    right: int
+    frequency: bool = False
+
+
+@dataclass(frozen=True)
+class RecursiveFftIr:
+    """RecursiveFftIr (src/recursive_ir.rs:1662-1696). `rader_primes`: the
+    primes of the DirectRader / FftRader nodes of `root` at any depth
+    (RecursiveFftNodeIr, recursive_ir.rs:917-922); `normalize`: the
+    StoreSharedToGlobal normalize flag of the root's final store
+    (kernel_ir.rs:1442-1445, set at :1582-1585)."""
+    logical_len: int
+    batch_count: int
+    direction: Direction
+    scalar: ScalarType
+    external_scalar: ScalarType
+    normalize: bool = False
+    rader_primes: Tuple[int, ...] = ()
+    # the effective PlannerTuning (config.rs:367-380) as (min/max direct prime,
+    # min/max FFT prime, allow_recursive_fft_rader); None = the device default
+    scheduler_tuning: Optional[Tuple[int, int, int, int, bool]] = None
+    zero_pad_pass: Optional[ZeroPadPassIr] = None
+
+
+@dataclass(frozen=True)
+class BluesteinPipelineIr:
+    """BluesteinPipelineIr (src/bluestein_ir.rs:436-451); `normalize` is the
+    postprocess pass's Postprocess { normalize } (bluestein_ir.rs:29, 658)."""
+    logical_len: int
+    convolution_len: int
+    batch_count: int
+    direction: Direction
+    scalar: ScalarType
+    external_scalar: ScalarType
+    normalize: bool = False
+    zero_pad_pass: Optional[ZeroPadPassIr] = None
+
+
+@dataclass(frozen=True)
+class NdAxisIr:
+    """NdAxisIr (src/nd_ir.rs:528-537): the axis and its one-dimensional
+    transform (OneDimFftIr::Recursive or ::Bluestein)."""
+    axis: int
+    transform: object
+
+
+@dataclass(frozen=True)
+class NdFftIr:
+    """NdFftIr (src/nd_ir.rs:541-557). Strides are in stored elements, 0 =
+    dense; `zero_padding` holds one ZeroPadPassIr (or None) per axis, the
+    ranges of the NdZeroPadPassIr."""
+    dimensions: Tuple[int, ...]
+    batch_count: int
+    direction: Direction
+    scalar: ScalarType
+    external_scalar: ScalarType
+    axes: Tuple[NdAxisIr, ...]
+    input_buffer_axis_strides: Tuple[int, ...] = ()
+    output_buffer_axis_strides: Tuple[int, ...] = ()
+    input_buffer_batch_stride: int = 0
+    output_buffer_batch_stride: int = 0
+    omitted_axes: Tuple[bool, ...] = ()
+    zero_padding: Tuple[Optional[ZeroPadPassIr], ...] = ()
+
+
+@dataclass(frozen=True)
+class RealFftIr:
+    """RealFftIr (src/real_ir.rs:264-279): R2C (forward) or C2R (inverse) of
+    `length` reals; `normalize` is the C2R PreprocessEvenHalf { normalize }
+    (real_ir.rs:55, 412) or the odd-length inner transform's store flag."""
+    kind: TransformKind
+    length: int
+    batch_count: int
+    scalar: ScalarType
+    input_storage_scalar: ScalarType
+    output_storage_scalar: ScalarType
+    normalize: bool = False
+    zero_pad_pass: Optional[ZeroPadPassIr] = None
+
+
+@dataclass(frozen=True)
+class NdRealFftIr:
+    """NdRealFftIr (src/nd_real_ir.rs:754-870): R2C / C2R over `dimensions`
+    (the last axis real), with the formatted layouts and zero padding of the
+    compact-spectrum application."""
+    kind: TransformKind
+    dimensions: Tuple[int, ...]
+    batch_count: int
+    scalar: ScalarType
+    input_storage_scalar: ScalarType
+    output_storage_scalar: ScalarType
+    normalize: bool = False
+    input_buffer_axis_strides: Tuple[int, ...] = ()
+    output_buffer_axis_strides: Tuple[int, ...] = ()
+    input_buffer_batch_stride: int = 0
+    output_buffer_batch_stride: int = 0
+    omitted_axes: Tuple[bool, ...] = ()
+    zero_padding: Tuple[Optional[ZeroPadPassIr], ...] = ()
+
+
+@dataclass(frozen=True)
+class R2rIr:
+    """R2rIr (src/r2r_ir.rs:600-620): one DCT/DST type over `length` reals,
+    normalize / normalization_scale of the inverse partner."""
+    kind: TransformKind
+    length: int
+    batch_count: int
+    direction: Direction
+    scalar: ScalarType
+    external_scalar: ScalarType
+    normalize: bool = False
+    zero_pad_pass: Optional[ZeroPadPassIr] = None
+
+
+def _prime_factors(n: int) -> List[int]:
+    out, p = [], 2
+    while p * p <= n:
+        while n % p == 0:
+            out.append(p)
+            n //= p
+        p += 1
+    if n > 1:
+        out.append(n)
+    return out
+
+
+def _precision_of(scalar: ScalarType, storage: ScalarType) -> Precision:
+    """(compute scalar, storage scalar) -> Precision (config.rs:108-145)."""
+    table = {(ScalarType.F32, ScalarType.F32): Precision.F32, (ScalarType.F64, ScalarType.F64): Precision.F64,
+             (ScalarType.F32, ScalarType.F16): Precision.F16StorageF32Compute,
+             (ScalarType.F64, ScalarType.F32): Precision.F64ComputeF32Storage}
+    if (scalar, storage) not in table:
+        raise VkFftError(-4, f"UnsupportedPrecision: no MI355X kernels for {scalar.name} compute with "
+                             f"{storage.name} storage")
+    return table[(scalar, storage)]
+
+
+def _one_dim_algorithm(t) -> Tuple[AlgorithmKind, int, bool]:
+    """(axis algorithm, Bluestein M, normalize) of a OneDimFftIr."""
+    if isinstance(t, BluesteinPipelineIr):
+        return AlgorithmKind.Bluestein, t.convolution_len, t.normalize
+    if isinstance(t, RecursiveFftIr):
+        return (AlgorithmKind.Rader if t.rader_primes else AlgorithmKind.Stockham), 0, t.normalize
+    raise VkFftError(-7, f"InvalidKernelIr: {type(t).__name__} is not a one-dimensional FFT IR")
+
+
+def _set_zero(d: _PlanDesc, axis: int, z: Optional[ZeroPadPassIr]):
+    if z is not None and z.right > z.left:
+        d.zero_left[axis], d.zero_right[axis] = z.left, z.right
+        d.zero_frequency = int(z.frequency)
+
+
+def _set_layout(d: _PlanDesc, ir):
+    for i, v in enumerate(ir.input_buffer_axis_strides):
+        d.in_axis_stride[i] = v
+    for i, v in enumerate(ir.output_buffer_axis_strides):
+        d.out_axis_stride[i] = v
+    d.in_batch_stride = ir.input_buffer_batch_stride
+    d.out_batch_stride = ir.output_buffer_batch_stride
+    d.omit_dimension = sum(1 << i for i, o in enumerate(ir.omitted_axes) if o)
+    for i, z in enumerate(ir.zero_padding):
+        _set_zero(d, i, z)
+
+
+def desc_from_ir(ir) -> _PlanDesc:
+    """The library's plan descriptor from the IR's own fields (the planner's
+    per-axis decisions included): no FftConfig is consulted."""
+    d = _PlanDesc()
+    if isinstance(ir, (RecursiveFftIr, BluesteinPipelineIr)):      # TransformIr::Complex1d
+        d.rank, d.dims[0], d.batch = 1, ir.logical_len, ir.batch_count
+        d.transform = int(TransformKind.ComplexToComplex)
+        d.precision = int(_precision_of(ir.scalar, ir.external_scalar))
+        d.direction = int(ir.direction)
+        alg, m, norm = _one_dim_algorithm(ir)
+        d.axis_algorithm[0], d.convolution_len[0], d.normalize = int(alg), m, int(norm)
+        _set_zero(d, 0, ir.zero_pad_pass)
+        t = getattr(ir, "scheduler_tuning", None)
+        if t is not None:
+            d.custom_tuning, d.tuning = 1, _PlannerTuning(t[0], t[1], t[2], t[3], int(t[4]))
+        return d
+    if isinstance(ir, NdFftIr):                                      # TransformIr::ComplexNd
+        d.rank = len(ir.dimensions)
+        for i, n in enumerate(ir.dimensions):
+            d.dims[i] = n
+        d.batch = ir.batch_count
+        d.transform = int(TransformKind.ComplexToComplex)
+        d.precision = int(_precision_of(ir.scalar, ir.external_scalar))
+        d.direction = int(ir.direction)
+        norm = False
+        for ax in ir.axes:
+            alg, m, n_ = _one_dim_algorithm(ax.transform)
+            d.axis_algorithm[ax.axis], d.convolution_len[ax.axis] = int(alg), m
+            norm = norm or n_
+        d.normalize = int(norm)
+        _set_layout(d, ir)
+        return d
+    if isinstance(ir, (RealFftIr, NdRealFftIr)):                     # TransformIr::Real / RealNd
+        dims = (ir.length,) if isinstance(ir, RealFftIr) else ir.dimensions
+        d.rank = len(dims)
+        for i, n in enumerate(dims):
+            d.dims[i] = n
+        d.batch = ir.batch_count
+        if ir.kind not in (TransformKind.RealToComplex, TransformKind.ComplexToReal):
+            raise VkFftError(-7, "InvalidKernelIr: a real FFT IR is R2C or C2R")
+        d.transform = int(ir.kind)
+        storage = ir.input_storage_scalar if ir.kind == TransformKind.RealToComplex else ir.output_storage_scalar
+        d.precision = int(_precision_of(ir.scalar, storage))
+        d.direction = int(Direction.Forward if ir.kind == TransformKind.RealToComplex else Direction.Inverse)
+        d.normalize = int(ir.normalize)
+        d.use_library_planner = 1          # half-length / full-complex axes are planned inside
+        if isinstance(ir, RealFftIr):
+            _set_zero(d, 0, ir.zero_pad_pass)
+        else:
+            _set_layout(d, ir)
+        return d
+    if isinstance(ir, R2rIr):                                        # TransformIr::RealToReal
+        d.rank, d.dims[0], d.batch = 1, ir.length, ir.batch_count
+        if not ir.kind.is_r2r:
+            raise VkFftError(-7, "InvalidKernelIr: an R2rIr is a DCT or DST")
+        d.transform = int(ir.kind)
+        d.precision = int(_precision_of(ir.scalar, ir.external_scalar))
+        d.direction = int(ir.direction)
+        d.normalize = int(ir.normalize)
+        d.use_library_planner = 1
+        _set_zero(d, 0, ir.zero_pad_pass)
+        return d
+    raise VkFftError(-3, f"UnsupportedKernelPath: no MI355X plan for {type(ir).__name__}")
+
+
+class NativeRuntime:
+    """The IR-driven boundary (the Rust HipNativeRuntime of INTEGRATION.md):
+    execute_transform_f32/f64 and submit take only the IR, plan it on first use
+    from desc_from_ir and keep the plan keyed by the IR."""
+
+    def __init__(self, ctx: "HipExecutionContext"):
+        self.ctx = ctx
+        self._plans = {}
+
+    def plan_for(self, ir) -> "Plan":
+        p = self._plans.get(ir)
+        if p is None or not p.handle:
+            p = Plan(self.ctx, ir, desc=desc_from_ir(ir))
+            self._plans[ir] = p
+        return p
+
+    @staticmethod
+    def _storage(ir):
+        if isinstance(ir, (RealFftIr, NdRealFftIr)):
+            return ir.input_storage_scalar if ir.kind == TransformKind.RealToComplex else ir.output_storage_scalar
+        return ir.external_scalar
+
+    def _run(self, ir, x: np.ndarray, host_scalar):
+        plan = self.plan_for(ir)
+        storage = self._storage(ir)
+        xs = np.ascontiguousarray(x).reshape(-1)
+        scal = xs.view(host_scalar) if np.iscomplexobj(xs) else xs.astype(host_scalar, copy=False)
+        if storage == ScalarType.F16:
+            scal = scal.astype(np.float16)      # Binary16::from_f32, round to nearest even
+        scal = np.ascontiguousarray(scal)
+        if scal.nbytes != plan.in_bytes:
+            raise VkFftError(-5, f"InputLengthMismatch {{ expected: {plan.in_bytes}, actual: {scal.nbytes} }}")
+        real = ctypes.c_int32()
+        _check(self.ctx._L.vkfx_plan_output_info(plan.handle, ctypes.byref(real), None), self.ctx._L)
+        sdt = {ScalarType.F16: np.float16, ScalarType.F32: np.float32, ScalarType.F64: np.float64}[storage]
+        out = np.empty(plan.out_bytes // np.dtype(sdt).itemsize, dtype=sdt)
+        _check(self.ctx._L.vkfx_execute_host(plan.handle, scal.ctypes.data, scal.nbytes, out.ctypes.data,
+                                             out.nbytes), self.ctx._L)
+        y = out.astype(host_scalar, copy=False)
+        return y if real.value else y.view(np.complex64 if host_scalar == np.float32 else np.complex128)
+
+    def execute_transform_f32(self, ir, x: np.ndarray) -> np.ndarray:
+        """native_runtime.rs:339-349: Complex32 / f32 in, Complex32 / f32 out."""
+        if ir.scalar == ScalarType.F64 and self._storage(ir) == ScalarType.F64:
+            raise VkFftError(-4, "execute_transform_f32 needs an F32-family TransformIr")
+        return self._run(ir, x, np.float32)
+
+    def execute_transform_f64(self, ir, x: np.ndarray) -> np.ndarray:
+        """native_runtime.rs:351-359: Complex64 / f64 in and out."""
+        if ir.scalar != ScalarType.F64 or self._storage(ir) != ScalarType.F64:
+            raise VkFftError(-4, "execute_transform_f64 needs an F64 TransformIr")
+        return self._run(ir, x, np.float64)
+
+    def submit_transform_async(self, ir, x: np.ndarray) -> "IrTicket":
+        """NativeAsyncRuntime::submit_transform_f32/f64_async (native_runtime.rs:
+        458-529): the same lazy plan; the ticket's wait returns complex values
+        for every IR kind ({v, 0} for real outputs, whose .re
+        finish_transform_output32/64 takes, native_runtime.rs:2045-2087)."""
+        plan = self.plan_for(ir)
+        host = np.float64 if ir.scalar == ScalarType.F64 and self._storage(ir) == ScalarType.F64 else np.float32
+        return IrTicket(self, plan, ir, x, host)
+
+    def close(self):
+        for p in self._plans.values():
+            p.close()
+        self._plans.clear()
+
+
+class IrTicket:
+    """A submitted IR transform (vkfx_submit_host / vkfx_ticket_wait_complex)."""
+
+    def __init__(self, rt: NativeRuntime, plan: "Plan", ir, x: np.ndarray, host_scalar):
+        L = rt.ctx._L
+        self._L, self.plan, self._host = L, plan, host_scalar
+        storage = rt._storage(ir)
+        xs = np.ascontiguousarray(x).reshape(-1)
+        scal = xs.view(host_scalar) if np.iscomplexobj(xs) else xs.astype(host_scalar, copy=False)
+        if storage == ScalarType.F16:
+            scal = scal.astype(np.float16)
+        self._x = np.ascontiguousarray(scal)
+        self._sdt = {ScalarType.F16: np.float16, ScalarType.F32: np.float32, ScalarType.F64: np.float64}[storage]
+        widened = ctypes.c_uint64()
+        _check(L.vkfx_plan_output_info(plan.handle, None, ctypes.byref(widened)), L)
+        self._out = np.empty(int(widened.value) // np.dtype(self._sdt).itemsize, dtype=self._sdt)
+        self.handle = ctypes.c_void_p()
+        _check(L.vkfx_submit_host(plan.handle, self._x.ctypes.data, self._x.nbytes, ctypes.byref(self.handle)), L)
+        plan.ctx._live_tickets.add(self)
+
+    def wait(self) -> np.ndarray:
+        if not self.handle:
+            raise VkFftError(-2, "ticket was released")
+        _check(self._L.vkfx_ticket_wait_complex(self.handle, self._out.ctypes.data, self._out.nbytes), self._L)
+        self.close()
+        y = self._out.astype(self._host, copy=False)
+        return y.view(np.complex64 if self._host == np.float32 else np.complex128)
+
+    def close(self):
+        if self.handle:
+            self._L.vkfx_ticket_destroy(self.handle)
+        self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class HipExecutionContext:
