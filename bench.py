@@ -152,8 +152,8 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
             x = torch.randn(in_bytes // fsz, device="cuda", generator=gen, dtype=fdt)
         else:                         # uniform[-1,1) re and im
             x = torch.rand(in_bytes // fsz, device="cuda", generator=gen, dtype=fdt) * 2 - 1
-        y = torch.empty(out_bytes // fsz, device="cuda", dtype=fdt)
-        z = torch.empty(in_bytes // fsz, device="cuda", dtype=fdt) if len(plans) == 2 else None
+        y = torch.zeros(out_bytes // fsz, device="cuda", dtype=fdt)  # touched before timing
+        z = torch.zeros(in_bytes // fsz, device="cuda", dtype=fdt) if len(plans) == 2 else None
         bufs.append((x, y, z))
     s = stream.cuda_stream
 
@@ -727,8 +727,9 @@ def main():
             if name == "c1":
                 continue
             cfg = dict(CONFIGS[name])
-            # the other configs' steps are 1-6 ms: at most 30 keep the run short
-            ksteps = min(steps, 30)
+            # at least 50 steps: the mean of a short region weighs the first
+            # steps' dispatch ramp more (C5a: 0.255 ms at 20 steps, 0.234 at 200)
+            ksteps = max(steps, 50)
             r = run_gpu(cfg, ksteps, warmup, args.rotate, check=None if args.no_check else make_check(cfg, threads))
             row = summarize(name, cfg, r, ksteps, warmup, threads, False)
             acc = row.pop("accuracy") or {}

@@ -3,6 +3,8 @@
 #include <hip/hip_ext.h>
 
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "kernels.hpp"
@@ -171,6 +173,22 @@ static KernelFn pick_kernel(KernelKind kind, int prec, int dir, int flags) {
                      : (dir < 0 ? pick_f64_fwd(kind, wide, direct, edge) : pick_f64_inv(kind, wide, direct, edge));
 }
 
+// Raises a kernel's dynamic-LDS limit once per (device, kernel) to the
+// largest size launched so far: the attribute persists, and setting it on
+// every launch costs host time on the launch path.
+static int raise_lds_limit(const void* fn, size_t bytes) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, size_t> done;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = done[{dev, fn}];
+    if (have >= bytes) return (int)hipSuccess;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) have = bytes;
+    return (int)e;
+}
+
 const void* fft_kernel_fn(KernelKind kind, int prec, int dir, const FixedKernel* fixed, int flags) {
     if (kind < 0 || kind >= KK_COUNT || (dir != -1 && dir != 1) || (prec != 0 && prec != 1)) return nullptr;
     if (fixed) return (const void*)fixed->fn;
@@ -188,9 +206,8 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     args.nblk = grid;
     if (xcd_groups(kind)) args.flags |= KF_XCD_GROUPS;
     if (lds_bytes > 65536) {
-        hipError_t e =
-            hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-        if (e != hipSuccess) return (int)e;
+        int e = raise_lds_limit((const void*)fn, lds_bytes);
+        if (e != (int)hipSuccess) return e;
     }
     if (t_begin && t_end) {
         void* kargs[1] = {&args};
