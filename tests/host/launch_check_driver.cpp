@@ -34,6 +34,7 @@ static KArgs rader_args() {
     a.in_es = a.out_es = 1;
     static const int table = 0;
     a.rtab = &table;
+    a.flags = KF_RADER;
     return a;
 }
 
@@ -48,12 +49,16 @@ int main() {
            hipErrorInvalidConfiguration);
     expect("rader f64 sized for f32", check_launch(KK_PLAIN, 1, -1, r, block, two, limit, nullptr),
            hipErrorInvalidConfiguration);
+    KArgs f = r;
+    f.flags = 0;
+    expect("rader stages without KF_RADER", check_launch(KK_PLAIN, 0, -1, f, block, two, limit, nullptr),
+           hipErrorInvalidConfiguration);
     KArgs d = r;
-    d.flags = KF_DYN_DIRECT;
+    d.flags |= KF_DYN_DIRECT;
     expect("rader with HBM-direct stages", check_launch(KK_PLAIN, 0, -1, d, block, two, limit, nullptr),
            hipErrorInvalidConfiguration);
     KArgs e = r;
-    e.flags = KF_EDGE;
+    e.flags |= KF_EDGE;
     e.zr = e.N;
     expect("rader with edge work", check_launch(KK_PLAIN, 0, -1, e, block, two, limit, nullptr),
            hipErrorInvalidConfiguration);
@@ -86,6 +91,7 @@ int main() {
     // ordinary launches around the new rules
     KArgs p = s;
     p.rtab = nullptr;
+    p.flags = 0;
     expect("plain staged", check_launch(KK_PLAIN, 0, -1, p, 32, (size_t)p.G * p.LS * 8, limit, nullptr),
            hipSuccess);
     expect("plain, block != G * TT", check_launch(KK_PLAIN, 0, -1, p, 64, (size_t)p.G * p.LS * 8, limit, nullptr),

@@ -237,6 +237,8 @@ def test_rader_recursive_opt_in_runs_the_rader_tree(hip_ctx, prec):
     assert "rader_fallback" not in desc
     assert desc["rader"]["mode"] == "fft" and desc["rader"]["convolution_len"] == 4098
     assert desc["rader"]["nested_rader_primes"] == [683]
+    # 683 -> 682 = 2 * 11 * 31 convolves by FFT, 31 by direct multiplication
+    assert desc["rader"]["nested"]["fft_convolution"] == {"683": RADER_FFT_STAGES[683]}
     x = rand(n * batch, 3, prec)
     ref = oracle_c2c(x, n)
     tol = TOL[F32] if prec == F32 else max(TOL[F64], 2 * o.rel_l2(ref, np.fft.fft(x.reshape(batch, n), axis=1)
@@ -255,7 +257,11 @@ def test_rader_recursive_opt_in_runs_the_rader_tree(hip_ctx, prec):
 # reference folds Rader into the mixed-radix tree (mixed_ir.rs); here each
 # such factor is a Rader stage of the Stockham sequence
 RADER_MIXED = [(17 * 64, [17]), (19 * 12, [19]), (23 * 5, [23]), (17 * 19, [17, 19]), (2 * 29 * 31, [29, 31]),
-               (47 * 4, [47]), (97 * 8, [97]), (17 * 17 * 3, [17, 17])]
+               (47 * 4, [47]), (97 * 8, [97]), (17 * 17 * 3, [17, 17]), (89 * 4, [89]), (113 * 2, [113]),
+               (193 * 2, [193]), (257 * 4, [257])]
+# Rader stages from 89 on convolve by FFT (the reference's FFT-Rader node):
+# the plan reports the sub-radices of each such stage's length p - 1 FFTs
+RADER_FFT_STAGES = {89: [8, 11], 97: [8, 4, 3], 113: [16, 7], 193: [8, 8, 3], 257: [16, 16], 683: [2, 11, 31]}
 
 
 @pytest.mark.parametrize("n,primes", RADER_MIXED)
@@ -268,6 +274,8 @@ def test_rader_inside_mixed_radix(hip_ctx, n, primes, prec):
     desc = hip_ctx.plan(ir).describe()
     assert "rader_fallback" not in desc, desc
     assert desc["rader_mixed"]["rader_primes"] == primes
+    fft_stages = {int(k): v for k, v in desc["rader_mixed"]["fft_convolution"].items()}
+    assert fft_stages == {p: RADER_FFT_STAGES[p] for p in primes if p >= 89}, fft_stages
     ref = oracle_c2c(x, n)
     npref = np.fft.fft(x.reshape(batch, n).astype(np.complex128), axis=1).reshape(-1)
     tol = TOL[prec] if prec == F32 else max(TOL[F64], 2 * o.rel_l2(ref, npref))

@@ -2,8 +2,8 @@
 applies before any dispatch, built with g++ beside a driver of accepted and
 rejected launches (tests/host/launch_check_driver.cpp). Covers the Rader
 stage scratch region (2 G LS elements), Rader stages on kernels that have no
-scratch region (fixed shapes, HBM-direct and edge kernels), and the ordinary
-block / LDS / direction checks."""
+scratch region (fixed shapes, HBM-direct and edge kernels) or without the
+KF_RADER instantiation, and the ordinary block / LDS / direction checks."""
 import os
 import shutil
 import subprocess

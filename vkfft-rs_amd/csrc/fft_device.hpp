@@ -564,9 +564,203 @@ __device__ __noinline__ void stage_rader(cpx<T>* __restrict__ line, cpx<T>* __re
     __syncthreads();
 }
 
+// One radix-R stage of the length-L FFTs inside an FFT-mode Rader stage: NB
+// sequences at stride q (element stride 1) in `src`, out of place into
+// `dst`, Stockham order (natural-order output after the last stage). Stage
+// twiddles W_L^(j i L/(Pp R)) from `roots` (exp(-2 pi i k/L)); SG is the
+// sign of the sub-FFT.
+template <typename T, int SG, int R>
+__device__ __noinline__ void rader_sub_stage(const cpx<T>* __restrict__ src, cpx<T>* __restrict__ dst,
+                                             const int NB, const int L, const int q, const int Pp, const int TT,
+                                             const int t, const void* roots) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)src));
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)dst));
+#endif
+    const int nb = L / R, total = NB * nb, tstep = L / (Pp * R);
+#pragma unroll 1
+    for (int u = t; u < total; u += TT) {
+        const int seq = u / nb, bb = u - seq * nb, j = bb % Pp;
+        const cpx<T>* s = src + seq * q + bb;
+        cpx<T> v[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) v[i] = s[i * nb];
+        if (j > 0) {
+#pragma unroll
+            for (int i = 1; i < R; ++i) v[i] = twmul<SG>(v[i], ld_table<T>(roots, j * i * tstep));
+        }
+        dft<R, SG>(v);
+        cpx<T>* d = dst + seq * q + j + (bb - j) * R;
+#pragma unroll
+        for (int k = 0; k < R; ++k) d[k * Pp] = v[k];
+    }
+}
+
+// The same for a prime sub-radix R in (13, kRaderSubPrimeMax]: the R-point
+// DFT by direct multiplication (the direct Rader node of the reference's
+// tree computes the same sums), pairing x[m] with x[R - m] as dft_odd does
+// and writing each output pair as soon as it is formed, so only the paired
+// sums stay in registers; the roots are compile-time constants.
+template <typename T, int SG, int R>
+__device__ __noinline__ void rader_sub_stage_prime(const cpx<T>* __restrict__ src, cpx<T>* __restrict__ dst,
+                                                   const int NB, const int L, const int q, const int Pp,
+                                                   const int TT, const int t, const void* roots) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)src));
+    __builtin_assume(__builtin_amdgcn_is_shared((const void*)dst));
+#endif
+    constexpr int H = (R - 1) / 2;
+    const int nb = L / R, total = NB * nb, tstep = L / (Pp * R);
+#pragma unroll 1
+    for (int u = t; u < total; u += TT) {
+        const int seq = u / nb, bb = u - seq * nb, j = bb % Pp;
+        const cpx<T>* s = src + seq * q + bb;
+        cpx<T>* d = dst + seq * q + j + (bb - j) * R;
+        const cpx<T> x0 = s[0];
+        cpx<T> sa[H], sb[H];
+#pragma unroll
+        for (int m = 1; m <= H; ++m) {
+            cpx<T> lo = s[m * nb], hi = s[(R - m) * nb];
+            if (j > 0) {
+                lo = twmul<SG>(lo, ld_table<T>(roots, j * m * tstep));
+                hi = twmul<SG>(hi, ld_table<T>(roots, j * (R - m) * tstep));
+            }
+            if constexpr (kIndexTest) {
+                d[m * Pp] = lo;
+                d[(R - m) * Pp] = hi;
+            }
+            sa[m - 1] = lo + hi;
+            sb[m - 1] = lo - hi;
+        }
+        if constexpr (kIndexTest) {
+            d[0] = x0;
+            continue;
+        }
+        cpx<T> y0 = x0;
+#pragma unroll
+        for (int m = 0; m < H; ++m) y0 = y0 + sa[m];
+        d[0] = y0;
+#pragma unroll
+        for (int k = 1; k <= H; ++k) {
+            cpx<T> A = x0;
+            cpx<T> B = mk((T)0, (T)0);
+#pragma unroll
+            for (int m = 1; m <= H; ++m) {
+                const cpx<T> w = unit_root<R, -1, T>(m * k);  // cos and -sin of 2 pi m k / R
+                A = mk(A.re + sa[m - 1].re * w.re, A.im + sa[m - 1].im * w.re);
+                B = mk(B.re - sb[m - 1].re * w.im, B.im - sb[m - 1].im * w.im);
+            }
+            const cpx<T> iB = muli<SG>(B);
+            d[k * Pp] = A + iB;
+            d[(R - k) * Pp] = A - iB;
+        }
+    }
+}
+
+template <typename T, int SG>
+__device__ __forceinline__ void rader_sub_stage_radix(int R, const cpx<T>* src, cpx<T>* dst, int NB, int L, int q,
+                                                      int Pp, int TT, int t, const void* roots) {
+    switch (R) {
+        case 2: rader_sub_stage<T, SG, 2>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 3: rader_sub_stage<T, SG, 3>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 4: rader_sub_stage<T, SG, 4>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 5: rader_sub_stage<T, SG, 5>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 7: rader_sub_stage<T, SG, 7>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 8: rader_sub_stage<T, SG, 8>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 9: rader_sub_stage<T, SG, 9>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 11: rader_sub_stage<T, SG, 11>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 13: rader_sub_stage<T, SG, 13>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 16: rader_sub_stage<T, SG, 16>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 17: rader_sub_stage_prime<T, SG, 17>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 19: rader_sub_stage_prime<T, SG, 19>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 23: rader_sub_stage_prime<T, SG, 23>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 29: rader_sub_stage_prime<T, SG, 29>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        case 31: rader_sub_stage_prime<T, SG, 31>(src, dst, NB, L, q, Pp, TT, t, roots); break;
+        default: break;  // the host plans no other sub-radix (rader_sub_schedule)
+    }
+}
+
+// FFT-mode Rader stage (prime radix q >= kRaderFftStageMin, table layout in
+// kernels.hpp): the gather of stage_rader into `scr` (butterfly b's inputs
+// at b*q + slot[i], x0 at b*q + L), the forward length-L FFTs of all NB
+// butterflies, the spectrum multiply, the inverse FFTs, and the outputs
+// X[0] = x0 + A[0], X[g^m] = x0 + conv[m] written to the Stockham positions
+// j + (b - j) q + {0, g^m} P. Once gathered, the line's own LDS region is
+// free until the outputs: the length-L FFTs ping-pong between `scr` and the
+// line region (unpadded, sequences at the same b*q offsets; an even number
+// of sub-stages in all brings the result back to `scr`), and X[0] waits in
+// the line region's slot b*q + L, which no sub-stage writes.
+template <typename T, int S>
+__device__ __noinline__ void stage_rader_fft(cpx<T>* __restrict__ line, cpx<T>* __restrict__ scr, const int N,
+                                             const int P, const int q, const int TT, const int t, const int ps,
+                                             const StageTw tw, const unsigned char* rt) {
+    const int L = q - 1, NB = N / q, step = N / (P * q);
+    const int* hdr = (const int*)rt;
+    const int* slot = hdr + 16;
+    const int* pw = slot + q;
+    const unsigned char* data = rt + rader_fft_data_offset(q);
+    const void* roots = data;
+    const void* spec = data + (size_t)(S < 0 ? 1 : 2) * L * sizeof(cpx<T>);
+    const int nsub = hdr[0];
+    for (int e = t; e < N; e += TT) {
+        const int i = e / NB, b = e - i * NB, j = b % P;
+        cpx<T> v = line[lpad(e, ps)];
+        if (i > 0 && j > 0) v = twmul<S>(v, stage_root<T>(tw, j * i * step, P >= kScatterP));
+        scr[b * q + slot[i]] = v;
+    }
+    __syncthreads();
+    cpx<T>* src = scr;
+    cpx<T>* dst = line;
+    int Pp = 1;
+    for (int k = 0; k < nsub; ++k) {
+        const int R = hdr[1 + k];
+        rader_sub_stage_radix<T, -1>(R, src, dst, NB, L, q, Pp, TT, t, roots);
+        __syncthreads();
+        cpx<T>* tmp = src;
+        src = dst;
+        dst = tmp;
+        Pp *= R;
+    }
+    // A *= FFT_L(b) / L; X[0] = x0 + A[0] parks in line[b*q + L]
+    for (int e = t; e < NB * L; e += TT) {
+        const int b = e / L, k = e - b * L;
+        cpx<T> a = src[b * q + k];
+        if (k == 0) line[b * q + L] = scr[b * q + L] + a;
+        if constexpr (!kIndexTest) a = cmul(a, ld_table<T>(spec, k));
+        src[b * q + k] = a;
+    }
+    __syncthreads();
+    Pp = 1;
+    for (int k = 0; k < nsub; ++k) {
+        const int R = hdr[1 + k];
+        rader_sub_stage_radix<T, 1>(R, src, dst, NB, L, q, Pp, TT, t, roots);
+        __syncthreads();
+        cpx<T>* tmp = src;
+        src = dst;
+        dst = tmp;
+        Pp *= R;
+    }
+    // src == scr: conv[m] + x0, then X[0] into the x0 slot
+    for (int e = t; e < NB * L; e += TT) {
+        const int b = e / L, m = e - b * L;
+        scr[b * q + m] = scr[b * q + L] + scr[b * q + m];
+    }
+    __syncthreads();
+    for (int b = t; b < NB; b += TT) scr[b * q + L] = line[b * q + L];
+    __syncthreads();
+    for (int e = t; e < N; e += TT) {
+        const int b = e / q, r = e - b * q, j = b % P;
+        const int out = r == L ? 0 : pw[r];
+        line[lpad((b - j) * q + j + out * P, ps)] = scr[b * q + r];
+    }
+    __syncthreads();
+}
+
 // Runs every stage of a runtime radix list over the line at `line` (in LDS);
-// a Rader stage uses `scr` and its table block in `rtab`.
-template <typename T, int S, bool WIDE>
+// with RAD, a Rader stage (radix above kMaxStockhamRadix) uses `scr` and its
+// table block in `rtab` (RAD instantiations only, so the Rader stages'
+// registers stay out of the other kernels).
+template <typename T, int S, bool WIDE, bool RAD = false>
 __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int N, const int TT,
                                            const int t, const int ps, const int nst,
                                            const int* __restrict__ radix, const StageTw& tw,
@@ -574,7 +768,12 @@ __device__ __forceinline__ void run_stages(cpx<T>* __restrict__ line, const int 
                                            const int* roff = nullptr) {
     int P = 1;
     for (int s = 0; s < nst; ++s) {
-        if (radix[s] > kMaxStockhamRadix)
+        if (!RAD)
+            stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, nullptr, 0, (T)1);
+        else if (radix[s] > kMaxStockhamRadix && (roff[s] & kRaderFftStage))
+            stage_rader_fft<T, S>(line, scr, N, P, radix[s], TT, t, ps, tw,
+                                  (const unsigned char*)rtab + (roff[s] & ~kRaderFftStage));
+        else if (radix[s] > kMaxStockhamRadix)
             stage_rader<T, S>(line, scr, N, P, radix[s], TT, t, ps, tw, (const unsigned char*)rtab + roff[s]);
         else
             stage_rt_radix<T, S, WIDE, SM_LDS>(radix[s], line, N, P, TT, t, ps, tw, nullptr, nullptr, 0, (T)1);

@@ -911,7 +911,7 @@ __global__ __launch_bounds__(512) void k_rader_direct(const KArgs a) {
 
 // ------------------------------------------------------- dynamic kernel
 
-template <typename T, int S, class IO, bool WIDE>
+template <typename T, int S, class IO, bool WIDE, bool RAD = false>
 __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     cpx<T>* lds = reinterpret_cast<cpx<T>*>(smem_raw);
@@ -926,12 +926,12 @@ __global__ __launch_bounds__(512) void k_dyn(const KArgs a) {
     const StageTw tw{a.tw, a.swlo, a.swhi, a.swshift};
     // Rader stages (radix > kMaxStockhamRadix) stage their inputs in a second
     // region of G lines after the lines themselves
-    cpx<T>* scr = a.rtab ? lds + a.G * a.LS + g * a.LS : nullptr;
-    run_stages<T, S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw, scr, a.rtab, a.roff);
+    cpx<T>* scr = RAD ? lds + a.G * a.LS + g * a.LS : nullptr;
+    run_stages<T, S, WIDE, RAD>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw, scr, a.rtab, a.roff);
     if constexpr (IO::kTwoPass) {
         IO::template mid<T, DynDims>(a, lds, li);
         __syncthreads();
-        run_stages<T, -S, WIDE>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw, scr, a.rtab, a.roff);
+        run_stages<T, -S, WIDE, RAD>(line, a.N, a.TT, t, a.PS, a.nstages, a.radix, tw, scr, a.rtab, a.roff);
     }
     IO::template epilogue<T, S, DynDims>(a, lds, li);
 }
@@ -1534,7 +1534,15 @@ KernelFn pick_edge(int edge, bool direct) {
     }
 }
 template <typename T, int S>
-KernelFn pick(KernelKind kind, bool wide, int direct, int edge) {
+KernelFn pick(KernelKind kind, bool wide, int direct, int edge, bool rad) {
+    if (rad) {
+        // Rader stages: the staged kernels of mixed-radix lines and of the
+        // FFT-mode Rader kernel with a nested Rader prime
+        if (direct || edge) return nullptr;
+        if (kind == KK_PLAIN) return wide ? k_dyn<T, S, IoPlain, true, true> : k_dyn<T, S, IoPlain, false, true>;
+        if (kind == KK_RADER_FFT) return wide ? k_dyn<T, S, IoRader, true, true> : k_dyn<T, S, IoRader, false, true>;
+        return nullptr;
+    }
     if (edge) {
         if (kind != KK_PLAIN || direct > 1) return nullptr;
         return wide ? pick_edge<T, S, true>(edge, direct == 1) : pick_edge<T, S, false>(edge, direct == 1);

@@ -3,7 +3,7 @@
 #include "fft_kernels_impl.hpp"
 
 namespace vkfx {
-KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct, int edge) {
-    return pick<float, -1>(kind, wide, direct, edge);
+KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct, int edge, bool rad) {
+    return pick<float, -1>(kind, wide, direct, edge, rad);
 }
 }  // namespace vkfx

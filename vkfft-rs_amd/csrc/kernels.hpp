@@ -59,6 +59,9 @@ enum KFlags : int {
     // with KF_MIRROR_PAIRS: the direct first stage loads each (X[k], X[M-k])
     // once for a butterfly of the column and one of its mirror
     KF_PAIR_LOADS = 16384,
+    // the radix list has Rader stages (KArgs::rtab): the staged runtime-shape
+    // instantiation that carries them (the others leave their registers out)
+    KF_RADER = 32768,
 };
 
 // Butterflies per thread in one radix-R stage of the runtime-shape kernel
@@ -127,6 +130,22 @@ constexpr int kMaxStockhamRadix = 16;
 // complex kernels b[n] = exp(-2 pi i g^n / p) (forward) and its conjugate
 // (inverse), L entries each.
 constexpr int rader_kernel_offset(int p) { return (2 * p * 4 + 15) / 16 * 16; }
+
+// A Rader stage whose prime p is at least kRaderFftStageMin and whose
+// L = p - 1 factors into primes up to kRaderSubPrimeMax runs its length-L
+// cyclic convolution by FFT (the FFT-Rader node of rader_ir.rs:706-745):
+// forward FFT_L of every butterfly's generator-ordered inputs, multiply by
+// the kernel spectrum, inverse FFT_L. Its table block (flagged by
+// kRaderFftStage in KArgs::roff) is: int hdr[16] (hdr[0] = number of
+// sub-radices, hdr[1..] the sub-radices, product L), int slot[p] (as above),
+// int pw[L] (pw[m] = g^m mod p), then from byte rader_fft_data_offset(p) the
+// complex roots exp(-2 pi i k/L), k < L, and the spectra FFT_L(b)/L of
+// b[n] = exp(-2 pi i g^n / p) and of its conjugate. The length-L FFTs
+// ping-pong between the stage's scratch region and the line's own region.
+constexpr int kRaderFftStageMin = 89;
+constexpr int kRaderSubPrimeMax = 31;
+constexpr int kRaderFftStage = 1 << 30;
+constexpr int rader_fft_data_offset(int p) { return ((16 + p + (p - 1)) * 4 + 15) / 16 * 16; }
 
 using KernelFn = void (*)(const KArgs);
 

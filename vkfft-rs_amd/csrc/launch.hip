@@ -11,10 +11,10 @@
 
 namespace vkfx {
 
-KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct, int edge);
-KernelFn pick_f32_inv(KernelKind kind, bool wide, int direct, int edge);
-KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct, int edge);
-KernelFn pick_f64_inv(KernelKind kind, bool wide, int direct, int edge);
+KernelFn pick_f32_fwd(KernelKind kind, bool wide, int direct, int edge, bool rad);
+KernelFn pick_f32_inv(KernelKind kind, bool wide, int direct, int edge, bool rad);
+KernelFn pick_f64_fwd(KernelKind kind, bool wide, int direct, int edge, bool rad);
+KernelFn pick_f64_inv(KernelKind kind, bool wide, int direct, int edge, bool rad);
 const FixedKernel* fixed_table_wave(int* count);
 const FixedKernel* fixed_table_plain(int* count);
 const FixedKernel* fixed_table_real(int* count);
@@ -169,8 +169,9 @@ static KernelFn pick_kernel(KernelKind kind, int prec, int dir, int flags) {
     const int direct = (flags & KF_DYN_DIRECT) ? ((flags & KF_DYN_PRE) ? 2 : 1) : 0;
     const int edge =
         (flags & KF_EDGE) ? 1 + ((flags & KF_NARROW_IN) ? 1 : 0) + ((flags & KF_NARROW_OUT) ? 2 : 0) : 0;
-    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide, direct, edge) : pick_f32_inv(kind, wide, direct, edge))
-                     : (dir < 0 ? pick_f64_fwd(kind, wide, direct, edge) : pick_f64_inv(kind, wide, direct, edge));
+    const bool rad = (flags & KF_RADER) != 0;
+    return prec == 0 ? (dir < 0 ? pick_f32_fwd(kind, wide, direct, edge, rad) : pick_f32_inv(kind, wide, direct, edge, rad))
+                     : (dir < 0 ? pick_f64_fwd(kind, wide, direct, edge, rad) : pick_f64_inv(kind, wide, direct, edge, rad));
 }
 
 // Raises a kernel's dynamic-LDS limit once per (device, kernel) to the

@@ -58,6 +58,7 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
     bool rader_stage = false;
     for (int i = 0; i < a.nstages; ++i) rader_stage = rader_stage || a.radix[i] > kMaxStockhamRadix;
     if (rader_stage && !a.rtab) return hipErrorInvalidConfiguration;
+    if (((a.flags & KF_RADER) != 0) != (a.rtab != nullptr)) return hipErrorInvalidConfiguration;
     if (a.rtab) {
         if (fixed || (a.flags & (KF_DYN_DIRECT | KF_EDGE)) || !rader_stage) return hipErrorInvalidConfiguration;
         if (lds_bytes < 2 * (size_t)a.G * (size_t)a.LS * (prec ? 16 : 8)) return hipErrorInvalidConfiguration;

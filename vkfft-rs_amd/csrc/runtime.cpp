@@ -138,6 +138,7 @@ struct Geometry {
     bool ok = false;
     bool wide = false;  // runtime-shape kernel with up to 32 elements per thread per stage
     bool rader = false;  // the radix list has Rader stages (lds holds a second region of G lines)
+    int regions = 1;     // LDS regions of G lines (2 with Rader stages)
     const FixedKernel* fixed = nullptr;
 };
 
@@ -234,6 +235,37 @@ bool radix_schedule_rader(size_t n, std::vector<int>& out) {
     return !out.empty() && (int)out.size() <= kMaxStages;
 }
 
+void host_fft(std::vector<ld>& re, std::vector<ld>& im);
+struct Ctx;
+void note_rader_stages(Ctx& c, const Geometry& g);
+
+// Sub-radices of the length L = q - 1 FFTs of an FFT-mode Rader stage: the
+// Stockham schedule of L's factors up to 13, then each prime factor in
+// (13, kRaderSubPrimeMax] as a direct-multiplication stage.
+bool rader_sub_schedule(size_t L, std::vector<int>& out) {
+    out.clear();
+    size_t smooth = L;
+    std::vector<int> big;
+    for (size_t f : prime_factorization(L))
+        if (f > 13) {
+            if (f > (size_t)kRaderSubPrimeMax) return false;
+            big.push_back((int)f);
+            smooth /= f;
+        }
+    if (smooth > 1 && !radix_schedule(smooth, out)) return false;
+    if (smooth == 1) out.clear();
+    out.insert(out.end(), big.begin(), big.end());
+    return !out.empty() && out.size() <= 15;
+}
+
+// A Rader stage of prime q convolves by FFT (the reference's FFT-Rader node,
+// rader_ir.rs:706-745) from kRaderFftStageMin on, as its direct
+// multiplication costs q - 1 multiply-adds per output.
+bool rader_stage_fft(size_t q) {
+    std::vector<int> sub;
+    return q >= (size_t)kRaderFftStageMin && rader_sub_schedule(q - 1, sub);
+}
+
 // Runtime-shape geometry of a radix list with Rader stages: the threads of a
 // line cover its Stockham stages and at least min(N, 256) work items of the
 // Rader stages; LDS holds the G lines and G scratch lines. `slot` adds one
@@ -260,7 +292,8 @@ Geometry geometry_rader(size_t n, int prec, int want_g, size_t lds_max, size_t l
     int ls = (int)n + ((int)n >> g.PS) + (slot ? 2 : 0);
     if (ls % 2 == 0) ls += 1;
     g.LS = ls;
-    const size_t line_bytes = 2 * (size_t)ls * sz;  // line + scratch line
+    g.regions = 2;  // line + scratch line
+    const size_t line_bytes = (size_t)g.regions * (size_t)ls * sz;
     if (line_bytes > lds_max) return g;
     size_t budget = std::min(std::max(lds_budget, line_bytes), lds_max);
     int G = std::max(1, want_g);
@@ -481,22 +514,70 @@ std::vector<unsigned char> rader_stage_block(size_t q, int prec) {
     return b;
 }
 
+// Table block of an FFT-mode Rader stage for prime q (layout in kernels.hpp,
+// rader_fft_data_offset): the sub-radices of L = q - 1, slot, pw = g^m, the
+// roots exp(-2 pi i k/L) and the spectra FFT_L(b)/L of the forward kernel
+// b[n] = exp(-2 pi i g^n / q) and of its conjugate, in long double.
+std::vector<unsigned char> rader_fft_stage_block(size_t q, int prec) {
+    const size_t L = q - 1, g = primitive_root(q);
+    std::vector<int> sub;
+    rader_sub_schedule(L, sub);
+    std::vector<size_t> pw(L);
+    size_t r = 1;
+    for (size_t e = 0; e < L; ++e) {
+        pw[e] = r;
+        r = (r * g) % q;
+    }
+    const size_t doff = (size_t)rader_fft_data_offset((int)q), es = prec ? 16 : 8;
+    std::vector<unsigned char> b(doff + 3 * L * es, 0);
+    int* hdr = (int*)b.data();
+    hdr[0] = (int)sub.size();
+    for (size_t i = 0; i < sub.size(); ++i) hdr[1 + i] = sub[i];
+    int* slot = hdr + 16;
+    int* pwi = slot + q;
+    slot[0] = (int)L;
+    for (size_t e = 0; e < L; ++e) {
+        slot[pw[(L - e) % L]] = (int)e;  // g^-e
+        pwi[e] = (int)pw[e];
+    }
+    std::vector<ld> re(3 * L), im(3 * L);
+    for (size_t k = 0; k < L; ++k) root((ld)k, (ld)L, re[k], im[k]);
+    for (int sgn = 0; sgn < 2; ++sgn) {
+        std::vector<ld> br(L), bi(L);
+        for (size_t n = 0; n < L; ++n) {
+            root((ld)pw[n], (ld)q, br[n], bi[n]);
+            if (sgn) bi[n] = -bi[n];
+        }
+        host_fft(br, bi);
+        for (size_t k = 0; k < L; ++k) {
+            re[(1 + sgn) * L + k] = br[k] / (ld)L;
+            im[(1 + sgn) * L + k] = bi[k] / (ld)L;
+        }
+    }
+    auto d = pack(re, im, prec);
+    std::memcpy(b.data() + doff, d.data(), d.size());
+    return b;
+}
+
 // Device table of every Rader stage of a radix list: rtab and per-stage byte
-// offsets (distinct primes share a block).
+// offsets (distinct primes share a block; FFT-mode blocks carry
+// kRaderFftStage in roff).
 int rader_stage_tables(vkfx_plan* p, const std::vector<int>& radix, int prec, KArgs& a) {
     std::vector<unsigned char> all;
     std::map<int, size_t> at;
     std::string key = "rstages:" + std::to_string(prec);
     for (size_t s = 0; s < radix.size(); ++s) {
         if (radix[s] <= kMaxStockhamRadix) continue;
+        const bool fft = rader_stage_fft((size_t)radix[s]);
         if (!at.count(radix[s])) {
             at[radix[s]] = all.size();
-            auto b = rader_stage_block((size_t)radix[s], prec);
+            auto b = fft ? rader_fft_stage_block((size_t)radix[s], prec) : rader_stage_block((size_t)radix[s], prec);
             all.insert(all.end(), b.begin(), b.end());
             all.resize((all.size() + 15) / 16 * 16, 0);
-            key += ":" + std::to_string(radix[s]);
+            key += std::string(fft ? ":f" : ":") + std::to_string(radix[s]);
         }
-        a.roff[s] = (int)at[radix[s]];
+        if (at[radix[s]] >= (size_t)kRaderFftStage) return fail(VKFX_ERR_RESOURCE_LIMIT, "Rader stage tables too large");
+        a.roff[s] = (int)at[radix[s]] | (fft ? kRaderFftStage : 0);
     }
     if (all.empty()) return VKFX_OK;
     return upload(p, key, all.data(), all.size(), &a.rtab);
@@ -776,6 +857,7 @@ int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, lon
         // Rader stages run in the staged runtime-shape kernel only
         int rc = rader_stage_tables(c.p, g.radix, c.prec, a);
         if (rc) return rc;
+        if (a.rtab) a.flags |= KF_RADER;
     }
     // runtime-shape C2C over contiguous lines: HBM-direct first and last stages
     if (!g.fixed && !g.rader && kind == KK_PLAIN && (a.flags & KF_IN_ROWMAJOR) && (a.flags & KF_OUT_ROWMAJOR) &&
@@ -966,7 +1048,7 @@ int add_rader(Ctx& c, size_t prime, int dir, KArgs a, long long lines, int in_se
         const int need = (int)L + (int)((L - 1) >> g.PS) + 2;  // x0 slot after the line
         if (g.LS < need) {
             g.LS = need | 1;
-            g.lds = (size_t)g.G * g.LS * csize(c.prec) * (g.rader ? 2 : 1);
+            g.lds = (size_t)g.G * g.LS * csize(c.prec) * (g.rader ? g.regions : 1);
         }
         c.js << "\"rader\":{\"prime\":" << prime << ",\"mode\":\"fft\",\"convolution_len\":" << L;
         if (nested) {
@@ -977,7 +1059,9 @@ int add_rader(Ctx& c, size_t prime, int dir, KArgs a, long long lines, int in_se
                     c.js << (first ? "" : ",") << r;
                     first = false;
                 }
-            c.js << "]";
+            c.js << "],\"nested\":{";
+            note_rader_stages(c, g);
+            c.js << "}";
         }
         c.js << "},";
         rc = add_launch(c, KK_RADER_FFT, -1, g, a, lines, blocks_for(lines, g.G), in_sel, in_off, out_sel, out_off,
@@ -1000,15 +1084,34 @@ int add_rader(Ctx& c, size_t prime, int dir, KArgs a, long long lines, int in_se
     return VKFX_OK;
 }
 
-void note_rader_mixed(Ctx& c, size_t n, const Geometry& g) {
-    c.js << "\"rader_mixed\":{\"len\":" << n << ",\"rader_primes\":[";
+// Primes of the Rader stages of a radix list and, for FFT-mode stages, the
+// sub-radices of their length p - 1 convolutions.
+void note_rader_stages(Ctx& c, const Geometry& g) {
+    c.js << "\"rader_primes\":[";
     bool first = true;
     for (int r : g.radix)
         if (r > kMaxStockhamRadix) {
             c.js << (first ? "" : ",") << r;
             first = false;
         }
-    c.js << "]},";
+    c.js << "],\"fft_convolution\":{";
+    first = true;
+    for (int r : g.radix)
+        if (r > kMaxStockhamRadix && rader_stage_fft((size_t)r)) {
+            std::vector<int> sub;
+            rader_sub_schedule((size_t)r - 1, sub);
+            c.js << (first ? "" : ",") << "\"" << r << "\":[";
+            for (size_t i = 0; i < sub.size(); ++i) c.js << (i ? "," : "") << sub[i];
+            c.js << "]";
+            first = false;
+        }
+    c.js << "}";
+}
+
+void note_rader_mixed(Ctx& c, size_t n, const Geometry& g) {
+    c.js << "\"rader_mixed\":{\"len\":" << n << ",";
+    note_rader_stages(c, g);
+    c.js << "},";
 }
 
 // ---- 1-D complex -----------------------------------------------------------
