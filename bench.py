@@ -136,7 +136,7 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
     torch.cuda.init()  # torch's HIP runtime first: the library then binds to the same one
     import vkfft_amd as vk
 
-    ctx = vk.HipExecutionContext(0)
+    ctx = vk.HipExecutionContext(0, library=vk.INDEX_LIB_PATH if _INDEX_BUILD["on"] else None)
     plans = build_plans(vk, ctx, cfg)
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream()
@@ -208,6 +208,11 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
 
 MEDIAN_BLOCKS = 20
 _ROCTX = {"on": False, "lib": None}
+# --index-build: time the identity-arithmetic build of the same kernels (the
+# index-map test library: every butterfly, twiddle, chirp and spectrum
+# product replaced by the identity), i.e. the plan's data movement alone:
+# the same loads, stores, LDS exchanges and barriers
+_INDEX_BUILD = {"on": False}
 
 
 def _profile_region(begin):
@@ -684,6 +689,8 @@ def main():
     ap.add_argument("--no-check", action="store_true", help="skip the oracle check of the timed output")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch (tuning runs)")
+    ap.add_argument("--index-build", action="store_true",
+                    help="time the identity-arithmetic build (data movement only); implies --no-check --no-cpu")
     ap.add_argument("--profile-region", action="store_true",
                     help="bracket the kernel-timing run with roctxProfilerResume/Pause (rocprofv3 --selected-regions)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
@@ -693,6 +700,9 @@ def main():
         print(rocprof_summary(args.rocprof_summary))
         return
     _ROCTX["on"] = args.profile_region
+    if args.index_build:
+        _INDEX_BUILD["on"] = True
+        args.no_check = args.no_cpu = True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path.",
               file=sys.stderr)
@@ -713,6 +723,8 @@ def main():
             copy_gbs = copy_bandwidth()
             plain_gbs = plain_copy_bandwidth()
         out = summarize(name, cfg, r, steps, warmup, threads, not args.no_cpu)
+        if args.index_build:
+            out["build"] = "index (identity arithmetic: data movement only; not the product)"
         out["hbm_copy_gbs"] = round(copy_gbs, 1)
         out["hbm_plain_copy_gbs"] = round(plain_gbs, 1)
         out["pct_of_copy"] = round(100 * out["value"] / copy_gbs, 2)
