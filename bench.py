@@ -231,6 +231,7 @@ def _profile_region(begin):
 # rocprofv3 kernel names carry it, with the line length of fixed shapes).
 PASS_IO = {
     "stockham": ["IoPlain", "IoPlainStaged"], "stockham_columns": ["IoPlain", "IoPlainStaged"],
+    "stockham_rows": ["IoPlain", "IoPlainStaged"],
     "split_axis_pass1": ["IoFsA"], "split_axis_pass2": ["IoPlain", "IoPlainStaged"],
     "four_step_columns": ["IoFsA"], "four_step_rows": ["IoFsB"],
     "r2c_columns": ["IoFsA"], "r2c_rows_post": ["IoFsBR2C"],
