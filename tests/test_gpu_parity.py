@@ -464,6 +464,49 @@ def test_round_length_fixed_rows(hip_ctx, prec):
         assert o.rel_l2(z, x) <= 4 * TOL[prec], (n, prec)
 
 
+def _lines_against_pocketfft(y, x, n, batch, direction, tol):
+    """Indices of the lines of y whose relative L2 error against numpy's FFT of
+    the same line exceeds tol (normalized inverse for direction INV)."""
+    xs = x.reshape(batch, n).astype(np.complex128)
+    ref = np.fft.fft(xs, axis=1) if direction == FWD else np.fft.ifft(xs, axis=1)
+    err = np.linalg.norm(y.reshape(batch, n) - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    return np.nonzero(err > tol)[0][:8].tolist()
+
+
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_fixed_rows_several_blocks(hip_ctx, prec):
+    """Round-length and Bluestein fixed row shapes at a batch of 3*G + 1 lines
+    (G = the shape's lines per block): three full blocks and a partial one, so
+    the line placement of the second and later blocks and of the partial block
+    runs on each shape's own length. Every line, forward and normalized inverse,
+    against pocketfft."""
+    round_sample = [200, 240, 480, 600, 720, 1200, 2000, 3000, 5000, 8000, 16000]
+    blue = BLUE_PRIMES[prec]
+    blue_sample = [p for i, p in enumerate(sorted(blue)) if i % 3 == 0]
+    tol = 4 * TOL[prec]
+    bad, seen_g = {}, set()
+    for n in round_sample + blue_sample:
+        if prec == F64 and n in ROUND and n > 8192:
+            continue  # longer f64 lines are two uploads
+        probe = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(1).with_precision(prec), FWD)
+        first = hip_ctx.plan(probe).describe()["passes"][0]
+        assert first["fixed_shape"], n
+        g = int(first["lines_per_block"])
+        seen_g.add(g)
+        batch = 3 * g + 1
+        x = rand(n * batch, 3 * n + g, prec)
+        for direction in (FWD, INV):
+            y, ir = c2c(hip_ctx, [n], batch, x, prec, direction, normalize=True)
+            p0 = hip_ctx.plan(ir).describe()["passes"][0]
+            assert p0["fixed_shape"] and p0["lines_per_block"] == g, (n, direction, p0)
+            assert p0["grid"] >= 4, (n, p0["grid"])
+            lines = _lines_against_pocketfft(y, x, n, batch, direction, tol)
+            if lines:
+                bad[(n, direction)] = lines
+    assert not bad, bad
+    assert max(seen_g) >= 4, seen_g  # the sample holds multi-line blocks
+
+
 @pytest.mark.parametrize("prec", [F32, F64])
 def test_r2c_c2r_fixed_half_lengths(hip_ctx, prec):
     """Even lengths whose half-size FFT has a fixed shape, at batch 37 (several

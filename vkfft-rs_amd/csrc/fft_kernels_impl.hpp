@@ -1410,12 +1410,14 @@ __device__ __forceinline__ void fix_body(const KArgs& a, cpx<T>* lds, LineInfo* 
     constexpr bool LD = Direct<IO, Sh::COL>::load;
     constexpr bool SD = Direct<IO, Sh::COL>::store;
     const int tid = threadIdx.x;
-    const int g = Sh::COL ? tid % Sh::G : tid / Sh::TT;
-    const int t = Sh::COL ? tid / Sh::G : tid % Sh::TT;
+    const int g = Sh::G == 1 ? 0 : Sh::COL ? tid % Sh::G : tid / Sh::TT;
+    const int t = Sh::G == 1 ? tid : Sh::COL ? tid / Sh::G : tid % Sh::TT;
     // A pass that reads and writes HBM only from its own registers needs
     // nothing but its own line's placement: every thread computes it, with no
-    // shared table and no barrier before the first loads.
-    constexpr bool kOwnLine = LD && SD && !IO::kTwoPass;
+    // shared table and no barrier before the first loads. With one line per
+    // block the placement is uniform (scalar registers), which also holds for
+    // two-pass kernels whose mid product is fused into the stages.
+    constexpr bool kOwnLine = LD && SD && (!IO::kTwoPass || (Sh::G == 1 && IO::kMidFused));
     if constexpr (!kOwnLine) {
         if (tid < Sh::G) li[tid] = IO::line(a, blk, tid);
         __syncthreads();
