@@ -245,6 +245,13 @@ struct IoPlain {
     // access sets kPtrLoad / kPtrStore false.
     static constexpr bool kPtrLoad = true;
     static constexpr bool kPtrStore = true;
+    // Butterfly forms of the element functions for the direct stages of
+    // policies whose element functions weigh and mask elements by their
+    // position in the line: load_bfly fills the R inputs b + i*NB of a
+    // first-stage butterfly, store_bfly stores the R outputs base + q*P of a
+    // last-stage butterfly, each stepping its addresses by a uniform stride.
+    static constexpr bool kBflyLoad = false;
+    static constexpr bool kBflyStore = false;
     template <typename T>
     static __device__ __forceinline__ const cpx<T>* in_ptr(const KArgs& a, const LineInfo& L, int e) {
         return (const cpx<T>*)a.in + L.ib + (long long)e * a.in_es;
@@ -474,6 +481,22 @@ struct IoFsABlue : IoFsA {
         const long long n = L.c + (long long)e * a.N2;
         if (n >= a.nvalid) return zero<T>();
         return cmul(ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es), ((const cpx<T>*)a.chirp)[n]);
+    }
+    // element e = b + i*NB sits at n = c + e*N2 of the padded line
+    static constexpr bool kBflyLoad = true;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        long long n = L.c + (long long)b * a.N2;
+        const long long dn = (long long)NB * a.N2;
+        const cpx<T>* x = (const cpx<T>*)a.in + L.ib + (long long)b * a.in_es;
+        const long long dx = (long long)NB * a.in_es;
+        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            v[i] = n < a.nvalid ? cmul(ldg_in<NTIO>(a, x), chirp[n]) : zero<T>();
+            n += dn;
+            x += dx;
+        }
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -748,6 +771,23 @@ struct IoFsCBlue : IoPlain {
         const long long m = L.c + (long long)e * a.N2;
         if (m >= a.nout) return;
         stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, scale(cmul(v, ((const cpx<T>*)a.chirp)[m]), (T)a.scale));
+    }
+    // outputs e = base + q*P sit at m = c + e*N2 of the convolution
+    static constexpr bool kBflyStore = true;
+    template <typename T, int S, bool NTIO, int R, int P>
+    static __device__ __forceinline__ void store_bfly(const KArgs& a, const LineInfo& L, int base, const cpx<T>* v) {
+        long long m = L.c + (long long)base * a.N2;
+        const long long dm = (long long)P * a.N2;
+        cpx<T>* y = (cpx<T>*)a.out + L.ob + (long long)base * a.out_es;
+        const long long dy = (long long)P * a.out_es;
+        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
+        const T sc = (T)a.scale;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            if (m < a.nout) stg_out<NTIO>(a, y, scale(cmul(v[q], chirp[m]), sc));
+            m += dm;
+            y += dy;
+        }
     }
     template <typename T, class D>
     static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
@@ -1207,6 +1247,13 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                 const long long st = (long long)NB * a.in_es;
 #pragma unroll
                 for (int i = 0; i < R; ++i) v[j][i] = ldg_in<NTI>(a, p + i * st);
+            } else if constexpr (SRC && IO::kBflyLoad) {
+                if (L.valid) {
+                    IO::template load_bfly<T, NTI, R, NB>(a, L, b, v[j]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < R; ++i) v[j][i] = zero<T>();
+                }
             } else if constexpr (SRC && IO::kLoadTw) {
                 // inputs b + i*NB carry the load twiddle root(b) * root(NB)^i
                 if (L.valid) {
@@ -1277,6 +1324,8 @@ __device__ __forceinline__ void fstage(const KArgs& a, cpx<T>* __restrict__ line
                             IO::template store_twiddled<T, S, NTO>(a, L, base + q * P, v[j][q], cmul(wb, sp[q]));
                     }
                 }
+            } else if constexpr (DST && IO::kBflyStore) {
+                if (L.valid) IO::template store_bfly<T, S, NTO, R, P>(a, L, base, v[j]);
             } else if constexpr (DST && IO::kPtrStore) {
                 if (L.valid) {
                     cpx<T>* p = IO::template out_ptr<T>(a, L, base);
@@ -1374,6 +1423,8 @@ __device__ __forceinline__ void fstages(const KArgs& a, cpx<T>* line, cpx<T>* al
                                         const StageTw& tw, RList<R, Rest...>) {
     constexpr bool last = sizeof...(Rest) == 0;
     constexpr int PSO = !Sh::SPAD ? Sh::PS : last ? 30 : stage_pad<Sh::N, P, R, rlist_head(RList<Rest..., 0>{})>();
+    // every padded slot of the buffer this stage writes lies inside the line stride
+    static_assert(PSO >= 30 || (Sh::N - 1) + ((Sh::N - 1) >> PSO) < Sh::LS, "LDS line stride below the padded length");
     constexpr bool kPairs = IO::kPairFirst && P == 1 && SRC0 && !last && !Sh::PP && !Sh::SPAD && Sh::COL &&
                             Sh::N / R == 2 * Sh::TT;
     if constexpr (kPairs) {

@@ -5,27 +5,29 @@
 namespace vkfx {
 
 static const FixedKernel kTable[] = {
-    // M = 8232: in place with per-stage twiddle tables and pads, 80 VGPRs so
-    // two 74 KiB blocks share a CU; then the ping-pong form (one block per
+    // M = 8232: in place with per-stage twiddle tables and pads, at most 80
+    // VGPRs (74, no spill) so two 74 KiB blocks share a CU; then the ping-pong form (one block per
     // CU, one barrier per stage) and the in-place form with product-tree
     // twiddles and one uniform pad (VKFX_FIXED_PICK_K12=1, 2)
     VKFX_FIXED_TS(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 3, 9261, false, 6, true, true, 8, 3, 7, 7, 7),
     VKFX_FIXED_PPTS(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 3, 9261, false, true, true, 8, 3, 7, 7, 7),
     VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
-    // M = 131220: product-tree twiddles (per-stage tables measured 4% slower).
-    // Column passes of 405 with 45 threads per column (one radix-9 butterfly
-    // each: 1.3% over 27 threads, the second variant); the 324-point row pass
-    // with 36 threads per row (radix 4, 9, 9: one radix-9 butterfly per thread,
-    // three radix-4 rounds) and 8 rows per block, 6-7% over 27 threads per row
-    // (the second variant) on two boxes; 16 rows per block, an LDS pad of one
-    // per 16, radix orders 9-9-4 / 9-4-9 (fewer modelled LDS bank conflicts)
-    // and 81 threads per row ran slower (5.50-6.86 ms against 5.41-5.47)
+    // M = 131220: product-tree twiddles (per-stage tables measured 4% slower;
+    // on the row pass 10-20% slower). Column passes of 405 with 45 threads
+    // per column (one radix-9 butterfly each: 1.3% over 27 threads, the second
+    // variant; 8 columns per block, 64-byte row segments, ran 5-14% slower).
+    // The 324-point row pass with 36 threads per row (radix 4, 9, 9: one
+    // radix-9 butterfly per thread, three radix-4 rounds) and 7 rows per block:
+    // 252 threads fill four waves, where 8 rows (the second variant) leave the
+    // fifth wave half empty; 7 rows took the pass from 82 to 60 us per chunk
+    // and C5b from 5.36 to 5.09-5.14 ms on one box (3, 5 and 14 rows, an odd
+    // line stride and 27 threads per row ran slower)
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 45, 16, 30, 405, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 45, 16, 30, 405, true, false, true, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 407, true, false, true, 9, 9, 5),
+    VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 36, 7, 30, 324, false, false, false, 4, 9, 9),
     VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 36, 8, 30, 324, false, false, false, 4, 9, 9),
-    VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 27, 8, 30, 347, false, false, false, 4, 9, 9),
 };
 
 const FixedKernel* fixed_table_blue(int* count) {
