@@ -54,7 +54,10 @@ def run_case(ctx, dims, batch, prec, matrix=1, symmetric=False, kernels=1, conj=
 
 @pytest.mark.parametrize("dims,batch,prec", [([1024], 8, F32), ([2048], 4, F64), ([4099], 3, F32),
                                              ([1009], 2, F64), ([1 << 20], 1, F32), ([360], 5, F32),
-                                             ([64, 48], 2, F32), ([16, 12, 10], 2, F64), ([256, 256], 1, F32)])
+                                             ([64, 48], 2, F32), ([16, 12, 10], 2, F64), ([256, 256], 1, F32),
+                                             ([97, 16], 2, F32), ([48, 97], 3, F64), ([8, 6, 5, 4], 3, F32),
+                                             ([1024, 48], 2, F32), ([768, 16, 4], 1, F32),
+                                             ([1024, 8], 2, F64)])
 def test_scalar_kernel(hip_ctx, dims, batch, prec):
     conv, _, _ = run_case(hip_ctx, dims, batch, prec)
     desc = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
@@ -62,9 +65,29 @@ def test_scalar_kernel(hip_ctx, dims, batch, prec):
     if dims in ([1024], [2048], [360]):
         # one upload: forward FFT, multiply and normalized inverse in one pass
         assert desc["convolution"]["fused"] and labels == ["convolution_fused"], labels
+    elif len(dims) > 1 and dims[0] > 640 and prec == F32:
+        # N-D over Stockham axes whose axis 0 the plain plan splits (and whose
+        # runtime geometry holds 8 or more columns per block: 1024, 768): the
+        # forward FFT of axes 1.., one kernel per axis-0 line (forward FFT,
+        # multiply, inverse FFT), the inverse of axes 1..: 2D - 1 passes
+        assert desc["convolution"]["fused"] and desc["convolution"]["fused_axis"] == 0, desc["convolution"]
+        assert labels.count("convolution_fused_axis0") == 1 and "convolution_multiply" not in labels, labels
+        assert len(labels) == 2 * len(dims) - 1, labels
     else:
+        # a Rader axis, an axis 0 of one pass, or (f64) too few columns per
+        # block for the fused kernel keep the separate multiply
         assert not desc["convolution"]["fused"] and "convolution_multiply" in labels
     assert desc["convolution"]["kernels"] == 1 and desc["convolution"]["matrix"] == 0
+
+
+@pytest.mark.parametrize("dims,prec", [([1024, 24], F32), ([768, 10, 3], F32)])
+@pytest.mark.parametrize("conj,cross", [(True, False), (False, True), (True, True)])
+def test_fused_nd_policies(hip_ctx, dims, prec, conj, cross):
+    """Sequence conjugation and cross-power normalization in the fused axis-0
+    kernel of an N-D convolution (the spectrum of each axis-0 column indexed
+    by its position in the tensor), batch 3, against the oracle."""
+    conv, _, _ = run_case(hip_ctx, dims, 3, prec, conj=conj, cross=cross, seed=12)
+    assert vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()["convolution"]["fused_axis"] == 0
 
 
 @pytest.mark.parametrize("conj,cross,batch", [(True, False, 3), (False, True, 2), (True, True, 5)])

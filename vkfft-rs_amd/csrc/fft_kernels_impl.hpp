@@ -852,6 +852,9 @@ struct IoConv1 : IoPlain {
     static constexpr bool kTwoPass = true;
     static constexpr int kLoad = LAY_STAGED;
     static constexpr int kStore = LAY_STAGED;
+    // element e of line (o, c) multiplies the spectrum at c + e * N2: a 1-D
+    // line (C = 1, N2 = 1) the spectrum itself, an axis-0 line of an N-D
+    // tensor (column c of C = N2 = the product of the other axes) its column
     template <typename T, class D>
     static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
         const cpx<T>* spec = (const cpx<T>*)a.spec;
@@ -859,7 +862,7 @@ struct IoConv1 : IoPlain {
             cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
             cpx<T> x = v;
             if (a.flags & KF_CONV_CONJ) x = conj(x);
-            cpx<T> y = cmul(x, spec[e]);
+            cpx<T> y = cmul(x, spec[li[g].c + (long long)e * a.N2]);
             if (a.flags & KF_CONV_CROSS) {
                 const T r = (T)1 / sqrt(y.re * y.re + y.im * y.im);
                 y = mk(y.re * r, y.im * r);
