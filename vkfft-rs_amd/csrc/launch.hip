@@ -147,23 +147,6 @@ static int lds_limit_bytes() {
 
 size_t max_lds_bytes() { return (size_t)lds_limit_bytes(); }
 
-// Launches whose blocks share HBM cache lines with their neighbours get their
-// groups dealt to XCDs in contiguous ranges: the four-step passes that read
-// or write the N/2+1-pitch real-transform spectra (unaligned 128-byte
-// segments) and the Bluestein passes over pitch-N lines. Measured on C2: the
-// C2R column pass reads 1.0x its bytes instead of 2.0x and the R2C row pass
-// writes 1.0x instead of 1.19x. VKFX_XCD_GROUPS=0/1 forces it off/on for
-// every launch (tuning runs).
-static bool xcd_groups(KernelKind kind) {
-    static const int forced = [] {
-        const char* e = getenv("VKFX_XCD_GROUPS");
-        return e ? (e[0] == '1' ? 1 : 0) : -1;
-    }();
-    if (forced >= 0) return forced == 1;
-    return kind == KK_FS_B_R2C || kind == KK_FS_A_C2R || kind == KK_FS_A_BLUE || kind == KK_BLUE_B ||
-           kind == KK_FS_C_BLUE;
-}
-
 static KernelFn pick_kernel(KernelKind kind, int prec, int dir, int flags) {
     const bool wide = (flags & KF_DYN_WIDE) != 0;
     const int direct = (flags & KF_DYN_DIRECT) ? ((flags & KF_DYN_PRE) ? 2 : 1) : 0;
@@ -205,7 +188,6 @@ int launch(KernelKind kind, int prec, int dir, const KArgs& a, unsigned grid, un
     if (!fn) return (int)hipErrorInvalidValue;
     KArgs args = a;
     args.nblk = grid;
-    if (xcd_groups(kind)) args.flags |= KF_XCD_GROUPS;
     if (lds_bytes > 65536) {
         int e = raise_lds_limit((const void*)fn, lds_bytes);
         if (e != (int)hipSuccess) return e;

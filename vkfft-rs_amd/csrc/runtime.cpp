@@ -837,13 +837,29 @@ void note_pass(Ctx& c, const Launch& L) {
          << ",\"runtime_variant\":{\"wide\":" << ((L.a.flags & KF_DYN_WIDE) ? "true" : "false")
          << ",\"hbm_direct\":" << ((L.a.flags & KF_DYN_DIRECT) ? "true" : "false")
          << ",\"direct_preprocess\":" << ((L.a.flags & KF_DYN_PRE) ? "true" : "false") << "}"
+         << ",\"xcd_groups\":" << ((L.a.flags & KF_XCD_GROUPS) ? "true" : "false")
+         << ",\"pair_loads\":" << ((L.a.flags & KF_PAIR_LOADS) ? "true" : "false")
          << ",\"radices\":[";
     for (int i = 0; i < L.a.nstages; ++i) c.js << (i ? "," : "") << L.a.radix[i];
     c.js << "]}";
 }
 
+// Launches whose blocks share HBM cache lines with their neighbours get their
+// groups dealt to XCDs in contiguous ranges: the four-step passes that read
+// or write the N/2+1-pitch real-transform spectra (unaligned 128-byte
+// segments) and the Bluestein passes over pitch-N lines. Measured on C2: the
+// C2R column pass reads 1.0x its bytes instead of 2.0x and the R2C row pass
+// writes 1.0x instead of 1.19x. VKFX_XCD_GROUPS=0/1 forces it off/on for
+// every launch of the plans built after it is set (tuning runs).
+bool xcd_groups(KernelKind kind) {
+    if (const char* e = getenv("VKFX_XCD_GROUPS")) return e[0] == '1';
+    return kind == KK_FS_B_R2C || kind == KK_FS_A_C2R || kind == KK_FS_A_BLUE || kind == KK_BLUE_B ||
+           kind == KK_FS_C_BLUE;
+}
+
 int add_launch(Ctx& c, KernelKind kind, int dir, const Geometry& g, KArgs a, long long nlines, unsigned grid,
                int in_sel, size_t in_off, int out_sel, size_t out_off, const char* label) {
+    if (xcd_groups(kind)) a.flags |= KF_XCD_GROUPS;
     a.N = g.N;
     a.TT = g.TT;
     a.G = g.G;
@@ -2154,10 +2170,8 @@ int plan_c2r(Ctx& c, size_t n, size_t batch, bool normalize) {
     const bool pairs = ga.G % 2 == 0 && n2 % 2 == 0 && n2 % (size_t)ga.G == 0;
     // fixed shapes whose first stage can take the pair loads use them
     // (VKFX_C2R_PAIR_LOADS=0: every element reads X[k] and X[M-k] itself)
-    static const bool pair_loads = [] {
-        const char* e = getenv("VKFX_C2R_PAIR_LOADS");
-        return !(e && e[0] == '0');
-    }();
+    const char* pe = getenv("VKFX_C2R_PAIR_LOADS");
+    const bool pair_loads = !(pe && pe[0] == '0');
     const void *tlo, *thi;
     int tsh;
     rc = two_level(p, M, prec, &tlo, &thi, &tsh);
@@ -2825,10 +2839,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
     // stays cached so that a chunk's intermediate is served from the Infinity
     // Cache by the next pass. VKFX_NT_ROLES=0 keeps each shape's first
     // registered variant.
-    static const bool nt_roles = [] {
-        const char* e = getenv("VKFX_NT_ROLES");
-        return !(e && e[0] == '0');
-    }();
+    const char* ne = getenv("VKFX_NT_ROLES");
+    const bool nt_roles = !(ne && ne[0] == '0');
     for (size_t i = 0; nt_roles && i < p->launches.size(); ++i) {
         Launch& L = p->launches[i];
         if (!L.fixed) continue;
