@@ -26,7 +26,9 @@ steps, over three runs of the same K = max(20, --steps) steps:
                this host's cores over a bounded sample of the same workload
 
 The default line also carries `configs`: every other BASELINE configuration
-(C2-C5b) timed in the same process by the same protocol, each with its own
+(C2-C5b) timed in the same process by the same protocol (K at least 50, and
+the warmup continued until at least 50 ms of work has run; the row reports
+`warmup_steps_run`), each with its own
 roofline, HBM sweeps per step, CPU baseline and the relative L2 error of a
 sampled slice of its timed output against the oracle. `accuracy` is the same
 check for the headline's timed output (plus the sample-11 metrics of
@@ -114,7 +116,7 @@ def build_plans(vk, ctx, cfg):
     return [ctx.plan(ir)]
 
 
-def run_gpu(cfg, steps, warmup, rotate, check=None):
+def run_gpu(cfg, steps, warmup, rotate, check=None, warm_ms=0.0):
     """Times one configuration: `warmup` untimed steps, then three runs of
     the same `steps` steps. Returns a dict with
       ms_mean    host clock between the synchronizes around run 1 / steps
@@ -130,7 +132,8 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
                  `rocprofv3 --selected-regions` trace collects;
       info       device, plan descriptions, buffer pairs, accuracy.
     `check(bufs, pairs, steps)` runs on the timed output before the buffers
-    are released."""
+    are released. With `warm_ms` > 0 the warmup continues past `warmup` steps
+    until that much host-clocked work has run (info["warmup_steps_run"])."""
     import torch
 
     torch.cuda.init()  # torch's HIP runtime first: the library then binds to the same one
@@ -165,6 +168,18 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
 
     for i in range(warmup):
         step(i)
+    # a floor on the warmup's duration: a kernel bound by VALU issue runs its
+    # first milliseconds slower while the GPU's clocks leave their idle state
+    # (C5a: 20 steps averaged 226 us after 5 warmup steps, 193 us after 200)
+    warm_done = warmup
+    if warm_ms > 0:
+        torch.cuda.synchronize()
+        t_w = time.perf_counter()
+        while (time.perf_counter() - t_w) * 1e3 < warm_ms:
+            for _ in range(4):
+                step(warm_done)
+                warm_done += 1
+            torch.cuda.synchronize()
     # run 1: host clock, no event in the region
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -195,7 +210,8 @@ def run_gpu(cfg, steps, warmup, rotate, check=None):
     torch.cuda.synchronize()
     _profile_region(False)
     kernels = [p.timing_stop() for p in plans]
-    info = {"device": ctx.device_name(), "profile": ctx.device_profile(), "plans": launches, "pairs": pairs}
+    info = {"device": ctx.device_name(), "profile": ctx.device_profile(), "plans": launches, "pairs": pairs,
+            "warmup_steps_run": warm_done}
     if check is not None:
         # the last timed step's pair holds its output (runs 2 and 3 rewrote
         # the same inputs' outputs with the same plans)
@@ -740,11 +756,14 @@ def main():
             if name == "c1":
                 continue
             cfg = dict(CONFIGS[name])
-            # at least 50 steps: the mean of a short region weighs the first
-            # steps' dispatch ramp more (C5a: 0.255 ms at 20 steps, 0.234 at 200)
+            # at least 50 steps, after at least 50 ms of warmup work: the mean
+            # of a short region right after a short warmup weighs the first
+            # steps' ramp (C5a: 0.255 ms at 20 steps, 0.234 at 200)
             ksteps = max(steps, 50)
-            r = run_gpu(cfg, ksteps, warmup, args.rotate, check=None if args.no_check else make_check(cfg, threads))
+            r = run_gpu(cfg, ksteps, warmup, args.rotate, check=None if args.no_check else make_check(cfg, threads),
+                        warm_ms=50.0)
             row = summarize(name, cfg, r, ksteps, warmup, threads, False)
+            row["warmup_steps_run"] = r["info"]["warmup_steps_run"]
             acc = row.pop("accuracy") or {}
             for k in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "data", "unit"):
                 row.pop(k, None)
