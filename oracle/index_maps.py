@@ -17,6 +17,14 @@ out[k] = in[src[k]] (src = -1: a zero of Bluestein padding).
   four-step with each row of N2 = M1*M2 transformed by a four-step of its own.
 - Bluestein (src/bluestein_ir.rs:933-1089): a = x zero-padded to M, FFT_M,
   spectrum multiply, inverse FFT_M, truncation to N.
+- Rader butterfly of a prime p with generator g (src/rader_ir.rs:1957-2101,
+  lut.rs:374-435): a[s] = x[g^-s], a length p-1 cyclic convolution with the
+  kernel b[n] = exp(-2 pi i g^n / p), X[g^m] = x[0] + conv[m] and
+  X[0] = x[0] + sum(a). Under identity arithmetic the index-map build
+  replaces the kernel by the unit impulse and the sum by a[0] (direct
+  multiplication), or runs the convolution's two length p-1 FFTs as their
+  identity Stockham maps (FFT mode), so each output is x[0] plus one named
+  input and the gather and scatter show bit for bit.
 
 `stockham_fft` runs the same stage maps with real butterflies and twiddles;
 tests pin the maps by checking it against numpy.fft (pocketfft) and the
@@ -63,6 +71,57 @@ def stockham_fft(x: np.ndarray, radices, sign: int = -1) -> np.ndarray:
         base = j + (b - j) * r
         for q in range(r):
             nxt[base + q * p] = out[q]
+        cur = nxt
+        p *= r
+    return cur
+
+
+def rader_butterfly(x: np.ndarray, p: int, g: int, kernel=None, sub_perm=None) -> np.ndarray:
+    """Rader butterflies of prime p over x[..., i], i = 0..p-1 (generator g).
+    kernel None: the DFT's kernel exp(-2 pi i g^n / p) (the result is the
+    p-point DFT); kernel "impulse": the identity-arithmetic form of the direct
+    multiplication (conv[m] = a[m], a[0] for the sum); kernel "maps": the
+    identity-arithmetic FFT form with the convolution's Stockham map
+    sub_perm (f = a[sub_perm] for the sum, conv = f[sub_perm])."""
+    L = p - 1
+    pw = np.array([pow(g, e, p) for e in range(L)], dtype=np.int64)
+    a = x[..., pw[(L - np.arange(L)) % L]]          # a[s] = x[g^-s]
+    if kernel is None:
+        b = np.exp(-2j * np.pi * pw / p)
+        conv = np.fft.ifft(np.fft.fft(a, axis=-1) * np.fft.fft(b), axis=-1)
+        dc = a.sum(axis=-1)
+    elif kernel == "impulse":
+        conv, dc = a, a[..., 0]
+    else:
+        f = a[..., sub_perm]
+        conv, dc = f[..., sub_perm], f[..., 0]
+    out = np.empty(x.shape, dtype=np.result_type(x, conv))
+    out[..., 0] = x[..., 0] + dc
+    out[..., pw] = x[..., :1] + conv
+    return out
+
+
+def stockham_identity(x: np.ndarray, radices, rader=None) -> np.ndarray:
+    """The identity-arithmetic pass of a runtime radix list over lines
+    x[batch, n]: the Stockham stage maps with identity butterflies, and for a
+    prime radix above 16 the identity Rader butterfly. rader[p] = (g, None)
+    for a direct-multiplication stage, (g, sub_perm) for an FFT-mode stage."""
+    n = x.shape[-1]
+    assert int(np.prod(radices)) == n, (n, radices)
+    cur = x.copy()
+    p = 1
+    for r in radices:
+        nb = n // r
+        b = np.arange(nb, dtype=np.int64)
+        j = b % p
+        v = np.stack([cur[..., b + i * nb] for i in range(r)], axis=-1)  # [..., nb, r]
+        if r > 16:
+            g, sub = rader[r]
+            v = rader_butterfly(v, r, g, "impulse" if sub is None else "maps", sub)
+        nxt = np.empty_like(cur)
+        base = j + (b - j) * r
+        for q in range(r):
+            nxt[..., base + q * p] = v[..., q]
         cur = nxt
         p *= r
     return cur

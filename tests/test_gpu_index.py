@@ -11,9 +11,10 @@ kernels (one upload and four-step) combine each element with its mirror:
 with random integer tags their identity-arithmetic results (sums and
 differences of the paired elements) are exact, so the pairing and placement
 are checked bit for bit too, and likewise the FFT-mode Rader kernel's
-gather, slot-0 sum and scatter. The direct-multiplication Rader kernel sums
-every input into every output under identity arithmetic and is checked
-numerically elsewhere."""
+gather, slot-0 sum and scatter. The direct-multiplication Rader kernel and
+the Rader stages of mixed-radix lengths convolve with the unit impulse under
+identity arithmetic (the FFT-mode stages run their convolution's identity
+Stockham maps), so their gathers and scatters are checked bit for bit too."""
 import os
 
 import numpy as np
@@ -527,3 +528,61 @@ def test_rader_fft_addressing(idx_ctx, p, prec):
     expect[:, 0] = xb[:, 0] + f[:, 0]
     expect[:, pw] = xb[:, :1] + h
     assert np.array_equal(out.reshape(batch, p), expect.astype(out.dtype))
+
+
+@pytest.mark.parametrize("p", [47, 59, 83])
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_rader_direct_addressing(idx_ctx, p, prec):
+    """Direct-multiplication Rader of a prime p (rader_ir.rs:1957-2101): with
+    identity arithmetic the kernel build convolves with the unit impulse and
+    takes a[0] for the DC sum, so X[g^m] = x0 + x[g^-m] and X[0] = x0 + x[1]
+    (the gather of a[s] = x[g^-s] and the scatter to g^m), bit for bit on
+    random integer tags."""
+    from oracle import oracle as orc
+    batch = 4
+    rng = np.random.default_rng(1000 + p)
+    x = (rng.integers(0, 1 << 18, p * batch) + 1j * rng.integers(0, 1 << 18, p * batch))
+    x = x.astype(np.complex64 if prec == F32 else np.complex128)
+    ir = vk.TransformIr.build(vk.FftConfig.new([p]).with_batch_count(batch).with_precision(prec), FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    assert [q["kernel"] for q in desc["passes"]] == ["rader_direct"], desc["passes"]
+    expect = im.rader_butterfly(x.reshape(batch, p).astype(np.complex128), p, orc.primitive_root(p), "impulse")
+    assert np.array_equal(out.reshape(batch, p), expect.astype(out.dtype))
+
+
+RADER_STAGE_LENGTHS = [17 * 4, 19 * 12, 2 * 29 * 31, 17 * 17 * 3, 47 * 4, 89 * 4, 97 * 8, 113 * 2, 257 * 4]
+
+
+@pytest.mark.parametrize("n", RADER_STAGE_LENGTHS)
+@pytest.mark.parametrize("prec", [F32, F64])
+def test_rader_stage_addressing(idx_ctx, n, prec):
+    """Rader stages inside a mixed-radix runtime radix list: the Stockham
+    stage maps with identity butterflies, and at each prime radix the
+    identity Rader butterfly (direct stages below 89: unit impulse; FFT-mode
+    stages: the convolution's two identity Stockham maps of the plan's
+    sub-radices), against oracle/index_maps.py bit for bit."""
+    from oracle import oracle as orc
+    batch = 3
+    rng = np.random.default_rng(2000 + n)
+    x = (rng.integers(0, 1 << 16, n * batch) + 1j * rng.integers(0, 1 << 16, n * batch))
+    x = x.astype(np.complex64 if prec == F32 else np.complex128)
+    ir = vk.TransformIr.build(vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec), FWD)
+    plan = vk.Plan(idx_ctx, ir)
+    try:
+        desc = plan.describe()
+        out = idx_ctx.execute_transform(ir, x)
+    finally:
+        plan.close()
+    assert len(desc["passes"]) == 1, desc["passes"]
+    radices = desc["passes"][0]["radices"]
+    fft_stages = {int(k): v for k, v in desc["rader_mixed"]["fft_convolution"].items()}
+    rader = {r: (orc.primitive_root(r), im.stockham_perm(r - 1, fft_stages[r]) if r in fft_stages else None)
+             for r in radices if r > 16}
+    assert rader, radices
+    expect = im.stockham_identity(x.reshape(batch, n).astype(np.complex128), radices, rader)
+    assert np.array_equal(out.reshape(batch, n), expect.astype(out.dtype)), (n, radices)

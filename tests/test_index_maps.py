@@ -172,3 +172,59 @@ def test_bluestein_single_map_by_simulation(n, m, radices):
 def test_bluestein_three_pass_map_by_simulation(n, n1, rad1, n2, rad2, rad3):
     got = im.bluestein_three_pass_perm(n, n1, rad1, n2, rad2, rad3)
     assert np.array_equal(got, _bluestein_three_pass_sim(n, n1, rad1, n2, rad2, rad3))
+
+
+RADER_PRIMES = [17, 19, 23, 29, 31, 47, 83, 89, 97, 113, 193, 257]
+
+
+@pytest.mark.parametrize("p", RADER_PRIMES)
+def test_rader_butterfly_is_the_dft(p):
+    """The Rader butterfly's gather (a[s] = x[g^-s]), kernel and scatter
+    (X[g^m] = x0 + conv[m], X[0] = x0 + sum a) with the planner's generator
+    compute the p-point DFT: pins the maps the identity forms reuse."""
+    from oracle import oracle as orc
+    rng = np.random.default_rng(p)
+    x = rng.standard_normal((3, p)) + 1j * rng.standard_normal((3, p))
+    y = im.rader_butterfly(x, p, orc.primitive_root(p))
+    assert np.max(np.abs(y - np.fft.fft(x, axis=-1))) <= 1e-12 * p
+
+
+@pytest.mark.parametrize("p", RADER_PRIMES)
+def test_rader_identity_forms(p):
+    """Closed forms of the identity Rader butterflies: with the unit impulse
+    X[k] = x0 + x[k^-1 mod p] (k >= 1) and X[0] = x0 + x[1]; with the
+    convolution's identity Stockham maps (FFT mode) and an identity sub-map,
+    the same."""
+    from oracle import oracle as orc
+    g = orc.primitive_root(p)
+    x = np.arange(p, dtype=np.float64) * 1000 + 7
+    y = im.rader_butterfly(x, p, g, "impulse")
+    inv = np.array([pow(int(k), p - 2, p) for k in range(1, p)])
+    assert y[0] == x[0] + x[1]
+    assert np.array_equal(y[1:], x[0] + x[inv])
+    assert np.array_equal(im.rader_butterfly(x, p, g, "maps", np.arange(p - 1)), y)
+
+
+@pytest.mark.parametrize("radices", [[2, 17], [17, 4], [3, 17, 17], [29, 31, 2], [89, 4], [8, 97], [257, 2, 2]])
+def test_stockham_identity_maps(radices):
+    """stockham_identity: without Rader radices it is the identity-butterfly
+    Stockham permutation; with them, replacing every identity Rader
+    butterfly by the real one (a DFT, as pinned above) gives the plain
+    stage maps with real butterflies, i.e. numpy.fft."""
+    from oracle import oracle as orc
+    n = int(np.prod(radices))
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((2, n)) + 1j * rng.standard_normal((2, n))
+    plain = [r for r in radices if r <= 16]
+    if plain:
+        m = int(np.prod(plain))
+        xs = x[:, :m]
+        assert np.array_equal(im.stockham_identity(xs, plain), xs[:, im.stockham_perm(m, plain)])
+    # the same stage loop with real butterflies and twiddles is stockham_fft
+    assert np.max(np.abs(im.stockham_fft(x[0], radices) - np.fft.fft(x[0]))) <= 1e-10 * n
+    rader = {r: (orc.primitive_root(r), None) for r in radices if r > 16}
+    y = im.stockham_identity(x, radices, rader)
+    # every output is x0 of its butterfly plus one named input: integer tags stay exact
+    t = np.arange(2 * n, dtype=np.float64).reshape(2, n)
+    yt = im.stockham_identity(t, radices, rader)
+    assert np.array_equal(yt, np.round(yt)) and y.shape == x.shape

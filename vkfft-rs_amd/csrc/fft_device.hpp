@@ -548,7 +548,11 @@ __device__ __noinline__ void stage_rader(cpx<T>* __restrict__ line, cpx<T>* __re
         const int b = e / p, q = e - b * p, j = b % P;
         const cpx<T>* a = scr + b * p;
         cpx<T> acc = a[L];
-        if (q == 0) {
+        if constexpr (kIndexTest) {
+            // identity arithmetic: the unit impulse for the kernel and a[0]
+            // for the DC sum (the gather and scatter show bit for bit)
+            acc = acc + a[q == 0 ? 0 : logq[q]];
+        } else if (q == 0) {
             for (int s = 0; s < L; ++s) acc = acc + a[s];
         } else {
             cpx<T> conv = mk((T)0, (T)0);

@@ -939,6 +939,15 @@ __global__ __launch_bounds__(512) void k_rader_direct(const KArgs a) {
     const cpx<T>* av = lds + g * (N + 1);
     const cpx<T>* b = (const cpx<T>*)a.spec;
     const cpx<T> x0 = av[N];
+    cpx<T>* out = (cpx<T>*)a.out;
+    if constexpr (kIndexTest) {
+        // identity arithmetic: the convolution with the unit impulse
+        // (conv[m] = a[m]) and a[0] for the DC sum, so the gather and the
+        // scatter show bit for bit
+        out[li[g].ob + (long long)a.pout[m] * a.out_es] = x0 + av[m];
+        if (m == 0) out[li[g].ob] = x0 + av[0];
+        return;
+    }
     cpx<T> acc = zero<T>(), dc = zero<T>();
     int bi = m;
     for (int s = 0; s < N; ++s) {
@@ -946,7 +955,6 @@ __global__ __launch_bounds__(512) void k_rader_direct(const KArgs a) {
         dc = dc + av[s];
         bi = bi == 0 ? N - 1 : bi - 1;
     }
-    cpx<T>* out = (cpx<T>*)a.out;
     const T sc = (T)a.scale;
     out[li[g].ob + (long long)a.pout[m] * a.out_es] = scale(x0 + acc, sc);
     if (m == 0) out[li[g].ob] = scale(x0 + dc, sc);
