@@ -378,22 +378,39 @@ enum StageMode : int {
 // and inlined cases share no registers (a dozen radix cases in one body need
 // more than 256 VGPRs and spill to scratch).
 template <typename T, int S, int R, bool WIDE, int MODE, class Ld, class St>
-__device__ __forceinline__ void stage_rt_body(cpx<T>* __restrict__ line, const int N, const int P, const int TT,
-                                              const int t, const int ps, const StageTw& tw, Ld&& ld, St&& st) {
+__device__ __forceinline__ void stage_rt_body(cpx<T>* __restrict__ line, int N, int P, int TT, const int t, int ps,
+                                              const StageTw& tw, Ld&& ld, St&& st) {
+    // The stage's geometry is uniform over the block; the out-of-line stage
+    // receives it in vector registers, so move it to scalar registers and
+    // keep everything derived from it scalar.
+    N = __builtin_amdgcn_readfirstlane(N);
+    P = __builtin_amdgcn_readfirstlane(P);
+    TT = __builtin_amdgcn_readfirstlane(TT);
+    ps = __builtin_amdgcn_readfirstlane(ps);
     constexpr int MJ = dyn_butterflies_per_thread(R, WIDE);
     const int NB = N / R;
+    // LDS slot of element e: e + (e >> ps). When the butterfly stride NB (on
+    // the reads) or P (on the writes) is a multiple of the pad period 2^ps,
+    // the R slots of a butterfly are one padded base plus a uniform padded
+    // stride, one add per element instead of a shift and two adds.
+    const int pmask = ps >= 30 ? 0 : (1 << ps) - 1;
+    const bool rd_uni = (NB & pmask) == 0, wr_uni = (P & pmask) == 0;
+    const int rd_step = NB + (ps >= 30 ? 0 : NB >> ps), wr_step = P + (ps >= 30 ? 0 : P >> ps);
     cpx<T> v[MJ][R];
 #pragma unroll
     for (int j = 0; j < MJ; ++j) {
         const int b = t + j * TT;
         if (b < NB) {
+            if constexpr (MODE == SM_FIRST) {
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                if constexpr (MODE == SM_FIRST) {
-                    v[j][i] = ld(b + i * NB);
-                } else {
-                    v[j][i] = line[lpad(b + i * NB, ps)];
-                }
+                for (int i = 0; i < R; ++i) v[j][i] = ld(b + i * NB);
+            } else if (rd_uni) {
+                const int a0 = lpad(b, ps);
+#pragma unroll
+                for (int i = 0; i < R; ++i) v[j][i] = line[a0 + i * rd_step];
+            } else {
+#pragma unroll
+                for (int i = 0; i < R; ++i) v[j][i] = line[lpad(b + i * NB, ps)];
             }
         }
     }
@@ -403,7 +420,7 @@ __device__ __forceinline__ void stage_rt_body(cpx<T>* __restrict__ line, const i
     for (int j = 0; j < MJ; ++j) {
         const int b = t + j * TT;
         if (b < NB) {
-            const int k = b % P;
+            const int k = (int)((unsigned)b % (unsigned)P);
             if (P > 1) {
                 cpx<T> wp[R];
                 root_powers<R>(stage_root<T>(tw, k * step, P >= kScatterP), wp);
@@ -412,13 +429,16 @@ __device__ __forceinline__ void stage_rt_body(cpx<T>* __restrict__ line, const i
             }
             dft<R, S>(v[j]);
             const int base = (b - k) * R + k;
+            if constexpr (MODE == SM_LAST) {
 #pragma unroll
-            for (int q = 0; q < R; ++q) {
-                if constexpr (MODE == SM_LAST) {
-                    st(base + q * P, v[j][q]);
-                } else {
-                    line[lpad(base + q * P, ps)] = v[j][q];
-                }
+                for (int q = 0; q < R; ++q) st(base + q * P, v[j][q]);
+            } else if (wr_uni) {
+                const int w0 = lpad(base, ps);
+#pragma unroll
+                for (int q = 0; q < R; ++q) line[w0 + q * wr_step] = v[j][q];
+            } else {
+#pragma unroll
+                for (int q = 0; q < R; ++q) line[lpad(base + q * P, ps)] = v[j][q];
             }
         }
     }
