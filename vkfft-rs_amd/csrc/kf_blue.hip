@@ -23,7 +23,8 @@ static const FixedKernel kTable[] = {
     // 252 threads fill four waves, where 8 rows (the second variant) leave the
     // fifth wave half empty; 7 rows took the pass from 82 to 60 us per chunk
     // and C5b from 5.36 to 5.09-5.14 ms on one box (3, 5 and 14 rows, an odd
-    // line stride and 27 threads per row ran slower)
+    // line stride, 27 threads per row and the radix orders 9-9-4 and 9-4-9 at
+    // 7 rows ran slower)
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 45, 16, 30, 405, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 45, 16, 30, 405, true, false, true, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
