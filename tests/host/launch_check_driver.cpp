@@ -100,6 +100,34 @@ int main() {
            hipErrorInvalidConfiguration);
     expect("plain, bad direction", check_launch(KK_PLAIN, 0, 0, p, 32, (size_t)p.G * p.LS * 8, limit, nullptr),
            hipErrorInvalidValue);
+    // the four-step convolution row pass: rows of N2 = N, C = N1 rows per
+    // transform, the spectrum and the W_M table present
+    KArgs cb = p;
+    static const float spec = 0, tw = 0;
+    cb.C = cb.N1 = 4;
+    cb.N2 = cb.N;
+    cb.M = cb.N1 * cb.N2;
+    cb.spec = &spec;
+    cb.tlo = cb.thi = &tw;
+    const size_t cb_lds = (size_t)cb.G * cb.LS * 8;
+    expect("conv rows", check_launch(KK_CONV_B, 0, -1, cb, 32, cb_lds, limit, nullptr), hipSuccess);
+    KArgs cb1 = cb;
+    cb1.spec = nullptr;
+    expect("conv rows without the spectrum", check_launch(KK_CONV_B, 0, -1, cb1, 32, cb_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs cb2 = cb;
+    cb2.tlo = nullptr;
+    expect("conv rows without the twiddle table", check_launch(KK_CONV_B, 0, -1, cb2, 32, cb_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs cb3 = cb;
+    cb3.N2 = cb.N / 2;
+    cb3.M = cb3.N1 * cb3.N2;
+    expect("conv rows, N2 != row length", check_launch(KK_CONV_B, 0, -1, cb3, 32, cb_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs cb4 = cb;
+    cb4.C = cb.N1 + 1;
+    expect("conv rows, C != N1", check_launch(KK_CONV_B, 0, -1, cb4, 32, cb_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
     if (fails) return 1;
     std::printf("ok %d\n", cases);
     return 0;

@@ -57,7 +57,7 @@ def run_case(ctx, dims, batch, prec, matrix=1, symmetric=False, kernels=1, conj=
                                              ([64, 48], 2, F32), ([16, 12, 10], 2, F64), ([256, 256], 1, F32),
                                              ([97, 16], 2, F32), ([48, 97], 3, F64), ([8, 6, 5, 4], 3, F32),
                                              ([1024, 48], 2, F32), ([768, 16, 4], 1, F32),
-                                             ([1024, 8], 2, F64)])
+                                             ([1024, 8], 2, F64), ([3 << 16], 2, F64)])
 def test_scalar_kernel(hip_ctx, dims, batch, prec):
     conv, _, _ = run_case(hip_ctx, dims, batch, prec)
     desc = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
@@ -65,6 +65,10 @@ def test_scalar_kernel(hip_ctx, dims, batch, prec):
     if dims in ([1024], [2048], [360]):
         # one upload: forward FFT, multiply and normalized inverse in one pass
         assert desc["convolution"]["fused"] and labels == ["convolution_fused"], labels
+    elif dims == [1 << 20]:
+        # two uploads: forward column pass, row pass with the multiply between
+        # its forward and inverse FFTs, inverse column pass
+        assert desc["convolution"]["fused"] and labels == FOUR_STEP_LABELS, labels
     elif len(dims) > 1 and dims[0] > 640 and prec == F32:
         # N-D over Stockham axes whose axis 0 the plain plan splits (and whose
         # runtime geometry holds 8 or more columns per block: 1024, 768): the
@@ -74,10 +78,53 @@ def test_scalar_kernel(hip_ctx, dims, batch, prec):
         assert labels.count("convolution_fused_axis0") == 1 and "convolution_multiply" not in labels, labels
         assert len(labels) == 2 * len(dims) - 1, labels
     else:
-        # a Rader axis, an axis 0 of one pass, or (f64) too few columns per
-        # block for the fused kernel keep the separate multiply
+        # a Rader axis, an axis 0 of one pass, (f64) too few columns per
+        # block for the fused kernel, or a two-upload length whose rows (384
+        # for 3 * 2^16 = 512 x 384) have no fixed-shape row pass keep the
+        # separate multiply
         assert not desc["convolution"]["fused"] and "convolution_multiply" in labels
     assert desc["convolution"]["kernels"] == 1 and desc["convolution"]["matrix"] == 0
+
+
+FOUR_STEP_LABELS = ["convolution_columns", "convolution_rows", "convolution_columns_out"]
+
+
+@pytest.mark.parametrize("dims,batch,prec", [([1 << 17], 3, F64), ([100000], 2, F32), ([1000000], 1, F64),
+                                             ([1 << 16], 5, F32)])
+def test_fused_four_step(hip_ctx, dims, batch, prec):
+    """A 1-D scalar convolution over a two-upload length whose row length has
+    a fixed-shape row pass runs as three passes (forward columns with the W_N
+    twiddle; rows: forward FFT, natural-order spectrum multiply, inverse FFT,
+    inverse twiddle; inverse columns) and matches the oracle."""
+    conv, _, _ = run_case(hip_ctx, dims, batch, prec, seed=21)
+    desc = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    labels = [p["kernel"] for p in desc["passes"]]
+    assert desc["convolution"]["fused"] and labels == FOUR_STEP_LABELS, labels
+    assert desc["convolution"]["n1"] * desc["convolution"]["n2"] == dims[0]
+
+
+@pytest.mark.parametrize("conj,cross", [(True, False), (False, True), (True, True)])
+def test_fused_four_step_policies(hip_ctx, conj, cross):
+    """Sequence conjugation and cross-power normalization in the four-step
+    row pass, batch 3, against the oracle."""
+    conv, _, _ = run_case(hip_ctx, [1 << 16], 3, F32, conj=conj, cross=cross, seed=22)
+    assert vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()["convolution"]["fused"]
+
+
+def test_fused_four_step_chunks(monkeypatch, hip_ctx):
+    """Batch chunks of the fused four-step convolution on two stream lanes
+    (a 1 MB work budget: two lines of 2^16 per chunk, five chunks, the last
+    partial), every line against the oracle."""
+    monkeypatch.setenv("VKFX_WORK_BUDGET_MB", "1")
+    ctx = vk.HipExecutionContext(0)
+    try:
+        conv, _, _ = run_case(ctx, [1 << 16], 9, F32, seed=23)
+        desc = vk.Plan(ctx, conv.ir, desc=conv.desc()).describe()
+        labels = [p["kernel"] for p in desc["passes"]]
+        assert desc["convolution"]["chunk"] == 2 and labels == FOUR_STEP_LABELS * 5, labels
+        assert desc["lanes"] == 2
+    finally:
+        ctx.close()
 
 
 @pytest.mark.parametrize("dims,prec", [([1024, 24], F32), ([768, 10, 3], F32)])

@@ -23,6 +23,9 @@
 //                 the inverse four-step twiddle in one kernel
 //   IoFsCBlue     Bluestein column pass: IFFT, chirp multiply, truncate to N
 //   IoBlue1       whole Bluestein transform when the convolution fits LDS
+//   IoConv1       one-upload convolution: FFT, kernel-spectrum multiply, IFFT
+//   IoConvB       two-upload convolution row pass: FFT, natural-order
+//                 kernel-spectrum multiply, IFFT, inverse four-step twiddle
 //
 // Two kernel templates run these policies:
 //   k_dyn  -- runtime length and radix list; lines are staged through LDS on
@@ -872,6 +875,39 @@ struct IoConv1 : IoPlain {
     }
 };
 
+// Row pass of a convolution over a two-upload length N = N1 * N2, between the
+// forward column pass (KK_FS_A, W_N^(n2*k1) on store) and the inverse column
+// pass (KK_FS_A over k1 with no twiddle): FFT of row k1 over n2, multiply by
+// the kernel spectrum in natural order K[k1 + N1*k2] as KK_CONV_1 does
+// (conjugated sequence, cross-power normalization) and by the 1/N of the
+// normalized inverse, inverse FFT over k2, inverse twiddle W_N^(-k1*m2); rows
+// stay in place. Three HBM passes instead of the two forward passes, the
+// multiply pass and the two inverse passes.
+struct IoConvB : IoBlueB {
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> conv_mul(const KArgs& a, cpx<T> x, long long k) {
+        if constexpr (kIndexTest) return x;
+        if (a.flags & KF_CONV_CONJ) x = conj(x);
+        cpx<T> y = cmul(x, ((const cpx<T>*)a.spec)[k]);
+        if (a.flags & KF_CONV_CROSS) {
+            const T r = (T)1 / sqrt(y.re * y.re + y.im * y.im);
+            y = mk(y.re * r, y.im * r);
+        }
+        return scale(y, (T)a.scale);
+    }
+    template <typename T, class D>
+    static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
+            cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
+            v = conv_mul(a, v, li[g].c + (long long)e * a.N1);
+        });
+    }
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> mid_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        return conv_mul(a, v, L.c + (long long)e * a.N1);
+    }
+};
+
 // Rader, FFT convolution (rader_ir.rs:1957-2101): a[s] = x[g^-s] gathered
 // into LDS, FFT of length p-1 (= N here), multiply by FFT(b)/(p-1) with
 // b[n] = exp(dir 2 pi i g^n / p), inverse FFT, X[g^m] = x0 + conv[m] and
@@ -1582,6 +1618,7 @@ KernelFn pick_dyn(KernelKind kind) {
         case KK_RADER_FFT: return k_dyn<T, S, IoRader, W>;
         case KK_RADER_DIRECT: return k_rader_direct<T>;
         case KK_CONV_1: return k_dyn<T, S, IoConv1, W>;
+        case KK_CONV_B: return k_dyn<T, S, IoConvB, W>;
         default: return nullptr;
     }
 }

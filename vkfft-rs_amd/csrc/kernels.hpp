@@ -34,6 +34,7 @@ enum KernelKind : int {
     KK_RADER_FFT,      // prime length p: gather, FFT(p-1), kernel multiply, IFFT, scatter
     KK_RADER_DIRECT,   // prime length p: gather, O(p^2) cyclic convolution, scatter
     KK_CONV_1,         // convolution in one kernel: FFT, kernel-spectrum multiply, normalized IFFT
+    KK_CONV_B,         // four-step convolution row pass: FFT, natural-order spectrum multiply, IFFT, W_M^-1
     KK_COUNT
 };
 
@@ -45,8 +46,8 @@ enum KFlags : int {
     KF_DYN_WIDE = 16,     // runtime-shape kernel holding up to 32 elements per thread per stage
     KF_DYN_DIRECT = 32,   // runtime-shape C2C with HBM-direct first and last stages (contiguous lines)
     KF_DYN_PRE = 64,      // with KF_DYN_DIRECT, even C2R: the first stage forms the preprocess from HBM
-    KF_CONV_CONJ = 128,   // KK_CONV_1: conjugate the sequence spectrum (ConvolutionConjugation::Sequence)
-    KF_CONV_CROSS = 256,  // KK_CONV_1: cross-power-spectrum normalization of the product
+    KF_CONV_CONJ = 128,   // KK_CONV_1/B: conjugate the sequence spectrum (ConvolutionConjugation::Sequence)
+    KF_CONV_CROSS = 256,  // KK_CONV_1/B: cross-power-spectrum normalization of the product
     // KK_PLAIN in the staged runtime-shape kernel with the plan's boundary
     // work inside its loads and stores (IoEdge): storage of half the compute
     // precision on the input / output side, and the zero interval [zl, zr) of

@@ -36,6 +36,7 @@ const FixedKernel* fixed_table_round_fs_f32(int* count);
 const FixedKernel* fixed_table_round_fs_f64(int* count);
 const FixedKernel* fixed_table_blue_rows_f32(int* count);
 const FixedKernel* fixed_table_blue_rows_f64(int* count);
+const FixedKernel* fixed_table_conv(int* count);
 
 // All registered fixed-shape instantiations, merged once (thread-safe
 // static initialisation).
@@ -52,7 +53,8 @@ static const FixedKernel* registry(int* count) {
                                                 fixed_table_round_nd_f32, fixed_table_round_nd_f64,
                                                 fixed_table_round_real_f32, fixed_table_round_real_f64,
                                                 fixed_table_round_fs_f32, fixed_table_round_fs_f64,
-                                                fixed_table_blue_rows_f32, fixed_table_blue_rows_f64};
+                                                fixed_table_blue_rows_f32, fixed_table_blue_rows_f64,
+                                                fixed_table_conv};
         constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
         int counts[kTables], sum = 0;
         const FixedKernel* ptrs[kTables];

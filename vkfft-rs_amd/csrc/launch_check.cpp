@@ -18,6 +18,11 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
         lds_bytes > lds_limit)
         return hipErrorInvalidConfiguration;
     if (kind == KK_CONV_1 && !a.spec) return hipErrorInvalidConfiguration;
+    // the four-step convolution row pass: rows k1 < N1 of N2 = N elements,
+    // the N1 x N2 spectrum and the W_M table
+    if (kind == KK_CONV_B && (!a.spec || !a.tlo || !a.thi || a.N2 != a.N || a.N1 < 1 || a.C != a.N1 ||
+                              a.M != a.N1 * a.N2))
+        return hipErrorInvalidConfiguration;
     if (kind == KK_RADER_DIRECT && (a.TT != a.N || a.LS < a.N + 1 || a.N < 1 || !a.pin || !a.pout))
         return hipErrorInvalidConfiguration;
     if (kind == KK_RADER_FFT && (!a.pin || !a.pout || a.LS < a.N + ((a.N - 1) >> a.PS) + 1))

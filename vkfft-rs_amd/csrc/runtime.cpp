@@ -1830,6 +1830,72 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
             return add_launch(c, KK_CONV_1, -1, g, a, lines, blocks_for(lines, g.G), SEL_IN, 0, SEL_OUT, 0,
                               "convolution_fused");
         }
+        // two uploads (N = N1 * N2): the forward column pass (FFT over n1,
+        // W_N^(n2*k1)) into the workspace, one row pass (FFT over n2, multiply,
+        // inverse FFT, W_N^(-k1*m2)) in place, and the inverse column pass
+        // into the output, whose twiddle row c / N2 is 0 (no twiddle): three
+        // HBM passes per chunk instead of five
+        size_t n1 = 0, n2 = 0;
+        if (!g0.ok && four_step_split(n, c.prec, c.lds_max, &n1, &n2)) {
+            const int prec = c.prec;
+            Geometry ga = kernel_geometry(KK_FS_A, prec, -1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+            Geometry gc = kernel_geometry(KK_FS_A, prec, 1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
+            Geometry gb = kernel_geometry(KK_CONV_B, prec, -1, n2, false,
+                                          std::max(1, 256 / std::max(1, geometry(n2, prec, 1, c.lds_max, c.lds_max).TT)),
+                                          c.lds_max, c.lds_budget);
+            // only with a fixed-shape row pass: on the runtime-shape kernel
+            // the three passes are no faster than the five of fixed shapes
+            // (10^5 = 400 x 250 f32 before its row shape: 0.32 ms fused
+            // against 0.25 ms for the forward and inverse transforms alone)
+            if (ga.ok && gb.ok && gc.ok && gb.fixed) {
+                const void *tlo, *thi;
+                int tsh;
+                int rc = two_level(p, n, prec, &tlo, &thi, &tsh);
+                if (rc) return rc;
+                const size_t chunk = chunk_for(d.batch, n * cs, 64);
+                p->work_bytes = std::max(p->work_bytes, chunk * n * cs);
+                p->full_bytes = 0;
+                p->serial = false;
+                c.js << ",\"fused\":true,\"n1\":" << n1 << ",\"n2\":" << n2 << ",\"chunk\":" << chunk << "},";
+                for (size_t b0 = 0; b0 < d.batch; b0 += chunk) {
+                    c.cur_chunk = (int)(b0 / chunk);
+                    const size_t cb = std::min(chunk, d.batch - b0);
+                    KArgs a = blank();
+                    a.C = (long long)n2;
+                    a.in_es = a.out_es = (long long)n2;
+                    a.in_cs = a.out_cs = 1;
+                    a.in_os = a.out_os = (long long)n;
+                    a.tlo = tlo, a.thi = thi, a.tshift = tsh;
+                    a.M = (long long)n, a.N1 = (long long)n1, a.N2 = (long long)n2;
+                    long long lines = (long long)(cb * n2);
+                    rc = add_launch(c, KK_FS_A, -1, ga, a, lines, blocks_for(lines, ga.G), SEL_IN, b0 * n * cs,
+                                    SEL_WORK, 0, "convolution_columns");
+                    if (rc) return rc;
+                    KArgs b = blank();
+                    b.C = (long long)n1;
+                    b.in_es = b.out_es = 1;
+                    b.in_cs = b.out_cs = (long long)n2;
+                    b.in_os = b.out_os = (long long)n;
+                    b.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR | (ca.conj_seq ? KF_CONV_CONJ : 0) |
+                              (ca.cross_norm ? KF_CONV_CROSS : 0);
+                    b.spec = kernel;
+                    b.scale = 1.0 / (double)n;
+                    b.tlo = tlo, b.thi = thi, b.tshift = tsh;
+                    b.M = (long long)n, b.N1 = (long long)n1, b.N2 = (long long)n2;
+                    lines = (long long)(cb * n1);
+                    rc = add_launch(c, KK_CONV_B, -1, gb, b, lines, blocks_for(lines, gb.G), SEL_WORK, 0, SEL_WORK,
+                                    0, "convolution_rows");
+                    if (rc) return rc;
+                    KArgs e = a;
+                    e.twdiv = (long long)n2;
+                    lines = (long long)(cb * n2);
+                    rc = add_launch(c, KK_FS_A, 1, gc, e, lines, blocks_for(lines, gc.G), SEL_WORK, 0, SEL_OUT,
+                                    b0 * n * cs, "convolution_columns_out");
+                    if (rc) return rc;
+                }
+                return VKFX_OK;
+            }
+        }
     }
     // N-D scalar convolution over Stockham axes whose axis 0 the plain N-D
     // plan splits into two passes per direction: the forward FFT of every
