@@ -290,6 +290,8 @@ __device__ __forceinline__ void dft(cpx<T>* x) {
         dft_composite<5, 2, S>(x);
     } else if constexpr (R == 12) {
         dft_composite<3, 4, S>(x);
+    } else if constexpr (R == 18) {
+        dft_composite<9, 2, S>(x);
     } else {
         dft_odd<R, S>(x);
     }

@@ -17,20 +17,24 @@ static const FixedKernel kTable[] = {
     // M = 131220: product-tree twiddles (per-stage tables measured 4% slower;
     // on the row pass 10-20% slower). Column passes of 405 with 45 threads
     // per column (one radix-9 butterfly each: 1.3% over 27 threads, the second
-    // variant; 8 columns per block, 64-byte row segments, ran 5-14% slower).
-    // The 324-point row pass with 36 threads per row (radix 4, 9, 9: one
-    // radix-9 butterfly per thread, three radix-4 rounds) and 7 rows per block:
-    // 252 threads fill four waves, where 8 rows (the second variant) leave the
-    // fifth wave half empty; 7 rows took the pass from 82 to 60 us per chunk
-    // and C5b from 5.36 to 5.09-5.14 ms on one box (3, 5 and 14 rows, an odd
-    // line stride, 27 threads per row and the radix orders 9-9-4 and 9-4-9 at
-    // 7 rows ran slower)
+    // variant; 8 columns per block, 64-byte row segments, ran 5-14% slower;
+    // 15 threads per column with radices 27 and 15, two LDS exchanges
+    // instead of three and 30% fewer instructions per element but 101-117
+    // VGPRs, took C5b from 5.04-5.07 to 5.20-5.24 ms, its inverse column pass
+    // from 58 to 72 us). The 324-point row pass: 18 threads per row, two
+    // radix-18 stages (nine-by-two composite butterflies: 121 instead of 156
+    // VALU instructions per element, 7 instead of 11 barriers, 94 VGPRs),
+    // 7 rows per block, C5b 5.06-5.08 against 5.16 ms for the second variant
+    // (36 threads per row, radix 4, 9, 9, 7 rows: 252 threads fill four
+    // waves; 8 rows, 3, 5 and 14 rows, an odd line stride, 27 threads per row
+    // and the radix orders 9-9-4 and 9-4-9 ran slower; 14 rows of 18 threads
+    // measured the same as 7)
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 45, 16, 30, 405, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 45, 16, 30, 405, true, false, true, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_A_BLUE, IoFsABlue, float, 0, -1, 405, 27, 16, 30, 407, true, true, false, 9, 9, 5),
     VKFX_FIXED_NT(KK_FS_C_BLUE, IoFsCBlue, float, 0, 1, 405, 27, 16, 30, 407, true, false, true, 9, 9, 5),
+    VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 18, 7, 30, 324, false, false, false, 18, 18),
     VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 36, 7, 30, 324, false, false, false, 4, 9, 9),
-    VKFX_FIXED_NT(KK_BLUE_B, IoBlueB, float, 0, -1, 324, 36, 8, 30, 324, false, false, false, 4, 9, 9),
 };
 
 const FixedKernel* fixed_table_blue(int* count) {

@@ -61,7 +61,8 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
     // staged runtime-shape kernel, which gives each line a second LDS region
     // of LS elements after the G lines: 2 G LS elements in all
     bool rader_stage = false;
-    for (int i = 0; i < a.nstages; ++i) rader_stage = rader_stage || a.radix[i] > kMaxStockhamRadix;
+    // (a fixed shape's radices are compile-time Stockham butterflies)
+    for (int i = 0; i < a.nstages; ++i) rader_stage = rader_stage || (!fixed && a.radix[i] > kMaxStockhamRadix);
     if (rader_stage && !a.rtab) return hipErrorInvalidConfiguration;
     if (((a.flags & KF_RADER) != 0) != (a.rtab != nullptr)) return hipErrorInvalidConfiguration;
     if (a.rtab) {
