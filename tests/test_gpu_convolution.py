@@ -181,13 +181,16 @@ def test_phase_correlation_finds_shift(hip_ctx):
     assert np.max(np.abs(y - e)) <= 1e-5
 
 
-def test_mixed_storage_scalar(hip_ctx):
-    n = 4096
+@pytest.mark.parametrize("n", [4096, 1 << 16])
+def test_mixed_storage_scalar(hip_ctx, n):
+    """Mixed storage around the one-upload fused kernel (4096) and the
+    three-pass two-upload convolution (2^16)."""
     x = o.complex_uniform(n, 8, np.complex64)
     k = o.complex_uniform(n, 9, np.complex128)
     for prec, tol in ((vk.Precision.F64ComputeF32Storage, 1e-7), (vk.Precision.F16StorageF32Compute, 2e-3)):
         conv = vk.ConvolutionIr.build(conv_cfg([n], 1, prec), k)
         y = hip_ctx.execute_convolution(conv, x)
+        assert vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()["convolution"]["fused"], (n, prec)
         xin = x if prec == vk.Precision.F64ComputeF32Storage else \
             x.view(np.float32).astype(np.float16).astype(np.float32).view(np.complex64)
         kin = k if prec == vk.Precision.F64ComputeF32Storage else k.astype(np.complex64)
