@@ -128,6 +128,67 @@ int main() {
     cb4.C = cb.N1 + 1;
     expect("conv rows, C != N1", check_launch(KK_CONV_B, 0, -1, cb4, 32, cb_lds, limit, nullptr),
            hipErrorInvalidConfiguration);
+    // the mixed-storage four-step passes: fixed shapes only, the column pass
+    // with the narrow input, the row pass with the narrow output
+    FixedKernel fe;
+    std::memset(&fe, 0, sizeof fe);
+    fe.kind = KK_FS_A_EDGE;
+    fe.dir = -1;
+    fe.N = p.N;
+    fe.TT = p.TT;
+    fe.G = p.G;
+    fe.PS = p.PS;
+    fe.LS = p.LS;
+    fe.nst = p.nstages;
+    fe.col = true;
+    for (int i = 0; i < p.nstages; ++i) fe.radix[i] = p.radix[i];
+    fe.lds_mult = 1;
+    KArgs ea = p;
+    ea.C = ea.N2 = 64;
+    ea.N1 = ea.N;
+    ea.M = ea.N1 * ea.N2;
+    ea.flags = KF_NARROW_IN;
+    const size_t e_lds = (size_t)ea.G * ea.LS * 8;
+    expect("fs edge columns", check_launch(KK_FS_A_EDGE, 0, -1, ea, 32, e_lds, limit, &fe), hipSuccess);
+    expect("fs edge columns on the runtime kernel", check_launch(KK_FS_A_EDGE, 0, -1, ea, 32, e_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs ea1 = ea;
+    ea1.flags = 0;
+    expect("fs edge columns without the narrow input", check_launch(KK_FS_A_EDGE, 0, -1, ea1, 32, e_lds, limit, &fe),
+           hipErrorInvalidConfiguration);
+    KArgs ea2 = ea;
+    ea2.flags |= KF_ZERO_IN;
+    ea2.zl = 10, ea2.zr = ea.M + 1;
+    expect("fs edge columns, zero interval past the line", check_launch(KK_FS_A_EDGE, 0, -1, ea2, 32, e_lds, limit, &fe),
+           hipErrorInvalidConfiguration);
+    ea2.zr = ea.M;
+    expect("fs edge columns, zero interval", check_launch(KK_FS_A_EDGE, 0, -1, ea2, 32, e_lds, limit, &fe), hipSuccess);
+    KArgs ea3 = ea;
+    ea3.flags |= KF_NARROW_OUT;
+    expect("fs edge columns with a narrow output", check_launch(KK_FS_A_EDGE, 0, -1, ea3, 32, e_lds, limit, &fe),
+           hipErrorInvalidConfiguration);
+    FixedKernel fb = fe;
+    fb.kind = KK_FS_B_EDGE;
+    fb.col = false;
+    KArgs eb = p;
+    eb.C = eb.N1 = 64;
+    eb.N2 = eb.N;
+    eb.M = eb.N1 * eb.N2;
+    eb.flags = KF_NARROW_OUT | KF_ZERO_OUT;
+    eb.zl = 0, eb.zr = 5;
+    expect("fs edge rows", check_launch(KK_FS_B_EDGE, 0, -1, eb, 32, e_lds, limit, &fb), hipSuccess);
+    KArgs eb1 = eb;
+    eb1.flags = KF_NARROW_OUT | KF_ZERO_IN;
+    expect("fs edge rows with an input zero interval", check_launch(KK_FS_B_EDGE, 0, -1, eb1, 32, e_lds, limit, &fb),
+           hipErrorInvalidConfiguration);
+    KArgs eb2 = eb;
+    eb2.C = eb.N1 - 1;
+    expect("fs edge rows, C != N1", check_launch(KK_FS_B_EDGE, 0, -1, eb2, 32, e_lds, limit, &fb),
+           hipErrorInvalidConfiguration);
+    KArgs eb3 = eb;
+    eb3.flags |= KF_EDGE;
+    expect("fs edge rows with KF_EDGE", check_launch(KK_FS_B_EDGE, 0, -1, eb3, 32, e_lds, limit, &fb),
+           hipErrorInvalidConfiguration);
     if (fails) return 1;
     std::printf("ok %d\n", cases);
     return 0;

@@ -178,13 +178,17 @@ def test_pass_resource_reports(hip_ctx):
     real = hip_ctx.plan(real_irs(1 << 20, 4)[0]).resources()
     assert [p["pass"] for p in real] == ["r2c_four_step_columns", "r2c_four_step_rows"] or len(real) == 2
     assert all(p["resident_blocks_per_cu"] >= 1 for p in real)
-    # mixed storage: converted inside the one-upload pass, or boundary passes
-    # around a four-step
+    # mixed storage: converted inside the one-upload pass or the two four-step
+    # passes with fixed edge shapes, else boundary passes around the plan
     mixed = vk.TransformIr.build(vk.FftConfig.new([1024]).with_batch_count(4)
                                  .with_precision(vk.Precision.F64ComputeF32Storage), FWD)
     fused = hip_ctx.plan(mixed).resources()
     assert [p["pass"] for p in fused] == ["stockham"] and fused[0]["resident_blocks_per_cu"] >= 1
     mixed = vk.TransformIr.build(vk.FftConfig.new([1 << 20]).with_batch_count(1)
+                                 .with_precision(vk.Precision.F64ComputeF32Storage), FWD)
+    names = [p["pass"] for p in hip_ctx.plan(mixed).resources()]
+    assert names == ["four_step_columns", "four_step_rows"], names
+    mixed = vk.TransformIr.build(vk.FftConfig.new([3 << 16]).with_batch_count(1)
                                  .with_precision(vk.Precision.F64ComputeF32Storage), FWD)
     names = [p["pass"] for p in hip_ctx.plan(mixed).resources()]
     assert names[0] == "boundary_in" and names[-1] == "boundary_out"

@@ -127,8 +127,9 @@ def test_zero_padding_fused(hip_ctx, monkeypatch, direction, domain, n, left, ri
 
 def test_fused_edges_device_resident_and_chunks(hip_ctx, monkeypatch):
     """Device-resident f16 buffers through the fused plan, a batch large
-    enough for several chunks, and a plan that does not qualify (four-step)
-    keeping its boundary passes."""
+    enough for several chunks, and a plan that does not qualify (a
+    two-upload length without fixed edge shapes) keeping its boundary
+    passes."""
     import torch
     n, batch = 1024, 4096
     x = o.complex_uniform(n * batch, 31, np.complex64)
@@ -145,10 +146,79 @@ def test_fused_edges_device_resident_and_chunks(hip_ctx, monkeypatch):
         for b in (0, 1, 2047, 4095):
             ref = o.fft(f16(x[b * n:(b + 1) * n]).astype(np.complex128))
             assert o.rel_l2(y[b * n:(b + 1) * n], ref) <= 1e-3, b
-        big = vk.TransformIr.build(vk.FftConfig.new([1 << 20]).with_batch_count(2).with_precision(F16S), FWD)
+        # 3 * 2^16 = 512 x 384: no fixed edge shape for the 384-point rows
+        big = vk.TransformIr.build(vk.FftConfig.new([3 << 16]).with_batch_count(2).with_precision(F16S), FWD)
         assert not ctx.plan(big).describe()["boundary"]["fused_edges"]
     finally:
         ctx.close()
+
+
+FOUR_STEP = ["four_step_columns", "four_step_rows"]
+
+
+@pytest.mark.parametrize("n,batch", [(1 << 16, 3), (1 << 18, 2), (1 << 20, 1)])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_mixed_storage_four_step(hip_ctx, monkeypatch, n, batch, direction):
+    """Two-upload C2C lengths whose factors have fixed edge shapes: the
+    column pass reads the storage type and the row pass writes it (no
+    boundary pass, no compute-type copy), against the oracle and against the
+    boundary-pass plan."""
+    x = o.complex_uniform(n * batch, n % 997 + batch, np.complex64)
+    for prec, tol in ((F64C, 1e-7), (F16S, 1e-3)):
+        c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_inverse_normalization(True)
+        y, desc, yb = run_both(monkeypatch, c, direction, x)
+        assert desc["boundary"]["four_step_edges"]
+        assert [p["kernel"] for p in desc["passes"]] == FOUR_STEP, desc["passes"]
+        xin = f16(x) if prec == F16S else x
+        ref = ref_c2c(xin, [n], batch, direction, normalize=True)
+        assert o.rel_l2(y, ref) <= tol, prec
+        assert o.rel_l2(yb, ref) <= tol, prec
+        if prec == F16S:
+            assert np.array_equal(y, f16(y))
+
+
+@pytest.mark.parametrize("direction,domain", [(FWD, SPATIAL), (INV, SPATIAL), (FWD, FREQ)])
+@pytest.mark.parametrize("left,right", [(1000, 40000), (0, 1), (65000, 65536)])
+def test_mixed_storage_four_step_zero_padding(hip_ctx, monkeypatch, direction, domain, left, right):
+    """The zero interval of a 1-D zero padding in the mixed-storage
+    four-step passes: element n2 + n1 * N2 of the column pass reads as zero,
+    element k1 + k2 * N1 of the row pass is written as zero."""
+    n, batch = 1 << 16, 2
+    x = o.complex_uniform(n * batch, left + 3, np.complex64)
+    mask = np.zeros((batch, n), dtype=bool)
+    mask[:, left:right] = True
+    mask = mask.reshape(-1)
+    input_side = (direction == FWD) == (domain == SPATIAL)
+    for prec, tol in ((F64C, 1e-7), (F16S, 1e-3)):
+        c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+            .with_zero_padding(0, left, right).with_zero_padding_domain(domain)
+        y, desc, yb = run_both(monkeypatch, c, direction, x)
+        assert desc["boundary"]["four_step_edges"]
+        xin = f16(x) if prec == F16S else x
+        xin = np.where(mask, 0, xin) if input_side else xin
+        expect = ref_c2c(xin, [n], batch, direction)
+        if not input_side:
+            expect = np.where(mask, 0, expect)
+            assert (y[mask] == 0).all() and (yb[mask] == 0).all()
+        assert o.rel_l2(y, expect) <= tol, prec
+        assert o.rel_l2(yb, expect) <= tol, prec
+
+
+def test_mixed_storage_four_step_chunks(hip_ctx, monkeypatch):
+    """Batch chunks of the mixed-storage four-step plan on two stream lanes
+    (a 1 MB work budget: five chunks of two lines in f32 compute, nine of
+    one line in f64 compute), every line against the oracle."""
+    monkeypatch.setenv("VKFX_WORK_BUDGET_MB", "1")
+    n, batch = 1 << 16, 9
+    x = o.complex_uniform(n * batch, 57, np.complex64)
+    for prec, tol, chunks in ((F16S, 1e-3, 5), (F64C, 1e-7, 9)):
+        c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec)
+        y, desc, yb = run_both(monkeypatch, c, FWD, x)
+        assert desc["boundary"]["four_step_edges"] and desc["lanes"] == 2
+        assert [p["kernel"] for p in desc["passes"]] == FOUR_STEP * chunks
+        xin = f16(x) if prec == F16S else x
+        ref = ref_c2c(xin, [n], batch, FWD)
+        assert o.rel_l2(y, ref) <= tol and o.rel_l2(yb, ref) <= tol, prec
 
 
 def layout_cfg(dims, batch, prec, fmt_in, fmt_out):

@@ -54,7 +54,7 @@ def test_hip_f64_compute_f32_storage_matches_cpu(hip_ctx):
 
 
 @pytest.mark.parametrize("dims,batch,fused", [([1024], 16, True), ([4099], 4, False), ([64, 48], 2, False),
-                                              ([1 << 20], 1, False), ([97], 5, False)])
+                                              ([1 << 20], 1, True), ([3 << 16], 1, False), ([97], 5, False)])
 def test_f64_compute_f32_storage(hip_ctx, dims, batch, fused):
     count = int(np.prod(dims)) * batch
     x = o.complex_uniform(count, count % 991, np.complex64)
@@ -65,8 +65,10 @@ def test_f64_compute_f32_storage(hip_ctx, dims, batch, fused):
     # f64 passes: the only error left is rounding the result to f32
     assert o.rel_l2(y, ref) <= 1e-7
     desc = hip_ctx.plan(ir).describe()
-    # a 1-D one-upload Stockham pass converts in its own loads and stores;
-    # N-D, four-step, Bluestein and Rader plans keep boundary passes
+    # a 1-D one-upload Stockham pass, and the two passes of a two-upload
+    # length with fixed edge shapes (2^20 = 1024 x 1024), convert in their
+    # own loads and stores; N-D, other four-step (3 * 2^16 = 512 x 384),
+    # Bluestein and Rader plans keep boundary passes
     assert desc["boundary"]["fused_edges"] == fused
     boundary = desc["passes"][0]["kernel"] == "boundary_in" and desc["passes"][-1]["kernel"] == "boundary_out"
     assert boundary != fused

@@ -17,6 +17,8 @@
 //                 (bluestein_ir.rs:436-708), the C2R variant fuses the
 //                 even-half preprocess
 //   IoFsB         four-step row pass with transposed (natural-order) store
+//   IoFsAEdge,    the two passes of a mixed-storage two-upload C2C with the
+//   IoFsBEdge     storage conversion and zero intervals in their loads / stores
 //   IoFsBR2C      row pass that owns mirror rows k1 and N1-k1 so the R2C
 //                 postprocess is fused into the store
 //   IoBlueB       Bluestein row pass: FFT, kernel-spectrum multiply, IFFT and
@@ -628,6 +630,28 @@ struct IoFsAC2RDirect : IoFsAC2R {
     }
 };
 
+// The first pass of a mixed-storage two-upload C2C: IoFsA reading the
+// caller's input in the storage type of half the compute precision
+// (KF_NARROW_IN), with the line's input zero interval [zl, zr) read as zero
+// (KF_ZERO_IN); element n1 of column n2 is line element n2 + n1 * N2.
+struct IoFsAEdge : IoFsA {
+    static constexpr bool kPtrLoad = false;
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        if (a.flags & KF_ZERO_IN) {
+            const long long n = L.c + (long long)e * a.N2;
+            if (n >= a.zl && n < a.zr) return zero<T>();
+        }
+        using U = typename Narrow<T>::type;
+        const cpx<U> v = ldg_in<NTIO>(a, (const cpx<U>*)a.in + L.ib + e * a.in_es);
+        return mk((T)v.re, (T)v.im);
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoFsAEdge, D>(a, lds, li, false);
+    }
+};
+
 // Four-step row pass. Line = row k1 (C = N1), contiguous in the scratch;
 // FFT over n2 (length N2); store X[k1 + N1*k2] (column-coalesced).
 struct IoFsB : IoPlain {
@@ -640,6 +664,29 @@ struct IoFsB : IoPlain {
     template <typename T, int S, class D>
     static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
         staged_store<IoPlain, D, T, S>(a, lds, li, false);
+    }
+};
+
+// The last pass of a mixed-storage two-upload C2C: IoFsB writing the
+// caller's output in the storage type of half the compute precision (scaled,
+// rounded to nearest, KF_NARROW_OUT), with the line's output zero interval
+// [zl, zr) written as zero (KF_ZERO_OUT); element k2 of row k1 is line
+// element k1 + k2 * N1.
+struct IoFsBEdge : IoFsB {
+    static constexpr bool kPtrStore = false;
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        v = scale(v, (T)a.scale);
+        if (a.flags & KF_ZERO_OUT) {
+            const long long k = L.c + (long long)e * a.N1;
+            if (k >= a.zl && k < a.zr) v = zero<T>();
+        }
+        using U = typename Narrow<T>::type;
+        stg_out<NTIO>(a, (cpx<U>*)a.out + L.ob + e * a.out_es, mk((U)v.re, (U)v.im));
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoFsBEdge, D, T, S>(a, lds, li, false);
     }
 };
 

@@ -35,6 +35,8 @@ enum KernelKind : int {
     KK_RADER_DIRECT,   // prime length p: gather, O(p^2) cyclic convolution, scatter
     KK_CONV_1,         // convolution in one kernel: FFT, kernel-spectrum multiply, normalized IFFT
     KK_CONV_B,         // four-step convolution row pass: FFT, natural-order spectrum multiply, IFFT, W_M^-1
+    KK_FS_A_EDGE,      // KK_FS_A reading half-precision storage, input zero interval (fixed shapes only)
+    KK_FS_B_EDGE,      // KK_FS_B writing half-precision storage, output zero interval (fixed shapes only)
     KK_COUNT
 };
 
@@ -184,6 +186,10 @@ const FixedKernel* find_fixed(KernelKind kind, int prec, int dir, int N, bool co
 // The registered instantiation with the same shape as f and the given
 // nontemporal load/store choice; f itself when none is registered.
 const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto);
+// The registered shape of another kind with f's geometry (length, threads,
+// lines per block, LDS stride and pad, radices), any nontemporal variant;
+// null if there is none.
+const FixedKernel* kind_variant(const FixedKernel* f, KernelKind kind);
 
 // Launches one kernel. prec: 0 = f32, 1 = f64. dir: -1 forward, +1 inverse
 // (direction of the first FFT the kernel runs). fixed: the fixed-shape

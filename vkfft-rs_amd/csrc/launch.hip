@@ -37,6 +37,7 @@ const FixedKernel* fixed_table_round_fs_f64(int* count);
 const FixedKernel* fixed_table_blue_rows_f32(int* count);
 const FixedKernel* fixed_table_blue_rows_f64(int* count);
 const FixedKernel* fixed_table_conv(int* count);
+const FixedKernel* fixed_table_fs_edge(int* count);
 
 // All registered fixed-shape instantiations, merged once (thread-safe
 // static initialisation).
@@ -54,7 +55,7 @@ static const FixedKernel* registry(int* count) {
                                                 fixed_table_round_real_f32, fixed_table_round_real_f64,
                                                 fixed_table_round_fs_f32, fixed_table_round_fs_f64,
                                                 fixed_table_blue_rows_f32, fixed_table_blue_rows_f64,
-                                                fixed_table_conv};
+                                                fixed_table_conv, fixed_table_fs_edge};
         constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
         int counts[kTables], sum = 0;
         const FixedKernel* ptrs[kTables];
@@ -132,6 +133,23 @@ const FixedKernel* fixed_variant(const FixedKernel* f, bool nti, bool nto) {
         if (same) return &v;
     }
     return f;
+}
+
+const FixedKernel* kind_variant(const FixedKernel* f, KernelKind kind) {
+    if (!f) return nullptr;
+    int total = 0;
+    const FixedKernel* all = registry(&total);
+    for (int i = 0; i < total; ++i) {
+        const FixedKernel& v = all[i];
+        if (v.kind != kind || v.prec != f->prec || v.dir != f->dir || v.N != f->N || v.col != f->col ||
+            v.TT != f->TT || v.G != f->G || v.PS != f->PS || v.LS != f->LS || v.nst != f->nst ||
+            v.table != f->table || v.lds_mult != f->lds_mult)
+            continue;
+        bool same = true;
+        for (int s = 0; s < v.nst; ++s) same = same && v.radix[s] == f->radix[s];
+        if (same) return &v;
+    }
+    return nullptr;
 }
 
 static int lds_limit_bytes() {

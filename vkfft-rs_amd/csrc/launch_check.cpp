@@ -39,8 +39,23 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
         return hipErrorInvalidConfiguration;
     // boundary work runs in the runtime-shape C2C kernels only (staged, or
     // HBM-direct under the direct kernel's own conditions below)
-    if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE))
+    const bool fs_edge = kind == KK_FS_A_EDGE || kind == KK_FS_B_EDGE;
+    if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE) && !fs_edge)
         return hipErrorInvalidValue;
+    // the mixed-storage four-step passes: fixed shapes, the first pass reads
+    // the narrow input (and its zero interval), the last writes the narrow
+    // output (and its zero interval), over line elements [0, M)
+    if (fs_edge) {
+        if (!fixed || (a.flags & KF_EDGE)) return hipErrorInvalidConfiguration;
+        if (kind == KK_FS_A_EDGE &&
+            (!(a.flags & KF_NARROW_IN) || (a.flags & (KF_NARROW_OUT | KF_ZERO_OUT)) || a.N2 < 1 || a.C != a.N2))
+            return hipErrorInvalidConfiguration;
+        if (kind == KK_FS_B_EDGE &&
+            (!(a.flags & KF_NARROW_OUT) || (a.flags & (KF_NARROW_IN | KF_ZERO_IN)) || a.N1 < 1 || a.C != a.N1))
+            return hipErrorInvalidConfiguration;
+        if ((a.flags & (KF_ZERO_IN | KF_ZERO_OUT)) && (a.zl < 0 || a.zl > a.zr || a.zr > a.M))
+            return hipErrorInvalidConfiguration;
+    }
     if ((a.flags & KF_EDGE) && (fixed || kind != KK_PLAIN || (a.flags & KF_DYN_PRE) || a.zl > a.zr || a.zl < 0 ||
                                 a.zr > a.N))
         return hipErrorInvalidConfiguration;

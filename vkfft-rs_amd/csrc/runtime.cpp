@@ -2761,7 +2761,50 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         // boundary passes) but not on N-D column passes (F16 2048^2 x 4: the
         // runtime-shape column pass with the conversion 145 us against 35 us
         // for the fixed shape plus 40 us for a flat conversion pass).
-        const bool fused_edges = shape_ok && (mixed || any_zero) && rank == 1 && (!want_layout || layout_ok);
+        // Mixed-storage 1-D two-upload C2C: per chunk the column pass (the
+        // caller's input into the workspace) and the row pass (the workspace
+        // into the caller's output) on fixed shapes, whose edge kinds read and
+        // write the storage type and apply the zero intervals; no boundary
+        // pass and no compute-type copy (F64ComputeF32Storage 2^20 x 8: two
+        // passes of 24 bytes per element instead of four passes of 112 bytes
+        // per element in all).
+        auto four_step_edges = [&]() {
+            if (!fuse_on || !mixed || rank != 1 || want_layout || d.transform != VKFX_C2C ||
+                d.perform_convolution || p->launches.empty() || p->launches.size() % 2)
+                return false;
+            for (size_t i = 0; i < p->launches.size(); i += 2) {
+                const Launch& A = p->launches[i];
+                const Launch& B = p->launches[i + 1];
+                if (A.boundary || A.copy || A.r2r || A.conv || B.boundary || B.copy || B.r2r || B.conv) return false;
+                if (A.kind != KK_FS_A || B.kind != KK_FS_B || A.chunk != B.chunk || A.a.rtab || B.a.rtab) return false;
+                if (A.in_sel != SEL_IN || A.out_sel != SEL_WORK || B.in_sel != SEL_WORK || B.out_sel != SEL_OUT)
+                    return false;
+                if (!kind_variant(A.fixed, KK_FS_A_EDGE) || !kind_variant(B.fixed, KK_FS_B_EDGE)) return false;
+            }
+            return true;
+        };
+        const bool fs_edges = four_step_edges();
+        if (fs_edges) {
+            const size_t cs = csize(c.prec);
+            const size_t scs = (store_t == 0 ? 2 : store_t == 1 ? 4 : 8) * 2;  // storage bytes per complex element
+            for (size_t i = 0; i < p->launches.size(); i += 2) {
+                Launch& A = p->launches[i];
+                Launch& B = p->launches[i + 1];
+                A.kind = KK_FS_A_EDGE;
+                A.fixed = kind_variant(A.fixed, KK_FS_A_EDGE);
+                A.a.flags |= KF_NARROW_IN | (zp_in ? KF_ZERO_IN : 0);
+                A.in_off = A.in_off / cs * scs;
+                B.kind = KK_FS_B_EDGE;
+                B.fixed = kind_variant(B.fixed, KK_FS_B_EDGE);
+                B.a.flags |= KF_NARROW_OUT | (zp_out ? KF_ZERO_OUT : 0);
+                B.out_off = B.out_off / cs * scs;
+                if (any_zero) {
+                    A.a.zl = B.a.zl = (long long)d.zero_left[0];
+                    A.a.zr = B.a.zr = (long long)d.zero_right[0];
+                }
+            }
+        }
+        const bool fused_edges = !fs_edges && shape_ok && (mixed || any_zero) && rank == 1 && (!want_layout || layout_ok);
         const bool fused_layout = layout_ok && (fused_edges || !(mixed || any_zero));
         bool edge_stage = false;  // passes between the first and the last run on a compute-type copy
         if (fused_edges || fused_layout) {
@@ -2836,7 +2879,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 }
             }
         }
-        const bool fused_all = fused_edges || fused_layout;
+        const bool fused_all = fused_edges || fused_layout || fs_edges;
         const bool need_in = !fused_all && (mixed || (fmt_in && !fused_in) || zp_in);
         const bool need_out = !fused_all && (mixed || (fmt_out && !fused_out) || zp_out);
         const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
@@ -2890,7 +2933,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->stage_out_bytes = (need_out && !p->stage_shared) || edge_stage ? cout : 0;
         c.js << "\"boundary\":{\"input\":" << (need_in ? "true" : "false") << ",\"output\":"
              << (need_out ? "true" : "false") << ",\"fused_batch_stride\":[" << (fused_in ? "true" : "false")
-             << "," << (fused_out ? "true" : "false") << "],\"fused_edges\":" << (fused_edges ? "true" : "false")
+             << "," << (fused_out ? "true" : "false") << "],\"fused_edges\":" << (fused_edges || fs_edges ? "true" : "false")
+             << ",\"four_step_edges\":" << (fs_edges ? "true" : "false")
              << ",\"fused_layout\":" << (fused_layout ? "true" : "false")
              << ",\"zero_padding\":\""
              << (!any_zero ? "none" : d.zero_frequency ? "frequency" : "spatial") << "\",\"grouped_batch\":[";
