@@ -69,24 +69,28 @@ def test_scalar_kernel(hip_ctx, dims, batch, prec):
         # two uploads: forward column pass, row pass with the multiply between
         # its forward and inverse FFTs, inverse column pass
         assert desc["convolution"]["fused"] and labels == FOUR_STEP_LABELS, labels
-    elif len(dims) > 1 and dims[0] > 640 and prec == F32:
-        # N-D over Stockham axes whose axis 0 the plain plan splits (and whose
-        # runtime geometry holds 8 or more columns per block: 1024, 768): the
-        # forward FFT of axes 1.., one kernel per axis-0 line (forward FFT,
-        # multiply, inverse FFT), the inverse of axes 1..: 2D - 1 passes
+    elif len(dims) > 1 and ((dims[0] > 640 and prec == F32) or dims[0] in FIXED_CONV_COLUMNS):
+        # N-D over Stockham axes whose axis 0 has a fixed-shape convolution
+        # column kernel (64, 128, 256, 512), or which the plain plan splits
+        # (and whose runtime geometry holds 8 or more columns per block: 1024,
+        # 768): the forward FFT of axes 1.., one kernel per axis-0 line
+        # (forward FFT, multiply, inverse FFT), the inverse of axes 1..: 2D - 1
+        # passes
         assert desc["convolution"]["fused"] and desc["convolution"]["fused_axis"] == 0, desc["convolution"]
         assert labels.count("convolution_fused_axis0") == 1 and "convolution_multiply" not in labels, labels
         assert len(labels) == 2 * len(dims) - 1, labels
     else:
-        # a Rader axis, an axis 0 of one pass, (f64) too few columns per
-        # block for the fused kernel, or a two-upload length whose rows (384
-        # for 3 * 2^16 = 512 x 384) have no fixed-shape row pass keep the
-        # separate multiply
+        # a Rader axis, an axis 0 of one pass without a fixed-shape column
+        # kernel, (f64) too few columns per block for the fused kernel, or a
+        # two-upload length whose rows (384 for 3 * 2^16 = 512 x 384) have no
+        # fixed-shape row pass keep the separate multiply
         assert not desc["convolution"]["fused"] and "convolution_multiply" in labels
     assert desc["convolution"]["kernels"] == 1 and desc["convolution"]["matrix"] == 0
 
 
 FOUR_STEP_LABELS = ["convolution_columns", "convolution_rows", "convolution_columns_out"]
+# axis-0 lengths with a fixed-shape one-upload convolution column kernel
+FIXED_CONV_COLUMNS = (64, 128, 256, 512)
 
 
 @pytest.mark.parametrize("dims,batch,prec", [([1 << 17], 3, F64), ([100000], 2, F32), ([1000000], 1, F64),
@@ -138,11 +142,29 @@ def test_fused_nd_policies(hip_ctx, dims, prec, conj, cross):
 
 
 @pytest.mark.parametrize("conj,cross,batch", [(True, False, 3), (False, True, 2), (True, True, 5)])
-def test_fused_convolution_policies(hip_ctx, conj, cross, batch):
+@pytest.mark.parametrize("n,prec", [(1536, F32), (1024, F32), (8192, F32), (4096, F64)])
+def test_fused_convolution_policies(hip_ctx, conj, cross, batch, n, prec):
     """Sequence conjugation and cross-power normalization inside the fused
-    one-pass kernel, against the oracle's three-step definition."""
-    conv, _, _ = run_case(hip_ctx, [1536], batch, F32, conj=conj, cross=cross, seed=5)
-    assert vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()["convolution"]["fused"]
+    one-pass kernel (runtime shape for 1536, fixed shapes with the product in
+    the forward FFT's last stage otherwise), against the oracle's three-step
+    definition."""
+    conv, _, _ = run_case(hip_ctx, [n], batch, prec, conj=conj, cross=cross, seed=5)
+    d = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    assert d["convolution"]["fused"] and d["passes"][0]["fixed_shape"] == (n != 1536), d["passes"]
+
+
+@pytest.mark.parametrize("dims,prec", [([256, 20], F32), ([64, 33], F32), ([128, 12, 3], F64), ([512, 9], F64)])
+@pytest.mark.parametrize("conj,cross", [(False, False), (True, True)])
+def test_fused_nd_fixed_columns(hip_ctx, dims, prec, conj, cross):
+    """N-D convolutions whose axis 0 fits one pass with a fixed-shape column
+    kernel: 2D - 1 passes with the fused axis-0 kernel, batch 3, against the
+    oracle."""
+    conv, _, _ = run_case(hip_ctx, dims, 3, prec, conj=conj, cross=cross, seed=13)
+    d = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    labels = [p["kernel"] for p in d["passes"]]
+    assert d["convolution"]["fused_axis"] == 0 and len(labels) == 2 * len(dims) - 1, labels
+    fused = [p for p in d["passes"] if p["kernel"] == "convolution_fused_axis0"]
+    assert len(fused) == 1 and fused[0]["fixed_shape"], fused
 
 
 @pytest.mark.parametrize("dims,prec", [([1024], F32), ([4099], F32), ([32, 40], F64)])

@@ -922,6 +922,29 @@ struct IoConv1 : IoPlain {
     }
 };
 
+// IoConv1 on the fixed shapes: the first stage reads HBM and the last stage
+// writes HBM in the shape's own lane mapping (rows of a 1-D convolution,
+// axis-0 columns of an N-D one), and the spectrum product is applied as the
+// forward FFT's last stage writes its outputs, so the block exchanges no
+// extra LDS pass between the two FFTs.
+struct IoConv1F : IoConv1 {
+    static constexpr int kLoad = LAY_ANY;
+    static constexpr int kStore = LAY_ANY;
+    static constexpr bool kPtrLoad = true, kPtrStore = true;  // plain accesses, scale on store
+    static constexpr bool kMidFused = true;
+    template <typename T>
+    static __device__ __forceinline__ cpx<T> mid_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        if constexpr (kIndexTest) return v;
+        if (a.flags & KF_CONV_CONJ) v = conj(v);
+        cpx<T> y = cmul(v, ((const cpx<T>*)a.spec)[L.c + (long long)e * a.N2]);
+        if (a.flags & KF_CONV_CROSS) {
+            const T r = (T)1 / sqrt(y.re * y.re + y.im * y.im);
+            y = mk(y.re * r, y.im * r);
+        }
+        return y;
+    }
+};
+
 // Row pass of a convolution over a two-upload length N = N1 * N2, between the
 // forward column pass (KK_FS_A, W_N^(n2*k1) on store) and the inverse column
 // pass (KK_FS_A over k1 with no twiddle): FFT of row k1 over n2, multiply by

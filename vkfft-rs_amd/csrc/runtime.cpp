@@ -1814,7 +1814,8 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
         const size_t n = d.dims[0];
         Geometry g0 = geometry(n, c.prec, 1, c.lds_max, c.lds_max);
         if (g0.ok) {
-            Geometry g = geometry(n, c.prec, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+            Geometry g = kernel_geometry(KK_CONV_1, c.prec, -1, n, false, std::max(1, 256 / g0.TT), c.lds_max,
+                                         c.lds_budget);
             KArgs a = blank();
             a.in_es = a.out_es = 1;
             a.in_os = a.out_os = (long long)n;
@@ -1897,26 +1898,29 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
             }
         }
     }
-    // N-D scalar convolution over Stockham axes whose axis 0 the plain N-D
-    // plan splits into two passes per direction: the forward FFT of every
+    // N-D scalar convolution over Stockham axes: the forward FFT of every
     // axis but axis 0 into the workspace, one kernel per axis-0 line (forward
     // FFT, multiply, inverse FFT normalized by 1/N0) into the output, and the
     // normalized inverse of the other axes in place, 2D - 1 passes over the
-    // data instead of 2D + 3 (the multiply folded into the last forward / first
-    // inverse axis, as the reference folds it into its uploads). An axis 0 of
-    // one pass keeps the separate multiply: its fixed-shape column passes
-    // beat the runtime-shape fused kernel ([128, 128, 128] x 4 f32: 192 us
-    // unfused, 201 us fused).
+    // data instead of 2D + 1 (the multiply folded into the last forward /
+    // first inverse axis, as the reference folds it into its uploads), or
+    // 2D - 1 instead of 2D + 3 where the plain plan splits axis 0 into two
+    // passes per direction. Taken with a fixed-shape column kernel for N0, or
+    // where axis 0 would be split (its runtime-shape column kernel then still
+    // wins); an axis 0 of one pass without a fixed-shape kernel keeps the
+    // separate multiply, since its fixed-shape FFT column passes beat the
+    // runtime-shape fused kernel ([128, 128, 128] x 4 f32 before the fixed
+    // column kernel: 192 us unfused, 201 us fused).
     size_t sl1 = 0, sl2 = 0;
-    bool nd_fused = d.rank >= 2 && !ca.matrix && ca.kernel_count <= 1 && coords == 1 && d.dims[0] > 1 &&
-                    split_strided_axis(d.dims[0], c.prec, c.lds_budget, &sl1, &sl2);
+    bool nd_fused = d.rank >= 2 && !ca.matrix && ca.kernel_count <= 1 && coords == 1 && d.dims[0] > 1;
     for (uint32_t i = 0; nd_fused && i < d.rank; ++i) nd_fused = d.axis_algorithm[i] == VKFX_ALG_STOCKHAM;
     if (nd_fused) {
         const size_t n0 = d.dims[0], rest = T / n0;
-        Geometry g = geometry(n0, c.prec, c.prec ? 8 : 16, c.lds_max, c.lds_budget);
+        const bool split = split_strided_axis(n0, c.prec, c.lds_budget, &sl1, &sl2);
+        Geometry g = kernel_geometry(KK_CONV_1, c.prec, -1, n0, true, c.prec ? 8 : 16, c.lds_max, c.lds_budget);
         // strided columns: at least 8 adjacent columns per block, so each
-        // HBM access of the staged copies moves 64 bytes or more
-        if (g.ok && g.G >= 8) {
+        // HBM access moves 64 bytes or more
+        if (g.ok && g.G >= 8 && (g.fixed || split)) {
             c.js << ",\"fused\":true,\"fused_axis\":0},";
             int rc = transform(d.batch, -1, false, SEL_IN, SEL_FULL, 1u);
             if (rc) return rc;
