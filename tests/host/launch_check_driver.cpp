@@ -189,6 +189,33 @@ int main() {
     eb3.flags |= KF_EDGE;
     expect("fs edge rows with KF_EDGE", check_launch(KK_FS_B_EDGE, 0, -1, eb3, 32, e_lds, limit, &fb),
            hipErrorInvalidConfiguration);
+    // the matrix convolution product: whole systems of C1 lines per block on
+    // the runtime-shape kernel
+    KArgs cm = p;
+    static const float mspec = 0;
+    cm.spec = &mspec;
+    cm.C = 1;
+    cm.C1 = 2;
+    cm.flags = KF_CONV_MATRIX;
+    const size_t cm_lds = (size_t)cm.G * cm.LS * 8;
+    expect("conv matrix", check_launch(KK_CONV_1, 0, -1, cm, 32, cm_lds, limit, nullptr), hipSuccess);
+    KArgs cm1 = cm;
+    cm1.C1 = 3;
+    expect("conv matrix, lines per block not whole systems", check_launch(KK_CONV_1, 0, -1, cm1, 32, cm_lds, limit,
+                                                                         nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs cm2 = cm;
+    cm2.C1 = 4;
+    cm2.G = 4;
+    cm2.TT = 8;
+    expect("conv matrix beyond 3 x 3", check_launch(KK_CONV_1, 0, -1, cm2, 32, (size_t)4 * cm.LS * 8, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs cm3 = cm;
+    cm3.flags = KF_CONV_SYM;
+    expect("conv symmetric without the matrix flag", check_launch(KK_CONV_1, 0, -1, cm3, 32, cm_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    expect("conv matrix on a plain pass", check_launch(KK_PLAIN, 0, -1, cm, 32, cm_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
     if (fails) return 1;
     std::printf("ok %d\n", cases);
     return 0;

@@ -167,16 +167,41 @@ def test_fused_nd_fixed_columns(hip_ctx, dims, prec, conj, cross):
     assert len(fused) == 1 and fused[0]["fixed_shape"], fused
 
 
-@pytest.mark.parametrize("dims,prec", [([1024], F32), ([4099], F32), ([32, 40], F64)])
+@pytest.mark.parametrize("dims,prec", [([1024], F32), ([256], F64), ([1536], F32), ([4099], F32), ([32, 40], F64)])
 def test_multi_kernel_fan_out(hip_ctx, dims, prec):
-    run_case(hip_ctx, dims, 1, prec, kernels=3, seed=1)
+    """K kernels over one input: a one-upload 1-D Stockham length runs one
+    fused kernel line per kernel (the input read by every line, spectrum
+    plane k); other lengths keep the separate multiply."""
+    conv, _, _ = run_case(hip_ctx, dims, 1, prec, kernels=3, seed=1)
+    d = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    fused = len(dims) == 1 and dims[0] != 4099
+    assert d["convolution"]["fused"] == fused, d["convolution"]
+    if fused:
+        assert [p["kernel"] for p in d["passes"]] == ["convolution_fused"]
 
 
 @pytest.mark.parametrize("matrix,symmetric,batch,kernels,prec",
                          [(2, False, 3, 1, F32), (3, False, 2, 1, F64), (2, True, 4, 1, F64), (3, False, 1, 2, F32),
                           (2, True, 1, 3, F32)])
-def test_matrix_1d(hip_ctx, matrix, symmetric, batch, kernels, prec):
-    run_case(hip_ctx, [512], batch, prec, matrix, symmetric, kernels, seed=2)
+@pytest.mark.parametrize("n", [512, 2048])
+def test_matrix_1d(hip_ctx, matrix, symmetric, batch, kernels, prec, n):
+    """Matrix convolutions of one-upload 1-D lengths: one fused kernel whose
+    blocks hold whole systems of coordinate lines and mix them between the
+    forward and inverse FFTs."""
+    conv, _, _ = run_case(hip_ctx, [n], batch, prec, matrix, symmetric, kernels, seed=2)
+    d = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    assert d["convolution"]["fused"] and [p["kernel"] for p in d["passes"]] == ["convolution_fused"], d["passes"]
+    assert d["passes"][0]["lines_per_block"] % matrix == 0, d["passes"][0]
+
+
+@pytest.mark.parametrize("matrix,symmetric,kernels", [(2, False, 1), (3, False, 2), (2, True, 1)])
+@pytest.mark.parametrize("conj,cross", [(True, False), (False, True)])
+def test_matrix_1d_policies(hip_ctx, matrix, symmetric, kernels, conj, cross):
+    """Sequence conjugation and cross-power normalization of the mixed
+    product (the normalization applies to the row sum), against the oracle."""
+    batch = 2 if kernels == 1 else 1
+    conv, _, _ = run_case(hip_ctx, [1024], batch, F32, matrix, symmetric, kernels, conj, cross, seed=4)
+    assert vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()["convolution"]["fused"]
 
 
 def test_matrix_nd_batch1(hip_ctx):

@@ -902,12 +902,27 @@ struct IoConv1 : IoPlain {
     static constexpr bool kTwoPass = true;
     static constexpr int kLoad = LAY_STAGED;
     static constexpr int kStore = LAY_STAGED;
+    // 1-D lines of a fan-out over kernels and coordinates (C = 1, line =
+    // o * C1 + o1, spec_os or spec_os1 set): c holds the offset of the line's
+    // spectrum plane, o * spec_os + o1 * spec_os1 (N2 = 1)
+    static __device__ LineInfo line(const KArgs& a, long long blk, int g) {
+        LineInfo L = line_default(a, blk, g);
+        if (a.C == 1 && (a.spec_os || a.spec_os1)) {
+            const long long o1 = (L.valid ? blk * a.G + g : 0) - L.o * a.C1;
+            L.c = L.o * a.spec_os + o1 * a.spec_os1;
+        }
+        return L;
+    }
     // element e of line (o, c) multiplies the spectrum at c + e * N2: a 1-D
-    // line (C = 1, N2 = 1) the spectrum itself, an axis-0 line of an N-D
+    // line (C = 1, N2 = 1) its spectrum plane, an axis-0 line of an N-D
     // tensor (column c of C = N2 = the product of the other axes) its column
     template <typename T, class D>
     static __device__ void mid(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
         const cpx<T>* spec = (const cpx<T>*)a.spec;
+        if (a.flags & KF_CONV_MATRIX) {
+            mid_matrix<T, D>(a, lds, li);
+            return;
+        }
         coop_for(D::G(a), D::N(a), true, [&](int g, int e) {
             cpx<T>& v = lds[g * D::LS(a) + lpad(e, D::PS(a))];
             cpx<T> x = v;
@@ -919,6 +934,40 @@ struct IoConv1 : IoPlain {
             }
             v = y;
         });
+    }
+    // Matrix convolution (ConvolutionMatrixLayout, convolution_ir.rs:128-147):
+    // for the M = C1 coordinate lines g0 .. g0 + M - 1 of a system and each
+    // bin e, y_o = sum_i prep(x_i) K[plane(o, i)][e], plane o*M + i, or the
+    // upper-triangle index of (min, max) with KF_CONV_SYM; the system's
+    // planes start at li[g0].c (its kernel's when there are several).
+    template <typename T, class D>
+    static __device__ void mid_matrix(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        const cpx<T>* spec = (const cpx<T>*)a.spec;
+        const int M = (int)a.C1, n = D::N(a), S = D::G(a) / M;
+        const bool sym = (a.flags & KF_CONV_SYM) != 0;
+        for (int idx = (int)threadIdx.x; idx < S * n; idx += (int)blockDim.x) {
+            const int sb = idx / n, e = idx - sb * n, g0 = sb * M;
+            if (!li[g0].valid) continue;
+            cpx<T> x[kMaxConvMatrix], y[kMaxConvMatrix];
+            for (int i = 0; i < M; ++i) {
+                x[i] = lds[(g0 + i) * D::LS(a) + lpad(e, D::PS(a))];
+                if (a.flags & KF_CONV_CONJ) x[i] = conj(x[i]);
+            }
+            for (int o = 0; o < M; ++o) {
+                cpx<T> acc = zero<T>();
+                for (int i = 0; i < M; ++i) {
+                    const int lo = i < o ? i : o, hi = i < o ? o : i;
+                    const int plane = sym ? lo * M - lo * lo + hi : o * M + i;
+                    acc = acc + cmul(x[i], spec[li[g0].c + (long long)plane * n + e]);
+                }
+                if (a.flags & KF_CONV_CROSS) {
+                    const T r = (T)1 / sqrt(acc.re * acc.re + acc.im * acc.im);
+                    acc = mk(acc.re * r, acc.im * r);
+                }
+                y[o] = acc;
+            }
+            for (int o = 0; o < M; ++o) lds[(g0 + o) * D::LS(a) + lpad(e, D::PS(a))] = y[o];
+        }
     }
 };
 

@@ -9,6 +9,7 @@ namespace vkfx {
 
 constexpr int kMaxStages = 24;
 constexpr int kMaxLinesPerBlock = 64;
+constexpr int kMaxConvMatrix = 3;  // coordinates of a matrix convolution (2 x 2, 3 x 3)
 // Bytes of the static device scratch behind vkfx_execute_noalloc (one copy
 // per GPU), and the device ordinals it tracks.
 constexpr size_t kStaticScratchBytes = size_t(64) << 20;
@@ -65,6 +66,11 @@ enum KFlags : int {
     // the radix list has Rader stages (KArgs::rtab): the staged runtime-shape
     // instantiation that carries them (the others leave their registers out)
     KF_RADER = 32768,
+    // KK_CONV_1 on the runtime-shape kernel: a block holds whole systems of
+    // C1 coordinate lines (G a multiple of C1) and the product mixes them
+    // through the M x M kernel matrix (symmetric planes with KF_CONV_SYM)
+    KF_CONV_MATRIX = 65536,
+    KF_CONV_SYM = 131072,
 };
 
 // Butterflies per thread in one radix-R stage of the runtime-shape kernel
@@ -121,6 +127,9 @@ struct KArgs {
     const void* rtab;
     int roff[kMaxStages];
     long long zl, zr;                  // KF_ZERO_IN / KF_ZERO_OUT element interval of a line
+    // KK_CONV_1 over 1-D lines (C = 1, line = o * C1 + o1): the line's
+    // kernel-spectrum plane starts at o * spec_os + o1 * spec_os1
+    long long spec_os, spec_os1;
 };
 
 // Radices up to this are Stockham butterflies; a larger (prime) radix in a

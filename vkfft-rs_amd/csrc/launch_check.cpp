@@ -18,6 +18,12 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
         lds_bytes > lds_limit)
         return hipErrorInvalidConfiguration;
     if (kind == KK_CONV_1 && !a.spec) return hipErrorInvalidConfiguration;
+    // the matrix product mixes whole systems of C1 coordinate lines in a
+    // block of the runtime-shape kernel
+    if ((a.flags & (KF_CONV_MATRIX | KF_CONV_SYM)) &&
+        (kind != KK_CONV_1 || fixed || !(a.flags & KF_CONV_MATRIX) || a.C != 1 || a.C1 < 2 ||
+         a.C1 > kMaxConvMatrix || a.G % a.C1 != 0))
+        return hipErrorInvalidConfiguration;
     // the four-step convolution row pass: rows k1 < N1 of N2 = N elements,
     // the N1 x N2 spectrum and the W_M table
     if (kind == KK_CONV_B && (!a.spec || !a.tlo || !a.thi || a.N2 != a.N || a.N1 < 1 || a.C != a.N1 ||

@@ -1810,24 +1810,46 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
     // the multiply and the normalized inverse FFT in one kernel, one HBM pass
     // (the reference fuses the multiply into its last forward / first inverse
     // upload, convolution_ir.rs:4252-4440)
-    if (d.rank == 1 && !ca.matrix && ca.kernel_count <= 1 && coords == 1 && d.axis_algorithm[0] == VKFX_ALG_STOCKHAM) {
+    // The fan-out over kernels and coordinates without coordinate mixing
+    // rides on the same kernel: output line (s, o) of system s (kernel s when
+    // there are several kernels, whose input is system 0) reads input line
+    // (s_in, o) and multiplies by plane kid * planes + (independent ? o : 0)
+    // (conv.hip states the rule), one HBM read and write per output line.
+    // A matrix convolution runs the runtime-shape kernel with whole systems
+    // of M coordinate lines per block, whose product mixes the coordinates.
+    if (d.rank == 1 && d.axis_algorithm[0] == VKFX_ALG_STOCKHAM) {
         const size_t n = d.dims[0];
         Geometry g0 = geometry(n, c.prec, 1, c.lds_max, c.lds_max);
-        if (g0.ok) {
-            Geometry g = kernel_geometry(KK_CONV_1, c.prec, -1, n, false, std::max(1, 256 / g0.TT), c.lds_max,
-                                         c.lds_budget);
+        const int Mx = ca.matrix;
+        Geometry g;
+        if (g0.ok && Mx) {
+            const int want = std::max(1, 256 / g0.TT) / Mx * Mx;
+            g = geometry(n, c.prec, std::max(want, Mx), c.lds_max, c.lds_budget);
+            if (g.ok && g.G % Mx) g = geometry(n, c.prec, Mx, c.lds_max, c.lds_max);
+            if (g.G % Mx) g.ok = false;
+        } else if (g0.ok) {
+            g = kernel_geometry(KK_CONV_1, c.prec, -1, n, false, std::max(1, 256 / g0.TT), c.lds_max, c.lds_budget);
+        }
+        if (g0.ok && g.ok) {
+            const bool fan = ca.kernel_count > 1;
+            const long long M = (long long)coords, ln = (long long)n;
             KArgs a = blank();
             a.in_es = a.out_es = 1;
-            a.in_os = a.out_os = (long long)n;
+            a.C1 = M;
+            a.in_os = fan ? 0 : M * ln, a.in_os1 = ln;
+            a.out_os = M * ln, a.out_os1 = ln;
+            a.spec_os = fan ? (long long)ca.planes * ln : 0;
+            a.spec_os1 = ca.independent ? ln : 0;
             a.flags = KF_IN_ROWMAJOR | KF_OUT_ROWMAJOR | (ca.conj_seq ? KF_CONV_CONJ : 0) |
-                      (ca.cross_norm ? KF_CONV_CROSS : 0);
+                      (ca.cross_norm ? KF_CONV_CROSS : 0) | (Mx ? KF_CONV_MATRIX : 0) |
+                      (Mx && ca.symmetric ? KF_CONV_SYM : 0);
             a.scale = 1.0 / (double)n;
             a.spec = kernel;
             a.N2 = 1;
             p->full_bytes = 0;
             p->serial = false;
             c.js << ",\"fused\":true},";
-            const long long lines = (long long)(d.batch * coords);
+            const long long lines = (long long)(out_systems * coords);
             return add_launch(c, KK_CONV_1, -1, g, a, lines, blocks_for(lines, g.G), SEL_IN, 0, SEL_OUT, 0,
                               "convolution_fused");
         }
