@@ -110,23 +110,37 @@ int main() {
     cb.spec = &spec;
     cb.tlo = cb.thi = &tw;
     const size_t cb_lds = (size_t)cb.G * cb.LS * 8;
-    expect("conv rows", check_launch(KK_CONV_B, 0, -1, cb, 32, cb_lds, limit, nullptr), hipSuccess);
+    FixedKernel fc;
+    std::memset(&fc, 0, sizeof fc);
+    fc.kind = KK_CONV_B;
+    fc.dir = -1;
+    fc.N = cb.N;
+    fc.TT = cb.TT;
+    fc.G = cb.G;
+    fc.PS = cb.PS;
+    fc.LS = cb.LS;
+    fc.nst = cb.nstages;
+    for (int i = 0; i < cb.nstages; ++i) fc.radix[i] = cb.radix[i];
+    fc.lds_mult = 1;
+    expect("conv rows", check_launch(KK_CONV_B, 0, -1, cb, 32, cb_lds, limit, &fc), hipSuccess);
+    expect("conv rows on the runtime kernel", check_launch(KK_CONV_B, 0, -1, cb, 32, cb_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
     KArgs cb1 = cb;
     cb1.spec = nullptr;
-    expect("conv rows without the spectrum", check_launch(KK_CONV_B, 0, -1, cb1, 32, cb_lds, limit, nullptr),
+    expect("conv rows without the spectrum", check_launch(KK_CONV_B, 0, -1, cb1, 32, cb_lds, limit, &fc),
            hipErrorInvalidConfiguration);
     KArgs cb2 = cb;
     cb2.tlo = nullptr;
-    expect("conv rows without the twiddle table", check_launch(KK_CONV_B, 0, -1, cb2, 32, cb_lds, limit, nullptr),
+    expect("conv rows without the twiddle table", check_launch(KK_CONV_B, 0, -1, cb2, 32, cb_lds, limit, &fc),
            hipErrorInvalidConfiguration);
     KArgs cb3 = cb;
     cb3.N2 = cb.N / 2;
     cb3.M = cb3.N1 * cb3.N2;
-    expect("conv rows, N2 != row length", check_launch(KK_CONV_B, 0, -1, cb3, 32, cb_lds, limit, nullptr),
+    expect("conv rows, N2 != row length", check_launch(KK_CONV_B, 0, -1, cb3, 32, cb_lds, limit, &fc),
            hipErrorInvalidConfiguration);
     KArgs cb4 = cb;
     cb4.C = cb.N1 + 1;
-    expect("conv rows, C != N1", check_launch(KK_CONV_B, 0, -1, cb4, 32, cb_lds, limit, nullptr),
+    expect("conv rows, C != N1", check_launch(KK_CONV_B, 0, -1, cb4, 32, cb_lds, limit, &fc),
            hipErrorInvalidConfiguration);
     // the mixed-storage four-step passes: fixed shapes only, the column pass
     // with the narrow input, the row pass with the narrow output

@@ -1737,7 +1737,6 @@ KernelFn pick_dyn(KernelKind kind) {
         case KK_RADER_FFT: return k_dyn<T, S, IoRader, W>;
         case KK_RADER_DIRECT: return k_rader_direct<T>;
         case KK_CONV_1: return k_dyn<T, S, IoConv1, W>;
-        case KK_CONV_B: return k_dyn<T, S, IoConvB, W>;
         default: return nullptr;
     }
 }

@@ -35,7 +35,7 @@ enum KernelKind : int {
     KK_RADER_FFT,      // prime length p: gather, FFT(p-1), kernel multiply, IFFT, scatter
     KK_RADER_DIRECT,   // prime length p: gather, O(p^2) cyclic convolution, scatter
     KK_CONV_1,         // convolution in one kernel: FFT, kernel-spectrum multiply, normalized IFFT
-    KK_CONV_B,         // four-step convolution row pass: FFT, natural-order spectrum multiply, IFFT, W_M^-1
+    KK_CONV_B,         // four-step convolution row pass: FFT, natural-order spectrum multiply, IFFT, W_M^-1 (fixed shapes only)
     KK_FS_A_EDGE,      // KK_FS_A reading half-precision storage, input zero interval (fixed shapes only)
     KK_FS_B_EDGE,      // KK_FS_B writing half-precision storage, output zero interval (fixed shapes only)
     KK_COUNT

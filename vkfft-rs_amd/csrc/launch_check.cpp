@@ -26,7 +26,7 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
         return hipErrorInvalidConfiguration;
     // the four-step convolution row pass: rows k1 < N1 of N2 = N elements,
     // the N1 x N2 spectrum and the W_M table
-    if (kind == KK_CONV_B && (!a.spec || !a.tlo || !a.thi || a.N2 != a.N || a.N1 < 1 || a.C != a.N1 ||
+    if (kind == KK_CONV_B && (!fixed || !a.spec || !a.tlo || !a.thi || a.N2 != a.N || a.N1 < 1 || a.C != a.N1 ||
                               a.M != a.N1 * a.N2))
         return hipErrorInvalidConfiguration;
     if (kind == KK_RADER_DIRECT && (a.TT != a.N || a.LS < a.N + 1 || a.N < 1 || !a.pin || !a.pout))
