@@ -1202,9 +1202,11 @@ def desc_from_ir(ir) -> _PlanDesc:
 
 
 class NativeRuntime:
-    """The IR-driven boundary (the Rust HipNativeRuntime of INTEGRATION.md):
-    execute_transform_f32/f64 and submit take only the IR, plan it on first use
-    from desc_from_ir and keep the plan keyed by the IR."""
+    """The IR-driven boundary, the Python side of a Rust HipNativeRuntime
+    over the C ABI (NativeRuntime::execute_transform_f32/f64 and the async
+    submit, src/backend/native_runtime.rs:339-359, 406-451): they take only
+    the IR, plan it on first use from desc_from_ir and keep the plan keyed by
+    the IR."""
 
     def __init__(self, ctx: "HipExecutionContext"):
         self.ctx = ctx
