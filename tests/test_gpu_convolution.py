@@ -107,6 +107,17 @@ def test_fused_four_step(hip_ctx, dims, batch, prec):
     assert desc["convolution"]["n1"] * desc["convolution"]["n2"] == dims[0]
 
 
+@pytest.mark.parametrize("matrix,symmetric,batch,kernels", [(0, False, 1, 3), (2, False, 2, 1), (2, True, 1, 2),
+                                                             (3, False, 1, 1)])
+def test_two_upload_fan_out_and_matrix(hip_ctx, matrix, symmetric, batch, kernels):
+    """Multi-kernel and matrix convolutions over a two-upload length keep
+    the separate multiply (the three-pass plan is scalar only), against the
+    oracle."""
+    conv, _, _ = run_case(hip_ctx, [1 << 16], batch, F32, matrix, symmetric, kernels, seed=24)
+    d = vk.Plan(hip_ctx, conv.ir, desc=conv.desc()).describe()
+    assert not d["convolution"]["fused"] and "convolution_multiply" in [p["kernel"] for p in d["passes"]]
+
+
 @pytest.mark.parametrize("conj,cross", [(True, False), (False, True), (True, True)])
 def test_fused_four_step_policies(hip_ctx, conj, cross):
     """Sequence conjugation and cross-power normalization in the four-step

@@ -1853,13 +1853,15 @@ int plan_convolution(Ctx& c, const vkfx_plan_desc& d, size_t coords, size_t out_
             return add_launch(c, KK_CONV_1, -1, g, a, lines, blocks_for(lines, g.G), SEL_IN, 0, SEL_OUT, 0,
                               "convolution_fused");
         }
-        // two uploads (N = N1 * N2): the forward column pass (FFT over n1,
+        // two uploads (N = N1 * N2), scalar convolutions only (one
+        // coordinate, one kernel): the forward column pass (FFT over n1,
         // W_N^(n2*k1)) into the workspace, one row pass (FFT over n2, multiply,
         // inverse FFT, W_N^(-k1*m2)) in place, and the inverse column pass
         // into the output, whose twiddle row c / N2 is 0 (no twiddle): three
         // HBM passes per chunk instead of five
         size_t n1 = 0, n2 = 0;
-        if (!g0.ok && four_step_split(n, c.prec, c.lds_max, &n1, &n2)) {
+        const bool scalar = !Mx && ca.kernel_count <= 1 && coords == 1;
+        if (!g0.ok && scalar && four_step_split(n, c.prec, c.lds_max, &n1, &n2)) {
             const int prec = c.prec;
             Geometry ga = kernel_geometry(KK_FS_A, prec, -1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
             Geometry gc = kernel_geometry(KK_FS_A, prec, 1, n1, true, prec ? 8 : 16, c.lds_max, c.lds_budget);
