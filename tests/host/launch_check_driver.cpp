@@ -203,6 +203,35 @@ int main() {
     eb3.flags |= KF_EDGE;
     expect("fs edge rows with KF_EDGE", check_launch(KK_FS_B_EDGE, 0, -1, eb3, 32, e_lds, limit, &fb),
            hipErrorInvalidConfiguration);
+    // the one-upload Bluestein kernel with its boundary work: fixed shapes
+    // with chirp and spectrum, zero intervals within the line's N elements
+    FixedKernel fbl = fe;
+    fbl.kind = KK_BLUE_1_EDGE;
+    fbl.col = false;
+    static const float btab = 0;
+    KArgs bl = p;
+    bl.chirp = bl.spec = &btab;
+    bl.nvalid = bl.nout = 100;
+    bl.flags = KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN;
+    bl.zl = 3, bl.zr = 100;
+    expect("bluestein edges", check_launch(KK_BLUE_1_EDGE, 0, -1, bl, 32, e_lds, limit, &fbl), hipSuccess);
+    expect("bluestein edges on the runtime kernel", check_launch(KK_BLUE_1_EDGE, 0, -1, bl, 32, e_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    KArgs bl1 = bl;
+    bl1.zr = 101;
+    expect("bluestein edges, zero interval past the line",
+           check_launch(KK_BLUE_1_EDGE, 0, -1, bl1, 32, e_lds, limit, &fbl), hipErrorInvalidConfiguration);
+    KArgs bl2 = bl;
+    bl2.chirp = nullptr;
+    expect("bluestein edges without a chirp", check_launch(KK_BLUE_1_EDGE, 0, -1, bl2, 32, e_lds, limit, &fbl),
+           hipErrorInvalidConfiguration);
+    KArgs bl3 = bl;
+    bl3.flags |= KF_EDGE;
+    expect("bluestein edges with KF_EDGE", check_launch(KK_BLUE_1_EDGE, 0, -1, bl3, 32, e_lds, limit, &fbl),
+           hipErrorInvalidConfiguration);
+    KArgs bl4 = bl;
+    expect("narrow input on the plain Bluestein kernel", check_launch(KK_BLUE_1, 0, -1, bl4, 32, e_lds, limit, nullptr),
+           hipErrorInvalidValue);
     // the matrix convolution product: whole systems of C1 lines per block on
     // the runtime-shape kernel
     KArgs cm = p;

@@ -290,3 +290,83 @@ def test_formatted_layout_fused_gaps_untouched(hip_ctx, dims, prec):
     assert gaps.any() and np.isnan(y[gaps].real).all() and np.isnan(y[gaps].imag).all()
     xin = f16(x) if prec == F16S else x
     assert o.rel_l2(y[idx], ref_c2c(xin, dims, batch, FWD)) <= (1e-3 if prec == F16S else 1e-5)
+
+
+# prime lengths whose one-upload Bluestein convolution length M has a fixed
+# shape with an edge variant (f32 compute: M = 8232, 4096, 1024, 16384, 256;
+# f64 compute: M = 3430, 2048, 8192, 512), batches spanning several blocks
+def ref_np(x, n, batch, direction, normalize=False):
+    """pocketfft's float64 1-D transform (the f64 gate of the Bluestein
+    tests: the oracle's own f64 Bluestein sits near 1e-12)."""
+    v = x.astype(np.complex128).reshape(batch, n)
+    y = np.fft.fft(v, axis=1) if direction == FWD else np.fft.ifft(v, axis=1) * (1 if normalize else n)
+    return y.reshape(-1)
+
+
+BLUE_EDGE = [(4099, F16S, 5), (1583, F16S, 3), (409, F16S, 9), (6133, F16S, 2), (103, F16S, 35),
+             (1583, F64C, 3), (1019, F64C, 4), (3461, F64C, 2), (137, F64C, 17)]
+
+
+@pytest.mark.parametrize("n,prec,batch", BLUE_EDGE)
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_mixed_storage_bluestein(hip_ctx, monkeypatch, n, prec, batch, direction):
+    """Mixed-storage 1-D Bluestein transforms in one kernel: the edge variant
+    of the fixed shape reads the storage type before the chirp weighting and
+    writes it after the chirp and scale (no boundary pass), against the
+    oracle and against the boundary-pass plan."""
+    x = o.complex_uniform(n * batch, n % 997 + batch, np.complex64)
+    tol = {F16S: 1e-3, F64C: 1e-7}[prec]
+    c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_inverse_normalization(True)
+    y, desc, yb = run_both(monkeypatch, c, direction, x)
+    assert desc["boundary"]["bluestein_edges"]
+    assert [p["kernel"] for p in desc["passes"]] == ["bluestein_single"], desc["passes"]
+    xin = f16(x) if prec == F16S else x
+    ref = ref_np(xin, n, batch, direction, normalize=True)
+    assert o.rel_l2(y, ref) <= tol
+    assert o.rel_l2(yb, ref) <= tol
+    if prec == F16S:
+        assert np.array_equal(y, f16(y))
+
+
+def test_mixed_storage_bluestein_without_edge_shape(hip_ctx):
+    """A Bluestein length whose convolution length has no fixed shape in the
+    compute precision (4099 in f64: M = 8232) keeps its boundary passes."""
+    n, batch = 4099, 2
+    x = o.complex_uniform(n * batch, 11, np.complex64)
+    c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(F64C)
+    ir = vk.TransformIr.build(c, FWD)
+    y = hip_ctx.execute_transform(ir, x)
+    desc = hip_ctx.plan(ir).describe()
+    assert not desc["boundary"]["bluestein_edges"]
+    kernels = [p["kernel"] for p in desc["passes"]]
+    assert "boundary_in" in kernels and "boundary_out" in kernels, kernels
+    assert o.rel_l2(y, ref_np(x, n, batch, FWD)) <= 1e-7
+
+
+@pytest.mark.parametrize("direction,domain", [(FWD, SPATIAL), (INV, SPATIAL), (FWD, FREQ), (INV, FREQ)])
+@pytest.mark.parametrize("prec", [F32, F64, F16S, F64C])
+def test_bluestein_zero_padding_fused(hip_ctx, monkeypatch, direction, domain, prec):
+    """The 1-D zero interval inside the one-upload Bluestein kernel, on the
+    plain and the mixed precisions: input elements [l, r) read as zero before
+    the chirp weighting, output elements [l, r) written as zero."""
+    n, batch, left, right = 1583, 3, 100, 1200
+    cdt = np.complex128 if prec == F64 else np.complex64
+    x = o.complex_uniform(n * batch, 29, cdt)
+    mask = np.zeros((batch, n), dtype=bool)
+    mask[:, left:right] = True
+    mask = mask.reshape(-1)
+    input_side = (direction == FWD) == (domain == SPATIAL)
+    c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec) \
+        .with_zero_padding(0, left, right).with_zero_padding_domain(domain)
+    y, desc, yb = run_both(monkeypatch, c, direction, x)
+    assert desc["boundary"]["bluestein_edges"]
+    assert [p["kernel"] for p in desc["passes"]] == ["bluestein_single"], desc["passes"]
+    xin = f16(x) if prec == F16S else x
+    xin = np.where(mask, 0, xin) if input_side else xin
+    expect = ref_np(xin, n, batch, direction)
+    if not input_side:
+        expect = np.where(mask, 0, expect)
+        assert (y[mask] == 0).all() and (yb[mask] == 0).all()
+    tol = {F32: 2e-5, F64: 2e-13, F16S: 1e-3, F64C: 1e-7}[prec]
+    assert o.rel_l2(y, expect) <= tol
+    assert o.rel_l2(yb, expect) <= tol

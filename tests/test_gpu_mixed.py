@@ -67,8 +67,9 @@ def test_f64_compute_f32_storage(hip_ctx, dims, batch, fused):
     desc = hip_ctx.plan(ir).describe()
     # a 1-D one-upload Stockham pass, and the two passes of a two-upload
     # length with fixed edge shapes (2^20 = 1024 x 1024), convert in their
-    # own loads and stores; N-D, other four-step (3 * 2^16 = 512 x 384),
-    # Bluestein and Rader plans keep boundary passes
+    # own loads and stores; N-D, other four-step (3 * 2^16 = 512 x 384) and
+    # Rader plans keep boundary passes, and so do Bluestein plans whose
+    # convolution length has no fixed shape in f64 (4099: M = 8232)
     assert desc["boundary"]["fused_edges"] == fused
     boundary = desc["passes"][0]["kernel"] == "boundary_in" and desc["passes"][-1]["kernel"] == "boundary_out"
     assert boundary != fused

@@ -891,6 +891,49 @@ struct IoBlue1 : IoPlain {
     }
 };
 
+// The one-upload Bluestein kernel with the 1-D boundary work inside: the
+// caller's input read in the storage type of half the compute precision
+// (KF_NARROW_IN) with the input zero interval [zl, zr) read as zero
+// (KF_ZERO_IN) before the chirp weighting, and the output scaled, written in
+// the storage type (KF_NARROW_OUT, rounded to nearest) with the output zero
+// interval written as zero (KF_ZERO_OUT).
+struct IoBlue1Edge : IoBlue1 {
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        if (e >= a.nvalid) return zero<T>();
+        if ((a.flags & KF_ZERO_IN) && e >= a.zl && e < a.zr) return zero<T>();
+        cpx<T> x;
+        if (a.flags & KF_NARROW_IN) {
+            using U = typename Narrow<T>::type;
+            const cpx<U> v = ldg_in<NTIO>(a, (const cpx<U>*)a.in + L.ib + e * a.in_es);
+            x = mk((T)v.re, (T)v.im);
+        } else {
+            x = ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es);
+        }
+        return cmul(x, ((const cpx<T>*)a.chirp)[e]);
+    }
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        if (e >= a.nout) return;
+        v = scale(cmul(v, ((const cpx<T>*)a.chirp)[e]), (T)a.scale);
+        if ((a.flags & KF_ZERO_OUT) && e >= a.zl && e < a.zr) v = zero<T>();
+        if (a.flags & KF_NARROW_OUT) {
+            using U = typename Narrow<T>::type;
+            stg_out<NTIO>(a, (cpx<U>*)a.out + L.ob + e * a.out_es, mk((U)v.re, (U)v.im));
+        } else {
+            stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, v);
+        }
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoBlue1Edge, D>(a, lds, li, a.flags & KF_IN_ROWMAJOR);
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoBlue1Edge, D, T, S>(a, lds, li, a.flags & KF_OUT_ROWMAJOR);
+    }
+};
+
 // Convolution of one tensor line in one kernel (performConvolution,
 // convolution_ir.rs:4252-4440, with the multiply that the reference fuses
 // into its last forward / first inverse upload): staged load, forward FFT,

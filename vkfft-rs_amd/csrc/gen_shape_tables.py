@@ -607,6 +607,17 @@ HEADS_BLUE = ("// Fixed shapes of the one-kernel Bluestein transform, {p}, for t
               "// slot per 16 (f32) / 8 (f64) elements.\n")
 HEADS['kf_blue_rows_f32'] = HEADS_BLUE.format(p='f32')
 HEADS['kf_blue_rows_f64'] = HEADS_BLUE.format(p='f64')
+# the same shapes with the 1-D boundary work inside (storage conversion and
+# zero intervals), found by kind_variant from the plain entry
+TABLES['kf_blue_edge_f32'] = [('BLUE_1_EDGE', 'Blue1Edge') + r[2:] for r in blue_rows(0)]
+TABLES['kf_blue_edge_f64'] = [('BLUE_1_EDGE', 'Blue1Edge') + r[2:] for r in blue_rows(1)]
+HEADS_BLUE_EDGE = ("// Fixed shapes of the one-kernel Bluestein transform with the 1-D boundary\n"
+                   "// work inside, {p}: the caller's input and output in the storage type of\n"
+                   "// half the compute precision and the zero intervals of zero padding\n"
+                   "// (IoBlue1Edge), one entry for each shape of kf_blue_rows_{p} with the same\n"
+                   "// threads, lines per block, radices and LDS strides.\n")
+HEADS['kf_blue_edge_f32'] = HEADS_BLUE_EDGE.format(p='f32')
+HEADS['kf_blue_edge_f64'] = HEADS_BLUE_EDGE.format(p='f64')
 # fourstep_rows(0 / 1, registered_keys(0 / 1)) before these tables existed
 TABLES['kf_round_fs_f32'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 4, 137), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 4, 255), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 4, 265), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 4, 273), ('FS_A', 'FsA', 400, 25, 32, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 4, 425), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 4, 531), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 4, 545), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 4, 1063), ('FS_A', 'FsA', 1024, 64, 16, True, [16, 8, 8], 30, 1025), ('FS_A', 'FsA', 2000, 125, 8, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 8, False, [16, 5, 5, 5], 4, 2125), ('FS_A', 'FsA', 2048, 128, 8, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 8, False, [16, 16, 8], 4, 2177)]
 TABLES['kf_round_fs_f64'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 3, 145), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 3, 271), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 3, 281), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 3, 289), ('FS_A', 'FsA', 400, 25, 16, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 3, 451), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 3, 563), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 3, 577), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 3, 1125), ('FS_A', 'FsA', 1024, 64, 8, True, [16, 8, 8], 30, 1025), ('FS_B', 'FsB', 1024, 64, 8, False, [16, 8, 8], 3, 1153), ('FS_A', 'FsA', 2000, 125, 4, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 4, False, [16, 5, 5, 5], 3, 2251), ('FS_A', 'FsA', 2048, 128, 4, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 4, False, [16, 16, 8], 3, 2305)]
@@ -627,6 +638,7 @@ HEADS['kf_round_f32'] = HEADS_ROUND.format(p='f32')
 HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 
 FUNCS = {'kf_blue_rows_f32': 'fixed_table_blue_rows_f32', 'kf_blue_rows_f64': 'fixed_table_blue_rows_f64',
+         'kf_blue_edge_f32': 'fixed_table_blue_edge_f32', 'kf_blue_edge_f64': 'fixed_table_blue_edge_f64',
          'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
          'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
          'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
@@ -635,7 +647,7 @@ FUNCS = {'kf_blue_rows_f32': 'fixed_table_blue_rows_f32', 'kf_blue_rows_f64': 'f
 
 def roles(kind, col):
     """(direction, nontemporal input, nontemporal output) registered."""
-    if kind == "BLUE_1":
+    if kind in ("BLUE_1", "BLUE_1_EDGE"):
         return [(-1, True, True)]
     if kind in ("FS_A", "FS_B"):
         return [(-1, False, False), (1, False, False)]
@@ -696,7 +708,7 @@ def check():
 
 if __name__ == "__main__":
     if len(sys.argv) > 1 and sys.argv[1] == "emit":
-        for n in TABLES:
+        for n in (sys.argv[2:] or TABLES):
             emit(n)
     elif len(sys.argv) > 1 and sys.argv[1] == "check":
         check()

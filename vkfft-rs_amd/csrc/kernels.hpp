@@ -38,6 +38,7 @@ enum KernelKind : int {
     KK_CONV_B,         // four-step convolution row pass: FFT, natural-order spectrum multiply, IFFT, W_M^-1 (fixed shapes only)
     KK_FS_A_EDGE,      // KK_FS_A reading half-precision storage, input zero interval (fixed shapes only)
     KK_FS_B_EDGE,      // KK_FS_B writing half-precision storage, output zero interval (fixed shapes only)
+    KK_BLUE_1_EDGE,    // KK_BLUE_1 reading / writing half-precision storage, zero intervals (fixed shapes only)
     KK_COUNT
 };
 

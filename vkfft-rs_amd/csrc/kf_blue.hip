@@ -14,6 +14,9 @@ static const FixedKernel kTable[] = {
     VKFX_FIXED_TS(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 3, 9261, false, 6, true, true, 8, 3, 7, 7, 7),
     VKFX_FIXED_PPTS(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 3, 9261, false, true, true, 8, 3, 7, 7, 7),
     VKFX_FIXED_NT(KK_BLUE_1, IoBlue1, float, 0, -1, 8232, 686, 1, 5, 8489, false, true, true, 8, 3, 7, 7, 7),
+    // the first M = 8232 shape with the 1-D boundary work inside (storage
+    // conversion and zero intervals)
+    VKFX_FIXED_TS(KK_BLUE_1_EDGE, IoBlue1Edge, float, 0, -1, 8232, 686, 1, 3, 9261, false, 6, true, true, 8, 3, 7, 7, 7),
     // M = 131220: product-tree twiddles (per-stage tables measured 4% slower;
     // on the row pass 10-20% slower). Column passes of 405 with 45 threads
     // per column (one radix-9 butterfly each: 1.3% over 27 threads, the second

@@ -46,8 +46,16 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
     // boundary work runs in the runtime-shape C2C kernels only (staged, or
     // HBM-direct under the direct kernel's own conditions below)
     const bool fs_edge = kind == KK_FS_A_EDGE || kind == KK_FS_B_EDGE;
-    if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE) && !fs_edge)
+    const bool blue_edge = kind == KK_BLUE_1_EDGE;
+    if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE) && !fs_edge &&
+        !blue_edge)
         return hipErrorInvalidValue;
+    // the one-upload Bluestein kernel with its boundary work: fixed shapes,
+    // chirp and spectrum tables, zero intervals over the line's N elements
+    if (blue_edge && (!fixed || (a.flags & KF_EDGE) || !a.chirp || !a.spec ||
+                      ((a.flags & (KF_ZERO_IN | KF_ZERO_OUT)) &&
+                       (a.zl < 0 || a.zl > a.zr || a.zr > a.nvalid || a.zr > a.nout))))
+        return hipErrorInvalidConfiguration;
     // the mixed-storage four-step passes: fixed shapes, the first pass reads
     // the narrow input (and its zero interval), the last writes the narrow
     // output (and its zero interval), over line elements [0, M)
