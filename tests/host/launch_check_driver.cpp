@@ -232,6 +232,34 @@ int main() {
     KArgs bl4 = bl;
     expect("narrow input on the plain Bluestein kernel", check_launch(KK_BLUE_1, 0, -1, bl4, 32, e_lds, limit, nullptr),
            hipErrorInvalidValue);
+    // the even-length real kernels with their boundary work: the zero
+    // interval on the real side only, within 2N reals
+    FixedKernel fr = fe;
+    fr.kind = KK_R2C_HALF_EDGE;
+    fr.col = false;
+    KArgs re = p;
+    re.flags = KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN;
+    re.zl = 1, re.zr = 2 * re.N;
+    expect("real edges, R2C", check_launch(KK_R2C_HALF_EDGE, 0, -1, re, 32, e_lds, limit, &fr), hipSuccess);
+    KArgs re1 = re;
+    re1.zr = 2 * re.N + 1;
+    expect("real edges, zero interval past the reals", check_launch(KK_R2C_HALF_EDGE, 0, -1, re1, 32, e_lds, limit, &fr),
+           hipErrorInvalidConfiguration);
+    KArgs re2 = re;
+    re2.flags = KF_NARROW_IN | KF_ZERO_OUT;
+    expect("real edges, R2C with an output zero interval",
+           check_launch(KK_R2C_HALF_EDGE, 0, -1, re2, 32, e_lds, limit, &fr), hipErrorInvalidConfiguration);
+    expect("real edges on the runtime kernel", check_launch(KK_R2C_HALF_EDGE, 0, -1, re, 32, e_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
+    FixedKernel fc2 = fr;
+    fc2.kind = KK_C2R_HALF_EDGE;
+    fc2.dir = 1;
+    KArgs rc2 = re;
+    rc2.flags = KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_OUT;
+    expect("real edges, C2R", check_launch(KK_C2R_HALF_EDGE, 0, 1, rc2, 32, e_lds, limit, &fc2), hipSuccess);
+    rc2.flags = KF_NARROW_IN | KF_ZERO_IN;
+    expect("real edges, C2R with an input zero interval", check_launch(KK_C2R_HALF_EDGE, 0, 1, rc2, 32, e_lds, limit, &fc2),
+           hipErrorInvalidConfiguration);
     // the matrix convolution product: whole systems of C1 lines per block on
     // the runtime-shape kernel
     KArgs cm = p;

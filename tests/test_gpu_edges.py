@@ -370,3 +370,71 @@ def test_bluestein_zero_padding_fused(hip_ctx, monkeypatch, direction, domain, p
     tol = {F32: 2e-5, F64: 2e-13, F16S: 1e-3, F64C: 1e-7}[prec]
     assert o.rel_l2(y, expect) <= tol
     assert o.rel_l2(yb, expect) <= tol
+
+
+R2C, C2R = vk.TransformKind.RealToComplex, vk.TransformKind.ComplexToReal
+# even lengths whose half length has a fixed real row shape with an edge
+# variant (f32 compute: 8192, 512, 1536, 640; f64 compute: 4096, 512, 384, 160)
+REAL_EDGE = [(16384, F16S, 3), (1024, F16S, 9), (3072, F16S, 5), (1280, F16S, 4),
+             (8192, F64C, 2), (1024, F64C, 7), (768, F64C, 3), (320, F64C, 10)]
+
+
+def f16_real(v):
+    return v.astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,prec,batch", REAL_EDGE)
+def test_mixed_storage_real(hip_ctx, monkeypatch, n, prec, batch):
+    """Mixed-storage 1-D even-length R2C and C2R in one kernel each: the edge
+    variant of the fixed real row shape reads and writes the storage type (no
+    boundary pass), against pocketfft and against the boundary-pass plan."""
+    x = o.normal(n * batch, n % 991 + batch, np.float32)
+    tol = {F16S: 2e-3, F64C: 1e-7}[prec]
+    c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_transform(R2C)
+    X, desc, Xb = run_both(monkeypatch, c, FWD, x)
+    assert desc["boundary"]["real_edges"]
+    assert [p["kernel"] for p in desc["passes"]] == ["r2c_even_half"], desc["passes"]
+    xin = f16_real(x) if prec == F16S else x
+    ref = np.fft.rfft(xin.astype(np.float64).reshape(batch, n), axis=1).reshape(-1)
+    assert o.rel_l2(X, ref) <= tol and o.rel_l2(Xb, ref) <= tol
+    if prec == F16S:
+        assert np.array_equal(X, f16(X))
+    ci = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_transform(C2R) \
+        .with_inverse_normalization(True)
+    z, desc, zb = run_both(monkeypatch, ci, INV, ref.astype(np.complex64))
+    assert desc["boundary"]["real_edges"]
+    assert [p["kernel"] for p in desc["passes"]] == ["c2r_even_half"], desc["passes"]
+    assert o.rel_l2(z, xin.astype(np.float64)) <= tol and o.rel_l2(zb, xin.astype(np.float64)) <= tol
+    if prec == F16S:
+        assert np.array_equal(z, f16_real(z))
+
+
+@pytest.mark.parametrize("prec", [F32, F64, F16S, F64C])
+def test_real_zero_padding_fused(hip_ctx, monkeypatch, prec):
+    """The zero interval of a 1-D zero padding inside the even-length real
+    kernels, over real elements (an odd left end splits a packed pair): R2C
+    reads reals [l, r) as zero, C2R writes them as zero."""
+    n, batch, left, right = 2048, 3, 101, 1500
+    rdt = np.float64 if prec == F64 else np.float32
+    x = o.normal(n * batch, 71, rdt)
+    mask = np.zeros((batch, n), dtype=bool)
+    mask[:, left:right] = True
+    tol = {F32: 2e-5, F64: 2e-13, F16S: 2e-3, F64C: 1e-7}[prec]
+    c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_transform(R2C) \
+        .with_zero_padding(0, left, right)
+    X, desc, Xb = run_both(monkeypatch, c, FWD, x)
+    assert desc["boundary"]["real_edges"]
+    xin = (f16_real(x) if prec == F16S else x).astype(np.float64).reshape(batch, n)
+    ref = np.fft.rfft(np.where(mask, 0, xin), axis=1).reshape(-1)
+    assert o.rel_l2(X, ref) <= tol and o.rel_l2(Xb, ref) <= tol
+    # C2R of a spectrum: the output reals [l, r) written as zero
+    S = np.fft.rfft(xin, axis=1).astype(np.complex128 if prec == F64 else np.complex64)
+    ci = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_transform(C2R) \
+        .with_zero_padding(0, left, right)
+    z, desc, zb = run_both(monkeypatch, ci, INV, S.reshape(-1))
+    assert desc["boundary"]["real_edges"]
+    Sin = f16(S.astype(np.complex64)) if prec == F16S else S
+    expect = np.where(mask, 0, np.fft.irfft(Sin.astype(np.complex128), n, axis=1) * n).reshape(-1)
+    m = mask.reshape(-1)
+    assert (z[m] == 0).all() and (zb[m] == 0).all()
+    assert o.rel_l2(z, expect) <= tol and o.rel_l2(zb, expect) <= tol

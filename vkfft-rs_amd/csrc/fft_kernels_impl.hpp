@@ -446,6 +446,94 @@ struct IoC2RHalf : IoPlain {
     }
 };
 
+// The even-length R2C and C2R kernels with the 1-D boundary work inside:
+// the caller's buffers in the storage type of half the compute precision
+// (KF_NARROW_IN / KF_NARROW_OUT) and the zero interval [zl, zr) of the real
+// side (KF_ZERO_IN on the R2C input, KF_ZERO_OUT on the C2R output), over
+// real elements: element e of the packed line holds reals 2e and 2e + 1.
+template <typename T>
+__device__ __forceinline__ cpx<T> real_pair_mask(const KArgs& a, long long e, cpx<T> v) {
+    const long long r = 2 * e;
+    if (r >= a.zl && r < a.zr) v.re = (T)0;
+    if (r + 1 >= a.zl && r + 1 < a.zr) v.im = (T)0;
+    return v;
+}
+template <typename T, bool NTIO>
+__device__ __forceinline__ cpx<T> ld_storage(const KArgs& a, const void* base, long long i) {
+    if (a.flags & KF_NARROW_IN) {
+        using U = typename Narrow<T>::type;
+        const cpx<U> v = ldg_in<NTIO>(a, (const cpx<U>*)base + i);
+        return mk((T)v.re, (T)v.im);
+    }
+    return ldg_in<NTIO>(a, (const cpx<T>*)base + i);
+}
+template <typename T, bool NTIO>
+__device__ __forceinline__ void st_storage(const KArgs& a, void* base, long long i, cpx<T> v) {
+    if (a.flags & KF_NARROW_OUT) {
+        using U = typename Narrow<T>::type;
+        stg_out<NTIO>(a, (cpx<U>*)base + i, mk((U)v.re, (U)v.im));
+    } else {
+        stg_out<NTIO>(a, (cpx<T>*)base + i, v);
+    }
+}
+
+struct IoR2CHalfEdge : IoR2CHalf {
+    static constexpr bool kPtrLoad = false;
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        const cpx<T> v = ld_storage<T, NTIO>(a, a.in, L.ib + (long long)e * a.in_es);
+        return (a.flags & KF_ZERO_IN) ? real_pair_mask(a, e, v) : v;
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoR2CHalfEdge, D>(a, lds, li, true);
+    }
+    // the postprocess of IoR2CHalf, stored in the storage type
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        const int M = D::N(a);
+        coop_for(D::G(a), M + 1, true, [&](int g, int k) {
+            if (!li[g].valid) return;
+            const cpx<T>* Z = lds + g * D::LS(a);
+            const int k0 = k == M ? 0 : k;
+            const int km = k == 0 ? 0 : M - k;
+            cpx<T> A = Z[lpad(k0, D::PS(a))];
+            cpx<T> B = conj(Z[lpad(km, D::PS(a))]);
+            cpx<T> w = tw2<T>(a.rlo, a.rhi, a.rshift, k);
+            cpx<T> X = (A + B) + muli<-1>(cmul(A - B, w));
+            st_storage<T, D::NTO>(a, a.out, li[g].ob + (long long)k * a.out_es, scale(X, (T)0.5));
+        });
+    }
+};
+
+struct IoC2RHalfEdge : IoC2RHalf {
+    static constexpr bool kPtrStore = false;
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int k) {
+        return load_tw<T, NTIO>(a, L, k, tw2<T>(a.rlo, a.rhi, a.rshift, k));
+    }
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_tw(const KArgs& a, const LineInfo& L, int k, cpx<T> w) {
+        cpx<T> X = ld_storage<T, NTIO>(a, a.in, L.ib + (long long)k * a.in_es);
+        cpx<T> Xm = conj(ld_storage<T, NTIO>(a, a.in, L.ib + (long long)(a.N - k) * a.in_es));
+        return (X + Xm) + muli<1>(cmulc(X - Xm, w));
+    }
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        v = scale(v, (T)a.scale);
+        if (a.flags & KF_ZERO_OUT) v = real_pair_mask(a, e, v);
+        st_storage<T, NTIO>(a, a.out, L.ob + (long long)e * a.out_es, v);
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoC2RHalfEdge, D>(a, lds, li, true);
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoC2RHalfEdge, D, T, S>(a, lds, li, true);
+    }
+};
+
 // Four-step column pass. Line = column n2 of the [N1][N2] view (C = N2);
 // FFT over n1 (length N1); store Y[k1][n2] * W_M^(dir * n2 * k1).
 struct IoFsA : IoPlain {

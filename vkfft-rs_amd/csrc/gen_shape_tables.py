@@ -618,6 +618,17 @@ HEADS_BLUE_EDGE = ("// Fixed shapes of the one-kernel Bluestein transform with t
                    "// threads, lines per block, radices and LDS strides.\n")
 HEADS['kf_blue_edge_f32'] = HEADS_BLUE_EDGE.format(p='f32')
 HEADS['kf_blue_edge_f64'] = HEADS_BLUE_EDGE.format(p='f64')
+# the real rows with the 1-D boundary work inside, one nontemporal role each
+TABLES['kf_real_edge_f32'] = [(r[0] + '_EDGE', r[1] + 'Edge') + r[2:] for r in TABLES['kf_real_rows_f32']]
+TABLES['kf_real_edge_f64'] = [(r[0] + '_EDGE', r[1] + 'Edge') + r[2:] for r in TABLES['kf_real_rows_f64']]
+HEADS_REAL_EDGE = ("// Fixed shapes of the one-upload even-length real transforms with the 1-D\n"
+                   "// boundary work inside, {p}: the caller's buffers in the storage type of\n"
+                   "// half the compute precision and the zero interval of the real side\n"
+                   "// (IoR2CHalfEdge, IoC2RHalfEdge), one entry for each shape of\n"
+                   "// kf_real_rows_{p} with the same threads, lines per block, radices and LDS\n"
+                   "// strides.\n")
+HEADS['kf_real_edge_f32'] = HEADS_REAL_EDGE.format(p='f32')
+HEADS['kf_real_edge_f64'] = HEADS_REAL_EDGE.format(p='f64')
 # fourstep_rows(0 / 1, registered_keys(0 / 1)) before these tables existed
 TABLES['kf_round_fs_f32'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 4, 137), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 4, 255), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 4, 265), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 4, 273), ('FS_A', 'FsA', 400, 25, 32, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 4, 425), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 4, 531), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 4, 545), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 4, 1063), ('FS_A', 'FsA', 1024, 64, 16, True, [16, 8, 8], 30, 1025), ('FS_A', 'FsA', 2000, 125, 8, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 8, False, [16, 5, 5, 5], 4, 2125), ('FS_A', 'FsA', 2048, 128, 8, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 8, False, [16, 16, 8], 4, 2177)]
 TABLES['kf_round_fs_f64'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 3, 145), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 3, 271), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 3, 281), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 3, 289), ('FS_A', 'FsA', 400, 25, 16, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 3, 451), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 3, 563), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 3, 577), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 3, 1125), ('FS_A', 'FsA', 1024, 64, 8, True, [16, 8, 8], 30, 1025), ('FS_B', 'FsB', 1024, 64, 8, False, [16, 8, 8], 3, 1153), ('FS_A', 'FsA', 2000, 125, 4, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 4, False, [16, 5, 5, 5], 3, 2251), ('FS_A', 'FsA', 2048, 128, 4, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 4, False, [16, 16, 8], 3, 2305)]
@@ -639,6 +650,7 @@ HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 
 FUNCS = {'kf_blue_rows_f32': 'fixed_table_blue_rows_f32', 'kf_blue_rows_f64': 'fixed_table_blue_rows_f64',
          'kf_blue_edge_f32': 'fixed_table_blue_edge_f32', 'kf_blue_edge_f64': 'fixed_table_blue_edge_f64',
+         'kf_real_edge_f32': 'fixed_table_real_edge_f32', 'kf_real_edge_f64': 'fixed_table_real_edge_f64',
          'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
          'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
          'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
@@ -655,6 +667,10 @@ def roles(kind, col):
         return [(-1, True, True), (-1, True, False)]
     if kind == "C2R_HALF":
         return [(1, True, True), (1, False, True)]
+    if kind == "R2C_HALF_EDGE":
+        return [(-1, True, True)]
+    if kind == "C2R_HALF_EDGE":
+        return [(1, True, True)]
     if col:
         return [(-1, False, False), (-1, False, True), (1, False, False), (1, False, True)]
     return [(-1, True, True), (-1, True, False), (1, True, True), (1, True, False)]
@@ -696,7 +712,7 @@ def check():
     for name, items in TABLES.items():
         eb = 16 if name.endswith("f64") else 8
         for it in items:
-            if isinstance(it, str) or it[0] in ("R2C_HALF", "C2R_HALF"):
+            if isinstance(it, str) or it[0] in ("R2C_HALF", "C2R_HALF", "R2C_HALF_EDGE", "C2R_HALF_EDGE"):
                 continue
             kind, io, N, TT, G, col, rad, PS, LS = it
             staged = io == "PlainStaged"

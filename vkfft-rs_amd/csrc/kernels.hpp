@@ -39,6 +39,8 @@ enum KernelKind : int {
     KK_FS_A_EDGE,      // KK_FS_A reading half-precision storage, input zero interval (fixed shapes only)
     KK_FS_B_EDGE,      // KK_FS_B writing half-precision storage, output zero interval (fixed shapes only)
     KK_BLUE_1_EDGE,    // KK_BLUE_1 reading / writing half-precision storage, zero intervals (fixed shapes only)
+    KK_R2C_HALF_EDGE,  // KK_R2C_HALF reading / writing half-precision storage, input zero interval (fixed shapes only)
+    KK_C2R_HALF_EDGE,  // KK_C2R_HALF reading / writing half-precision storage, output zero interval (fixed shapes only)
     KK_COUNT
 };
 

@@ -47,9 +47,18 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
     // HBM-direct under the direct kernel's own conditions below)
     const bool fs_edge = kind == KK_FS_A_EDGE || kind == KK_FS_B_EDGE;
     const bool blue_edge = kind == KK_BLUE_1_EDGE;
+    const bool real_edge = kind == KK_R2C_HALF_EDGE || kind == KK_C2R_HALF_EDGE;
     if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE) && !fs_edge &&
-        !blue_edge)
+        !blue_edge && !real_edge)
         return hipErrorInvalidValue;
+    // the even-length real kernels with their boundary work: fixed shapes,
+    // the zero interval on the real side (R2C input, C2R output) within the
+    // line's 2N real elements
+    if (real_edge &&
+        (!fixed || (a.flags & KF_EDGE) ||
+         (a.flags & (kind == KK_R2C_HALF_EDGE ? KF_ZERO_OUT : KF_ZERO_IN)) ||
+         ((a.flags & (KF_ZERO_IN | KF_ZERO_OUT)) && (a.zl < 0 || a.zl > a.zr || a.zr > 2 * (long long)a.N))))
+        return hipErrorInvalidConfiguration;
     // the one-upload Bluestein kernel with its boundary work: fixed shapes,
     // chirp and spectrum tables, zero intervals over the line's N elements
     if (blue_edge && (!fixed || (a.flags & KF_EDGE) || !a.chirp || !a.spec ||

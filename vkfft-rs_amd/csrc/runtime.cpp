@@ -2865,8 +2865,44 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 }
             }
         }
-        const bool fused_edges = !fs_edges && !bl_edges && shape_ok && (mixed || any_zero) && rank == 1 &&
-                                 (!want_layout || layout_ok);
+        // 1-D even-length real transforms of one upload: the R2C or C2R kernel
+        // reads and writes the caller's buffers in the storage type, with the
+        // zero interval of the real side, on the edge variant of its fixed shape
+        auto real_edges = [&]() {
+            if (!fuse_on || !(mixed || any_zero) || rank != 1 || want_layout || d.perform_convolution ||
+                (d.transform != VKFX_R2C && d.transform != VKFX_C2R) || p->launches.empty())
+                return false;
+            const KernelKind k = d.transform == VKFX_R2C ? KK_R2C_HALF : KK_C2R_HALF;
+            const KernelKind ke = d.transform == VKFX_R2C ? KK_R2C_HALF_EDGE : KK_C2R_HALF_EDGE;
+            for (const Launch& L : p->launches)
+                if (L.boundary || L.copy || L.r2r || L.conv || L.kind != k || L.in_sel != SEL_IN ||
+                    L.out_sel != SEL_OUT || L.a.rtab || !kind_variant(L.fixed, ke))
+                    return false;
+            return true;
+        };
+        const bool re_edges = !fs_edges && !bl_edges && real_edges();
+        if (re_edges) {
+            const size_t cs = csize(c.prec);
+            const size_t scs = (store_t == 0 ? 2 : store_t == 1 ? 4 : 8) * 2;  // storage bytes per complex element
+            const KernelKind ke = d.transform == VKFX_R2C ? KK_R2C_HALF_EDGE : KK_C2R_HALF_EDGE;
+            for (Launch& L : p->launches) {
+                L.kind = ke;
+                L.fixed = kind_variant(L.fixed, ke);
+                if (mixed) {
+                    L.a.flags |= KF_NARROW_IN | KF_NARROW_OUT;
+                    L.in_off = L.in_off / cs * scs;
+                    L.out_off = L.out_off / cs * scs;
+                }
+                if (zp_in) L.a.flags |= KF_ZERO_IN;
+                if (zp_out) L.a.flags |= KF_ZERO_OUT;
+                if (any_zero) {
+                    L.a.zl = (long long)d.zero_left[0];
+                    L.a.zr = (long long)d.zero_right[0];
+                }
+            }
+        }
+        const bool fused_edges = !fs_edges && !bl_edges && !re_edges && shape_ok && (mixed || any_zero) &&
+                                 rank == 1 && (!want_layout || layout_ok);
         const bool fused_layout = layout_ok && (fused_edges || !(mixed || any_zero));
         bool edge_stage = false;  // passes between the first and the last run on a compute-type copy
         if (fused_edges || fused_layout) {
@@ -2941,7 +2977,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 }
             }
         }
-        const bool fused_all = fused_edges || fused_layout || fs_edges || bl_edges;
+        const bool fused_all = fused_edges || fused_layout || fs_edges || bl_edges || re_edges;
         const bool need_in = !fused_all && (mixed || (fmt_in && !fused_in) || zp_in);
         const bool need_out = !fused_all && (mixed || (fmt_out && !fused_out) || zp_out);
         const size_t ssz = store_t == 0 ? 2 : store_t == 1 ? 4 : 8;
@@ -2995,9 +3031,10 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         p->stage_out_bytes = (need_out && !p->stage_shared) || edge_stage ? cout : 0;
         c.js << "\"boundary\":{\"input\":" << (need_in ? "true" : "false") << ",\"output\":"
              << (need_out ? "true" : "false") << ",\"fused_batch_stride\":[" << (fused_in ? "true" : "false")
-             << "," << (fused_out ? "true" : "false") << "],\"fused_edges\":" << (fused_edges || fs_edges || bl_edges ? "true" : "false")
+             << "," << (fused_out ? "true" : "false") << "],\"fused_edges\":" << (fused_edges || fs_edges || bl_edges || re_edges ? "true" : "false")
              << ",\"four_step_edges\":" << (fs_edges ? "true" : "false")
              << ",\"bluestein_edges\":" << (bl_edges ? "true" : "false")
+             << ",\"real_edges\":" << (re_edges ? "true" : "false")
              << ",\"fused_layout\":" << (fused_layout ? "true" : "false")
              << ",\"zero_padding\":\""
              << (!any_zero ? "none" : d.zero_frequency ? "frequency" : "spatial") << "\",\"grouped_batch\":[";
