@@ -260,6 +260,23 @@ int main() {
     rc2.flags = KF_NARROW_IN | KF_ZERO_IN;
     expect("real edges, C2R with an input zero interval", check_launch(KK_C2R_HALF_EDGE, 0, 1, rc2, 32, e_lds, limit, &fc2),
            hipErrorInvalidConfiguration);
+    // fixed one-upload rows with their boundary work
+    FixedKernel fpl = fr;
+    fpl.kind = KK_PLAIN_EDGE;
+    KArgs pe = p;
+    pe.flags = KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_OUT;
+    pe.zl = 0, pe.zr = pe.N;
+    expect("plain edges", check_launch(KK_PLAIN_EDGE, 0, -1, pe, 32, e_lds, limit, &fpl), hipSuccess);
+    KArgs pe1 = pe;
+    pe1.zr = pe.N + 1;
+    expect("plain edges, zero interval past the line", check_launch(KK_PLAIN_EDGE, 0, -1, pe1, 32, e_lds, limit, &fpl),
+           hipErrorInvalidConfiguration);
+    KArgs pe2 = pe;
+    pe2.flags |= KF_EDGE;
+    expect("plain edges with KF_EDGE", check_launch(KK_PLAIN_EDGE, 0, -1, pe2, 32, e_lds, limit, &fpl),
+           hipErrorInvalidConfiguration);
+    expect("plain edges on the runtime kernel", check_launch(KK_PLAIN_EDGE, 0, -1, pe, 32, e_lds, limit, nullptr),
+           hipErrorInvalidConfiguration);
     // the matrix convolution product: whole systems of C1 lines per block on
     // the runtime-shape kernel
     KArgs cm = p;

@@ -438,3 +438,26 @@ def test_real_zero_padding_fused(hip_ctx, monkeypatch, prec):
     m = mask.reshape(-1)
     assert (z[m] == 0).all() and (zb[m] == 0).all()
     assert o.rel_l2(z, expect) <= tol and o.rel_l2(zb, expect) <= tol
+
+
+@pytest.mark.parametrize("n,batch", [(1024, 33), (4096, 5), (512, 17), (1000, 7), (8, 100), (96, 40), (2048, 9),
+                                     (720, 6)])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_mixed_storage_fixed_rows(hip_ctx, monkeypatch, n, batch, direction):
+    """Mixed-storage one-upload 1-D C2C keeps the fixed row shape of its
+    length where that shape has an edge variant (3/5-family rows; in f64
+    compute also the power-of-two rows), else runs the runtime-shape edge
+    kernel (f32 power-of-two rows, short rows, round lengths such as 720),
+    against pocketfft and the boundary-pass plan."""
+    x = o.complex_uniform(n * batch, n % 977 + batch, np.complex64)
+    fixed_edge = {F16S: {1000}, F64C: {1024, 4096, 512, 1000, 2048}}
+    for prec, tol in ((F16S, 1e-3), (F64C, 1e-7)):
+        c = vk.FftConfig.new([n]).with_batch_count(batch).with_precision(prec).with_inverse_normalization(True)
+        y, desc, yb = run_both(monkeypatch, c, direction, x)
+        assert [p["kernel"] for p in desc["passes"]] == ["stockham"]
+        assert desc["passes"][0]["fixed_shape"] == (n in fixed_edge[prec]), (prec, desc["passes"][0])
+        xin = f16(x) if prec == F16S else x
+        ref = ref_np(xin, n, batch, direction, normalize=True)
+        assert o.rel_l2(y, ref) <= tol and o.rel_l2(yb, ref) <= tol, prec
+        if prec == F16S:
+            assert np.array_equal(y, f16(y))

@@ -341,6 +341,38 @@ struct IoEdge : IoPlain {
     }
 };
 
+// IoEdge on the fixed one-upload row shapes (KK_PLAIN_EDGE) of mixed-storage
+// plans: the ends of the plain shape read and write the caller's storage type of half the compute
+// precision (compile time, so the loads of a butterfly stay one batch), and
+// the zero intervals of the line replace loaded or stored values by zero.
+template <class Base>
+struct IoEdgeFixed : Base {
+    static constexpr bool kPtrLoad = false, kPtrStore = false;
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        using U = typename Narrow<T>::type;
+        const cpx<U> v = ldg_in<NTIO>(a, (const cpx<U>*)a.in + L.ib + e * a.in_es);
+        const bool z = (a.flags & KF_ZERO_IN) && e >= a.zl && e < a.zr;
+        return z ? zero<T>() : mk((T)v.re, (T)v.im);
+    }
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        using U = typename Narrow<T>::type;
+        const bool z = (a.flags & KF_ZERO_OUT) && e >= a.zl && e < a.zr;
+        v = z ? zero<T>() : scale(v, (T)a.scale);
+        stg_out<NTIO>(a, (cpx<U>*)a.out + L.ob + e * a.out_es, mk((U)v.re, (U)v.im));
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoEdgeFixed, D>(a, lds, li, a.flags & KF_IN_ROWMAJOR);
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoEdgeFixed, D, T, S>(a, lds, li, a.flags & KF_OUT_ROWMAJOR);
+    }
+};
+using IoPlainEdge = IoEdgeFixed<IoPlain>;
+
 struct IoR2CFull : IoPlain {
     static constexpr bool kPtrLoad = false, kPtrStore = false;
     template <class D>

@@ -629,6 +629,35 @@ HEADS_REAL_EDGE = ("// Fixed shapes of the one-upload even-length real transform
                    "// strides.\n")
 HEADS['kf_real_edge_f32'] = HEADS_REAL_EDGE.format(p='f32')
 HEADS['kf_real_edge_f64'] = HEADS_REAL_EDGE.format(p='f64')
+# the one-upload rows with the 1-D boundary work inside, where they beat the
+# runtime-shape edge kernels (F16 storage x 8192-16384 lines, one box): the
+# 3/5-family rows in both precisions (1000: 28.5 against 46.7 us, 1536: 29.0
+# against 34.5, 360: 25.3 against 29.9) and the f64 power-of-two rows (512:
+# 21.7 against 29.1 us, 2048: 27.4 against 27.9); f32 power-of-two rows
+# (256: 30.1 against 23.5 us, 1024: 34.9 against 30.5) and short rows with
+# staged ends (96: 49.7 against 36.9 us) keep the runtime-shape edge kernels
+PLAIN_CFG_ROWS = {0: [], 1: [('PLAIN', 'Plain', 512, 64, 2, False, [8, 8, 8], 3, 576)]}
+
+
+def plain_edge_rows(prec):
+    p = 'f64' if prec else 'f32'
+    tables = ('kf_pow2_f64', 'kf_fam_f64') if prec else ('kf_fam_f32',)
+    rows = PLAIN_CFG_ROWS[prec] + [r for t in tables for r in TABLES[t]
+                                   if not isinstance(r, str) and r[0] == 'PLAIN' and not r[5] and r[1] == 'Plain']
+    return [('PLAIN_EDGE', r[1] + 'Edge') + r[2:] for r in rows]
+
+
+TABLES['kf_plain_edge_f32'] = plain_edge_rows(0)
+TABLES['kf_plain_edge_f64'] = plain_edge_rows(1)
+HEADS_PLAIN_EDGE = ("// Fixed one-upload C2C row shapes with the 1-D boundary work inside, {p}:\n"
+                    "// the caller's input and output in the storage type of half the compute\n"
+                    "// precision and the zero intervals of zero padding (IoPlainEdge), one\n"
+                    "// entry per direction for the row shapes where the fixed shape beats the\n"
+                    "// runtime-shape edge kernel (the 3/5-family rows; in f64 also the\n"
+                    "// power-of-two rows and the 512-point benchmark row), with the same\n"
+                    "// threads, lines per block, radices and LDS strides.\n")
+HEADS['kf_plain_edge_f32'] = HEADS_PLAIN_EDGE.format(p='f32')
+HEADS['kf_plain_edge_f64'] = HEADS_PLAIN_EDGE.format(p='f64')
 # fourstep_rows(0 / 1, registered_keys(0 / 1)) before these tables existed
 TABLES['kf_round_fs_f32'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 4, 137), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 4, 255), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 4, 265), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 4, 273), ('FS_A', 'FsA', 400, 25, 32, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 4, 425), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 4, 531), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 4, 545), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 4, 1063), ('FS_A', 'FsA', 1024, 64, 16, True, [16, 8, 8], 30, 1025), ('FS_A', 'FsA', 2000, 125, 8, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 8, False, [16, 5, 5, 5], 4, 2125), ('FS_A', 'FsA', 2048, 128, 8, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 8, False, [16, 16, 8], 4, 2177)]
 TABLES['kf_round_fs_f64'] = [('FS_B', 'FsB', 128, 8, 16, False, [16, 8], 3, 145), ('FS_A', 'FsA', 240, 30, 32, True, [8, 6, 5], 30, 241), ('FS_B', 'FsB', 240, 30, 16, False, [8, 6, 5], 3, 271), ('FS_A', 'FsA', 250, 25, 32, True, [10, 5, 5], 30, 251), ('FS_B', 'FsB', 250, 25, 16, False, [10, 5, 5], 3, 281), ('FS_A', 'FsA', 256, 16, 32, True, [16, 16], 30, 257), ('FS_B', 'FsB', 256, 16, 16, False, [16, 16], 3, 289), ('FS_A', 'FsA', 400, 25, 16, True, [16, 5, 5], 30, 401), ('FS_B', 'FsB', 400, 25, 16, False, [16, 5, 5], 3, 451), ('FS_A', 'FsA', 500, 50, 16, True, [10, 10, 5], 30, 501), ('FS_B', 'FsB', 500, 50, 16, False, [10, 10, 5], 3, 563), ('FS_A', 'FsA', 512, 64, 16, True, [8, 8, 8], 30, 513), ('FS_B', 'FsB', 512, 64, 16, False, [8, 8, 8], 3, 577), ('FS_A', 'FsA', 1000, 100, 8, True, [10, 10, 10], 30, 1001), ('FS_B', 'FsB', 1000, 100, 8, False, [10, 10, 10], 3, 1125), ('FS_A', 'FsA', 1024, 64, 8, True, [16, 8, 8], 30, 1025), ('FS_B', 'FsB', 1024, 64, 8, False, [16, 8, 8], 3, 1153), ('FS_A', 'FsA', 2000, 125, 4, True, [16, 5, 5, 5], 30, 2001), ('FS_B', 'FsB', 2000, 125, 4, False, [16, 5, 5, 5], 3, 2251), ('FS_A', 'FsA', 2048, 128, 4, True, [16, 16, 8], 30, 2049), ('FS_B', 'FsB', 2048, 128, 4, False, [16, 16, 8], 3, 2305)]
@@ -651,6 +680,7 @@ HEADS['kf_round_f64'] = HEADS_ROUND.format(p='f64')
 FUNCS = {'kf_blue_rows_f32': 'fixed_table_blue_rows_f32', 'kf_blue_rows_f64': 'fixed_table_blue_rows_f64',
          'kf_blue_edge_f32': 'fixed_table_blue_edge_f32', 'kf_blue_edge_f64': 'fixed_table_blue_edge_f64',
          'kf_real_edge_f32': 'fixed_table_real_edge_f32', 'kf_real_edge_f64': 'fixed_table_real_edge_f64',
+         'kf_plain_edge_f32': 'fixed_table_plain_edge_f32', 'kf_plain_edge_f64': 'fixed_table_plain_edge_f64',
          'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
          'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
          'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
@@ -671,6 +701,8 @@ def roles(kind, col):
         return [(-1, True, True)]
     if kind == "C2R_HALF_EDGE":
         return [(1, True, True)]
+    if kind == "PLAIN_EDGE":
+        return [(-1, True, True), (1, True, True)]
     if col:
         return [(-1, False, False), (-1, False, True), (1, False, False), (1, False, True)]
     return [(-1, True, True), (-1, True, False), (1, True, True), (1, True, False)]

@@ -41,6 +41,7 @@ enum KernelKind : int {
     KK_BLUE_1_EDGE,    // KK_BLUE_1 reading / writing half-precision storage, zero intervals (fixed shapes only)
     KK_R2C_HALF_EDGE,  // KK_R2C_HALF reading / writing half-precision storage, input zero interval (fixed shapes only)
     KK_C2R_HALF_EDGE,  // KK_C2R_HALF reading / writing half-precision storage, output zero interval (fixed shapes only)
+    KK_PLAIN_EDGE,     // one-upload 1-D KK_PLAIN rows with storage conversion and zero intervals (fixed shapes only)
     KK_COUNT
 };
 

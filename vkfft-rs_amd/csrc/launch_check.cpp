@@ -48,9 +48,15 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
     const bool fs_edge = kind == KK_FS_A_EDGE || kind == KK_FS_B_EDGE;
     const bool blue_edge = kind == KK_BLUE_1_EDGE;
     const bool real_edge = kind == KK_R2C_HALF_EDGE || kind == KK_C2R_HALF_EDGE;
+    const bool plain_edge = kind == KK_PLAIN_EDGE;
     if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE) && !fs_edge &&
-        !blue_edge && !real_edge)
+        !blue_edge && !real_edge && !plain_edge)
         return hipErrorInvalidValue;
+    // the fixed one-upload rows of mixed-storage plans: narrow input and
+    // output, zero intervals within the line's N elements
+    if (plain_edge && (!fixed || (a.flags & KF_EDGE) || !(a.flags & KF_NARROW_IN) || !(a.flags & KF_NARROW_OUT) ||
+                       ((a.flags & (KF_ZERO_IN | KF_ZERO_OUT)) && (a.zl < 0 || a.zl > a.zr || a.zr > a.N))))
+        return hipErrorInvalidConfiguration;
     // the even-length real kernels with their boundary work: fixed shapes,
     // the zero interval on the real side (R2C input, C2R output) within the
     // line's 2N real elements

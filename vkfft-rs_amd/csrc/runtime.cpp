@@ -2742,6 +2742,10 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         // VKFX_FUSED_EDGES=0 keeps the boundary passes (comparison runs).
         const char* fe = getenv("VKFX_FUSED_EDGES");
         const bool fuse_on = !(fe && fe[0] == '0');
+        // mixed-storage one-pass chunks keep a fixed row shape that has an
+        // edge variant (VKFX_FIXED_EDGES=0: the runtime-shape edge kernels)
+        const char* fxe = getenv("VKFX_FIXED_EDGES");
+        const bool fixed_edges = mixed && !(fxe && fxe[0] == '0');
         bool all_active = true;
         for (size_t i = 0; i < rank; ++i) all_active &= d.dims[i] > 1 && !(d.omit_dimension >> i & 1u);
         // the first and last passes of a chunk are plain one-upload line
@@ -2757,8 +2761,11 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
                 const bool plain = L.kind == KK_PLAIN && !L.a.rtab;
                 if ((first || last) && !plain) return false;
-                // a fixed shape that would carry edges needs a runtime geometry of its length
-                if ((first || last) && (mixed || any_zero) && L.fixed && !edge_geometry(c, L.a).ok) return false;
+                // a fixed shape that would carry edges needs an edge variant (one-pass
+                // chunks) or a runtime geometry of its length
+                if ((first || last) && (mixed || any_zero) && L.fixed &&
+                    !(fixed_edges && first && last && kind_variant(L.fixed, KK_PLAIN_EDGE)) && !edge_geometry(c, L.a).ok)
+                    return false;
                 if ((L.in_sel == SEL_IN) != first || (first && L.out_sel != SEL_OUT && !last)) return false;
                 if (last && L.out_sel != SEL_OUT) return false;
                 if ((L.in_sel != SEL_IN && L.in_sel != SEL_OUT && L.in_sel != SEL_WORK) ||
@@ -2919,12 +2926,21 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
                 prev_chunk = L.chunk;
                 if (fused_edges && (first || last)) {
-                    int rc = to_edge_kernel(c, L);
-                    if (rc) {
-                        delete p;
-                        return rc;
+                    // a one-pass chunk on a fixed row shape with an edge
+                    // variant keeps its shape; the others move to the
+                    // runtime-shape edge kernels
+                    const FixedKernel* fe = fixed_edges && first && last && L.fixed ? kind_variant(L.fixed, KK_PLAIN_EDGE) : nullptr;
+                    if (fe) {
+                        L.kind = KK_PLAIN_EDGE;
+                        L.fixed = fe;
+                    } else {
+                        int rc = to_edge_kernel(c, L);
+                        if (rc) {
+                            delete p;
+                            return rc;
+                        }
+                        L.a.flags |= KF_EDGE;
                     }
-                    L.a.flags |= KF_EDGE;
                     if (any_zero) L.a.zl = (long long)d.zero_left[0], L.a.zr = (long long)d.zero_right[0];
                     if (first && mixed) L.a.flags |= KF_NARROW_IN;
                     if (first && zp_in) L.a.flags |= KF_ZERO_IN;
