@@ -82,8 +82,10 @@ def test_mixed_storage_fused(hip_ctx, monkeypatch, dims, batch, direction):
 @pytest.mark.parametrize("dims,batch", [([16, 24, 40], 2), ([64, 48], 3), ([6, 10, 12, 14], 1), ([4096, 16], 2),
                                         ([8, 2048, 24], 1), ([8, 97, 40], 1)])
 def test_mixed_storage_nd_flat_boundary(hip_ctx, dims, batch):
-    """N-D mixed storage keeps its fixed-shape passes between two boundary
-    passes, which are flat vectorized conversions for dense layouts."""
+    """N-D mixed storage: the first and last passes of each chunk convert in
+    their own loads and stores when both have fixed shapes with edge
+    variants, else the fixed-shape passes run between two boundary passes
+    (flat vectorized conversions for dense layouts)."""
     count = int(np.prod(dims)) * batch
     x = o.complex_uniform(count, count % 983, np.complex64)
     for prec, tol in ((F64C, 1e-7), (F16S, 1e-3)):
@@ -92,7 +94,8 @@ def test_mixed_storage_nd_flat_boundary(hip_ctx, dims, batch):
         y = hip_ctx.execute_transform(ir, x)
         desc = hip_ctx.plan(ir).describe()
         kernels = [p["kernel"] for p in desc["passes"]]
-        assert kernels[0] == "boundary_in" and kernels[-1] == "boundary_out", kernels
+        boundary = kernels[0] == "boundary_in" and kernels[-1] == "boundary_out"
+        assert boundary != desc["boundary"]["fused_edges"], kernels
         xin = f16(x) if prec == F16S else x
         assert o.rel_l2(y, ref_c2c(xin, dims, batch, FWD)) <= tol, prec
 
@@ -458,6 +461,31 @@ def test_mixed_storage_fixed_rows(hip_ctx, monkeypatch, n, batch, direction):
         assert desc["passes"][0]["fixed_shape"] == (n in fixed_edge[prec]), (prec, desc["passes"][0])
         xin = f16(x) if prec == F16S else x
         ref = ref_np(xin, n, batch, direction, normalize=True)
+        assert o.rel_l2(y, ref) <= tol and o.rel_l2(yb, ref) <= tol, prec
+        if prec == F16S:
+            assert np.array_equal(y, f16(y))
+
+
+@pytest.mark.parametrize("dims,batch,precs", [([256, 256], 2, (F16S, F64C)), ([64, 512], 3, (F16S, F64C)),
+                                              ([4096, 4096], 1, (F16S,)), ([96, 360], 2, (F16S, F64C))])
+@pytest.mark.parametrize("direction", [FWD, INV])
+def test_mixed_storage_nd_fused(hip_ctx, monkeypatch, dims, batch, precs, direction):
+    """Mixed-storage N-D plans whose chunks start and end on fixed shapes with
+    edge variants: the row pass reads the storage type, the column (or split
+    second) pass writes it, the passes between run on a compute-type stage;
+    against pocketfft and the boundary-pass plan."""
+    count = int(np.prod(dims)) * batch
+    x = o.complex_uniform(count, count % 971, np.complex64)
+    for prec in precs:
+        tol = {F16S: 1e-3, F64C: 1e-7}[prec]
+        c = vk.FftConfig.new(dims).with_batch_count(batch).with_precision(prec).with_inverse_normalization(True)
+        y, desc, yb = run_both(monkeypatch, c, direction, x)
+        kernels = [p["kernel"] for p in desc["passes"]]
+        assert "boundary_in" not in kernels and "boundary_out" not in kernels, kernels
+        assert desc["passes"][0]["fixed_shape"] and desc["passes"][-1]["fixed_shape"]
+        xin = (f16(x) if prec == F16S else x).astype(np.complex128).reshape((batch,) + tuple(dims))
+        axes = tuple(range(1, len(dims) + 1))
+        ref = (np.fft.fftn(xin, axes=axes) if direction == FWD else np.fft.ifftn(xin, axes=axes)).reshape(-1)
         assert o.rel_l2(y, ref) <= tol and o.rel_l2(yb, ref) <= tol, prec
         if prec == F16S:
             assert np.array_equal(y, f16(y))

@@ -373,6 +373,44 @@ struct IoEdgeFixed : Base {
 };
 using IoPlainEdge = IoEdgeFixed<IoPlain>;
 
+// The first (NI) or last (NO) pass of a mixed-storage N-D chunk on a fixed
+// row or column shape: the caller's side in the storage type of half the
+// compute precision (compile time), the other side the compute-type stage.
+template <bool NI, bool NO>
+struct IoEdgeSide : IoPlain {
+    static constexpr bool kPtrLoad = !NI, kPtrStore = !NO;
+    template <typename T, bool NTIO = false>
+    static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
+        if constexpr (NI) {
+            using U = typename Narrow<T>::type;
+            const cpx<U> v = ldg_in<NTIO>(a, (const cpx<U>*)a.in + L.ib + e * a.in_es);
+            return mk((T)v.re, (T)v.im);
+        } else {
+            return ldg_in<NTIO>(a, (const cpx<T>*)a.in + L.ib + e * a.in_es);
+        }
+    }
+    template <typename T, int S, bool NTIO = false>
+    static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
+        v = scale(v, (T)a.scale);
+        if constexpr (NO) {
+            using U = typename Narrow<T>::type;
+            stg_out<NTIO>(a, (cpx<U>*)a.out + L.ob + e * a.out_es, mk((U)v.re, (U)v.im));
+        } else {
+            stg_out<NTIO>(a, (cpx<T>*)a.out + L.ob + e * a.out_es, v);
+        }
+    }
+    template <typename T, class D>
+    static __device__ void prologue(const KArgs& a, cpx<T>* lds, const LineInfo* li) {
+        staged_load<IoEdgeSide, D>(a, lds, li, a.flags & KF_IN_ROWMAJOR);
+    }
+    template <typename T, int S, class D>
+    static __device__ void epilogue(const KArgs& a, const cpx<T>* lds, const LineInfo* li) {
+        staged_store<IoEdgeSide, D, T, S>(a, lds, li, a.flags & KF_OUT_ROWMAJOR);
+    }
+};
+using IoPlainEdgeIn = IoEdgeSide<true, false>;
+using IoPlainEdgeOut = IoEdgeSide<false, true>;
+
 struct IoR2CFull : IoPlain {
     static constexpr bool kPtrLoad = false, kPtrStore = false;
     template <class D>

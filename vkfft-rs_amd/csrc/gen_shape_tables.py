@@ -647,6 +647,33 @@ def plain_edge_rows(prec):
     return [('PLAIN_EDGE', r[1] + 'Edge') + r[2:] for r in rows]
 
 
+# the first pass (rows, storage-type input) and the last pass (columns,
+# storage-type output) of mixed-storage N-D chunks: every row and column shape
+# of the benchmark lengths, kf_pow2_* and kf_fam_* (staged rows excepted)
+ND_CFG = {0: [('PLAIN', 'Plain', 1024, 128, 1, False, [16, 8, 8], 4, 1088),
+              ('PLAIN', 'Plain', 4096, 256, 1, False, [16, 16, 16], 4, 4352),
+              ('PLAIN', 'Plain', 64, 8, 32, True, [8, 8], 30, 65)],
+          1: [('PLAIN', 'Plain', 512, 64, 2, False, [8, 8, 8], 3, 576),
+              ('PLAIN', 'Plain', 512, 64, 16, True, [8, 8, 8], 30, 513)]}
+
+
+def nd_edge_rows(prec):
+    p = 'f64' if prec else 'f32'
+    rows = ND_CFG[prec] + [r for t in ('kf_pow2_' + p, 'kf_fam_' + p) for r in TABLES[t]
+                           if not isinstance(r, str) and r[0] == 'PLAIN' and r[1] == 'Plain']
+    return [(('PLAIN_EDGE_OUT', 'PlainEdgeOut') if r[5] else ('PLAIN_EDGE_IN', 'PlainEdgeIn')) + r[2:] for r in rows]
+
+
+TABLES['kf_nd_edge_f32'] = nd_edge_rows(0)
+TABLES['kf_nd_edge_f64'] = nd_edge_rows(1)
+HEADS_ND_EDGE = ("// Fixed shapes of the first and last passes of mixed-storage N-D chunks,\n"
+                 "// {p}: rows reading the caller's storage type of half the compute precision\n"
+                 "// (IoPlainEdgeIn) and columns writing it (IoPlainEdgeOut), the middle\n"
+                 "// passes running on a compute-type stage; one entry per direction for each\n"
+                 "// row and column shape of the benchmark lengths, kf_pow2_{p} and kf_fam_{p},\n"
+                 "// with the same threads, lines per block, radices and LDS strides.\n")
+HEADS['kf_nd_edge_f32'] = HEADS_ND_EDGE.format(p='f32')
+HEADS['kf_nd_edge_f64'] = HEADS_ND_EDGE.format(p='f64')
 TABLES['kf_plain_edge_f32'] = plain_edge_rows(0)
 TABLES['kf_plain_edge_f64'] = plain_edge_rows(1)
 HEADS_PLAIN_EDGE = ("// Fixed one-upload C2C row shapes with the 1-D boundary work inside, {p}:\n"
@@ -681,6 +708,7 @@ FUNCS = {'kf_blue_rows_f32': 'fixed_table_blue_rows_f32', 'kf_blue_rows_f64': 'f
          'kf_blue_edge_f32': 'fixed_table_blue_edge_f32', 'kf_blue_edge_f64': 'fixed_table_blue_edge_f64',
          'kf_real_edge_f32': 'fixed_table_real_edge_f32', 'kf_real_edge_f64': 'fixed_table_real_edge_f64',
          'kf_plain_edge_f32': 'fixed_table_plain_edge_f32', 'kf_plain_edge_f64': 'fixed_table_plain_edge_f64',
+         'kf_nd_edge_f32': 'fixed_table_nd_edge_f32', 'kf_nd_edge_f64': 'fixed_table_nd_edge_f64',
          'kf_round_fs_f32': 'fixed_table_round_fs_f32', 'kf_round_fs_f64': 'fixed_table_round_fs_f64',
          'kf_round_real_f32': 'fixed_table_round_real_f32', 'kf_round_real_f64': 'fixed_table_round_real_f64',
          'kf_round_nd_f32': 'fixed_table_round_nd_f32', 'kf_round_nd_f64': 'fixed_table_round_nd_f64',
@@ -703,6 +731,10 @@ def roles(kind, col):
         return [(1, True, True)]
     if kind == "PLAIN_EDGE":
         return [(-1, True, True), (1, True, True)]
+    if kind == "PLAIN_EDGE_IN":
+        return [(-1, True, False), (1, True, False)]
+    if kind == "PLAIN_EDGE_OUT":
+        return [(-1, False, True), (1, False, True)]
     if col:
         return [(-1, False, False), (-1, False, True), (1, False, False), (1, False, True)]
     return [(-1, True, True), (-1, True, False), (1, True, True), (1, True, False)]

@@ -42,6 +42,8 @@ enum KernelKind : int {
     KK_R2C_HALF_EDGE,  // KK_R2C_HALF reading / writing half-precision storage, input zero interval (fixed shapes only)
     KK_C2R_HALF_EDGE,  // KK_C2R_HALF reading / writing half-precision storage, output zero interval (fixed shapes only)
     KK_PLAIN_EDGE,     // one-upload 1-D KK_PLAIN rows with storage conversion and zero intervals (fixed shapes only)
+    KK_PLAIN_EDGE_IN,  // KK_PLAIN first pass of an N-D chunk reading half-precision storage (fixed shapes only)
+    KK_PLAIN_EDGE_OUT, // KK_PLAIN last pass of an N-D chunk writing half-precision storage (fixed shapes only)
     KK_COUNT
 };
 

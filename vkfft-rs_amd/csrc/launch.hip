@@ -45,6 +45,8 @@ const FixedKernel* fixed_table_real_edge_f32(int* count);
 const FixedKernel* fixed_table_real_edge_f64(int* count);
 const FixedKernel* fixed_table_plain_edge_f32(int* count);
 const FixedKernel* fixed_table_plain_edge_f64(int* count);
+const FixedKernel* fixed_table_nd_edge_f32(int* count);
+const FixedKernel* fixed_table_nd_edge_f64(int* count);
 
 // All registered fixed-shape instantiations, merged once (thread-safe
 // static initialisation).
@@ -66,7 +68,8 @@ static const FixedKernel* registry(int* count) {
                                                 fixed_table_conv1, fixed_table_blue_edge_f32,
                                                 fixed_table_blue_edge_f64, fixed_table_real_edge_f32,
                                                 fixed_table_real_edge_f64, fixed_table_plain_edge_f32,
-                                                fixed_table_plain_edge_f64};
+                                                fixed_table_plain_edge_f64, fixed_table_nd_edge_f32,
+                                                fixed_table_nd_edge_f64};
         constexpr int kTables = (int)(sizeof(tables) / sizeof(tables[0]));
         int counts[kTables], sum = 0;
         const FixedKernel* ptrs[kTables];

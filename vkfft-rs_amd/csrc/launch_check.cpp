@@ -49,9 +49,16 @@ hipError_t check_launch(KernelKind kind, int prec, int dir, const KArgs& a, unsi
     const bool blue_edge = kind == KK_BLUE_1_EDGE;
     const bool real_edge = kind == KK_R2C_HALF_EDGE || kind == KK_C2R_HALF_EDGE;
     const bool plain_edge = kind == KK_PLAIN_EDGE;
+    const bool side_edge = kind == KK_PLAIN_EDGE_IN || kind == KK_PLAIN_EDGE_OUT;
     if ((a.flags & (KF_NARROW_IN | KF_NARROW_OUT | KF_ZERO_IN | KF_ZERO_OUT)) && !(a.flags & KF_EDGE) && !fs_edge &&
-        !blue_edge && !real_edge && !plain_edge)
+        !blue_edge && !real_edge && !plain_edge && !side_edge)
         return hipErrorInvalidValue;
+    // the first / last pass of a mixed-storage N-D chunk: fixed shapes, the
+    // storage type on one side, no zero intervals
+    if (side_edge && (!fixed || (a.flags & (KF_EDGE | KF_ZERO_IN | KF_ZERO_OUT)) ||
+                      ((a.flags & KF_NARROW_IN) != 0) != (kind == KK_PLAIN_EDGE_IN) ||
+                      ((a.flags & KF_NARROW_OUT) != 0) != (kind == KK_PLAIN_EDGE_OUT)))
+        return hipErrorInvalidConfiguration;
     // the fixed one-upload rows of mixed-storage plans: narrow input and
     // output, zero intervals within the line's N elements
     if (plain_edge && (!fixed || (a.flags & KF_EDGE) || !(a.flags & KF_NARROW_IN) || !(a.flags & KF_NARROW_OUT) ||

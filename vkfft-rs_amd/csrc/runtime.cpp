@@ -2743,9 +2743,17 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
         const char* fe = getenv("VKFX_FUSED_EDGES");
         const bool fuse_on = !(fe && fe[0] == '0');
         // mixed-storage one-pass chunks keep a fixed row shape that has an
-        // edge variant (VKFX_FIXED_EDGES=0: the runtime-shape edge kernels)
+        // edge variant (VKFX_FIXED_EDGES=0: the runtime-shape edge kernels);
+        // the first and last passes of a multi-pass chunk (N-D) keep theirs
+        // when both have input / output variants and there is no zero interval
         const char* fxe = getenv("VKFX_FIXED_EDGES");
         const bool fixed_edges = mixed && !(fxe && fxe[0] == '0');
+        auto end_variant = [&](const Launch& L, bool first, bool last) -> const FixedKernel* {
+            if (!fixed_edges || !L.fixed) return nullptr;
+            if (first && last) return kind_variant(L.fixed, KK_PLAIN_EDGE);
+            if (any_zero) return nullptr;
+            return kind_variant(L.fixed, first ? KK_PLAIN_EDGE_IN : KK_PLAIN_EDGE_OUT);
+        };
         bool all_active = true;
         for (size_t i = 0; i < rank; ++i) all_active &= d.dims[i] > 1 && !(d.omit_dimension >> i & 1u);
         // the first and last passes of a chunk are plain one-upload line
@@ -2763,8 +2771,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 if ((first || last) && !plain) return false;
                 // a fixed shape that would carry edges needs an edge variant (one-pass
                 // chunks) or a runtime geometry of its length
-                if ((first || last) && (mixed || any_zero) && L.fixed &&
-                    !(fixed_edges && first && last && kind_variant(L.fixed, KK_PLAIN_EDGE)) && !edge_geometry(c, L.a).ok)
+                if ((first || last) && (mixed || any_zero) && L.fixed && !end_variant(L, first, last) &&
+                    !edge_geometry(c, L.a).ok)
                     return false;
                 if ((L.in_sel == SEL_IN) != first || (first && L.out_sel != SEL_OUT && !last)) return false;
                 if (last && L.out_sel != SEL_OUT) return false;
@@ -2908,8 +2916,21 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                 }
             }
         }
+        // N-D: every chunk's first and last pass on a fixed shape with its variant
+        auto nd_ends_fixed = [&]() {
+            if (rank < 2 || !mixed || any_zero || want_layout) return false;
+            int prev_chunk = -1;
+            for (size_t i = 0; i < p->launches.size(); ++i) {
+                const Launch& L = p->launches[i];
+                const bool first = L.chunk != prev_chunk;
+                const bool last = i + 1 == p->launches.size() || p->launches[i + 1].chunk != L.chunk;
+                prev_chunk = L.chunk;
+                if ((first || last) && (first == last || !end_variant(L, first, last))) return false;
+            }
+            return true;
+        };
         const bool fused_edges = !fs_edges && !bl_edges && !re_edges && shape_ok && (mixed || any_zero) &&
-                                 rank == 1 && (!want_layout || layout_ok);
+                                 (rank == 1 || nd_ends_fixed()) && (!want_layout || layout_ok);
         const bool fused_layout = layout_ok && (fused_edges || !(mixed || any_zero));
         bool edge_stage = false;  // passes between the first and the last run on a compute-type copy
         if (fused_edges || fused_layout) {
@@ -2929,9 +2950,9 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                     // a one-pass chunk on a fixed row shape with an edge
                     // variant keeps its shape; the others move to the
                     // runtime-shape edge kernels
-                    const FixedKernel* fe = fixed_edges && first && last && L.fixed ? kind_variant(L.fixed, KK_PLAIN_EDGE) : nullptr;
+                    const FixedKernel* fe = end_variant(L, first, last);
                     if (fe) {
-                        L.kind = KK_PLAIN_EDGE;
+                        L.kind = first && last ? KK_PLAIN_EDGE : first ? KK_PLAIN_EDGE_IN : KK_PLAIN_EDGE_OUT;
                         L.fixed = fe;
                     } else {
                         int rc = to_edge_kernel(c, L);
@@ -2952,7 +2973,8 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                     const long long b0 = (long long)(L.in_off / ((size_t)per_batch * cs));
                     const bool fmt = fmt_in && fused_layout;
                     const long long bst = fmt ? in_bst : per_batch;
-                    L.in_off = (size_t)(b0 * bst) * (mixed ? scs : cs);
+                    // dense: the same element offset in the storage type
+                    L.in_off = fmt ? (size_t)(b0 * bst) * (mixed ? scs : cs) : L.in_off / cs * (mixed ? scs : cs);
                     if (fmt && rank == 1) {
                         a.in_os = bst;
                     } else if (fmt) {
@@ -2973,7 +2995,7 @@ int vkfx_plan_create(vkfx_context* ctx, const vkfx_plan_desc* desc_in, vkfx_plan
                     const long long b0 = (long long)(L.out_off / ((size_t)per_batch * cs));
                     const bool fmt = fmt_out && fused_layout;
                     const long long bst = fmt ? out_bst : per_batch;
-                    L.out_off = (size_t)(b0 * bst) * (mixed ? scs : cs);
+                    L.out_off = fmt ? (size_t)(b0 * bst) * (mixed ? scs : cs) : L.out_off / cs * (mixed ? scs : cs);
                     if (fmt && rank == 1) {
                         a.out_os = bst;
                     } else if (fmt) {
