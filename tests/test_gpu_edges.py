@@ -467,7 +467,8 @@ def test_mixed_storage_fixed_rows(hip_ctx, monkeypatch, n, batch, direction):
 
 
 @pytest.mark.parametrize("dims,batch,precs", [([256, 256], 2, (F16S, F64C)), ([64, 512], 3, (F16S, F64C)),
-                                              ([4096, 4096], 1, (F16S,)), ([96, 360], 2, (F16S, F64C))])
+                                              ([4096, 4096], 1, (F16S,)), ([96, 360], 2, (F16S, F64C)),
+                                              ([32, 256, 256], 2, (F16S, F64C))])
 @pytest.mark.parametrize("direction", [FWD, INV])
 def test_mixed_storage_nd_fused(hip_ctx, monkeypatch, dims, batch, precs, direction):
     """Mixed-storage N-D plans whose chunks start and end on fixed shapes with
