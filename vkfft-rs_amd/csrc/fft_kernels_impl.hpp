@@ -348,6 +348,34 @@ struct IoEdge : IoPlain {
 template <class Base>
 struct IoEdgeFixed : Base {
     static constexpr bool kPtrLoad = false, kPtrStore = false;
+    static constexpr bool kBflyLoad = true, kBflyStore = true;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        using U = typename Narrow<T>::type;
+        const cpx<U>* x = (const cpx<U>*)a.in + L.ib + (long long)b * a.in_es;
+        const long long dx = (long long)NB * a.in_es;
+        const bool zi = (a.flags & KF_ZERO_IN) != 0;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const cpx<U> u = ldg_in<NTIO>(a, x + i * dx);
+            const int e = b + i * NB;
+            v[i] = (zi && e >= a.zl && e < a.zr) ? zero<T>() : mk((T)u.re, (T)u.im);
+        }
+    }
+    template <typename T, int S, bool NTIO, int R, int P>
+    static __device__ __forceinline__ void store_bfly(const KArgs& a, const LineInfo& L, int base, const cpx<T>* v) {
+        using U = typename Narrow<T>::type;
+        cpx<U>* y = (cpx<U>*)a.out + L.ob + (long long)base * a.out_es;
+        const long long dy = (long long)P * a.out_es;
+        const T sc = (T)a.scale;
+        const bool zo = (a.flags & KF_ZERO_OUT) != 0;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const int e = base + q * P;
+            const bool z = zo && e >= a.zl && e < a.zr;
+            stg_out<NTIO>(a, y + q * dy, z ? mk((U)0, (U)0) : mk((U)(v[q].re * sc), (U)(v[q].im * sc)));
+        }
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         using U = typename Narrow<T>::type;
@@ -379,6 +407,29 @@ using IoPlainEdge = IoEdgeFixed<IoPlain>;
 template <bool NI, bool NO>
 struct IoEdgeSide : IoPlain {
     static constexpr bool kPtrLoad = !NI, kPtrStore = !NO;
+    // direct stages: one storage-type address per butterfly, stepped by the
+    // butterfly's element stride
+    static constexpr bool kBflyLoad = NI, kBflyStore = NO;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        using U = typename Narrow<T>::type;
+        const cpx<U>* x = (const cpx<U>*)a.in + L.ib + (long long)b * a.in_es;
+        const long long dx = (long long)NB * a.in_es;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const cpx<U> u = ldg_in<NTIO>(a, x + i * dx);
+            v[i] = mk((T)u.re, (T)u.im);
+        }
+    }
+    template <typename T, int S, bool NTIO, int R, int P>
+    static __device__ __forceinline__ void store_bfly(const KArgs& a, const LineInfo& L, int base, const cpx<T>* v) {
+        using U = typename Narrow<T>::type;
+        cpx<U>* y = (cpx<U>*)a.out + L.ob + (long long)base * a.out_es;
+        const long long dy = (long long)P * a.out_es;
+        const T sc = (T)a.scale;
+#pragma unroll
+        for (int q = 0; q < R; ++q) stg_out<NTIO>(a, y + q * dy, mk((U)(v[q].re * sc), (U)(v[q].im * sc)));
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         if constexpr (NI) {

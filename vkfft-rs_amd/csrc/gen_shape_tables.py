@@ -630,11 +630,11 @@ HEADS_REAL_EDGE = ("// Fixed shapes of the one-upload even-length real transform
 HEADS['kf_real_edge_f32'] = HEADS_REAL_EDGE.format(p='f32')
 HEADS['kf_real_edge_f64'] = HEADS_REAL_EDGE.format(p='f64')
 # the one-upload rows with the 1-D boundary work inside, where they beat the
-# runtime-shape edge kernels (F16 storage x 8192-16384 lines, one box): the
-# 3/5-family rows in both precisions (1000: 28.5 against 46.7 us, 1536: 29.0
-# against 34.5, 360: 25.3 against 29.9) and the f64 power-of-two rows (512:
-# 21.7 against 29.1 us, 2048: 27.4 against 27.9); f32 power-of-two rows
-# (256: 30.1 against 23.5 us, 1024: 34.9 against 30.5) and short rows with
+# runtime-shape edge kernels (2048-16384 lines, one box): the 3/5-family rows
+# in both precisions (F16 storage 1000: 31.9 against 46.8 us, 1536: 28.6
+# against 34.5; F64 compute 1000: 18.6 against 48.2) and the f64 power-of-two
+# rows (512: 15.4 against 29.5 us, 2048: 16.5 against 27.9); f32 power-of-two
+# rows (256: 30.1 against 23.5 us, 1024: 34.9 against 30.5) and short rows with
 # staged ends (96: 49.7 against 36.9 us) keep the runtime-shape edge kernels
 PLAIN_CFG_ROWS = {0: [], 1: [('PLAIN', 'Plain', 512, 64, 2, False, [8, 8, 8], 3, 576)]}
 
