@@ -600,6 +600,30 @@ __device__ __forceinline__ void st_storage(const KArgs& a, void* base, long long
 
 struct IoR2CHalfEdge : IoR2CHalf {
     static constexpr bool kPtrLoad = false;
+    // direct first stage: one address per butterfly, the storage type
+    // decided once per butterfly so its loads issue together
+    static constexpr bool kBflyLoad = true;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        const long long i0 = L.ib + (long long)b * a.in_es, di = (long long)NB * a.in_es;
+        if (a.flags & KF_NARROW_IN) {
+            using U = typename Narrow<T>::type;
+            const cpx<U>* x = (const cpx<U>*)a.in + i0;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const cpx<U> u = ldg_in<NTIO>(a, x + i * di);
+                v[i] = mk((T)u.re, (T)u.im);
+            }
+        } else {
+            const cpx<T>* x = (const cpx<T>*)a.in + i0;
+#pragma unroll
+            for (int i = 0; i < R; ++i) v[i] = ldg_in<NTIO>(a, x + i * di);
+        }
+        if (a.flags & KF_ZERO_IN) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) v[i] = real_pair_mask(a, b + i * NB, v[i]);
+        }
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         const cpx<T> v = ld_storage<T, NTIO>(a, a.in, L.ib + (long long)e * a.in_es);
@@ -629,6 +653,29 @@ struct IoR2CHalfEdge : IoR2CHalf {
 
 struct IoC2RHalfEdge : IoC2RHalf {
     static constexpr bool kPtrStore = false;
+    // direct last stage: one address per butterfly, the storage type decided
+    // once per butterfly
+    static constexpr bool kBflyStore = true;
+    template <typename T, int S, bool NTIO, int R, int P>
+    static __device__ __forceinline__ void store_bfly(const KArgs& a, const LineInfo& L, int base, const cpx<T>* v) {
+        const long long o0 = L.ob + (long long)base * a.out_es, dq = (long long)P * a.out_es;
+        cpx<T> w[R];
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            w[q] = scale(v[q], (T)a.scale);
+            if (a.flags & KF_ZERO_OUT) w[q] = real_pair_mask(a, base + q * P, w[q]);
+        }
+        if (a.flags & KF_NARROW_OUT) {
+            using U = typename Narrow<T>::type;
+            cpx<U>* y = (cpx<U>*)a.out + o0;
+#pragma unroll
+            for (int q = 0; q < R; ++q) stg_out<NTIO>(a, y + q * dq, mk((U)w[q].re, (U)w[q].im));
+        } else {
+            cpx<T>* y = (cpx<T>*)a.out + o0;
+#pragma unroll
+            for (int q = 0; q < R; ++q) stg_out<NTIO>(a, y + q * dq, w[q]);
+        }
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int k) {
         return load_tw<T, NTIO>(a, L, k, tw2<T>(a.rlo, a.rhi, a.rshift, k));
