@@ -892,6 +892,21 @@ struct IoFsAC2RDirect : IoFsAC2R {
 // (KF_ZERO_IN); element n1 of column n2 is line element n2 + n1 * N2.
 struct IoFsAEdge : IoFsA {
     static constexpr bool kPtrLoad = false;
+    // direct first stage: one storage-type address per butterfly
+    static constexpr bool kBflyLoad = true;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        using U = typename Narrow<T>::type;
+        const cpx<U>* x = (const cpx<U>*)a.in + L.ib + (long long)b * a.in_es;
+        const long long dx = (long long)NB * a.in_es;
+        const bool zi = (a.flags & KF_ZERO_IN) != 0;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const cpx<U> u = ldg_in<NTIO>(a, x + i * dx);
+            const long long n = L.c + (long long)(b + i * NB) * a.N2;
+            v[i] = (zi && n >= a.zl && n < a.zr) ? zero<T>() : mk((T)u.re, (T)u.im);
+        }
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         if (a.flags & KF_ZERO_IN) {
@@ -930,6 +945,22 @@ struct IoFsB : IoPlain {
 // element k1 + k2 * N1.
 struct IoFsBEdge : IoFsB {
     static constexpr bool kPtrStore = false;
+    // direct last stage: one storage-type address per butterfly
+    static constexpr bool kBflyStore = true;
+    template <typename T, int S, bool NTIO, int R, int P>
+    static __device__ __forceinline__ void store_bfly(const KArgs& a, const LineInfo& L, int base, const cpx<T>* v) {
+        using U = typename Narrow<T>::type;
+        cpx<U>* y = (cpx<U>*)a.out + L.ob + (long long)base * a.out_es;
+        const long long dy = (long long)P * a.out_es;
+        const T sc = (T)a.scale;
+        const bool zo = (a.flags & KF_ZERO_OUT) != 0;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const long long k = L.c + (long long)(base + q * P) * a.N1;
+            const bool z = zo && k >= a.zl && k < a.zr;
+            stg_out<NTIO>(a, y + q * dy, z ? mk((U)0, (U)0) : mk((U)(v[q].re * sc), (U)(v[q].im * sc)));
+        }
+    }
     template <typename T, int S, bool NTIO = false>
     static __device__ __forceinline__ void store_elem(const KArgs& a, const LineInfo& L, int e, cpx<T> v) {
         v = scale(v, (T)a.scale);
