@@ -1185,6 +1185,50 @@ struct IoBlue1 : IoPlain {
 // the storage type (KF_NARROW_OUT, rounded to nearest) with the output zero
 // interval written as zero (KF_ZERO_OUT).
 struct IoBlue1Edge : IoBlue1 {
+    // direct first stage: one address per butterfly, the storage type decided
+    // once per butterfly; padding elements (e >= N) load the line's last
+    // element (the address stays inside the line) and are replaced by zero
+    static constexpr bool kBflyLoad = true;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        constexpr int ZF = kZeroFrom(R * NB);
+        const long long last = a.nvalid - 1;
+        cpx<T> u[R];
+        if (a.flags & KF_NARROW_IN) {
+            using U = typename Narrow<T>::type;
+            const cpx<U>* x = (const cpx<U>*)a.in + L.ib;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                if (i * NB < ZF) {
+                    const long long e = b + i * NB;
+                    const cpx<U> w = ldg_in<NTIO>(a, x + (e < last ? e : last) * a.in_es);
+                    u[i] = mk((T)w.re, (T)w.im);
+                }
+            }
+        } else {
+            const cpx<T>* x = (const cpx<T>*)a.in + L.ib;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                if (i * NB < ZF) {
+                    const long long e = b + i * NB;
+                    u[i] = ldg_in<NTIO>(a, x + (e < last ? e : last) * a.in_es);
+                }
+            }
+        }
+        const cpx<T>* chirp = (const cpx<T>*)a.chirp;
+        const bool zi = (a.flags & KF_ZERO_IN) != 0;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if (i * NB < ZF) {
+                const long long e = b + i * NB;
+                const long long ec = e < last ? e : last;
+                const bool keep = e <= last && !(zi && e >= a.zl && e < a.zr);
+                v[i] = keep ? cmul(u[i], chirp[ec]) : zero<T>();
+            } else {
+                v[i] = zero<T>();
+            }
+        }
+    }
     template <typename T, bool NTIO = false>
     static __device__ __forceinline__ cpx<T> load_elem(const KArgs& a, const LineInfo& L, int e) {
         if (e >= a.nvalid) return zero<T>();
