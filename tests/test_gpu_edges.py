@@ -462,6 +462,18 @@ def test_mixed_storage_fixed_rows(hip_ctx, monkeypatch, n, batch, direction):
         xin = f16(x) if prec == F16S else x
         ref = ref_np(xin, n, batch, direction, normalize=True)
         assert o.rel_l2(y, ref) <= tol and o.rel_l2(yb, ref) <= tol, prec
+        # VKFX_FIXED_EDGES=0: the same plan on the runtime-shape edge kernel
+        monkeypatch.setenv("VKFX_FUSED_EDGES", "1")
+        monkeypatch.setenv("VKFX_FIXED_EDGES", "0")
+        ctx = vk.HipExecutionContext(0)
+        try:
+            ir = vk.TransformIr.build(c, direction)
+            yr = ctx.execute_transform(ir, x)
+            assert not ctx.plan(ir).describe()["passes"][0]["fixed_shape"]
+        finally:
+            ctx.close()
+            monkeypatch.delenv("VKFX_FIXED_EDGES")
+        assert o.rel_l2(yr, ref) <= tol, prec
         if prec == F16S:
             assert np.array_equal(y, f16(y))
 
