@@ -653,6 +653,41 @@ struct IoR2CHalfEdge : IoR2CHalf {
 
 struct IoC2RHalfEdge : IoC2RHalf {
     static constexpr bool kPtrStore = false;
+    // direct first stage: the pairs (X[k], X[M-k]) of a butterfly read
+    // together, the storage type decided once per butterfly, the twiddles
+    // W_N^k from the butterfly's root and the powers of its step
+    static constexpr bool kBflyLoad = true;
+    template <typename T, bool NTIO, int R, int NB>
+    static __device__ __forceinline__ void load_bfly(const KArgs& a, const LineInfo& L, int b, cpx<T>* v) {
+        cpx<T> X[R], Xm[R];
+        const long long di = (long long)NB * a.in_es;
+        const long long i0 = L.ib + (long long)b * a.in_es, m0 = L.ib + (long long)(a.N - b) * a.in_es;
+        if (a.flags & KF_NARROW_IN) {
+            using U = typename Narrow<T>::type;
+            const cpx<U>* x = (const cpx<U>*)a.in;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const cpx<U> p = ldg_in<NTIO>(a, x + i0 + i * di), q = ldg_in<NTIO>(a, x + m0 - i * di);
+                X[i] = mk((T)p.re, (T)p.im);
+                Xm[i] = mk((T)q.re, (T)q.im);
+            }
+        } else {
+            const cpx<T>* x = (const cpx<T>*)a.in;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                X[i] = ldg_in<NTIO>(a, x + i0 + i * di);
+                Xm[i] = ldg_in<NTIO>(a, x + m0 - i * di);
+            }
+        }
+        const cpx<T> wb = tw2<T>(a.rlo, a.rhi, a.rshift, b);
+        cpx<T> sp[R];
+        root_powers<R>(tw2<T>(a.rlo, a.rhi, a.rshift, NB), sp);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const cpx<T> xm = conj(Xm[i]);
+            v[i] = (X[i] + xm) + muli<1>(cmulc(X[i] - xm, cmul(wb, sp[i])));
+        }
+    }
     // direct last stage: one address per butterfly, the storage type decided
     // once per butterfly
     static constexpr bool kBflyStore = true;
